@@ -1,0 +1,165 @@
+// Shared host/device helpers for the MI355X learner library.
+//
+// Error convention (mirrors robolearn/cuda/kernels.cu:70-79, 408): every
+// extern "C" entry point returns 0 on success and -1 on a synchronous error,
+// and leaves a message in a thread-local 512-byte buffer read through
+// rl_last_error().  Run/step calls only enqueue work on the caller's HIP
+// stream: they never allocate, free or synchronize, so they are legal inside
+// hipStreamBeginCapture.  Plan create/destroy calls may allocate and must run
+// outside capture.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <limits>
+
+#define RL_API extern "C" __attribute__((visibility("default")))
+
+namespace rl {
+
+extern thread_local char last_error[512];
+
+struct Failure {};
+
+inline void set_error(const char* format, ...) noexcept {
+    va_list args;
+    va_start(args, format);
+    std::vsnprintf(last_error, sizeof(last_error), format, args);
+    va_end(args);
+}
+
+inline void clear_error() noexcept { last_error[0] = '\0'; }
+
+inline void require(bool condition, const char* message) {
+    if (!condition) {
+        set_error("%s", message);
+        throw Failure{};
+    }
+}
+
+inline void check_hip(hipError_t status, const char* operation) {
+    if (status != hipSuccess) {
+        set_error("%s: %s", operation, hipGetErrorString(status));
+        throw Failure{};
+    }
+}
+
+// Reports a launch error without clearing HIP's sticky state.
+inline void check_launch(const char* operation) {
+    const hipError_t status = hipPeekAtLastError();
+    if (status != hipSuccess) {
+        set_error("%s: %s", operation, hipGetErrorString(status));
+        throw Failure{};
+    }
+}
+
+inline bool aligned(const void* pointer, std::size_t bytes) noexcept {
+    return reinterpret_cast<std::uintptr_t>(pointer) % bytes == 0;
+}
+
+inline hipStream_t as_stream(void* stream) noexcept { return reinterpret_cast<hipStream_t>(stream); }
+
+// Runs body() and maps exceptions to the -1 status convention.
+template <class Body>
+int guarded(const char* what, Body&& body) noexcept {
+    clear_error();
+    try {
+        body();
+        return 0;
+    } catch (const Failure&) {
+        return -1;
+    } catch (...) {
+        set_error("Unexpected host error in %s.", what);
+        return -1;
+    }
+}
+
+template <class Body>
+void* guarded_ptr(const char* what, Body&& body) noexcept {
+    clear_error();
+    try {
+        return body();
+    } catch (const Failure&) {
+        return nullptr;
+    } catch (...) {
+        set_error("Unexpected host error in %s.", what);
+        return nullptr;
+    }
+}
+
+inline unsigned ceil_div(long long a, long long b) { return static_cast<unsigned>((a + b - 1) / b); }
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+
+constexpr int kWave = 64;
+
+// Round-to-nearest-even fp32 -> bf16, written from the IEEE-754 definition:
+// add 0x7FFF plus the lowest kept mantissa bit, then truncate.  NaN keeps a
+// quiet payload.
+__device__ __forceinline__ unsigned short f32_to_bf16_bits(float value) {
+    unsigned int bits = __float_as_uint(value);
+    if ((bits & 0x7F800000u) == 0x7F800000u && (bits & 0x007FFFFFu)) return static_cast<unsigned short>((bits >> 16) | 0x40u);
+    bits += 0x7FFFu + ((bits >> 16) & 1u);
+    return static_cast<unsigned short>(bits >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(unsigned short bits) {
+    return __uint_as_float(static_cast<unsigned int>(bits) << 16);
+}
+
+__device__ __forceinline__ float wave_sum(float value) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) value += __shfl_xor(value, offset, kWave);
+    return value;
+}
+
+__device__ __forceinline__ double wave_sum(double value) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) value += __shfl_xor(value, offset, kWave);
+    return value;
+}
+
+__device__ __forceinline__ float wave_max(float value) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset, kWave));
+    return value;
+}
+
+// Fixed-order block sum for blockDim.x == Threads; the result is broadcast.
+template <int Threads>
+__device__ __forceinline__ float block_sum(float value, float* scratch) {
+    value = wave_sum(value);
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = value;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < Threads / kWave; ++w) total += scratch[w];
+    return total;
+}
+
+template <int Threads>
+__device__ __forceinline__ double block_sum(double value, double* scratch) {
+    value = wave_sum(value);
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = value;
+    __syncthreads();
+    double total = 0.0;
+#pragma unroll
+    for (int w = 0; w < Threads / kWave; ++w) total += scratch[w];
+    return total;
+}
+
+}  // namespace rl

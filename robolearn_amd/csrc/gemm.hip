@@ -1,0 +1,426 @@
+// Dense layer GEMMs on CDNA4 matrix cores.
+//
+// One row-major kernel family covers the three products of a bias-free
+// Linear layer (the reference's CudaLinear plans, robolearn/cuda/linear.py:179-185):
+//   forward  Y[R,N]  = X[R,K]  . W[N,K]^T     (A K-contiguous, B K-contiguous)
+//   input    dX[R,K] = dY[R,N] . W[N,K]       (A K-contiguous, B N-contiguous)
+//   weight   dW[N,K] = dY[R,N]^T . X[R,K]     (A M-contiguous, B N-contiguous)
+// batched over a leading ensemble index (the stacked twin critics).
+//
+// Mode 0 computes with v_mfma_f32_32x32x2_f32 (fp32 operands), mode 1 with
+// v_mfma_f32_32x32x16_bf16 (operands rounded to bf16 when staged into LDS,
+// fp32 accumulation).  A 256-thread workgroup owns a 128x128 output tile as
+// 2x2 waves of 64x64; each wave holds 2x2 32x32 accumulators.  Operands are
+// staged through LDS in [row][k] order so each lane reads its K-slice with one
+// or two 16-byte LDS loads; the K order inside a tile is permuted identically
+// for both operands, which leaves the dot products unchanged.
+#include "common.hpp"
+
+#include <cmath>
+#include <string>
+
+namespace rl {
+namespace gemm {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
+
+constexpr int kThreads = 256;
+constexpr int kTile = 128;
+
+enum Epilogue : int { kNone = 0, kRelu = 1, kElu = 2 };
+
+struct Params {
+    const void* a;
+    const void* b;
+    float* d;            // output (or split-K workspace)
+    const float* c;      // beta operand (same layout as d), may alias d
+    const float* bias;   // length n, may be null
+    long long lda, ldb, ldd;
+    long long stride_a, stride_b, stride_d, stride_bias;
+    int m, n, k;
+    int batch;           // ensemble count
+    int splits;          // K splits; >1 writes partial tiles into d = workspace
+    int k_per_split;     // multiple of the K tile
+    float beta;          // D = act(AB + bias) + beta * C (direct mode only)
+    int epilogue;        // Epilogue (direct mode only)
+    int a_vec, b_vec;    // 16-byte vector loads allowed
+};
+
+template <typename T> struct Src;
+template <> struct Src<float> {
+    static __device__ __forceinline__ float load(const float* p) { return *p; }
+};
+template <> struct Src<unsigned short> {
+    static __device__ __forceinline__ float load(const unsigned short* p) { return bf16_bits_to_f32(*p); }
+};
+
+template <int Mode> struct Lds;
+template <> struct Lds<0> {
+    using T = float;
+    static constexpr int KT = 16;
+    static constexpr int Pitch = KT + 4;
+    static __device__ __forceinline__ T cvt(float v) { return v; }
+};
+template <> struct Lds<1> {
+    using T = unsigned short;
+    static constexpr int KT = 32;
+    static constexpr int Pitch = KT + 8;
+    static __device__ __forceinline__ T cvt(float v) { return f32_to_bf16_bits(v); }
+};
+
+// Loads one 128 x KT operand tile into registers, already converted to the
+// LDS element type, and later stores it.  Element (r, k) of the operand is
+// src[r * ld + k] when KContig, else src[k * ld + r].
+template <int Mode, typename S, bool KContig>
+struct TileLoader {
+    using L = Lds<Mode>;
+    using T = typename L::T;
+    static constexpr int KT = L::KT;
+    static constexpr int VecElems = 16 / sizeof(S);
+    static constexpr int VecPerRow = KT / VecElems;
+    static constexpr int PerThread = KContig ? (kTile * VecPerRow) / kThreads : 1;
+    static constexpr int Count = KContig ? PerThread * VecElems : KT / 2;
+    T regs[Count];
+
+    __device__ __forceinline__ void load(const S* src, long long ld, int r0, int k0, int rows, int ks, bool vec) {
+        const int t = threadIdx.x;
+        if constexpr (KContig) {
+#pragma unroll
+            for (int i = 0; i < PerThread; ++i) {
+                const int v = i * kThreads + t;
+                const int r = r0 + v / VecPerRow;
+                const int k = k0 + (v % VecPerRow) * VecElems;
+                const S* p = src + static_cast<long long>(r) * ld + k;
+                if (r < rows && vec && k + VecElems <= ks) {
+                    if constexpr (sizeof(S) == 4) {
+                        const float4 x = *reinterpret_cast<const float4*>(p);
+                        regs[i * VecElems + 0] = L::cvt(x.x);
+                        regs[i * VecElems + 1] = L::cvt(x.y);
+                        regs[i * VecElems + 2] = L::cvt(x.z);
+                        regs[i * VecElems + 3] = L::cvt(x.w);
+                    } else {
+                        const u16x8_t x = *reinterpret_cast<const u16x8_t*>(p);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) regs[i * VecElems + e] = L::cvt(bf16_bits_to_f32(x[e]));
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < VecElems; ++e)
+                        regs[i * VecElems + e] = (r < rows && k + e < ks) ? L::cvt(Src<S>::load(p + e)) : L::cvt(0.0f);
+                }
+            }
+        } else {
+            const int r = r0 + t % kTile;
+            const int kb = k0 + (t / kTile) * (KT / 2);
+            const bool rv = r < rows;
+#pragma unroll
+            for (int e = 0; e < KT / 2; ++e) {
+                const int k = kb + e;
+                regs[e] = (rv && k < ks) ? L::cvt(Src<S>::load(src + static_cast<long long>(k) * ld + r)) : L::cvt(0.0f);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(T* lds) const {
+        const int t = threadIdx.x;
+        if constexpr (KContig) {
+#pragma unroll
+            for (int i = 0; i < PerThread; ++i) {
+                const int v = i * kThreads + t;
+                T* q = lds + (v / VecPerRow) * L::Pitch + (v % VecPerRow) * VecElems;
+#pragma unroll
+                for (int e = 0; e < VecElems; ++e) q[e] = regs[i * VecElems + e];
+            }
+        } else {
+            T* q = lds + (t % kTile) * L::Pitch + (t / kTile) * (KT / 2);
+#pragma unroll
+            for (int e = 0; e < KT / 2; ++e) q[e] = regs[e];
+        }
+    }
+};
+
+__device__ __forceinline__ float apply_epilogue(float v, int epilogue) {
+    if (epilogue == kRelu) return v > 0.0f ? v : 0.0f;
+    if (epilogue == kElu) return v > 0.0f ? v : expm1f(v);
+    return v;
+}
+
+template <int Mode, typename SA, typename SB, bool AK, bool BK>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
+    using L = Lds<Mode>;
+    using T = typename L::T;
+    constexpr int KT = L::KT;
+    constexpr int Pitch = L::Pitch;
+    __shared__ __attribute__((aligned(16))) T sa[kTile * Pitch];
+    __shared__ __attribute__((aligned(16))) T sb[kTile * Pitch];
+
+    const int split = static_cast<int>(blockIdx.z) % p.splits;
+    const int batch = static_cast<int>(blockIdx.z) / p.splits;
+    const SA* A = static_cast<const SA*>(p.a) + batch * p.stride_a;
+    const SB* B = static_cast<const SB*>(p.b) + batch * p.stride_b;
+    const int m0 = static_cast<int>(blockIdx.y) * kTile;
+    const int n0 = static_cast<int>(blockIdx.x) * kTile;
+    const int k_begin = split * p.k_per_split;
+    const int k_end = min(p.k, k_begin + p.k_per_split);
+
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int wm = wave / 2;
+    const int wn = wave % 2;
+
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    TileLoader<Mode, SA, AK> la;
+    TileLoader<Mode, SB, BK> lb;
+    const bool avec = p.a_vec != 0;
+    const bool bvec = p.b_vec != 0;
+
+    // B is indexed (n, k) when BK else (k, n); the loader wants (row=n, k).
+    if (k_begin < k_end) {
+        la.load(A, p.lda, m0, k_begin, p.m, k_end, avec);
+        lb.load(B, p.ldb, n0, k_begin, p.n, k_end, bvec);
+        la.store(sa);
+        lb.store(sb);
+    }
+    __syncthreads();
+
+    for (int k0 = k_begin; k0 < k_end; k0 += KT) {
+        const bool more = k0 + KT < k_end;
+        if (more) {
+            la.load(A, p.lda, m0, k0 + KT, p.m, k_end, avec);
+            lb.load(B, p.ldb, n0, k0 + KT, p.n, k_end, bvec);
+        }
+        if constexpr (Mode == 1) {
+            bf16x8_t af[2][2], bfr[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const T* q = sa + (wm * 64 + i * 32 + lane % 32) * Pitch + (lane / 32) * 16;
+                af[i][0] = *reinterpret_cast<const bf16x8_t*>(q);
+                af[i][1] = *reinterpret_cast<const bf16x8_t*>(q + 8);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const T* q = sb + (wn * 64 + j * 32 + lane % 32) * Pitch + (lane / 32) * 16;
+                bfr[j][0] = *reinterpret_cast<const bf16x8_t*>(q);
+                bfr[j][1] = *reinterpret_cast<const bf16x8_t*>(q + 8);
+            }
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][s], bfr[j][s], acc[i][j], 0, 0, 0);
+        } else {
+            float4 af[2][2], bfr[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const T* q = sa + (wm * 64 + i * 32 + lane % 32) * Pitch + (lane / 32) * 8;
+                af[i][0] = *reinterpret_cast<const float4*>(q);
+                af[i][1] = *reinterpret_cast<const float4*>(q + 4);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const T* q = sb + (wn * 64 + j * 32 + lane % 32) * Pitch + (lane / 32) * 8;
+                bfr[j][0] = *reinterpret_cast<const float4*>(q);
+                bfr[j][1] = *reinterpret_cast<const float4*>(q + 4);
+            }
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const float a = s < 4 ? af[i][0][s] : af[i][1][s - 4];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const float b = s < 4 ? bfr[j][0][s] : bfr[j][1][s - 4];
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (more) {
+            la.store(sa);
+            lb.store(sb);
+        }
+        __syncthreads();
+    }
+
+    // Accumulator layout of a 32x32 MFMA tile: lane l holds column l % 32 and
+    // rows 8 * (v / 4) + 4 * (l / 32) + v % 4 for v = 0..15.
+    const bool direct = p.splits == 1;
+    float* D = p.d + (direct ? batch * p.stride_d
+                             : (static_cast<long long>(split) * p.batch + batch) * static_cast<long long>(p.m) * p.n);
+    const long long ldd = direct ? p.ldd : p.n;
+    const float* bias = p.bias ? p.bias + batch * p.stride_bias : nullptr;
+    const float* C = p.c ? p.c + batch * p.stride_d : nullptr;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + wn * 64 + j * 32 + lane % 32;
+            if (col >= p.n) continue;
+            const float bcol = (direct && bias) ? bias[col] : 0.0f;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + wm * 64 + i * 32 + 8 * (v / 4) + 4 * (lane / 32) + (v % 4);
+                if (row >= p.m) continue;
+                const long long offset = static_cast<long long>(row) * ldd + col;
+                float* out = D + offset;
+                if (direct) {
+                    float value = apply_epilogue(acc[i][j][v] + bcol, p.epilogue);
+                    if (p.beta != 0.0f) value += p.beta * C[offset];
+                    *out = value;
+                } else {
+                    *out = acc[i][j][v];
+                }
+            }
+        }
+    }
+}
+
+// Fixed-order split-K reduction: D = act(sum_s W[s] + bias) + beta * C.
+__global__ void splitk_reduce(const float* work, float* d, const float* c, const float* bias, long long ldd,
+                              long long stride_d, long long stride_bias, int m, int n, int batch, int splits,
+                              float beta, int epilogue) {
+    const long long total = static_cast<long long>(batch) * m * n;
+    for (long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; idx < total;
+         idx += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int col = static_cast<int>(idx % n);
+        const int row = static_cast<int>((idx / n) % m);
+        const int b = static_cast<int>(idx / (static_cast<long long>(m) * n));
+        float value = 0.0f;
+        for (int s = 0; s < splits; ++s) value += work[(static_cast<long long>(s) * batch + b) * m * n + static_cast<long long>(row) * n + col];
+        if (bias) value += bias[b * stride_bias + col];
+        value = apply_epilogue(value, epilogue);
+        const long long offset = b * stride_d + static_cast<long long>(row) * ldd + col;
+        if (beta != 0.0f) value += beta * c[offset];
+        d[offset] = value;
+    }
+}
+
+template <int Mode, typename SA, typename SB, bool AK, bool BK>
+void launch_typed(const Params& p, hipStream_t stream) {
+    const dim3 grid(ceil_div(p.n, kTile), ceil_div(p.m, kTile), static_cast<unsigned>(p.batch * p.splits));
+    hipLaunchKernelGGL((gemm_kernel<Mode, SA, SB, AK, BK>), grid, dim3(kThreads), 0, stream, p);
+}
+
+template <int Mode, typename SA, typename SB>
+void launch_layout(const Params& p, bool ak, bool bk, hipStream_t stream) {
+    if (ak && bk) launch_typed<Mode, SA, SB, true, true>(p, stream);
+    else if (ak && !bk) launch_typed<Mode, SA, SB, true, false>(p, stream);
+    else if (!ak && bk) launch_typed<Mode, SA, SB, false, true>(p, stream);
+    else launch_typed<Mode, SA, SB, false, false>(p, stream);
+}
+
+template <int Mode>
+void launch_mode(const Params& p, int a_bf16, int b_bf16, bool ak, bool bk, hipStream_t stream) {
+    using F = float;
+    using H = unsigned short;
+    if (!a_bf16 && !b_bf16) launch_layout<Mode, F, F>(p, ak, bk, stream);
+    else if (!a_bf16 && b_bf16) launch_layout<Mode, F, H>(p, ak, bk, stream);
+    else if (a_bf16 && !b_bf16) launch_layout<Mode, H, F>(p, ak, bk, stream);
+    else launch_layout<Mode, H, H>(p, ak, bk, stream);
+}
+
+}  // namespace gemm
+
+// Row-major batched GEMM with optional split-K.  See the header for the
+// argument contract.  Returns the workspace bytes needed when d == nullptr.
+int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int m, int n, int k, int batch,
+             const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
+             const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
+             float beta, int epilogue, int splits, float* workspace, std::size_t workspace_bytes, hipStream_t stream) {
+    require(mode == 0 || mode == 1, "GEMM mode must be 0 (fp32) or 1 (bf16 operands).");
+    require(!(mode == 0 && (a_bf16 || b_bf16)), "fp32 GEMM mode requires fp32 operands.");
+    require(m > 0 && n > 0 && k > 0 && batch > 0, "GEMM dimensions must be positive.");
+    require(a && b && d, "GEMM operands must be nonnull.");
+    require(std::isfinite(beta) && (beta == 0.0f || c), "Nonzero beta requires C; beta must be finite.");
+    require(epilogue >= 0 && epilogue <= 2, "Unknown GEMM epilogue.");
+    require(splits >= 1, "GEMM split count must be positive.");
+    require(static_cast<long long>(m) * n <= std::numeric_limits<int>::max(), "GEMM output exceeds 2^31 elements.");
+    gemm::Params p{};
+    p.a = a;
+    p.b = b;
+    p.bias = bias;
+    p.lda = lda;
+    p.ldb = ldb;
+    p.ldd = ldd;
+    p.stride_a = stride_a;
+    p.stride_b = stride_b;
+    p.stride_d = stride_d;
+    p.stride_bias = stride_bias;
+    p.m = m;
+    p.n = n;
+    p.k = k;
+    p.batch = batch;
+    p.c = c;
+    p.beta = beta;
+    p.epilogue = epilogue;
+    const int kt = mode == 1 ? 32 : 16;
+    const int ktiles = (k + kt - 1) / kt;
+    if (splits > ktiles) splits = ktiles;
+    const int tiles_per_split = (ktiles + splits - 1) / splits;
+    splits = (ktiles + tiles_per_split - 1) / tiles_per_split;
+    p.splits = splits;
+    p.k_per_split = tiles_per_split * kt;
+    const std::size_t a_elem = a_bf16 ? 2 : 4;
+    const std::size_t b_elem = b_bf16 ? 2 : 4;
+    p.a_vec = aligned(a, 16) && (lda * a_elem) % 16 == 0 && (stride_a * a_elem) % 16 == 0;
+    p.b_vec = aligned(b, 16) && (ldb * b_elem) % 16 == 0 && (stride_b * b_elem) % 16 == 0;
+    if (splits > 1) {
+        const std::size_t need = static_cast<std::size_t>(splits) * batch * m * n * sizeof(float);
+        require(workspace && workspace_bytes >= need && aligned(workspace, 16),
+                "Split-K GEMM workspace is null, misaligned or too small.");
+        p.d = workspace;
+        p.c = nullptr;
+        p.beta = 0.0f;
+        p.epilogue = 0;
+    } else {
+        p.d = d;
+    }
+    if (mode == 0) gemm::launch_mode<0>(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
+    else gemm::launch_mode<1>(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
+    check_launch("Launch GEMM");
+    if (splits > 1) {
+        const long long total = static_cast<long long>(batch) * m * n;
+        const unsigned blocks = static_cast<unsigned>(std::min<long long>((total + 255) / 256, 4096));
+        hipLaunchKernelGGL(gemm::splitk_reduce, dim3(blocks), dim3(256), 0, stream, workspace, d, c, bias, ldd,
+                           stride_d, stride_bias, m, n, batch, splits, beta, epilogue);
+        check_launch("Launch split-K reduction");
+    }
+    return 0;
+}
+
+}  // namespace rl
+
+RL_API int rl_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int m, int n, int k, int batch,
+                   const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
+                   const float* c, float* d, long long ldd, long long stride_d, const float* bias,
+                   long long stride_bias, float beta, int epilogue, int splits, float* workspace,
+                   std::size_t workspace_bytes, void* stream) noexcept {
+    return rl::guarded("rl_gemm", [&] {
+        rl::run_gemm(mode, a_bf16, b_bf16, a_kcontig, b_kcontig, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
+                     d, ldd, stride_d, bias, stride_bias, beta, epilogue, splits, workspace, workspace_bytes,
+                     rl::as_stream(stream));
+    });
+}
+
+RL_API std::size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, int splits) noexcept {
+    if (m <= 0 || n <= 0 || k <= 0 || batch <= 0 || splits <= 1) return 0;
+    const int kt = mode == 1 ? 32 : 16;
+    const int ktiles = (k + kt - 1) / kt;
+    if (splits > ktiles) splits = ktiles;
+    const int per = (ktiles + splits - 1) / splits;
+    splits = (ktiles + per - 1) / per;
+    if (splits <= 1) return 0;
+    return static_cast<std::size_t>(splits) * batch * m * n * sizeof(float);
+}

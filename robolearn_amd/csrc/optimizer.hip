@@ -1,0 +1,613 @@
+// One coalesced pass that fuses Adam, the unit-norm weight projection, the
+// target EMA and bf16 operand shadows over every tensor of a network.
+//
+// Reference semantics:
+//   Adam          torch.optim.Adam single-tensor path, as called from
+//                 robolearn/flashsac/agent.py:64-65 (form 0), or the native
+//                 bias-corrected form of robolearn/cuda/kernels.cu:310-337 (form 1).
+//   LR schedule   warmup + cosine, robolearn/flashsac/_utils/scheduler.py:43-65,
+//                 stepped after each optimizer step (agent.py:66-69, updates.py:151-153).
+//   Projection    unit Linear rows (layers.py:24-29, 185-186), BN affine pairs
+//                 (layers.py:57-64, 216-222), RMS scales (layers.py:76-81, 235-240),
+//                 robolearn/cuda/flash_kernels.cuh:112-131.
+//   EMA           target <- target + tau * (online - target), network.py:66-80.
+//
+// Work decomposition: one wavefront owns one projection unit (a weight row, one
+// BN (weight, bias) pair, one RMS vector) or one 1024-element chunk of a plain
+// tensor, so the row norm needed by the projection is a wave reduction and no
+// inter-workgroup communication is needed.  Pass 1 reads p, g, m1, m2, writes
+// the moments and the unprojected parameter and accumulates the row's squared
+// norm; pass 2 rereads the row (resident in L2), scales it, writes it, its bf16
+// shadow and the EMA target.  All scalar step state lives on the device, so a
+// step is graph-capturable.
+#include "common.hpp"
+
+#include <cmath>
+#include <memory>
+#include <vector>
+
+namespace rl {
+namespace opt {
+
+enum Kind : int { kUnitRow = 0, kBatchNormPair = 1, kRmsScale = 2, kPlain = 3 };
+constexpr int kChunk = 1024;
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+struct Part {
+    float* p;
+    const float* g;
+    float* m1;
+    float* m2;
+    float* target;
+    unsigned short* shadow;
+    unsigned short* target_shadow;
+};
+
+struct Tensor {
+    Part part[2];        // part[1] is the BN bias of a kBatchNormPair
+    long long rows;      // projection units (rows of a unit Linear, ensemble members of BN/RMS)
+    long long cols;      // elements per unit (plain: total elements, rows == 1)
+    int kind;
+    int vec4;
+};
+
+struct Work {
+    int tensor;
+    int unit;            // row, or chunk index for kPlain
+};
+
+struct Schedule {
+    int enabled;
+    double init, peak, end;
+    double warmup, decay;
+};
+
+struct Scalars {
+    float a;             // form 0: -lr / bc1          form 1: lr
+    float b;             // form 0: sqrt(bc2)          form 1: 1 / bc1
+    float c;             // form 1: 1 / bc2
+    float pad;
+};
+
+__device__ double schedule_value(const Schedule& s, double step) {
+    double value = s.end;
+    if (step < s.warmup) value = s.init + (s.peak - s.init) * (step / s.warmup);
+    else if (step < s.decay) {
+        const double progress = (step - s.warmup) / (s.decay - s.warmup);
+        value = s.end + (s.peak - s.end) * 0.5 * (1.0 + cos(M_PI * progress));
+    }
+    // LambdaLR scales the base (peak) rate by schedule / peak.
+    return s.peak * (value / s.peak);
+}
+
+__global__ void prepare(float* timestep, float* lr, Schedule schedule, double beta1, double beta2, int form,
+                        const int* skip, Scalars* out) {
+    if (skip && skip[0]) return;
+    const float t = timestep[0] + 1.0f;
+    timestep[0] = t;
+    double lr_used = lr[0];
+    if (schedule.enabled) {
+        lr_used = schedule_value(schedule, static_cast<double>(t) - 1.0);
+        lr[0] = static_cast<float>(schedule_value(schedule, static_cast<double>(t)));
+    }
+    Scalars s{};
+    if (form == 0) {
+        const double bc1 = 1.0 - pow(beta1, static_cast<double>(t));
+        const double bc2 = 1.0 - pow(beta2, static_cast<double>(t));
+        s.a = static_cast<float>(-(lr_used / bc1));
+        s.b = static_cast<float>(sqrt(bc2));
+    } else {
+        s.a = static_cast<float>(lr_used);
+        s.b = 1.0f / (1.0f - powf(static_cast<float>(beta1), t));
+        s.c = 1.0f / (1.0f - powf(static_cast<float>(beta2), t));
+    }
+    out[0] = s;
+}
+
+struct StepArgs {
+    const Tensor* tensors;
+    const Work* work;
+    int work_count;
+    const Scalars* scalars;
+    float beta1, beta2, one_minus_beta1, one_minus_beta2, eps, tau;
+    int form, do_adam, do_project, do_ema;
+    const int* skip;
+};
+
+__device__ __forceinline__ float adam_element(const StepArgs& a, const Scalars& s, float p, float g, float& m1, float& m2) {
+    if (a.form == 0) {
+        // exp_avg.lerp_(grad, 1 - beta1); exp_avg_sq.mul_(beta2).addcmul_(grad, grad, 1 - beta2)
+        m1 = m1 + a.one_minus_beta1 * (g - m1);
+        m2 = m2 * a.beta2 + a.one_minus_beta2 * g * g;
+        const float denom = sqrtf(m2) / s.b + a.eps;
+        return p + s.a * (m1 / denom);
+    }
+    m1 = a.beta1 * m1 + a.one_minus_beta1 * g;
+    m2 = a.beta2 * m2 + a.one_minus_beta2 * (g * g);
+    return p - s.a * ((m1 * s.b) / (sqrtf(m2 * s.c) + a.eps));
+}
+
+// Pass 1 over one contiguous span: optional Adam, returns the squared norm of
+// the resulting parameters.
+__device__ float update_span(const StepArgs& a, const Scalars& s, const Part& part, long long offset, long long length,
+                             bool vec4) {
+    const int lane = threadIdx.x % kWave;
+    float sumsq = 0.0f;
+    float* p = part.p + offset;
+    if (vec4) {
+        const long long n4 = length / 4;
+        for (long long i = lane; i < n4; i += kWave) {
+            float4 pv = reinterpret_cast<float4*>(p)[i];
+            if (a.do_adam) {
+                const float4 gv = reinterpret_cast<const float4*>(part.g + offset)[i];
+                float4 m1v = reinterpret_cast<float4*>(part.m1 + offset)[i];
+                float4 m2v = reinterpret_cast<float4*>(part.m2 + offset)[i];
+                pv.x = adam_element(a, s, pv.x, gv.x, m1v.x, m2v.x);
+                pv.y = adam_element(a, s, pv.y, gv.y, m1v.y, m2v.y);
+                pv.z = adam_element(a, s, pv.z, gv.z, m1v.z, m2v.z);
+                pv.w = adam_element(a, s, pv.w, gv.w, m1v.w, m2v.w);
+                reinterpret_cast<float4*>(part.m1 + offset)[i] = m1v;
+                reinterpret_cast<float4*>(part.m2 + offset)[i] = m2v;
+                reinterpret_cast<float4*>(p)[i] = pv;
+            }
+            sumsq += pv.x * pv.x + pv.y * pv.y + pv.z * pv.z + pv.w * pv.w;
+        }
+    } else {
+        for (long long i = lane; i < length; i += kWave) {
+            float pv = p[i];
+            if (a.do_adam) {
+                float m1 = part.m1[offset + i];
+                float m2 = part.m2[offset + i];
+                pv = adam_element(a, s, pv, part.g[offset + i], m1, m2);
+                part.m1[offset + i] = m1;
+                part.m2[offset + i] = m2;
+                p[i] = pv;
+            }
+            sumsq += pv * pv;
+        }
+    }
+    return sumsq;
+}
+
+// Pass 2: scale (projection), shadows and EMA.  mode 0 divides by factor
+// (unit rows, F.normalize), mode 1 multiplies (BN/RMS norm factors), mode 2
+// leaves values unchanged.
+__device__ void finish_span(const StepArgs& a, const Part& part, long long offset, long long length, bool vec4,
+                            int mode, float factor) {
+    const int lane = threadIdx.x % kWave;
+    const bool write_p = mode != 2;
+    if (!write_p && !part.shadow && !(a.do_ema && part.target)) return;
+    float* p = part.p + offset;
+    auto scale = [&](float v) { return mode == 0 ? v / factor : (mode == 1 ? v * factor : v); };
+    auto tail = [&](long long i, float v) {
+        if (part.shadow) part.shadow[offset + i] = f32_to_bf16_bits(v);
+        if (a.do_ema && part.target) {
+            float t = part.target[offset + i];
+            t = t + a.tau * (v - t);
+            part.target[offset + i] = t;
+            if (part.target_shadow) part.target_shadow[offset + i] = f32_to_bf16_bits(t);
+        }
+    };
+    if (vec4) {
+        const long long n4 = length / 4;
+        for (long long i = lane; i < n4; i += kWave) {
+            float4 v = reinterpret_cast<float4*>(p)[i];
+            if (write_p) {
+                v.x = scale(v.x);
+                v.y = scale(v.y);
+                v.z = scale(v.z);
+                v.w = scale(v.w);
+                reinterpret_cast<float4*>(p)[i] = v;
+            }
+            if (a.do_ema && part.target) {
+                float4 t = reinterpret_cast<float4*>(part.target + offset)[i];
+                t.x = t.x + a.tau * (v.x - t.x);
+                t.y = t.y + a.tau * (v.y - t.y);
+                t.z = t.z + a.tau * (v.z - t.z);
+                t.w = t.w + a.tau * (v.w - t.w);
+                reinterpret_cast<float4*>(part.target + offset)[i] = t;
+                if (part.target_shadow) {
+                    unsigned short* ts = part.target_shadow + offset + 4 * i;
+                    ts[0] = f32_to_bf16_bits(t.x);
+                    ts[1] = f32_to_bf16_bits(t.y);
+                    ts[2] = f32_to_bf16_bits(t.z);
+                    ts[3] = f32_to_bf16_bits(t.w);
+                }
+            }
+            if (part.shadow) {
+                unsigned short* sh = part.shadow + offset + 4 * i;
+                sh[0] = f32_to_bf16_bits(v.x);
+                sh[1] = f32_to_bf16_bits(v.y);
+                sh[2] = f32_to_bf16_bits(v.z);
+                sh[3] = f32_to_bf16_bits(v.w);
+            }
+        }
+    } else {
+        for (long long i = lane; i < length; i += kWave) {
+            float v = p[i];
+            if (write_p) {
+                v = scale(v);
+                p[i] = v;
+            }
+            tail(i, v);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void step_kernel(StepArgs a) {
+    if (a.skip && a.skip[0]) return;
+    const int item = static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x) / kWave;
+    if (item >= a.work_count) return;
+    const Work w = a.work[item];
+    const Tensor t = a.tensors[w.tensor];
+    const Scalars s = a.do_adam ? a.scalars[0] : Scalars{};
+    const bool vec4 = t.vec4 != 0;
+    if (t.kind == kPlain) {
+        const long long offset = static_cast<long long>(w.unit) * kChunk;
+        const long long length = min(static_cast<long long>(kChunk), t.cols - offset);
+        update_span(a, s, t.part[0], offset, length, vec4);
+        finish_span(a, t.part[0], offset, length, vec4, 2, 1.0f);
+        return;
+    }
+    const long long offset = static_cast<long long>(w.unit) * t.cols;
+    float sumsq = update_span(a, s, t.part[0], offset, t.cols, vec4);
+    if (t.kind == kBatchNormPair) sumsq += update_span(a, s, t.part[1], offset, t.cols, vec4);
+    sumsq = wave_sum(sumsq);
+    if (!a.do_project) {
+        finish_span(a, t.part[0], offset, t.cols, vec4, 2, 1.0f);
+        if (t.kind == kBatchNormPair) finish_span(a, t.part[1], offset, t.cols, vec4, 2, 1.0f);
+        return;
+    }
+    if (t.kind == kUnitRow) {
+        finish_span(a, t.part[0], offset, t.cols, vec4, 0, fmaxf(sqrtf(sumsq), 1.0e-8f));
+    } else {
+        const float factor = sqrtf(static_cast<float>(t.cols)) * (1.0f / sqrtf(sumsq + 1.0e-8f));
+        finish_span(a, t.part[0], offset, t.cols, vec4, 1, factor);
+        if (t.kind == kBatchNormPair) finish_span(a, t.part[1], offset, t.cols, vec4, 1, factor);
+    }
+}
+
+struct Plan {
+    Tensor* tensors = nullptr;
+    Work* work = nullptr;
+    Scalars* scalars = nullptr;
+    int work_count = 0;
+    float* timestep = nullptr;
+    float* lr = nullptr;
+    Schedule schedule{};
+    double beta1 = 0.9, beta2 = 0.999, eps = 1e-8;
+    float tau = 0.0f;
+    int form = 0;
+    int has_adam = 0;
+    int has_projection = 0;
+    int has_ema = 0;
+
+    ~Plan() {
+        if (tensors) (void)hipFree(tensors);
+        if (work) (void)hipFree(work);
+        if (scalars) (void)hipFree(scalars);
+    }
+};
+
+bool all_aligned16(const Part& part) {
+    auto ok = [](const void* q) { return q == nullptr || aligned(q, 16); };
+    return ok(part.p) && ok(part.g) && ok(part.m1) && ok(part.m2) && ok(part.target);
+}
+
+std::unique_ptr<Plan> build(std::vector<Tensor> tensors) {
+    require(!tensors.empty(), "Optimizer plan needs at least one tensor.");
+    std::vector<Work> work;
+    for (std::size_t i = 0; i < tensors.size(); ++i) {
+        Tensor& t = tensors[i];
+        require(t.rows > 0 && t.cols > 0, "Optimizer tensors must be nonempty.");
+        require(t.kind >= 0 && t.kind <= 3, "Unknown optimizer tensor kind.");
+        require(t.part[0].p != nullptr, "Optimizer tensor parameters must be nonnull.");
+        if (t.kind == kBatchNormPair) require(t.part[1].p != nullptr, "BN projection needs both weight and bias.");
+        bool vec = t.cols % 4 == 0 && all_aligned16(t.part[0]) && (t.kind != kBatchNormPair || all_aligned16(t.part[1]));
+        t.vec4 = vec ? 1 : 0;
+        if (t.kind == kPlain) {
+            const long long total = t.rows * t.cols;
+            t.cols = total;
+            t.rows = 1;
+            t.vec4 = (total % 4 == 0 && all_aligned16(t.part[0])) ? 1 : 0;
+            const long long chunks = (total + kChunk - 1) / kChunk;
+            for (long long c = 0; c < chunks; ++c) work.push_back({static_cast<int>(i), static_cast<int>(c)});
+        } else {
+            for (long long r = 0; r < t.rows; ++r) work.push_back({static_cast<int>(i), static_cast<int>(r)});
+        }
+        require(work.size() < static_cast<std::size_t>(std::numeric_limits<int>::max() / 2), "Too many optimizer work items.");
+    }
+    auto plan = std::make_unique<Plan>();
+    check_hip(hipMalloc(&plan->tensors, tensors.size() * sizeof(Tensor)), "Allocate optimizer tensor table");
+    check_hip(hipMalloc(&plan->work, work.size() * sizeof(Work)), "Allocate optimizer work table");
+    check_hip(hipMalloc(&plan->scalars, sizeof(Scalars)), "Allocate optimizer scalars");
+    check_hip(hipMemcpy(plan->tensors, tensors.data(), tensors.size() * sizeof(Tensor), hipMemcpyHostToDevice),
+              "Copy optimizer tensor table");
+    check_hip(hipMemcpy(plan->work, work.data(), work.size() * sizeof(Work), hipMemcpyHostToDevice),
+              "Copy optimizer work table");
+    check_hip(hipMemset(plan->scalars, 0, sizeof(Scalars)), "Clear optimizer scalars");
+    plan->work_count = static_cast<int>(work.size());
+    return plan;
+}
+
+void step(Plan* plan, int do_adam, int do_project, int do_ema, const int* skip, hipStream_t stream) {
+    require(plan != nullptr, "Optimizer plan is null.");
+    require(!do_adam || plan->has_adam, "This plan has no Adam state.");
+    if (do_adam) {
+        hipLaunchKernelGGL(prepare, dim3(1), dim3(1), 0, stream, plan->timestep, plan->lr, plan->schedule, plan->beta1,
+                           plan->beta2, plan->form, skip, plan->scalars);
+        check_launch("Launch optimizer prepare");
+    }
+    StepArgs a{};
+    a.tensors = plan->tensors;
+    a.work = plan->work;
+    a.work_count = plan->work_count;
+    a.scalars = plan->scalars;
+    a.beta1 = static_cast<float>(plan->beta1);
+    a.beta2 = static_cast<float>(plan->beta2);
+    a.one_minus_beta1 = static_cast<float>(1.0 - plan->beta1);
+    a.one_minus_beta2 = static_cast<float>(1.0 - plan->beta2);
+    a.eps = static_cast<float>(plan->eps);
+    a.tau = plan->tau;
+    a.form = plan->form;
+    a.do_adam = do_adam;
+    a.do_project = do_project;
+    a.do_ema = do_ema;
+    a.skip = skip;
+    hipLaunchKernelGGL(step_kernel, dim3(ceil_div(plan->work_count, kWaves)), dim3(kThreads), 0, stream, a);
+    check_launch("Launch fused optimizer step");
+}
+
+}  // namespace opt
+}  // namespace rl
+
+using rl::opt::Part;
+using rl::opt::Plan;
+using rl::opt::Tensor;
+
+// ---------------------------------------------------------------------------
+// Fused plan (no reference counterpart; replaces the sequence CudaAdam.step ->
+// CudaProjection.step -> CudaEMA.step of robolearn/warp/flashsac.py:645-649,
+// 788-789, 874-876, 927-929 with one pass).
+// ---------------------------------------------------------------------------
+RL_API void* rl_fused_optimizer_create(std::size_t count, const int* kinds, const long long* rows,
+                                       const long long* cols, void* const* params, const void* const* grads,
+                                       void* const* m1, void* const* m2, void* const* targets, void* const* shadows,
+                                       void* const* target_shadows, const int* partner, void* timestep,
+                                       void* learning_rate, double beta1, double beta2, double eps, double tau,
+                                       int form, int schedule_enabled, double lr_init, double lr_peak, double lr_end,
+                                       long long warmup_steps, long long decay_steps) noexcept {
+    return rl::guarded_ptr("rl_fused_optimizer_create", [&]() -> void* {
+        rl::require(count && kinds && rows && cols && params, "Fused optimizer requires nonempty tensor tables.");
+        rl::require(form == 0 || form == 1, "Optimizer form must be 0 (torch) or 1 (native).");
+        const bool adam = grads != nullptr;
+        if (adam) {
+            rl::require(m1 && m2 && timestep && learning_rate, "Adam needs moments, timestep and learning rate.");
+            rl::require(std::isfinite(beta1) && std::isfinite(beta2) && beta1 >= 0 && beta1 < 1 && beta2 >= 0 &&
+                            beta2 < 1 && eps > 0,
+                        "Adam betas must lie in [0,1) and epsilon must be positive.");
+        }
+        rl::require(std::isfinite(tau) && tau >= 0 && tau <= 1, "EMA tau must lie in [0, 1].");
+        if (schedule_enabled)
+            rl::require(lr_peak > 0 && decay_steps > 0 && warmup_steps >= 0 && warmup_steps < decay_steps,
+                        "Learning-rate schedule needs positive peak and warmup < decay.");
+        std::vector<Tensor> tensors;
+        std::vector<bool> is_partner(count, false);
+        if (partner)
+            for (std::size_t i = 0; i < count; ++i)
+                if (partner[i] >= 0) {
+                    rl::require(static_cast<std::size_t>(partner[i]) < count, "Partner index out of range.");
+                    is_partner[partner[i]] = true;
+                }
+        auto part_of = [&](std::size_t i) {
+            Part part{};
+            part.p = static_cast<float*>(params[i]);
+            part.g = adam ? static_cast<const float*>(grads[i]) : nullptr;
+            part.m1 = adam ? static_cast<float*>(m1[i]) : nullptr;
+            part.m2 = adam ? static_cast<float*>(m2[i]) : nullptr;
+            part.target = targets ? static_cast<float*>(targets[i]) : nullptr;
+            part.shadow = shadows ? static_cast<unsigned short*>(shadows[i]) : nullptr;
+            part.target_shadow = target_shadows ? static_cast<unsigned short*>(target_shadows[i]) : nullptr;
+            if (adam) rl::require(part.g && part.m1 && part.m2, "Adam tensors must be nonnull.");
+            return part;
+        };
+        bool has_projection = false, has_ema = false;
+        for (std::size_t i = 0; i < count; ++i) {
+            if (is_partner[i]) continue;
+            Tensor t{};
+            t.kind = kinds[i];
+            t.rows = rows[i];
+            t.cols = cols[i];
+            t.part[0] = part_of(i);
+            if (t.kind == rl::opt::kBatchNormPair) {
+                rl::require(partner && partner[i] >= 0, "BN pair needs a partner bias tensor.");
+                const std::size_t j = static_cast<std::size_t>(partner[i]);
+                rl::require(rows[j] == rows[i] && cols[j] == cols[i], "BN weight and bias shapes differ.");
+                t.part[1] = part_of(j);
+            }
+            has_projection = has_projection || t.kind != rl::opt::kPlain;
+            has_ema = has_ema || t.part[0].target != nullptr;
+            tensors.push_back(t);
+        }
+        auto plan = rl::opt::build(std::move(tensors));
+        plan->timestep = static_cast<float*>(timestep);
+        plan->lr = static_cast<float*>(learning_rate);
+        plan->beta1 = beta1;
+        plan->beta2 = beta2;
+        plan->eps = eps;
+        plan->tau = static_cast<float>(tau);
+        plan->form = form;
+        plan->has_adam = adam;
+        plan->has_projection = has_projection;
+        plan->has_ema = has_ema;
+        plan->schedule.enabled = schedule_enabled;
+        plan->schedule.init = lr_init;
+        plan->schedule.peak = lr_peak;
+        plan->schedule.end = lr_end;
+        plan->schedule.warmup = static_cast<double>(warmup_steps);
+        plan->schedule.decay = static_cast<double>(decay_steps);
+        return plan.release();
+    });
+}
+
+RL_API int rl_fused_optimizer_step(void* plan, int do_adam, int do_project, int do_ema, const void* skip,
+                                   void* stream) noexcept {
+    return rl::guarded("rl_fused_optimizer_step", [&] {
+        rl::opt::step(static_cast<Plan*>(plan), do_adam, do_project, do_ema, static_cast<const int*>(skip),
+                      rl::as_stream(stream));
+    });
+}
+
+RL_API int rl_fused_optimizer_destroy(void* plan) noexcept {
+    rl::clear_error();
+    delete static_cast<Plan*>(plan);
+    return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Reference-compatible plans.
+// ---------------------------------------------------------------------------
+
+// robolearn/cuda/kernels.cu:760-820, 878-916: native-form Adam over a pointer
+// table, device float timestep and learning rate.
+RL_API void* rl_adam_create(std::size_t count, const void* const* parameters, const void* const* gradients,
+                            const void* const* m1, const void* const* m2, const std::size_t* sizes, void* timestep,
+                            void* learning_rate, double beta1, double beta2, double eps) noexcept {
+    return rl::guarded_ptr("rl_adam_create", [&]() -> void* {
+        rl::require(count && parameters && gradients && m1 && m2 && sizes && timestep && learning_rate,
+                    "Adam requires nonempty host pointer tables and device step/lr buffers.");
+        rl::require(std::isfinite(beta1) && std::isfinite(beta2) && std::isfinite(eps) && beta1 >= 0.0 &&
+                        beta1 < 1.0 && beta2 >= 0.0 && beta2 < 1.0 && eps > 0.0,
+                    "Adam betas must lie in [0,1) and epsilon must be positive.");
+        std::vector<Tensor> tensors;
+        for (std::size_t i = 0; i < count; ++i) {
+            rl::require(parameters[i] && gradients[i] && m1[i] && m2[i] && sizes[i] > 0,
+                        "Adam tensors must be nonnull and nonempty.");
+            Tensor t{};
+            t.kind = rl::opt::kPlain;
+            t.rows = 1;
+            t.cols = static_cast<long long>(sizes[i]);
+            t.part[0].p = static_cast<float*>(const_cast<void*>(parameters[i]));
+            t.part[0].g = static_cast<const float*>(gradients[i]);
+            t.part[0].m1 = static_cast<float*>(const_cast<void*>(m1[i]));
+            t.part[0].m2 = static_cast<float*>(const_cast<void*>(m2[i]));
+            tensors.push_back(t);
+        }
+        auto plan = rl::opt::build(std::move(tensors));
+        plan->timestep = static_cast<float*>(timestep);
+        plan->lr = static_cast<float*>(learning_rate);
+        plan->beta1 = beta1;
+        plan->beta2 = beta2;
+        plan->eps = eps;
+        plan->form = 1;
+        plan->has_adam = 1;
+        return plan.release();
+    });
+}
+
+RL_API int rl_adam_step(void* plan, void* stream) noexcept {
+    return rl::guarded("rl_adam_step", [&] { rl::opt::step(static_cast<Plan*>(plan), 1, 0, 0, nullptr, rl::as_stream(stream)); });
+}
+
+RL_API int rl_adam_destroy(void* plan) noexcept {
+    rl::clear_error();
+    delete static_cast<Plan*>(plan);
+    return 0;
+}
+
+// robolearn/cuda/flash_kernels.cuh:398-445: one descriptor per unit row
+// (kind 0), BN (weight, bias) pair (kind 1) or RMS scale (kind 2); optional
+// shadows receive the 16-bit copy (bf16 here) of the projected first vector.
+static void* create_projection(std::size_t count, const void* const* first, const void* const* second,
+                               const std::size_t* lengths, const int* kinds, const void* const* shadows) {
+    rl::require(count && first && lengths && kinds, "Projection requires nonempty host tables.");
+    std::vector<Tensor> tensors;
+    for (std::size_t i = 0; i < count; ++i) {
+        rl::require(first[i] && lengths[i] > 0 && kinds[i] >= 0 && kinds[i] <= 2,
+                    "Projection descriptors need nonnull rows, positive lengths and kinds 0..2.");
+        rl::require(kinds[i] != 1 || (second && second[i]), "BN projection needs a bias vector.");
+        Tensor t{};
+        t.kind = kinds[i];
+        t.rows = 1;
+        t.cols = static_cast<long long>(lengths[i]);
+        t.part[0].p = static_cast<float*>(const_cast<void*>(first[i]));
+        t.part[0].shadow = shadows ? static_cast<unsigned short*>(const_cast<void*>(shadows[i])) : nullptr;
+        if (kinds[i] == 1) t.part[1].p = static_cast<float*>(const_cast<void*>(second[i]));
+        tensors.push_back(t);
+    }
+    auto plan = rl::opt::build(std::move(tensors));
+    plan->has_projection = 1;
+    return plan.release();
+}
+
+RL_API void* rl_flash_projection_create(std::size_t count, const void* const* first, const void* const* second,
+                                        const std::size_t* lengths, const int* kinds) noexcept {
+    return rl::guarded_ptr("rl_flash_projection_create",
+                           [&]() -> void* { return create_projection(count, first, second, lengths, kinds, nullptr); });
+}
+
+RL_API void* rl_flash_projection_create_with_shadows(std::size_t count, const void* const* first,
+                                                     const void* const* second, const std::size_t* lengths,
+                                                     const int* kinds, const void* const* shadows) noexcept {
+    return rl::guarded_ptr("rl_flash_projection_create_with_shadows",
+                           [&]() -> void* { return create_projection(count, first, second, lengths, kinds, shadows); });
+}
+
+RL_API int rl_flash_projection_step(void* plan, void* stream) noexcept {
+    return rl::guarded("rl_flash_projection_step",
+                       [&] { rl::opt::step(static_cast<Plan*>(plan), 0, 1, 0, nullptr, rl::as_stream(stream)); });
+}
+
+RL_API int rl_flash_projection_destroy(void* plan) noexcept {
+    rl::clear_error();
+    delete static_cast<Plan*>(plan);
+    return 0;
+}
+
+// robolearn/cuda/flash_kernels.cuh:447-498: target = (1 - tau) target + tau source.
+static void* create_ema(std::size_t count, const void* const* source, const void* const* target,
+                        const std::size_t* lengths, float tau, const void* const* shadows) {
+    rl::require(count && source && target && lengths, "EMA requires nonempty host tables.");
+    rl::require(std::isfinite(tau) && tau >= 0.0f && tau <= 1.0f, "EMA tau must lie in [0, 1].");
+    std::vector<Tensor> tensors;
+    for (std::size_t i = 0; i < count; ++i) {
+        rl::require(source[i] && target[i] && lengths[i] > 0, "EMA descriptors need nonnull buffers.");
+        Tensor t{};
+        t.kind = rl::opt::kPlain;
+        t.rows = 1;
+        t.cols = static_cast<long long>(lengths[i]);
+        t.part[0].p = static_cast<float*>(const_cast<void*>(source[i]));
+        t.part[0].target = static_cast<float*>(const_cast<void*>(target[i]));
+        t.part[0].target_shadow = shadows ? static_cast<unsigned short*>(const_cast<void*>(shadows[i])) : nullptr;
+        tensors.push_back(t);
+    }
+    auto plan = rl::opt::build(std::move(tensors));
+    plan->tau = tau;
+    plan->has_ema = 1;
+    return plan.release();
+}
+
+RL_API void* rl_flash_ema_create(std::size_t count, const void* const* source, const void* const* target,
+                                 const std::size_t* lengths, float tau) noexcept {
+    return rl::guarded_ptr("rl_flash_ema_create",
+                           [&]() -> void* { return create_ema(count, source, target, lengths, tau, nullptr); });
+}
+
+RL_API void* rl_flash_ema_create_with_shadows(std::size_t count, const void* const* source, const void* const* target,
+                                              const std::size_t* lengths, float tau,
+                                              const void* const* shadows) noexcept {
+    return rl::guarded_ptr("rl_flash_ema_create_with_shadows",
+                           [&]() -> void* { return create_ema(count, source, target, lengths, tau, shadows); });
+}
+
+RL_API int rl_flash_ema_step(void* plan, void* stream) noexcept {
+    return rl::guarded("rl_flash_ema_step",
+                       [&] { rl::opt::step(static_cast<Plan*>(plan), 0, 0, 1, nullptr, rl::as_stream(stream)); });
+}
+
+RL_API int rl_flash_ema_destroy(void* plan) noexcept {
+    rl::clear_error();
+    delete static_cast<Plan*>(plan);
+    return 0;
+}

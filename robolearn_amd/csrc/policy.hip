@@ -1,0 +1,482 @@
+// Tanh-Gaussian policy head, actor/temperature objectives, replay sampling
+// and gather, counter-based random numbers and small glue kernels.
+//
+// Reference semantics:
+//   policy head  NormalTanhPolicy, robolearn/flashsac/layers.py:116-166:
+//                log_std = -10 + 6 (1 + tanh(raw)), std = exp(log_std),
+//                raw_a = mean + std eps, a = tanh(raw_a),
+//                log pi = sum_j Normal(mean, std).log_prob(raw_a)
+//                         - 2 (ln 2 - raw_a - softplus(-2 raw_a))
+//                (robolearn/flashsac/_utils/distribution.py:12-19).
+//   actor loss   robolearn/flashsac/updates.py:105-137 (torch.minimum splits
+//                its derivative equally at ties, as robolearn/warp/flashsac.py:140-145).
+//   temperature  updates.py:297-326.
+//   replay       TorchUniformBuffer.sample, robolearn/flashsac/replay.py:179-194.
+//
+// Random numbers: Philox-4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random
+// numbers: as easy as 1, 2, 3", SC 2011) keyed by a 64-bit seed, with the
+// counter built from (element block, device draw counter, stream id).  Normal
+// variates use the Box-Muller transform.  The draw counter lives in device
+// memory and is advanced by a kernel, so captured graphs draw fresh numbers on
+// every replay.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace rl {
+namespace policy {
+
+__device__ __forceinline__ void mulhilo(unsigned int a, unsigned int b, unsigned int& hi, unsigned int& lo) {
+    const unsigned long long p = static_cast<unsigned long long>(a) * b;
+    hi = static_cast<unsigned int>(p >> 32);
+    lo = static_cast<unsigned int>(p);
+}
+
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
+#pragma unroll
+    for (int round = 0; round < 10; ++round) {
+        unsigned int hi0, lo0, hi1, lo1;
+        mulhilo(0xD2511F53u, c.x, hi0, lo0);
+        mulhilo(0xCD9E8D57u, c.z, hi1, lo1);
+        c = make_uint4(hi1 ^ c.y ^ k.x, lo1, hi0 ^ c.w ^ k.y, lo0);
+        k.x += 0x9E3779B9u;
+        k.y += 0xBB67AE85u;
+    }
+    return c;
+}
+
+__device__ __forceinline__ float uniform_open0(unsigned int x) {  // (0, 1]
+    return (static_cast<float>(x >> 8) + 1.0f) * (1.0f / 16777216.0f);
+}
+__device__ __forceinline__ float uniform01(unsigned int x) {  // [0, 1)
+    return static_cast<float>(x >> 8) * (1.0f / 16777216.0f);
+}
+
+// out[i] ~ N(0, 1) for i < n.  Four variates per Philox block.
+__global__ void normal_kernel(unsigned long long seed, const long long* counter, unsigned int stream_id, float* out,
+                              long long n) {
+    const long long block = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    const long long first = block * 4;
+    if (first >= n) return;
+    const unsigned long long draw = static_cast<unsigned long long>(counter ? counter[0] : 0);
+    const uint4 c = make_uint4(static_cast<unsigned int>(block), static_cast<unsigned int>(draw),
+                               static_cast<unsigned int>(draw >> 32), stream_id);
+    const uint4 r = philox4x32_10(c, make_uint2(static_cast<unsigned int>(seed), static_cast<unsigned int>(seed >> 32)));
+    const float two_pi = 6.28318530717958647692f;
+    const float r0 = sqrtf(-2.0f * logf(uniform_open0(r.x)));
+    const float r1 = sqrtf(-2.0f * logf(uniform_open0(r.z)));
+    float s0, c0, s1, c1;
+    sincosf(two_pi * uniform01(r.y), &s0, &c0);
+    sincosf(two_pi * uniform01(r.w), &s1, &c1);
+    const float v[4] = {r0 * c0, r0 * s0, r1 * c1, r1 * s1};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (first + i < n) out[first + i] = v[i];
+}
+
+// idx[i] uniform in [0, count) by 32x64-bit multiply-high of a Philox word.
+__global__ void sample_indices(unsigned long long seed, const long long* counter, unsigned int stream_id,
+                               const long long* count, long long fixed_count, long long* idx, long long n) {
+    const long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (i >= n) return;
+    const unsigned long long draw = static_cast<unsigned long long>(counter ? counter[0] : 0);
+    const uint4 c = make_uint4(static_cast<unsigned int>(i), static_cast<unsigned int>(i >> 32),
+                               static_cast<unsigned int>(draw), stream_id ^ (static_cast<unsigned int>(draw >> 32) << 16));
+    const uint4 r = philox4x32_10(c, make_uint2(static_cast<unsigned int>(seed), static_cast<unsigned int>(seed >> 32)));
+    const unsigned long long limit = static_cast<unsigned long long>(count ? count[0] : fixed_count);
+    const unsigned long long word = (static_cast<unsigned long long>(r.x) << 32) | r.y;
+    // 64-bit multiply-high maps the uniform word onto [0, limit).
+    idx[i] = static_cast<long long>(__umul64hi(word, limit));
+}
+
+// batch_x[i, :] = store_x[idx[i], :] for the seven replay fields.
+struct GatherArgs {
+    const long long* idx;
+    long long batch;
+    const float* obs;
+    const float* next_obs;
+    const float* action;
+    const float* reward;
+    const float* terminated;
+    const float* truncated;
+    const float* discount;
+    float* out_obs;
+    float* out_next_obs;
+    float* out_action;
+    float* out_reward;
+    float* out_terminated;
+    float* out_truncated;
+    float* out_discount;
+    int obs_dim, action_dim;
+    long long capacity;
+    int* error;
+};
+
+__global__ void gather_kernel(GatherArgs a) {
+    const long long i = blockIdx.y;
+    if (i >= a.batch) return;
+    long long k = a.idx[i];
+    if (k < 0 || k >= a.capacity) {
+        if (threadIdx.x == 0 && blockIdx.x == 0 && a.error) atomicExch(a.error, 1);
+        k = 0;
+    }
+    const int width = 2 * a.obs_dim + a.action_dim + 4;
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < width; j += gridDim.x * blockDim.x) {
+        if (j < a.obs_dim) a.out_obs[i * a.obs_dim + j] = a.obs[k * a.obs_dim + j];
+        else if (j < 2 * a.obs_dim) {
+            const int c = j - a.obs_dim;
+            a.out_next_obs[i * a.obs_dim + c] = a.next_obs[k * a.obs_dim + c];
+        } else if (j < 2 * a.obs_dim + a.action_dim) {
+            const int c = j - 2 * a.obs_dim;
+            a.out_action[i * a.action_dim + c] = a.action[k * a.action_dim + c];
+        } else {
+            const int f = j - 2 * a.obs_dim - a.action_dim;
+            if (f == 0) a.out_reward[i] = a.reward[k];
+            else if (f == 1) a.out_terminated[i] = a.terminated[k];
+            else if (f == 2) {
+                if (a.out_truncated) a.out_truncated[i] = a.truncated ? a.truncated[k] : 0.0f;
+            } else a.out_discount[i] = a.discount[k];
+        }
+    }
+}
+
+// out[r, :] = [a[r, :ca], b[r, :cb]] for rows r; b may be null (cb == 0).
+__global__ void concat_kernel(float* out, long long ld_out, long long rows, const float* a, long long lda, int ca,
+                              const float* b, long long ldb, int cb) {
+    const long long total = rows * (ca + cb);
+    for (long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; idx < total;
+         idx += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const long long r = idx / (ca + cb);
+        const int c = static_cast<int>(idx % (ca + cb));
+        out[r * ld_out + c] = c < ca ? a[r * lda + c] : b[r * ldb + (c - ca)];
+    }
+}
+
+__device__ __forceinline__ float softplus(float x) {
+    // torch.nn.functional.softplus with beta 1 and threshold 20.
+    return x > 20.0f ? x : log1pf(expf(x));
+}
+
+// head[r, :A] = mean, head[r, A:2A] = raw log-std (bias already added).
+// Writes actions (ld_actions stride), log pi and optionally std.
+__global__ void tanh_gaussian_forward(const float* head, const float* noise, float* actions, long long ld_actions,
+                                      float* log_probs, long long rows, int action_dim, int deterministic) {
+    const long long r = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (r >= rows) return;
+    const float* h = head + r * 2 * action_dim;
+    const float half_log_two_pi = 0.91893853320467274178f;  // log(sqrt(2 pi))
+    const float ln2 = 0.69314718055994530942f;
+    float lp = 0.0f;
+    for (int j = 0; j < action_dim; ++j) {
+        const float mean = h[j];
+        if (deterministic) {
+            actions[r * ld_actions + j] = tanhf(mean);
+            continue;
+        }
+        const float log_std = -10.0f + 6.0f * (1.0f + tanhf(h[action_dim + j]));
+        const float std = expf(log_std);
+        const float eps = noise[r * action_dim + j];
+        const float raw = mean + eps * std;
+        actions[r * ld_actions + j] = tanhf(raw);
+        const float diff = raw - mean;
+        const float log_normal = -(diff * diff) / (2.0f * (std * std)) - logf(std) - half_log_two_pi;
+        const float correction = 2.0f * (ln2 - raw - softplus(-2.0f * raw));
+        lp += log_normal - correction;
+    }
+    if (log_probs && !deterministic) log_probs[r] = lp;
+}
+
+// Backward of the head given dL/da (rows < grad_rows, else zero) and dL/dlogpi.
+// dhead[r, :A] = dL/dmean, dhead[r, A:] = dL/draw_log_std.
+__global__ void tanh_gaussian_backward(const float* head, const float* noise, const float* dactions,
+                                       long long ld_dactions, long long grad_rows, const float* dlog_probs,
+                                       float* dhead, long long rows, int action_dim) {
+    const long long r = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (r >= rows) return;
+    const float* h = head + r * 2 * action_dim;
+    const float dlp = dlog_probs ? dlog_probs[r] : 0.0f;
+    for (int j = 0; j < action_dim; ++j) {
+        const float mean = h[j];
+        const float t = tanhf(h[action_dim + j]);
+        const float log_std = -10.0f + 6.0f * (1.0f + t);
+        const float std = expf(log_std);
+        const float eps = noise[r * action_dim + j];
+        const float raw = mean + eps * std;
+        const float a = tanhf(raw);
+        const float da = (dactions && r < grad_rows) ? dactions[r * ld_dactions + j] : 0.0f;
+        const float g_raw = da * (1.0f - a * a) + dlp * 2.0f * a;
+        const float dstd = g_raw * eps - dlp / std;
+        const float dlog_std = dstd * std;
+        dhead[r * 2 * action_dim + j] = g_raw;
+        dhead[r * 2 * action_dim + action_dim + j] = dlog_std * 6.0f * (1.0f - t * t);
+    }
+}
+
+// Single-workgroup actor objective over the first `batch` rows:
+//   q = min(q0, q1); loss = mean(alpha logpi - q) [+ bc term];
+//   entropy = -mean(logpi); mean_action = mean(a).
+// Gradients: dlogpi (2B rows, zero past batch), dq [2, batch], daction_bc
+// (optional, batch x A) for the behaviour-cloning term.
+constexpr int kObjThreads = 1024;
+
+__device__ float block_sum_1024(float v, float* s) {
+    s[threadIdx.x] = v;
+    __syncthreads();
+    for (int stride = kObjThreads / 2; stride > 0; stride >>= 1) {
+        if (static_cast<int>(threadIdx.x) < stride) s[threadIdx.x] += s[threadIdx.x + stride];
+        __syncthreads();
+    }
+    const float total = s[0];
+    __syncthreads();
+    return total;
+}
+
+__global__ __launch_bounds__(kObjThreads) void actor_objective(const float* q0, const float* q1, const float* log_probs,
+                                                               const float* actions, long long ld_actions,
+                                                               const float* replay_actions, const float* alpha,
+                                                               float bc_alpha, long long batch, long long total_rows,
+                                                               int action_dim, float* metrics, float* dlog_probs,
+                                                               float* dq0, float* dq1, float* dactions_bc) {
+    __shared__ float s[kObjThreads];
+    const float a = alpha[0];
+    const float inv = 1.0f / static_cast<float>(batch);
+    float qabs = 0.0f, lp_sum = 0.0f, act_sum = 0.0f, bc_sum = 0.0f;
+    for (long long i = threadIdx.x; i < batch; i += kObjThreads) {
+        const float q = fminf(q0[i], q1[i]);
+        qabs += fabsf(q);
+        lp_sum += log_probs[i];
+        for (int j = 0; j < action_dim; ++j) act_sum += actions[i * ld_actions + j];
+        if (bc_alpha > 0.0f) {
+            for (int j = 0; j < action_dim; ++j) {
+                const float d = actions[i * ld_actions + j] - replay_actions[i * action_dim + j];
+                bc_sum += d * d;
+            }
+        }
+    }
+    qabs = block_sum_1024(qabs, s) * inv;
+    lp_sum = block_sum_1024(lp_sum, s);
+    act_sum = block_sum_1024(act_sum, s);
+    bc_sum = block_sum_1024(bc_sum, s);
+    float loss_sum = 0.0f;
+    for (long long i = threadIdx.x; i < batch; i += kObjThreads) {
+        const float x0 = q0[i], x1 = q1[i];
+        const float q = fminf(x0, x1);
+        loss_sum += a * log_probs[i] - q;
+        dlog_probs[i] = a * inv;
+        dq0[i] = -inv * (x0 < x1 ? 1.0f : (x0 == x1 ? 0.5f : 0.0f));
+        dq1[i] = -inv * (x1 < x0 ? 1.0f : (x0 == x1 ? 0.5f : 0.0f));
+        if (dactions_bc) {
+            for (int j = 0; j < action_dim; ++j) {
+                const float d = actions[i * ld_actions + j] - replay_actions[i * action_dim + j];
+                dactions_bc[i * action_dim + j] =
+                    bc_alpha > 0.0f ? bc_alpha * qabs * 2.0f * d / static_cast<float>(batch * action_dim) : 0.0f;
+            }
+        }
+    }
+    for (long long i = batch + threadIdx.x; i < total_rows; i += kObjThreads) dlog_probs[i] = 0.0f;
+    loss_sum = block_sum_1024(loss_sum, s);
+    if (threadIdx.x == 0) {
+        float loss = loss_sum * inv;
+        if (bc_alpha > 0.0f) loss += bc_alpha * qabs * (bc_sum / static_cast<float>(batch * action_dim));
+        metrics[0] = loss;
+        metrics[1] = -lp_sum * inv;
+        metrics[2] = act_sum / static_cast<float>(batch * action_dim);
+    }
+}
+
+// Temperature objective: value = exp(log_temp); loss = value (entropy - H*);
+// d loss / d log_temp = loss.  metrics[0] = loss, metrics[1] = value.
+__global__ void temperature_objective(const float* log_temp, const float* entropy, float target_entropy,
+                                      float* grad, float* metrics) {
+    const float value = expf(log_temp[0]);
+    const float loss = value * (entropy[0] - target_entropy);
+    grad[0] = loss;
+    metrics[0] = loss;
+    metrics[1] = value;
+}
+
+__global__ void exp_scalar(const float* x, float* out) { out[0] = expf(x[0]); }
+
+__global__ void fill_kernel(float* x, long long n, float value) {
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<long long>(gridDim.x) * blockDim.x)
+        x[i] = value;
+}
+
+__global__ void add_kernel(float* x, const float* y, long long n) {
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<long long>(gridDim.x) * blockDim.x)
+        x[i] += y[i];
+}
+
+// counters[0] += 1 (updates), counters[1..2] += actor (actor, temperature).
+__global__ void advance_counters(long long* counters, int actor) {
+    counters[0] += 1;
+    counters[1] += actor;
+    counters[2] += actor;
+}
+
+// rewards[i] *= 1 / max(sqrt(var + eps), G_r_max / G_max) (reward_normalization.py:28-38).
+__global__ void scale_rewards(float* rewards, long long n, const float* var, const float* r_max, float g_max, float eps) {
+    const long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (i >= n) return;
+    const float denominator = fmaxf(sqrtf(var[0] + eps), r_max[0] / g_max);
+    rewards[i] = rewards[i] / denominator;
+}
+
+inline unsigned blocks_for(long long n, int threads = 256) {
+    return static_cast<unsigned>(std::max<long long>(1, std::min<long long>((n + threads - 1) / threads, 65536)));
+}
+
+}  // namespace policy
+}  // namespace rl
+
+namespace P = rl::policy;
+
+RL_API int rl_philox_normal(unsigned long long seed, const long long* counter, unsigned int stream_id, float* out,
+                            long long n, void* stream) noexcept {
+    return rl::guarded("rl_philox_normal", [&] {
+        rl::require(out && n > 0, "Normal sampling needs a nonempty output.");
+        const long long blocks = (n + 3) / 4;
+        hipLaunchKernelGGL(P::normal_kernel, dim3(rl::ceil_div(blocks, 256)), dim3(256), 0, rl::as_stream(stream),
+                           seed, counter, stream_id, out, n);
+        rl::check_launch("Launch normal sampling");
+    });
+}
+
+RL_API int rl_replay_sample_indices(unsigned long long seed, const long long* counter, unsigned int stream_id,
+                                    const long long* count, long long fixed_count, long long* idx, long long n,
+                                    void* stream) noexcept {
+    return rl::guarded("rl_replay_sample_indices", [&] {
+        rl::require(idx && n > 0 && (count || fixed_count > 0), "Index sampling needs an output and a positive count.");
+        hipLaunchKernelGGL(P::sample_indices, dim3(rl::ceil_div(n, 256)), dim3(256), 0, rl::as_stream(stream), seed,
+                           counter, stream_id, count, fixed_count, idx, n);
+        rl::check_launch("Launch index sampling");
+    });
+}
+
+RL_API int rl_replay_gather(const long long* idx, long long batch, long long capacity, int obs_dim, int action_dim,
+                            const float* obs, const float* next_obs, const float* action, const float* reward,
+                            const float* terminated, const float* truncated, const float* discount, float* out_obs,
+                            float* out_next_obs, float* out_action, float* out_reward, float* out_terminated,
+                            float* out_truncated, float* out_discount, int* error, void* stream) noexcept {
+    return rl::guarded("rl_replay_gather", [&] {
+        rl::require(idx && batch > 0 && capacity > 0 && obs_dim > 0 && action_dim > 0, "Gather needs indices and shapes.");
+        rl::require(obs && next_obs && action && reward && terminated && discount && out_obs && out_next_obs &&
+                        out_action && out_reward && out_terminated && out_discount,
+                    "Gather needs every storage and output field.");
+        rl::require(batch <= 65535, "Gather batch must not exceed 65535 rows per launch.");
+        P::GatherArgs a{idx, batch, obs, next_obs, action, reward, terminated, truncated, discount, out_obs,
+                        out_next_obs, out_action, out_reward, out_terminated, out_truncated, out_discount, obs_dim,
+                        action_dim, capacity, error};
+        const int width = 2 * obs_dim + action_dim + 4;
+        hipLaunchKernelGGL(P::gather_kernel, dim3(rl::ceil_div(width, 256), static_cast<unsigned>(batch)), dim3(256), 0,
+                           rl::as_stream(stream), a);
+        rl::check_launch("Launch replay gather");
+    });
+}
+
+RL_API int rl_concat_columns(float* out, long long ld_out, long long rows, const float* a, long long lda, int ca,
+                             const float* b, long long ldb, int cb, void* stream) noexcept {
+    return rl::guarded("rl_concat_columns", [&] {
+        rl::require(out && a && rows > 0 && ca > 0 && cb >= 0 && (cb == 0 || b) && ld_out >= ca + cb,
+                    "Concatenation needs valid buffers and widths.");
+        hipLaunchKernelGGL(P::concat_kernel, dim3(P::blocks_for(rows * (ca + cb))), dim3(256), 0,
+                           rl::as_stream(stream), out, ld_out, rows, a, lda, ca, b, ldb, cb);
+        rl::check_launch("Launch concatenation");
+    });
+}
+
+RL_API int rl_tanh_gaussian_forward(const float* head, const float* noise, float* actions, long long ld_actions,
+                                    float* log_probs, long long rows, int action_dim, int deterministic,
+                                    void* stream) noexcept {
+    return rl::guarded("rl_tanh_gaussian_forward", [&] {
+        rl::require(head && actions && rows > 0 && action_dim > 0 && (deterministic || noise),
+                    "Policy forward needs head, noise and actions.");
+        hipLaunchKernelGGL(P::tanh_gaussian_forward, dim3(rl::ceil_div(rows, 256)), dim3(256), 0,
+                           rl::as_stream(stream), head, noise, actions, ld_actions, log_probs, rows, action_dim,
+                           deterministic);
+        rl::check_launch("Launch policy forward");
+    });
+}
+
+RL_API int rl_tanh_gaussian_backward(const float* head, const float* noise, const float* dactions,
+                                     long long ld_dactions, long long grad_rows, const float* dlog_probs, float* dhead,
+                                     long long rows, int action_dim, void* stream) noexcept {
+    return rl::guarded("rl_tanh_gaussian_backward", [&] {
+        rl::require(head && noise && dhead && rows > 0 && action_dim > 0, "Policy backward needs head, noise and dhead.");
+        hipLaunchKernelGGL(P::tanh_gaussian_backward, dim3(rl::ceil_div(rows, 256)), dim3(256), 0,
+                           rl::as_stream(stream), head, noise, dactions, ld_dactions, grad_rows, dlog_probs, dhead,
+                           rows, action_dim);
+        rl::check_launch("Launch policy backward");
+    });
+}
+
+RL_API int rl_actor_objective(const float* q0, const float* q1, const float* log_probs, const float* actions,
+                              long long ld_actions, const float* replay_actions, const float* alpha, float bc_alpha,
+                              long long batch, long long total_rows, int action_dim, float* metrics, float* dlog_probs,
+                              float* dq0, float* dq1, float* dactions_bc, void* stream) noexcept {
+    return rl::guarded("rl_actor_objective", [&] {
+        rl::require(q0 && q1 && log_probs && actions && alpha && metrics && dlog_probs && dq0 && dq1,
+                    "Actor objective needs Q values, log-probs, actions, alpha and outputs.");
+        rl::require(batch > 0 && total_rows >= batch && action_dim > 0, "Actor objective shapes are invalid.");
+        rl::require(bc_alpha <= 0.0f || replay_actions, "Behaviour cloning needs replay actions.");
+        hipLaunchKernelGGL(P::actor_objective, dim3(1), dim3(P::kObjThreads), 0, rl::as_stream(stream), q0, q1,
+                           log_probs, actions, ld_actions, replay_actions, alpha, bc_alpha, batch, total_rows,
+                           action_dim, metrics, dlog_probs, dq0, dq1, dactions_bc);
+        rl::check_launch("Launch actor objective");
+    });
+}
+
+RL_API int rl_temperature_objective(const float* log_temp, const float* entropy, float target_entropy, float* grad,
+                                    float* metrics, void* stream) noexcept {
+    return rl::guarded("rl_temperature_objective", [&] {
+        rl::require(log_temp && entropy && grad && metrics, "Temperature objective needs all buffers.");
+        hipLaunchKernelGGL(P::temperature_objective, dim3(1), dim3(1), 0, rl::as_stream(stream), log_temp, entropy,
+                           target_entropy, grad, metrics);
+        rl::check_launch("Launch temperature objective");
+    });
+}
+
+RL_API int rl_exp_scalar(const float* x, float* out, void* stream) noexcept {
+    return rl::guarded("rl_exp_scalar", [&] {
+        rl::require(x && out, "exp needs buffers.");
+        hipLaunchKernelGGL(P::exp_scalar, dim3(1), dim3(1), 0, rl::as_stream(stream), x, out);
+        rl::check_launch("Launch exp");
+    });
+}
+
+// Graph-safe fill (a kernel, never a memset node).
+RL_API int rl_fill(float* x, long long n, float value, void* stream) noexcept {
+    return rl::guarded("rl_fill", [&] {
+        rl::require(x && n > 0, "Fill needs a nonempty buffer.");
+        hipLaunchKernelGGL(P::fill_kernel, dim3(P::blocks_for(n)), dim3(256), 0, rl::as_stream(stream), x, n, value);
+        rl::check_launch("Launch fill");
+    });
+}
+
+RL_API int rl_add(float* x, const float* y, long long n, void* stream) noexcept {
+    return rl::guarded("rl_add", [&] {
+        rl::require(x && y && n > 0, "Add needs nonempty buffers.");
+        hipLaunchKernelGGL(P::add_kernel, dim3(P::blocks_for(n)), dim3(256), 0, rl::as_stream(stream), x, y, n);
+        rl::check_launch("Launch add");
+    });
+}
+
+RL_API int rl_advance_counters(long long* counters, int actor, void* stream) noexcept {
+    return rl::guarded("rl_advance_counters", [&] {
+        rl::require(counters != nullptr, "Counters must be nonnull.");
+        hipLaunchKernelGGL(P::advance_counters, dim3(1), dim3(1), 0, rl::as_stream(stream), counters, actor);
+        rl::check_launch("Launch counter advance");
+    });
+}
+
+RL_API int rl_scale_rewards(float* rewards, long long n, const float* var, const float* r_max, float g_max, float eps,
+                            void* stream) noexcept {
+    return rl::guarded("rl_scale_rewards", [&] {
+        rl::require(rewards && var && r_max && n > 0 && g_max > 0, "Reward scaling needs buffers and G_max > 0.");
+        hipLaunchKernelGGL(P::scale_rewards, dim3(rl::ceil_div(n, 256)), dim3(256), 0, rl::as_stream(stream), rewards,
+                           n, var, r_max, g_max, eps);
+        rl::check_launch("Launch reward scaling");
+    });
+}

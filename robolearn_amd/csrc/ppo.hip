@@ -1,0 +1,470 @@
+// PPO update kernels: GAE, advantage normalization, minibatch permutation
+// and gather, the clipped surrogate / value / entropy loss with its
+// gradients, KL-adaptive learning rate and gradient-norm statistics.
+//
+// Reference semantics (robolearn/warp/ppo.py):
+//   _gae :101-133            reverse scan per environment, time-major k = t E + i
+//   _advantage_* :136-159    two-pass mean / variance normalization
+//   _gather_batch :172-204   minibatch gather
+//   kl_kernel :207-230       KL(N_old || N_new) averaged over the minibatch
+//   _adapt_learning_rate :233-238
+//   _gradient_sum_squares / _clip_gradients :241-252
+//   loss_kernel :255-310
+// All reductions are fixed-order (no atomics), so captured replays are
+// bitwise repeatable.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace rl {
+namespace ppo {
+
+constexpr int kThreads = 1024;
+
+// One thread per environment.
+__global__ void gae_kernel(int horizon, int num_envs, float gamma, float lambda, int current_timeout_bootstrap,
+                           const float* rewards, const float* values, const float* next_values, const int* terminated,
+                           const int* truncated, float* advantages, float* returns) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= num_envs) return;
+    float advantage = 0.0f;
+    for (int step = horizon - 1; step >= 0; --step) {
+        const long long k = static_cast<long long>(step) * num_envs + i;
+        float bootstrap = terminated[k] != 0 ? 0.0f : 1.0f;
+        const float continuation = (terminated[k] != 0 || truncated[k] != 0) ? 0.0f : 1.0f;
+        float next_value = next_values[k];
+        if (current_timeout_bootstrap && truncated[k] != 0) {
+            next_value = values[k];
+            bootstrap = 1.0f;
+        }
+        const float delta = rewards[k] + gamma * bootstrap * next_value - values[k];
+        advantage = delta + gamma * lambda * continuation * advantage;
+        advantages[k] = advantage;
+        returns[k] = advantage + values[k];
+    }
+}
+
+__device__ float block_sum(float v, float* s) {
+    s[threadIdx.x] = v;
+    __syncthreads();
+    for (int stride = kThreads / 2; stride > 0; stride >>= 1) {
+        if (static_cast<int>(threadIdx.x) < stride) s[threadIdx.x] += s[threadIdx.x + stride];
+        __syncthreads();
+    }
+    const float total = s[0];
+    __syncthreads();
+    return total;
+}
+
+// Single workgroup: mean, then centered variance, then normalize in place.
+// stats[0] = sum, stats[1] = sum of squared deviations.
+__global__ __launch_bounds__(kThreads) void normalize_kernel(float* advantages, long long n, int sample_std,
+                                                             float* stats) {
+    __shared__ float s[kThreads];
+    float sum = 0.0f;
+    for (long long i = threadIdx.x; i < n; i += kThreads) sum += advantages[i];
+    sum = block_sum(sum, s);
+    const float nf = static_cast<float>(n);
+    const float mean = sum / nf;
+    float sq = 0.0f;
+    for (long long i = threadIdx.x; i < n; i += kThreads) {
+        const float c = advantages[i] - mean;
+        sq += c * c;
+    }
+    sq = block_sum(sq, s);
+    if (threadIdx.x == 0 && stats) {
+        stats[0] = sum;
+        stats[1] = sq;
+    }
+    if (sample_std) {
+        const float std = sqrtf(sq / fmaxf(nf - 1.0f, 1.0f));
+        for (long long i = threadIdx.x; i < n; i += kThreads) advantages[i] = (advantages[i] - mean) / (std + 1.0e-8f);
+    } else {
+        const float denom = sqrtf(sq / nf + 1.0e-8f);
+        for (long long i = threadIdx.x; i < n; i += kThreads) advantages[i] = (advantages[i] - mean) / denom;
+    }
+}
+
+__device__ __forceinline__ unsigned int mix32(unsigned int x) {
+    // Integer finalizer (murmur3 fmix32).
+    x ^= x >> 16;
+    x *= 0x85EBCA6Bu;
+    x ^= x >> 13;
+    x *= 0xC2B2AE35u;
+    x ^= x >> 16;
+    return x;
+}
+
+// Keyed 4-round balanced Feistel bijection on [0, 2^(2h)).
+__device__ __forceinline__ unsigned long long feistel(unsigned long long x, int h, unsigned int key0, unsigned int key1) {
+    const unsigned long long mask = (1ull << h) - 1ull;
+    unsigned long long left = x >> h;
+    unsigned long long right = x & mask;
+#pragma unroll
+    for (int round = 0; round < 4; ++round) {
+        const unsigned int f = mix32(static_cast<unsigned int>(right) ^ mix32(key0 + 0x9E3779B9u * (round + 1)) ^ key1);
+        const unsigned long long next = left ^ (f & mask);
+        left = right;
+        right = next;
+    }
+    return (left << h) | right;
+}
+
+// perm[i] for i < n: cycle-walk the Feistel permutation back into [0, n).
+// The walk starting from i < n returns into [0, n) before it can complete the
+// cycle through i, so at most 2^(2h) steps are taken.
+__global__ void permutation_kernel(long long n, int h, unsigned long long seed, const int* seed_counter,
+                                   long long* perm_out, int* perm32_out) {
+    const long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (i >= n) return;
+    const unsigned int c = seed_counter ? static_cast<unsigned int>(seed_counter[0]) : 0u;
+    const unsigned int key0 = mix32(static_cast<unsigned int>(seed) ^ mix32(c));
+    const unsigned int key1 = mix32(static_cast<unsigned int>(seed >> 32) + 0x632BE5ABu * (c + 1u));
+    const unsigned long long domain = 1ull << (2 * h);
+    unsigned long long x = static_cast<unsigned long long>(i);
+    for (unsigned long long step = 0; step < domain; ++step) {
+        x = feistel(x, h, key0, key1);
+        if (x < static_cast<unsigned long long>(n)) break;
+    }
+    if (perm_out) perm_out[i] = static_cast<long long>(x);
+    if (perm32_out) perm32_out[i] = static_cast<int>(x);
+}
+
+__global__ void advance_int(int* value) { value[0] += 1; }
+
+struct GatherArgs {
+    const int* indices;
+    long long offset, rows;
+    int obs_dim, action_dim, obs_ld;
+    const float *obs, *actions, *log_probs, *values, *advantages, *returns, *means, *stds;
+    float *b_obs, *b_actions, *b_log_probs, *b_values, *b_advantages, *b_returns, *b_means, *b_stds;
+};
+
+__global__ void gather_kernel(GatherArgs a) {
+    const long long r = blockIdx.y;
+    if (r >= a.rows) return;
+    const long long k = a.indices[a.offset + r];
+    const int width = a.obs_dim + 3 * a.action_dim + 4;
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < width; j += gridDim.x * blockDim.x) {
+        if (j < a.obs_dim) a.b_obs[r * a.obs_ld + j] = a.obs[k * a.obs_dim + j];
+        else if (j < a.obs_dim + a.action_dim) {
+            const int c = j - a.obs_dim;
+            a.b_actions[r * a.action_dim + c] = a.actions[k * a.action_dim + c];
+        } else if (j < a.obs_dim + 2 * a.action_dim) {
+            const int c = j - a.obs_dim - a.action_dim;
+            a.b_means[r * a.action_dim + c] = a.means[k * a.action_dim + c];
+        } else if (j < a.obs_dim + 3 * a.action_dim) {
+            const int c = j - a.obs_dim - 2 * a.action_dim;
+            a.b_stds[r * a.action_dim + c] = a.stds[k * a.action_dim + c];
+        } else {
+            const int f = j - a.obs_dim - 3 * a.action_dim;
+            if (f == 0) a.b_log_probs[r] = a.log_probs[k];
+            else if (f == 1) a.b_values[r] = a.values[k];
+            else if (f == 2) a.b_advantages[r] = a.advantages[k];
+            else a.b_returns[r] = a.returns[k];
+        }
+    }
+}
+
+// KL(N_old || N_new) per row, then a single-workgroup fixed-order mean and
+// the adaptive learning-rate rule.  std_type 0: std = exp(p), 1: clamp(p).
+__global__ __launch_bounds__(kThreads) void kl_adapt_kernel(const float* mean, long long ld_mean, const float* std_param,
+                                                            const float* old_mean, const float* old_std, long long rows,
+                                                            int action_dim, int std_type, float std_min, float std_max,
+                                                            float desired_kl, int adapt, float* kl_out, float* lr) {
+    __shared__ float s[kThreads];
+    float total = 0.0f;
+    for (long long i = threadIdx.x; i < rows; i += kThreads) {
+        float value = 0.0f;
+        for (int j = 0; j < action_dim; ++j) {
+            const float p = std_param[j];
+            const float std = std_type == 1 ? fminf(fmaxf(p, std_min), std_max) : expf(p);
+            const float ratio = old_std[i * action_dim + j] / std;
+            const float delta = (old_mean[i * action_dim + j] - mean[i * ld_mean + j]) / std;
+            value = value + 0.5f * (ratio * ratio + delta * delta - 1.0f);
+            value = value - logf(ratio);
+        }
+        total += value;
+    }
+    total = block_sum(total, s);
+    if (threadIdx.x == 0) {
+        const float kl = total / static_cast<float>(rows);
+        kl_out[0] = kl;
+        if (adapt) {
+            if (kl > desired_kl * 2.0f) lr[0] = fmaxf(1.0e-5f, lr[0] / 1.5f);
+            else if (kl < desired_kl / 2.0f && kl > 0.0f) lr[0] = fminf(1.0e-2f, lr[0] * 1.5f);
+        }
+    }
+}
+
+struct LossArgs {
+    const float* mean;
+    long long ld_mean;
+    const float* value;       // critic output [rows, 1]
+    const float* std_param;
+    const float* actions;
+    const float* old_log_probs;
+    const float* old_values;
+    const float* advantages;
+    const float* returns;
+    long long rows;
+    int action_dim;
+    int std_type;
+    float std_min, std_max;
+    float clip_ratio, value_coefficient, entropy_coefficient, value_loss_scale;
+    int clip_value;
+    float* dmean;             // [rows, A]
+    float* dvalue;            // [rows]
+    float* dstd_rows;         // [rows, A] per-row std-parameter gradient
+    float* row_terms;         // [4, rows]: total, policy, value, entropy (already scaled by 1/rows)
+};
+
+__global__ void loss_kernel(LossArgs a) {
+    const long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    if (i >= a.rows) return;
+    const float ln_two_pi = 1.8378770664093453f;
+    const float entropy_const = 1.4189385332046727f;
+    const float scale = 1.0f / static_cast<float>(a.rows);
+    float log_prob = 0.0f;
+    float entropy = 0.0f;
+    for (int j = 0; j < a.action_dim; ++j) {
+        const float p = a.std_param[j];
+        const float ls = a.std_type == 1 ? logf(fminf(fmaxf(p, a.std_min), a.std_max)) : p;
+        const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * expf(-ls);
+        log_prob = log_prob - 0.5f * (residual * residual + 2.0f * ls + ln_two_pi);
+        entropy = entropy + ls + entropy_const;
+    }
+    const float ratio = expf(log_prob - a.old_log_probs[i]);
+    const float adv = a.advantages[i];
+    const float lo = 1.0f - a.clip_ratio, hi = 1.0f + a.clip_ratio;
+    const float clipped_ratio = fminf(fmaxf(ratio, lo), hi);
+    const float unclipped = ratio * adv;
+    const float clipped = clipped_ratio * adv;
+    const float policy_loss = -fminf(unclipped, clipped);
+    // d policy / d ratio: the smaller branch carries the gradient; on a tie
+    // inside the clip range both branches have derivative -adv.
+    float dratio;
+    if (unclipped <= clipped) dratio = -adv;
+    else dratio = (ratio > lo && ratio < hi) ? -adv : 0.0f;
+    const float v = a.value[i];
+    const float error = v - a.returns[i];
+    float value_loss = error * error;
+    float dv = 2.0f * error;
+    if (a.clip_value) {
+        const float d = v - a.old_values[i];
+        const float cv = a.old_values[i] + fminf(fmaxf(d, -a.clip_ratio), a.clip_ratio);
+        const float ce = cv - a.returns[i];
+        if (ce * ce > value_loss) {
+            value_loss = ce * ce;
+            dv = (d >= -a.clip_ratio && d <= a.clip_ratio) ? 2.0f * ce : 0.0f;
+        }
+    }
+    value_loss = a.value_loss_scale * value_loss;
+    dv *= a.value_loss_scale;
+    a.dvalue[i] = scale * a.value_coefficient * dv;
+    const float dlp = scale * dratio * ratio;
+    for (int j = 0; j < a.action_dim; ++j) {
+        const float p = a.std_param[j];
+        float ls, dls_dp;
+        if (a.std_type == 1) {
+            const float c = fminf(fmaxf(p, a.std_min), a.std_max);
+            ls = logf(c);
+            dls_dp = (p >= a.std_min && p <= a.std_max) ? 1.0f / c : 0.0f;
+        } else {
+            ls = p;
+            dls_dp = 1.0f;
+        }
+        const float inv_std = expf(-ls);
+        const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * inv_std;
+        a.dmean[i * a.action_dim + j] = dlp * residual * inv_std;
+        a.dstd_rows[i * a.action_dim + j] = (dlp * (residual * residual - 1.0f) - scale * a.entropy_coefficient) * dls_dp;
+    }
+    a.row_terms[i] = scale * (policy_loss + a.value_coefficient * value_loss - a.entropy_coefficient * entropy);
+    a.row_terms[a.rows + i] = scale * policy_loss;
+    a.row_terms[2 * a.rows + i] = scale * value_loss;
+    a.row_terms[3 * a.rows + i] = scale * entropy;
+}
+
+// Sum of four row vectors in fixed order: out[q] = sum_i terms[q, i].
+__global__ __launch_bounds__(kThreads) void sum_rows_kernel(const float* terms, long long rows, int count, float* out) {
+    __shared__ float s[kThreads];
+    for (int q = 0; q < count; ++q) {
+        float v = 0.0f;
+        for (long long i = threadIdx.x; i < rows; i += kThreads) v += terms[q * rows + i];
+        v = block_sum(v, s);
+        if (threadIdx.x == 0) out[q] = v;
+    }
+}
+
+// Sum of squares over a flat vector: per-block partials (fixed order), then one block.
+__global__ void sumsq_partials(const float* x, long long n, float* partial) {
+    __shared__ float s[256];
+    float v = 0.0f;
+    const long long start = static_cast<long long>(blockIdx.x) * 4096;
+    const long long end = min(n, start + 4096);
+    for (long long i = start + threadIdx.x; i < end; i += 256) v += x[i] * x[i];
+    s[threadIdx.x] = v;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if (static_cast<int>(threadIdx.x) < stride) s[threadIdx.x] += s[threadIdx.x + stride];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = s[0];
+}
+
+__global__ __launch_bounds__(kThreads) void sumsq_finish(const float* partial, long long blocks, float* out) {
+    __shared__ float s[kThreads];
+    float v = 0.0f;
+    for (long long i = threadIdx.x; i < blocks; i += kThreads) v += partial[i];
+    v = block_sum(v, s);
+    if (threadIdx.x == 0) out[0] = v;
+}
+
+// g *= min(1, max_norm / (sqrt(sum_squares) + 1e-6)).
+__global__ void clip_kernel(float* g, long long n, const float* sum_squares, float max_norm) {
+    const float coefficient = fminf(1.0f, max_norm / (sqrtf(sum_squares[0]) + 1.0e-6f));
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<long long>(gridDim.x) * blockDim.x)
+        g[i] *= coefficient;
+}
+
+// dx *= elu'(y) = 1 if y > 0 else y + 1 (ELU with alpha 1, from its output).
+__global__ void elu_backward_kernel(float* dx, const float* y, long long n) {
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<long long>(gridDim.x) * blockDim.x)
+        dx[i] *= y[i] > 0.0f ? 1.0f : y[i] + 1.0f;
+}
+
+}  // namespace ppo
+}  // namespace rl
+
+namespace Q = rl::ppo;
+
+RL_API int rl_gae(int horizon, int num_envs, float gamma, float lambda, int current_timeout_bootstrap,
+                  const float* rewards, const float* values, const float* next_values, const int* terminated,
+                  const int* truncated, float* advantages, float* returns, void* stream) noexcept {
+    return rl::guarded("rl_gae", [&] {
+        rl::require(horizon > 0 && num_envs > 0, "GAE needs a positive horizon and environment count.");
+        rl::require(rewards && values && next_values && terminated && truncated && advantages && returns,
+                    "GAE needs every rollout buffer.");
+        hipLaunchKernelGGL(Q::gae_kernel, dim3(rl::ceil_div(num_envs, 256)), dim3(256), 0, rl::as_stream(stream),
+                           horizon, num_envs, gamma, lambda, current_timeout_bootstrap, rewards, values, next_values,
+                           terminated, truncated, advantages, returns);
+        rl::check_launch("Launch GAE");
+    });
+}
+
+RL_API int rl_normalize_advantages(float* advantages, long long n, int sample_std, float* stats, void* stream) noexcept {
+    return rl::guarded("rl_normalize_advantages", [&] {
+        rl::require(advantages && n > 0, "Advantage normalization needs a nonempty vector.");
+        hipLaunchKernelGGL(Q::normalize_kernel, dim3(1), dim3(Q::kThreads), 0, rl::as_stream(stream), advantages, n,
+                           sample_std, stats);
+        rl::check_launch("Launch advantage normalization");
+    });
+}
+
+RL_API int rl_permutation(long long n, unsigned long long seed, const int* seed_counter, long long* perm64,
+                          int* perm32, void* stream) noexcept {
+    return rl::guarded("rl_permutation", [&] {
+        rl::require(n > 0 && n < (1ll << 40) && (perm64 || perm32), "Permutation needs 0 < n < 2^40 and an output.");
+        int bits = 1;
+        while ((1ll << bits) < n) ++bits;
+        const int h = (bits + 1) / 2;
+        hipLaunchKernelGGL(Q::permutation_kernel, dim3(rl::ceil_div(n, 256)), dim3(256), 0, rl::as_stream(stream), n,
+                           h, seed, seed_counter, perm64, perm32);
+        rl::check_launch("Launch permutation");
+    });
+}
+
+RL_API int rl_advance_int(int* value, void* stream) noexcept {
+    return rl::guarded("rl_advance_int", [&] {
+        rl::require(value != nullptr, "Counter must be nonnull.");
+        hipLaunchKernelGGL(Q::advance_int, dim3(1), dim3(1), 0, rl::as_stream(stream), value);
+        rl::check_launch("Launch counter advance");
+    });
+}
+
+RL_API int rl_ppo_gather(const int* indices, long long offset, long long rows, int obs_dim, int action_dim, int obs_ld,
+                         const float* obs, const float* actions, const float* log_probs, const float* values,
+                         const float* advantages, const float* returns, const float* means, const float* stds,
+                         float* b_obs, float* b_actions, float* b_log_probs, float* b_values, float* b_advantages,
+                         float* b_returns, float* b_means, float* b_stds, void* stream) noexcept {
+    return rl::guarded("rl_ppo_gather", [&] {
+        rl::require(indices && rows > 0 && rows <= 65535 * 4 && obs_dim > 0 && action_dim > 0 && obs_ld >= obs_dim,
+                    "PPO gather shapes are invalid.");
+        rl::require(rows <= 65535, "PPO gather supports at most 65535 rows per launch.");
+        Q::GatherArgs a{indices, offset, rows, obs_dim, action_dim, obs_ld, obs, actions, log_probs, values, advantages,
+                        returns, means, stds, b_obs, b_actions, b_log_probs, b_values, b_advantages, b_returns, b_means,
+                        b_stds};
+        const int width = obs_dim + 3 * action_dim + 4;
+        hipLaunchKernelGGL(Q::gather_kernel, dim3(rl::ceil_div(width, 256), static_cast<unsigned>(rows)), dim3(256), 0,
+                           rl::as_stream(stream), a);
+        rl::check_launch("Launch PPO gather");
+    });
+}
+
+RL_API int rl_ppo_kl_adapt(const float* mean, long long ld_mean, const float* std_param, const float* old_mean,
+                           const float* old_std, long long rows, int action_dim, int std_type, float std_min,
+                           float std_max, float desired_kl, int adapt, float* kl_out, float* lr, void* stream) noexcept {
+    return rl::guarded("rl_ppo_kl_adapt", [&] {
+        rl::require(mean && std_param && old_mean && old_std && kl_out && (!adapt || lr) && rows > 0 && action_dim > 0,
+                    "KL needs means, std parameters and outputs.");
+        hipLaunchKernelGGL(Q::kl_adapt_kernel, dim3(1), dim3(Q::kThreads), 0, rl::as_stream(stream), mean, ld_mean,
+                           std_param, old_mean, old_std, rows, action_dim, std_type, std_min, std_max, desired_kl,
+                           adapt, kl_out, lr);
+        rl::check_launch("Launch KL adapt");
+    });
+}
+
+RL_API int rl_ppo_loss(const float* mean, long long ld_mean, const float* value, const float* std_param,
+                       const float* actions, const float* old_log_probs, const float* old_values,
+                       const float* advantages, const float* returns, long long rows, int action_dim, int std_type,
+                       float std_min, float std_max, float clip_ratio, float value_coefficient,
+                       float entropy_coefficient, float value_loss_scale, int clip_value, float* dmean, float* dvalue,
+                       float* dstd_rows, float* row_terms, float* totals, void* stream) noexcept {
+    return rl::guarded("rl_ppo_loss", [&] {
+        rl::require(mean && value && std_param && actions && old_log_probs && old_values && advantages && returns &&
+                        dmean && dvalue && dstd_rows && row_terms && totals && rows > 0 && action_dim > 0,
+                    "PPO loss needs every input and output buffer.");
+        Q::LossArgs a{mean, ld_mean, value, std_param, actions, old_log_probs, old_values, advantages, returns, rows,
+                      action_dim, std_type, std_min, std_max, clip_ratio, value_coefficient, entropy_coefficient,
+                      value_loss_scale, clip_value, dmean, dvalue, dstd_rows, row_terms};
+        const hipStream_t st = rl::as_stream(stream);
+        hipLaunchKernelGGL(Q::loss_kernel, dim3(rl::ceil_div(rows, 256)), dim3(256), 0, st, a);
+        rl::check_launch("Launch PPO loss");
+        hipLaunchKernelGGL(Q::sum_rows_kernel, dim3(1), dim3(Q::kThreads), 0, st, row_terms, rows, 4, totals);
+        rl::check_launch("Launch PPO loss reduction");
+    });
+}
+
+// Squared L2 norm of a flat vector; partial needs ceil(n / 4096) floats.
+RL_API int rl_sum_squares(const float* x, long long n, float* partial, float* out, void* stream) noexcept {
+    return rl::guarded("rl_sum_squares", [&] {
+        rl::require(x && partial && out && n > 0, "Sum of squares needs buffers.");
+        const long long blocks = (n + 4095) / 4096;
+        const hipStream_t st = rl::as_stream(stream);
+        hipLaunchKernelGGL(Q::sumsq_partials, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, x, n, partial);
+        rl::check_launch("Launch sum of squares");
+        hipLaunchKernelGGL(Q::sumsq_finish, dim3(1), dim3(Q::kThreads), 0, st, partial, blocks, out);
+        rl::check_launch("Launch sum of squares finish");
+    });
+}
+
+RL_API int rl_clip_by_norm(float* g, long long n, const float* sum_squares, float max_norm, void* stream) noexcept {
+    return rl::guarded("rl_clip_by_norm", [&] {
+        rl::require(g && sum_squares && n > 0 && max_norm > 0, "Clipping needs buffers and a positive norm.");
+        hipLaunchKernelGGL(Q::clip_kernel, dim3(static_cast<unsigned>(std::min<long long>((n + 255) / 256, 65536))),
+                           dim3(256), 0, rl::as_stream(stream), g, n, sum_squares, max_norm);
+        rl::check_launch("Launch gradient clipping");
+    });
+}
+
+RL_API int rl_elu_backward(float* dx, const float* y, long long n, void* stream) noexcept {
+    return rl::guarded("rl_elu_backward", [&] {
+        rl::require(dx && y && n > 0, "ELU backward needs buffers.");
+        hipLaunchKernelGGL(Q::elu_backward_kernel,
+                           dim3(static_cast<unsigned>(std::min<long long>((n + 255) / 256, 65536))), dim3(256), 0,
+                           rl::as_stream(stream), dx, y, n);
+        rl::check_launch("Launch ELU backward");
+    });
+}

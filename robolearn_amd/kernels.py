@@ -1,0 +1,200 @@
+"""Thin tensor-level wrappers over the C ABI.
+
+Every wrapper takes torch tensors that already live on the GPU, validates the
+shapes the kernel assumes, and enqueues on torch's current stream.  Nothing
+here computes on the host; a missing library raises from ``_native.load``.
+"""
+
+import torch
+
+from . import _native
+
+FP32 = 0
+BF16 = 1
+EPILOGUES = {None: 0, "relu": 1, "elu": 2}
+
+
+def stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def ptr(tensor: torch.Tensor | None) -> int | None:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def _check(tensor: torch.Tensor, numel: int, name: str, dtype=torch.float32):
+    if not tensor.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor.")
+    if tensor.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {tensor.dtype}.")
+    if not tensor.is_contiguous():
+        raise ValueError(f"{name} must be contiguous.")
+    if tensor.numel() < numel:
+        raise ValueError(f"{name} holds {tensor.numel()} elements, {numel} are needed.")
+
+
+def _is_bf16(tensor: torch.Tensor) -> int:
+    return 1 if tensor.dtype == torch.bfloat16 else 0
+
+
+def gemm(
+    a, b, d, *, m, n, k, batch=1, a_kcontig, b_kcontig, lda, ldb, ldd, stride_a=0, stride_b=0, stride_d=0,
+    c=None, beta=0.0, bias=None, stride_bias=0, epilogue=None, mode=FP32, splits=1, workspace=None,
+):
+    """Row-major batched D = act(op(A) op(B) + bias) + beta * C."""
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _native.call(
+        "rl_gemm", mode, _is_bf16(a), _is_bf16(b), int(a_kcontig), int(b_kcontig), m, n, k, batch, ptr(a), lda,
+        stride_a, ptr(b), ldb, stride_b, ptr(c), ptr(d), ldd, stride_d, ptr(bias), stride_bias, float(beta),
+        EPILOGUES[epilogue], splits, ptr(workspace), ws_bytes, stream(),
+    )
+
+
+def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None, bias=None, epilogue=None,
+                   mode=FP32, c=None, beta=0.0):
+    """y[e] = act(x[e] w[e]^T + bias[e]) (+ beta c); x_stride 0 broadcasts x."""
+    if x_stride is None:
+        x_stride = rows * in_dim
+    _check(w, ensemble * out_dim * in_dim, "weight", w.dtype)
+    _check(y, ensemble * rows * out_dim, "output")
+    gemm(x, w, y, m=rows, n=out_dim, k=in_dim, batch=ensemble, a_kcontig=True, b_kcontig=True, lda=in_dim,
+         ldb=in_dim, ldd=out_dim, stride_a=x_stride, stride_b=out_dim * in_dim, stride_d=rows * out_dim, bias=bias,
+         stride_bias=out_dim, epilogue=epilogue, mode=mode, c=c, beta=beta)
+
+
+def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=FP32, c=None, beta=0.0):
+    """dx[e] = dy[e] w[e] (+ beta c)."""
+    _check(dx, ensemble * rows * in_dim, "input gradient")
+    gemm(dy, w, dx, m=rows, n=in_dim, k=out_dim, batch=ensemble, a_kcontig=True, b_kcontig=False, lda=out_dim,
+         ldb=in_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=out_dim * in_dim, stride_d=rows * in_dim,
+         mode=mode, c=c, beta=beta)
+
+
+def split_count(m, n, k, batch, mode):
+    tiles = ((m + 127) // 128) * ((n + 127) // 128) * batch
+    ktiles = (k + (31 if mode == BF16 else 15)) // (32 if mode == BF16 else 16)
+    splits = 1
+    while tiles * splits < 512 and splits * 2 <= max(1, ktiles // 8) and splits < 64:
+        splits *= 2
+    return splits
+
+
+def linear_backward_weight(dy, x, dw, *, rows, in_dim, out_dim, ensemble=1, x_stride=None, mode=FP32,
+                           workspace=None, beta=0.0):
+    """dw[e] = dy[e]^T x[e] (+ beta dw), split-K over rows when the tile grid is small."""
+    if x_stride is None:
+        x_stride = rows * in_dim
+    _check(dw, ensemble * out_dim * in_dim, "weight gradient")
+    splits = split_count(out_dim, in_dim, rows, ensemble, mode) if workspace is not None else 1
+    if splits > 1:
+        need = _native.load().rl_gemm_workspace(mode, out_dim, in_dim, rows, ensemble, splits)
+        if need > workspace.numel() * workspace.element_size():
+            splits = 1
+    gemm(dy, x, dw, m=out_dim, n=in_dim, k=rows, batch=ensemble, a_kcontig=False, b_kcontig=False, lda=out_dim,
+         ldb=in_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=x_stride, stride_d=out_dim * in_dim, mode=mode,
+         splits=splits, workspace=workspace if splits > 1 else None, c=dw if beta else None, beta=beta)
+
+
+# ---------------------------------------------------------------------------
+# Normalization
+# ---------------------------------------------------------------------------
+def bn_forward(x, w, b, running_mean, running_var, mean, var, partial, y, *, rows, channels, ensemble=1,
+               x_stride=None, eps=1e-5, momentum=0.01, training=True, relu=False, update_running=True, y_bf16=None):
+    if x_stride is None:
+        x_stride = rows * channels
+    _native.call("rl_bn_forward_ex", ensemble, ptr(x), x_stride, ptr(w), ptr(b), ptr(running_mean), ptr(running_var),
+                 ptr(mean), ptr(var), ptr(partial), ptr(y), ptr(y_bf16), rows, channels, eps, momentum, int(training),
+                 int(relu), int(update_running), stream())
+
+
+def bn_backward(x, dy, y, w, mean, var, partial, sums, dx, dw, db, *, rows, channels, ensemble=1, x_stride=None,
+                eps=1e-5, training=True, relu=False, accumulate_dx=False, accumulate_params=False, dx_bf16=None):
+    if x_stride is None:
+        x_stride = rows * channels
+    _native.call("rl_bn_backward_ex", ensemble, ptr(x), x_stride, ptr(dy), ptr(y), ptr(w), ptr(mean), ptr(var),
+                 ptr(partial), ptr(sums), ptr(dx), ptr(dw), ptr(db), ptr(dx_bf16), rows, channels, eps,
+                 int(training), int(relu), int(accumulate_dx), int(accumulate_params), stream())
+
+
+def rms_forward(x, w, ms, y, *, rows, channels, ensemble=1, eps=1e-6):
+    _native.call("rl_rms_forward_ex", ensemble, ptr(x), ptr(w), ptr(ms), ptr(y), rows, channels, eps, stream())
+
+
+def rms_backward(x, dy, w, ms, partial, dx, dw, *, rows, channels, ensemble=1, eps=1e-6, accumulate_dx=False,
+                 accumulate_dw=False):
+    _native.call("rl_rms_backward_ex", ensemble, ptr(x), ptr(dy), ptr(w), ptr(ms), ptr(partial), ptr(dx), ptr(dw),
+                 rows, channels, eps, int(accumulate_dx), int(accumulate_dw), stream())
+
+
+def bias_grad(dy, db, partial, *, rows, channels, ensemble=1, accumulate=False):
+    _native.call("rl_bias_grad_ex", ensemble, ptr(dy), ptr(db), ptr(partial), rows, channels, int(accumulate),
+                 stream())
+
+
+def chunks(rows: int) -> int:
+    return (rows + 255) // 256
+
+
+# ---------------------------------------------------------------------------
+# Categorical head
+# ---------------------------------------------------------------------------
+def reduce_sum(x, out, *, scale=1.0):
+    _native.call("rl_reduce", ptr(x), x.numel(), float(scale), 0, ptr(out), stream())
+
+
+def reduce_max(x, out):
+    _native.call("rl_reduce", ptr(x), x.numel(), 1.0, 1, ptr(out), stream())
+
+
+def categorical_head_forward(logits, support, values, *, rows, bins, ensemble=1, bias=None, log_probs=None):
+    _native.call("rl_categorical_head_forward", ptr(logits), ptr(bias), bins, ptr(support), ptr(log_probs),
+                 ptr(values), rows, bins, ensemble, stream())
+
+
+def categorical_head_backward_q(logits, support, dvalues, dlogits, *, rows, bins, ensemble=1, bias=None):
+    _native.call("rl_categorical_head_backward_q", ptr(logits), ptr(bias), bins, ptr(support), ptr(dvalues),
+                 ptr(dlogits), rows, bins, ensemble, stream())
+
+
+def td_cross_entropy(target_logits, target_bias, target_rows, online_logits, online_bias, online_rows, support,
+                     reward, terminated, discount, next_log_probs, alpha, *, min_v, max_v, batch, bins, scale,
+                     dlogits, loss_rows, entropy_rows, target_out=None, q_next=None):
+    _native.call("rl_categorical_td_cross_entropy", ptr(target_logits), ptr(target_bias), target_rows,
+                 ptr(online_logits), ptr(online_bias), online_rows, ptr(support), ptr(reward), ptr(terminated),
+                 ptr(discount), ptr(next_log_probs), ptr(alpha), float(min_v), float(max_v), batch, bins,
+                 float(scale), ptr(target_out), ptr(dlogits), ptr(loss_rows), ptr(entropy_rows), ptr(q_next),
+                 stream())
+
+
+# ---------------------------------------------------------------------------
+# Policy / replay
+# ---------------------------------------------------------------------------
+def philox_normal(out, *, seed, counter=None, stream_id=0):
+    _native.call("rl_philox_normal", int(seed), ptr(counter), int(stream_id), ptr(out), out.numel(), stream())
+
+
+def sample_indices(idx, *, seed, count=None, fixed_count=0, counter=None, stream_id=0):
+    _native.call("rl_replay_sample_indices", int(seed), ptr(counter), int(stream_id), ptr(count), int(fixed_count),
+                 ptr(idx), idx.numel(), stream())
+
+
+def concat_columns(out, ld_out, rows, a, lda, ca, b=None, ldb=0, cb=0):
+    _native.call("rl_concat_columns", ptr(out), ld_out, rows, ptr(a), lda, ca, ptr(b), ldb, cb, stream())
+
+
+def tanh_gaussian_forward(head, noise, actions, log_probs, *, rows, action_dim, ld_actions=None,
+                          deterministic=False):
+    _native.call("rl_tanh_gaussian_forward", ptr(head), ptr(noise), ptr(actions),
+                 action_dim if ld_actions is None else ld_actions, ptr(log_probs), rows, action_dim,
+                 int(deterministic), stream())
+
+
+def tanh_gaussian_backward(head, noise, dactions, dlog_probs, dhead, *, rows, action_dim, grad_rows,
+                           ld_dactions=None):
+    _native.call("rl_tanh_gaussian_backward", ptr(head), ptr(noise), ptr(dactions),
+                 action_dim if ld_dactions is None else ld_dactions, grad_rows, ptr(dlog_probs), ptr(dhead), rows,
+                 action_dim, stream())
+
+
+def fill(x, value):
+    _native.call("rl_fill", ptr(x), x.numel(), float(value), stream())
