@@ -59,12 +59,12 @@ SIGNATURES = {
     "rl_flash_ema_step": (c_int, [P, P]),
     "rl_flash_ema_destroy": (c_int, [P]),
     # normalization
-    "rl_bn_forward_ex": (c_int, [c_int, P, c_ll, P, P, P, P, P, P, P, P, P, c_int, c_int, c_float, c_float, c_int,
+    "rl_bn_forward_ex": (c_int, [c_int, P, c_ll, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_float, c_float, c_int,
                                  c_int, c_int, P]),
-    "rl_bn_backward_ex": (c_int, [c_int, P, c_ll, P, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_float, c_int, c_int,
-                                  c_int, c_int, P]),
-    "rl_rms_forward_ex": (c_int, [c_int, P, P, P, P, c_int, c_int, c_float, P]),
-    "rl_rms_backward_ex": (c_int, [c_int, P, P, P, P, P, P, P, c_int, c_int, c_float, c_int, c_int, P]),
+    "rl_bn_backward_ex": (c_int, [c_int, P, c_ll, P, P, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_float, c_int,
+                                  c_int, c_int, c_int, P]),
+    "rl_rms_forward_ex": (c_int, [c_int, P, P, P, P, c_int, c_int, c_ll, c_float, P]),
+    "rl_rms_backward_ex": (c_int, [c_int, P, P, P, P, P, P, P, c_int, c_int, c_ll, c_float, c_int, c_int, P]),
     "rl_bias_grad_ex": (c_int, [c_int, P, P, P, c_int, c_int, c_int, P]),
     "rl_flash_bn_forward": (c_int, [P] * 9 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),
     "rl_flash_bn_forward_with_bf16": (c_int, [P] * 10 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),

@@ -28,6 +28,12 @@ constexpr int kThreads = 256;
 constexpr int kCols = 64;
 constexpr int kRowGroups = kThreads / kCols;
 
+// Normalized affine value; forward apply and the backward ReLU-mask recompute
+// both call this, so the mask is bitwise identical to the forward decision.
+__device__ __forceinline__ float bn_value(float x, float mean, float inv, float w, float b) {
+    return __fmaf_rn((x - mean) * inv, w, b);
+}
+
 // Welford merge of (count_b, mean_b, m2_b) into (count, mean, m2).
 __device__ __forceinline__ void merge(float& count, float& mean, float& m2, float count_b, float mean_b, float m2_b) {
     if (count_b == 0.0f) return;
@@ -105,10 +111,10 @@ __global__ void bn_statistics(const float* partial, float* mean_out, float* var_
     }
 }
 
-// y = (x - mean) * rsqrt(var + eps) * w + b, optional ReLU, optional bf16 copy.
+// y = act((x - mean) * rsqrt(var + eps) * w + b) [+ residual], optional bf16 copy.
 __global__ void bn_apply(const float* x, long long x_stride, const float* mean, const float* var, const float* w,
-                         const float* b, float* y, unsigned short* y_bf16, long long rows, int channels, int ensemble,
-                         float eps, int relu) {
+                         const float* b, const float* residual, float* y, unsigned short* y_bf16, long long rows,
+                         int channels, int ensemble, float eps, int relu) {
     const long long per = rows * channels;
     const long long total = per * ensemble;
     for (long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; idx < total;
@@ -118,8 +124,9 @@ __global__ void bn_apply(const float* x, long long x_stride, const float* mean, 
         const int c = static_cast<int>(within % channels);
         const int pc = e * channels + c;
         const float inv = 1.0f / sqrtf(var[pc] + eps);
-        float v = (x[e * x_stride + within] - mean[pc]) * inv * w[pc] + b[pc];
+        float v = bn_value(x[e * x_stride + within], mean[pc], inv, w[pc], b[pc]);
         if (relu) v = v > 0.0f ? v : 0.0f;
+        if (residual) v += residual[idx];
         y[idx] = v;
         if (y_bf16) y_bf16[idx] = f32_to_bf16_bits(v);
     }
@@ -128,9 +135,9 @@ __global__ void bn_apply(const float* x, long long x_stride, const float* mean, 
 // Backward partial sums per chunk: sum(dy'), sum(dy' * xhat) with dy' the
 // ReLU-masked output gradient.
 __global__ __launch_bounds__(kThreads) void bn_grad_partials(const float* x, long long x_stride, const float* dy,
-                                                             const float* y, const float* mean, const float* var,
-                                                             float* partial, int rows, int channels, int chunks,
-                                                             float eps, int relu) {
+                                                             const float* y, const float* w, const float* b,
+                                                             const float* mean, const float* var, float* partial,
+                                                             int rows, int channels, int chunks, float eps, int relu) {
     const int e = blockIdx.z;
     const int c = blockIdx.x * kCols + threadIdx.x % kCols;
     const int group = threadIdx.x / kCols;
@@ -143,22 +150,28 @@ __global__ __launch_bounds__(kThreads) void bn_grad_partials(const float* x, lon
         const int pc = e * channels + c;
         const float mu = mean[pc];
         const float inv = 1.0f / sqrtf(var[pc] + eps);
+        const float wc = w[pc];
+        const float bc = b ? b[pc] : 0.0f;
         for (int r = r0 + group; r < r1; r += kRowGroups) {
             const long long i = static_cast<long long>(r) * channels + c;
+            const float xv = x[e * x_stride + i];
             float g = dy[off + i];
-            if (relu && !(y[off + i] > 0.0f)) g = 0.0f;
+            if (relu) {
+                const float out = y ? y[off + i] : bn_value(xv, mu, inv, wc, bc);
+                if (!(out > 0.0f)) g = 0.0f;
+            }
             s0 += g;
-            s1 += g * ((x[e * x_stride + i] - mu) * inv);
+            s1 += g * ((xv - mu) * inv);
         }
     }
-    __shared__ float a[kThreads], b[kThreads];
-    a[threadIdx.x] = s0;
-    b[threadIdx.x] = s1;
+    __shared__ float sa[kThreads], sb[kThreads];
+    sa[threadIdx.x] = s0;
+    sb[threadIdx.x] = s1;
     __syncthreads();
     if (group == 0 && c < channels) {
         for (int g = 1; g < kRowGroups; ++g) {
-            s0 += a[g * kCols + threadIdx.x];
-            s1 += b[g * kCols + threadIdx.x];
+            s0 += sa[g * kCols + threadIdx.x];
+            s1 += sb[g * kCols + threadIdx.x];
         }
         float* out = partial + (static_cast<long long>(e) * chunks + chunk) * 2 * channels;
         out[c] = s0;
@@ -188,7 +201,7 @@ __global__ void bn_grad_reduce(const float* partial, float* sums, float* dw, flo
 // dx (+)= w * rsqrt(var + eps) * (dy' - mean(dy') - xhat * mean(dy' xhat))  (training)
 // dx (+)= w * rsqrt(var + eps) * dy'                                        (eval)
 __global__ void bn_grad_apply(const float* x, long long x_stride, const float* dy, const float* y, const float* w,
-                              const float* mean, const float* var, const float* sums, float* dx,
+                              const float* b, const float* mean, const float* var, const float* sums, float* dx,
                               unsigned short* dx_bf16, long long rows, int channels, int ensemble, float eps,
                               int training, int relu, int accumulate) {
     const long long per = rows * channels;
@@ -200,11 +213,15 @@ __global__ void bn_grad_apply(const float* x, long long x_stride, const float* d
         const int c = static_cast<int>(within % channels);
         const int pc = e * channels + c;
         const float inv = 1.0f / sqrtf(var[pc] + eps);
+        const float xv = x[e * x_stride + within];
         float g = dy[idx];
-        if (relu && !(y[idx] > 0.0f)) g = 0.0f;
+        if (relu) {
+            const float out = y ? y[idx] : bn_value(xv, mean[pc], inv, w[pc], b ? b[pc] : 0.0f);
+            if (!(out > 0.0f)) g = 0.0f;
+        }
         float value;
         if (training) {
-            const float xhat = (x[e * x_stride + within] - mean[pc]) * inv;
+            const float xhat = (xv - mean[pc]) * inv;
             value = w[pc] * inv * (g - sums[pc] - xhat * sums[ensemble * channels + pc]);
         } else {
             value = w[pc] * inv * g;
@@ -218,37 +235,39 @@ __global__ void bn_grad_apply(const float* x, long long x_stride, const float* d
 // One wave per row: rs = rsqrt(mean(x^2) + eps); y = x * rs * w.  Stores
 // mean(x^2) per row in ms (the reference's "var").
 __global__ void rms_forward(const float* x, const float* w, float* ms, float* y, long long rows, int channels,
-                            int ensemble, float eps) {
+                            int ensemble, long long member_stride, float eps) {
     const long long row = blockIdx.x * static_cast<long long>(blockDim.x / kWave) + threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
     if (row >= rows * ensemble) return;
     const int e = static_cast<int>(row / rows);
-    const float* xr = x + row * channels;
+    const long long base = e * member_stride + (row - e * rows) * channels;
+    const float* xr = x + base;
     float s = 0.0f;
     for (int c = lane; c < channels; c += kWave) s += xr[c] * xr[c];
     s = wave_sum(s) / static_cast<float>(channels);
     const float rs = 1.0f / sqrtf(s + eps);
     if (lane == 0) ms[row] = s;
     const float* we = w + e * channels;
-    float* yr = y + row * channels;
+    float* yr = y + base;
     for (int c = lane; c < channels; c += kWave) yr[c] = xr[c] * rs * we[c];
 }
 
 // dx (+)= rs * (dy * w - x * rs^2 * mean(dy * w * x)).
 __global__ void rms_dx(const float* x, const float* dy, const float* w, const float* ms, float* dx, long long rows,
-                       int channels, int ensemble, float eps, int accumulate) {
+                       int channels, int ensemble, long long member_stride, float eps, int accumulate) {
     const long long row = blockIdx.x * static_cast<long long>(blockDim.x / kWave) + threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
     if (row >= rows * ensemble) return;
     const int e = static_cast<int>(row / rows);
-    const float* xr = x + row * channels;
-    const float* gr = dy + row * channels;
+    const long long base = e * member_stride + (row - e * rows) * channels;
+    const float* xr = x + base;
+    const float* gr = dy + base;
     const float* we = w + e * channels;
     float s = 0.0f;
     for (int c = lane; c < channels; c += kWave) s += gr[c] * we[c] * xr[c];
     s = wave_sum(s) / static_cast<float>(channels);
     const float rs = 1.0f / sqrtf(ms[row] + eps);
-    float* out = dx + row * channels;
+    float* out = dx + base;
     for (int c = lane; c < channels; c += kWave) {
         float v = rs * (gr[c] * we[c] - xr[c] * rs * rs * s);
         if (accumulate) v += out[c];
@@ -261,14 +280,14 @@ __global__ void rms_dx(const float* x, const float* dy, const float* w, const fl
 //   mode 1: sum dy * x * rsqrt(ms + eps) (RMS weight gradient)
 __global__ __launch_bounds__(kThreads) void column_partials(const float* dy, const float* x, const float* ms,
                                                             float* partial, int rows, int channels, int chunks,
-                                                            float eps, int mode) {
+                                                            long long member_stride, float eps, int mode) {
     const int e = blockIdx.z;
     const int c = blockIdx.x * kCols + threadIdx.x % kCols;
     const int group = threadIdx.x / kCols;
     const int chunk = blockIdx.y;
     const int r0 = chunk * kChunk;
     const int r1 = min(rows, r0 + kChunk);
-    const long long off = static_cast<long long>(e) * rows * channels;
+    const long long off = static_cast<long long>(e) * member_stride;
     float s = 0.0f;
     if (c < channels) {
         for (int r = r0 + group; r < r1; r += kRowGroups) {
@@ -305,9 +324,9 @@ inline unsigned elementwise_blocks(long long total) {
 int chunks_for(int rows) { return (rows + norm::kChunk - 1) / norm::kChunk; }
 
 void bn_forward(int ensemble, const float* x, long long x_stride, const float* w, const float* b, float* running_mean,
-                float* running_var, float* mean, float* var, float* partial, float* y, unsigned short* y_bf16,
-                int rows, int channels, float eps, float momentum, int training, int relu, int update_running,
-                hipStream_t stream) {
+                float* running_var, float* mean, float* var, float* partial, const float* residual, float* y,
+                unsigned short* y_bf16, int rows, int channels, float eps, float momentum, int training, int relu,
+                int update_running, hipStream_t stream) {
     require(ensemble > 0 && rows > 0 && channels > 0, "BatchNorm dimensions must be positive.");
     require(static_cast<long long>(rows) * channels <= std::numeric_limits<int>::max(), "BatchNorm exceeds 2^31 elements.");
     require(std::isfinite(eps) && eps >= 0.0f && std::isfinite(momentum), "BatchNorm eps/momentum are invalid.");
@@ -332,25 +351,27 @@ void bn_forward(int ensemble, const float* x, long long x_stride, const float* w
     }
     const long long total = static_cast<long long>(ensemble) * rows * channels;
     hipLaunchKernelGGL(norm::bn_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream, x, x_stride,
-                       use_mean, use_var, w, b, y, y_bf16, static_cast<long long>(rows), channels, ensemble, eps, relu);
+                       use_mean, use_var, w, b, residual, y, y_bf16, static_cast<long long>(rows), channels, ensemble,
+                       eps, relu);
     check_launch("Launch BN apply");
 }
 
 void bn_backward(int ensemble, const float* x, long long x_stride, const float* dy, const float* y, const float* w,
-                 const float* mean, const float* var, float* partial, float* sums, float* dx, float* dw, float* db,
+                 const float* b, const float* mean, const float* var, float* partial, float* sums, float* dx, float* dw,
+                 float* db,
                  unsigned short* dx_bf16, int rows, int channels, float eps, int training, int relu,
                  int accumulate_dx, int accumulate_params, hipStream_t stream) {
     require(ensemble > 0 && rows > 0 && channels > 0, "BatchNorm dimensions must be positive.");
     require(x && dy && w && mean && var, "BatchNorm backward requires x, dy, weight and statistics.");
-    require(!relu || y, "ReLU BatchNorm backward requires the output.");
+    require(!relu || y || b, "ReLU BatchNorm backward requires the output or the bias to recompute it.");
     require(!dx_bf16 || dx, "bf16 BN input adjoint requires an fp32 input adjoint.");
     const bool need_sums = training || dw || db;
     if (need_sums) {
         require(partial && sums, "BatchNorm backward requires partial and sums scratch.");
         const int chunks = chunks_for(rows);
         const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
-        hipLaunchKernelGGL(norm::bn_grad_partials, grid, dim3(norm::kThreads), 0, stream, x, x_stride, dy, y, mean,
-                           var, partial, rows, channels, chunks, eps, relu);
+        hipLaunchKernelGGL(norm::bn_grad_partials, grid, dim3(norm::kThreads), 0, stream, x, x_stride, dy, y, w, b,
+                           mean, var, partial, rows, channels, chunks, eps, relu);
         check_launch("Launch BN gradient partials");
         hipLaunchKernelGGL(norm::bn_grad_reduce, dim3(ceil_div(ensemble * channels, 256)), dim3(256), 0, stream,
                            partial, sums, dw, db, rows, channels, chunks, ensemble, accumulate_params);
@@ -359,33 +380,35 @@ void bn_backward(int ensemble, const float* x, long long x_stride, const float* 
     if (dx) {
         const long long total = static_cast<long long>(ensemble) * rows * channels;
         hipLaunchKernelGGL(norm::bn_grad_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream, x,
-                           x_stride, dy, y, w, mean, var, sums, dx, dx_bf16, static_cast<long long>(rows), channels,
+                           x_stride, dy, y, w, b, mean, var, sums, dx, dx_bf16, static_cast<long long>(rows), channels,
                            ensemble, eps, training, relu, accumulate_dx);
         check_launch("Launch BN gradient apply");
     }
 }
 
-void rms_forward(int ensemble, const float* x, const float* w, float* ms, float* y, int rows, int channels, float eps,
-                 hipStream_t stream) {
+void rms_forward(int ensemble, const float* x, const float* w, float* ms, float* y, int rows, int channels,
+                 long long member_stride, float eps, hipStream_t stream) {
     require(ensemble > 0 && rows > 0 && channels > 0, "RMSNorm dimensions must be positive.");
     require(x && w && ms && y, "RMSNorm forward requires x, weight, ms and y.");
     const long long total_rows = static_cast<long long>(rows) * ensemble;
+    if (member_stride <= 0) member_stride = static_cast<long long>(rows) * channels;
     hipLaunchKernelGGL(norm::rms_forward, dim3(ceil_div(total_rows, 4)), dim3(256), 0, stream, x, w, ms, y,
-                       static_cast<long long>(rows), channels, ensemble, eps);
+                       static_cast<long long>(rows), channels, ensemble, member_stride, eps);
     check_launch("Launch RMS forward");
 }
 
 void rms_backward(int ensemble, const float* x, const float* dy, const float* w, const float* ms, float* partial,
-                  float* dx, float* dw, int rows, int channels, float eps, int accumulate_dx, int accumulate_dw,
-                  hipStream_t stream) {
+                  float* dx, float* dw, int rows, int channels, long long member_stride, float eps, int accumulate_dx,
+                  int accumulate_dw, hipStream_t stream) {
     require(ensemble > 0 && rows > 0 && channels > 0, "RMSNorm dimensions must be positive.");
     require(x && dy && w && ms, "RMSNorm backward requires x, dy, weight and ms.");
+    if (member_stride <= 0) member_stride = static_cast<long long>(rows) * channels;
     if (dw) {
         require(partial, "RMS weight gradient requires partial scratch.");
         const int chunks = chunks_for(rows);
         const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
         hipLaunchKernelGGL(norm::column_partials, grid, dim3(norm::kThreads), 0, stream, dy, x, ms, partial, rows,
-                           channels, chunks, eps, 1);
+                           channels, chunks, member_stride, eps, 1);
         check_launch("Launch RMS weight partials");
         hipLaunchKernelGGL(norm::column_reduce, dim3(ceil_div(ensemble * channels, 256)), dim3(256), 0, stream,
                            partial, dw, channels, chunks, ensemble, accumulate_dw);
@@ -394,7 +417,7 @@ void rms_backward(int ensemble, const float* x, const float* dy, const float* w,
     if (dx) {
         const long long total_rows = static_cast<long long>(rows) * ensemble;
         hipLaunchKernelGGL(norm::rms_dx, dim3(ceil_div(total_rows, 4)), dim3(256), 0, stream, x, dy, w, ms, dx,
-                           static_cast<long long>(rows), channels, ensemble, eps, accumulate_dx);
+                           static_cast<long long>(rows), channels, ensemble, member_stride, eps, accumulate_dx);
         check_launch("Launch RMS input gradient");
     }
 }
@@ -406,7 +429,7 @@ void bias_grad(int ensemble, const float* dy, float* db, float* partial, int row
     const int chunks = chunks_for(rows);
     const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
     hipLaunchKernelGGL(norm::column_partials, grid, dim3(norm::kThreads), 0, stream, dy, nullptr, nullptr, partial,
-                       rows, channels, chunks, 0.0f, 0);
+                       rows, channels, chunks, static_cast<long long>(rows) * channels, 0.0f, 0);
     check_launch("Launch bias gradient partials");
     hipLaunchKernelGGL(norm::column_reduce, dim3(ceil_div(ensemble * channels, 256)), dim3(256), 0, stream, partial,
                        db, channels, chunks, ensemble, accumulate);
@@ -420,39 +443,41 @@ void bias_grad(int ensemble, const float* dy, float* db, float* partial, int row
 // every member, as the critic embedder does with its shared input).
 // ---------------------------------------------------------------------------
 RL_API int rl_bn_forward_ex(int ensemble, const float* x, long long x_stride, const float* w, const float* b,
-                            float* running_mean, float* running_var, float* mean, float* var, float* partial, float* y,
-                            void* y_bf16, int rows, int channels, float eps, float momentum, int training, int relu,
-                            int update_running, void* stream) noexcept {
+                            float* running_mean, float* running_var, float* mean, float* var, float* partial,
+                            const float* residual, float* y, void* y_bf16, int rows, int channels, float eps,
+                            float momentum, int training, int relu, int update_running, void* stream) noexcept {
     return rl::guarded("rl_bn_forward_ex", [&] {
-        rl::bn_forward(ensemble, x, x_stride, w, b, running_mean, running_var, mean, var, partial, y,
+        rl::bn_forward(ensemble, x, x_stride, w, b, running_mean, running_var, mean, var, partial, residual, y,
                        static_cast<unsigned short*>(y_bf16), rows, channels, eps, momentum, training, relu,
                        update_running, rl::as_stream(stream));
     });
 }
 
 RL_API int rl_bn_backward_ex(int ensemble, const float* x, long long x_stride, const float* dy, const float* y,
-                             const float* w, const float* mean, const float* var, float* partial, float* sums,
-                             float* dx, float* dw, float* db, void* dx_bf16, int rows, int channels, float eps,
-                             int training, int relu, int accumulate_dx, int accumulate_params, void* stream) noexcept {
+                             const float* w, const float* b, const float* mean, const float* var, float* partial,
+                             float* sums, float* dx, float* dw, float* db, void* dx_bf16, int rows, int channels,
+                             float eps, int training, int relu, int accumulate_dx, int accumulate_params,
+                             void* stream) noexcept {
     return rl::guarded("rl_bn_backward_ex", [&] {
-        rl::bn_backward(ensemble, x, x_stride, dy, y, w, mean, var, partial, sums, dx, dw, db,
+        rl::bn_backward(ensemble, x, x_stride, dy, y, w, b, mean, var, partial, sums, dx, dw, db,
                         static_cast<unsigned short*>(dx_bf16), rows, channels, eps, training, relu, accumulate_dx,
                         accumulate_params, rl::as_stream(stream));
     });
 }
 
 RL_API int rl_rms_forward_ex(int ensemble, const float* x, const float* w, float* ms, float* y, int rows, int channels,
-                             float eps, void* stream) noexcept {
-    return rl::guarded("rl_rms_forward_ex",
-                       [&] { rl::rms_forward(ensemble, x, w, ms, y, rows, channels, eps, rl::as_stream(stream)); });
+                             long long member_stride, float eps, void* stream) noexcept {
+    return rl::guarded("rl_rms_forward_ex", [&] {
+        rl::rms_forward(ensemble, x, w, ms, y, rows, channels, member_stride, eps, rl::as_stream(stream));
+    });
 }
 
 RL_API int rl_rms_backward_ex(int ensemble, const float* x, const float* dy, const float* w, const float* ms,
-                              float* partial, float* dx, float* dw, int rows, int channels, float eps,
-                              int accumulate_dx, int accumulate_dw, void* stream) noexcept {
+                              float* partial, float* dx, float* dw, int rows, int channels, long long member_stride,
+                              float eps, int accumulate_dx, int accumulate_dw, void* stream) noexcept {
     return rl::guarded("rl_rms_backward_ex", [&] {
-        rl::rms_backward(ensemble, x, dy, w, ms, partial, dx, dw, rows, channels, eps, accumulate_dx, accumulate_dw,
-                         rl::as_stream(stream));
+        rl::rms_backward(ensemble, x, dy, w, ms, partial, dx, dw, rows, channels, member_stride, eps, accumulate_dx,
+                         accumulate_dw, rl::as_stream(stream));
     });
 }
 
@@ -471,8 +496,8 @@ RL_API int rl_flash_bn_forward(const float* x, const float* w, const float* b, f
                                float* mean, float* var, float* partial, float* y, int batch, int channels, float eps,
                                float momentum, int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_forward", [&] {
-        rl::bn_forward(1, x, 0, w, b, running_mean, running_var, mean, var, partial, y, nullptr, batch, channels, eps,
-                       momentum, training, relu, 1, rl::as_stream(stream));
+        rl::bn_forward(1, x, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y, nullptr, batch, channels,
+                       eps, momentum, training, relu, 1, rl::as_stream(stream));
     });
 }
 
@@ -482,7 +507,7 @@ RL_API int rl_flash_bn_forward_with_bf16(const float* x, const float* w, const f
                                          int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_forward_with_bf16", [&] {
         rl::require(half_output != nullptr, "bf16 BN output must be nonnull.");
-        rl::bn_forward(1, x, 0, w, b, running_mean, running_var, mean, var, partial, y,
+        rl::bn_forward(1, x, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y,
                        static_cast<unsigned short*>(half_output), batch, channels, eps, momentum, training, relu, 1,
                        rl::as_stream(stream));
     });
@@ -492,8 +517,8 @@ RL_API int rl_flash_bn_backward(const float* x, const float* dy, const float* y,
                                 const float* var, float* partial, float* sums, float* dx, float* dw, float* db,
                                 int batch, int channels, float eps, int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_backward", [&] {
-        rl::bn_backward(1, x, 0, dy, y, w, mean, var, partial, sums, dx, dw, db, nullptr, batch, channels, eps,
-                        training, relu, 1, 1, rl::as_stream(stream));
+        rl::bn_backward(1, x, 0, dy, y, w, nullptr, mean, var, partial, sums, dx, dw, db, nullptr, batch, channels,
+                        eps, training, relu, 1, 1, rl::as_stream(stream));
     });
 }
 
@@ -502,21 +527,22 @@ RL_API int rl_flash_bn_backward_controlled(const float* x, const float* dy, cons
                                            float* dw, float* db, void* half_dx, int overwrite_dx, int batch,
                                            int channels, float eps, int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_backward_controlled", [&] {
-        rl::bn_backward(1, x, 0, dy, y, w, mean, var, partial, sums, dx, dw, db, static_cast<unsigned short*>(half_dx),
-                        batch, channels, eps, training, relu, overwrite_dx ? 0 : 1, 1, rl::as_stream(stream));
+        rl::bn_backward(1, x, 0, dy, y, w, nullptr, mean, var, partial, sums, dx, dw, db,
+                        static_cast<unsigned short*>(half_dx), batch, channels, eps, training, relu,
+                        overwrite_dx ? 0 : 1, 1, rl::as_stream(stream));
     });
 }
 
 RL_API int rl_flash_rms_forward(const float* x, const float* w, float* var, float* y, int batch, int channels, float eps,
                                 void* stream) noexcept {
     return rl::guarded("rl_flash_rms_forward",
-                       [&] { rl::rms_forward(1, x, w, var, y, batch, channels, eps, rl::as_stream(stream)); });
+                       [&] { rl::rms_forward(1, x, w, var, y, batch, channels, 0, eps, rl::as_stream(stream)); });
 }
 
 RL_API int rl_flash_rms_backward(const float* x, const float* dy, const float* w, const float* var, float* partial,
                                  float* dx, float* dw, int batch, int channels, float eps, void* stream) noexcept {
     return rl::guarded("rl_flash_rms_backward", [&] {
-        rl::rms_backward(1, x, dy, w, var, partial, dx, dw, batch, channels, eps, 1, 1, rl::as_stream(stream));
+        rl::rms_backward(1, x, dy, w, var, partial, dx, dw, batch, channels, 0, eps, 1, 1, rl::as_stream(stream));
     });
 }
 

@@ -99,31 +99,37 @@ def linear_backward_weight(dy, x, dw, *, rows, in_dim, out_dim, ensemble=1, x_st
 # Normalization
 # ---------------------------------------------------------------------------
 def bn_forward(x, w, b, running_mean, running_var, mean, var, partial, y, *, rows, channels, ensemble=1,
-               x_stride=None, eps=1e-5, momentum=0.01, training=True, relu=False, update_running=True, y_bf16=None):
+               x_stride=None, eps=1e-5, momentum=0.01, training=True, relu=False, update_running=True, y_bf16=None,
+               residual=None):
+    """y = act(BN(x)) [+ residual]; x_stride 0 broadcasts one input to every member."""
     if x_stride is None:
         x_stride = rows * channels
     _native.call("rl_bn_forward_ex", ensemble, ptr(x), x_stride, ptr(w), ptr(b), ptr(running_mean), ptr(running_var),
-                 ptr(mean), ptr(var), ptr(partial), ptr(y), ptr(y_bf16), rows, channels, eps, momentum, int(training),
-                 int(relu), int(update_running), stream())
+                 ptr(mean), ptr(var), ptr(partial), ptr(residual), ptr(y), ptr(y_bf16), rows, channels, eps, momentum,
+                 int(training), int(relu), int(update_running), stream())
 
 
 def bn_backward(x, dy, y, w, mean, var, partial, sums, dx, dw, db, *, rows, channels, ensemble=1, x_stride=None,
-                eps=1e-5, training=True, relu=False, accumulate_dx=False, accumulate_params=False, dx_bf16=None):
+                eps=1e-5, training=True, relu=False, accumulate_dx=False, accumulate_params=False, dx_bf16=None,
+                b=None):
+    """BN backward; with relu and y=None the ReLU mask is recomputed from x and (w, b)."""
     if x_stride is None:
         x_stride = rows * channels
-    _native.call("rl_bn_backward_ex", ensemble, ptr(x), x_stride, ptr(dy), ptr(y), ptr(w), ptr(mean), ptr(var),
-                 ptr(partial), ptr(sums), ptr(dx), ptr(dw), ptr(db), ptr(dx_bf16), rows, channels, eps,
+    _native.call("rl_bn_backward_ex", ensemble, ptr(x), x_stride, ptr(dy), ptr(y), ptr(w), ptr(b), ptr(mean),
+                 ptr(var), ptr(partial), ptr(sums), ptr(dx), ptr(dw), ptr(db), ptr(dx_bf16), rows, channels, eps,
                  int(training), int(relu), int(accumulate_dx), int(accumulate_params), stream())
 
 
-def rms_forward(x, w, ms, y, *, rows, channels, ensemble=1, eps=1e-6):
-    _native.call("rl_rms_forward_ex", ensemble, ptr(x), ptr(w), ptr(ms), ptr(y), rows, channels, eps, stream())
+def rms_forward(x, w, ms, y, *, rows, channels, ensemble=1, eps=1e-6, member_stride=0):
+    """Row RMSNorm over `rows` rows per member; member_stride (elements) defaults to rows * channels."""
+    _native.call("rl_rms_forward_ex", ensemble, ptr(x), ptr(w), ptr(ms), ptr(y), rows, channels, member_stride, eps,
+                 stream())
 
 
 def rms_backward(x, dy, w, ms, partial, dx, dw, *, rows, channels, ensemble=1, eps=1e-6, accumulate_dx=False,
-                 accumulate_dw=False):
+                 accumulate_dw=False, member_stride=0):
     _native.call("rl_rms_backward_ex", ensemble, ptr(x), ptr(dy), ptr(w), ptr(ms), ptr(partial), ptr(dx), ptr(dw),
-                 rows, channels, eps, int(accumulate_dx), int(accumulate_dw), stream())
+                 rows, channels, member_stride, eps, int(accumulate_dx), int(accumulate_dw), stream())
 
 
 def bias_grad(dy, db, partial, *, rows, channels, ensemble=1, accumulate=False):

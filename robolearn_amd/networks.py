@@ -1,0 +1,301 @@
+"""FlashSAC networks on persistent GPU buffers, driven through the C ABI.
+
+Structure follows robolearn/flashsac/layers.py and networks.py:
+  embedder   BN(x) -> Linear (bias-free)                         layers.py:84-93
+  block      Linear -> BN -> ReLU -> Linear -> BN -> ReLU -> +x    layers.py:96-113
+  post norm  RMSNorm (eps 1e-6)                                   layers.py:67-74, 225-240
+  heads      tanh-Gaussian policy (layers.py:116-166) or categorical value
+             head (layers.py:275-303)
+The twin critic is one ensemble of two members (layers.py:174-303); every
+kernel takes the member count and strides, so both critics run in one launch.
+
+Parameters of a network live in one flat fp32 buffer with named views that
+match the reference state_dict keys; gradients, Adam moments and the EMA target
+are parallel flat buffers with the same offsets.  Activations are laid out
+[member, row, channel] for the largest row count the learner uses.  Every
+backward writes each gradient element exactly once (first writer overwrites),
+so no gradient clearing pass exists.
+"""
+
+import math
+from collections import OrderedDict
+
+import torch
+
+from . import _native
+from . import kernels as K
+
+ALIGN = 64  # floats: 256-byte alignment of every tensor in a flat buffer
+
+
+def _numel(shape) -> int:
+    return int(math.prod(shape))
+
+
+def _align(value: int) -> int:
+    return (value + ALIGN - 1) // ALIGN * ALIGN
+
+
+class FlatStore:
+    """Named views into flat parameter / gradient / moment / target buffers."""
+
+    def __init__(self, shapes: "OrderedDict[str, tuple]", device, *, groups=None, adam=True, target=False,
+                 grads=True):
+        self.shapes = OrderedDict(shapes)
+        groups = groups or [[name] for name in shapes]
+        grouped = {name for group in groups for name in group}
+        groups = list(groups) + [[name] for name in shapes if name not in grouped]
+        self.offsets = {}
+        position = 0
+        for group in groups:
+            position = _align(position)
+            for name in group:
+                self.offsets[name] = position
+                position += _numel(self.shapes[name])
+        self.size = _align(position)
+        self.param = torch.zeros(self.size, device=device)
+        self.grad = torch.zeros(self.size, device=device) if grads else None
+        self.m1 = torch.zeros(self.size, device=device) if adam else None
+        self.m2 = torch.zeros(self.size, device=device) if adam else None
+        self.target = torch.zeros(self.size, device=device) if target else None
+
+    def view(self, buffer, name):
+        offset = self.offsets[name]
+        return buffer[offset: offset + _numel(self.shapes[name])].view(self.shapes[name])
+
+    def span(self, buffer, names, shape):
+        """Contiguous view over consecutive tensors of one allocation group."""
+        offset = self.offsets[names[0]]
+        total = sum(_numel(self.shapes[n]) for n in names)
+        for a, b in zip(names, names[1:]):
+            if self.offsets[b] != self.offsets[a] + _numel(self.shapes[a]):
+                raise ValueError(f"{a} and {b} are not adjacent")
+        return buffer[offset: offset + total].view(shape)
+
+    def params(self):
+        return OrderedDict((n, self.view(self.param, n)) for n in self.shapes)
+
+    def grads(self):
+        return OrderedDict((n, self.view(self.grad, n)) for n in self.shapes)
+
+    def targets(self):
+        return OrderedDict((n, self.view(self.target, n)) for n in self.shapes)
+
+    def moments(self):
+        return (OrderedDict((n, self.view(self.m1, n)) for n in self.shapes),
+                OrderedDict((n, self.view(self.m2, n)) for n in self.shapes))
+
+
+def projection_kind(name: str) -> int:
+    """0 unit row, 1 BN pair, 2 RMS scale, 3 plain (layers.py:24-29, 57-64, 76-81)."""
+    if name.endswith("mean_bias") or name.endswith("std_bias") or name == "predictor.bias":
+        return 3
+    if ".norm" in name or name.startswith("embedder.norm"):
+        return 1
+    if name.startswith("post_norm"):
+        return 2
+    return 0
+
+
+class FusedOptimizer:
+    """Adam + projection (+ EMA into the target copy) in one pass per step.
+
+    Per-network scalar state (timestep, lr) lives on the device, as in
+    robolearn/cuda/kernels.cu:310-337; the LR schedule is evaluated on the device
+    before each step (robolearn/warp/flashsac.py:242-259, 645-649).
+    """
+
+    def __init__(self, store: FlatStore, cfg, *, project=True, ema_tau=None, plain=False, form=0,
+                 schedule=True):
+        self.store = store
+        device = store.param.device
+        self.timestep = torch.zeros(1, device=device)
+        self.lr = torch.full((1,), float(cfg.learning_rate_init), device=device)
+        names = list(store.shapes)
+        kinds, rows, cols, params, grads, m1, m2, targets, partner = [], [], [], [], [], [], [], [], []
+        index = {n: i for i, n in enumerate(names)}
+        for name in names:
+            shape = store.shapes[name]
+            kind = 3 if (plain or not project) else projection_kind(name)
+            if kind == 0:
+                r, c = _numel(shape[:-1]), shape[-1]
+            elif kind in (1, 2):
+                r, c = _numel(shape[:-1]) if len(shape) > 1 else 1, shape[-1]
+            else:
+                r, c = 1, _numel(shape)
+            kinds.append(kind)
+            rows.append(r)
+            cols.append(c)
+            params.append(store.view(store.param, name).data_ptr())
+            grads.append(store.view(store.grad, name).data_ptr())
+            m1.append(store.view(store.m1, name).data_ptr())
+            m2.append(store.view(store.m2, name).data_ptr())
+            targets.append(store.view(store.target, name).data_ptr() if ema_tau is not None else None)
+            partner.append(-1)
+        for i, name in enumerate(names):
+            if kinds[i] == 1 and name.endswith(".weight"):
+                partner[i] = index[name[: -len("weight")] + "bias"]
+        warmup, decay = cfg.learning_rate_warmup_step, cfg.learning_rate_decay_step
+        self.handle = _native.create(
+            "rl_fused_optimizer_create", len(names), _native.int_array(kinds), _native.ll_array(rows),
+            _native.ll_array(cols), _native.pointer_array(params), _native.pointer_array(grads),
+            _native.pointer_array(m1), _native.pointer_array(m2),
+            _native.pointer_array(targets) if ema_tau is not None else None, None, None, _native.int_array(partner),
+            self.timestep.data_ptr(), self.lr.data_ptr(), 0.9, 0.999, 1e-8,
+            float(ema_tau if ema_tau is not None else 0.0), form, int(schedule), float(cfg.learning_rate_init),
+            float(cfg.learning_rate_peak), float(cfg.learning_rate_end), int(warmup), int(decay),
+        )
+        self.project = project and not plain
+        self.ema = ema_tau is not None
+
+    def step(self, *, adam=True, project=None, ema=None):
+        project = self.project if project is None else project
+        ema = self.ema if ema is None else ema
+        _native.call("rl_fused_optimizer_step", self.handle, int(adam), int(project), int(ema), None, K.stream())
+
+    def close(self):
+        if getattr(self, "handle", None):
+            try:
+                _native.load().rl_fused_optimizer_destroy(self.handle)
+            except Exception:  # interpreter shutdown
+                pass
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+
+class Trunk:
+    """BN -> Linear embedder, residual BN blocks and the post RMSNorm, batched over members."""
+
+    def __init__(self, *, ensemble, in_dim, hidden, blocks, max_rows, device, mode, prefix_linear):
+        self.E, self.in_dim, self.h, self.blocks, self.R = ensemble, in_dim, hidden, blocks, max_rows
+        self.mode = mode
+        self.linear = prefix_linear  # name suffix of unit-linear weights (".w.weight" actor, ".weight" critic)
+        E, R, h = ensemble, max_rows, hidden
+
+        def buf(*shape):
+            return torch.zeros(*shape, device=device)
+
+        self.y0 = buf(E, R, in_dim)
+        self.stream = [buf(E, R, h) for _ in range(blocks + 1)]
+        self.u1 = [buf(E, R, 4 * h) for _ in range(blocks)]
+        self.r1 = [buf(E, R, 4 * h) for _ in range(blocks)]
+        self.u2 = [buf(E, R, h) for _ in range(blocks)]
+        self.z = buf(E, R, h)
+        self.ms = buf(E * R)
+        self.stats = {}
+        for name, width in self.bn_layers():
+            self.stats[name] = (buf(E, width), buf(E, width))
+        self.d_stream = buf(E, R, h)
+        self.d_u2 = buf(E, R, h)
+        self.d_r1 = buf(E, R, 4 * h)
+        self.dy0 = buf(E, R, in_dim)
+        self.dz = buf(E, R, h)
+        widest = max(4 * h, in_dim)
+        self.partial = buf(E * 2 * K.chunks(R) * widest)
+        self.sums = buf(2 * E * widest)
+
+    def bn_layers(self):
+        yield "embedder.norm", self.in_dim
+        for i in range(self.blocks):
+            yield f"encoder.{i}.norm1", 4 * self.h
+            yield f"encoder.{i}.norm2", self.h
+
+    def _stats(self, name, running, training):
+        if training:
+            return self.stats[name]
+        return running[name + ".running_mean"], running[name + ".running_var"]
+
+    def forward(self, p, running, x, *, rows, x_stride, training, update_running=True):
+        """Runs the trunk on `rows` rows of x; leaves the block outputs in self.stream."""
+        E, h, mode = self.E, self.h, self.mode
+        name = "embedder.norm"
+        mean, var = self.stats[name]
+        K.bn_forward(x, p[name + ".weight"], p[name + ".bias"], running[name + ".running_mean"],
+                     running[name + ".running_var"], mean, var, self.partial, self.y0, rows=rows,
+                     channels=self.in_dim, ensemble=E, x_stride=x_stride, training=training,
+                     update_running=update_running)
+        K.linear_forward(self.y0, p["embedder.w" + self.linear], self.stream[0], rows=rows, in_dim=self.in_dim,
+                         out_dim=h, ensemble=E, mode=mode)
+        for i in range(self.blocks):
+            pre = f"encoder.{i}"
+            K.linear_forward(self.stream[i], p[f"{pre}.w1{self.linear}"], self.u1[i], rows=rows, in_dim=h,
+                             out_dim=4 * h, ensemble=E, mode=mode)
+            mean, var = self.stats[pre + ".norm1"]
+            K.bn_forward(self.u1[i], p[pre + ".norm1.weight"], p[pre + ".norm1.bias"],
+                         running[pre + ".norm1.running_mean"], running[pre + ".norm1.running_var"], mean, var,
+                         self.partial, self.r1[i], rows=rows, channels=4 * h, ensemble=E, training=training,
+                         relu=True, update_running=update_running)
+            K.linear_forward(self.r1[i], p[f"{pre}.w2{self.linear}"], self.u2[i], rows=rows, in_dim=4 * h,
+                             out_dim=h, ensemble=E, mode=mode)
+            mean, var = self.stats[pre + ".norm2"]
+            K.bn_forward(self.u2[i], p[pre + ".norm2.weight"], p[pre + ".norm2.bias"],
+                         running[pre + ".norm2.running_mean"], running[pre + ".norm2.running_var"], mean, var,
+                         self.partial, self.stream[i + 1], rows=rows, channels=h, ensemble=E, training=training,
+                         relu=True, update_running=update_running, residual=self.stream[i])
+
+    def post_norm(self, p, *, rows, row0, count):
+        """RMSNorm of rows [row0, row0 + count) of the last block output into self.z (same rows)."""
+        offset = row0 * self.h
+        K.rms_forward(self.stream[-1].view(-1)[offset:], p["post_norm.weight"], self.ms,
+                      self.z.view(-1)[offset:], rows=count, channels=self.h, ensemble=self.E,
+                      member_stride=rows * self.h)
+
+    def post_norm_backward(self, p, g, *, rows, row0, count):
+        """dz rows [row0, row0+count) -> d_stream (same rows, overwrite), RMS weight grad."""
+        offset = row0 * self.h
+        K.rms_backward(self.stream[-1].view(-1)[offset:], self.dz.view(-1)[offset:], p["post_norm.weight"], self.ms,
+                       self.partial, self.d_stream.view(-1)[offset:],
+                       None if g is None else g["post_norm.weight"], rows=count, channels=self.h, ensemble=self.E,
+                       member_stride=rows * self.h)
+        if count < rows:
+            # rows outside the head subset receive no gradient from the head
+            for e in range(self.E):
+                base = self.d_stream[e]
+                if row0 > 0:
+                    K.fill(base[:row0], 0.0)
+                if row0 + count < rows:
+                    K.fill(base[row0 + count: rows], 0.0)
+
+    def backward(self, p, running, g, x, *, rows, x_stride, training, workspace, input_grad=None):
+        """Backward from self.d_stream (gradient of the last block output).
+
+        g: gradient views (None for a frozen network: only input gradients).
+        input_grad: optional [E, rows, in_dim] buffer receiving dL/dx per member.
+        """
+        E, h, mode = self.E, self.h, self.mode
+        for i in reversed(range(self.blocks)):
+            pre = f"encoder.{i}"
+            mean, var = self._stats(pre + ".norm2", running, training)
+            K.bn_backward(self.u2[i], self.d_stream, None, p[pre + ".norm2.weight"], mean, var, self.partial,
+                          self.sums, self.d_u2, None if g is None else g[pre + ".norm2.weight"],
+                          None if g is None else g[pre + ".norm2.bias"], rows=rows, channels=h, ensemble=E,
+                          training=training, relu=True, b=p[pre + ".norm2.bias"])
+            K.linear_backward_input(self.d_u2, p[f"{pre}.w2{self.linear}"], self.d_r1, rows=rows, in_dim=4 * h,
+                                    out_dim=h, ensemble=E, mode=mode)
+            if g is not None:
+                K.linear_backward_weight(self.d_u2, self.r1[i], g[f"{pre}.w2{self.linear}"], rows=rows,
+                                         in_dim=4 * h, out_dim=h, ensemble=E, mode=mode, workspace=workspace)
+            mean, var = self._stats(pre + ".norm1", running, training)
+            K.bn_backward(self.u1[i], self.d_r1, self.r1[i], p[pre + ".norm1.weight"], mean, var, self.partial,
+                          self.sums, self.d_r1, None if g is None else g[pre + ".norm1.weight"],
+                          None if g is None else g[pre + ".norm1.bias"], rows=rows, channels=4 * h, ensemble=E,
+                          training=training, relu=True)
+            K.linear_backward_input(self.d_r1, p[f"{pre}.w1{self.linear}"], self.d_stream, rows=rows, in_dim=h,
+                                    out_dim=4 * h, ensemble=E, mode=mode, c=self.d_stream, beta=1.0)
+            if g is not None:
+                K.linear_backward_weight(self.d_r1, self.stream[i], g[f"{pre}.w1{self.linear}"], rows=rows,
+                                         in_dim=h, out_dim=4 * h, ensemble=E, mode=mode, workspace=workspace)
+        if g is not None:
+            K.linear_backward_weight(self.d_stream, self.y0, g["embedder.w" + self.linear], rows=rows,
+                                     in_dim=self.in_dim, out_dim=h, ensemble=E, mode=mode, workspace=workspace)
+        if g is None and input_grad is None:
+            return
+        K.linear_backward_input(self.d_stream, p["embedder.w" + self.linear], self.dy0, rows=rows,
+                                in_dim=self.in_dim, out_dim=h, ensemble=E, mode=mode)
+        name = "embedder.norm"
+        mean, var = self._stats(name, running, training)
+        K.bn_backward(x, self.dy0, None, p[name + ".weight"], mean, var, self.partial, self.sums, input_grad,
+                      None if g is None else g[name + ".weight"], None if g is None else g[name + ".bias"],
+                      rows=rows, channels=self.in_dim, ensemble=E, x_stride=x_stride, training=training)
