@@ -1,0 +1,273 @@
+#!/usr/bin/env python3
+"""Learner hot-path benchmark on one MI355X.
+
+Default workload ("g1"): one captured HIP graph per
+step holding two FlashSAC updates (update-to-data 2: an actor+critic update and
+a critic-only update) at batch 8192, obs 123, act 37, actor 256x2, twin critics
+1024x2, 101 bins on [-20, 20], bf16 dense operands with fp32 state; replay
+4096 envs x 256 steps of seeded synthetic transitions resident in HBM.
+
+Prints ONE JSON line: value = FlashSAC updates/sec on the GPU, with
+  roofline      the dominant kernel (critic block-1 forward GEMM, bf16 MFMA)
+                timed live with HIP events on the stream it runs on,
+  update_roofline  two-term serial roofline of the whole update,
+  cpu_baseline  the CPU oracle (PyTorch-CPU restatement of the reference update,
+                fp32) timed on this host's cores on one update of the same shape.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+
+WORKLOADS = {
+    "g1": dict(obs=123, act=37, batch=8192, envs=4096, horizon=256, actor_hidden=256, actor_blocks=2,
+               critic_hidden=1024, critic_blocks=2, bins=101, min_v=-20.0, max_v=20.0, amp=True, utd=2,
+               reward_std=0.5, done=0.005),
+    "readme": dict(obs=31, act=8, batch=2048, envs=1024, horizon=1000, actor_hidden=256, actor_blocks=1,
+                   critic_hidden=512, critic_blocks=2, bins=101, min_v=-10.0, max_v=10.0, amp=False, utd=2,
+                   reward_std=1.0, done=0.01),
+    "cartpole": dict(obs=4, act=1, batch=512, envs=64, horizon=500, actor_hidden=128, actor_blocks=1,
+                     critic_hidden=256, critic_blocks=2, bins=101, min_v=-10.0, max_v=10.0, amp=False, utd=2,
+                     reward_std=1.0, done=0.01),
+}
+
+
+def gemm_flops(w: dict) -> float:
+    """Algorithmic GEMM FLOPs (2 M N K per product) of one actor-phase + one critic-only update.
+
+    Counts forward, input-gradient and weight-gradient products actually needed:
+    the actor embedder needs no input gradient; the frozen critic in the actor
+    phase needs input gradients only; heads run on the rows whose outputs are used.
+    """
+    B, O, A = w["batch"], w["obs"], w["act"]
+    I = O + A
+    ha, hc, K = w["actor_hidden"], w["critic_hidden"], w["bins"]
+
+    def trunk(rows, inp, h, blocks, members):
+        embed = members * 2 * rows * inp * h
+        body = members * 2 * rows * blocks * 2 * h * 4 * h
+        return embed, body
+
+    def actor(rows):
+        e, b = trunk(rows, O, ha, w["actor_blocks"], 1)
+        return e, b + 2 * rows * ha * 2 * A
+
+    def critic_trunk(rows):
+        return trunk(rows, I, hc, w["critic_blocks"], 2)
+
+    def head(rows):
+        return 2 * 2 * rows * hc * K
+
+    ae, ab = actor(2 * B)
+    ce_b, cb_b = critic_trunk(B)
+    actor_phase = (ae + ab) + (ce_b + cb_b + head(B)) * 2 + (ae + ab) + ab
+    ae1, ab1 = actor(B)
+    ce, cb = critic_trunk(2 * B)
+    critic_phase = (ae1 + ab1) + 2 * (ce + cb + head(B)) + (ce + cb + head(B)) + (cb + head(B))
+    return actor_phase + 2 * critic_phase
+
+
+def elementwise_bytes(w: dict) -> float:
+    """Approximate compulsory HBM bytes of the non-GEMM kernels for the same update pair."""
+    B, hc, ha, K = w["batch"], w["critic_hidden"], w["actor_hidden"], w["bins"]
+    per_block = 2 * 2 * B * (4 * hc + hc)  # members x rows x channels of one critic block
+    bn_fwd = 3 * 4 * per_block * w["critic_blocks"]  # stats read + apply read + write
+    bn_bwd = 5 * 4 * per_block * w["critic_blocks"]
+    critic_pass = bn_fwd
+    critic_total = 2 * critic_pass * 2 + bn_bwd * 2 + bn_bwd  # 2 updates x (target + online) fwd, bwd
+    actor_bytes = 10 * 4 * 2 * B * 5 * ha * w["actor_blocks"]
+    params = 2 * (w["critic_hidden"] * (w["obs"] + w["act"]) + w["critic_blocks"] * 8 * hc * hc + hc * K)
+    optimizer = 36 * params * 2
+    return critic_total + actor_bytes + optimizer + 3 * 2 * B * K * 4 * 4
+
+
+def cpu_baseline(w: dict, cfg_kwargs: dict) -> dict:
+    """Time the CPU oracle (fp32) on one actor-phase update at the workload shape."""
+    import torch
+
+    from oracle import flashsac as O
+    from robolearn_amd.config import FlashSACConfig
+    from dataclasses import replace
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    cfg = FlashSACConfig(**cfg_kwargs)
+    cfg = replace(cfg, temp_target_entropy=O.target_entropy(w["act"], cfg.temp_target_sigma))
+    d = O.dims_from_config(w["obs"], w["act"], cfg)
+    state = O.init_state(d, cfg, seed=0, dtype=torch.float32)
+    g = torch.Generator().manual_seed(5)
+    B = w["batch"]
+    batch = {
+        "observation": torch.randn(B, w["obs"], generator=g), "next_observation": torch.randn(B, w["obs"], generator=g),
+        "action": torch.rand(B, w["act"], generator=g) * 2 - 1, "reward": torch.randn(B, generator=g),
+        "terminated": (torch.rand(B, generator=g) < w["done"]).float(), "discount": torch.full((B,), cfg.gamma),
+    }
+    noise = torch.randn(2 * B, w["act"], generator=g)
+    next_noise = torch.randn(B, w["act"], generator=g)
+    O.update(state, batch, noise, next_noise, do_actor_update=False)  # warm-up (critic-only)
+    t0 = time.perf_counter()
+    O.update(state, batch, noise, next_noise, do_actor_update=True)
+    actor_seconds = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    O.update(state, batch, noise, next_noise, do_actor_update=False)
+    critic_seconds = time.perf_counter() - t0
+    per_update = 0.5 * (actor_seconds + critic_seconds)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as stream:
+            for line in stream:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": 1.0 / per_update,
+        "unit": "updates/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle.flashsac (PyTorch CPU fp32) at the same shape: 1 critic-only warm-up, then 1 actor-phase "
+                   f"({actor_seconds:.2f} s) + 1 critic-only ({critic_seconds:.2f} s) update timed; {model}"),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="g1")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--profile-dominant", action="store_true",
+                        help="also launch the dominant kernel alone (for rocprof agreement)")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the learner path is single-GPU (see DESIGN.md for sharding).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from robolearn_amd import kernels as K
+    from robolearn_amd.config import FlashSACConfig
+    from robolearn_amd.flashsac import FlashSAC
+
+    w = WORKLOADS[args.workload]
+    B = w["batch"]
+    capacity = w["envs"] * w["horizon"]
+    cfg_kwargs = dict(seed=0, normalize_reward=False, n_step=1, sample_batch_size=B, buffer_max_length=capacity,
+                      buffer_min_length=B, actor_hidden_dim=w["actor_hidden"], actor_num_blocks=w["actor_blocks"],
+                      critic_hidden_dim=w["critic_hidden"], critic_num_blocks=w["critic_blocks"],
+                      critic_num_bins=w["bins"], critic_min_v=w["min_v"], critic_max_v=w["max_v"],
+                      critic_target_update_tau=0.005, learning_rate_init=3e-4, learning_rate_peak=3e-4,
+                      learning_rate_end=3e-4, gamma=0.99, use_amp=w["amp"], actor_update_period=2)
+    cfg = FlashSACConfig(**cfg_kwargs)
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    agent = FlashSAC(w["obs"], w["act"], num_envs=w["envs"], cfg=cfg)
+    g = torch.Generator(device=device).manual_seed(0)
+    data = {
+        "observation": torch.randn(capacity, w["obs"], generator=g, device=device),
+        "next_observation": torch.randn(capacity, w["obs"], generator=g, device=device),
+        "action": torch.rand(capacity, w["act"], generator=g, device=device) * 2 - 1,
+        "reward": torch.randn(capacity, generator=g, device=device) * w["reward_std"],
+        "terminated": (torch.rand(capacity, generator=g, device=device) < w["done"]).float(),
+        "truncated": torch.zeros(capacity, device=device),
+        "discount": torch.full((capacity,), cfg.gamma, device=device),
+    }
+    agent.load_replay(data)
+    del data
+    graph = agent.capture_pair() if w["utd"] == 2 else None
+    print(f"[bench] workload {args.workload}: captured update-to-data-{w['utd']} graph", file=sys.stderr, flush=True)
+
+    def step():
+        if graph is not None:
+            graph.replay()
+        else:
+            agent.update()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / args.steps
+    updates_per_second = w["utd"] * 1000.0 / ms_per_step
+    print(f"[bench] {ms_per_step:.3f} ms per step, {updates_per_second:.1f} updates/s", file=sys.stderr, flush=True)
+
+    # Dominant kernel: critic block-1 forward GEMM [2 x 2B x h] . [4h x h]^T (bf16 MFMA), timed live on the
+    # stream it is launched on, at the shape it runs with inside the update.
+    net = agent.critic_net
+    h = net.h
+    rows = 2 * B
+    reps = 20
+    launch = lambda: K.linear_forward(net.stream[0], agent.critic_p["encoder.0.w1.weight"], net.u1[0], rows=rows,  # noqa
+                                      in_dim=h, out_dim=4 * h, ensemble=2, mode=agent.mode)
+    launch()
+    torch.cuda.synchronize()
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    k0.record()
+    for _ in range(reps):
+        launch()
+    k1.record()
+    torch.cuda.synchronize()
+    kernel_ms = k0.elapsed_time(k1) / reps
+    kernel_flops = 2.0 * 2 * rows * h * 4 * h
+    peak = BF16_PEAK_TFLOPS if agent.mode == K.BF16 else FP32_PEAK_TFLOPS
+    achieved = kernel_flops / (kernel_ms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4), "traffic": None,
+                "kernel": "gemm_kernel<1,float,float,true,true> critic block-1 forward",
+                "kernel_ms": round(kernel_ms, 4), "flops_per_launch": kernel_flops}
+    flops = gemm_flops(w)
+    hbm_bytes = elementwise_bytes(w)
+    t_roof_ms = (flops / (peak * 1e12) + hbm_bytes / (HBM_PEAK_GBS * 1e9)) * 1e3
+    update_roofline = {"gemm_tflop_per_step": round(flops / 1e12, 3),
+                       "elementwise_gb_per_step": round(hbm_bytes / 1e9, 3),
+                       "t_roof_ms_per_step": round(t_roof_ms, 3),
+                       "frac": round(t_roof_ms / ms_per_step, 4)}
+
+    baseline = None
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
+        baseline = cpu_baseline(w, cfg_kwargs)
+
+    result = {
+        "metric": "FlashSAC updates/sec at batch 8192 (1 GPU)" if args.workload == "g1"
+        else f"FlashSAC updates/sec at batch {B} (1 GPU)",
+        "value": round(updates_per_second, 3),
+        "unit": "updates/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if w["amp"] else "fp32",
+        "data": "synthetic",
+        "config": {"workload": f"flashsac_{args.workload}", "batch": B, "obs_dim": w["obs"], "act_dim": w["act"],
+                   "actor": f"{w['actor_hidden']}x{w['actor_blocks']}",
+                   "critic": f"2x {w['critic_hidden']}x{w['critic_blocks']}", "bins": w["bins"],
+                   "updates_per_step": w["utd"], "replay_rows": capacity, "parallelism": "single-gpu"},
+        "roofline": roofline,
+        "update_roofline": update_roofline,
+        "cpu_baseline": baseline,
+    }
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -392,7 +392,8 @@ class FlashSAC:
             raise ValueError("Replay contents exceed the configured capacity.")
         for key in BATCH_KEYS:
             value = data[key] if key in data else np.zeros((n,), dtype=np.float32)
-            self.replay[key][:n].copy_(torch.as_tensor(np.asarray(value)[:n]).to(torch.float32).reshape(
+            value = value if torch.is_tensor(value) else torch.as_tensor(np.asarray(value))
+            self.replay[key][:n].copy_(value[:n].to(device=self.device, dtype=torch.float32).reshape(
                 self.replay[key][:n].shape))
         self._num_in_buffer_host = n
         self._replay_position = (position if position is not None else n) % self.capacity
