@@ -1,0 +1,356 @@
+"""Fixed-shape PPO update on MI355X: GAE, advantage normalization, one device
+permutation reused across epochs, and per minibatch the KL-adaptive learning
+rate, the clipped surrogate/value/entropy loss, backward through both MLPs,
+gradient clipping and Adam, all enqueued on one stream and captured in one
+HIP graph.
+
+Interface mirrors robolearn/warp/ppo.py:353-778 (WarpPPO): constructor, act,
+store, compute_returns, launch_update, warmup, update, health_metrics,
+state_dict/load_state_dict/save/load, with the same checkpoint keys.
+Rollout buffers are time-major (k = step * num_envs + env), as the reference's.
+"""
+
+import math
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from . import _native
+from . import kernels as K
+from .config import PPOConfig
+from .networks import FlatStore, _align
+
+
+def _mlp_shapes(prefix, input_dim, output_dim, hidden_dims):
+    widths = (input_dim, *hidden_dims, output_dim)
+    shapes = []
+    for i, (a, b) in enumerate(zip(widths[:-1], widths[1:])):
+        shapes.append((f"{prefix}.{i}.weight", (b, a)))
+        shapes.append((f"{prefix}.{i}.bias", (b,)))
+    return shapes
+
+
+class WarpPPO:
+    """PPO learner with the reference's WarpPPO interface, backed by HIP kernels."""
+
+    def __init__(self, observation_dim: int, action_dim: int, num_envs: int, horizon: int,
+                 config: PPOConfig | None = None, device: str = "cuda"):
+        self.config = cfg = config or PPOConfig()
+        if min(observation_dim, action_dim, num_envs, horizon, cfg.epochs, *cfg.hidden_dims) < 1:
+            raise ValueError("Dimensions, horizon, and epochs must be positive.")
+        if cfg.initial_std <= 0:
+            raise ValueError("initial_std must be positive.")
+        if cfg.activation not in ("tanh", "elu") or cfg.std_type not in ("log", "scalar"):
+            raise ValueError("activation must be 'tanh' or 'elu', and std_type must be 'log' or 'scalar'.")
+        if cfg.schedule not in ("fixed", "adaptive") or cfg.desired_kl <= 0:
+            raise ValueError("schedule must be 'fixed' or 'adaptive', and desired_kl must be positive.")
+        if cfg.timeout_bootstrap not in ("next", "current"):
+            raise ValueError("timeout_bootstrap must be 'next' or 'current'.")
+        if cfg.std_range[0] <= 0 or cfg.std_range[0] > cfg.std_range[1]:
+            raise ValueError("std_range must contain positive increasing bounds.")
+        if cfg.activation != "elu":
+            raise NotImplementedError("The MI355X PPO path implements ELU activations (the G1 recipe).")
+        if not torch.cuda.is_available():
+            raise RuntimeError("WarpPPO on MI355X requires a visible GPU; there is no CPU fallback.")
+        _native.load()
+        self.device = torch.device(device if ":" in str(device) else "cuda:0")
+        self.num_envs, self.horizon = num_envs, horizon
+        self.observation_dim, self.action_dim = observation_dim, action_dim
+        self.batch_size = N = num_envs * horizon
+        if cfg.num_mini_batches < 1 or N % cfg.num_mini_batches:
+            raise ValueError("num_mini_batches must be positive and divide the rollout batch size.")
+        self.mini_batch_size = M = N // cfg.num_mini_batches
+        if M > 65535:
+            raise ValueError("Minibatches above 65535 rows are not supported by the gather kernel.")
+        O, A = observation_dim, action_dim
+        self.layers = len(cfg.hidden_dims) + 1
+        actor = _mlp_shapes("actor", O, A, cfg.hidden_dims)
+        critic = _mlp_shapes("critic", O, 1, cfg.hidden_dims)
+        shapes = dict(actor + critic + [("std", (A,))])
+        dev = self.device
+        with torch.cuda.device(dev):
+            # actor tensors + std parameter form clipping group 0, critic tensors group 1
+            order = [[n for n, _ in actor] + ["std"], [n for n, _ in critic]]
+            self.store = FlatStore(shapes, dev, groups=[[n] for n in order[0]] + [[n] for n in order[1]])
+            self.names = [n for n, _ in actor] + [n for n, _ in critic] + ["std"]
+            views = self.store.params()
+            self.parameters = [views[n] for n in self.names]
+            self.grads = self.store.grads()
+            rng = np.random.default_rng(cfg.seed)
+            for n, shape in actor + critic:
+                bound = 1.0 / math.sqrt(shape[-1] if n.endswith("weight") else shapes[n[:-4] + "weight"][-1])
+                views[n].copy_(torch.as_tensor(rng.uniform(-bound, bound, shape).astype(np.float32)))
+            std0 = math.log(cfg.initial_std) if cfg.std_type == "log" else cfg.initial_std
+            views["std"].fill_(std0)
+            self.distribution_parameter = views["std"]
+            if cfg.std_type == "log":
+                self.log_std = self.distribution_parameter
+            else:
+                self.std_param = self.distribution_parameter
+            first_critic = self.store.offsets[critic[0][0]]
+            self.group_ranges = [(0, first_critic), (first_critic, self.store.size)]
+            if not cfg.separate_grad_clipping:
+                self.group_ranges = [(0, self.store.size)]
+            self.timestep = torch.zeros(1, device=dev)
+            self.lr = torch.full((1,), float(cfg.learning_rate), device=dev)
+            self._make_optimizer()
+            z = lambda *s: torch.zeros(*s, device=dev)  # noqa: E731
+            self.observations = z(N, O)
+            self.actions = z(N, A)
+            self.means = z(N, A)
+            self.stds = z(N, A)
+            for name in ("log_probs", "values", "rewards", "next_values", "advantages", "returns"):
+                setattr(self, name, z(N))
+            self.terminated = torch.zeros(N, dtype=torch.int32, device=dev)
+            self.truncated = torch.zeros(N, dtype=torch.int32, device=dev)
+            self._seed = torch.tensor([cfg.seed], dtype=torch.int32, device=dev)
+            self._stats = z(2)
+            self._perm = torch.zeros(N, dtype=torch.int32, device=dev)
+            self.b_obs = z(M, O)
+            self.b_actions, self.b_means, self.b_stds = z(M, A), z(M, A), z(M, A)
+            self.b_log_probs, self.b_values, self.b_advantages, self.b_returns = z(M), z(M), z(M), z(M)
+            widths = (O, *cfg.hidden_dims)
+            self.actor_h = [z(M, w) for w in cfg.hidden_dims]
+            self.critic_h = [z(M, w) for w in cfg.hidden_dims]
+            self.actor_d = [z(M, w) for w in widths]
+            self.critic_d = [z(M, w) for w in widths]
+            self.mean = z(M, A)
+            self.value = z(M, 1)
+            self.dmean = z(M, A)
+            self.dvalue = z(M, 1)
+            self.dstd_rows = z(M, A)
+            self.row_terms = z(4, M)
+            self.totals = z(4)
+            self.metrics = self.totals[1:]  # policy loss, value loss, entropy of the last minibatch
+            self.loss = self.totals[:1]
+            self.kl = z(1)
+            max_width = max(A, 1, *cfg.hidden_dims)
+            self.partial = z(K.chunks(M) * max_width)
+            self.norm_partial = z((self.store.size + 4095) // 4096 + 1)
+            self.group_norms = [z(1) for _ in self.group_ranges]
+            self.workspace = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+            self._act_mean = None
+        self._update_graph = None
+
+    def _make_optimizer(self):
+        n = len(self.names)
+        store = self.store
+        ptrs = lambda buf: _native.pointer_array([store.view(buf, name).data_ptr() for name in self.names])  # noqa
+        rows = [1] * n
+        cols = [int(np.prod(store.shapes[name])) for name in self.names]
+        self.optimizer_handle = _native.create(
+            "rl_fused_optimizer_create", n, _native.int_array([3] * n), _native.ll_array(rows),
+            _native.ll_array(cols), ptrs(store.param), ptrs(store.grad), ptrs(store.m1), ptrs(store.m2), None, None,
+            None, _native.int_array([-1] * n), self.timestep.data_ptr(), self.lr.data_ptr(), 0.9, 0.999, 1e-8, 0.0, 1,
+            0, 0.0, 0.0, 0.0, 0, 1)
+
+    def __del__(self):
+        handle = getattr(self, "optimizer_handle", None)
+        if handle:
+            try:
+                _native.load().rl_fused_optimizer_destroy(handle)
+            except Exception:
+                pass
+
+    # ------------------------------------------------------------------
+    def _layer(self, prefix, i):
+        p = self.store.params()
+        return p[f"{prefix}.{i}.weight"], p[f"{prefix}.{i}.bias"]
+
+    def _mlp_forward(self, prefix, x, rows, hidden, out):
+        """Linear + ELU hidden layers (ELU fused in the GEMM epilogue), linear output."""
+        widths = (self.observation_dim, *self.config.hidden_dims)
+        inputs = x
+        for i, width in enumerate(self.config.hidden_dims):
+            w, b = self._layer(prefix, i)
+            K.linear_forward(inputs, w, hidden[i], rows=rows, in_dim=widths[i], out_dim=width, bias=b,
+                             epilogue="elu", mode=K.FP32)
+            inputs = hidden[i]
+        w, b = self._layer(prefix, self.layers - 1)
+        K.linear_forward(inputs, w, out, rows=rows, in_dim=widths[-1], out_dim=out.shape[1], bias=b, mode=K.FP32)
+
+    def _mlp_backward(self, prefix, x, rows, hidden, dout, dbufs):
+        widths = (self.observation_dim, *self.config.hidden_dims)
+        g = self.grads
+        d = dout
+        out_dim = dout.shape[1]
+        for i in reversed(range(self.layers)):
+            w, _ = self._layer(prefix, i)
+            inputs = x if i == 0 else hidden[i - 1]
+            K.linear_backward_weight(d, inputs, g[f"{prefix}.{i}.weight"], rows=rows, in_dim=widths[i],
+                                     out_dim=out_dim, mode=K.FP32, workspace=self.workspace)
+            K.bias_grad(d, g[f"{prefix}.{i}.bias"], self.partial, rows=rows, channels=out_dim)
+            if i > 0:
+                K.linear_backward_input(d, w, dbufs[i], rows=rows, in_dim=widths[i], out_dim=out_dim, mode=K.FP32)
+                _native.call("rl_elu_backward", dbufs[i].data_ptr(), hidden[i - 1].data_ptr(), dbufs[i].numel(),
+                             K.stream())
+                d = dbufs[i]
+                out_dim = widths[i]
+
+    # ------------------------------------------------------------------
+    def compute_returns(self) -> None:
+        cfg = self.config
+        _native.call("rl_gae", self.horizon, self.num_envs, float(cfg.gamma), float(cfg.gae_lambda),
+                     int(cfg.timeout_bootstrap == "current"), self.rewards.data_ptr(), self.values.data_ptr(),
+                     self.next_values.data_ptr(), self.terminated.data_ptr(), self.truncated.data_ptr(),
+                     self.advantages.data_ptr(), self.returns.data_ptr(), K.stream())
+        if cfg.normalize_advantages:
+            _native.call("rl_normalize_advantages", self.advantages.data_ptr(), self.batch_size,
+                         int(cfg.advantage_sample_std), self._stats.data_ptr(), K.stream())
+
+    def _minibatch(self, offset: int):
+        cfg = self.config
+        M, A, O = self.mini_batch_size, self.action_dim, self.observation_dim
+        _native.call("rl_ppo_gather", self._perm.data_ptr(), offset, M, O, A, O, self.observations.data_ptr(),
+                     self.actions.data_ptr(), self.log_probs.data_ptr(), self.values.data_ptr(),
+                     self.advantages.data_ptr(), self.returns.data_ptr(), self.means.data_ptr(),
+                     self.stds.data_ptr(), self.b_obs.data_ptr(), self.b_actions.data_ptr(),
+                     self.b_log_probs.data_ptr(), self.b_values.data_ptr(), self.b_advantages.data_ptr(),
+                     self.b_returns.data_ptr(), self.b_means.data_ptr(), self.b_stds.data_ptr(), K.stream())
+        self._mlp_forward("actor", self.b_obs, M, self.actor_h, self.mean)
+        std_type = int(cfg.std_type == "scalar")
+        _native.call("rl_ppo_kl_adapt", self.mean.data_ptr(), A, self.distribution_parameter.data_ptr(),
+                     self.b_means.data_ptr(), self.b_stds.data_ptr(), M, A, std_type, float(cfg.std_range[0]),
+                     float(cfg.std_range[1]), float(cfg.desired_kl), int(cfg.schedule == "adaptive"),
+                     self.kl.data_ptr(), self.lr.data_ptr(), K.stream())
+        self._mlp_forward("critic", self.b_obs, M, self.critic_h, self.value)
+        _native.call("rl_ppo_loss", self.mean.data_ptr(), A, self.value.data_ptr(),
+                     self.distribution_parameter.data_ptr(), self.b_actions.data_ptr(), self.b_log_probs.data_ptr(),
+                     self.b_values.data_ptr(), self.b_advantages.data_ptr(), self.b_returns.data_ptr(), M, A, std_type,
+                     float(cfg.std_range[0]), float(cfg.std_range[1]), float(cfg.clip_ratio),
+                     float(cfg.value_coefficient), float(cfg.entropy_coefficient), float(cfg.value_loss_scale),
+                     int(cfg.clip_value), self.dmean.data_ptr(), self.dvalue.data_ptr(), self.dstd_rows.data_ptr(),
+                     self.row_terms.data_ptr(), self.totals.data_ptr(), K.stream())
+        K.bias_grad(self.dstd_rows, self.grads["std"], self.partial, rows=M, channels=A)
+        self._mlp_backward("actor", self.b_obs, M, self.actor_h, self.dmean, self.actor_d)
+        self._mlp_backward("critic", self.b_obs, M, self.critic_h, self.dvalue, self.critic_d)
+        for (start, end), norm in zip(self.group_ranges, self.group_norms):
+            grad = self.store.grad[start:end]
+            _native.call("rl_sum_squares", grad.data_ptr(), grad.numel(), self.norm_partial.data_ptr(),
+                         norm.data_ptr(), K.stream())
+            _native.call("rl_clip_by_norm", grad.data_ptr(), grad.numel(), norm.data_ptr(),
+                         float(cfg.max_grad_norm), K.stream())
+        _native.call("rl_fused_optimizer_step", self.optimizer_handle, 1, 0, 0, None, K.stream())
+
+    def launch_update(self) -> None:
+        """Enqueue the entire PPO update (graph-capturable)."""
+        cfg = self.config
+        self.compute_returns()
+        if cfg.num_mini_batches > 1:
+            _native.call("rl_advance_int", self._seed.data_ptr(), K.stream())
+            _native.call("rl_permutation", self.batch_size, int(cfg.seed) * 2654435761 + 1, self._seed.data_ptr(),
+                         None, self._perm.data_ptr(), K.stream())
+        else:
+            self._perm.copy_(torch.arange(self.batch_size, dtype=torch.int32, device=self.device))
+        for _ in range(cfg.epochs):
+            for mb in range(cfg.num_mini_batches):
+                self._minibatch(mb * self.mini_batch_size)
+
+    def warmup(self) -> None:
+        state = self.state_dict()
+        self.launch_update()
+        torch.cuda.synchronize(self.device)
+        self.load_state_dict(state)
+
+    def update(self, capture: bool = True) -> None:
+        with torch.cuda.device(self.device):
+            if not capture:
+                self.launch_update()
+                return
+            if self._update_graph is None:
+                self.warmup()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    self.launch_update()
+                self._update_graph = graph
+            self._update_graph.replay()
+
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def act(self, observations, deterministic: bool = False):
+        """Gaussian actions from the actor mean and the distribution parameter (rollout helper)."""
+        obs = torch.as_tensor(observations, device=self.device, dtype=torch.float32).contiguous()
+        n = obs.shape[0]
+        hidden = [torch.empty(n, w, device=self.device) for w in self.config.hidden_dims]
+        mean = torch.empty(n, self.action_dim, device=self.device)
+        value = torch.empty(n, 1, device=self.device)
+        self._mlp_forward("actor", obs, n, hidden, mean)
+        self._mlp_forward("critic", obs, n, hidden, value)
+        p = self.distribution_parameter
+        std = p.clamp(*self.config.std_range) if self.config.std_type == "scalar" else torch.exp(p)
+        noise = torch.zeros_like(mean) if deterministic else torch.randn_like(mean)
+        actions = mean + std * noise
+        log_std = torch.log(std)
+        self._act = (actions, (-0.5 * (noise * noise + 2 * log_std + math.log(2 * math.pi))).sum(1), value[:, 0],
+                     mean, std.expand_as(mean).contiguous())
+        return actions
+
+    @torch.no_grad()
+    def store(self, step, observations, rewards, terminated, truncated, next_observations) -> None:
+        if not 0 <= step < self.horizon:
+            raise ValueError("step must be within the rollout horizon.")
+        actions, log_probs, values, mean, std = self._act
+        n = self.num_envs
+        sl = slice(step * n, (step + 1) * n)
+        hidden = [torch.empty(n, w, device=self.device) for w in self.config.hidden_dims]
+        next_value = torch.empty(n, 1, device=self.device)
+        self._mlp_forward("critic", torch.as_tensor(next_observations, device=self.device).float().contiguous(), n,
+                          hidden, next_value)
+        self.observations[sl] = torch.as_tensor(observations, device=self.device).float()
+        self.actions[sl], self.log_probs[sl], self.values[sl] = actions, log_probs, values
+        self.means[sl], self.stds[sl] = mean, std
+        self.rewards[sl] = torch.as_tensor(rewards, device=self.device).float()
+        self.terminated[sl] = torch.as_tensor(terminated, device=self.device).int()
+        self.truncated[sl] = torch.as_tensor(truncated, device=self.device).int()
+        self.next_values[sl] = next_value[:, 0]
+
+    def health_metrics(self) -> dict:
+        parameter = self.distribution_parameter.detach().cpu().numpy()
+        std = np.clip(parameter, *self.config.std_range) if self.config.std_type == "scalar" else np.exp(parameter)
+        totals = self.totals.cpu().numpy()
+        result = {
+            "std_min": float(std.min()), "std_mean": float(std.mean()), "std_max": float(std.max()),
+            "std_parameter_min": float(parameter.min()), "std_parameter_max": float(parameter.max()),
+            "learning_rate": float(self.lr.item()), "kl": float(self.kl.item()),
+            "policy_loss": float(totals[1]), "value_loss": float(totals[2]), "entropy": float(totals[3]),
+            "optimizer_updates": float(self.timestep.item()),
+        }
+        if self.config.separate_grad_clipping:
+            result["actor_grad_norm"] = float(np.sqrt(self.group_norms[0].item()))
+            result["critic_grad_norm"] = float(np.sqrt(self.group_norms[1].item()))
+        return result
+
+    def state_dict(self) -> dict:
+        torch.cuda.synchronize(self.device)
+        m1, m2 = self.store.moments()
+        state = {f"parameter_{i}": p.detach().cpu().numpy().copy() for i, p in enumerate(self.parameters)}
+        state.update({f"adam_m1_{i}": m1[n].cpu().numpy().copy() for i, n in enumerate(self.names)})
+        state.update({f"adam_m2_{i}": m2[n].cpu().numpy().copy() for i, n in enumerate(self.names)})
+        state["adam_timestep"] = self.timestep.cpu().numpy().copy()
+        state["adam_lr"] = self.lr.cpu().numpy().copy()
+        state["seed"] = self._seed.cpu().numpy().copy()
+        return state
+
+    @torch.no_grad()
+    def load_state_dict(self, state: dict) -> None:
+        m1, m2 = self.store.moments()
+        arrays = {f"parameter_{i}": p for i, p in enumerate(self.parameters)}
+        arrays.update({f"adam_m1_{i}": m1[n] for i, n in enumerate(self.names)})
+        arrays.update({f"adam_m2_{i}": m2[n] for i, n in enumerate(self.names)})
+        arrays.update(adam_timestep=self.timestep, adam_lr=self.lr, seed=self._seed)
+        if set(state) != set(arrays):
+            raise ValueError("Checkpoint parameter or optimizer keys do not match this model.")
+        for name, array in arrays.items():
+            if tuple(np.asarray(state[name]).shape) != tuple(array.shape):
+                raise ValueError(f"Checkpoint shape for {name} does not match this model.")
+        for name, array in arrays.items():
+            array.copy_(torch.as_tensor(np.asarray(state[name])).to(array.dtype))
+
+    def save(self, path) -> None:
+        with Path(path).open("wb") as file:
+            np.savez(file, **self.state_dict())
+
+    def load(self, path) -> None:
+        with np.load(path, allow_pickle=False) as state:
+            self.load_state_dict(dict(state))

@@ -1,0 +1,183 @@
+"""PPO update on the GPU: the reference's known answers and parity with the CPU oracle."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ppo as OP
+from robolearn_amd import _native
+from robolearn_amd import kernels as K
+from robolearn_amd.config import PPOConfig
+
+pytestmark = pytest.mark.gpu
+
+
+def _agent(obs, act, envs, horizon, cfg):
+    from robolearn_amd.ppo import WarpPPO
+
+    return WarpPPO(obs, act, envs, horizon, cfg)
+
+
+def test_gae_distinguishes_termination_timeout_and_rollout_boundary(gpu):
+    """Known answer of tests/test_warp_ppo.py:23-46."""
+    agent = _agent(1, 1, 2, 3, PPOConfig(hidden_dims=(), normalize_advantages=False, activation="elu"))
+    reward = np.array([[1, 2], [3, 4], [5, 6]], dtype=np.float32)
+    value = np.array([[0.1, 0.2], [0.3, 0.4], [0.5, 0.6]], dtype=np.float32)
+    next_value = np.array([[0.3, 0.4], [9, 10], [11, 12]], dtype=np.float32)
+    terminated = np.array([[0, 0], [1, 0], [0, 0]], dtype=np.int32)
+    truncated = np.array([[0, 0], [0, 1], [0, 0]], dtype=np.int32)
+    for name, data in (("rewards", reward), ("values", value), ("next_values", next_value),
+                       ("terminated", terminated), ("truncated", truncated)):
+        getattr(agent, name).copy_(torch.as_tensor(data.flatten()))
+    expected = np.zeros_like(reward)
+    tail = np.zeros(2, dtype=np.float32)
+    for t in range(2, -1, -1):
+        delta = reward[t] + 0.99 * (1 - terminated[t]) * next_value[t] - value[t]
+        tail = delta + 0.99 * 0.95 * (1 - np.maximum(terminated[t], truncated[t])) * tail
+        expected[t] = tail
+    agent.compute_returns()
+    np.testing.assert_allclose(agent.advantages.cpu().numpy().reshape(3, 2), expected, rtol=1e-6)
+    np.testing.assert_allclose(agent.returns.cpu().numpy().reshape(3, 2), expected + value, rtol=1e-6)
+
+
+def test_advantage_normalization_preserves_small_variance_at_large_offset(gpu):
+    """Known answer of tests/test_warp_ppo.py:49-56."""
+    agent = _agent(1, 1, 2, 1, PPOConfig(hidden_dims=(), gamma=0.0, activation="elu"))
+    rewards = np.array([10000.0, 10001.0], dtype=np.float32)
+    agent.rewards.copy_(torch.as_tensor(rewards))
+    agent.compute_returns()
+    np.testing.assert_allclose(agent.advantages.cpu().numpy(), [-1.0, 1.0], rtol=1e-6)
+    np.testing.assert_array_equal(agent.returns.cpu().numpy(), rewards)
+
+
+def test_clipped_gaussian_loss_and_gradient_match_reference(gpu):
+    """Known answer + central finite differences of tests/test_warp_ppo.py:59-119."""
+    mean_np = np.array([[0.4, 0.1], [-0.3, 0.2], [0.2, -0.2]], dtype=np.float32)
+    action_np = np.array([[0.0, 0.5], [0.6, 0.1], [-0.5, 0.4]], dtype=np.float32)
+    old_lp_np = np.array([-2.4, -1.8, -2.0], dtype=np.float32)
+    advantage_np = np.array([1.0, -0.8, 0.4], dtype=np.float32)
+    value_np = np.array([[0.8], [1.0], [-0.5]], dtype=np.float32)
+    old_value_np = np.array([0.2, 1.3, -0.4], dtype=np.float32)
+    return_np = np.array([0.7, -0.2, 1.0], dtype=np.float32)
+    log_std_np = np.array([-0.2, 0.1], dtype=np.float32)
+    d = lambda a: torch.as_tensor(a).to(gpu).contiguous()  # noqa: E731
+    dmean, dvalue, dstd_rows = d(np.zeros((3, 2), np.float32)), d(np.zeros(3, np.float32)), d(np.zeros((3, 2), np.float32))
+    row_terms, totals = d(np.zeros((4, 3), np.float32)), d(np.zeros(4, np.float32))
+    args = [d(mean_np), d(value_np), d(log_std_np), d(action_np), d(old_lp_np), d(old_value_np), d(advantage_np),
+            d(return_np)]
+    _native.call("rl_ppo_loss", args[0].data_ptr(), 2, args[1].data_ptr(), args[2].data_ptr(), args[3].data_ptr(),
+                 args[4].data_ptr(), args[5].data_ptr(), args[6].data_ptr(), args[7].data_ptr(), 3, 2, 0, 1e-6, 1e6,
+                 0.2, 0.5, 0.01, 0.5, 1, dmean.data_ptr(), dvalue.data_ptr(), dstd_rows.data_ptr(),
+                 row_terms.data_ptr(), totals.data_ptr(), K.stream())
+    torch.cuda.synchronize()
+
+    def reference(mean_values=mean_np, value_values=value_np, std_values=log_std_np):
+        lp = (-0.5 * (((action_np - mean_values) * np.exp(-std_values)) ** 2 + 2 * std_values + np.log(2 * np.pi))).sum(1)
+        ratio = np.exp(lp - old_lp_np)
+        policy = -np.minimum(ratio * advantage_np, np.clip(ratio, 0.8, 1.2) * advantage_np).mean()
+        clipped_value = old_value_np + np.clip(value_values[:, 0] - old_value_np, -0.2, 0.2)
+        value_loss = 0.5 * np.maximum((value_values[:, 0] - return_np) ** 2, (clipped_value - return_np) ** 2).mean()
+        entropy = (std_values + 0.5 * np.log(2 * np.pi * np.e)).sum()
+        return policy + 0.5 * value_loss - 0.01 * entropy
+
+    np.testing.assert_allclose(totals.cpu().numpy()[0], reference(), rtol=1e-5, atol=1e-7)
+    gradients = {"mean_values": dmean.cpu().numpy(), "value_values": dvalue.cpu().numpy().reshape(3, 1),
+                 "std_values": dstd_rows.cpu().numpy().sum(0)}
+    for argument, data in (("mean_values", mean_np), ("value_values", value_np), ("std_values", log_std_np)):
+        numerical = np.zeros_like(data)
+        for index in np.ndindex(data.shape):
+            plus, minus = data.copy(), data.copy()
+            plus[index] += 1e-3
+            minus[index] -= 1e-3
+            numerical[index] = (reference(**{argument: plus}) - reference(**{argument: minus})) / 2e-3
+        np.testing.assert_allclose(gradients[argument], numerical, atol=2e-4, rtol=2e-3, err_msg=argument)
+
+
+def _config(**overrides):
+    base = dict(hidden_dims=(16, 8), activation="elu", std_type="scalar", epochs=5, num_mini_batches=4,
+                learning_rate=1.0e-3, schedule="adaptive", desired_kl=0.01, value_coefficient=1.0,
+                value_loss_scale=1.0, entropy_coefficient=0.008, advantage_sample_std=True,
+                timeout_bootstrap="current", separate_grad_clipping=True)
+    base.update(overrides)
+    return PPOConfig(**base)
+
+
+def _rollout(agent, seed=29):
+    """The fixed rollout of examples/diagnose_ppo_update.py:50-72 (synthetic, seeded)."""
+    rng = np.random.default_rng(seed)
+    n, obs_dim, act_dim = agent.batch_size, agent.observation_dim, agent.action_dim
+    observations = rng.normal(size=(n, obs_dim)).astype(np.float32)
+    means = rng.normal(scale=0.3, size=(n, act_dim)).astype(np.float32)
+    actions = means + rng.normal(size=(n, act_dim)).astype(np.float32)
+    data = {
+        "observations": observations, "actions": actions, "means": means, "stds": np.ones_like(means),
+        "values": rng.normal(scale=0.5, size=n).astype(np.float32),
+        "log_probs": (-0.5 * ((actions - means) ** 2 + math.log(2 * math.pi))).sum(1).astype(np.float32),
+        "rewards": rng.normal(0.2, 0.05, size=n).astype(np.float32),
+        "next_values": rng.normal(0.0, 0.2, size=n).astype(np.float32),
+        "terminated": np.zeros(n, dtype=np.int32), "truncated": np.zeros(n, dtype=np.int32),
+    }
+    data["terminated"][min(18, n - 1)] = 1
+    data["truncated"][min(39, n - 2)] = 1
+    for key, value in data.items():
+        getattr(agent, key).copy_(torch.as_tensor(value))
+    return data
+
+
+@pytest.mark.parametrize("separate", [True, False])
+def test_update_matches_oracle(gpu, separate):
+    cfg = _config(separate_grad_clipping=separate)
+    agent = _agent(7, 3, 16, 4, cfg)
+    initial = agent.state_dict()
+    data = _rollout(agent)
+    agent.launch_update()
+    torch.cuda.synchronize()
+    permutation = agent._perm.cpu().numpy().astype(np.int64)
+    assert np.array_equal(np.sort(permutation), np.arange(agent.batch_size))
+    oracle = OP.PPOOracle(7, 3, 16, 4, cfg, [initial[f"parameter_{i}"] for i in range(len(agent.parameters))])
+    result = oracle.update(data, permutation)
+    state = agent.state_dict()
+    health = agent.health_metrics()
+    assert health["learning_rate"] == pytest.approx(result["learning_rate"], rel=1e-6)
+    assert health["kl"] == pytest.approx(result["kl"], rel=1e-4, abs=1e-7)
+    assert health["policy_loss"] == pytest.approx(result["policy_loss"], rel=1e-4, abs=1e-6)
+    assert health["value_loss"] == pytest.approx(result["value_loss"], rel=1e-4, abs=1e-6)
+    assert health["entropy"] == pytest.approx(result["entropy"], rel=1e-4, abs=1e-6)
+    np.testing.assert_allclose(agent.advantages.cpu().numpy(), oracle.advantages.numpy(), atol=1e-5)
+    np.testing.assert_allclose(agent.returns.cpu().numpy(), oracle.returns.numpy(), atol=1e-5)
+    moments = oracle.moments()
+    for i, p in enumerate(oracle.params):
+        np.testing.assert_allclose(state[f"parameter_{i}"], p.detach().numpy(), atol=2e-4, rtol=0, err_msg=str(i))
+        np.testing.assert_allclose(state[f"adam_m1_{i}"].reshape(-1), moments[i][0].numpy().reshape(-1), atol=2e-4)
+        np.testing.assert_allclose(state[f"adam_m2_{i}"].reshape(-1), moments[i][1].numpy().reshape(-1), atol=2e-4)
+
+
+def test_captured_update_matches_eager_and_checkpoint_preserves_graph(gpu, tmp_path):
+    """Mirrors tests/test_warp_ppo.py:122-148."""
+    config = PPOConfig(hidden_dims=(16,), epochs=2, activation="elu")
+    eager = _agent(3, 2, 8, 4, config)
+    captured = _agent(3, 2, 8, 4, config)
+    captured.load_state_dict(eager.state_dict())
+    rng = np.random.default_rng(7)
+    for name, shape in (("observations", (32, 3)), ("actions", (32, 2)), ("rewards", (32,))):
+        samples = torch.as_tensor(rng.normal(size=shape).astype(np.float32))
+        getattr(eager, name).copy_(samples)
+        getattr(captured, name).copy_(samples)
+    for _ in range(2):
+        eager.update(capture=False)
+        captured.update()
+    for expected, actual in zip(eager.parameters, captured.parameters):
+        np.testing.assert_allclose(actual.cpu().numpy(), expected.cpu().numpy(), rtol=2e-5, atol=2e-6)
+    checkpoint = tmp_path / "ppo.npz"
+    captured.save(checkpoint)
+    saved = captured.state_dict()
+    captured.update()
+    captured.load(checkpoint)
+    for key, value in saved.items():
+        np.testing.assert_array_equal(captured.state_dict()[key], value)
+    captured.update()
+    eager.update(capture=False)
+    for expected, actual in zip(eager.parameters, captured.parameters):
+        np.testing.assert_allclose(actual.cpu().numpy(), expected.cpu().numpy(), rtol=2e-5, atol=2e-6)
