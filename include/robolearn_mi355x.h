@@ -1,0 +1,263 @@
+/* C ABI of librl_mi355x.so: the MI355X learner hot path of RoboLearn.
+ *
+ * Conventions (as robolearn/cuda/kernels.cu:4-49):
+ *   - int status 0 on success, -1 on a synchronous error; the message is in a
+ *     thread-local buffer returned by rl_last_error().
+ *   - Handle-returning create calls return NULL on error.  Create/destroy may
+ *     allocate and must run outside stream capture.
+ *   - Run/step calls only enqueue work on the caller's stream (a hipStream_t
+ *     passed as void*): no allocation, no synchronization, graph-capturable.
+ *   - All device buffers are caller-owned; float arrays are fp32 unless a
+ *     parameter says bf16 (stored as 16-bit bf16 bit patterns, RNE).
+ *   - Row-major layouts; "ensemble" batches independent members (the twin
+ *     critics) with member strides.
+ * Paths below are relative to the reference tree.
+ */
+#ifndef ROBOLEARN_MI355X_H
+#define ROBOLEARN_MI355X_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- errors ------------------------------------------------------------ */
+/* replaces robolearn/cuda/kernels.cu:408 */
+const char* rl_last_error(void);
+
+/* ---- dense layers ------------------------------------------------------ */
+/* Column-major D = op(A) op(B) + beta C (+ bias[m]); replaces
+ * robolearn/cuda/kernels.cu:528-538 (create), :689 (workspace), :540 (autotune,
+ * accepted as a no-op), :654 (metadata), :698-731 (run), :733 (destroy).
+ * input_dtype: 0 fp32, 1 bf16 operands in memory (the reference's fp16), 2 fp32
+ * stored with bf16 compute. */
+void* rl_plan_create(int m, int n, int k, int transa, int transb, int lda, int ldb, int ldd, int use_bias,
+                     int allow_tf32, size_t workspace_limit);
+void* rl_plan_create_mixed(int m, int n, int k, int transa, int transb, int lda, int ldb, int ldd, int use_bias,
+                           int allow_tf32, int input_dtype, size_t workspace_limit);
+size_t rl_plan_workspace(void* plan);
+int rl_plan_autotune(void* plan, float beta, void* stream);
+const char* rl_plan_tuning_metadata(void* plan);
+int rl_plan_run(void* plan, const void* a, const void* b, const void* c, void* d, const void* bias, void* workspace,
+                size_t workspace_bytes, float beta, void* stream);
+int rl_plan_destroy(void* plan);
+
+/* Row-major batched D[b] = act(op(A[b]) op(B[b]) + bias[b]) + beta C[b] on MFMA
+ * (mode 0: fp32 v_mfma_f32_32x32x2_f32, mode 1: bf16 v_mfma_f32_32x32x16_bf16).
+ * A(m,k) = a_kcontig ? A[m*lda+k] : A[k*lda+m]; B(k,n) = b_kcontig ? B[n*ldb+k]
+ * : B[k*ldb+n].  epilogue 0 none, 1 ReLU, 2 ELU.  splits > 1 reduces over K in
+ * fixed order through workspace.  Serves the three plans of one Linear,
+ * robolearn/cuda/linear.py:179-185, 341-360, and the ensemble einsum of
+ * robolearn/flashsac/layers.py:174-186. */
+int rl_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int m, int n, int k, int batch,
+            const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
+            const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
+            float beta, int epilogue, int splits, float* workspace, size_t workspace_bytes, void* stream);
+size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, int splits);
+
+/* ---- optimizer ---------------------------------------------------------- */
+/* One pass fusing Adam (form 0: torch.optim.Adam as robolearn/flashsac/agent.py:64-65;
+ * form 1: robolearn/cuda/kernels.cu:317-337), the on-device LR schedule
+ * (robolearn/flashsac/_utils/scheduler.py:43-65, robolearn/warp/flashsac.py:242-259),
+ * the unit-norm projection (kinds 0 row / 1 BN pair / 2 RMS, robolearn/cuda/flash_kernels.cuh:112-131)
+ * and the target EMA (flash_kernels.cuh:133-140).  Replaces the CudaAdam.step ->
+ * CudaProjection.step -> CudaEMA.step sequence of robolearn/warp/flashsac.py:645-649,
+ * 788-789, 874-876, 927-929.  kind 3 = plain (no projection).  partner[i] names the
+ * BN bias tensor of a kind-1 weight.  grads == NULL creates a projection/EMA-only plan. */
+void* rl_fused_optimizer_create(size_t count, const int* kinds, const long long* rows, const long long* cols,
+                                void* const* params, const void* const* grads, void* const* m1, void* const* m2,
+                                void* const* targets, void* const* shadows, void* const* target_shadows,
+                                const int* partner, void* timestep, void* learning_rate, double beta1, double beta2,
+                                double eps, double tau, int form, int schedule_enabled, double lr_init,
+                                double lr_peak, double lr_end, long long warmup_steps, long long decay_steps);
+int rl_fused_optimizer_step(void* plan, int do_adam, int do_project, int do_ema, const void* skip, void* stream);
+int rl_fused_optimizer_destroy(void* plan);
+
+/* robolearn/cuda/kernels.cu:760-820, 878-916 */
+void* rl_adam_create(size_t count, const void* const* parameters, const void* const* gradients,
+                     const void* const* m1, const void* const* m2, const size_t* sizes, void* timestep,
+                     void* learning_rate, double beta1, double beta2, double eps);
+int rl_adam_step(void* plan, void* stream);
+int rl_adam_destroy(void* plan);
+
+/* robolearn/cuda/flash_kernels.cuh:398-445 (shadows receive bf16 copies) */
+void* rl_flash_projection_create(size_t count, const void* const* first, const void* const* second,
+                                 const size_t* lengths, const int* kinds);
+void* rl_flash_projection_create_with_shadows(size_t count, const void* const* first, const void* const* second,
+                                              const size_t* lengths, const int* kinds, const void* const* shadows);
+int rl_flash_projection_step(void* plan, void* stream);
+int rl_flash_projection_destroy(void* plan);
+
+/* robolearn/cuda/flash_kernels.cuh:447-498 */
+void* rl_flash_ema_create(size_t count, const void* const* source, const void* const* target,
+                          const size_t* lengths, float tau);
+void* rl_flash_ema_create_with_shadows(size_t count, const void* const* source, const void* const* target,
+                                       const size_t* lengths, float tau, const void* const* shadows);
+int rl_flash_ema_step(void* plan, void* stream);
+int rl_flash_ema_destroy(void* plan);
+
+/* ---- normalization ------------------------------------------------------ */
+/* Ensemble BatchNorm; x_stride 0 broadcasts one input to every member; optional
+ * residual is added after the ReLU (fuses robolearn/flashsac/layers.py:105-113).
+ * Replaces robolearn/cuda/flash_kernels.cuh:500-543 for the stacked critics of
+ * robolearn/flashsac/layers.py:189-222.  partial: ensemble*2*ceil(rows/256)*channels. */
+int rl_bn_forward_ex(int ensemble, const float* x, long long x_stride, const float* w, const float* b,
+                     float* running_mean, float* running_var, float* mean, float* var, float* partial,
+                     const float* residual, float* y, void* y_bf16, int rows, int channels, float eps,
+                     float momentum, int training, int relu, int update_running, void* stream);
+/* y == NULL with relu recomputes the ReLU mask from x, the statistics and (w, b).
+ * sums: 2*ensemble*channels.  Replaces flash_kernels.cuh:545-609. */
+int rl_bn_backward_ex(int ensemble, const float* x, long long x_stride, const float* dy, const float* y,
+                      const float* w, const float* b, const float* mean, const float* var, float* partial,
+                      float* sums, float* dx, float* dw, float* db, void* dx_bf16, int rows, int channels,
+                      float eps, int training, int relu, int accumulate_dx, int accumulate_params, void* stream);
+/* RMSNorm over rows [0, rows) of each member (member_stride elements apart);
+ * replaces flash_kernels.cuh:611-634, covers layers.py:67-74 and :225-240. */
+int rl_rms_forward_ex(int ensemble, const float* x, const float* w, float* ms, float* y, int rows, int channels,
+                      long long member_stride, float eps, void* stream);
+int rl_rms_backward_ex(int ensemble, const float* x, const float* dy, const float* w, const float* ms,
+                       float* partial, float* dx, float* dw, int rows, int channels, long long member_stride,
+                       float eps, int accumulate_dx, int accumulate_dw, void* stream);
+/* Deterministic column sums; replaces robolearn/cuda/kernels.cu:237-251, 742-758. */
+int rl_bias_grad_ex(int ensemble, const float* dy, float* db, float* partial, int rows, int channels, int accumulate,
+                    void* stream);
+
+/* Reference-signature entries: robolearn/cuda/flash_kernels.cuh:529-634 (fp16
+ * side outputs become bf16), robolearn/cuda/kernels.cu:742. */
+int rl_flash_bn_forward(const float* x, const float* w, const float* b, float* running_mean, float* running_var,
+                        float* mean, float* var, float* partial, float* y, int batch, int channels, float eps,
+                        float momentum, int training, int relu, void* stream);
+int rl_flash_bn_forward_with_bf16(const float* x, const float* w, const float* b, float* running_mean,
+                                  float* running_var, float* mean, float* var, float* partial, float* y,
+                                  void* half_output, int batch, int channels, float eps, float momentum,
+                                  int training, int relu, void* stream);
+int rl_flash_bn_backward(const float* x, const float* dy, const float* y, const float* w, const float* mean,
+                         const float* var, float* partial, float* sums, float* dx, float* dw, float* db, int batch,
+                         int channels, float eps, int training, int relu, void* stream);
+int rl_flash_bn_backward_controlled(const float* x, const float* dy, const float* y, const float* w,
+                                    const float* mean, const float* var, float* partial, float* sums, float* dx,
+                                    float* dw, float* db, void* half_dx, int overwrite_dx, int batch, int channels,
+                                    float eps, int training, int relu, void* stream);
+int rl_flash_rms_forward(const float* x, const float* w, float* var, float* y, int batch, int channels, float eps,
+                         void* stream);
+int rl_flash_rms_backward(const float* x, const float* dy, const float* w, const float* var, float* partial,
+                          float* dx, float* dw, int batch, int channels, float eps, void* stream);
+int rl_bias_grad(const void* dy, void* db, int batch, int channels, void* stream);
+
+/* ---- categorical head and TD target ------------------------------------- */
+/* Fixed-order sum (op 0, times scale) or max (op 1) of a vector into out[0]. */
+int rl_reduce(const float* x, long long n, float scale, int op, float* out, void* stream);
+/* lp = log_softmax(logits + bias), Q = sum exp(lp) support (robolearn/flashsac/layers.py:294-303). */
+int rl_categorical_head_forward(const float* logits, const float* bias, long long bias_stride, const float* support,
+                                float* log_probs, float* values, long long rows, int bins, int ensemble,
+                                void* stream);
+/* dlogits = dQ p (z - Q): the value path of robolearn/cuda/categorical_kernels.cuh:56-75. */
+int rl_categorical_head_backward_q(const float* logits, const float* bias, long long bias_stride,
+                                   const float* support, const float* dvalues, float* dlogits, long long rows,
+                                   int bins, int ensemble, void* stream);
+/* Fused min-Q selection + two-hot TD projection + cross-entropy + its logit
+ * gradient for both online critics: robolearn/flashsac/updates.py:19-80, 248-257
+ * (replaces rl_flash_categorical_target + the CE kernel, robolearn/warp/flashsac.py:223-233). */
+int rl_categorical_td_cross_entropy(const float* target_logits, const float* target_bias, long long target_rows,
+                                    const float* online_logits, const float* online_bias, long long online_rows,
+                                    const float* support, const float* reward, const float* terminated,
+                                    const float* discount, const float* next_log_probs, const float* alpha,
+                                    float min_v, float max_v, long long batch, int bins, float scale,
+                                    float* target_out, float* dlogits, float* loss_rows, float* entropy_rows,
+                                    float* q_next, void* stream);
+/* robolearn/cuda/categorical_kernels.cuh:126-176 (bins <= 512). */
+int rl_flash_categorical_forward(const void* raw, const void* bias, const void* support, void* log_probs,
+                                 void* values, int batch, int bins, void* stream);
+int rl_flash_categorical_backward(const void* log_probs, const void* support, const void* dlog_probs,
+                                  const void* dvalues, void* scratch, void* draw, void* dbias, int batch, int bins,
+                                  void* stream);
+int rl_flash_categorical_target(const void* q, const void* log_probs, const void* reward, const void* terminated,
+                                const void* discount, const void* next_log_probs, const void* alpha, void* target,
+                                void* maximum_entropy, int batch, int bins, float min_v, float max_v, void* stream);
+
+/* ---- policy, replay and glue -------------------------------------------- */
+/* Philox-4x32-10 normals / replay indices; counter is a device int64 draw counter
+ * (replaces the Warp RNG of robolearn/warp/flashsac.py:38-50 and
+ * robolearn/warp/_flash_replay.py:116-160; robolearn/flashsac/replay.py:179-183 samples
+ * with torch.randint). */
+int rl_philox_normal(unsigned long long seed, const long long* counter, unsigned int stream_id, float* out,
+                     long long n, void* stream);
+int rl_replay_sample_indices(unsigned long long seed, const long long* counter, unsigned int stream_id,
+                             const long long* count, long long fixed_count, long long* idx, long long n,
+                             void* stream);
+/* Seven-field replay gather, robolearn/flashsac/replay.py:185-194 (out_truncated/truncated optional). */
+int rl_replay_gather(const long long* idx, long long batch, long long capacity, int obs_dim, int action_dim,
+                     const float* obs, const float* next_obs, const float* action, const float* reward,
+                     const float* terminated, const float* truncated, const float* discount, float* out_obs,
+                     float* out_next_obs, float* out_action, float* out_reward, float* out_terminated,
+                     float* out_truncated, float* out_discount, int* error, void* stream);
+/* Column concatenation (robolearn/warp/flashsac.py:53-63, 166-182). */
+int rl_concat_columns(float* out, long long ld_out, long long rows, const float* a, long long lda, int ca,
+                      const float* b, long long ldb, int cb, void* stream);
+/* Tanh-Gaussian sample and log-prob (robolearn/flashsac/layers.py:134-166,
+ * robolearn/warp/flashsac.py:72-95) and its backward. head = [mean | raw log-std]. */
+int rl_tanh_gaussian_forward(const float* head, const float* noise, float* actions, long long ld_actions,
+                             float* log_probs, long long rows, int action_dim, int deterministic, void* stream);
+int rl_tanh_gaussian_backward(const float* head, const float* noise, const float* dactions, long long ld_dactions,
+                              long long grad_rows, const float* dlog_probs, float* dhead, long long rows,
+                              int action_dim, void* stream);
+/* Actor loss, entropy, mean action and their gradients (robolearn/flashsac/updates.py:105-137,
+ * robolearn/warp/flashsac.py:109-153). */
+int rl_actor_objective(const float* q0, const float* q1, const float* log_probs, const float* actions,
+                       long long ld_actions, const float* replay_actions, const float* alpha, float bc_alpha,
+                       long long batch, long long total_rows, int action_dim, float* metrics, float* dlog_probs,
+                       float* dq0, float* dq1, float* dactions_bc, void* stream);
+/* Temperature loss and gradient (robolearn/flashsac/updates.py:297-326). */
+int rl_temperature_objective(const float* log_temp, const float* entropy, float target_entropy, float* grad,
+                             float* metrics, void* stream);
+int rl_exp_scalar(const float* x, float* out, void* stream);
+int rl_fill(float* x, long long n, float value, void* stream);
+int rl_add(float* x, const float* y, long long n, void* stream);
+/* robolearn/warp/flashsac.py:262-266 */
+int rl_advance_counters(long long* counters, int actor, void* stream);
+/* robolearn/flashsac/_utils/reward_normalization.py:28-38 */
+int rl_scale_rewards(float* rewards, long long n, const float* var, const float* r_max, float g_max, float eps,
+                     void* stream);
+
+/* ---- PPO ------------------------------------------------------------------ */
+/* robolearn/warp/ppo.py:101-133 */
+int rl_gae(int horizon, int num_envs, float gamma, float lambda, int current_timeout_bootstrap, const float* rewards,
+           const float* values, const float* next_values, const int* terminated, const int* truncated,
+           float* advantages, float* returns, void* stream);
+/* robolearn/warp/ppo.py:136-159 (fixed-order two-pass) */
+int rl_normalize_advantages(float* advantages, long long n, int sample_std, float* stats, void* stream);
+/* Keyed Feistel permutation with cycle walking; replaces _shuffle_keys +
+ * radix_sort_pairs, robolearn/warp/ppo.py:162-169, 595-603. */
+int rl_permutation(long long n, unsigned long long seed, const int* seed_counter, long long* perm64, int* perm32,
+                   void* stream);
+/* robolearn/warp/ppo.py:21-23 */
+int rl_advance_int(int* value, void* stream);
+/* robolearn/warp/ppo.py:172-204 */
+int rl_ppo_gather(const int* indices, long long offset, long long rows, int obs_dim, int action_dim, int obs_ld,
+                  const float* obs, const float* actions, const float* log_probs, const float* values,
+                  const float* advantages, const float* returns, const float* means, const float* stds, float* b_obs,
+                  float* b_actions, float* b_log_probs, float* b_values, float* b_advantages, float* b_returns,
+                  float* b_means, float* b_stds, void* stream);
+/* robolearn/warp/ppo.py:207-238 */
+int rl_ppo_kl_adapt(const float* mean, long long ld_mean, const float* std_param, const float* old_mean,
+                    const float* old_std, long long rows, int action_dim, int std_type, float std_min, float std_max,
+                    float desired_kl, int adapt, float* kl_out, float* lr, void* stream);
+/* robolearn/warp/ppo.py:255-310 forward and analytic backward; totals = (loss, policy, value, entropy). */
+int rl_ppo_loss(const float* mean, long long ld_mean, const float* value, const float* std_param,
+                const float* actions, const float* old_log_probs, const float* old_values, const float* advantages,
+                const float* returns, long long rows, int action_dim, int std_type, float std_min, float std_max,
+                float clip_ratio, float value_coefficient, float entropy_coefficient, float value_loss_scale,
+                int clip_value, float* dmean, float* dvalue, float* dstd_rows, float* row_terms, float* totals,
+                void* stream);
+/* robolearn/warp/ppo.py:241-252 (fixed-order partials: ceil(n/4096) floats) */
+int rl_sum_squares(const float* x, long long n, float* partial, float* out, void* stream);
+int rl_clip_by_norm(float* g, long long n, const float* sum_squares, float max_norm, void* stream);
+/* ELU backward from the activation output (robolearn/warp/ppo.py:345). */
+int rl_elu_backward(float* dx, const float* y, long long n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,311 @@
+"""Pins the CPU oracle: reference golden vectors, reference known answers,
+closed forms and brute force.  CPU only."""
+
+import math
+from collections import OrderedDict
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import flashsac as O
+from oracle import ppo as OP
+from robolearn_amd.config import FlashSACConfig, PPOConfig
+
+GOLDEN = np.load(Path(__file__).resolve().parent / "golden" / "flashsac_modules.npz", allow_pickle=False)
+
+
+def _group(prefix):
+    return OrderedDict((k[len(prefix):], torch.tensor(GOLDEN[k])) for k in GOLDEN.files if k.startswith(prefix))
+
+
+def _dims():
+    return O.Dims(actor_obs=4, critic_obs=4, action=2, actor_hidden=16, actor_blocks=1, critic_hidden=16,
+                  critic_blocks=2, bins=11, min_v=-10.0, max_v=10.0)
+
+
+def _split(state, shapes):
+    params = OrderedDict((k, state[k].clone().requires_grad_(True)) for k in shapes)
+    buffers = OrderedDict((k, v.clone()) for k, v in state.items() if k not in shapes)
+    return params, buffers
+
+
+def test_actor_forward_backward_matches_reference_modules():
+    d = _dims()
+    params, buffers = _split(_group("actor.init."), O.actor_parameter_shapes(d))
+    x, noise = torch.tensor(GOLDEN["actor.train.x"]), torch.tensor(GOLDEN["actor.train.noise"])
+    actions, log_prob, _, _ = O.actor_forward(params, buffers, x, True, noise, d)
+    torch.testing.assert_close(actions, torch.tensor(GOLDEN["actor.train.actions"]), rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(log_prob, torch.tensor(GOLDEN["actor.train.log_prob"]), rtol=1e-5, atol=1e-5)
+    coef = torch.tensor(GOLDEN["actor.train.coef"])
+    loss = (0.3 * log_prob).mean() + (coef * actions).mean()
+    grads = torch.autograd.grad(loss, list(params.values()))
+    for (name, _), grad in zip(params.items(), grads):
+        torch.testing.assert_close(grad, torch.tensor(GOLDEN[f"actor.grad.{name}"]), rtol=1e-4, atol=1e-6,
+                                   msg=name)
+    for name, value in buffers.items():
+        torch.testing.assert_close(value, torch.tensor(GOLDEN[f"actor.after.{name}"]), rtol=1e-6, atol=1e-7,
+                                   msg=name)
+    xe, ne = torch.tensor(GOLDEN["actor.eval.x"]), torch.tensor(GOLDEN["actor.eval.noise"])
+    with torch.no_grad():
+        a, lp, mean, std = O.actor_forward(params, buffers, xe, False, ne, d)
+    torch.testing.assert_close(a, torch.tensor(GOLDEN["actor.eval.actions"]), rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(lp, torch.tensor(GOLDEN["actor.eval.log_prob"]), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(mean, torch.tensor(GOLDEN["actor.eval.mean"]), rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(std, torch.tensor(GOLDEN["actor.eval.std"]), rtol=1e-6, atol=1e-7)
+
+
+def test_critic_forward_backward_matches_reference_modules():
+    d = _dims()
+    state = _group("critic.init.")
+    state.pop("predictor.bin_values")
+    params, buffers = _split(state, O.critic_parameter_shapes(d))
+    obs, act = torch.tensor(GOLDEN["critic.train.obs"]), torch.tensor(GOLDEN["critic.train.act"])
+    q, lp = O.critic_forward(params, buffers, obs, act, True, d)
+    torch.testing.assert_close(q, torch.tensor(GOLDEN["critic.train.q"]), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(lp, torch.tensor(GOLDEN["critic.train.log_prob"]), rtol=1e-5, atol=1e-6)
+    loss = (torch.tensor(GOLDEN["critic.train.cq"]) * q).sum() + (torch.tensor(GOLDEN["critic.train.clp"]) * lp).sum() * 0.05
+    grads = torch.autograd.grad(loss, list(params.values()))
+    for (name, _), grad in zip(params.items(), grads):
+        torch.testing.assert_close(grad, torch.tensor(GOLDEN[f"critic.grad.{name}"]), rtol=1e-4, atol=1e-5,
+                                   msg=name)
+    for name, value in buffers.items():
+        torch.testing.assert_close(value, torch.tensor(GOLDEN[f"critic.after.{name}"]), rtol=1e-6, atol=1e-7,
+                                   msg=name)
+    with torch.no_grad():
+        q2, lp2 = O.critic_forward(params, buffers, obs, act, False, d)
+    torch.testing.assert_close(q2, torch.tensor(GOLDEN["critic.eval.q"]), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(lp2, torch.tensor(GOLDEN["critic.eval.log_prob"]), rtol=1e-5, atol=1e-6)
+
+
+def test_projection_and_ema_match_reference_network():
+    before = _group("project.before.")
+    O.normalize_parameters(before)
+    for name, value in before.items():
+        torch.testing.assert_close(value, torch.tensor(GOLDEN[f"project.after.{name}"]), rtol=1e-6, atol=1e-7,
+                                   msg=name)
+    target = _group("ema.before.")
+    source = _group("project.after.")
+    O.ema_update(target, source, 0.005)
+    for name, value in target.items():
+        torch.testing.assert_close(value, torch.tensor(GOLDEN[f"ema.after.{name}"]), rtol=0, atol=0, msg=name)
+
+
+def test_projection_invariants():
+    g = torch.Generator().manual_seed(0)
+    params = OrderedDict(
+        (k, torch.randn(v, generator=g)) for k, v in O.critic_parameter_shapes(_dims()).items())
+    O.normalize_parameters(params)
+    w = params["encoder.0.w1.weight"]
+    torch.testing.assert_close(w.norm(dim=-1), torch.ones(w.shape[:-1]), rtol=1e-6, atol=1e-6)
+    bn_w, bn_b = params["encoder.0.norm1.weight"], params["encoder.0.norm1.bias"]
+    torch.testing.assert_close((bn_w ** 2 + bn_b ** 2).sum(-1), torch.full((2,), float(bn_w.shape[-1])), rtol=1e-5,
+                               atol=1e-5)
+    rms = params["post_norm.weight"]
+    torch.testing.assert_close((rms ** 2).sum(-1), torch.full((2,), float(rms.shape[-1])), rtol=1e-5, atol=1e-5)
+
+
+def test_schedule_matches_reference_and_closed_form():
+    steps = GOLDEN["schedule.steps"]
+    for label in ("a", "b"):
+        f = O.warmup_cosine(*GOLDEN[f"schedule.{label}.args"])
+        np.testing.assert_allclose([f(int(s)) for s in steps], GOLDEN[f"schedule.{label}.values"], rtol=0, atol=0)
+    f = O.warmup_cosine(1e-5, 3e-4, 1e-4, 10, 110)
+    assert f(5) == pytest.approx(1e-5 + (3e-4 - 1e-5) * 0.5)
+    assert f(60) == pytest.approx(1e-4 + (3e-4 - 1e-4) * 0.5)  # cosine midpoint
+    assert f(200) == 1e-4
+
+
+def test_log_det_and_temperature_match_reference():
+    x = torch.tensor(GOLDEN["logdet.x"])
+    torch.testing.assert_close(O.safe_tanh_log_det_jacobian(x), torch.tensor(GOLDEN["logdet.y"]), rtol=0, atol=0)
+    # closed form log(1 - tanh(x)^2) away from saturation
+    xs = torch.linspace(-3, 3, 13, dtype=torch.float64)
+    torch.testing.assert_close(O.safe_tanh_log_det_jacobian(xs), torch.log(1 - torch.tanh(xs) ** 2))
+    assert float(GOLDEN["temperature.value"][0]) == pytest.approx(math.exp(math.log(0.01)), rel=1e-7)
+
+
+# ---------------------------------------------------------------------------
+# categorical TD projection: closed forms
+# ---------------------------------------------------------------------------
+def _td(reward, done, entropy, gamma, lp, bins=11, min_v=-10.0, max_v=10.0):
+    return O.categorical_td_target(lp, reward, done, entropy, gamma, bins, min_v, max_v)
+
+
+def test_td_target_mass_and_grid_points():
+    g = torch.Generator().manual_seed(1)
+    rows, bins = 64, 11
+    lp = torch.log_softmax(torch.randn(rows, bins, generator=g, dtype=torch.float64), -1)
+    reward = torch.randn(rows, generator=g, dtype=torch.float64) * 5
+    done = (torch.rand(rows, generator=g) < 0.3).double()
+    entropy = torch.randn(rows, generator=g, dtype=torch.float64) * 0.1
+    t = _td(reward, done, entropy, torch.full((rows,), 0.99, dtype=torch.float64), lp)
+    torch.testing.assert_close(t.sum(-1), torch.ones(rows, dtype=torch.float64))
+    assert (t >= 0).all()
+    # terminal rows collapse all mass onto the reward (two-hot of one value)
+    expected_mean = torch.clamp(reward, -10, 10)
+    support = torch.linspace(-10, 10, bins, dtype=torch.float64)
+    term = done == 1
+    torch.testing.assert_close((t[term] * support).sum(-1), expected_mean[term])
+    # values exactly on the grid: reward on a bin center, gamma 0 -> one-hot
+    reward = torch.tensor([-10.0, -6.0, 0.0, 4.0, 10.0], dtype=torch.float64)
+    t = _td(reward, torch.zeros(5, dtype=torch.float64), torch.zeros(5, dtype=torch.float64),
+            torch.zeros(5, dtype=torch.float64), lp[:5])
+    for row, r in enumerate(reward):
+        k = int(round((float(r) + 10) / 2))
+        assert t[row, k] == pytest.approx(1.0)
+    # everything beyond max_v lands in the last bin
+    t = _td(torch.full((3,), 50.0, dtype=torch.float64), torch.zeros(3, dtype=torch.float64),
+            torch.zeros(3, dtype=torch.float64), torch.full((3,), 0.99, dtype=torch.float64), lp[:3])
+    torch.testing.assert_close(t[:, -1], torch.ones(3, dtype=torch.float64))
+
+
+def test_td_target_brute_force():
+    """Direct per-atom two-hot accumulation on tiny inputs."""
+    g = torch.Generator().manual_seed(2)
+    rows, bins = 7, 5
+    lp = torch.log_softmax(torch.randn(rows, bins, generator=g, dtype=torch.float64), -1)
+    reward = torch.randn(rows, generator=g, dtype=torch.float64) * 3
+    done = torch.tensor([0, 1, 0, 0, 1, 0, 0], dtype=torch.float64)
+    entropy = torch.randn(rows, generator=g, dtype=torch.float64) * 0.2
+    gamma = torch.full((rows,), 0.9, dtype=torch.float64)
+    t = _td(reward, done, entropy, gamma, lp, bins=bins, min_v=-4.0, max_v=4.0)
+    support = np.linspace(-4, 4, bins)
+    for i in range(rows):
+        expected = np.zeros(bins)
+        for j in range(bins):
+            v = reward[i].item() + gamma[i].item() * (support[j] - entropy[i].item()) * (1 - done[i].item())
+            v = min(max(v, -4.0), 4.0)
+            b = (v + 4.0) / 2.0
+            lo = int(math.floor(b))
+            hi = min(lo + 1, bins - 1)
+            p = math.exp(lp[i, j].item())
+            expected[lo] += p * (1 - (b - lo))
+            expected[hi] += p * (b - lo)
+        np.testing.assert_allclose(t[i].numpy(), expected, atol=1e-12)
+
+
+def test_select_min_q_prefers_first_critic_on_ties():
+    q = torch.tensor([[1.0, 2.0, 3.0], [1.0, 1.0, 4.0]])
+    lp = torch.stack([torch.zeros(3, 4), torch.ones(3, 4)])
+    out = O.select_min_q_log_probs(q, lp)
+    assert out[0].eq(0).all() and out[1].eq(1).all() and out[2].eq(0).all()
+
+
+# ---------------------------------------------------------------------------
+# composite update: finite differences on a tiny network (float64)
+# ---------------------------------------------------------------------------
+def _tiny_config():
+    cfg = FlashSACConfig(seed=0, normalize_reward=False, n_step=1, sample_batch_size=6, buffer_max_length=32,
+                         buffer_min_length=6, actor_hidden_dim=4, actor_num_blocks=1, critic_hidden_dim=4,
+                         critic_num_blocks=1, critic_num_bins=5, critic_min_v=-4.0, critic_max_v=4.0)
+    from dataclasses import replace
+
+    return replace(cfg, temp_target_entropy=O.target_entropy(2, cfg.temp_target_sigma))
+
+
+def test_actor_and_critic_loss_gradients_match_finite_differences():
+    cfg = _tiny_config()
+    d = O.dims_from_config(3, 2, cfg)
+    state = O.init_state(d, cfg, seed=4, dtype=torch.float64)
+    store = O.synthetic_replay(32, 3, 2, seed=1, gamma=0.99, done_prob=0.2)
+    batch = {k: v.double() for k, v in O.sample(store, torch.arange(6)).items()}
+    g = torch.Generator().manual_seed(3)
+    noise = torch.randn(12, 2, generator=g, dtype=torch.float64)
+
+    def actor_loss():
+        actions, log_probs, _, _ = O.actor_forward(state.actor, OrderedDict((k, v.clone()) for k, v in state.actor_buffers.items()),
+                                                   torch.cat([batch["observation"], batch["next_observation"]]), True,
+                                                   noise, d)
+        qs, _ = O.critic_forward(state.critic, state.critic_buffers, batch["observation"], actions[:6], False, d)
+        return (log_probs[:6] * 0.01 - torch.minimum(qs[0], qs[1])).mean()
+
+    for name in ("embedder.w.w.weight", "encoder.0.norm1.bias", "predictor.std_w.w.weight", "predictor.mean_bias"):
+        param = state.actor[name]
+        (grad,) = torch.autograd.grad(actor_loss(), [param])
+        flat = param.detach().view(-1)
+        for index in (0, flat.numel() // 2, flat.numel() - 1):
+            saved = flat[index].item()
+            with torch.no_grad():
+                flat[index] = saved + 1e-6
+                plus = actor_loss().item()
+                flat[index] = saved - 1e-6
+                minus = actor_loss().item()
+                flat[index] = saved
+            assert grad.view(-1)[index].item() == pytest.approx((plus - minus) / 2e-6, rel=1e-4, abs=1e-8), name
+
+
+# ---------------------------------------------------------------------------
+# PPO: reference known answers (tests/test_warp_ppo.py)
+# ---------------------------------------------------------------------------
+def test_ppo_gae_known_answer():
+    reward = np.array([[1, 2], [3, 4], [5, 6]], dtype=np.float32)
+    value = np.array([[0.1, 0.2], [0.3, 0.4], [0.5, 0.6]], dtype=np.float32)
+    next_value = np.array([[0.3, 0.4], [9, 10], [11, 12]], dtype=np.float32)
+    terminated = np.array([[0, 0], [1, 0], [0, 0]], dtype=np.int32)
+    truncated = np.array([[0, 0], [0, 1], [0, 0]], dtype=np.int32)
+    adv, ret = OP.gae(reward.flatten(), value.flatten(), next_value.flatten(), terminated.flatten(),
+                      truncated.flatten(), 3, 2, 0.99, 0.95)
+    expected = np.zeros_like(reward)
+    tail = np.zeros(2, dtype=np.float32)
+    for t in range(2, -1, -1):
+        delta = reward[t] + 0.99 * (1 - terminated[t]) * next_value[t] - value[t]
+        tail = delta + 0.99 * 0.95 * (1 - np.maximum(terminated[t], truncated[t])) * tail
+        expected[t] = tail
+    np.testing.assert_allclose(adv.numpy().reshape(3, 2), expected, rtol=1e-6)
+    np.testing.assert_allclose(ret.numpy().reshape(3, 2), expected + value, rtol=1e-6)
+
+
+def test_ppo_timeout_current_bootstrap_uses_own_value():
+    adv, _ = OP.gae([1.0], [0.5], [9.0], [0], [1], 1, 1, 0.9, 0.95, "current")
+    assert adv[0].item() == pytest.approx(1.0 + 0.9 * 0.5 - 0.5)
+
+
+def test_ppo_advantage_normalization_at_large_offset():
+    adv, ret = OP.gae(np.array([10000.0, 10001.0]), np.zeros(2), np.zeros(2), np.zeros(2), np.zeros(2), 1, 2,
+                      0.0, 0.95)
+    np.testing.assert_allclose(OP.normalize(adv.float(), False).numpy(), [-1.0, 1.0], rtol=1e-6)
+
+
+def test_ppo_loss_and_gradients_match_reference_known_answer():
+    mean = torch.tensor([[0.4, 0.1], [-0.3, 0.2], [0.2, -0.2]], dtype=torch.float64, requires_grad=True)
+    action = torch.tensor([[0.0, 0.5], [0.6, 0.1], [-0.5, 0.4]], dtype=torch.float64)
+    old_lp = torch.tensor([-2.4, -1.8, -2.0], dtype=torch.float64)
+    advantage = torch.tensor([1.0, -0.8, 0.4], dtype=torch.float64)
+    value = torch.tensor([[0.8], [1.0], [-0.5]], dtype=torch.float64, requires_grad=True)
+    old_value = torch.tensor([0.2, 1.3, -0.4], dtype=torch.float64)
+    returns = torch.tensor([0.7, -0.2, 1.0], dtype=torch.float64)
+    log_std = torch.tensor([-0.2, 0.1], dtype=torch.float64, requires_grad=True)
+    cfg = PPOConfig(clip_ratio=0.2, value_coefficient=0.5, entropy_coefficient=0.01, value_loss_scale=0.5)
+    loss, *_ = OP.loss_terms(mean, value, log_std, action, old_lp, old_value, advantage, returns, cfg)
+
+    def reference(m=mean.detach().numpy(), v=value.detach().numpy(), s=log_std.detach().numpy()):
+        a = action.numpy()
+        lp = (-0.5 * (((a - m) * np.exp(-s)) ** 2 + 2 * s + np.log(2 * np.pi))).sum(1)
+        ratio = np.exp(lp - old_lp.numpy())
+        policy = -np.minimum(ratio * advantage.numpy(), np.clip(ratio, 0.8, 1.2) * advantage.numpy()).mean()
+        clipped = old_value.numpy() + np.clip(v[:, 0] - old_value.numpy(), -0.2, 0.2)
+        vl = 0.5 * np.maximum((v[:, 0] - returns.numpy()) ** 2, (clipped - returns.numpy()) ** 2).mean()
+        return policy + 0.5 * vl - 0.01 * (s + 0.5 * np.log(2 * np.pi * np.e)).sum()
+
+    assert loss.item() == pytest.approx(reference(), rel=1e-10)
+    grads = torch.autograd.grad(loss, [mean, value, log_std])
+    for key, data, grad in (("m", mean, grads[0]), ("v", value, grads[1]), ("s", log_std, grads[2])):
+        base = data.detach().numpy()
+        numerical = np.zeros_like(base)
+        for index in np.ndindex(base.shape):
+            plus, minus = base.copy(), base.copy()
+            plus[index] += 1e-6
+            minus[index] -= 1e-6
+            numerical[index] = (reference(**{key: plus}) - reference(**{key: minus})) / 2e-6
+        np.testing.assert_allclose(grad.numpy(), numerical, atol=1e-7, rtol=1e-6)
+
+
+def test_gaussian_kl_closed_form():
+    old_mean, new_mean = torch.tensor([[0.3]]), torch.tensor([[-0.1]])
+    old_std, new_std = torch.tensor([[0.7]]), torch.tensor([[1.2]])
+    kl = OP.gaussian_kl(old_mean, old_std, new_mean, new_std)
+    expected = torch.distributions.kl_divergence(torch.distributions.Normal(old_mean, old_std),
+                                                 torch.distributions.Normal(new_mean, new_std)).sum(-1)
+    torch.testing.assert_close(kl, expected)
