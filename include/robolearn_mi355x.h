@@ -47,13 +47,14 @@ int rl_plan_destroy(void* plan);
  * (mode 0: fp32 v_mfma_f32_32x32x2_f32, mode 1: bf16 v_mfma_f32_32x32x16_bf16).
  * A(m,k) = a_kcontig ? A[m*lda+k] : A[k*lda+m]; B(k,n) = b_kcontig ? B[n*ldb+k]
  * : B[k*ldb+n].  epilogue 0 none, 1 ReLU, 2 ELU.  splits > 1 reduces over K in
- * fixed order through workspace.  Serves the three plans of one Linear,
+ * fixed order through workspace; d_bf16 (optional) receives a bf16 copy of D.  Serves the three plans of one Linear,
  * robolearn/cuda/linear.py:179-185, 341-360, and the ensemble einsum of
  * robolearn/flashsac/layers.py:174-186. */
 int rl_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int m, int n, int k, int batch,
             const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
             const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
-            float beta, int epilogue, int splits, float* workspace, size_t workspace_bytes, void* stream);
+            float beta, int epilogue, int splits, float* workspace, size_t workspace_bytes, void* d_bf16,
+            void* stream);
 size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, int splits);
 
 /* ---- optimizer ---------------------------------------------------------- */

@@ -101,14 +101,18 @@ inline unsigned ceil_div(long long a, long long b) { return static_cast<unsigned
 
 constexpr int kWave = 64;
 
-// Round-to-nearest-even fp32 -> bf16, written from the IEEE-754 definition:
-// add 0x7FFF plus the lowest kept mantissa bit, then truncate.  NaN keeps a
-// quiet payload.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 with round-to-nearest-even; on gfx950 this is the hardware
+// conversion (v_cvt_pk_bf16_f32), two values per instruction.
 __device__ __forceinline__ unsigned short f32_to_bf16_bits(float value) {
-    unsigned int bits = __float_as_uint(value);
-    if ((bits & 0x7F800000u) == 0x7F800000u && (bits & 0x007FFFFFu)) return static_cast<unsigned short>((bits >> 16) | 0x40u);
-    bits += 0x7FFFu + ((bits >> 16) & 1u);
-    return static_cast<unsigned short>(bits >> 16);
+    return __builtin_bit_cast(unsigned short, static_cast<__bf16>(value));
+}
+
+// Packs (lo, hi) as two bf16 in one 32-bit word, lo in the low half.
+__device__ __forceinline__ unsigned int f32x2_to_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(unsigned int, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(unsigned short bits) {

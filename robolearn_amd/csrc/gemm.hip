@@ -14,39 +14,13 @@
 // staged through LDS in [row][k] order so each lane reads its K-slice with one
 // or two 16-byte LDS loads; the K order inside a tile is permuted identically
 // for both operands, which leaves the dot products unchanged.
-#include "common.hpp"
+#include "gemm.hpp"
 
 #include <cmath>
 #include <string>
 
 namespace rl {
 namespace gemm {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
-
-constexpr int kThreads = 256;
-constexpr int kTile = 128;
-
-enum Epilogue : int { kNone = 0, kRelu = 1, kElu = 2 };
-
-struct Params {
-    const void* a;
-    const void* b;
-    float* d;            // output (or split-K workspace)
-    const float* c;      // beta operand (same layout as d), may alias d
-    const float* bias;   // length n, may be null
-    long long lda, ldb, ldd;
-    long long stride_a, stride_b, stride_d, stride_bias;
-    int m, n, k;
-    int batch;           // ensemble count
-    int splits;          // K splits; >1 writes partial tiles into d = workspace
-    int k_per_split;     // multiple of the K tile
-    float beta;          // D = act(AB + bias) + beta * C (direct mode only)
-    int epilogue;        // Epilogue (direct mode only)
-    int a_vec, b_vec;    // 16-byte vector loads allowed
-};
 
 template <typename T> struct Src;
 template <> struct Src<float> {
@@ -140,12 +114,6 @@ struct TileLoader {
         }
     }
 };
-
-__device__ __forceinline__ float apply_epilogue(float v, int epilogue) {
-    if (epilogue == kRelu) return v > 0.0f ? v : 0.0f;
-    if (epilogue == kElu) return v > 0.0f ? v : expm1f(v);
-    return v;
-}
 
 template <int Mode, typename SA, typename SB, bool AK, bool BK>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
@@ -279,6 +247,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
                     float value = apply_epilogue(acc[i][j][v] + bcol, p.epilogue);
                     if (p.beta != 0.0f) value += p.beta * C[offset];
                     *out = value;
+                    if (p.d_bf16) p.d_bf16[batch * p.stride_d + offset] = f32_to_bf16_bits(value);
                 } else {
                     *out = acc[i][j][v];
                 }
@@ -288,9 +257,9 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
 }
 
 // Fixed-order split-K reduction: D = act(sum_s W[s] + bias) + beta * C.
-__global__ void splitk_reduce(const float* work, float* d, const float* c, const float* bias, long long ldd,
-                              long long stride_d, long long stride_bias, int m, int n, int batch, int splits,
-                              float beta, int epilogue) {
+__global__ void splitk_reduce(const float* work, float* d, unsigned short* d_bf16, const float* c, const float* bias,
+                              long long ldd, long long stride_d, long long stride_bias, int m, int n, int batch,
+                              int splits, float beta, int epilogue) {
     const long long total = static_cast<long long>(batch) * m * n;
     for (long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; idx < total;
          idx += static_cast<long long>(gridDim.x) * blockDim.x) {
@@ -304,6 +273,7 @@ __global__ void splitk_reduce(const float* work, float* d, const float* c, const
         const long long offset = b * stride_d + static_cast<long long>(row) * ldd + col;
         if (beta != 0.0f) value += beta * c[offset];
         d[offset] = value;
+        if (d_bf16) d_bf16[offset] = f32_to_bf16_bits(value);
     }
 }
 
@@ -338,7 +308,8 @@ void launch_mode(const Params& p, int a_bf16, int b_bf16, bool ak, bool bk, hipS
 int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int m, int n, int k, int batch,
              const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
              const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
-             float beta, int epilogue, int splits, float* workspace, std::size_t workspace_bytes, hipStream_t stream) {
+             float beta, int epilogue, int splits, float* workspace, std::size_t workspace_bytes, hipStream_t stream,
+             unsigned short* d_bf16) {
     require(mode == 0 || mode == 1, "GEMM mode must be 0 (fp32) or 1 (bf16 operands).");
     require(!(mode == 0 && (a_bf16 || b_bf16)), "fp32 GEMM mode requires fp32 operands.");
     require(m > 0 && n > 0 && k > 0 && batch > 0, "GEMM dimensions must be positive.");
@@ -365,10 +336,11 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     p.c = c;
     p.beta = beta;
     p.epilogue = epilogue;
+    p.d_bf16 = d_bf16;
     const int kt = mode == 1 ? 32 : 16;
     const int ktiles = (k + kt - 1) / kt;
     if (splits > ktiles) splits = ktiles;
-    const int tiles_per_split = (ktiles + splits - 1) / splits;
+    const int tiles_per_split = (ktiles + splits - 1) / splits;  // split boundaries are multiples of 32 in both modes
     splits = (ktiles + tiles_per_split - 1) / tiles_per_split;
     p.splits = splits;
     p.k_per_split = tiles_per_split * kt;
@@ -384,16 +356,17 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
         p.c = nullptr;
         p.beta = 0.0f;
         p.epilogue = 0;
+        p.d_bf16 = nullptr;
     } else {
         p.d = d;
     }
     if (mode == 0) gemm::launch_mode<0>(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
-    else gemm::launch_mode<1>(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
+    else gemm::launch_bf16(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
     check_launch("Launch GEMM");
     if (splits > 1) {
         const long long total = static_cast<long long>(batch) * m * n;
         const unsigned blocks = static_cast<unsigned>(std::min<long long>((total + 255) / 256, 4096));
-        hipLaunchKernelGGL(gemm::splitk_reduce, dim3(blocks), dim3(256), 0, stream, workspace, d, c, bias, ldd,
+        hipLaunchKernelGGL(gemm::splitk_reduce, dim3(blocks), dim3(256), 0, stream, workspace, d, d_bf16, c, bias, ldd,
                            stride_d, stride_bias, m, n, batch, splits, beta, epilogue);
         check_launch("Launch split-K reduction");
     }
@@ -406,11 +379,11 @@ RL_API int rl_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kconti
                    const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
                    const float* c, float* d, long long ldd, long long stride_d, const float* bias,
                    long long stride_bias, float beta, int epilogue, int splits, float* workspace,
-                   std::size_t workspace_bytes, void* stream) noexcept {
+                   std::size_t workspace_bytes, void* d_bf16, void* stream) noexcept {
     return rl::guarded("rl_gemm", [&] {
         rl::run_gemm(mode, a_bf16, b_bf16, a_kcontig, b_kcontig, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
                      d, ldd, stride_d, bias, stride_bias, beta, epilogue, splits, workspace, workspace_bytes,
-                     rl::as_stream(stream));
+                     rl::as_stream(stream), static_cast<unsigned short*>(d_bf16));
     });
 }
 

@@ -39,14 +39,14 @@ def _is_bf16(tensor: torch.Tensor) -> int:
 
 def gemm(
     a, b, d, *, m, n, k, batch=1, a_kcontig, b_kcontig, lda, ldb, ldd, stride_a=0, stride_b=0, stride_d=0,
-    c=None, beta=0.0, bias=None, stride_bias=0, epilogue=None, mode=FP32, splits=1, workspace=None,
+    c=None, beta=0.0, bias=None, stride_bias=0, epilogue=None, mode=FP32, splits=1, workspace=None, d_bf16=None,
 ):
-    """Row-major batched D = act(op(A) op(B) + bias) + beta * C."""
+    """Row-major batched D = act(op(A) op(B) + bias) + beta * C (optional bf16 copy of D)."""
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _native.call(
         "rl_gemm", mode, _is_bf16(a), _is_bf16(b), int(a_kcontig), int(b_kcontig), m, n, k, batch, ptr(a), lda,
         stride_a, ptr(b), ldb, stride_b, ptr(c), ptr(d), ldd, stride_d, ptr(bias), stride_bias, float(beta),
-        EPILOGUES[epilogue], splits, ptr(workspace), ws_bytes, stream(),
+        EPILOGUES[epilogue], splits, ptr(workspace), ws_bytes, ptr(d_bf16), stream(),
     )
 
 
