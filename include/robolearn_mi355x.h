@@ -100,7 +100,8 @@ int rl_flash_ema_destroy(void* plan);
 
 /* ---- normalization ------------------------------------------------------ */
 /* Ensemble BatchNorm; x_stride 0 broadcasts one input to every member; optional
- * residual is added after the ReLU (fuses robolearn/flashsac/layers.py:105-113).
+ * residual is added after the ReLU (fuses robolearn/flashsac/layers.py:105-113);
+ * y or y_bf16 may be NULL (at least one output).
  * Replaces robolearn/cuda/flash_kernels.cuh:500-543 for the stacked critics of
  * robolearn/flashsac/layers.py:189-222.  partial: ensemble*2*ceil(rows/256)*channels. */
 int rl_bn_forward_ex(int ensemble, const float* x, long long x_stride, const float* w, const float* b,
@@ -115,11 +116,13 @@ int rl_bn_backward_ex(int ensemble, const float* x, long long x_stride, const fl
                       float eps, int training, int relu, int accumulate_dx, int accumulate_params, void* stream);
 /* RMSNorm over rows [0, rows) of each member (member_stride elements apart);
  * replaces flash_kernels.cuh:611-634, covers layers.py:67-74 and :225-240. */
-int rl_rms_forward_ex(int ensemble, const float* x, const float* w, float* ms, float* y, int rows, int channels,
-                      long long member_stride, float eps, void* stream);
+int rl_rms_forward_ex(int ensemble, const float* x, const float* w, float* ms, float* y, void* y_bf16, int rows,
+                      int channels, long long member_stride, float eps, void* stream);
 int rl_rms_backward_ex(int ensemble, const float* x, const float* dy, const float* w, const float* ms,
-                       float* partial, float* dx, float* dw, int rows, int channels, long long member_stride,
-                       float eps, int accumulate_dx, int accumulate_dw, void* stream);
+                       float* partial, float* dx, void* dx_bf16, float* dw, int rows, int channels,
+                       long long member_stride, float eps, int accumulate_dx, int accumulate_dw, void* stream);
+/* fp32 -> bf16 RNE copy (weight shadows); counterpart of robolearn/cuda/kernels.cu:663-687. */
+int rl_cast_f32_bf16(const float* source, void* destination, long long count, void* stream);
 /* Deterministic column sums; replaces robolearn/cuda/kernels.cu:237-251, 742-758. */
 int rl_bias_grad_ex(int ensemble, const float* dy, float* db, float* partial, int rows, int channels, int accumulate,
                     void* stream);
@@ -155,8 +158,8 @@ int rl_categorical_head_forward(const float* logits, const float* bias, long lon
                                 void* stream);
 /* dlogits = dQ p (z - Q): the value path of robolearn/cuda/categorical_kernels.cuh:56-75. */
 int rl_categorical_head_backward_q(const float* logits, const float* bias, long long bias_stride,
-                                   const float* support, const float* dvalues, float* dlogits, long long rows,
-                                   int bins, int ensemble, void* stream);
+                                   const float* support, const float* dvalues, float* dlogits, void* dlogits_bf16,
+                                   long long rows, int bins, int ensemble, void* stream);
 /* Fused min-Q selection + two-hot TD projection + cross-entropy + its logit
  * gradient for both online critics: robolearn/flashsac/updates.py:19-80, 248-257
  * (replaces rl_flash_categorical_target + the CE kernel, robolearn/warp/flashsac.py:223-233). */
@@ -165,8 +168,8 @@ int rl_categorical_td_cross_entropy(const float* target_logits, const float* tar
                                     const float* support, const float* reward, const float* terminated,
                                     const float* discount, const float* next_log_probs, const float* alpha,
                                     float min_v, float max_v, long long batch, int bins, float scale,
-                                    float* target_out, float* dlogits, float* loss_rows, float* entropy_rows,
-                                    float* q_next, void* stream);
+                                    float* target_out, float* dlogits, void* dlogits_bf16, float* loss_rows,
+                                    float* entropy_rows, float* q_next, void* stream);
 /* robolearn/cuda/categorical_kernels.cuh:126-176 (bins <= 512). */
 int rl_flash_categorical_forward(const void* raw, const void* bias, const void* support, void* log_probs,
                                  void* values, int batch, int bins, void* stream);
@@ -201,8 +204,8 @@ int rl_concat_columns(float* out, long long ld_out, long long rows, const float*
 int rl_tanh_gaussian_forward(const float* head, const float* noise, float* actions, long long ld_actions,
                              float* log_probs, long long rows, int action_dim, int deterministic, void* stream);
 int rl_tanh_gaussian_backward(const float* head, const float* noise, const float* dactions, long long ld_dactions,
-                              long long grad_rows, const float* dlog_probs, float* dhead, long long rows,
-                              int action_dim, void* stream);
+                              long long grad_rows, const float* dlog_probs, float* dhead, void* dhead_bf16,
+                              long long rows, int action_dim, void* stream);
 /* Actor loss, entropy, mean action and their gradients (robolearn/flashsac/updates.py:105-137,
  * robolearn/warp/flashsac.py:109-153). */
 int rl_actor_objective(const float* q0, const float* q1, const float* log_probs, const float* actions,

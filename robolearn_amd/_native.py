@@ -63,8 +63,9 @@ SIGNATURES = {
                                  c_int, c_int, P]),
     "rl_bn_backward_ex": (c_int, [c_int, P, c_ll, P, P, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_float, c_int,
                                   c_int, c_int, c_int, P]),
-    "rl_rms_forward_ex": (c_int, [c_int, P, P, P, P, c_int, c_int, c_ll, c_float, P]),
-    "rl_rms_backward_ex": (c_int, [c_int, P, P, P, P, P, P, P, c_int, c_int, c_ll, c_float, c_int, c_int, P]),
+    "rl_rms_forward_ex": (c_int, [c_int, P, P, P, P, P, c_int, c_int, c_ll, c_float, P]),
+    "rl_rms_backward_ex": (c_int, [c_int, P, P, P, P, P, P, P, P, c_int, c_int, c_ll, c_float, c_int, c_int, P]),
+    "rl_cast_f32_bf16": (c_int, [P, P, c_ll, P]),
     "rl_bias_grad_ex": (c_int, [c_int, P, P, P, c_int, c_int, c_int, P]),
     "rl_flash_bn_forward": (c_int, [P] * 9 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),
     "rl_flash_bn_forward_with_bf16": (c_int, [P] * 10 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),
@@ -76,9 +77,9 @@ SIGNATURES = {
     # categorical
     "rl_reduce": (c_int, [P, c_ll, c_float, c_int, P, P]),
     "rl_categorical_head_forward": (c_int, [P, P, c_ll, P, P, P, c_ll, c_int, c_int, P]),
-    "rl_categorical_head_backward_q": (c_int, [P, P, c_ll, P, P, P, c_ll, c_int, c_int, P]),
+    "rl_categorical_head_backward_q": (c_int, [P, P, c_ll, P, P, P, P, c_ll, c_int, c_int, P]),
     "rl_categorical_td_cross_entropy": (c_int, [P, P, c_ll, P, P, c_ll, P, P, P, P, P, P, c_float, c_float, c_ll, c_int,
-                                                c_float, P, P, P, P, P, P]),
+                                                c_float, P, P, P, P, P, P, P]),
     "rl_flash_categorical_forward": (c_int, [P, P, P, P, P, c_int, c_int, P]),
     "rl_flash_categorical_backward": (c_int, [P, P, P, P, P, P, P, c_int, c_int, P]),
     "rl_flash_categorical_target": (c_int, [P] * 9 + [c_int, c_int, c_float, c_float, P]),
@@ -88,7 +89,7 @@ SIGNATURES = {
     "rl_replay_gather": (c_int, [P, c_ll, c_ll, c_int, c_int] + [P] * 15 + [P]),
     "rl_concat_columns": (c_int, [P, c_ll, c_ll, P, c_ll, c_int, P, c_ll, c_int, P]),
     "rl_tanh_gaussian_forward": (c_int, [P, P, P, c_ll, P, c_ll, c_int, c_int, P]),
-    "rl_tanh_gaussian_backward": (c_int, [P, P, P, c_ll, c_ll, P, P, c_ll, c_int, P]),
+    "rl_tanh_gaussian_backward": (c_int, [P, P, P, c_ll, c_ll, P, P, P, c_ll, c_int, P]),
     "rl_actor_objective": (c_int, [P, P, P, P, c_ll, P, P, c_float, c_ll, c_ll, c_int, P, P, P, P, P, P]),
     "rl_temperature_objective": (c_int, [P, P, c_float, P, P, P]),
     "rl_exp_scalar": (c_int, [P, P, P]),

@@ -110,8 +110,9 @@ __global__ __launch_bounds__(kThreads) void head_backward(const float* log_probs
 // Q-gradient through a head given raw logits (actor phase): dlogits = dq p (z - Q).
 __global__ __launch_bounds__(kThreads) void head_backward_q(const float* logits, const float* bias,
                                                             long long bias_stride, const float* support,
-                                                            const float* dvalues, float* dlogits, long long rows,
-                                                            int bins, int ensemble) {
+                                                            const float* dvalues, float* dlogits,
+                                                            unsigned short* dlogits_bf16, long long rows, int bins,
+                                                            int ensemble) {
     const long long row = blockIdx.x * static_cast<long long>(kWaves) + threadIdx.x / kWave;
     if (row >= rows * ensemble) return;
     const int e = static_cast<int>(row / rows);
@@ -123,7 +124,11 @@ __global__ __launch_bounds__(kThreads) void head_backward_q(const float* logits,
 #pragma unroll
     for (int i = 0; i < kPerLane; ++i) {
         const int j = lane + i * kWave;
-        if (j < bins) dlogits[row * bins + j] = dq * expf(lp[i]) * (support[j] - q);
+        if (j < bins) {
+            const float g = dq * expf(lp[i]) * (support[j] - q);
+            if (dlogits) dlogits[row * bins + j] = g;
+            if (dlogits_bf16) dlogits_bf16[row * bins + j] = f32_to_bf16_bits(g);
+        }
     }
 }
 
@@ -200,7 +205,8 @@ __global__ __launch_bounds__(kThreads) void td_cross_entropy(TargetArgs a, const
                                                              const float* target_bias, long long target_rows,
                                                              const float* online_logits, const float* online_bias,
                                                              long long online_rows, long long batch, float scale,
-                                                             float* target_out, float* dlogits, float* loss_rows,
+                                                             float* target_out, float* dlogits,
+                                                             unsigned short* dlogits_bf16, float* loss_rows,
                                                              float* entropy_rows, float* q_next) {
     __shared__ float lds[kWaves][4 * kMaxBins];
     const int wave = threadIdx.x / kWave;
@@ -243,7 +249,9 @@ __global__ __launch_bounds__(kThreads) void td_cross_entropy(TargetArgs a, const
             const int j = lane + i * kWave;
             if (j < bins) {
                 ce -= t[i] * lp[i];
-                dlogits[orow * bins + j] = scale * (expf(lp[i]) * tsum - t[i]);
+                const float g = scale * (expf(lp[i]) * tsum - t[i]);
+                if (dlogits) dlogits[orow * bins + j] = g;
+                if (dlogits_bf16) dlogits_bf16[orow * bins + j] = f32_to_bf16_bits(g);
             }
         }
         ce = wave_sum(ce);
@@ -345,14 +353,16 @@ RL_API int rl_categorical_head_forward(const float* logits, const float* bias, l
 }
 
 RL_API int rl_categorical_head_backward_q(const float* logits, const float* bias, long long bias_stride,
-                                          const float* support, const float* dvalues, float* dlogits, long long rows,
-                                          int bins, int ensemble, void* stream) noexcept {
+                                          const float* support, const float* dvalues, float* dlogits,
+                                          void* dlogits_bf16, long long rows, int bins, int ensemble,
+                                          void* stream) noexcept {
     return rl::guarded("rl_categorical_head_backward_q", [&] {
-        rl::require(logits && support && dvalues && dlogits && rows > 0 && bins >= 2 && bins <= kMaxBins,
-                    "Categorical Q backward needs logits, support, dvalues, dlogits and 2..512 bins.");
+        rl::require(logits && support && dvalues && (dlogits || dlogits_bf16) && rows > 0 && bins >= 2 &&
+                        bins <= kMaxBins,
+                    "Categorical Q backward needs logits, support, dvalues, an output and 2..512 bins.");
         hipLaunchKernelGGL(rl::cat::head_backward_q, dim3(rl::ceil_div(rows * ensemble, rl::cat::kWaves)),
                            dim3(rl::cat::kThreads), 0, rl::as_stream(stream), logits, bias, bias_stride, support,
-                           dvalues, dlogits, rows, bins, ensemble);
+                           dvalues, dlogits, static_cast<unsigned short*>(dlogits_bf16), rows, bins, ensemble);
         rl::check_launch("Launch categorical Q backward");
     });
 }
@@ -363,11 +373,11 @@ RL_API int rl_categorical_td_cross_entropy(const float* target_logits, const flo
                                            const float* reward, const float* terminated, const float* discount,
                                            const float* next_log_probs, const float* alpha, float min_v, float max_v,
                                            long long batch, int bins, float scale, float* target_out, float* dlogits,
-                                           float* loss_rows, float* entropy_rows, float* q_next,
+                                           void* dlogits_bf16, float* loss_rows, float* entropy_rows, float* q_next,
                                            void* stream) noexcept {
     return rl::guarded("rl_categorical_td_cross_entropy", [&] {
         rl::require(target_logits && online_logits && support && reward && terminated && discount && next_log_probs &&
-                        alpha && dlogits && loss_rows && entropy_rows,
+                        alpha && (dlogits || dlogits_bf16) && loss_rows && entropy_rows,
                     "TD cross-entropy needs every input and output buffer.");
         rl::require(batch > 0 && bins >= 2 && bins <= kMaxBins && min_v < max_v, "TD cross-entropy needs 2..512 bins.");
         rl::require(target_rows >= batch && online_rows >= batch, "Member row strides must cover the batch.");
@@ -376,7 +386,7 @@ RL_API int rl_categorical_td_cross_entropy(const float* target_logits, const flo
         hipLaunchKernelGGL(rl::cat::td_cross_entropy, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
                            dim3(rl::cat::kThreads), 0, rl::as_stream(stream), a, target_logits, target_bias,
                            target_rows, online_logits, online_bias, online_rows, batch, scale, target_out, dlogits,
-                           loss_rows, entropy_rows, q_next);
+                           static_cast<unsigned short*>(dlogits_bf16), loss_rows, entropy_rows, q_next);
         rl::check_launch("Launch TD cross-entropy");
     });
 }

@@ -127,7 +127,7 @@ __global__ void bn_apply(const float* x, long long x_stride, const float* mean, 
         float v = bn_value(x[e * x_stride + within], mean[pc], inv, w[pc], b[pc]);
         if (relu) v = v > 0.0f ? v : 0.0f;
         if (residual) v += residual[idx];
-        y[idx] = v;
+        if (y) y[idx] = v;
         if (y_bf16) y_bf16[idx] = f32_to_bf16_bits(v);
     }
 }
@@ -227,15 +227,15 @@ __global__ void bn_grad_apply(const float* x, long long x_stride, const float* d
             value = w[pc] * inv * g;
         }
         if (accumulate) value += dx[idx];
-        dx[idx] = value;
+        if (dx) dx[idx] = value;
         if (dx_bf16) dx_bf16[idx] = f32_to_bf16_bits(value);
     }
 }
 
 // One wave per row: rs = rsqrt(mean(x^2) + eps); y = x * rs * w.  Stores
 // mean(x^2) per row in ms (the reference's "var").
-__global__ void rms_forward(const float* x, const float* w, float* ms, float* y, long long rows, int channels,
-                            int ensemble, long long member_stride, float eps) {
+__global__ void rms_forward(const float* x, const float* w, float* ms, float* y, unsigned short* y_bf16, long long rows,
+                            int channels, int ensemble, long long member_stride, float eps) {
     const long long row = blockIdx.x * static_cast<long long>(blockDim.x / kWave) + threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
     if (row >= rows * ensemble) return;
@@ -248,13 +248,17 @@ __global__ void rms_forward(const float* x, const float* w, float* ms, float* y,
     const float rs = 1.0f / sqrtf(s + eps);
     if (lane == 0) ms[row] = s;
     const float* we = w + e * channels;
-    float* yr = y + base;
-    for (int c = lane; c < channels; c += kWave) yr[c] = xr[c] * rs * we[c];
+    for (int c = lane; c < channels; c += kWave) {
+        const float v = xr[c] * rs * we[c];
+        if (y) y[base + c] = v;
+        if (y_bf16) y_bf16[base + c] = f32_to_bf16_bits(v);
+    }
 }
 
 // dx (+)= rs * (dy * w - x * rs^2 * mean(dy * w * x)).
-__global__ void rms_dx(const float* x, const float* dy, const float* w, const float* ms, float* dx, long long rows,
-                       int channels, int ensemble, long long member_stride, float eps, int accumulate) {
+__global__ void rms_dx(const float* x, const float* dy, const float* w, const float* ms, float* dx,
+                       unsigned short* dx_bf16, long long rows, int channels, int ensemble, long long member_stride,
+                       float eps, int accumulate) {
     const long long row = blockIdx.x * static_cast<long long>(blockDim.x / kWave) + threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
     if (row >= rows * ensemble) return;
@@ -267,11 +271,11 @@ __global__ void rms_dx(const float* x, const float* dy, const float* w, const fl
     for (int c = lane; c < channels; c += kWave) s += gr[c] * we[c] * xr[c];
     s = wave_sum(s) / static_cast<float>(channels);
     const float rs = 1.0f / sqrtf(ms[row] + eps);
-    float* out = dx + base;
     for (int c = lane; c < channels; c += kWave) {
         float v = rs * (gr[c] * we[c] - xr[c] * rs * rs * s);
-        if (accumulate) v += out[c];
-        out[c] = v;
+        if (accumulate) v += dx[base + c];
+        if (dx) dx[base + c] = v;
+        if (dx_bf16) dx_bf16[base + c] = f32_to_bf16_bits(v);
     }
 }
 
@@ -330,7 +334,7 @@ void bn_forward(int ensemble, const float* x, long long x_stride, const float* w
     require(ensemble > 0 && rows > 0 && channels > 0, "BatchNorm dimensions must be positive.");
     require(static_cast<long long>(rows) * channels <= std::numeric_limits<int>::max(), "BatchNorm exceeds 2^31 elements.");
     require(std::isfinite(eps) && eps >= 0.0f && std::isfinite(momentum), "BatchNorm eps/momentum are invalid.");
-    require(x && w && b && y, "BatchNorm requires x, weight, bias and y.");
+    require(x && w && b && (y || y_bf16), "BatchNorm requires x, weight, bias and an output.");
     const float* use_mean = running_mean;
     const float* use_var = running_var;
     if (training) {
@@ -364,7 +368,7 @@ void bn_backward(int ensemble, const float* x, long long x_stride, const float* 
     require(ensemble > 0 && rows > 0 && channels > 0, "BatchNorm dimensions must be positive.");
     require(x && dy && w && mean && var, "BatchNorm backward requires x, dy, weight and statistics.");
     require(!relu || y || b, "ReLU BatchNorm backward requires the output or the bias to recompute it.");
-    require(!dx_bf16 || dx, "bf16 BN input adjoint requires an fp32 input adjoint.");
+    require(!accumulate_dx || dx, "Accumulating BN input adjoints requires the fp32 adjoint.");
     const bool need_sums = training || dw || db;
     if (need_sums) {
         require(partial && sums, "BatchNorm backward requires partial and sums scratch.");
@@ -377,7 +381,7 @@ void bn_backward(int ensemble, const float* x, long long x_stride, const float* 
                            partial, sums, dw, db, rows, channels, chunks, ensemble, accumulate_params);
         check_launch("Launch BN gradient reduce");
     }
-    if (dx) {
+    if (dx || dx_bf16) {
         const long long total = static_cast<long long>(ensemble) * rows * channels;
         hipLaunchKernelGGL(norm::bn_grad_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream, x,
                            x_stride, dy, y, w, b, mean, var, sums, dx, dx_bf16, static_cast<long long>(rows), channels,
@@ -386,20 +390,20 @@ void bn_backward(int ensemble, const float* x, long long x_stride, const float* 
     }
 }
 
-void rms_forward(int ensemble, const float* x, const float* w, float* ms, float* y, int rows, int channels,
-                 long long member_stride, float eps, hipStream_t stream) {
+void rms_forward(int ensemble, const float* x, const float* w, float* ms, float* y, unsigned short* y_bf16, int rows,
+                 int channels, long long member_stride, float eps, hipStream_t stream) {
     require(ensemble > 0 && rows > 0 && channels > 0, "RMSNorm dimensions must be positive.");
-    require(x && w && ms && y, "RMSNorm forward requires x, weight, ms and y.");
+    require(x && w && ms && (y || y_bf16), "RMSNorm forward requires x, weight, ms and an output.");
     const long long total_rows = static_cast<long long>(rows) * ensemble;
     if (member_stride <= 0) member_stride = static_cast<long long>(rows) * channels;
-    hipLaunchKernelGGL(norm::rms_forward, dim3(ceil_div(total_rows, 4)), dim3(256), 0, stream, x, w, ms, y,
+    hipLaunchKernelGGL(norm::rms_forward, dim3(ceil_div(total_rows, 4)), dim3(256), 0, stream, x, w, ms, y, y_bf16,
                        static_cast<long long>(rows), channels, ensemble, member_stride, eps);
     check_launch("Launch RMS forward");
 }
 
 void rms_backward(int ensemble, const float* x, const float* dy, const float* w, const float* ms, float* partial,
-                  float* dx, float* dw, int rows, int channels, long long member_stride, float eps, int accumulate_dx,
-                  int accumulate_dw, hipStream_t stream) {
+                  float* dx, unsigned short* dx_bf16, float* dw, int rows, int channels, long long member_stride,
+                  float eps, int accumulate_dx, int accumulate_dw, hipStream_t stream) {
     require(ensemble > 0 && rows > 0 && channels > 0, "RMSNorm dimensions must be positive.");
     require(x && dy && w && ms, "RMSNorm backward requires x, dy, weight and ms.");
     if (member_stride <= 0) member_stride = static_cast<long long>(rows) * channels;
@@ -414,10 +418,12 @@ void rms_backward(int ensemble, const float* x, const float* dy, const float* w,
                            partial, dw, channels, chunks, ensemble, accumulate_dw);
         check_launch("Launch RMS weight reduce");
     }
-    if (dx) {
+    if (dx || dx_bf16) {
+        require(!accumulate_dx || dx, "Accumulating RMS input adjoints requires the fp32 adjoint.");
         const long long total_rows = static_cast<long long>(rows) * ensemble;
         hipLaunchKernelGGL(norm::rms_dx, dim3(ceil_div(total_rows, 4)), dim3(256), 0, stream, x, dy, w, ms, dx,
-                           static_cast<long long>(rows), channels, ensemble, member_stride, eps, accumulate_dx);
+                           dx_bf16, static_cast<long long>(rows), channels, ensemble, member_stride, eps,
+                           accumulate_dx);
         check_launch("Launch RMS input gradient");
     }
 }
@@ -465,19 +471,21 @@ RL_API int rl_bn_backward_ex(int ensemble, const float* x, long long x_stride, c
     });
 }
 
-RL_API int rl_rms_forward_ex(int ensemble, const float* x, const float* w, float* ms, float* y, int rows, int channels,
-                             long long member_stride, float eps, void* stream) noexcept {
+RL_API int rl_rms_forward_ex(int ensemble, const float* x, const float* w, float* ms, float* y, void* y_bf16, int rows,
+                             int channels, long long member_stride, float eps, void* stream) noexcept {
     return rl::guarded("rl_rms_forward_ex", [&] {
-        rl::rms_forward(ensemble, x, w, ms, y, rows, channels, member_stride, eps, rl::as_stream(stream));
+        rl::rms_forward(ensemble, x, w, ms, y, static_cast<unsigned short*>(y_bf16), rows, channels, member_stride, eps,
+                        rl::as_stream(stream));
     });
 }
 
 RL_API int rl_rms_backward_ex(int ensemble, const float* x, const float* dy, const float* w, const float* ms,
-                              float* partial, float* dx, float* dw, int rows, int channels, long long member_stride,
-                              float eps, int accumulate_dx, int accumulate_dw, void* stream) noexcept {
+                              float* partial, float* dx, void* dx_bf16, float* dw, int rows, int channels,
+                              long long member_stride, float eps, int accumulate_dx, int accumulate_dw,
+                              void* stream) noexcept {
     return rl::guarded("rl_rms_backward_ex", [&] {
-        rl::rms_backward(ensemble, x, dy, w, ms, partial, dx, dw, rows, channels, member_stride, eps, accumulate_dx,
-                         accumulate_dw, rl::as_stream(stream));
+        rl::rms_backward(ensemble, x, dy, w, ms, partial, dx, static_cast<unsigned short*>(dx_bf16), dw, rows, channels,
+                         member_stride, eps, accumulate_dx, accumulate_dw, rl::as_stream(stream));
     });
 }
 
@@ -536,13 +544,13 @@ RL_API int rl_flash_bn_backward_controlled(const float* x, const float* dy, cons
 RL_API int rl_flash_rms_forward(const float* x, const float* w, float* var, float* y, int batch, int channels, float eps,
                                 void* stream) noexcept {
     return rl::guarded("rl_flash_rms_forward",
-                       [&] { rl::rms_forward(1, x, w, var, y, batch, channels, 0, eps, rl::as_stream(stream)); });
+                       [&] { rl::rms_forward(1, x, w, var, y, nullptr, batch, channels, 0, eps, rl::as_stream(stream)); });
 }
 
 RL_API int rl_flash_rms_backward(const float* x, const float* dy, const float* w, const float* var, float* partial,
                                  float* dx, float* dw, int batch, int channels, float eps, void* stream) noexcept {
     return rl::guarded("rl_flash_rms_backward", [&] {
-        rl::rms_backward(1, x, dy, w, var, partial, dx, dw, batch, channels, 0, eps, 1, 1, rl::as_stream(stream));
+        rl::rms_backward(1, x, dy, w, var, partial, dx, nullptr, dw, batch, channels, 0, eps, 1, 1, rl::as_stream(stream));
     });
 }
 
@@ -571,5 +579,25 @@ RL_API int rl_bias_grad(const void* dy, void* db, int batch, int channels, void*
                            rl::as_stream(stream), static_cast<const float*>(dy), static_cast<float*>(db), batch,
                            channels);
         rl::check_launch("Launch bias gradient");
+    });
+}
+
+namespace rl {
+namespace norm {
+__global__ void cast_bf16(const float* src, unsigned short* dst, long long n) {
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<long long>(gridDim.x) * blockDim.x)
+        dst[i] = f32_to_bf16_bits(src[i]);
+}
+}  // namespace norm
+}  // namespace rl
+
+// fp32 -> bf16 (RNE) copy; the MI355X counterpart of robolearn/cuda/kernels.cu:663-687.
+RL_API int rl_cast_f32_bf16(const float* source, void* destination, long long count, void* stream) noexcept {
+    return rl::guarded("rl_cast_f32_bf16", [&] {
+        rl::require(source && destination && count > 0, "Cast needs buffers and a positive count.");
+        hipLaunchKernelGGL(rl::norm::cast_bf16, dim3(rl::norm::elementwise_blocks(count)), dim3(256), 0,
+                           rl::as_stream(stream), source, static_cast<unsigned short*>(destination), count);
+        rl::check_launch("Launch cast");
     });
 }

@@ -190,7 +190,7 @@ __global__ void tanh_gaussian_forward(const float* head, const float* noise, flo
 // dhead[r, :A] = dL/dmean, dhead[r, A:] = dL/draw_log_std.
 __global__ void tanh_gaussian_backward(const float* head, const float* noise, const float* dactions,
                                        long long ld_dactions, long long grad_rows, const float* dlog_probs,
-                                       float* dhead, long long rows, int action_dim) {
+                                       float* dhead, unsigned short* dhead_bf16, long long rows, int action_dim) {
     const long long r = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
     if (r >= rows) return;
     const float* h = head + r * 2 * action_dim;
@@ -207,8 +207,15 @@ __global__ void tanh_gaussian_backward(const float* head, const float* noise, co
         const float g_raw = da * (1.0f - a * a) + dlp * 2.0f * a;
         const float dstd = g_raw * eps - dlp / std;
         const float dlog_std = dstd * std;
-        dhead[r * 2 * action_dim + j] = g_raw;
-        dhead[r * 2 * action_dim + action_dim + j] = dlog_std * 6.0f * (1.0f - t * t);
+        const float g_std = dlog_std * 6.0f * (1.0f - t * t);
+        if (dhead) {
+            dhead[r * 2 * action_dim + j] = g_raw;
+            dhead[r * 2 * action_dim + action_dim + j] = g_std;
+        }
+        if (dhead_bf16) {
+            dhead_bf16[r * 2 * action_dim + j] = f32_to_bf16_bits(g_raw);
+            dhead_bf16[r * 2 * action_dim + action_dim + j] = f32_to_bf16_bits(g_std);
+        }
     }
 }
 
@@ -402,12 +409,13 @@ RL_API int rl_tanh_gaussian_forward(const float* head, const float* noise, float
 
 RL_API int rl_tanh_gaussian_backward(const float* head, const float* noise, const float* dactions,
                                      long long ld_dactions, long long grad_rows, const float* dlog_probs, float* dhead,
-                                     long long rows, int action_dim, void* stream) noexcept {
+                                     void* dhead_bf16, long long rows, int action_dim, void* stream) noexcept {
     return rl::guarded("rl_tanh_gaussian_backward", [&] {
-        rl::require(head && noise && dhead && rows > 0 && action_dim > 0, "Policy backward needs head, noise and dhead.");
+        rl::require(head && noise && (dhead || dhead_bf16) && rows > 0 && action_dim > 0,
+                    "Policy backward needs head, noise and an output.");
         hipLaunchKernelGGL(P::tanh_gaussian_backward, dim3(rl::ceil_div(rows, 256)), dim3(256), 0,
                            rl::as_stream(stream), head, noise, dactions, ld_dactions, grad_rows, dlog_probs, dhead,
-                           rows, action_dim);
+                           static_cast<unsigned short*>(dhead_bf16), rows, action_dim);
         rl::check_launch("Launch policy backward");
     });
 }

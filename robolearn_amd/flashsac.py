@@ -157,9 +157,10 @@ class FlashSAC:
             # parameters (mean/std head rows contiguous so one GEMM computes both heads)
             groups = [["predictor.mean_w.w.weight", "predictor.std_w.w.weight"],
                       ["predictor.mean_bias", "predictor.std_bias"]]
-            self.actor = FlatStore(actor_shapes(Oa, A, ha, cfg.actor_num_blocks), dev, groups=groups)
+            bf = self.mode == K.BF16
+            self.actor = FlatStore(actor_shapes(Oa, A, ha, cfg.actor_num_blocks), dev, groups=groups, shadows=bf)
             self.critic = FlatStore(critic_shapes(I, hc, cfg.critic_num_blocks, cfg.critic_num_bins), dev,
-                                    target=True)
+                                    target=True, shadows=bf)
             self.log_temperature = torch.full((1,), math.log(cfg.temp_initial_value), device=dev)
             self.temperature = FlatStore({"log_temp": (1,)}, dev)
             self.temperature.param.zero_()
@@ -174,14 +175,21 @@ class FlashSAC:
             self.target_running = _Running(running_shapes(critic_bn, 2), dev)
             self._init_parameters(cfg.seed)
             self.actor_p, self.actor_g = self.actor.params(), self.actor.grads()
+            # GEMM weight operands: bf16 shadows in bf16 mode, the fp32 masters otherwise
+            self.actor_w = self.actor.shadows() or self.actor_p
             heads = ["predictor.mean_w.w.weight", "predictor.std_w.w.weight"]
             head_bias = ["predictor.mean_bias", "predictor.std_bias"]
             self.head_w = self.actor.span(self.actor.param, heads, (2 * A, ha))
+            self.head_w_op = self.actor.span(self.actor.shadow, heads, (2 * A, ha)) if bf else self.head_w
             self.head_b = self.actor.span(self.actor.param, head_bias, (2 * A,))
             self.head_dw = self.actor.span(self.actor.grad, heads, (2 * A, ha))
             self.head_db = self.actor.span(self.actor.grad, head_bias, (2 * A,))
             self.critic_p, self.critic_g = self.critic.params(), self.critic.grads()
             self.target_p = self.critic.targets()
+            self.critic_w = self.critic.shadows() or self.critic_p
+            self.target_w = self.critic.target_shadows() or self.target_p
+            self.actor.refresh_shadows()
+            self.critic.refresh_shadows()
             # optimizers
             self.actor_optimizer = FusedOptimizer(self.actor, cfg)
             self.critic_optimizer = FusedOptimizer(self.critic, cfg, ema_tau=cfg.critic_target_update_tau)
@@ -191,7 +199,7 @@ class FlashSAC:
                                    device=dev, mode=self.mode, prefix_linear=".w.weight")
             self.critic_net = Trunk(ensemble=2, in_dim=I, hidden=hc, blocks=cfg.critic_num_blocks, max_rows=2 * B,
                                     device=dev, mode=self.mode, prefix_linear=".weight")
-            self.workspace = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+            self.workspace = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
             z = lambda *s: torch.zeros(*s, device=dev)  # noqa: E731
             self.batch = {"observation": z(B, Oc), "action": z(B, A), "reward": z(B), "terminated": z(B),
                           "truncated": z(B), "next_observation": z(B, Oc), "discount": z(B)}
@@ -201,6 +209,8 @@ class FlashSAC:
             self.critic_in = z(2 * B, I)
             self.actor_head = z(2 * B, 2 * A)
             self.actor_dhead = z(2 * B, 2 * A)
+            half = lambda *s: torch.zeros(*s, dtype=torch.bfloat16, device=dev) if bf else None  # noqa: E731
+            self.actor_dhead_h = half(2 * B, 2 * A)
             self.actor_noise = z(2 * B, A)
             self.next_noise = z(B, A)
             self.actions_all = z(2 * B, A)
@@ -216,6 +226,7 @@ class FlashSAC:
             self.logits = z(2, B, cfg.critic_num_bins)
             self.target_logits = z(2, B, cfg.critic_num_bins)
             self.dlogits = z(2, B, cfg.critic_num_bins)
+            self.dlogits_h = half(2, B, cfg.critic_num_bins)
             self.loss_rows = z(2, B)
             self.entropy_rows = z(B)
             self.target_probabilities = z(B, cfg.critic_num_bins)
@@ -327,6 +338,8 @@ class FlashSAC:
                 raise ValueError(f"Checkpoint array {key} is missing or has the wrong shape.")
         for key, array in arrays.items():
             array.copy_(torch.as_tensor(np.asarray(state[key])).to(array.dtype))
+        self.actor.refresh_shadows()
+        self.critic.refresh_shadows()
         if bool(np.asarray(state.get("replay_storage_included", [False]))[0]):
             n = int(np.asarray(state["replay.num_in_buffer"])[0])
             self.load_replay({key: state[f"replay.{key}"] for key in BATCH_KEYS}, count=n,
@@ -436,11 +449,11 @@ class FlashSAC:
         if n > 2 * self.batch_size:
             raise ValueError("act() supports at most 2 * sample_batch_size rows.")
         net, p = self.actor_net, self.actor_p
-        net.forward(p, self.actor_running, obs, rows=n, x_stride=0, training=False)
+        net.forward(p, self.actor_w, self.actor_running, obs, rows=n, x_stride=0, training=False)
         net.post_norm(p, rows=n, row0=0, count=n)
         head = torch.empty(n, 2 * self.action_dim, device=self.device)
-        K.linear_forward(net.z, self.head_w, head, rows=n, in_dim=net.h, out_dim=2 * self.action_dim,
-                         bias=self.head_b, mode=K.FP32)
+        K.linear_forward(net.z_op, self.head_w_op, head, rows=n, in_dim=net.h, out_dim=2 * self.action_dim,
+                         bias=self.head_b, mode=self.mode)
         actions = torch.empty(n, self.action_dim, device=self.device)
         noise = torch.randn(n, self.action_dim, device=self.device) if training else None
         K.tanh_gaussian_forward(head, noise, actions, None, rows=n, action_dim=self.action_dim,
@@ -474,38 +487,38 @@ class FlashSAC:
 
     def _actor_phase(self, apply_optimizer: bool):
         cfg, B, A, I, Oc = self.cfg, self.batch_size, self.action_dim, self.critic_in_dim, self.critic_observation_dim
+        bins = cfg.critic_num_bins
         net, p, g = self.actor_net, self.actor_p, self.actor_g
         cn, cp = self.critic_net, self.critic_p
         _native.call("rl_exp_scalar", self.log_temperature.data_ptr(), self.alpha.data_ptr(), K.stream())
         # actor forward on [obs; next_obs] in training mode (BN statistics over 2B rows)
-        net.forward(p, self.actor_running, self.actor_in, rows=2 * B, x_stride=0, training=True)
+        net.forward(p, self.actor_w, self.actor_running, self.actor_in, rows=2 * B, x_stride=0, training=True)
         net.post_norm(p, rows=2 * B, row0=0, count=2 * B)
-        K.linear_forward(net.z, self.head_w, self.actor_head, rows=2 * B, in_dim=net.h, out_dim=2 * A,
+        K.linear_forward(net.z_op, self.head_w_op, self.actor_head, rows=2 * B, in_dim=net.h, out_dim=2 * A,
                          bias=self.head_b, mode=self.mode)
         K.tanh_gaussian_forward(self.actor_head, self.actor_noise, self.actions_all, self.log_probs_all,
                                 rows=2 * B, action_dim=A)
         # frozen critic in eval mode on (obs, first-half actions)
         K.concat_columns(self.critic_in_actor, I, B, self.batch["observation"], Oc, Oc, self.actions_all, A, A)
-        cn.forward(cp, self.critic_running, self.critic_in_actor, rows=B, x_stride=0, training=False)
+        cn.forward(cp, self.critic_w, self.critic_running, self.critic_in_actor, rows=B, x_stride=0, training=False)
         cn.post_norm(cp, rows=B, row0=0, count=B)
-        K.linear_forward(cn.z, cp["predictor.w.weight"], self.logits, rows=B, in_dim=cn.h,
-                         out_dim=cfg.critic_num_bins, ensemble=2, x_stride=B * cn.h, bias=cp["predictor.bias"],
-                         mode=self.mode)
-        K.categorical_head_forward(self.logits, self.support, self.q, rows=B, bins=cfg.critic_num_bins, ensemble=2)
+        K.linear_forward(cn.z_op, self.critic_w["predictor.w.weight"], self.logits, rows=B, in_dim=cn.h,
+                         out_dim=bins, ensemble=2, x_stride=B * cn.h, bias=cp["predictor.bias"], mode=self.mode)
+        K.categorical_head_forward(self.logits, self.support, self.q, rows=B, bins=bins, ensemble=2)
         _native.call("rl_actor_objective", self.q.data_ptr(), self.q[1].data_ptr(), self.log_probs_all.data_ptr(),
                      self.actions_all.data_ptr(), A, self.batch["action"].data_ptr(), self.alpha.data_ptr(),
                      float(cfg.actor_bc_alpha), B, 2 * B, A, self.metrics_buffer.data_ptr(),
                      self.dlog_probs.data_ptr(), self.dq.data_ptr(), self.dq[1].data_ptr(),
                      self.dactions_bc.data_ptr() if cfg.actor_bc_alpha > 0 else None, K.stream())
         # critic backward to the action inputs (parameters frozen, BN in eval mode)
-        K.categorical_head_backward_q(self.logits, self.support, self.dq, self.dlogits, rows=B,
-                                      bins=cfg.critic_num_bins, ensemble=2)
-        dz = cn.dz
-        K.linear_backward_input(self.dlogits, cp["predictor.w.weight"], dz, rows=B, in_dim=cn.h,
-                                out_dim=cfg.critic_num_bins, ensemble=2, mode=self.mode)
+        bf = self.mode == K.BF16
+        K.categorical_head_backward_q(self.logits, self.support, self.dq, None if bf else self.dlogits, rows=B,
+                                      bins=bins, ensemble=2, dlogits_bf16=self.dlogits_h)
+        K.linear_backward_input(self.dlogits_h if bf else self.dlogits, self.critic_w["predictor.w.weight"], cn.dz,
+                                rows=B, in_dim=cn.h, out_dim=bins, ensemble=2, mode=self.mode)
         cn.post_norm_backward(cp, None, rows=B, row0=0, count=B)
-        cn.backward(cp, self.critic_running, None, self.critic_in_actor, rows=B, x_stride=0, training=False,
-                    workspace=self.workspace, input_grad=self.critic_dx)
+        cn.backward(cp, self.critic_w, self.critic_running, None, self.critic_in_actor, rows=B, x_stride=0,
+                    training=False, workspace=self.workspace, input_grad=self.critic_dx)
         _native.call("rl_add", self.critic_dx[0].data_ptr(), self.critic_dx[1].data_ptr(), B * I, K.stream())
         if cfg.actor_bc_alpha > 0:
             K.concat_columns(self.dactions_sum, A, B, self.critic_dx[0].view(-1)[Oc:], I, A)
@@ -514,15 +527,16 @@ class FlashSAC:
         else:
             dact, ld = self.critic_dx[0].view(-1)[Oc:], I
         K.tanh_gaussian_backward(self.actor_head, self.actor_noise, dact, self.dlog_probs, self.actor_dhead,
-                                 rows=2 * B, action_dim=A, grad_rows=B, ld_dactions=ld)
+                                 rows=2 * B, action_dim=A, grad_rows=B, ld_dactions=ld, dhead_bf16=self.actor_dhead_h)
         # actor backward
-        K.linear_backward_weight(self.actor_dhead, net.z, self.head_dw, rows=2 * B, in_dim=net.h, out_dim=2 * A,
+        dhead = self.actor_dhead_h if bf else self.actor_dhead
+        K.linear_backward_weight(dhead, net.z_op, self.head_dw, rows=2 * B, in_dim=net.h, out_dim=2 * A,
                                  mode=self.mode, workspace=self.workspace)
         K.bias_grad(self.actor_dhead, self.head_db, self.bias_partial, rows=2 * B, channels=2 * A)
-        K.linear_backward_input(self.actor_dhead, self.head_w, net.dz, rows=2 * B, in_dim=net.h, out_dim=2 * A,
+        K.linear_backward_input(dhead, self.head_w_op, net.dz, rows=2 * B, in_dim=net.h, out_dim=2 * A,
                                 mode=self.mode)
         net.post_norm_backward(p, g, rows=2 * B, row0=0, count=2 * B)
-        net.backward(p, self.actor_running, g, self.actor_in, rows=2 * B, x_stride=0, training=True,
+        net.backward(p, self.actor_w, self.actor_running, g, self.actor_in, rows=2 * B, x_stride=0, training=True,
                      workspace=self.workspace)
         if apply_optimizer:
             self.actor_optimizer.step()
@@ -540,49 +554,47 @@ class FlashSAC:
         net, p = self.actor_net, self.actor_p
         cn, cp, cg = self.critic_net, self.critic_p, self.critic_g
         bins = cfg.critic_num_bins
+        bf = self.mode == K.BF16
         # next actions from the updated actor in eval mode
-        net.forward(p, self.actor_running, self.actor_in[B:], rows=B, x_stride=0, training=False)
+        net.forward(p, self.actor_w, self.actor_running, self.actor_in[B:], rows=B, x_stride=0, training=False)
         net.post_norm(p, rows=B, row0=0, count=B)
-        K.linear_forward(net.z, self.head_w, self.actor_head, rows=B, in_dim=net.h, out_dim=2 * A,
+        K.linear_forward(net.z_op, self.head_w_op, self.actor_head, rows=B, in_dim=net.h, out_dim=2 * A,
                          bias=self.head_b, mode=self.mode)
         K.tanh_gaussian_forward(self.actor_head, self.next_noise, self.critic_in[B:].view(-1)[Oc:],
                                 self.next_log_probs, rows=B, action_dim=A, ld_actions=I)
         _native.call("rl_exp_scalar", self.log_temperature.data_ptr(), self.alpha.data_ptr(), K.stream())
         # target critic, training-mode BN over 2B rows; head only on the next-observation half
-        cn.forward(self.target_p, self.target_running, self.critic_in, rows=2 * B, x_stride=0, training=True)
+        cn.forward(self.target_p, self.target_w, self.target_running, self.critic_in, rows=2 * B, x_stride=0,
+                   training=True)
         cn.post_norm(self.target_p, rows=2 * B, row0=B, count=B)
-        K.linear_forward(cn.z.view(-1)[B * cn.h:], self.target_p["predictor.w.weight"], self.target_logits, rows=B,
-                         in_dim=cn.h, out_dim=bins, ensemble=2, x_stride=2 * B * cn.h,
+        K.linear_forward(cn.z_op.view(-1)[B * cn.h:], self.target_w["predictor.w.weight"], self.target_logits,
+                         rows=B, in_dim=cn.h, out_dim=bins, ensemble=2, x_stride=2 * B * cn.h,
                          bias=self.target_p["predictor.bias"], mode=self.mode)
         # online critic, training mode; head on the current-observation half
-        cn.forward(cp, self.critic_running, self.critic_in, rows=2 * B, x_stride=0, training=True)
+        cn.forward(cp, self.critic_w, self.critic_running, self.critic_in, rows=2 * B, x_stride=0, training=True)
         cn.post_norm(cp, rows=2 * B, row0=0, count=B)
-        K.linear_forward(cn.z, cp["predictor.w.weight"], self.logits, rows=B, in_dim=cn.h, out_dim=bins, ensemble=2,
-                         x_stride=2 * B * cn.h, bias=cp["predictor.bias"], mode=self.mode)
+        K.linear_forward(cn.z_op, self.critic_w["predictor.w.weight"], self.logits, rows=B, in_dim=cn.h,
+                         out_dim=bins, ensemble=2, x_stride=2 * B * cn.h, bias=cp["predictor.bias"], mode=self.mode)
         K.td_cross_entropy(self.target_logits, None, B, self.logits, None, B, self.support, self.reward_used,
                            self.batch["terminated"], self.batch["discount"], self.next_log_probs, self.alpha,
                            min_v=cfg.critic_min_v, max_v=cfg.critic_max_v, batch=B, bins=bins, scale=1.0 / (2 * B),
                            dlogits=self.dlogits, loss_rows=self.loss_rows, entropy_rows=self.entropy_rows,
-                           target_out=self.target_probabilities, q_next=self.q_next)
+                           target_out=self.target_probabilities, q_next=self.q_next, dlogits_bf16=self.dlogits_h)
         K.reduce_sum(self.loss_rows, self.metrics_buffer[3:], scale=1.0 / (2 * B))
         K.reduce_max(self.entropy_rows, self.metrics_buffer[4:])
         # critic backward
-        K.linear_backward_weight(self.dlogits, cn.z, cg["predictor.w.weight"], rows=B, in_dim=cn.h, out_dim=bins,
+        dlogits = self.dlogits_h if bf else self.dlogits
+        K.linear_backward_weight(dlogits, cn.z_op, cg["predictor.w.weight"], rows=B, in_dim=cn.h, out_dim=bins,
                                  ensemble=2, x_stride=2 * B * cn.h, mode=self.mode, workspace=self.workspace)
         K.bias_grad(self.dlogits, cg["predictor.bias"], self.bias_partial, rows=B, channels=bins, ensemble=2)
-        self._head_input_grad(cn, cp, rows_total=2 * B, rows=B)
+        K.gemm(dlogits, self.critic_w["predictor.w.weight"], cn.dz, m=B, n=cn.h, k=bins, batch=2, a_kcontig=True,
+               b_kcontig=False, lda=bins, ldb=cn.h, ldd=cn.h, stride_a=B * bins, stride_b=bins * cn.h,
+               stride_d=2 * B * cn.h, mode=self.mode)
         cn.post_norm_backward(cp, cg, rows=2 * B, row0=0, count=B)
-        cn.backward(cp, self.critic_running, cg, self.critic_in, rows=2 * B, x_stride=0, training=True,
+        cn.backward(cp, self.critic_w, self.critic_running, cg, self.critic_in, rows=2 * B, x_stride=0, training=True,
                     workspace=self.workspace)
         if apply_optimizer:
             self.critic_optimizer.step()
-
-    def _head_input_grad(self, cn, cp, *, rows_total, rows):
-        """dz[e, :rows] = dlogits[e] W[e] with dz laid out [2, rows_total, h]."""
-        bins = self.cfg.critic_num_bins
-        K.gemm(self.dlogits, cp["predictor.w.weight"], cn.dz, m=rows, n=cn.h, k=bins, batch=2, a_kcontig=True,
-               b_kcontig=False, lda=bins, ldb=cn.h, ldd=cn.h, stride_a=rows * bins, stride_b=bins * cn.h,
-               stride_d=rows_total * cn.h, mode=self.mode)
 
     def launch_update(self, do_actor_update: bool = True, *, sample: bool = True, randomize_noise: bool = True,
                       apply_optimizer: bool = True, normalize_reward: bool = True) -> None:

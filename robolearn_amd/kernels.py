@@ -51,7 +51,7 @@ def gemm(
 
 
 def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None, bias=None, epilogue=None,
-                   mode=FP32, c=None, beta=0.0):
+                   mode=FP32, c=None, beta=0.0, d_bf16=None):
     """y[e] = act(x[e] w[e]^T + bias[e]) (+ beta c); x_stride 0 broadcasts x."""
     if x_stride is None:
         x_stride = rows * in_dim
@@ -59,22 +59,25 @@ def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None,
     _check(y, ensemble * rows * out_dim, "output")
     gemm(x, w, y, m=rows, n=out_dim, k=in_dim, batch=ensemble, a_kcontig=True, b_kcontig=True, lda=in_dim,
          ldb=in_dim, ldd=out_dim, stride_a=x_stride, stride_b=out_dim * in_dim, stride_d=rows * out_dim, bias=bias,
-         stride_bias=out_dim, epilogue=epilogue, mode=mode, c=c, beta=beta)
+         stride_bias=out_dim, epilogue=epilogue, mode=mode, c=c, beta=beta, d_bf16=d_bf16)
 
 
-def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=FP32, c=None, beta=0.0):
+def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=FP32, c=None, beta=0.0,
+                          d_bf16=None):
     """dx[e] = dy[e] w[e] (+ beta c)."""
     _check(dx, ensemble * rows * in_dim, "input gradient")
     gemm(dy, w, dx, m=rows, n=in_dim, k=out_dim, batch=ensemble, a_kcontig=True, b_kcontig=False, lda=out_dim,
          ldb=in_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=out_dim * in_dim, stride_d=rows * in_dim,
-         mode=mode, c=c, beta=beta)
+         mode=mode, c=c, beta=beta, d_bf16=d_bf16)
 
 
 def split_count(m, n, k, batch, mode):
-    tiles = ((m + 127) // 128) * ((n + 127) // 128) * batch
-    ktiles = (k + (31 if mode == BF16 else 15)) // (32 if mode == BF16 else 16)
+    """K splits so that a weight-gradient product puts at least two workgroups on each of the 256 CUs."""
+    tm = 256 if mode == BF16 else 128
+    tiles = ((m + tm - 1) // tm) * ((n + 127) // 128) * batch
+    ktiles = (k + 31) // 32
     splits = 1
-    while tiles * splits < 512 and splits * 2 <= max(1, ktiles // 8) and splits < 64:
+    while tiles * splits < 512 and splits * 2 <= max(1, ktiles // 16) and splits < 64:
         splits *= 2
     return splits
 
@@ -120,16 +123,21 @@ def bn_backward(x, dy, y, w, mean, var, partial, sums, dx, dw, db, *, rows, chan
                  int(training), int(relu), int(accumulate_dx), int(accumulate_params), stream())
 
 
-def rms_forward(x, w, ms, y, *, rows, channels, ensemble=1, eps=1e-6, member_stride=0):
+def rms_forward(x, w, ms, y, *, rows, channels, ensemble=1, eps=1e-6, member_stride=0, y_bf16=None):
     """Row RMSNorm over `rows` rows per member; member_stride (elements) defaults to rows * channels."""
-    _native.call("rl_rms_forward_ex", ensemble, ptr(x), ptr(w), ptr(ms), ptr(y), rows, channels, member_stride, eps,
-                 stream())
+    _native.call("rl_rms_forward_ex", ensemble, ptr(x), ptr(w), ptr(ms), ptr(y), ptr(y_bf16), rows, channels,
+                 member_stride, eps, stream())
 
 
 def rms_backward(x, dy, w, ms, partial, dx, dw, *, rows, channels, ensemble=1, eps=1e-6, accumulate_dx=False,
-                 accumulate_dw=False, member_stride=0):
-    _native.call("rl_rms_backward_ex", ensemble, ptr(x), ptr(dy), ptr(w), ptr(ms), ptr(partial), ptr(dx), ptr(dw),
-                 rows, channels, member_stride, eps, int(accumulate_dx), int(accumulate_dw), stream())
+                 accumulate_dw=False, member_stride=0, dx_bf16=None):
+    _native.call("rl_rms_backward_ex", ensemble, ptr(x), ptr(dy), ptr(w), ptr(ms), ptr(partial), ptr(dx),
+                 ptr(dx_bf16), ptr(dw), rows, channels, member_stride, eps, int(accumulate_dx), int(accumulate_dw),
+                 stream())
+
+
+def cast_bf16(source, destination):
+    _native.call("rl_cast_f32_bf16", ptr(source), ptr(destination), source.numel(), stream())
 
 
 def bias_grad(dy, db, partial, *, rows, channels, ensemble=1, accumulate=False):
@@ -157,19 +165,20 @@ def categorical_head_forward(logits, support, values, *, rows, bins, ensemble=1,
                  ptr(values), rows, bins, ensemble, stream())
 
 
-def categorical_head_backward_q(logits, support, dvalues, dlogits, *, rows, bins, ensemble=1, bias=None):
+def categorical_head_backward_q(logits, support, dvalues, dlogits, *, rows, bins, ensemble=1, bias=None,
+                                dlogits_bf16=None):
     _native.call("rl_categorical_head_backward_q", ptr(logits), ptr(bias), bins, ptr(support), ptr(dvalues),
-                 ptr(dlogits), rows, bins, ensemble, stream())
+                 ptr(dlogits), ptr(dlogits_bf16), rows, bins, ensemble, stream())
 
 
 def td_cross_entropy(target_logits, target_bias, target_rows, online_logits, online_bias, online_rows, support,
                      reward, terminated, discount, next_log_probs, alpha, *, min_v, max_v, batch, bins, scale,
-                     dlogits, loss_rows, entropy_rows, target_out=None, q_next=None):
+                     dlogits, loss_rows, entropy_rows, target_out=None, q_next=None, dlogits_bf16=None):
     _native.call("rl_categorical_td_cross_entropy", ptr(target_logits), ptr(target_bias), target_rows,
                  ptr(online_logits), ptr(online_bias), online_rows, ptr(support), ptr(reward), ptr(terminated),
                  ptr(discount), ptr(next_log_probs), ptr(alpha), float(min_v), float(max_v), batch, bins,
-                 float(scale), ptr(target_out), ptr(dlogits), ptr(loss_rows), ptr(entropy_rows), ptr(q_next),
-                 stream())
+                 float(scale), ptr(target_out), ptr(dlogits), ptr(dlogits_bf16), ptr(loss_rows), ptr(entropy_rows),
+                 ptr(q_next), stream())
 
 
 # ---------------------------------------------------------------------------
@@ -196,10 +205,10 @@ def tanh_gaussian_forward(head, noise, actions, log_probs, *, rows, action_dim, 
 
 
 def tanh_gaussian_backward(head, noise, dactions, dlog_probs, dhead, *, rows, action_dim, grad_rows,
-                           ld_dactions=None):
+                           ld_dactions=None, dhead_bf16=None):
     _native.call("rl_tanh_gaussian_backward", ptr(head), ptr(noise), ptr(dactions),
-                 action_dim if ld_dactions is None else ld_dactions, grad_rows, ptr(dlog_probs), ptr(dhead), rows,
-                 action_dim, stream())
+                 action_dim if ld_dactions is None else ld_dactions, grad_rows, ptr(dlog_probs), ptr(dhead),
+                 ptr(dhead_bf16), rows, action_dim, stream())
 
 
 def fill(x, value):

@@ -40,7 +40,7 @@ class FlatStore:
     """Named views into flat parameter / gradient / moment / target buffers."""
 
     def __init__(self, shapes: "OrderedDict[str, tuple]", device, *, groups=None, adam=True, target=False,
-                 grads=True):
+                 grads=True, shadows=False):
         self.shapes = OrderedDict(shapes)
         groups = groups or [[name] for name in shapes]
         grouped = {name for group in groups for name in group}
@@ -58,6 +58,17 @@ class FlatStore:
         self.m1 = torch.zeros(self.size, device=device) if adam else None
         self.m2 = torch.zeros(self.size, device=device) if adam else None
         self.target = torch.zeros(self.size, device=device) if target else None
+        # bf16 operand copies of the parameters (and of the target), written by the optimizer
+        self.shadow = torch.zeros(self.size, dtype=torch.bfloat16, device=device) if shadows else None
+        self.target_shadow = (torch.zeros(self.size, dtype=torch.bfloat16, device=device)
+                              if shadows and target else None)
+
+    def refresh_shadows(self):
+        """Re-derive the bf16 copies from the fp32 masters (after init or a checkpoint load)."""
+        if self.shadow is not None:
+            K.cast_bf16(self.param, self.shadow)
+        if self.target_shadow is not None:
+            K.cast_bf16(self.target, self.target_shadow)
 
     def view(self, buffer, name):
         offset = self.offsets[name]
@@ -80,6 +91,14 @@ class FlatStore:
 
     def targets(self):
         return OrderedDict((n, self.view(self.target, n)) for n in self.shapes)
+
+    def shadows(self):
+        return OrderedDict((n, self.view(self.shadow, n)) for n in self.shapes) if self.shadow is not None else None
+
+    def target_shadows(self):
+        if self.target_shadow is None:
+            return None
+        return OrderedDict((n, self.view(self.target_shadow, n)) for n in self.shapes)
 
     def moments(self):
         return (OrderedDict((n, self.view(self.m1, n)) for n in self.shapes),
@@ -140,7 +159,12 @@ class FusedOptimizer:
             "rl_fused_optimizer_create", len(names), _native.int_array(kinds), _native.ll_array(rows),
             _native.ll_array(cols), _native.pointer_array(params), _native.pointer_array(grads),
             _native.pointer_array(m1), _native.pointer_array(m2),
-            _native.pointer_array(targets) if ema_tau is not None else None, None, None, _native.int_array(partner),
+            _native.pointer_array(targets) if ema_tau is not None else None,
+            _native.pointer_array([store.view(store.shadow, n).data_ptr() for n in names])
+            if store.shadow is not None else None,
+            _native.pointer_array([store.view(store.target_shadow, n).data_ptr() for n in names])
+            if (store.target_shadow is not None and ema_tau is not None) else None,
+            _native.int_array(partner),
             self.timestep.data_ptr(), self.lr.data_ptr(), 0.9, 0.999, 1e-8,
             float(ema_tau if ema_tau is not None else 0.0), form, int(schedule), float(cfg.learning_rate_init),
             float(cfg.learning_rate_peak), float(cfg.learning_rate_end), int(warmup), int(decay),
@@ -166,35 +190,58 @@ class FusedOptimizer:
 
 
 class Trunk:
-    """BN -> Linear embedder, residual BN blocks and the post RMSNorm, batched over members."""
+    """BN -> Linear embedder, residual BN blocks and the post RMSNorm, batched over members.
+
+    In bf16 mode every GEMM operand is a bf16 tensor written by its producer
+    (BN apply, RMS, GEMM epilogues, BN backward), so the GEMMs never convert;
+    fp32 copies exist only where an fp32 consumer needs them (BN statistics,
+    the residual stream, the BN backward inputs).
+    """
 
     def __init__(self, *, ensemble, in_dim, hidden, blocks, max_rows, device, mode, prefix_linear):
         self.E, self.in_dim, self.h, self.blocks, self.R = ensemble, in_dim, hidden, blocks, max_rows
         self.mode = mode
+        self.bf = mode == K.BF16
         self.linear = prefix_linear  # name suffix of unit-linear weights (".w.weight" actor, ".weight" critic)
         E, R, h = ensemble, max_rows, hidden
 
         def buf(*shape):
             return torch.zeros(*shape, device=device)
 
-        self.y0 = buf(E, R, in_dim)
+        def half(*shape):
+            return torch.zeros(*shape, dtype=torch.bfloat16, device=device) if self.bf else None
+
+        def full(*shape):
+            return None if self.bf else buf(*shape)
+
+        self.y0, self.y0_h = full(E, R, in_dim), half(E, R, in_dim)
         self.stream = [buf(E, R, h) for _ in range(blocks + 1)]
+        self.stream_h = [half(E, R, h) for _ in range(blocks + 1)]
         self.u1 = [buf(E, R, 4 * h) for _ in range(blocks)]
-        self.r1 = [buf(E, R, 4 * h) for _ in range(blocks)]
+        self.r1 = [full(E, R, 4 * h) for _ in range(blocks)]
+        self.r1_h = [half(E, R, 4 * h) for _ in range(blocks)]
         self.u2 = [buf(E, R, h) for _ in range(blocks)]
-        self.z = buf(E, R, h)
+        self.z, self.z_h = full(E, R, h), half(E, R, h)
         self.ms = buf(E * R)
         self.stats = {}
         for name, width in self.bn_layers():
             self.stats[name] = (buf(E, width), buf(E, width))
-        self.d_stream = buf(E, R, h)
-        self.d_u2 = buf(E, R, h)
-        self.d_r1 = buf(E, R, 4 * h)
+        self.d_stream, self.d_stream_h = buf(E, R, h), half(E, R, h)
+        self.d_u2, self.d_u2_h = full(E, R, h), half(E, R, h)
+        self.d_r1, self.d_r1_h = buf(E, R, 4 * h), half(E, R, 4 * h)
         self.dy0 = buf(E, R, in_dim)
         self.dz = buf(E, R, h)
         widest = max(4 * h, in_dim)
         self.partial = buf(E * 2 * K.chunks(R) * widest)
         self.sums = buf(2 * E * widest)
+
+    # operand views: bf16 tensors in bf16 mode, fp32 otherwise
+    def op(self, fp32, bf16):
+        return bf16 if self.bf else fp32
+
+    @property
+    def z_op(self):
+        return self.op(self.z, self.z_h)
 
     def bn_layers(self):
         yield "embedder.norm", self.in_dim
@@ -207,40 +254,46 @@ class Trunk:
             return self.stats[name]
         return running[name + ".running_mean"], running[name + ".running_var"]
 
-    def forward(self, p, running, x, *, rows, x_stride, training, update_running=True):
-        """Runs the trunk on `rows` rows of x; leaves the block outputs in self.stream."""
+    def forward(self, p, w, running, x, *, rows, x_stride, training, update_running=True):
+        """Runs the trunk on `rows` rows of x; leaves the block outputs in self.stream.
+
+        p: fp32 parameter views (BN, RMS); w: GEMM weight views (bf16 shadows in bf16 mode).
+        """
         E, h, mode = self.E, self.h, self.mode
         name = "embedder.norm"
         mean, var = self.stats[name]
         K.bn_forward(x, p[name + ".weight"], p[name + ".bias"], running[name + ".running_mean"],
                      running[name + ".running_var"], mean, var, self.partial, self.y0, rows=rows,
                      channels=self.in_dim, ensemble=E, x_stride=x_stride, training=training,
-                     update_running=update_running)
-        K.linear_forward(self.y0, p["embedder.w" + self.linear], self.stream[0], rows=rows, in_dim=self.in_dim,
-                         out_dim=h, ensemble=E, mode=mode)
+                     update_running=update_running, y_bf16=self.y0_h)
+        K.gemm(self.op(self.y0, self.y0_h), w["embedder.w" + self.linear], self.stream[0], m=rows, n=h,
+               k=self.in_dim, batch=E, a_kcontig=True, b_kcontig=True, lda=self.in_dim, ldb=self.in_dim, ldd=h,
+               stride_a=rows * self.in_dim, stride_b=h * self.in_dim, stride_d=rows * h, mode=mode,
+               d_bf16=self.stream_h[0])
         for i in range(self.blocks):
             pre = f"encoder.{i}"
-            K.linear_forward(self.stream[i], p[f"{pre}.w1{self.linear}"], self.u1[i], rows=rows, in_dim=h,
-                             out_dim=4 * h, ensemble=E, mode=mode)
+            K.linear_forward(self.op(self.stream[i], self.stream_h[i]), w[f"{pre}.w1{self.linear}"], self.u1[i],
+                             rows=rows, in_dim=h, out_dim=4 * h, ensemble=E, mode=mode)
             mean, var = self.stats[pre + ".norm1"]
             K.bn_forward(self.u1[i], p[pre + ".norm1.weight"], p[pre + ".norm1.bias"],
                          running[pre + ".norm1.running_mean"], running[pre + ".norm1.running_var"], mean, var,
                          self.partial, self.r1[i], rows=rows, channels=4 * h, ensemble=E, training=training,
-                         relu=True, update_running=update_running)
-            K.linear_forward(self.r1[i], p[f"{pre}.w2{self.linear}"], self.u2[i], rows=rows, in_dim=4 * h,
-                             out_dim=h, ensemble=E, mode=mode)
+                         relu=True, update_running=update_running, y_bf16=self.r1_h[i])
+            K.linear_forward(self.op(self.r1[i], self.r1_h[i]), w[f"{pre}.w2{self.linear}"], self.u2[i], rows=rows,
+                             in_dim=4 * h, out_dim=h, ensemble=E, mode=mode)
             mean, var = self.stats[pre + ".norm2"]
             K.bn_forward(self.u2[i], p[pre + ".norm2.weight"], p[pre + ".norm2.bias"],
                          running[pre + ".norm2.running_mean"], running[pre + ".norm2.running_var"], mean, var,
                          self.partial, self.stream[i + 1], rows=rows, channels=h, ensemble=E, training=training,
-                         relu=True, update_running=update_running, residual=self.stream[i])
+                         relu=True, update_running=update_running, residual=self.stream[i],
+                         y_bf16=self.stream_h[i + 1])
 
     def post_norm(self, p, *, rows, row0, count):
-        """RMSNorm of rows [row0, row0 + count) of the last block output into self.z (same rows)."""
+        """RMSNorm of rows [row0, row0 + count) of the last block output into z (same rows)."""
         offset = row0 * self.h
         K.rms_forward(self.stream[-1].view(-1)[offset:], p["post_norm.weight"], self.ms,
-                      self.z.view(-1)[offset:], rows=count, channels=self.h, ensemble=self.E,
-                      member_stride=rows * self.h)
+                      None if self.bf else self.z.view(-1)[offset:], rows=count, channels=self.h, ensemble=self.E,
+                      member_stride=rows * self.h, y_bf16=self.z_h.view(-1)[offset:] if self.bf else None)
 
     def post_norm_backward(self, p, g, *, rows, row0, count):
         """dz rows [row0, row0+count) -> d_stream (same rows, overwrite), RMS weight grad."""
@@ -252,13 +305,15 @@ class Trunk:
         if count < rows:
             # rows outside the head subset receive no gradient from the head
             for e in range(self.E):
-                base = self.d_stream[e]
+                base = self.d_stream.view(-1)[e * rows * self.h: (e + 1) * rows * self.h].view(rows, self.h)
                 if row0 > 0:
                     K.fill(base[:row0], 0.0)
                 if row0 + count < rows:
                     K.fill(base[row0 + count: rows], 0.0)
+        if self.bf and self.blocks == 0:
+            K.cast_bf16(self.d_stream.view(-1)[: self.E * rows * self.h], self.d_stream_h)
 
-    def backward(self, p, running, g, x, *, rows, x_stride, training, workspace, input_grad=None):
+    def backward(self, p, w, running, g, x, *, rows, x_stride, training, workspace, input_grad=None):
         """Backward from self.d_stream (gradient of the last block output).
 
         g: gradient views (None for a frozen network: only input gradients).
@@ -271,29 +326,35 @@ class Trunk:
             K.bn_backward(self.u2[i], self.d_stream, None, p[pre + ".norm2.weight"], mean, var, self.partial,
                           self.sums, self.d_u2, None if g is None else g[pre + ".norm2.weight"],
                           None if g is None else g[pre + ".norm2.bias"], rows=rows, channels=h, ensemble=E,
-                          training=training, relu=True, b=p[pre + ".norm2.bias"])
-            K.linear_backward_input(self.d_u2, p[f"{pre}.w2{self.linear}"], self.d_r1, rows=rows, in_dim=4 * h,
+                          training=training, relu=True, b=p[pre + ".norm2.bias"], dx_bf16=self.d_u2_h)
+            d_u2 = self.op(self.d_u2, self.d_u2_h)
+            K.linear_backward_input(d_u2, w[f"{pre}.w2{self.linear}"], self.d_r1, rows=rows, in_dim=4 * h,
                                     out_dim=h, ensemble=E, mode=mode)
             if g is not None:
-                K.linear_backward_weight(self.d_u2, self.r1[i], g[f"{pre}.w2{self.linear}"], rows=rows,
-                                         in_dim=4 * h, out_dim=h, ensemble=E, mode=mode, workspace=workspace)
+                K.linear_backward_weight(d_u2, self.op(self.r1[i], self.r1_h[i]), g[f"{pre}.w2{self.linear}"],
+                                         rows=rows, in_dim=4 * h, out_dim=h, ensemble=E, mode=mode,
+                                         workspace=workspace)
             mean, var = self._stats(pre + ".norm1", running, training)
-            K.bn_backward(self.u1[i], self.d_r1, self.r1[i], p[pre + ".norm1.weight"], mean, var, self.partial,
-                          self.sums, self.d_r1, None if g is None else g[pre + ".norm1.weight"],
+            K.bn_backward(self.u1[i], self.d_r1, None, p[pre + ".norm1.weight"], mean, var, self.partial,
+                          self.sums, None if self.bf else self.d_r1, None if g is None else g[pre + ".norm1.weight"],
                           None if g is None else g[pre + ".norm1.bias"], rows=rows, channels=4 * h, ensemble=E,
-                          training=training, relu=True)
-            K.linear_backward_input(self.d_r1, p[f"{pre}.w1{self.linear}"], self.d_stream, rows=rows, in_dim=h,
-                                    out_dim=4 * h, ensemble=E, mode=mode, c=self.d_stream, beta=1.0)
+                          training=training, relu=True, b=p[pre + ".norm1.bias"], dx_bf16=self.d_r1_h)
+            d_r1 = self.op(self.d_r1, self.d_r1_h)
+            K.linear_backward_input(d_r1, w[f"{pre}.w1{self.linear}"], self.d_stream, rows=rows, in_dim=h,
+                                    out_dim=4 * h, ensemble=E, mode=mode, c=self.d_stream, beta=1.0,
+                                    d_bf16=self.d_stream_h)
             if g is not None:
-                K.linear_backward_weight(self.d_r1, self.stream[i], g[f"{pre}.w1{self.linear}"], rows=rows,
-                                         in_dim=h, out_dim=4 * h, ensemble=E, mode=mode, workspace=workspace)
+                K.linear_backward_weight(d_r1, self.op(self.stream[i], self.stream_h[i]), g[f"{pre}.w1{self.linear}"],
+                                         rows=rows, in_dim=h, out_dim=4 * h, ensemble=E, mode=mode,
+                                         workspace=workspace)
+        d_stream = self.op(self.d_stream, self.d_stream_h)
         if g is not None:
-            K.linear_backward_weight(self.d_stream, self.y0, g["embedder.w" + self.linear], rows=rows,
+            K.linear_backward_weight(d_stream, self.op(self.y0, self.y0_h), g["embedder.w" + self.linear], rows=rows,
                                      in_dim=self.in_dim, out_dim=h, ensemble=E, mode=mode, workspace=workspace)
         if g is None and input_grad is None:
             return
-        K.linear_backward_input(self.d_stream, p["embedder.w" + self.linear], self.dy0, rows=rows,
-                                in_dim=self.in_dim, out_dim=h, ensemble=E, mode=mode)
+        K.linear_backward_input(d_stream, w["embedder.w" + self.linear], self.dy0, rows=rows, in_dim=self.in_dim,
+                                out_dim=h, ensemble=E, mode=mode)
         name = "embedder.norm"
         mean, var = self._stats(name, running, training)
         K.bn_backward(x, self.dy0, None, p[name + ".weight"], mean, var, self.partial, self.sums, input_grad,
