@@ -17,11 +17,14 @@ Prints ONE JSON line: value = FlashSAC updates/sec on the GPU, with
 
 import argparse
 import json
-import math
 import os
+import re
 import sys
 import time
+from pathlib import Path
 
+ROOT = Path(__file__).resolve().parent
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_bf16_critic_fwd_g1_traffic.md"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
@@ -88,6 +91,24 @@ def elementwise_bytes(w: dict) -> float:
     return critic_total + actor_bytes + optimizer + 3 * 2 * B * K * 4 * 4
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary, if it covers this kernel.
+
+    The summary holds a `kernel:` line naming the launch and a
+    `traffic_bytes_per_launch:` line (FETCH_SIZE + WRITE_SIZE, each scaled by a
+    plain copy of known size); a summary for another kernel or shape is ignored.
+    """
+    try:
+        text = TRAFFIC_PROFILE.read_text()
+    except OSError:
+        return None
+    named = re.search(r"^kernel: (.+)$", text, flags=re.M)
+    value = re.search(r"^traffic_bytes_per_launch: (\d+)$", text, flags=re.M)
+    if named is None or value is None or named.group(1).strip() != kernel:
+        return None
+    return int(value.group(1))
+
+
 def cpu_baseline(w: dict, cfg_kwargs: dict) -> dict:
     """Time the CPU oracle (fp32) on one actor-phase update at the workload shape."""
     import torch
@@ -145,8 +166,10 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--workload", choices=sorted(WORKLOADS), default="g1")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--profile-dominant", action="store_true",
-                        help="also launch the dominant kernel alone (for rocprof agreement)")
+    parser.add_argument("--calibration-copy-mb", type=int, default=0,
+                        help="after timing, run one plain device copy of this size (counter calibration)")
+    parser.add_argument("--traffic", type=float, default=None,
+                        help="HBM bytes per launch of the dominant kernel measured with rocprofv3 --pmc (reported)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the learner path is single-GPU (see DESIGN.md for sharding).",
@@ -212,8 +235,9 @@ def main() -> int:
     h = net.h
     rows = 2 * B
     reps = 20
-    launch = lambda: K.linear_forward(net.stream[0], agent.critic_p["encoder.0.w1.weight"], net.u1[0], rows=rows,  # noqa
-                                      in_dim=h, out_dim=4 * h, ensemble=2, mode=agent.mode)
+    launch = lambda: K.linear_forward(net.op(net.stream[0], net.stream_h[0]),  # noqa: E731
+                                      agent.critic_w["encoder.0.w1.weight"], net.u1[0], rows=rows, in_dim=h,
+                                      out_dim=4 * h, ensemble=2, mode=agent.mode)
     launch()
     torch.cuda.synchronize()
     k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -226,10 +250,26 @@ def main() -> int:
     kernel_flops = 2.0 * 2 * rows * h * 4 * h
     peak = BF16_PEAK_TFLOPS if agent.mode == K.BF16 else FP32_PEAK_TFLOPS
     achieved = kernel_flops / (kernel_ms * 1e-3) / 1e12
+    operand = "unsigned short" if agent.mode == K.BF16 else "float"
+    kernel_name = (f"gemm_bf16_kernel<{operand}, {operand}, true, true> critic block-1 forward "
+                   f"[2 x {rows} x {h}] . [{4 * h} x {h}]^T" if agent.mode == K.BF16 else
+                   f"gemm_kernel<0, float, float, true, true> critic block-1 forward [2 x {rows} x {h}] . "
+                   f"[{4 * h} x {h}]^T")
+    traffic = args.traffic if args.traffic is not None else measured_traffic(kernel_name)
+    operand_bytes = 2 if agent.mode == K.BF16 else 4
+    algorithmic_bytes = 2 * (rows * h + 4 * h * h) * operand_bytes + 2 * rows * 4 * h * 4
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(achieved / peak, 4), "traffic": None,
-                "kernel": "gemm_kernel<1,float,float,true,true> critic block-1 forward",
-                "kernel_ms": round(kernel_ms, 4), "flops_per_launch": kernel_flops}
+                "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": kernel_name,
+                "kernel_ms": round(kernel_ms, 4), "flops_per_launch": kernel_flops,
+                "algorithmic_bytes_per_launch": algorithmic_bytes}
+    if args.calibration_copy_mb:
+        # plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE counter readings
+        n = args.calibration_copy_mb * (1 << 20) // 4
+        src = torch.ones(n, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     flops = gemm_flops(w)
     hbm_bytes = elementwise_bytes(w)
     t_roof_ms = (flops / (peak * 1e12) + hbm_bytes / (HBM_PEAK_GBS * 1e9)) * 1e3
