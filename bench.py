@@ -12,11 +12,16 @@ Prints ONE JSON line: value = FlashSAC updates/sec on the GPU, with
                 timed live with HIP events on the stream it runs on,
   update_roofline  two-term serial roofline of the whole update,
   cpu_baseline  the CPU oracle (PyTorch-CPU restatement of the reference update,
-                fp32) timed on this host's cores on one update of the same shape.
+                fp32) timed on this host's cores on one update of the same shape,
+  ppo           PPO update ms at configs[3] (one captured graph per update, fp32
+                MFMA roofline, CPU oracle on one epoch scaled to five),
+  kernel_sweep  configs[4]: fused categorical target + CE, fused optimizer and
+                RMSNorm at their sweep shapes against the HBM roofline.
 """
 
 import argparse
 import json
+import math
 import os
 import re
 import sys
@@ -159,6 +164,217 @@ def cpu_baseline(w: dict, cfg_kwargs: dict) -> dict:
     }
 
 
+PPO_C3 = dict(envs=4096, horizon=24, obs=123, act=37, hidden=(512, 256, 128))
+
+
+def ppo_config(**overrides):
+    """The c3 PPO recipe (warp/config.py fields; ELU MLPs 512-256-128, adaptive KL)."""
+    from robolearn_amd.config import PPOConfig
+
+    fields = dict(hidden_dims=PPO_C3["hidden"], activation="elu", std_type="log", epochs=5, num_mini_batches=4,
+                  clip_ratio=0.2, clip_value=True, entropy_coefficient=0.005, schedule="adaptive", desired_kl=0.01,
+                  gamma=0.99, gae_lambda=0.95)
+    fields.update(overrides)
+    return PPOConfig(**fields)
+
+
+def ppo_flops(cfg) -> float:
+    """2 M N K summed over forward, weight- and input-gradient products of both MLPs, all epochs."""
+    rows = PPO_C3["envs"] * PPO_C3["horizon"] * cfg.epochs
+    total = 0
+    for out in (PPO_C3["act"], 1):
+        widths = [PPO_C3["obs"], *cfg.hidden_dims, out]
+        layers = list(zip(widths[:-1], widths[1:]))
+        total += 2 * sum(2 * i * o for i, o in layers) + sum(2 * i * o for i, o in layers[1:])
+    return float(rows * total)
+
+
+def ppo_rollout(agent, seed=0):
+    """Synthetic c3 rollout on the device: obs, values ~ N(0,1); actions = mu(obs) + sigma*eps with their
+    Gaussian log-probs; rewards ~ N(0,1); terminated ~ Bernoulli(1/1000); no truncations."""
+    import torch
+
+    n = agent.batch_size
+    torch.manual_seed(seed)
+    obs = torch.randn(n, agent.observation_dim, device=agent.device)
+    agent.act(obs)
+    actions, log_probs, _, means, stds = agent._act
+    agent.observations.copy_(obs)
+    agent.actions.copy_(actions)
+    agent.log_probs.copy_(log_probs)
+    agent.means.copy_(means)
+    agent.stds.copy_(stds)
+    agent.values.copy_(torch.randn(n, device=agent.device))
+    agent.next_values.copy_(torch.randn(n, device=agent.device))
+    agent.rewards.copy_(torch.randn(n, device=agent.device))
+    agent.terminated.copy_((torch.rand(n, device=agent.device) < 1e-3).int())
+    agent.truncated.zero_()
+
+
+def bench_ppo(steps: int, warmup: int, with_cpu: bool) -> dict:
+    """PPO update ms at c3: one captured graph (GAE, permutation, 5 epochs x 4 minibatches) per update."""
+    import torch
+
+    from robolearn_amd.ppo import WarpPPO
+
+    cfg = ppo_config()
+    agent = WarpPPO(PPO_C3["obs"], PPO_C3["act"], PPO_C3["envs"], PPO_C3["horizon"], cfg)
+    ppo_rollout(agent)
+    initial = agent.state_dict() if with_cpu else None
+    agent.update()  # captures the graph (after an eager warm-up that restores the state)
+    for _ in range(warmup):
+        agent.update()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        agent.update()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    flops = ppo_flops(cfg)
+    achieved = flops / (ms * 1e-3) / 1e12
+    result = {
+        "metric": "PPO update ms", "value": round(ms, 4), "unit": "ms/update", "higher_is_better": False,
+        "dtype": "fp32", "steps": steps, "warmup": warmup,
+        "config": {"workload": "ppo_c3", "envs": PPO_C3["envs"], "horizon": PPO_C3["horizon"],
+                   "obs_dim": PPO_C3["obs"], "act_dim": PPO_C3["act"], "hidden": list(cfg.hidden_dims),
+                   "activation": cfg.activation, "epochs": cfg.epochs, "minibatches": cfg.num_mini_batches,
+                   "schedule": cfg.schedule, "desired_kl": cfg.desired_kl},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "flops_per_update": flops},
+        "cpu_baseline": None,
+    }
+    if with_cpu:
+        result["cpu_baseline"] = ppo_cpu_baseline(agent, initial)
+    del agent
+    return result
+
+
+def ppo_cpu_baseline(agent, initial: dict) -> dict:
+    """The CPU oracle (fp32) on one epoch of the same rollout (4 minibatch steps), scaled to 5 epochs."""
+    import numpy as np
+    import torch
+
+    from oracle import ppo as OP
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    cfg = ppo_config(epochs=1)
+    rollout = {name: getattr(agent, name).cpu().numpy() for name in
+               ("observations", "actions", "means", "stds", "values", "log_probs", "rewards", "next_values",
+                "terminated", "truncated")}
+    layers = [initial[f"parameter_{i}"] for i in range(len(agent.parameters))]
+    oracle = OP.PPOOracle(PPO_C3["obs"], PPO_C3["act"], PPO_C3["envs"], PPO_C3["horizon"], cfg, layers,
+                          dtype=torch.float32)
+    permutation = np.random.default_rng(0).permutation(agent.batch_size)
+    t0 = time.perf_counter()
+    oracle.update(rollout, permutation)
+    seconds = time.perf_counter() - t0
+    epochs = ppo_config().epochs
+    return {"value": round(seconds * epochs * 1e3, 1), "unit": "ms/update", "cores": threads, "kind": "port",
+            "sample": f"oracle.ppo (PyTorch CPU fp32): GAE + 1 epoch x 4 minibatches timed ({seconds:.2f} s), "
+                      f"scaled x{epochs} epochs"}
+
+
+def _time_launches(launch, reps: int = 20) -> float:
+    import torch
+
+    launch()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        launch()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def _hbm_line(name: str, ms: float, algorithmic_bytes: float, detail: str) -> dict:
+    achieved = algorithmic_bytes / (ms * 1e-3) / 1e9
+    return {"kernel": name, "ms": round(ms, 4), "algorithmic_bytes": int(algorithmic_bytes),
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "detail": detail}
+
+
+def kernel_sweep() -> list:
+    """c4: the HBM-bound kernels at their sweep shapes, each timed over 20 launches with HIP events."""
+    from collections import OrderedDict
+
+    import torch
+
+    from robolearn_amd import kernels as K
+    from robolearn_amd.config import FlashSACConfig
+    from robolearn_amd.networks import FlatStore, FusedOptimizer
+
+    device = torch.device("cuda:0")
+    g = torch.Generator(device=device).manual_seed(11)
+    lines = []
+
+    # (a) fused categorical TD target + cross-entropy, 65536 rows x 101 bins, twin critics
+    B, bins = 65536, 101
+    target_logits = torch.randn(2, B, bins, generator=g, device=device)
+    online_logits = torch.randn(2, B, bins, generator=g, device=device)
+    support = torch.linspace(-10.0, 10.0, bins, device=device)
+    reward = torch.randn(B, generator=g, device=device) * 5.0
+    terminated = (torch.rand(B, generator=g, device=device) < 0.01).float()
+    discount = torch.full((B,), 0.99, device=device)
+    next_log_probs = torch.randn(B, generator=g, device=device)
+    alpha = torch.full((1,), 0.01, device=device)
+    dlogits = torch.empty(2, B, bins, device=device)
+    loss_rows, entropy_rows = torch.empty(2, B, device=device), torch.empty(B, device=device)
+
+    def categorical():
+        K.td_cross_entropy(target_logits, None, B, online_logits, None, B, support, reward, terminated, discount,
+                           next_log_probs, alpha, min_v=-10.0, max_v=10.0, batch=B, bins=bins, scale=1.0 / B,
+                           dlogits=dlogits, loss_rows=loss_rows, entropy_rows=entropy_rows)
+
+    ms = _time_launches(categorical)
+    lines.append(_hbm_line("td_cross_entropy", ms, B * (6 * bins * 4 + 28),
+                           "65536 rows x 101 bins, 2 critics: read target + online logits, write d-logits"))
+
+    # (b) fused Adam + unit-row projection + EMA over 48 tensors (~25.2M fp32 parameters)
+    shapes, kinds = OrderedDict(), {}
+    for i in range(24):
+        out, inp = ((1024, 1024), (4096, 256))[i % 2]
+        shapes[f"layer{i}.weight"] = (out, inp)
+        shapes[f"layer{i}.bias"] = (out,)
+        kinds[f"layer{i}.weight"], kinds[f"layer{i}.bias"] = 0, 3
+    store = FlatStore(shapes, device, target=True)
+    count = sum(math.prod(s) for s in shapes.values())
+    store.param.normal_(0.0, 0.05, generator=g)
+    store.target.copy_(store.param)
+    store.grad.normal_(0.0, 1e-3, generator=g)
+    store.m1.normal_(0.0, 1e-4, generator=g)
+    store.m2.copy_(store.m1 * store.m1)
+    cfg = FlashSACConfig(learning_rate_init=3e-4, learning_rate_peak=3e-4, learning_rate_end=3e-4)
+    optimizer = FusedOptimizer(store, cfg, ema_tau=0.005, kinds=kinds)
+    ms = _time_launches(lambda: optimizer.step(adam=True, project=True, ema=True))
+    lines.append(_hbm_line("fused_optimizer step_kernel", ms, 36 * count,
+                           f"48 tensors, {count} params: read p, g, m1, m2, target; write p, m1, m2, target"))
+    optimizer.close()
+    del store, optimizer
+
+    # (c) RMSNorm forward + backward, 65536 x 1024
+    rows, channels = 65536, 1024
+    x = torch.randn(rows, channels, generator=g, device=device)
+    w = torch.rand(channels, generator=g, device=device) + 0.5
+    dy = torch.randn(rows, channels, generator=g, device=device)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    ms_buf = torch.empty(rows, device=device)
+    dw = torch.empty(channels, device=device)
+    partial = torch.empty(K.chunks(rows) * channels, device=device)
+    ms = _time_launches(lambda: K.rms_forward(x, w, ms_buf, y, rows=rows, channels=channels))
+    lines.append(_hbm_line("rms_forward", ms, 2 * rows * channels * 4 + rows * 4,
+                           "65536 x 1024: read x, write y and the per-row mean square"))
+    ms = _time_launches(lambda: K.rms_backward(x, dy, w, ms_buf, partial, dx, dw, rows=rows, channels=channels))
+    lines.append(_hbm_line("rms_backward (column_partials + column_reduce + rms_dx)", ms,
+                           3 * rows * channels * 4 + rows * 4,
+                           "65536 x 1024: read x, dy (and ms), write dx; weight gradient reduced in fixed order"))
+    return lines
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -166,6 +382,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--workload", choices=sorted(WORKLOADS), default="g1")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-extras", action="store_true",
+                        help="skip the PPO (c3) update timing and the HBM kernel sweep (c4)")
     parser.add_argument("--calibration-copy-mb", type=int, default=0,
                         help="after timing, run one plain device copy of this size (counter calibration)")
     parser.add_argument("--traffic", type=float, default=None,
@@ -278,6 +496,13 @@ def main() -> int:
                        "t_roof_ms_per_step": round(t_roof_ms, 3),
                        "frac": round(t_roof_ms / ms_per_step, 4)}
 
+    ppo, sweep = None, None
+    if not args.no_extras:
+        print("[bench] PPO c3 update", file=sys.stderr, flush=True)
+        ppo = bench_ppo(max(5, args.steps // 2), 2, not args.no_cpu_baseline)
+        print("[bench] kernel sweep", file=sys.stderr, flush=True)
+        sweep = kernel_sweep()
+
     baseline = None
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
@@ -304,6 +529,8 @@ def main() -> int:
         "roofline": roofline,
         "update_roofline": update_roofline,
         "cpu_baseline": baseline,
+        "ppo": ppo,
+        "kernel_sweep": sweep,
     }
     print(json.dumps(result))
     return 0

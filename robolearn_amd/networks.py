@@ -125,17 +125,19 @@ class FusedOptimizer:
     """
 
     def __init__(self, store: FlatStore, cfg, *, project=True, ema_tau=None, plain=False, form=0,
-                 schedule=True):
+                 schedule=True, kinds=None):
+        """`kinds` optionally maps tensor names to projection kinds, overriding the name rule."""
         self.store = store
         device = store.param.device
         self.timestep = torch.zeros(1, device=device)
         self.lr = torch.full((1,), float(cfg.learning_rate_init), device=device)
         names = list(store.shapes)
+        overrides = dict(kinds or {})
         kinds, rows, cols, params, grads, m1, m2, targets, partner = [], [], [], [], [], [], [], [], []
         index = {n: i for i, n in enumerate(names)}
         for name in names:
             shape = store.shapes[name]
-            kind = 3 if (plain or not project) else projection_kind(name)
+            kind = 3 if (plain or not project) else overrides.get(name, projection_kind(name))
             if kind == 0:
                 r, c = _numel(shape[:-1]), shape[-1]
             elif kind in (1, 2):

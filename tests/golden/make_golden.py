@@ -39,6 +39,7 @@ def injected_noise(noise):
 
 
 def main(src: str) -> None:
+    sys.dont_write_bytecode = True  # the reference tree is read-only input: leave no __pycache__ in it
     sys.path.insert(0, src)
     from robolearn.flashsac._utils.distribution import safe_tanh_log_det_jacobian
     from robolearn.flashsac._utils.network import Network
