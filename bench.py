@@ -369,7 +369,7 @@ def kernel_sweep() -> list:
     lines.append(_hbm_line("rms_forward", ms, 2 * rows * channels * 4 + rows * 4,
                            "65536 x 1024: read x, write y and the per-row mean square"))
     ms = _time_launches(lambda: K.rms_backward(x, dy, w, ms_buf, partial, dx, dw, rows=rows, channels=channels))
-    lines.append(_hbm_line("rms_backward (column_partials + column_reduce + rms_dx)", ms,
+    lines.append(_hbm_line("rms_backward (rms_backward_fused + column_reduce)", ms,
                            3 * rows * channels * 4 + rows * 4,
                            "65536 x 1024: read x, dy (and ms), write dx; weight gradient reduced in fixed order"))
     return lines

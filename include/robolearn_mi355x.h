@@ -243,11 +243,13 @@ int rl_ppo_gather(const int* indices, long long offset, long long rows, int obs_
                   const float* advantages, const float* returns, const float* means, const float* stds, float* b_obs,
                   float* b_actions, float* b_log_probs, float* b_values, float* b_advantages, float* b_returns,
                   float* b_means, float* b_stds, void* stream);
-/* robolearn/warp/ppo.py:207-238 */
+/* robolearn/warp/ppo.py:207-238 (KL kernel + adaptive LR rule); partial is
+ * scratch of ceil(rows / 16) floats (fixed-order per-workgroup sums). */
 int rl_ppo_kl_adapt(const float* mean, long long ld_mean, const float* std_param, const float* old_mean,
                     const float* old_std, long long rows, int action_dim, int std_type, float std_min, float std_max,
-                    float desired_kl, int adapt, float* kl_out, float* lr, void* stream);
-/* robolearn/warp/ppo.py:255-310 forward and analytic backward; totals = (loss, policy, value, entropy). */
+                    float desired_kl, int adapt, float* partial, float* kl_out, float* lr, void* stream);
+/* robolearn/warp/ppo.py:255-310 forward and analytic backward; totals = (loss, policy, value, entropy).
+ * row_terms is scratch of 4 * ceil(rows / 16) floats (per-workgroup sums). */
 int rl_ppo_loss(const float* mean, long long ld_mean, const float* value, const float* std_param,
                 const float* actions, const float* old_log_probs, const float* old_values, const float* advantages,
                 const float* returns, long long rows, int action_dim, int std_type, float std_min, float std_max,

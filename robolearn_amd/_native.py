@@ -103,7 +103,7 @@ SIGNATURES = {
     "rl_permutation": (c_int, [c_ll, c_ull, P, P, P, P]),
     "rl_advance_int": (c_int, [P, P]),
     "rl_ppo_gather": (c_int, [P, c_ll, c_ll, c_int, c_int, c_int] + [P] * 16 + [P]),
-    "rl_ppo_kl_adapt": (c_int, [P, c_ll, P, P, P, c_ll, c_int, c_int, c_float, c_float, c_float, c_int, P, P, P]),
+    "rl_ppo_kl_adapt": (c_int, [P, c_ll, P, P, P, c_ll, c_int, c_int, c_float, c_float, c_float, c_int, P, P, P, P]),
     "rl_ppo_loss": (c_int, [P, c_ll, P, P, P, P, P, P, P, c_ll, c_int, c_int, c_float, c_float, c_float, c_float,
                             c_float, c_float, c_int, P, P, P, P, P, P]),
     "rl_sum_squares": (c_int, [P, c_ll, P, P, P]),

@@ -14,10 +14,10 @@
 //             -sum_j t_j lp_j on the current-observation half.
 //   Native    robolearn/cuda/categorical_kernels.cuh:35-176.
 //
-// One wavefront owns one row (K <= 512, at most 8 bins per lane).  The
-// projection is deterministic and reproduces the reference's per-bin summation
-// order: every lane owns its target bins and walks the source bins in order,
-// so no atomics are involved.
+// One wavefront owns one row (K <= 512; kernels are instantiated for 1, 2, 4
+// or 8 bins per lane).  The projection is deterministic and reproduces the
+// reference's per-bin summation order: every lane owns its target bins and adds
+// the source bins that land there in source order, so no atomics are involved.
 #include "common.hpp"
 
 #include <cmath>
@@ -26,46 +26,77 @@ namespace rl {
 namespace cat {
 
 constexpr int kMaxBins = 512;
-constexpr int kPerLane = kMaxBins / kWave;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 
-struct RowSoftmax {
-    float lp[kPerLane];
-    float q;
-};
-
-// log_softmax of one row held as kPerLane values per lane, plus expectation.
-__device__ __forceinline__ void log_softmax_row(const float* logits, const float* bias, const float* support, int bins,
-                                                float* lp, float& q) {
+// One row of logits as PerLane values per lane, bin j = lane + i * 64.  The
+// loads are unconditional (the index is clamped into the row) so a wave can
+// keep every load of a row in flight; finish_row masks the missing bins.
+template <int PerLane>
+__device__ __forceinline__ void load_row(const float* logits, int bins, float* x) {
     const int lane = threadIdx.x % kWave;
-    float x[kPerLane];
+#pragma unroll
+    for (int i = 0; i < PerLane; ++i) x[i] = logits[min(lane + i * kWave, bins - 1)];
+}
+
+// Adds the bias (if any) and sets bins >= `bins` to -inf.
+template <int PerLane>
+__device__ __forceinline__ void finish_row(const float* bias, int bins, float* x) {
+    const int lane = threadIdx.x % kWave;
+    if (bias) {
+#pragma unroll
+        for (int i = 0; i < PerLane; ++i) x[i] += bias[min(lane + i * kWave, bins - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < PerLane; ++i)
+        if (lane + i * kWave >= bins) x[i] = -INFINITY;
+}
+
+template <int PerLane>
+__device__ __forceinline__ void load_support(const float* support, int bins, float* z) {
+    const int lane = threadIdx.x % kWave;
+#pragma unroll
+    for (int i = 0; i < PerLane; ++i) {
+        const int j = lane + i * kWave;
+        const float v = support[min(j, bins - 1)];
+        z[i] = j < bins ? v : 0.0f;
+    }
+}
+
+// log_softmax of a loaded row, plus the expectation over the support z.
+template <int PerLane>
+__device__ __forceinline__ void log_softmax_values(const float* x, const float* z, int bins, float* lp, float& q) {
+    const int lane = threadIdx.x % kWave;
     float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-        const int j = lane + i * kWave;
-        x[i] = j < bins ? logits[j] + (bias ? bias[j] : 0.0f) : -INFINITY;
-        m = fmaxf(m, x[i]);
-    }
+    for (int i = 0; i < PerLane; ++i) m = fmaxf(m, x[i]);
     m = wave_max(m);
     float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-        const int j = lane + i * kWave;
-        if (j < bins) s += expf(x[i] - m);
-    }
+    for (int i = 0; i < PerLane; ++i)
+        if (lane + i * kWave < bins) s += expf(x[i] - m);
     const float lse = logf(wave_sum(s));
     float e = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
-        const int j = lane + i * kWave;
+    for (int i = 0; i < PerLane; ++i) {
         lp[i] = x[i] - m - lse;
-        if (j < bins) e += expf(lp[i]) * support[j];
+        if (lane + i * kWave < bins) e += expf(lp[i]) * z[i];
     }
     q = wave_sum(e);
 }
 
+template <int PerLane>
+__device__ __forceinline__ void log_softmax_row(const float* logits, const float* bias, const float* support, int bins,
+                                                float* lp, float& q) {
+    float x[PerLane], z[PerLane];
+    load_row<PerLane>(logits, bins, x);
+    load_support<PerLane>(support, bins, z);
+    finish_row<PerLane>(bias, bins, x);
+    log_softmax_values<PerLane>(x, z, bins, lp, q);
+}
+
 // Head forward over ensemble x rows: lp (optional) and Q.
+template <int PerLane>
 __global__ __launch_bounds__(kThreads) void head_forward(const float* logits, const float* bias, long long bias_stride,
                                                          const float* support, float* log_probs, float* values,
                                                          long long rows, int bins, int ensemble) {
@@ -73,12 +104,12 @@ __global__ __launch_bounds__(kThreads) void head_forward(const float* logits, co
     if (row >= rows * ensemble) return;
     const int e = static_cast<int>(row / rows);
     const int lane = threadIdx.x % kWave;
-    float lp[kPerLane];
+    float lp[PerLane];
     float q;
-    log_softmax_row(logits + row * bins, bias ? bias + e * bias_stride : nullptr, support, bins, lp, q);
+    log_softmax_row<PerLane>(logits + row * bins, bias ? bias + e * bias_stride : nullptr, support, bins, lp, q);
     if (log_probs) {
 #pragma unroll
-        for (int i = 0; i < kPerLane; ++i) {
+        for (int i = 0; i < PerLane; ++i) {
             const int j = lane + i * kWave;
             if (j < bins) log_probs[row * bins + j] = lp[i];
         }
@@ -108,6 +139,7 @@ __global__ __launch_bounds__(kThreads) void head_backward(const float* log_probs
 }
 
 // Q-gradient through a head given raw logits (actor phase): dlogits = dq p (z - Q).
+template <int PerLane>
 __global__ __launch_bounds__(kThreads) void head_backward_q(const float* logits, const float* bias,
                                                             long long bias_stride, const float* support,
                                                             const float* dvalues, float* dlogits,
@@ -117,12 +149,12 @@ __global__ __launch_bounds__(kThreads) void head_backward_q(const float* logits,
     if (row >= rows * ensemble) return;
     const int e = static_cast<int>(row / rows);
     const int lane = threadIdx.x % kWave;
-    float lp[kPerLane];
+    float lp[PerLane];
     float q;
-    log_softmax_row(logits + row * bins, bias ? bias + e * bias_stride : nullptr, support, bins, lp, q);
+    log_softmax_row<PerLane>(logits + row * bins, bias ? bias + e * bias_stride : nullptr, support, bins, lp, q);
     const float dq = dvalues[row];
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
+    for (int i = 0; i < PerLane; ++i) {
         const int j = lane + i * kWave;
         if (j < bins) {
             const float g = dq * expf(lp[i]) * (support[j] - q);
@@ -143,26 +175,54 @@ struct TargetArgs {
     int bins;
 };
 
-// Two-hot projection of one row's selected probabilities, in the reference's
-// scatter order.  probs[i] holds p_j for j = lane + i * 64.  Returns t in the
-// same layout.  lds must hold 4 * bins floats for this wave.
-__device__ __forceinline__ void project_row(const TargetArgs& a, long long row, const float* probs, float* t,
-                                            float* lds) {
+// First j in [0, bins) with idx[j] >= k for a non-decreasing idx, else bins.
+__device__ __forceinline__ int first_at_least(const int* idx, int bins, int k) {
+    int lo = 0, hi = bins;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (idx[mid] < k) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Two-hot projection of one row's selected probabilities with the reference's
+// summation order: target bin k receives its lower-bin masses in source order,
+// then its upper-bin masses in source order (two scatter_add_ calls,
+// updates.py:76-79).  probs[i] holds p_j for j = lane + i * 64; t is returned
+// in the same layout.  lds holds 4 * PerLane * 64 words for this wave.
+//
+// The bin indices are non-decreasing in j whenever the support is (the map
+// z -> clamp(r + g (z - e) (1 - d)) is monotone for g (1 - d) >= 0), so the
+// sources of bin k form a contiguous range found by binary search.  A row whose
+// indices are not monotone falls back to scanning every source bin.
+// Scalars of one transition that the target needs.
+struct RowInputs {
+    float reward, discount, not_done, entropy;
+};
+
+__device__ __forceinline__ RowInputs load_row_inputs(const TargetArgs& a, long long row) {
+    return RowInputs{a.reward[row], a.discount[row], 1.0f - a.terminated[row], a.alpha[0] * a.next_log_probs[row]};
+}
+
+template <int PerLane>
+__device__ __forceinline__ void project_row(const TargetArgs& a, const RowInputs& in, const float* support_values,
+                                            const float* probs, float* t, int* lds) {
     const int lane = threadIdx.x % kWave;
     const int bins = a.bins;
-    float* lower_idx = lds;
-    float* upper_idx = lds + bins;
-    float* lower_mass = lds + 2 * bins;
-    float* upper_mass = lds + 3 * bins;
-    const float entropy = a.alpha[0] * a.next_log_probs[row];
-    const float r = a.reward[row];
-    const float g = a.discount[row];
-    const float not_done = 1.0f - a.terminated[row];
+    int* lower_idx = lds;
+    int* upper_idx = lds + PerLane * kWave;
+    float* lower_mass = reinterpret_cast<float*>(lds + 2 * PerLane * kWave);
+    float* upper_mass = reinterpret_cast<float*>(lds + 3 * PerLane * kWave);
+    const float entropy = in.entropy;
+    const float r = in.reward;
+    const float g = in.discount;
+    const float not_done = in.not_done;
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
+    for (int i = 0; i < PerLane; ++i) {
         const int j = lane + i * kWave;
         if (j < bins) {
-            const float z = a.support ? a.support[j] : a.min_v + static_cast<float>(j) * a.width;
+            const float z = a.support ? support_values[i] : a.min_v + static_cast<float>(j) * a.width;
             float v = r + (g * (z - entropy)) * not_done;
             v = fminf(fmaxf(v, a.min_v), a.max_v);
             const float b = (v - a.min_v) / a.width;
@@ -170,8 +230,8 @@ __device__ __forceinline__ void project_row(const TargetArgs& a, long long row, 
             lower = min(max(lower, 0), bins - 1);
             const int upper = min(lower + 1, bins - 1);
             const float frac = b - static_cast<float>(lower);
-            lower_idx[j] = static_cast<float>(lower);
-            upper_idx[j] = static_cast<float>(upper);
+            lower_idx[j] = lower;
+            upper_idx[j] = upper;
             lower_mass[j] = probs[i] * (1.0f - frac);
             upper_mass[j] = probs[i] * frac;
         }
@@ -179,20 +239,43 @@ __device__ __forceinline__ void project_row(const TargetArgs& a, long long row, 
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    bool monotone = true;
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) t[i] = 0.0f;
+    for (int i = 0; i < PerLane; ++i) {
+        const int j = lane + i * kWave;
+        if (j > 0 && j < bins) monotone = monotone && lower_idx[j] >= lower_idx[j - 1] && upper_idx[j] >= upper_idx[j - 1];
+    }
+    if (__all(monotone)) {
+#pragma unroll
+        for (int i = 0; i < PerLane; ++i) {
+            const int k = lane + i * kWave;
+            float sum = 0.0f;
+            if (k < bins) {
+                const int l0 = first_at_least(lower_idx, bins, k);
+                const int l1 = first_at_least(lower_idx, bins, k + 1);
+                for (int j = l0; j < l1; ++j) sum += lower_mass[j];
+                const int u0 = first_at_least(upper_idx, bins, k);
+                const int u1 = first_at_least(upper_idx, bins, k + 1);
+                for (int j = u0; j < u1; ++j) sum += upper_mass[j];
+            }
+            t[i] = sum;
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < PerLane; ++i) t[i] = 0.0f;
     for (int j = 0; j < bins; ++j) {
-        const int lj = static_cast<int>(lower_idx[j]);
+        const int lj = lower_idx[j];
         const float mj = lower_mass[j];
 #pragma unroll
-        for (int i = 0; i < kPerLane; ++i)
+        for (int i = 0; i < PerLane; ++i)
             if (lj == lane + i * kWave) t[i] += mj;
     }
     for (int j = 0; j < bins; ++j) {
-        const int uj = static_cast<int>(upper_idx[j]);
+        const int uj = upper_idx[j];
         const float mj = upper_mass[j];
 #pragma unroll
-        for (int i = 0; i < kPerLane; ++i)
+        for (int i = 0; i < PerLane; ++i)
             if (uj == lane + i * kWave) t[i] += mj;
     }
 }
@@ -201,6 +284,7 @@ __device__ __forceinline__ void project_row(const TargetArgs& a, long long row, 
 //   target critic (ensemble 2) logits of the next-observation rows -> min-Q
 //   selection -> two-hot target; online critic logits of the current rows ->
 //   loss rows and dlogits = scale * (p * sum(t) - t) for both members.
+template <int PerLane>
 __global__ __launch_bounds__(kThreads) void td_cross_entropy(TargetArgs a, const float* target_logits,
                                                              const float* target_bias, long long target_rows,
                                                              const float* online_logits, const float* online_bias,
@@ -208,44 +292,56 @@ __global__ __launch_bounds__(kThreads) void td_cross_entropy(TargetArgs a, const
                                                              float* target_out, float* dlogits,
                                                              unsigned short* dlogits_bf16, float* loss_rows,
                                                              float* entropy_rows, float* q_next) {
-    __shared__ float lds[kWaves][4 * kMaxBins];
+    __shared__ int lds[kWaves][4 * PerLane * kWave];
     const int wave = threadIdx.x / kWave;
     const long long row = blockIdx.x * static_cast<long long>(kWaves) + wave;
     if (row >= batch) return;
     const int lane = threadIdx.x % kWave;
     const int bins = a.bins;
-    float lp0[kPerLane], lp1[kPerLane];
+    // every global read of the row is issued before any arithmetic, so a row
+    // costs one memory round trip
+    float x0[PerLane], x1[PerLane], o0[PerLane], o1[PerLane], z[PerLane];
+    load_row<PerLane>(target_logits + row * bins, bins, x0);
+    load_row<PerLane>(target_logits + (target_rows + row) * bins, bins, x1);
+    load_row<PerLane>(online_logits + row * bins, bins, o0);
+    load_row<PerLane>(online_logits + (online_rows + row) * bins, bins, o1);
+    load_support<PerLane>(a.support, bins, z);
+    const RowInputs in = load_row_inputs(a, row);
+    finish_row<PerLane>(target_bias, bins, x0);
+    finish_row<PerLane>(target_bias ? target_bias + bins : nullptr, bins, x1);
+    finish_row<PerLane>(online_bias, bins, o0);
+    finish_row<PerLane>(online_bias ? online_bias + bins : nullptr, bins, o1);
+    float lp0[PerLane], lp1[PerLane];
     float q0, q1;
-    log_softmax_row(target_logits + row * bins, target_bias, a.support, bins, lp0, q0);
-    log_softmax_row(target_logits + (target_rows + row) * bins, target_bias ? target_bias + bins : nullptr, a.support,
-                    bins, lp1, q1);
+    log_softmax_values<PerLane>(x0, z, bins, lp0, q0);
+    log_softmax_values<PerLane>(x1, z, bins, lp1, q1);
     const bool second = q1 < q0;
-    float probs[kPerLane];
+    float probs[PerLane];
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) probs[i] = expf(second ? lp1[i] : lp0[i]);
-    float t[kPerLane];
-    project_row(a, row, probs, t, lds[wave]);
+    for (int i = 0; i < PerLane; ++i) probs[i] = expf(second ? lp1[i] : lp0[i]);
+    float t[PerLane];
+    project_row<PerLane>(a, in, z, probs, t, lds[wave]);
     float tsum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i)
+    for (int i = 0; i < PerLane; ++i)
         if (lane + i * kWave < bins) tsum += t[i];
     tsum = wave_sum(tsum);
     if (target_out) {
 #pragma unroll
-        for (int i = 0; i < kPerLane; ++i) {
+        for (int i = 0; i < PerLane; ++i) {
             const int j = lane + i * kWave;
             if (j < bins) target_out[row * bins + j] = t[i];
         }
     }
+#pragma unroll
     for (int member = 0; member < 2; ++member) {
         const long long orow = member * online_rows + row;
-        float lp[kPerLane];
+        float lp[PerLane];
         float q;
-        log_softmax_row(online_logits + orow * bins, online_bias ? online_bias + member * bins : nullptr, a.support,
-                        bins, lp, q);
+        log_softmax_values<PerLane>(member == 0 ? o0 : o1, z, bins, lp, q);
         float ce = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kPerLane; ++i) {
+        for (int i = 0; i < PerLane; ++i) {
             const int j = lane + i * kWave;
             if (j < bins) {
                 ce -= t[i] * lp[i];
@@ -258,7 +354,7 @@ __global__ __launch_bounds__(kThreads) void td_cross_entropy(TargetArgs a, const
         if (lane == 0) loss_rows[member * batch + row] = ce;
     }
     if (lane == 0) {
-        entropy_rows[row] = a.alpha[0] * a.next_log_probs[row];
+        entropy_rows[row] = in.entropy;
         if (q_next) {
             q_next[row] = q0;
             q_next[batch + row] = q1;
@@ -280,9 +376,10 @@ __device__ __forceinline__ void atomic_max_float(float* address, float value) {
     }
 }
 
+template <int PerLane>
 __global__ __launch_bounds__(kThreads) void project_target(TargetArgs a, const float* q, const float* log_probs,
                                                            long long batch, float* target, float* maximum_entropy) {
-    __shared__ float lds[kWaves][4 * kMaxBins];
+    __shared__ int lds[kWaves][4 * PerLane * kWave];
     const int wave = threadIdx.x / kWave;
     const long long row = blockIdx.x * static_cast<long long>(kWaves) + wave;
     if (row >= batch) return;
@@ -290,16 +387,16 @@ __global__ __launch_bounds__(kThreads) void project_target(TargetArgs a, const f
     const int bins = a.bins;
     const int selected = q[3 * batch + row] < q[batch + row] ? 1 : 0;
     const float* src = log_probs + (static_cast<long long>(selected) * (2 * batch) + batch + row) * bins;
-    float probs[kPerLane];
+    float probs[PerLane];
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
+    for (int i = 0; i < PerLane; ++i) {
         const int j = lane + i * kWave;
         probs[i] = j < bins ? expf(src[j]) : 0.0f;
     }
-    float t[kPerLane];
-    project_row(a, row, probs, t, lds[wave]);
+    float t[PerLane];
+    project_row<PerLane>(a, load_row_inputs(a, row), nullptr, probs, t, lds[wave]);
 #pragma unroll
-    for (int i = 0; i < kPerLane; ++i) {
+    for (int i = 0; i < PerLane; ++i) {
         const int j = lane + i * kWave;
         if (j < bins) target[row * bins + j] = t[i];
     }
@@ -321,6 +418,51 @@ __global__ __launch_bounds__(1024) void reduce_vector(const float* x, long long 
     }
     if (threadIdx.x == 0) out[0] = op == 1 ? part[0] : part[0] * scale;
 }
+
+// Launches Kernel<PerLane> with the narrowest per-lane width that holds `bins`.
+template <template <int> class Launch, class... Args>
+void dispatch_bins(int bins, Args&&... args) {
+    if (bins <= kWave) Launch<1>::run(args...);
+    else if (bins <= 2 * kWave) Launch<2>::run(args...);
+    else if (bins <= 4 * kWave) Launch<4>::run(args...);
+    else Launch<8>::run(args...);
+}
+
+template <int P> struct HeadForward {
+    static void run(dim3 grid, hipStream_t st, const float* logits, const float* bias, long long bias_stride,
+                    const float* support, float* log_probs, float* values, long long rows, int bins, int ensemble) {
+        hipLaunchKernelGGL(head_forward<P>, grid, dim3(kThreads), 0, st, logits, bias, bias_stride, support, log_probs,
+                           values, rows, bins, ensemble);
+    }
+};
+
+template <int P> struct HeadBackwardQ {
+    static void run(dim3 grid, hipStream_t st, const float* logits, const float* bias, long long bias_stride,
+                    const float* support, const float* dvalues, float* dlogits, unsigned short* dlogits_bf16,
+                    long long rows, int bins, int ensemble) {
+        hipLaunchKernelGGL(head_backward_q<P>, grid, dim3(kThreads), 0, st, logits, bias, bias_stride, support, dvalues,
+                           dlogits, dlogits_bf16, rows, bins, ensemble);
+    }
+};
+
+template <int P> struct TdCrossEntropy {
+    static void run(dim3 grid, hipStream_t st, const TargetArgs& a, const float* target_logits, const float* target_bias,
+                    long long target_rows, const float* online_logits, const float* online_bias, long long online_rows,
+                    long long batch, float scale, float* target_out, float* dlogits, unsigned short* dlogits_bf16,
+                    float* loss_rows, float* entropy_rows, float* q_next) {
+        hipLaunchKernelGGL(td_cross_entropy<P>, grid, dim3(kThreads), 0, st, a, target_logits, target_bias, target_rows,
+                           online_logits, online_bias, online_rows, batch, scale, target_out, dlogits, dlogits_bf16,
+                           loss_rows, entropy_rows, q_next);
+    }
+};
+
+template <int P> struct ProjectTarget {
+    static void run(dim3 grid, hipStream_t st, const TargetArgs& a, const float* q, const float* log_probs,
+                    long long batch, float* target, float* maximum_entropy) {
+        hipLaunchKernelGGL(project_target<P>, grid, dim3(kThreads), 0, st, a, q, log_probs, batch, target,
+                           maximum_entropy);
+    }
+};
 
 }  // namespace cat
 
@@ -345,9 +487,9 @@ RL_API int rl_categorical_head_forward(const float* logits, const float* bias, l
     return rl::guarded("rl_categorical_head_forward", [&] {
         rl::require(logits && support && values && rows > 0 && bins >= 2 && bins <= kMaxBins && ensemble > 0,
                     "Categorical head needs logits, support, values and 2..512 bins.");
-        hipLaunchKernelGGL(rl::cat::head_forward, dim3(rl::ceil_div(rows * ensemble, rl::cat::kWaves)),
-                           dim3(rl::cat::kThreads), 0, rl::as_stream(stream), logits, bias, bias_stride, support,
-                           log_probs, values, rows, bins, ensemble);
+        rl::cat::dispatch_bins<rl::cat::HeadForward>(bins, dim3(rl::ceil_div(rows * ensemble, rl::cat::kWaves)),
+                                                     rl::as_stream(stream), logits, bias, bias_stride, support,
+                                                     log_probs, values, rows, bins, ensemble);
         rl::check_launch("Launch categorical head forward");
     });
 }
@@ -360,9 +502,10 @@ RL_API int rl_categorical_head_backward_q(const float* logits, const float* bias
         rl::require(logits && support && dvalues && (dlogits || dlogits_bf16) && rows > 0 && bins >= 2 &&
                         bins <= kMaxBins,
                     "Categorical Q backward needs logits, support, dvalues, an output and 2..512 bins.");
-        hipLaunchKernelGGL(rl::cat::head_backward_q, dim3(rl::ceil_div(rows * ensemble, rl::cat::kWaves)),
-                           dim3(rl::cat::kThreads), 0, rl::as_stream(stream), logits, bias, bias_stride, support,
-                           dvalues, dlogits, static_cast<unsigned short*>(dlogits_bf16), rows, bins, ensemble);
+        rl::cat::dispatch_bins<rl::cat::HeadBackwardQ>(bins, dim3(rl::ceil_div(rows * ensemble, rl::cat::kWaves)),
+                                                       rl::as_stream(stream), logits, bias, bias_stride, support,
+                                                       dvalues, dlogits, static_cast<unsigned short*>(dlogits_bf16),
+                                                       rows, bins, ensemble);
         rl::check_launch("Launch categorical Q backward");
     });
 }
@@ -383,10 +526,12 @@ RL_API int rl_categorical_td_cross_entropy(const float* target_logits, const flo
         rl::require(target_rows >= batch && online_rows >= batch, "Member row strides must cover the batch.");
         rl::cat::TargetArgs a{support, reward, terminated, discount, next_log_probs, alpha, min_v, max_v,
                               static_cast<float>((static_cast<double>(max_v) - min_v) / (bins - 1)), bins};
-        hipLaunchKernelGGL(rl::cat::td_cross_entropy, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
-                           dim3(rl::cat::kThreads), 0, rl::as_stream(stream), a, target_logits, target_bias,
-                           target_rows, online_logits, online_bias, online_rows, batch, scale, target_out, dlogits,
-                           static_cast<unsigned short*>(dlogits_bf16), loss_rows, entropy_rows, q_next);
+        rl::cat::dispatch_bins<rl::cat::TdCrossEntropy>(bins, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
+                                                        rl::as_stream(stream), a, target_logits, target_bias,
+                                                        target_rows, online_logits, online_bias, online_rows, batch,
+                                                        scale, target_out, dlogits,
+                                                        static_cast<unsigned short*>(dlogits_bf16), loss_rows,
+                                                        entropy_rows, q_next);
         rl::check_launch("Launch TD cross-entropy");
     });
 }
@@ -399,10 +544,12 @@ RL_API int rl_flash_categorical_forward(const void* raw, const void* bias, const
     return rl::guarded("rl_flash_categorical_forward", [&] {
         rl::require(raw && bias && support && log_probs && values && batch >= 1 && bins >= 2 && bins <= kMaxBins,
                     "Categorical forward requires nonempty FP32 buffers and 2..512 bins.");
-        hipLaunchKernelGGL(rl::cat::head_forward, dim3(rl::ceil_div(batch, rl::cat::kWaves)), dim3(rl::cat::kThreads),
-                           0, rl::as_stream(stream), static_cast<const float*>(raw), static_cast<const float*>(bias),
-                           0LL, static_cast<const float*>(support), static_cast<float*>(log_probs),
-                           static_cast<float*>(values), static_cast<long long>(batch), bins, 1);
+        rl::cat::dispatch_bins<rl::cat::HeadForward>(bins, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
+                                                     rl::as_stream(stream), static_cast<const float*>(raw),
+                                                     static_cast<const float*>(bias), 0LL,
+                                                     static_cast<const float*>(support), static_cast<float*>(log_probs),
+                                                     static_cast<float*>(values), static_cast<long long>(batch), bins,
+                                                     1);
         rl::check_launch("Launch categorical forward");
     });
 }
@@ -439,10 +586,11 @@ RL_API int rl_flash_categorical_target(const void* q, const void* log_probs, con
                               static_cast<const float*>(discount), static_cast<const float*>(next_log_probs),
                               static_cast<const float*>(alpha), min_v, max_v, (max_v - min_v) / static_cast<float>(bins - 1),
                               bins};
-        hipLaunchKernelGGL(rl::cat::project_target, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
-                           dim3(rl::cat::kThreads), 0, rl::as_stream(stream), a, static_cast<const float*>(q),
-                           static_cast<const float*>(log_probs), static_cast<long long>(batch),
-                           static_cast<float*>(target), static_cast<float*>(maximum_entropy));
+        rl::cat::dispatch_bins<rl::cat::ProjectTarget>(bins, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
+                                                       rl::as_stream(stream), a, static_cast<const float*>(q),
+                                                       static_cast<const float*>(log_probs),
+                                                       static_cast<long long>(batch), static_cast<float*>(target),
+                                                       static_cast<float*>(maximum_entropy));
         rl::check_launch("Launch categorical target");
     });
 }

@@ -119,10 +119,31 @@ __device__ __forceinline__ float bf16_bits_to_f32(unsigned short bits) {
     return __uint_as_float(static_cast<unsigned int>(bits) << 16);
 }
 
+// DPP lane permutations within a row of 16 lanes (GCN/CDNA DPP16 controls).
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within each 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within each 16
+
+template <int Control>
+__device__ __forceinline__ float dpp(float value) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(value), Control, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float lane_value(float value, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(value), lane));
+}
+
+// Wave-wide sum, returned to every lane.  Four DPP butterfly steps (VALU, no
+// LDS round trips) leave each 16-lane row's sum in all of its lanes with
+// identical bits (every step adds the same two operands in either order); the
+// four row sums are then added in a fixed order.  Requires all 64 lanes active.
 __device__ __forceinline__ float wave_sum(float value) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) value += __shfl_xor(value, offset, kWave);
-    return value;
+    value += dpp<kDppXor1>(value);
+    value += dpp<kDppXor2>(value);
+    value += dpp<kDppHalfMirror>(value);
+    value += dpp<kDppMirror>(value);
+    return (lane_value(value, 0) + lane_value(value, 16)) + (lane_value(value, 32) + lane_value(value, 48));
 }
 
 __device__ __forceinline__ double wave_sum(double value) {
@@ -132,9 +153,11 @@ __device__ __forceinline__ double wave_sum(double value) {
 }
 
 __device__ __forceinline__ float wave_max(float value) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) value = fmaxf(value, __shfl_xor(value, offset, kWave));
-    return value;
+    value = fmaxf(value, dpp<kDppXor1>(value));
+    value = fmaxf(value, dpp<kDppXor2>(value));
+    value = fmaxf(value, dpp<kDppHalfMirror>(value));
+    value = fmaxf(value, dpp<kDppMirror>(value));
+    return fmaxf(fmaxf(lane_value(value, 0), lane_value(value, 16)), fmaxf(lane_value(value, 32), lane_value(value, 48)));
 }
 
 // Fixed-order block sum for blockDim.x == Threads; the result is broadcast.

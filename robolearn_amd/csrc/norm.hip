@@ -19,6 +19,7 @@
 #include "common.hpp"
 
 #include <cmath>
+#include <initializer_list>
 
 namespace rl {
 namespace norm {
@@ -279,22 +280,213 @@ __global__ void rms_dx(const float* x, const float* dy, const float* w, const fl
     }
 }
 
+// Register-cached RMSNorm rows for channels % 4 == 0 and channels <= 256 V:
+// lane l holds the float4 at columns 4 (l + 64 i), i < V, so each row is read
+// once and written once with 16-byte accesses.
+template <int V>
+__global__ __launch_bounds__(256) void rms_forward_vec(const float* x, const float* w, float* ms, float* y,
+                                                       unsigned short* y_bf16, long long rows, int channels,
+                                                       int ensemble, long long member_stride, float eps) {
+    const long long row = blockIdx.x * static_cast<long long>(blockDim.x / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (row >= rows * ensemble) return;
+    const int e = static_cast<int>(row / rows);
+    const long long base = e * member_stride + (row - e * rows) * channels;
+    float4 v[V];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = 4 * (lane + kWave * i);
+        v[i] = c < channels ? *reinterpret_cast<const float4*>(x + base + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        s += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+    }
+    s = wave_sum(s) / static_cast<float>(channels);
+    const float rs = 1.0f / sqrtf(s + eps);
+    if (lane == 0) ms[row] = s;
+    const float* we = w + static_cast<long long>(e) * channels;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = 4 * (lane + kWave * i);
+        if (c >= channels) continue;
+        const float4 g = *reinterpret_cast<const float4*>(we + c);
+        const float4 o = make_float4(v[i].x * rs * g.x, v[i].y * rs * g.y, v[i].z * rs * g.z, v[i].w * rs * g.w);
+        if (y) *reinterpret_cast<float4*>(y + base + c) = o;
+        if (y_bf16)
+            *reinterpret_cast<uint2*>(y_bf16 + base + c) = make_uint2(f32x2_to_bf16x2(o.x, o.y), f32x2_to_bf16x2(o.z, o.w));
+    }
+}
+
+// dx (+)= rs * (dy * w - x * rs^2 * mean(dy * w * x)), register-cached as above.
+template <int V>
+__global__ __launch_bounds__(256) void rms_dx_vec(const float* x, const float* dy, const float* w, const float* ms,
+                                                  float* dx, unsigned short* dx_bf16, long long rows, int channels,
+                                                  int ensemble, long long member_stride, float eps, int accumulate) {
+    const long long row = blockIdx.x * static_cast<long long>(blockDim.x / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (row >= rows * ensemble) return;
+    const int e = static_cast<int>(row / rows);
+    const long long base = e * member_stride + (row - e * rows) * channels;
+    const float* we = w + static_cast<long long>(e) * channels;
+    float4 xv[V], gw[V];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = 4 * (lane + kWave * i);
+        const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        xv[i] = c < channels ? *reinterpret_cast<const float4*>(x + base + c) : zero;
+        const float4 g = c < channels ? *reinterpret_cast<const float4*>(dy + base + c) : zero;
+        const float4 wv = c < channels ? *reinterpret_cast<const float4*>(we + c) : zero;
+        gw[i] = make_float4(g.x * wv.x, g.y * wv.y, g.z * wv.z, g.w * wv.w);
+        s += gw[i].x * xv[i].x + gw[i].y * xv[i].y + gw[i].z * xv[i].z + gw[i].w * xv[i].w;
+    }
+    s = wave_sum(s) / static_cast<float>(channels);
+    const float rs = 1.0f / sqrtf(ms[row] + eps);
+    const float k = rs * rs * s;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = 4 * (lane + kWave * i);
+        if (c >= channels) continue;
+        float4 o = make_float4(rs * (gw[i].x - xv[i].x * k), rs * (gw[i].y - xv[i].y * k),
+                               rs * (gw[i].z - xv[i].z * k), rs * (gw[i].w - xv[i].w * k));
+        if (accumulate) {
+            const float4 old = *reinterpret_cast<const float4*>(dx + base + c);
+            o = make_float4(o.x + old.x, o.y + old.y, o.z + old.z, o.w + old.w);
+        }
+        if (dx) *reinterpret_cast<float4*>(dx + base + c) = o;
+        if (dx_bf16)
+            *reinterpret_cast<uint2*>(dx_bf16 + base + c) = make_uint2(f32x2_to_bf16x2(o.x, o.y), f32x2_to_bf16x2(o.z, o.w));
+    }
+}
+
+// RMS backward in one pass over x and dy: dx as rms_dx_vec and the weight
+// gradient's per-chunk column partials sum_r dy x rsqrt(ms + eps) (the layout of
+// column_partials, reduced by column_reduce).  One workgroup per 256-row chunk
+// and member; 8 waves take rows wave, wave + 8, ... two at a time so two rows'
+// loads are in flight per wave; the waves' column sums are added in fixed order.
+constexpr int kFusedWaves = 8;
+template <int V>
+__global__ __launch_bounds__(kFusedWaves * kWave) void rms_backward_fused(const float* x, const float* dy,
+                                                                         const float* w, const float* ms,
+                                                                         float* partial, float* dx,
+                                                                         unsigned short* dx_bf16, int rows,
+                                                                         int channels, int chunks,
+                                                                         long long member_stride, float eps,
+                                                                         int accumulate) {
+    __shared__ float4 sums[kFusedWaves][V * kWave];
+    const int e = blockIdx.y;
+    const int chunk = blockIdx.x;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float* we = w + static_cast<long long>(e) * channels;
+    float4 wv[V], acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = 4 * (lane + kWave * i);
+        wv[i] = c < channels ? *reinterpret_cast<const float4*>(we + c) : zero;
+        acc[i] = zero;
+    }
+    const int r_end = min(rows, (chunk + 1) * kChunk);
+    for (int r0 = chunk * kChunk + wave; r0 < r_end; r0 += 2 * kFusedWaves) {
+        const int rr[2] = {r0, r0 + kFusedWaves};
+        float4 xv[2][V], gv[2][V];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const bool live = rr[q] < r_end;
+            const long long base = e * member_stride + static_cast<long long>(rr[q]) * channels;
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                const int c = 4 * (lane + kWave * i);
+                const bool ok = live && c < channels;
+                xv[q][i] = ok ? *reinterpret_cast<const float4*>(x + base + c) : zero;
+                gv[q][i] = ok ? *reinterpret_cast<const float4*>(dy + base + c) : zero;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            if (rr[q] >= r_end) break;  // uniform across the wave
+            const long long base = e * member_stride + static_cast<long long>(rr[q]) * channels;
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < V; ++i)
+                s += gv[q][i].x * wv[i].x * xv[q][i].x + gv[q][i].y * wv[i].y * xv[q][i].y +
+                     gv[q][i].z * wv[i].z * xv[q][i].z + gv[q][i].w * wv[i].w * xv[q][i].w;
+            s = wave_sum(s) / static_cast<float>(channels);
+            const float rs = 1.0f / sqrtf(ms[static_cast<long long>(e) * rows + rr[q]] + eps);
+            const float k = rs * rs * s;
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                const float4 g = gv[q][i], xi = xv[q][i];
+                acc[i].x += g.x * xi.x * rs;
+                acc[i].y += g.y * xi.y * rs;
+                acc[i].z += g.z * xi.z * rs;
+                acc[i].w += g.w * xi.w * rs;
+                const int c = 4 * (lane + kWave * i);
+                if (c >= channels || (!dx && !dx_bf16)) continue;
+                float4 o = make_float4(rs * (g.x * wv[i].x - xi.x * k), rs * (g.y * wv[i].y - xi.y * k),
+                                       rs * (g.z * wv[i].z - xi.z * k), rs * (g.w * wv[i].w - xi.w * k));
+                if (accumulate) {
+                    const float4 old = *reinterpret_cast<const float4*>(dx + base + c);
+                    o = make_float4(o.x + old.x, o.y + old.y, o.z + old.z, o.w + old.w);
+                }
+                if (dx) *reinterpret_cast<float4*>(dx + base + c) = o;
+                if (dx_bf16)
+                    *reinterpret_cast<uint2*>(dx_bf16 + base + c) =
+                        make_uint2(f32x2_to_bf16x2(o.x, o.y), f32x2_to_bf16x2(o.z, o.w));
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) sums[wave][lane + kWave * i] = acc[i];
+    __syncthreads();
+    float* out = partial + (static_cast<long long>(e) * chunks + chunk) * channels;
+    for (int q = threadIdx.x; q < V * kWave; q += kFusedWaves * kWave) {
+        const int c = 4 * q;
+        if (c >= channels) continue;
+        float4 t = sums[0][q];
+        for (int v = 1; v < kFusedWaves; ++v) {
+            const float4 u = sums[v][q];
+            t = make_float4(t.x + u.x, t.y + u.y, t.z + u.z, t.w + u.w);
+        }
+        *reinterpret_cast<float4*>(out + c) = t;
+    }
+}
+
+// Float4 vectors per lane for the register-cached RMS kernels, or 0 when the
+// layout does not allow them.
+inline int rms_vectors(int channels, long long member_stride, std::initializer_list<const void*> f32,
+                       std::initializer_list<const void*> b16) {
+    if (channels % 4 != 0 || member_stride % 4 != 0 || channels > 2048) return 0;
+    for (const void* q : f32)
+        if (q && !aligned(q, 16)) return 0;
+    for (const void* q : b16)
+        if (q && !aligned(q, 8)) return 0;
+    const int v = (channels + 255) / 256;
+    return v <= 1 ? 1 : v <= 2 ? 2 : v <= 4 ? 4 : 8;
+}
+
 // Column sums of up to two row-scaled products, per 256-row chunk:
 //   mode 0: sum dy                       (bias gradient)
 //   mode 1: sum dy * x * rsqrt(ms + eps) (RMS weight gradient)
+// Cols columns per workgroup and kThreads / Cols row groups, so narrow layers
+// (a value head, an action-sized bias) still spread a chunk over the whole
+// workgroup; the row groups are combined by a fixed-order tree.
+template <int Cols>
 __global__ __launch_bounds__(kThreads) void column_partials(const float* dy, const float* x, const float* ms,
                                                             float* partial, int rows, int channels, int chunks,
                                                             long long member_stride, float eps, int mode) {
+    constexpr int Groups = kThreads / Cols;
     const int e = blockIdx.z;
-    const int c = blockIdx.x * kCols + threadIdx.x % kCols;
-    const int group = threadIdx.x / kCols;
+    const int c = blockIdx.x * Cols + threadIdx.x % Cols;
+    const int group = threadIdx.x / Cols;
     const int chunk = blockIdx.y;
     const int r0 = chunk * kChunk;
     const int r1 = min(rows, r0 + kChunk);
     const long long off = static_cast<long long>(e) * member_stride;
     float s = 0.0f;
     if (c < channels) {
-        for (int r = r0 + group; r < r1; r += kRowGroups) {
+#pragma unroll 4
+        for (int r = r0 + group; r < r1; r += Groups) {
             const long long i = off + static_cast<long long>(r) * channels + c;
             if (mode == 0) s += dy[i];
             else s += dy[i] * x[i] * (1.0f / sqrtf(ms[static_cast<long long>(e) * rows + r] + eps));
@@ -303,20 +495,58 @@ __global__ __launch_bounds__(kThreads) void column_partials(const float* dy, con
     __shared__ float a[kThreads];
     a[threadIdx.x] = s;
     __syncthreads();
-    if (group == 0 && c < channels) {
-        for (int g = 1; g < kRowGroups; ++g) s += a[g * kCols + threadIdx.x];
-        partial[(static_cast<long long>(e) * chunks + chunk) * channels + c] = s;
+#pragma unroll
+    for (int stride = Groups / 2; stride > 0; stride >>= 1) {
+        if (group < stride) a[threadIdx.x] += a[threadIdx.x + stride * Cols];
+        __syncthreads();
     }
+    if (group == 0 && c < channels) partial[(static_cast<long long>(e) * chunks + chunk) * channels + c] = a[threadIdx.x];
 }
 
-__global__ void column_reduce(const float* partial, float* out, int channels, int chunks, int ensemble, int accumulate) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= ensemble * channels) return;
-    const int e = idx / channels;
-    const int c = idx % channels;
+// One wave per output column: lanes stride over the chunk partials, then a
+// fixed-order wave reduction.
+constexpr int kReduceWaves = kThreads / kWave;
+__global__ __launch_bounds__(kThreads) void column_reduce(const float* partial, float* out, int channels, int chunks,
+                                                          int ensemble, int accumulate) {
+    const long long idx = static_cast<long long>(blockIdx.x) * kReduceWaves + threadIdx.x / kWave;
+    if (idx >= static_cast<long long>(ensemble) * channels) return;  // uniform across the wave
+    const int lane = threadIdx.x % kWave;
+    const long long e = idx / channels;
+    const long long c = idx % channels;
     float s = 0.0f;
-    for (int k = 0; k < chunks; ++k) s += partial[(static_cast<long long>(e) * chunks + k) * channels + c];
-    out[idx] = (accumulate ? out[idx] : 0.0f) + s;
+    for (int k = lane; k < chunks; k += kWave) s += partial[(e * chunks + k) * channels + c];
+    s = wave_sum(s);
+    if (lane == 0) out[idx] = (accumulate ? out[idx] : 0.0f) + s;
+}
+
+// Column partials + reduction over a [ensemble][rows][channels] operand.
+inline void column_sums(const float* dy, const float* x, const float* ms, float* partial, float* out, int rows,
+                        int channels, int ensemble, long long member_stride, float eps, int mode, int accumulate,
+                        hipStream_t stream) {
+    const int chunks = (rows + kChunk - 1) / kChunk;
+    const int cols = channels >= 64 ? 64 : channels >= 16 ? 16 : channels >= 4 ? 4 : 1;
+    const dim3 grid(ceil_div(channels, cols), chunks, ensemble);
+    switch (cols) {
+        case 64:
+            hipLaunchKernelGGL(column_partials<64>, grid, dim3(kThreads), 0, stream, dy, x, ms, partial, rows, channels,
+                               chunks, member_stride, eps, mode);
+            break;
+        case 16:
+            hipLaunchKernelGGL(column_partials<16>, grid, dim3(kThreads), 0, stream, dy, x, ms, partial, rows, channels,
+                               chunks, member_stride, eps, mode);
+            break;
+        case 4:
+            hipLaunchKernelGGL(column_partials<4>, grid, dim3(kThreads), 0, stream, dy, x, ms, partial, rows, channels,
+                               chunks, member_stride, eps, mode);
+            break;
+        default:
+            hipLaunchKernelGGL(column_partials<1>, grid, dim3(kThreads), 0, stream, dy, x, ms, partial, rows, channels,
+                               chunks, member_stride, eps, mode);
+    }
+    check_launch("Launch column partials");
+    hipLaunchKernelGGL(column_reduce, dim3(ceil_div(static_cast<long long>(ensemble) * channels, kReduceWaves)),
+                       dim3(kThreads), 0, stream, partial, out, channels, chunks, ensemble, accumulate);
+    check_launch("Launch column reduce");
 }
 
 inline unsigned elementwise_blocks(long long total) {
@@ -396,8 +626,15 @@ void rms_forward(int ensemble, const float* x, const float* w, float* ms, float*
     require(x && w && ms && (y || y_bf16), "RMSNorm forward requires x, weight, ms and an output.");
     const long long total_rows = static_cast<long long>(rows) * ensemble;
     if (member_stride <= 0) member_stride = static_cast<long long>(rows) * channels;
-    hipLaunchKernelGGL(norm::rms_forward, dim3(ceil_div(total_rows, 4)), dim3(256), 0, stream, x, w, ms, y, y_bf16,
-                       static_cast<long long>(rows), channels, ensemble, member_stride, eps);
+    const dim3 grid(ceil_div(total_rows, 4));
+    const long long r = rows;
+    switch (norm::rms_vectors(channels, member_stride, {x, w, y}, {y_bf16})) {
+        case 1: hipLaunchKernelGGL(norm::rms_forward_vec<1>, grid, dim3(256), 0, stream, x, w, ms, y, y_bf16, r, channels, ensemble, member_stride, eps); break;
+        case 2: hipLaunchKernelGGL(norm::rms_forward_vec<2>, grid, dim3(256), 0, stream, x, w, ms, y, y_bf16, r, channels, ensemble, member_stride, eps); break;
+        case 4: hipLaunchKernelGGL(norm::rms_forward_vec<4>, grid, dim3(256), 0, stream, x, w, ms, y, y_bf16, r, channels, ensemble, member_stride, eps); break;
+        case 8: hipLaunchKernelGGL(norm::rms_forward_vec<8>, grid, dim3(256), 0, stream, x, w, ms, y, y_bf16, r, channels, ensemble, member_stride, eps); break;
+        default: hipLaunchKernelGGL(norm::rms_forward, grid, dim3(256), 0, stream, x, w, ms, y, y_bf16, r, channels, ensemble, member_stride, eps);
+    }
     check_launch("Launch RMS forward");
 }
 
@@ -407,23 +644,44 @@ void rms_backward(int ensemble, const float* x, const float* dy, const float* w,
     require(ensemble > 0 && rows > 0 && channels > 0, "RMSNorm dimensions must be positive.");
     require(x && dy && w && ms, "RMSNorm backward requires x, dy, weight and ms.");
     if (member_stride <= 0) member_stride = static_cast<long long>(rows) * channels;
+    const int vectors = norm::rms_vectors(channels, member_stride, {x, dy, w, dx, partial}, {dx_bf16});
+    // The one-pass kernel runs one workgroup per 256-row chunk; below a
+    // workgroup per CU (256 on MI355X) the row-parallel two-kernel path is faster.
+    if (dw && vectors && static_cast<long long>(chunks_for(rows)) * ensemble >= 256) {
+        // one pass: dx and the weight-gradient partials together
+        require(partial, "RMS weight gradient requires partial scratch.");
+        require(!accumulate_dx || dx, "Accumulating RMS input adjoints requires the fp32 adjoint.");
+        const int chunks = chunks_for(rows);
+        const dim3 grid(chunks, ensemble);
+        const dim3 block(norm::kFusedWaves * kWave);
+        switch (vectors) {
+            case 1: hipLaunchKernelGGL(norm::rms_backward_fused<1>, grid, block, 0, stream, x, dy, w, ms, partial, dx, dx_bf16, rows, channels, chunks, member_stride, eps, accumulate_dx); break;
+            case 2: hipLaunchKernelGGL(norm::rms_backward_fused<2>, grid, block, 0, stream, x, dy, w, ms, partial, dx, dx_bf16, rows, channels, chunks, member_stride, eps, accumulate_dx); break;
+            case 4: hipLaunchKernelGGL(norm::rms_backward_fused<4>, grid, block, 0, stream, x, dy, w, ms, partial, dx, dx_bf16, rows, channels, chunks, member_stride, eps, accumulate_dx); break;
+            default: hipLaunchKernelGGL(norm::rms_backward_fused<8>, grid, block, 0, stream, x, dy, w, ms, partial, dx, dx_bf16, rows, channels, chunks, member_stride, eps, accumulate_dx);
+        }
+        check_launch("Launch fused RMS backward");
+        hipLaunchKernelGGL(norm::column_reduce, dim3(ceil_div(static_cast<long long>(ensemble) * channels, norm::kReduceWaves)),
+                           dim3(norm::kThreads), 0, stream, partial, dw, channels, chunks, ensemble, accumulate_dw);
+        check_launch("Launch RMS weight reduce");
+        return;
+    }
     if (dw) {
         require(partial, "RMS weight gradient requires partial scratch.");
-        const int chunks = chunks_for(rows);
-        const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
-        hipLaunchKernelGGL(norm::column_partials, grid, dim3(norm::kThreads), 0, stream, dy, x, ms, partial, rows,
-                           channels, chunks, member_stride, eps, 1);
-        check_launch("Launch RMS weight partials");
-        hipLaunchKernelGGL(norm::column_reduce, dim3(ceil_div(ensemble * channels, 256)), dim3(256), 0, stream,
-                           partial, dw, channels, chunks, ensemble, accumulate_dw);
-        check_launch("Launch RMS weight reduce");
+        norm::column_sums(dy, x, ms, partial, dw, rows, channels, ensemble, member_stride, eps, 1, accumulate_dw, stream);
     }
     if (dx || dx_bf16) {
         require(!accumulate_dx || dx, "Accumulating RMS input adjoints requires the fp32 adjoint.");
         const long long total_rows = static_cast<long long>(rows) * ensemble;
-        hipLaunchKernelGGL(norm::rms_dx, dim3(ceil_div(total_rows, 4)), dim3(256), 0, stream, x, dy, w, ms, dx,
-                           dx_bf16, static_cast<long long>(rows), channels, ensemble, member_stride, eps,
-                           accumulate_dx);
+        const dim3 grid(ceil_div(total_rows, 4));
+        const long long r = rows;
+        switch (norm::rms_vectors(channels, member_stride, {x, dy, w, dx}, {dx_bf16})) {
+            case 1: hipLaunchKernelGGL(norm::rms_dx_vec<1>, grid, dim3(256), 0, stream, x, dy, w, ms, dx, dx_bf16, r, channels, ensemble, member_stride, eps, accumulate_dx); break;
+            case 2: hipLaunchKernelGGL(norm::rms_dx_vec<2>, grid, dim3(256), 0, stream, x, dy, w, ms, dx, dx_bf16, r, channels, ensemble, member_stride, eps, accumulate_dx); break;
+            case 4: hipLaunchKernelGGL(norm::rms_dx_vec<4>, grid, dim3(256), 0, stream, x, dy, w, ms, dx, dx_bf16, r, channels, ensemble, member_stride, eps, accumulate_dx); break;
+            case 8: hipLaunchKernelGGL(norm::rms_dx_vec<8>, grid, dim3(256), 0, stream, x, dy, w, ms, dx, dx_bf16, r, channels, ensemble, member_stride, eps, accumulate_dx); break;
+            default: hipLaunchKernelGGL(norm::rms_dx, grid, dim3(256), 0, stream, x, dy, w, ms, dx, dx_bf16, r, channels, ensemble, member_stride, eps, accumulate_dx);
+        }
         check_launch("Launch RMS input gradient");
     }
 }
@@ -432,14 +690,8 @@ void bias_grad(int ensemble, const float* dy, float* db, float* partial, int row
                hipStream_t stream) {
     require(ensemble > 0 && rows > 0 && channels > 0, "Bias gradient dimensions must be positive.");
     require(dy && db && partial, "Bias gradient requires dy, db and partial scratch.");
-    const int chunks = chunks_for(rows);
-    const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
-    hipLaunchKernelGGL(norm::column_partials, grid, dim3(norm::kThreads), 0, stream, dy, nullptr, nullptr, partial,
-                       rows, channels, chunks, static_cast<long long>(rows) * channels, 0.0f, 0);
-    check_launch("Launch bias gradient partials");
-    hipLaunchKernelGGL(norm::column_reduce, dim3(ceil_div(ensemble * channels, 256)), dim3(256), 0, stream, partial,
-                       db, channels, chunks, ensemble, accumulate);
-    check_launch("Launch bias gradient reduce");
+    norm::column_sums(dy, nullptr, nullptr, partial, db, rows, channels, ensemble, static_cast<long long>(rows) * channels,
+                      0.0f, 0, accumulate, stream);
 }
 
 }  // namespace rl

@@ -166,29 +166,59 @@ __global__ void gather_kernel(GatherArgs a) {
     }
 }
 
-// KL(N_old || N_new) per row, then a single-workgroup fixed-order mean and
-// the adaptive learning-rate rule.  std_type 0: std = exp(p), 1: clamp(p).
-__global__ __launch_bounds__(kThreads) void kl_adapt_kernel(const float* mean, long long ld_mean, const float* std_param,
-                                                            const float* old_mean, const float* old_std, long long rows,
-                                                            int action_dim, int std_type, float std_min, float std_max,
-                                                            float desired_kl, int adapt, float* kl_out, float* lr) {
-    __shared__ float s[kThreads];
-    float total = 0.0f;
-    for (long long i = threadIdx.x; i < rows; i += kThreads) {
-        float value = 0.0f;
-        for (int j = 0; j < action_dim; ++j) {
-            const float p = std_param[j];
-            const float std = std_type == 1 ? fminf(fmaxf(p, std_min), std_max) : expf(p);
-            const float ratio = old_std[i * action_dim + j] / std;
-            const float delta = (old_mean[i * action_dim + j] - mean[i * ld_mean + j]) / std;
-            value = value + 0.5f * (ratio * ratio + delta * delta - 1.0f);
-            value = value - logf(ratio);
+// Row-parallel passes over the minibatch: one wave per row (lanes over the
+// action dimensions), kRowsPerBlock rows per workgroup, per-workgroup sums in
+// fixed order, then one finishing workgroup that adds the partials in fixed
+// order.  No atomics, so captured replays are bitwise repeatable.
+constexpr int kRowThreads = 256;
+constexpr int kRowWaves = kRowThreads / kWave;
+constexpr int kRowsPerBlock = 16;
+
+__device__ __forceinline__ float std_of(float p, int std_type, float std_min, float std_max) {
+    return std_type == 1 ? fminf(fmaxf(p, std_min), std_max) : expf(p);
+}
+
+// Sum over the block's rows of KL(N_old || N_new) = sum_j log(s/s0) + (s0^2 + (m0 - m)^2) / (2 s^2) - 1/2.
+__global__ __launch_bounds__(kRowThreads) void kl_partials(const float* mean, long long ld_mean,
+                                                           const float* std_param, const float* old_mean,
+                                                           const float* old_std, long long rows, int action_dim,
+                                                           int std_type, float std_min, float std_max,
+                                                           float* partial) {
+    __shared__ float waves[kRowWaves];
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    float v = 0.0f;
+    for (int r = wave; r < kRowsPerBlock; r += kRowWaves) {
+        const long long row = blockIdx.x * static_cast<long long>(kRowsPerBlock) + r;
+        if (row >= rows) break;
+        for (int j = lane; j < action_dim; j += kWave) {
+            const float std = std_of(std_param[j], std_type, std_min, std_max);
+            const float ratio = old_std[row * action_dim + j] / std;
+            const float delta = (old_mean[row * action_dim + j] - mean[row * ld_mean + j]) / std;
+            v += 0.5f * (ratio * ratio + delta * delta - 1.0f) - logf(ratio);
         }
-        total += value;
     }
-    total = block_sum(total, s);
+    v = wave_sum(v);
+    if (lane == 0) waves[wave] = v;
+    __syncthreads();
     if (threadIdx.x == 0) {
-        const float kl = total / static_cast<float>(rows);
+        float total = 0.0f;
+        for (int w = 0; w < kRowWaves; ++w) total += waves[w];
+        partial[blockIdx.x] = total;
+    }
+}
+
+// Mean KL over the minibatch and the adaptive learning-rate rule
+// (robolearn/warp/ppo.py:233-238): lr / 1.5 (>= 1e-5) above 2 x target,
+// lr x 1.5 (<= 1e-2) for 0 < KL < target / 2.
+__global__ __launch_bounds__(kThreads) void kl_finish(const float* partial, int blocks, long long rows,
+                                                      float desired_kl, int adapt, float* kl_out, float* lr) {
+    __shared__ float s[kThreads];
+    float v = 0.0f;
+    for (int i = threadIdx.x; i < blocks; i += kThreads) v += partial[i];
+    v = block_sum(v, s);
+    if (threadIdx.x == 0) {
+        const float kl = v / static_cast<float>(rows);
         kl_out[0] = kl;
         if (adapt) {
             if (kl > desired_kl * 2.0f) lr[0] = fmaxf(1.0e-5f, lr[0] / 1.5f);
@@ -216,76 +246,96 @@ struct LossArgs {
     float* dmean;             // [rows, A]
     float* dvalue;            // [rows]
     float* dstd_rows;         // [rows, A] per-row std-parameter gradient
-    float* row_terms;         // [4, rows]: total, policy, value, entropy (already scaled by 1/rows)
+    float* partial;           // [4, blocks]: total, policy, value, entropy sums (already scaled by 1/rows)
 };
 
-__global__ void loss_kernel(LossArgs a) {
-    const long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
-    if (i >= a.rows) return;
+// Clipped surrogate, clipped value and entropy terms of one row and their
+// gradients with respect to the mean, the value and the std parameter.
+__global__ __launch_bounds__(kRowThreads) void loss_kernel(LossArgs a) {
+    __shared__ float waves[4][kRowWaves];
     const float ln_two_pi = 1.8378770664093453f;
     const float entropy_const = 1.4189385332046727f;
     const float scale = 1.0f / static_cast<float>(a.rows);
-    float log_prob = 0.0f;
-    float entropy = 0.0f;
-    for (int j = 0; j < a.action_dim; ++j) {
-        const float p = a.std_param[j];
-        const float ls = a.std_type == 1 ? logf(fminf(fmaxf(p, a.std_min), a.std_max)) : p;
-        const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * expf(-ls);
-        log_prob = log_prob - 0.5f * (residual * residual + 2.0f * ls + ln_two_pi);
-        entropy = entropy + ls + entropy_const;
-    }
-    const float ratio = expf(log_prob - a.old_log_probs[i]);
-    const float adv = a.advantages[i];
     const float lo = 1.0f - a.clip_ratio, hi = 1.0f + a.clip_ratio;
-    const float clipped_ratio = fminf(fmaxf(ratio, lo), hi);
-    const float unclipped = ratio * adv;
-    const float clipped = clipped_ratio * adv;
-    const float policy_loss = -fminf(unclipped, clipped);
-    // d policy / d ratio: the smaller branch carries the gradient; on a tie
-    // inside the clip range both branches have derivative -adv.
-    float dratio;
-    if (unclipped <= clipped) dratio = -adv;
-    else dratio = (ratio > lo && ratio < hi) ? -adv : 0.0f;
-    const float v = a.value[i];
-    const float error = v - a.returns[i];
-    float value_loss = error * error;
-    float dv = 2.0f * error;
-    if (a.clip_value) {
-        const float d = v - a.old_values[i];
-        const float cv = a.old_values[i] + fminf(fmaxf(d, -a.clip_ratio), a.clip_ratio);
-        const float ce = cv - a.returns[i];
-        if (ce * ce > value_loss) {
-            value_loss = ce * ce;
-            dv = (d >= -a.clip_ratio && d <= a.clip_ratio) ? 2.0f * ce : 0.0f;
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    float sums[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int r = wave; r < kRowsPerBlock; r += kRowWaves) {
+        const long long i = blockIdx.x * static_cast<long long>(kRowsPerBlock) + r;
+        if (i >= a.rows) break;
+        float log_prob = 0.0f, entropy = 0.0f;
+        for (int j = lane; j < a.action_dim; j += kWave) {
+            const float p = a.std_param[j];
+            const float ls = a.std_type == 1 ? logf(fminf(fmaxf(p, a.std_min), a.std_max)) : p;
+            const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * expf(-ls);
+            log_prob -= 0.5f * (residual * residual + 2.0f * ls + ln_two_pi);
+            entropy += ls + entropy_const;
         }
-    }
-    value_loss = a.value_loss_scale * value_loss;
-    dv *= a.value_loss_scale;
-    a.dvalue[i] = scale * a.value_coefficient * dv;
-    const float dlp = scale * dratio * ratio;
-    for (int j = 0; j < a.action_dim; ++j) {
-        const float p = a.std_param[j];
-        float ls, dls_dp;
-        if (a.std_type == 1) {
-            const float c = fminf(fmaxf(p, a.std_min), a.std_max);
-            ls = logf(c);
-            dls_dp = (p >= a.std_min && p <= a.std_max) ? 1.0f / c : 0.0f;
-        } else {
-            ls = p;
-            dls_dp = 1.0f;
+        log_prob = wave_sum(log_prob);
+        entropy = wave_sum(entropy);
+        const float ratio = expf(log_prob - a.old_log_probs[i]);
+        const float adv = a.advantages[i];
+        const float clipped_ratio = fminf(fmaxf(ratio, lo), hi);
+        const float unclipped = ratio * adv;
+        const float clipped = clipped_ratio * adv;
+        const float policy_loss = -fminf(unclipped, clipped);
+        // d policy / d ratio: the smaller branch carries the gradient; on a tie
+        // inside the clip range both branches have derivative -adv.
+        float dratio;
+        if (unclipped <= clipped) dratio = -adv;
+        else dratio = (ratio > lo && ratio < hi) ? -adv : 0.0f;
+        const float v = a.value[i];
+        const float error = v - a.returns[i];
+        float value_loss = error * error;
+        float dv = 2.0f * error;
+        if (a.clip_value) {
+            const float d = v - a.old_values[i];
+            const float cv = a.old_values[i] + fminf(fmaxf(d, -a.clip_ratio), a.clip_ratio);
+            const float ce = cv - a.returns[i];
+            if (ce * ce > value_loss) {
+                value_loss = ce * ce;
+                dv = (d >= -a.clip_ratio && d <= a.clip_ratio) ? 2.0f * ce : 0.0f;
+            }
         }
-        const float inv_std = expf(-ls);
-        const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * inv_std;
-        a.dmean[i * a.action_dim + j] = dlp * residual * inv_std;
-        a.dstd_rows[i * a.action_dim + j] = (dlp * (residual * residual - 1.0f) - scale * a.entropy_coefficient) * dls_dp;
+        value_loss = a.value_loss_scale * value_loss;
+        dv *= a.value_loss_scale;
+        if (lane == 0) a.dvalue[i] = scale * a.value_coefficient * dv;
+        const float dlp = scale * dratio * ratio;
+        for (int j = lane; j < a.action_dim; j += kWave) {
+            const float p = a.std_param[j];
+            float ls, dls_dp;
+            if (a.std_type == 1) {
+                const float c = fminf(fmaxf(p, a.std_min), a.std_max);
+                ls = logf(c);
+                dls_dp = (p >= a.std_min && p <= a.std_max) ? 1.0f / c : 0.0f;
+            } else {
+                ls = p;
+                dls_dp = 1.0f;
+            }
+            const float inv_std = expf(-ls);
+            const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * inv_std;
+            a.dmean[i * a.action_dim + j] = dlp * residual * inv_std;
+            a.dstd_rows[i * a.action_dim + j] =
+                (dlp * (residual * residual - 1.0f) - scale * a.entropy_coefficient) * dls_dp;
+        }
+        sums[0] += scale * (policy_loss + a.value_coefficient * value_loss - a.entropy_coefficient * entropy);
+        sums[1] += scale * policy_loss;
+        sums[2] += scale * value_loss;
+        sums[3] += scale * entropy;
     }
-    a.row_terms[i] = scale * (policy_loss + a.value_coefficient * value_loss - a.entropy_coefficient * entropy);
-    a.row_terms[a.rows + i] = scale * policy_loss;
-    a.row_terms[2 * a.rows + i] = scale * value_loss;
-    a.row_terms[3 * a.rows + i] = scale * entropy;
+    if (lane == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) waves[q][wave] = sums[q];
+    }
+    __syncthreads();
+    if (threadIdx.x < 4) {
+        float total = 0.0f;
+        for (int w = 0; w < kRowWaves; ++w) total += waves[threadIdx.x][w];
+        a.partial[threadIdx.x * static_cast<long long>(gridDim.x) + blockIdx.x] = total;
+    }
 }
 
-// Sum of four row vectors in fixed order: out[q] = sum_i terms[q, i].
+// out[q] = sum_b partial[q, b] in fixed order, for q < count.
 __global__ __launch_bounds__(kThreads) void sum_rows_kernel(const float* terms, long long rows, int count, float* out) {
     __shared__ float s[kThreads];
     for (int q = 0; q < count; ++q) {
@@ -405,13 +455,21 @@ RL_API int rl_ppo_gather(const int* indices, long long offset, long long rows, i
 
 RL_API int rl_ppo_kl_adapt(const float* mean, long long ld_mean, const float* std_param, const float* old_mean,
                            const float* old_std, long long rows, int action_dim, int std_type, float std_min,
-                           float std_max, float desired_kl, int adapt, float* kl_out, float* lr, void* stream) noexcept {
+                           float std_max, float desired_kl, int adapt, float* partial, float* kl_out, float* lr,
+                           void* stream) noexcept {
     return rl::guarded("rl_ppo_kl_adapt", [&] {
-        rl::require(mean && std_param && old_mean && old_std && kl_out && (!adapt || lr) && rows > 0 && action_dim > 0,
-                    "KL needs means, std parameters and outputs.");
-        hipLaunchKernelGGL(Q::kl_adapt_kernel, dim3(1), dim3(Q::kThreads), 0, rl::as_stream(stream), mean, ld_mean,
-                           std_param, old_mean, old_std, rows, action_dim, std_type, std_min, std_max, desired_kl,
-                           adapt, kl_out, lr);
+        rl::require(mean && std_param && old_mean && old_std && partial && kl_out && (!adapt || lr) && rows > 0 &&
+                        action_dim > 0,
+                    "KL needs means, std parameters, partial scratch and outputs.");
+        const long long blocks = (rows + Q::kRowsPerBlock - 1) / Q::kRowsPerBlock;
+        rl::require(blocks <= (1LL << 30), "KL row count is too large.");
+        const hipStream_t st = rl::as_stream(stream);
+        hipLaunchKernelGGL(Q::kl_partials, dim3(static_cast<unsigned>(blocks)), dim3(Q::kRowThreads), 0, st, mean,
+                           ld_mean, std_param, old_mean, old_std, rows, action_dim, std_type, std_min, std_max,
+                           partial);
+        rl::check_launch("Launch KL partials");
+        hipLaunchKernelGGL(Q::kl_finish, dim3(1), dim3(Q::kThreads), 0, st, partial, static_cast<int>(blocks), rows,
+                           desired_kl, adapt, kl_out, lr);
         rl::check_launch("Launch KL adapt");
     });
 }
@@ -426,13 +484,15 @@ RL_API int rl_ppo_loss(const float* mean, long long ld_mean, const float* value,
         rl::require(mean && value && std_param && actions && old_log_probs && old_values && advantages && returns &&
                         dmean && dvalue && dstd_rows && row_terms && totals && rows > 0 && action_dim > 0,
                     "PPO loss needs every input and output buffer.");
+        const long long blocks = (rows + Q::kRowsPerBlock - 1) / Q::kRowsPerBlock;
+        rl::require(blocks <= (1LL << 30), "PPO loss row count is too large.");
         Q::LossArgs a{mean, ld_mean, value, std_param, actions, old_log_probs, old_values, advantages, returns, rows,
                       action_dim, std_type, std_min, std_max, clip_ratio, value_coefficient, entropy_coefficient,
                       value_loss_scale, clip_value, dmean, dvalue, dstd_rows, row_terms};
         const hipStream_t st = rl::as_stream(stream);
-        hipLaunchKernelGGL(Q::loss_kernel, dim3(rl::ceil_div(rows, 256)), dim3(256), 0, st, a);
+        hipLaunchKernelGGL(Q::loss_kernel, dim3(static_cast<unsigned>(blocks)), dim3(Q::kRowThreads), 0, st, a);
         rl::check_launch("Launch PPO loss");
-        hipLaunchKernelGGL(Q::sum_rows_kernel, dim3(1), dim3(Q::kThreads), 0, st, row_terms, rows, 4, totals);
+        hipLaunchKernelGGL(Q::sum_rows_kernel, dim3(1), dim3(Q::kThreads), 0, st, row_terms, blocks, 4, totals);
         rl::check_launch("Launch PPO loss reduction");
     });
 }

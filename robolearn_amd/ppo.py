@@ -126,7 +126,7 @@ class WarpPPO:
             self.loss = self.totals[:1]
             self.kl = z(1)
             max_width = max(A, 1, *cfg.hidden_dims)
-            self.partial = z(K.chunks(M) * max_width)
+            self.partial = z(max(K.chunks(M) * max_width, (M + 15) // 16))  # column / KL partial sums
             self.norm_partial = z((self.store.size + 4095) // 4096 + 1)
             self.group_norms = [z(1) for _ in self.group_ranges]
             self.workspace = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
@@ -213,7 +213,7 @@ class WarpPPO:
         _native.call("rl_ppo_kl_adapt", self.mean.data_ptr(), A, self.distribution_parameter.data_ptr(),
                      self.b_means.data_ptr(), self.b_stds.data_ptr(), M, A, std_type, float(cfg.std_range[0]),
                      float(cfg.std_range[1]), float(cfg.desired_kl), int(cfg.schedule == "adaptive"),
-                     self.kl.data_ptr(), self.lr.data_ptr(), K.stream())
+                     self.partial.data_ptr(), self.kl.data_ptr(), self.lr.data_ptr(), K.stream())
         self._mlp_forward("critic", self.b_obs, M, self.critic_h, self.value)
         _native.call("rl_ppo_loss", self.mean.data_ptr(), A, self.value.data_ptr(),
                      self.distribution_parameter.data_ptr(), self.b_actions.data_ptr(), self.b_log_probs.data_ptr(),

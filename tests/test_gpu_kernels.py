@@ -124,8 +124,13 @@ def test_batchnorm_forward_backward_match_autograd(gpu, ensemble, rows, channels
     torch.testing.assert_close(y2.cpu().double(), ref2, rtol=1e-5, atol=1e-5)
 
 
-def test_rmsnorm_and_bias_grad(gpu):
-    ensemble, rows, channels = 2, 333, 96
+# channel counts cover the register-cached float4 paths (96, 300, 1024), the
+# scalar fallback (6, 37) and the narrow column-sum layouts (1, 3, 6, 37); the
+# last two shapes have >= 256 row chunks and take the one-pass backward kernel
+@pytest.mark.parametrize("ensemble,rows,channels", [(2, 333, 96), (1, 1000, 1024), (2, 257, 300), (1, 600, 37),
+                                                    (2, 513, 6), (1, 700, 3), (1, 2049, 1), (1, 65536, 8),
+                                                    (2, 32769, 12)])
+def test_rmsnorm_and_bias_grad(gpu, ensemble, rows, channels):
     x = _rand(ensemble, rows, channels, seed=20)
     w = _rand(ensemble, channels, seed=21).abs() + 0.5
     dy = _rand(ensemble, rows, channels, seed=22)
@@ -139,6 +144,11 @@ def test_rmsnorm_and_bias_grad(gpu):
     torch.testing.assert_close(y.cpu().double(), out.detach(), rtol=1e-5, atol=1e-5)
     out.backward(dy.double())
     partial = torch.empty(ensemble * K.chunks(rows) * channels, device=gpu)
+    # accumulate into a nonzero dx to cover the accumulate flag as well
+    dx_acc = torch.full_like(xd, 0.25)
+    K.rms_backward(xd, dyd, wd, ms, partial, dx_acc, None, rows=rows, channels=channels, ensemble=ensemble,
+                   accumulate_dx=True)
+    torch.testing.assert_close(dx_acc.cpu().double(), xr.grad + 0.25, rtol=1e-4, atol=1e-5)
     dx = torch.empty_like(xd)
     dw = torch.empty(ensemble, channels, device=gpu)
     K.rms_backward(xd, dyd, wd, ms, partial, dx, dw, rows=rows, channels=channels, ensemble=ensemble)
@@ -147,3 +157,50 @@ def test_rmsnorm_and_bias_grad(gpu):
     db = torch.empty(ensemble, channels, device=gpu)
     K.bias_grad(dyd, db, partial, rows=rows, channels=channels, ensemble=ensemble)
     torch.testing.assert_close(db.cpu().double(), dy.double().sum(1), rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("bins", [21, 101, 160, 300])
+def test_td_cross_entropy_matches_oracle_projection(gpu, bins):
+    """Fused min-Q target, two-hot projection, CE and d-logits against the oracle's
+    categorical_td_target (robolearn/flashsac/updates.py:19-80, 254-257).  Rows mix
+    terminal transitions, clamped returns, zero and negative discounts (the latter
+    take the scan path of the projection)."""
+    from oracle import flashsac as O
+
+    B, min_v, max_v = 300, -10.0, 10.0
+    g = torch.Generator().manual_seed(bins)
+    target_logits = torch.randn(2, B, bins, generator=g)
+    online_logits = torch.randn(2, B, bins, generator=g)
+    reward = torch.randn(B, generator=g) * 4.0
+    reward[:10] = 40.0
+    reward[10:20] = -40.0
+    terminated = (torch.rand(B, generator=g) < 0.1).float()
+    discount = torch.full((B,), 0.99)
+    discount[20:30] = 0.0
+    discount[30:40] = -0.5
+    next_log_probs = torch.randn(B, generator=g)
+    alpha = torch.tensor([0.2])
+    support = torch.linspace(min_v, max_v, bins)
+    d = {k: v.to(gpu).contiguous() for k, v in dict(tl=target_logits, ol=online_logits, r=reward, t=terminated,
+                                                     disc=discount, nlp=next_log_probs, a=alpha, z=support).items()}
+    dlogits = torch.empty(2, B, bins, device=gpu)
+    loss_rows, entropy_rows = torch.empty(2, B, device=gpu), torch.empty(B, device=gpu)
+    target_out, q_next = torch.empty(B, bins, device=gpu), torch.empty(2, B, device=gpu)
+    scale = 1.0 / (2 * B)
+    K.td_cross_entropy(d["tl"], None, B, d["ol"], None, B, d["z"], d["r"], d["t"], d["disc"], d["nlp"], d["a"],
+                       min_v=min_v, max_v=max_v, batch=B, bins=bins, scale=scale, dlogits=dlogits,
+                       loss_rows=loss_rows, entropy_rows=entropy_rows, target_out=target_out, q_next=q_next)
+    torch.cuda.synchronize()
+    lp_target = torch.log_softmax(target_logits, -1)
+    q = (lp_target.exp() * support).sum(-1)
+    selected = O.select_min_q_log_probs(q, lp_target)
+    entropy = alpha * next_log_probs
+    expected = O.categorical_td_target(selected, reward, terminated, entropy, discount, bins, min_v, max_v)
+    torch.testing.assert_close(q_next.cpu(), q, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(target_out.cpu(), expected, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(target_out.cpu().sum(-1), torch.ones(B), rtol=0, atol=1e-5)
+    lp_online = torch.log_softmax(online_logits, -1)
+    torch.testing.assert_close(loss_rows.cpu(), -(expected[None] * lp_online).sum(-1), rtol=1e-5, atol=1e-5)
+    grad = scale * (lp_online.exp() * expected.sum(-1, keepdim=True)[None] - expected[None])
+    torch.testing.assert_close(dlogits.cpu(), grad, rtol=1e-4, atol=1e-7)
+    torch.testing.assert_close(entropy_rows.cpu(), entropy, rtol=1e-6, atol=0)
