@@ -469,10 +469,13 @@ def main() -> int:
     peak = BF16_PEAK_TFLOPS if agent.mode == K.BF16 else FP32_PEAK_TFLOPS
     achieved = kernel_flops / (kernel_ms * 1e-3) / 1e12
     operand = "unsigned short" if agent.mode == K.BF16 else "float"
-    kernel_name = (f"gemm_bf16_kernel<{operand}, {operand}, true, true> critic block-1 forward "
-                   f"[2 x {rows} x {h}] . [{4 * h} x {h}]^T" if agent.mode == K.BF16 else
-                   f"gemm_kernel<0, float, float, true, true> critic block-1 forward [2 x {rows} x {h}] . "
-                   f"[{4 * h} x {h}]^T")
+    shape = f"critic block-1 forward [2 x {rows} x {h}] . [{4 * h} x {h}]^T"
+    if agent.mode == K.BF16 and rows % 256 == 0 and (4 * h) % 256 == 0 and h % 64 == 0:
+        kernel_name = f"gemm_big_kernel<true, true> {shape}"  # 256x256 tiles (exactly tiling bf16 operands)
+    elif agent.mode == K.BF16:
+        kernel_name = f"gemm_bf16_kernel<{operand}, {operand}, true, true> {shape}"
+    else:
+        kernel_name = f"gemm_kernel<0, float, float, true, true> {shape}"
     traffic = args.traffic if args.traffic is not None else measured_traffic(kernel_name)
     operand_bytes = 2 if agent.mode == K.BF16 else 4
     algorithmic_bytes = 2 * (rows * h + 4 * h * h) * operand_bytes + 2 * rows * 4 * h * 4

@@ -42,5 +42,9 @@ __device__ __forceinline__ float apply_epilogue(float v, int epilogue) {
 // bf16 MFMA kernel family with 256x128 tiles (gemm_bf16.hip).
 void launch_bf16(const Params& p, int a_bf16, int b_bf16, bool ak, bool bk, hipStream_t stream);
 
+// 256x256-tile bf16 kernel for exactly tiling bf16 operands (gemm_bf16_big.hip).
+bool big_eligible(const Params& p, int a_bf16, int b_bf16);
+void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream);
+
 }  // namespace gemm
 }  // namespace rl

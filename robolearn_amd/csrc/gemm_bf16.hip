@@ -278,6 +278,10 @@ void launch_layout_v2(const Params& p, bool ak, bool bk, hipStream_t stream) {
 }
 
 void launch_bf16(const Params& p, int a_bf16, int b_bf16, bool ak, bool bk, hipStream_t stream) {
+    if (big_eligible(p, a_bf16, b_bf16)) {
+        launch_big(p, ak, bk, stream);
+        return;
+    }
     using F = float;
     using H = unsigned short;
     if (!a_bf16 && !b_bf16) launch_layout_v2<F, F>(p, ak, bk, stream);

@@ -204,3 +204,40 @@ def test_td_cross_entropy_matches_oracle_projection(gpu, bins):
     grad = scale * (lp_online.exp() * expected.sum(-1, keepdim=True)[None] - expected[None])
     torch.testing.assert_close(dlogits.cpu(), grad, rtol=1e-4, atol=1e-7)
     torch.testing.assert_close(entropy_rows.cpu(), entropy, rtol=1e-6, atol=0)
+
+
+# Shapes that take the 256x256-tile bf16 kernel (m, n multiples of 256, K ranges
+# multiples of 64): workgroup counts below and at multiples of 8 (the XCD
+# renumbering), partial M-tile groups, split-K, and every operand layout.
+BIG_SHAPES = [(2, 512, 256, 128, 1), (2, 2560, 512, 128, 1), (1, 3072, 256, 64, 1), (2, 1024, 512, 512, 4)]
+
+
+@pytest.mark.parametrize("a_kcontig", [True, False])
+@pytest.mark.parametrize("b_kcontig", [True, False])
+@pytest.mark.parametrize("batch,m,n,k,splits", BIG_SHAPES)
+def test_big_tile_bf16_gemm_layouts(gpu, a_kcontig, b_kcontig, batch, m, n, k, splits):
+    print(f"case big a_k={a_kcontig} b_k={b_kcontig} batch={batch} m={m} n={n} k={k} splits={splits}", flush=True)
+    g = torch.Generator().manual_seed(m + n + k)
+    a = torch.randn(batch, m, k, generator=g).to(torch.bfloat16)
+    b = torch.randn(batch, n, k, generator=g).to(torch.bfloat16)
+    bias = torch.randn(batch, n, generator=g)
+    c = torch.randn(batch, m, n, generator=g)
+    a_mem = a if a_kcontig else a.transpose(1, 2).contiguous()
+    b_mem = b if b_kcontig else b.transpose(1, 2).contiguous()
+    ad, bd = a_mem.to(gpu), b_mem.to(gpu)
+    workspace = torch.empty(splits * batch * m * n * 4, dtype=torch.uint8, device=gpu) if splits > 1 else None
+    ref = torch.einsum("bmk,bnk->bmn", a.double(), b.double())
+    d = torch.empty(batch, m, n, device=gpu)
+    d_bf16 = torch.empty(batch, m, n, dtype=torch.bfloat16, device=gpu)
+    K.gemm(ad, bd, d, m=m, n=n, k=k, batch=batch, a_kcontig=a_kcontig, b_kcontig=b_kcontig,
+           lda=k if a_kcontig else m, ldb=k if b_kcontig else n, ldd=n, stride_a=m * k, stride_b=n * k,
+           stride_d=m * n, mode=K.BF16, splits=splits, workspace=workspace, d_bf16=d_bf16)
+    torch.testing.assert_close(d.cpu().double(), ref, rtol=1e-5, atol=1e-5 * math.sqrt(k))
+    torch.testing.assert_close(d_bf16.cpu(), d.cpu().to(torch.bfloat16), rtol=0, atol=0)
+    # fused epilogue: relu(AB + bias) + C
+    K.gemm(ad, bd, d, m=m, n=n, k=k, batch=batch, a_kcontig=a_kcontig, b_kcontig=b_kcontig,
+           lda=k if a_kcontig else m, ldb=k if b_kcontig else n, ldd=n, stride_a=m * k, stride_b=n * k,
+           stride_d=m * n, mode=K.BF16, splits=splits, workspace=workspace, bias=bias.to(gpu), stride_bias=n,
+           epilogue="relu", c=c.to(gpu), beta=1.0)
+    expected = torch.relu(ref + bias.double()[:, None, :]) + c.double()
+    torch.testing.assert_close(d.cpu().double(), expected, rtol=1e-5, atol=1e-5 * math.sqrt(k))
