@@ -133,6 +133,128 @@ __global__ void bn_apply(const float* x, long long x_stride, const float* mean, 
     }
 }
 
+// Layout of the vectorized elementwise BN kernels: a workgroup covers
+// `tpr` float4 columns x (256 / tpr) row groups, each thread kRowsPerThread rows
+// of one float4 column; per-channel constants are loaded once per thread.
+constexpr int kRowsPerThread = 16;
+
+struct VecLayout {
+    int tpr;    // threads per row (float4 columns per workgroup)
+    dim3 grid;
+};
+
+inline VecLayout vec_layout(long long rows, int channels, int ensemble) {
+    const int cols4 = channels / 4;
+    int tpr = 1;
+    while (tpr < cols4 && tpr < 256) tpr *= 2;
+    const long long groups = 256 / tpr;
+    const long long row_blocks = (rows + groups * kRowsPerThread - 1) / (groups * kRowsPerThread);
+    return VecLayout{tpr, dim3(ceil_div(cols4, tpr), static_cast<unsigned>(row_blocks), ensemble)};
+}
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ void st4_bf16(unsigned short* p, float4 v) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(f32x2_to_bf16x2(v.x, v.y), f32x2_to_bf16x2(v.z, v.w));
+}
+
+// bn_apply for channels % 4 == 0 with 16-byte aligned rows.
+__global__ __launch_bounds__(256) void bn_apply_vec(const float* x, long long x_stride, const float* mean,
+                                                    const float* var, const float* w, const float* b,
+                                                    const float* residual, float* y, unsigned short* y_bf16,
+                                                    long long rows, int channels, float eps, int relu, int tpr) {
+    const int e = blockIdx.z;
+    const int q = blockIdx.x * tpr + threadIdx.x % tpr;  // float4 column
+    if (4 * q >= channels) return;
+    const int groups = 256 / tpr;
+    const long long r0 = static_cast<long long>(blockIdx.y) * groups * kRowsPerThread + threadIdx.x / tpr;
+    const int c = 4 * q;
+    const int pc = e * channels + c;
+    const float4 mu = ld4(mean + pc), va = ld4(var + pc), wv = ld4(w + pc), bv = ld4(b + pc);
+    const float4 inv = make_float4(1.0f / sqrtf(va.x + eps), 1.0f / sqrtf(va.y + eps), 1.0f / sqrtf(va.z + eps),
+                                   1.0f / sqrtf(va.w + eps));
+    const float* xe = x + e * x_stride;
+    const long long out_base = static_cast<long long>(e) * rows * channels;
+#pragma unroll 4
+    for (int k = 0; k < kRowsPerThread; ++k) {
+        const long long r = r0 + static_cast<long long>(k) * groups;
+        if (r >= rows) break;
+        const long long i = r * channels + c;
+        const float4 xv = ld4(xe + i);
+        float4 v = make_float4(bn_value(xv.x, mu.x, inv.x, wv.x, bv.x), bn_value(xv.y, mu.y, inv.y, wv.y, bv.y),
+                               bn_value(xv.z, mu.z, inv.z, wv.z, bv.z), bn_value(xv.w, mu.w, inv.w, wv.w, bv.w));
+        if (relu) v = make_float4(v.x > 0.0f ? v.x : 0.0f, v.y > 0.0f ? v.y : 0.0f, v.z > 0.0f ? v.z : 0.0f,
+                                  v.w > 0.0f ? v.w : 0.0f);
+        if (residual) {
+            const float4 rv = ld4(residual + out_base + i);
+            v = make_float4(v.x + rv.x, v.y + rv.y, v.z + rv.z, v.w + rv.w);
+        }
+        if (y) st4(y + out_base + i, v);
+        if (y_bf16) st4_bf16(y_bf16 + out_base + i, v);
+    }
+}
+
+// bn_grad_apply for channels % 4 == 0 with 16-byte aligned rows.
+__global__ __launch_bounds__(256) void bn_grad_apply_vec(const float* x, long long x_stride, const float* dy,
+                                                         const float* y, const float* w, const float* b,
+                                                         const float* mean, const float* var, const float* sums,
+                                                         float* dx, unsigned short* dx_bf16, long long rows,
+                                                         int channels, int ensemble, float eps, int training, int relu,
+                                                         int accumulate, int tpr) {
+    const int e = blockIdx.z;
+    const int q = blockIdx.x * tpr + threadIdx.x % tpr;
+    if (4 * q >= channels) return;
+    const int groups = 256 / tpr;
+    const long long r0 = static_cast<long long>(blockIdx.y) * groups * kRowsPerThread + threadIdx.x / tpr;
+    const int c = 4 * q;
+    const int pc = e * channels + c;
+    const float4 mu = ld4(mean + pc), va = ld4(var + pc), wv = ld4(w + pc);
+    const float4 bv = b ? ld4(b + pc) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 inv = make_float4(1.0f / sqrtf(va.x + eps), 1.0f / sqrtf(va.y + eps), 1.0f / sqrtf(va.z + eps),
+                                   1.0f / sqrtf(va.w + eps));
+    float4 s0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s1 = s0;
+    if (training) {
+        s0 = ld4(sums + pc);
+        s1 = ld4(sums + ensemble * channels + pc);
+    }
+    const float* xe = x + e * x_stride;
+    const long long out_base = static_cast<long long>(e) * rows * channels;
+    const float4 winv = make_float4(wv.x * inv.x, wv.y * inv.y, wv.z * inv.z, wv.w * inv.w);
+#pragma unroll 4
+    for (int k = 0; k < kRowsPerThread; ++k) {
+        const long long r = r0 + static_cast<long long>(k) * groups;
+        if (r >= rows) break;
+        const long long i = r * channels + c;
+        const float4 xv = ld4(xe + i);
+        float4 g = ld4(dy + out_base + i);
+        if (relu) {
+            float4 out;
+            if (y) out = ld4(y + out_base + i);
+            else out = make_float4(bn_value(xv.x, mu.x, inv.x, wv.x, bv.x), bn_value(xv.y, mu.y, inv.y, wv.y, bv.y),
+                                   bn_value(xv.z, mu.z, inv.z, wv.z, bv.z), bn_value(xv.w, mu.w, inv.w, wv.w, bv.w));
+            if (!(out.x > 0.0f)) g.x = 0.0f;
+            if (!(out.y > 0.0f)) g.y = 0.0f;
+            if (!(out.z > 0.0f)) g.z = 0.0f;
+            if (!(out.w > 0.0f)) g.w = 0.0f;
+        }
+        float4 v;
+        if (training) {
+            v = make_float4(winv.x * (g.x - s0.x - (xv.x - mu.x) * inv.x * s1.x),
+                            winv.y * (g.y - s0.y - (xv.y - mu.y) * inv.y * s1.y),
+                            winv.z * (g.z - s0.z - (xv.z - mu.z) * inv.z * s1.z),
+                            winv.w * (g.w - s0.w - (xv.w - mu.w) * inv.w * s1.w));
+        } else {
+            v = make_float4(winv.x * g.x, winv.y * g.y, winv.z * g.z, winv.w * g.w);
+        }
+        if (accumulate) {
+            const float4 o = ld4(dx + out_base + i);
+            v = make_float4(v.x + o.x, v.y + o.y, v.z + o.z, v.w + o.w);
+        }
+        if (dx) st4(dx + out_base + i, v);
+        if (dx_bf16) st4_bf16(dx_bf16 + out_base + i, v);
+    }
+}
+
 // Backward partial sums per chunk: sum(dy'), sum(dy' * xhat) with dy' the
 // ReLU-masked output gradient.
 __global__ __launch_bounds__(kThreads) void bn_grad_partials(const float* x, long long x_stride, const float* dy,
@@ -584,9 +706,18 @@ void bn_forward(int ensemble, const float* x, long long x_stride, const float* w
         require(running_mean && running_var, "Eval BatchNorm requires running statistics.");
     }
     const long long total = static_cast<long long>(ensemble) * rows * channels;
-    hipLaunchKernelGGL(norm::bn_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream, x, x_stride,
-                       use_mean, use_var, w, b, residual, y, y_bf16, static_cast<long long>(rows), channels, ensemble,
-                       eps, relu);
+    const bool vec = channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && (!y || aligned(y, 16)) &&
+                     (!y_bf16 || aligned(y_bf16, 8)) && (!residual || aligned(residual, 16)) &&
+                     aligned(use_mean, 16) && aligned(use_var, 16) && aligned(w, 16) && aligned(b, 16);
+    if (vec) {
+        const norm::VecLayout layout = norm::vec_layout(rows, channels, ensemble);
+        hipLaunchKernelGGL(norm::bn_apply_vec, layout.grid, dim3(256), 0, stream, x, x_stride, use_mean, use_var, w, b,
+                           residual, y, y_bf16, static_cast<long long>(rows), channels, eps, relu, layout.tpr);
+    } else {
+        hipLaunchKernelGGL(norm::bn_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream, x, x_stride,
+                           use_mean, use_var, w, b, residual, y, y_bf16, static_cast<long long>(rows), channels,
+                           ensemble, eps, relu);
+    }
     check_launch("Launch BN apply");
 }
 
@@ -613,9 +744,20 @@ void bn_backward(int ensemble, const float* x, long long x_stride, const float* 
     }
     if (dx || dx_bf16) {
         const long long total = static_cast<long long>(ensemble) * rows * channels;
-        hipLaunchKernelGGL(norm::bn_grad_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream, x,
-                           x_stride, dy, y, w, b, mean, var, sums, dx, dx_bf16, static_cast<long long>(rows), channels,
-                           ensemble, eps, training, relu, accumulate_dx);
+        const bool vec = channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && aligned(dy, 16) &&
+                         (!y || aligned(y, 16)) && (!dx || aligned(dx, 16)) && (!dx_bf16 || aligned(dx_bf16, 8)) &&
+                         aligned(w, 16) && (!b || aligned(b, 16)) && aligned(mean, 16) && aligned(var, 16) &&
+                         (!training || (aligned(sums, 16) && (ensemble * channels) % 4 == 0));
+        if (vec) {
+            const norm::VecLayout layout = norm::vec_layout(rows, channels, ensemble);
+            hipLaunchKernelGGL(norm::bn_grad_apply_vec, layout.grid, dim3(256), 0, stream, x, x_stride, dy, y, w, b,
+                               mean, var, sums, dx, dx_bf16, static_cast<long long>(rows), channels, ensemble, eps,
+                               training, relu, accumulate_dx, layout.tpr);
+        } else {
+            hipLaunchKernelGGL(norm::bn_grad_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream, x,
+                               x_stride, dy, y, w, b, mean, var, sums, dx, dx_bf16, static_cast<long long>(rows),
+                               channels, ensemble, eps, training, relu, accumulate_dx);
+        }
         check_launch("Launch BN gradient apply");
     }
 }

@@ -76,7 +76,10 @@ def test_bf16_operand_tensors(gpu):
     torch.testing.assert_close(y.cpu().double(), ref, rtol=1e-5, atol=1e-4)
 
 
-@pytest.mark.parametrize("ensemble,rows,channels,relu", [(1, 1000, 5, False), (2, 777, 130, True), (2, 300, 64, True)])
+# channels 64, 160 and 1024 take the float4 elementwise kernels (160: a partial
+# column block), 5 and 130 the scalar ones
+@pytest.mark.parametrize("ensemble,rows,channels,relu", [(1, 1000, 5, False), (2, 777, 130, True), (2, 300, 64, True),
+                                                         (1, 257, 160, False), (2, 513, 1024, True)])
 def test_batchnorm_forward_backward_match_autograd(gpu, ensemble, rows, channels, relu):
     x = _rand(ensemble, rows, channels, seed=10, scale=2.0) + 0.5
     w = _rand(ensemble, channels, seed=11).abs() + 0.5
@@ -115,6 +118,13 @@ def test_batchnorm_forward_backward_match_autograd(gpu, ensemble, rows, channels
     torch.testing.assert_close(dx.cpu().double(), xr.grad, rtol=1e-4, atol=1e-5)
     torch.testing.assert_close(dw.cpu().double(), wr.grad, rtol=1e-4, atol=1e-4)
     torch.testing.assert_close(db.cpu().double(), br.grad, rtol=1e-4, atol=1e-4)
+    # the ReLU mask recomputed from x and the bias (no stored output) gives the same adjoints
+    dx2 = torch.empty_like(y)
+    dx2_bf16 = torch.empty(y.shape, dtype=torch.bfloat16, device=gpu)
+    K.bn_backward(g["x"], g["dy"], None, g["w"], mean, var, partial, sums, dx2, None, None, rows=rows,
+                  channels=channels, ensemble=ensemble, relu=relu, b=g["b"], dx_bf16=dx2_bf16)
+    torch.testing.assert_close(dx2.cpu(), dx.cpu(), rtol=0, atol=0)
+    torch.testing.assert_close(dx2_bf16.cpu(), dx.cpu().to(torch.bfloat16), rtol=0, atol=0)
     # eval mode uses running statistics
     y2 = torch.empty_like(y)
     K.bn_forward(g["x"], g["w"], g["b"], g["rm"], g["rv"], None, None, None, y2, rows=rows, channels=channels,
