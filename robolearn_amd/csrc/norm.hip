@@ -255,6 +255,133 @@ __global__ __launch_bounds__(256) void bn_grad_apply_vec(const float* x, long lo
     }
 }
 
+// float4 variants of bn_moments / bn_grad_partials for channels % 4 == 0: a
+// workgroup covers 64 channels (16 float4 columns) x one 256-row chunk, 16 row
+// groups of 16 rows; each thread keeps its rows in registers.
+constexpr int kVecCols = 16;                     // float4 columns per workgroup
+constexpr int kVecGroups = kThreads / kVecCols;  // row groups
+constexpr int kVecRows = kChunk / kVecGroups;    // rows per thread
+
+__device__ __forceinline__ float4 f4(float v) { return make_float4(v, v, v, v); }
+
+// Chunk moments with a two-pass mean / M2 per thread, then a fixed-order merge
+// of the row groups.
+__global__ __launch_bounds__(kThreads) void bn_moments_vec(const float* x, long long x_stride, float* partial, int rows,
+                                                           int channels, int chunks) {
+    const int e = blockIdx.z;
+    const int q = blockIdx.x * kVecCols + threadIdx.x % kVecCols;
+    const int group = threadIdx.x / kVecCols;
+    const int chunk = blockIdx.y;
+    const int r0 = chunk * kChunk + group;
+    const int r_end = min(rows, (chunk + 1) * kChunk);
+    const bool live = 4 * q < channels;
+    const float* base = x + e * x_stride + 4 * q;
+    float4 v[kVecRows];
+    float count = 0.0f;
+    float4 mean = f4(0.0f);
+#pragma unroll
+    for (int k = 0; k < kVecRows; ++k) {
+        const int r = r0 + k * kVecGroups;
+        const bool ok = live && r < r_end;
+        v[k] = ok ? ld4(base + static_cast<long long>(r) * channels) : f4(0.0f);
+        if (ok) {
+            count += 1.0f;
+            mean = make_float4(mean.x + v[k].x, mean.y + v[k].y, mean.z + v[k].z, mean.w + v[k].w);
+        }
+    }
+    float4 m2 = f4(0.0f);
+    if (count > 0.0f) {
+        const float inv = 1.0f / count;
+        mean = make_float4(mean.x * inv, mean.y * inv, mean.z * inv, mean.w * inv);
+#pragma unroll
+        for (int k = 0; k < kVecRows; ++k) {
+            if (r0 + k * kVecGroups >= r_end) break;
+            const float4 d = make_float4(v[k].x - mean.x, v[k].y - mean.y, v[k].z - mean.z, v[k].w - mean.w);
+            m2 = make_float4(m2.x + d.x * d.x, m2.y + d.y * d.y, m2.z + d.z * d.z, m2.w + d.w * d.w);
+        }
+    }
+    __shared__ float s_count[kThreads];
+    __shared__ float4 s_mean[kThreads], s_m2[kThreads];
+    s_count[threadIdx.x] = count;
+    s_mean[threadIdx.x] = mean;
+    s_m2[threadIdx.x] = m2;
+    __syncthreads();
+    if (group == 0 && live) {
+        float cx = count, cy = count, cz = count, cw = count;
+        for (int g = 1; g < kVecGroups; ++g) {
+            const int t = g * kVecCols + threadIdx.x;
+            const float n = s_count[t];
+            const float4 mb = s_mean[t], qb = s_m2[t];
+            merge(cx, mean.x, m2.x, n, mb.x, qb.x);
+            merge(cy, mean.y, m2.y, n, mb.y, qb.y);
+            merge(cz, mean.z, m2.z, n, mb.z, qb.z);
+            merge(cw, mean.w, m2.w, n, mb.w, qb.w);
+        }
+        float* out = partial + (static_cast<long long>(e) * chunks + chunk) * 2 * channels + 4 * q;
+        st4(out, mean);
+        st4(out + channels, m2);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void bn_grad_partials_vec(const float* x, long long x_stride, const float* dy,
+                                                                 const float* y, const float* w, const float* b,
+                                                                 const float* mean, const float* var, float* partial,
+                                                                 int rows, int channels, int chunks, float eps,
+                                                                 int relu) {
+    const int e = blockIdx.z;
+    const int q = blockIdx.x * kVecCols + threadIdx.x % kVecCols;
+    const int group = threadIdx.x / kVecCols;
+    const int chunk = blockIdx.y;
+    const int r0 = chunk * kChunk + group;
+    const int r_end = min(rows, (chunk + 1) * kChunk);
+    const bool live = 4 * q < channels;
+    float4 s0 = f4(0.0f), s1 = f4(0.0f);
+    if (live) {
+        const int pc = e * channels + 4 * q;
+        const float4 mu = ld4(mean + pc), va = ld4(var + pc), wv = ld4(w + pc);
+        const float4 bv = b ? ld4(b + pc) : f4(0.0f);
+        const float4 inv = make_float4(1.0f / sqrtf(va.x + eps), 1.0f / sqrtf(va.y + eps), 1.0f / sqrtf(va.z + eps),
+                                       1.0f / sqrtf(va.w + eps));
+        const float* xe = x + e * x_stride + 4 * q;
+        const long long off = static_cast<long long>(e) * rows * channels + 4 * q;
+#pragma unroll 4
+        for (int k = 0; k < kVecRows; ++k) {
+            const int r = r0 + k * kVecGroups;
+            if (r >= r_end) break;
+            const long long i = static_cast<long long>(r) * channels;
+            const float4 xv = ld4(xe + i);
+            float4 g = ld4(dy + off + i);
+            if (relu) {
+                float4 out;
+                if (y) out = ld4(y + off + i);
+                else out = make_float4(bn_value(xv.x, mu.x, inv.x, wv.x, bv.x), bn_value(xv.y, mu.y, inv.y, wv.y, bv.y),
+                                       bn_value(xv.z, mu.z, inv.z, wv.z, bv.z), bn_value(xv.w, mu.w, inv.w, wv.w, bv.w));
+                if (!(out.x > 0.0f)) g.x = 0.0f;
+                if (!(out.y > 0.0f)) g.y = 0.0f;
+                if (!(out.z > 0.0f)) g.z = 0.0f;
+                if (!(out.w > 0.0f)) g.w = 0.0f;
+            }
+            s0 = make_float4(s0.x + g.x, s0.y + g.y, s0.z + g.z, s0.w + g.w);
+            s1 = make_float4(s1.x + g.x * ((xv.x - mu.x) * inv.x), s1.y + g.y * ((xv.y - mu.y) * inv.y),
+                             s1.z + g.z * ((xv.z - mu.z) * inv.z), s1.w + g.w * ((xv.w - mu.w) * inv.w));
+        }
+    }
+    __shared__ float4 sa[kThreads], sb[kThreads];
+    sa[threadIdx.x] = s0;
+    sb[threadIdx.x] = s1;
+    __syncthreads();
+    if (group == 0 && live) {
+        for (int g = 1; g < kVecGroups; ++g) {
+            const float4 a = sa[g * kVecCols + threadIdx.x], c = sb[g * kVecCols + threadIdx.x];
+            s0 = make_float4(s0.x + a.x, s0.y + a.y, s0.z + a.z, s0.w + a.w);
+            s1 = make_float4(s1.x + c.x, s1.y + c.y, s1.z + c.z, s1.w + c.w);
+        }
+        float* out = partial + (static_cast<long long>(e) * chunks + chunk) * 2 * channels + 4 * q;
+        st4(out, s0);
+        st4(out + channels, s1);
+    }
+}
+
 // Backward partial sums per chunk: sum(dy'), sum(dy' * xhat) with dy' the
 // ReLU-masked output gradient.
 __global__ __launch_bounds__(kThreads) void bn_grad_partials(const float* x, long long x_stride, const float* dy,
@@ -692,9 +819,15 @@ void bn_forward(int ensemble, const float* x, long long x_stride, const float* w
     if (training) {
         require(mean && var && partial, "Training BatchNorm requires mean, var and partial scratch.");
         const int chunks = chunks_for(rows);
-        const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
-        hipLaunchKernelGGL(norm::bn_moments, grid, dim3(norm::kThreads), 0, stream, x, x_stride, partial, rows,
-                           channels, chunks);
+        if (channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && aligned(partial, 16)) {
+            const dim3 grid(ceil_div(channels / 4, norm::kVecCols), chunks, ensemble);
+            hipLaunchKernelGGL(norm::bn_moments_vec, grid, dim3(norm::kThreads), 0, stream, x, x_stride, partial, rows,
+                               channels, chunks);
+        } else {
+            const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
+            hipLaunchKernelGGL(norm::bn_moments, grid, dim3(norm::kThreads), 0, stream, x, x_stride, partial, rows,
+                               channels, chunks);
+        }
         check_launch("Launch BN moments");
         hipLaunchKernelGGL(norm::bn_statistics, dim3(ceil_div(ensemble * channels, 256)), dim3(256), 0, stream,
                            partial, mean, var, running_mean, running_var, rows, channels, chunks, ensemble, momentum,
@@ -734,9 +867,16 @@ void bn_backward(int ensemble, const float* x, long long x_stride, const float* 
     if (need_sums) {
         require(partial && sums, "BatchNorm backward requires partial and sums scratch.");
         const int chunks = chunks_for(rows);
-        const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
-        hipLaunchKernelGGL(norm::bn_grad_partials, grid, dim3(norm::kThreads), 0, stream, x, x_stride, dy, y, w, b,
-                           mean, var, partial, rows, channels, chunks, eps, relu);
+        if (channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && aligned(dy, 16) && (!y || aligned(y, 16)) &&
+            aligned(w, 16) && (!b || aligned(b, 16)) && aligned(mean, 16) && aligned(var, 16) && aligned(partial, 16)) {
+            const dim3 grid(ceil_div(channels / 4, norm::kVecCols), chunks, ensemble);
+            hipLaunchKernelGGL(norm::bn_grad_partials_vec, grid, dim3(norm::kThreads), 0, stream, x, x_stride, dy, y, w,
+                               b, mean, var, partial, rows, channels, chunks, eps, relu);
+        } else {
+            const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
+            hipLaunchKernelGGL(norm::bn_grad_partials, grid, dim3(norm::kThreads), 0, stream, x, x_stride, dy, y, w, b,
+                               mean, var, partial, rows, channels, chunks, eps, relu);
+        }
         check_launch("Launch BN gradient partials");
         hipLaunchKernelGGL(norm::bn_grad_reduce, dim3(ceil_div(ensemble * channels, 256)), dim3(256), 0, stream,
                            partial, sums, dw, db, rows, channels, chunks, ensemble, accumulate_params);
