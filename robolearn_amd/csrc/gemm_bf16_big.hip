@@ -44,7 +44,9 @@ __device__ __forceinline__ unsigned int high_halves(unsigned int a, unsigned int
 
 // One operand tile of 256 rows x 32 k in registers (4 x 16 bytes per thread).
 // K-contiguous: vector i holds row i*64 + t/4, k chunk t%4.
-// M/N-contiguous: vector kk holds k row 4*(t/32) + kk, rows 8*(t%32) .. +7.
+// M/N-contiguous: vector kk holds k row 4*(t%8) + kk, rows 8*(t/8) .. +7; the
+// eight lanes that share a row group write one contiguous 64-byte LDS run, so
+// the transposed stores do not pile onto one bank group.
 template <bool KContig>
 struct Stage {
     u32x4 v[4];
@@ -58,8 +60,8 @@ struct Stage {
                 v[i] = *reinterpret_cast<const u32x4*>(src + static_cast<long long>(r0 + row) * ld + k0 + (t % 4) * 8);
             }
         } else {
-            const int mb = t % 32;
-            const int kg = t / 32;
+            const int mb = t / 8;
+            const int kg = t % 8;
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 const long long k = k0 + kg * 4 + kk;
@@ -77,8 +79,8 @@ struct Stage {
                 *reinterpret_cast<u32x4*>(lds + row * P + (t % 4) * 8) = v[i];
             }
         } else {
-            const int mb = t % 32;
-            const int kg = t / 32;
+            const int mb = t / 8;
+            const int kg = t % 8;
             // word j of element q holds k rows 2j (low half) and 2j + 1 (high half)
             unsigned int w[8][2];
 #pragma unroll
