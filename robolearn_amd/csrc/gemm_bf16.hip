@@ -92,8 +92,11 @@ struct Loader {
                 else raw[i] = r < rows ? gather(p, max(0, min(VE, ks - k))) : zero();
             }
         } else {
-            const int r = r0 + (t % VPK) * VE;
-            const int kb = k0 + (t / VPK) * KR;
+            // lanes that share a row group are adjacent (t % G), so their
+            // transposed LDS stores form one contiguous run instead of piling
+            // onto one bank group
+            const int r = r0 + (t / G) * VE;
+            const int kb = k0 + (t % G) * KR;
 #pragma unroll
             for (int kk = 0; kk < KR; ++kk) {
                 const int k = kb + kk;
@@ -119,8 +122,8 @@ struct Loader {
                 }
             }
         } else {
-            const int mb = t % VPK;
-            const int kg = t / VPK;
+            const int mb = t / G;
+            const int kg = t % G;
             // word j of element q holds k rows 2j (low half) and 2j + 1 (high half)
             unsigned int w[VE][KR / 2];
 #pragma unroll
