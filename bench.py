@@ -470,8 +470,8 @@ def main() -> int:
     achieved = kernel_flops / (kernel_ms * 1e-3) / 1e12
     operand = "unsigned short" if agent.mode == K.BF16 else "float"
     shape = f"critic block-1 forward [2 x {rows} x {h}] . [{4 * h} x {h}]^T"
-    if agent.mode == K.BF16 and rows % 256 == 0 and (4 * h) % 256 == 0 and h % 64 == 0:
-        kernel_name = f"gemm_big_kernel<true, true> {shape}"  # 256x256 tiles (exactly tiling bf16 operands)
+    if agent.mode == K.BF16 and rows % 256 == 0 and (4 * h) % 256 == 0 and h % 128 == 0:
+        kernel_name = f"gemm_dma_kernel {shape}"  # 256x256 tiles, DMA-fed (both operands K-contiguous)
     elif agent.mode == K.BF16:
         kernel_name = f"gemm_bf16_kernel<{operand}, {operand}, true, true> {shape}"
     else:

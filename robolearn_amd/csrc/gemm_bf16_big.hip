@@ -43,10 +43,17 @@ __device__ __forceinline__ unsigned int high_halves(unsigned int a, unsigned int
 }
 
 // One operand tile of 256 rows x 32 k in registers (4 x 16 bytes per thread).
-// K-contiguous: vector i holds row i*64 + t/4, k chunk t%4.
+// K-contiguous: vector i holds row i*64 + kc_row(t), k chunk t%4, where
+// kc_row pairs rows r and r + 4 inside each group of 8 lanes: with the 80-byte
+// pitch those two rows cover the eight 16-byte bank slots exactly once, so the
+// 16-byte LDS stores are conflict-free (rows r and r + 1 would share a slot).
 // M/N-contiguous: vector kk holds k row 4*(t%8) + kk, rows 8*(t/8) .. +7; the
 // eight lanes that share a row group write one contiguous 64-byte LDS run, so
 // the transposed stores do not pile onto one bank group.
+// Row within a 64-row block for thread t of the K-contiguous layout: lanes
+// 8g .. 8g+3 take row r, lanes 8g+4 .. 8g+7 row r + 4.
+__device__ __forceinline__ int kc_row(int t) { return 8 * (t / 32) + (t / 8) % 4 + 4 * ((t % 8) / 4); }
+
 template <bool KContig>
 struct Stage {
     u32x4 v[4];
@@ -56,7 +63,7 @@ struct Stage {
         if constexpr (KContig) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int row = i * 64 + t / 4;
+                const int row = i * 64 + kc_row(t);
                 v[i] = *reinterpret_cast<const u32x4*>(src + static_cast<long long>(r0 + row) * ld + k0 + (t % 4) * 8);
             }
         } else {
@@ -75,7 +82,7 @@ struct Stage {
         if constexpr (KContig) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int row = i * 64 + t / 4;
+                const int row = i * 64 + kc_row(t);
                 *reinterpret_cast<u32x4*>(lds + row * P + (t % 4) * 8) = v[i];
             }
         } else {
@@ -181,6 +188,73 @@ __device__ __forceinline__ Tile tile_of(int id, int tiles_m, int tiles_n, int sp
     return Tile{(first_m + local % group_m) * BM, (local / group_m) * BN, slice / splits, slice % splits};
 }
 
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
+// operations (lgkmcnt) but not for its global stores, which __syncthreads'
+// release fence would drain; the compiler may not move memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+// Writes one finished 256x256 tile: D = act(acc + bias) + beta C (and the bf16
+// copy) in direct mode, the raw partial tile in split-K mode.  `lds` must hold
+// 4 x 32 x EP floats and be free; the caller's last LDS reads must be complete.
+__device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f32x16_t (&acc)[4][4], void* lds, int wave,
+                                           int wm, int wn) {
+    const int lane = threadIdx.x % kWave;
+    const bool direct = p.splits == 1;
+    // Epilogue through LDS: each wave stages one 32 x 128 block of its
+    // outputs at a time (accumulator layout of a 32x32 MFMA tile: lane l
+    // holds column l % 32 and rows 8 (v / 4) + 4 (l / 32) + v % 4, v < 16)
+    // and writes it back as 16-byte stores, two 512-byte row segments per
+    // wave instruction.  The stores drain while the next tile starts.
+    float* D = p.d + (direct ? tile.batch * p.stride_d
+                             : (static_cast<long long>(tile.split) * p.batch + tile.batch) *
+                                   static_cast<long long>(p.m) * p.n);
+    const long long ldd = direct ? p.ldd : p.n;
+    const float* C = (direct && p.beta != 0.0f) ? p.c + tile.batch * p.stride_d : nullptr;
+    unsigned short* Dh = (direct && p.d_bf16) ? p.d_bf16 + tile.batch * p.stride_d : nullptr;
+    const int c4 = lane % 32;
+    const int col = tile.n0 + wn * 128 + 4 * c4;
+    float4 bias4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (direct && p.bias) bias4 = *reinterpret_cast<const float4*>(p.bias + tile.batch * p.stride_bias + col);
+    float* stage = static_cast<float*>(lds) + wave * 32 * EP;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        lds_barrier();  // the previous block (or the K loop) is done with LDS
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                stage[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * EP + j * 32 + lane % 32] = acc[i][j][v];
+        lds_barrier();
+#pragma unroll 4
+        for (int r = 0; r < 16; ++r) {
+            const int row = 2 * r + lane / 32;
+            float4 val = *reinterpret_cast<const float4*>(stage + row * EP + 4 * c4);
+            const long long offset = static_cast<long long>(tile.m0 + wm * 128 + i * 32 + row) * ldd + col;
+            if (direct) {
+                val = activate4(make_float4(val.x + bias4.x, val.y + bias4.y, val.z + bias4.z, val.w + bias4.w),
+                                p.epilogue);
+                if (C) {
+                    const float4 c = *reinterpret_cast<const float4*>(C + offset);
+                    val.x += p.beta * c.x;
+                    val.y += p.beta * c.y;
+                    val.z += p.beta * c.z;
+                    val.w += p.beta * c.w;
+                }
+                if (Dh)
+                    *reinterpret_cast<uint2*>(Dh + offset) =
+                        make_uint2(f32x2_to_bf16x2(val.x, val.y), f32x2_to_bf16x2(val.z, val.w));
+            }
+            *reinterpret_cast<float4*>(D + offset) = val;
+        }
+    }
+}
+
 // Persistent: gridDim.x workgroups (one per CU) walk the tiles in rounds.  The
 // hardware deals workgroups to the 8 XCDs in turn (workgroup b runs on XCD
 // b % 8), so round r gives XCD x the contiguous logical ids
@@ -194,10 +268,8 @@ __global__ __launch_bounds__(T, 1) void gemm_big_kernel(Params p, int tiles_m, i
     const int b = static_cast<int>(blockIdx.x);
     const int slot = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
     const int wave = threadIdx.x / kWave;
-    const int lane = threadIdx.x % kWave;
     const int wm = wave / 2;
     const int wn = wave % 2;
-    const bool direct = p.splits == 1;
 
     for (int id = slot; id < total; id += G) {
         const Tile tile = tile_of(id, tiles_m, tiles_n, p.splits);
@@ -244,53 +316,156 @@ __global__ __launch_bounds__(T, 1) void gemm_big_kernel(Params p, int tiles_m, i
             k_step(A, B, p, tile.m0, tile.n0, k_of(kt + 3), a1, b1, lds[1], a0, b0, lds[0], wm, wn, acc);
         }
 
-        // Epilogue through LDS: each wave stages one 32 x 128 block of its
-        // outputs at a time (accumulator layout of a 32x32 MFMA tile: lane l
-        // holds column l % 32 and rows 8 (v / 4) + 4 (l / 32) + v % 4, v < 16)
-        // and writes it back as 16-byte stores, two 512-byte row segments per
-        // wave instruction.  The stores drain while the next tile starts.
-        float* D = p.d + (direct ? tile.batch * p.stride_d
-                                 : (static_cast<long long>(tile.split) * p.batch + tile.batch) *
-                                       static_cast<long long>(p.m) * p.n);
-        const long long ldd = direct ? p.ldd : p.n;
-        const float* C = (direct && p.beta != 0.0f) ? p.c + tile.batch * p.stride_d : nullptr;
-        unsigned short* Dh = (direct && p.d_bf16) ? p.d_bf16 + tile.batch * p.stride_d : nullptr;
-        const int c4 = lane % 32;
-        const int col = tile.n0 + wn * 128 + 4 * c4;
-        float4 bias4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (direct && p.bias) bias4 = *reinterpret_cast<const float4*>(p.bias + tile.batch * p.stride_bias + col);
-        float* stage = reinterpret_cast<float*>(&lds[0][0]) + wave * 32 * EP;
+        store_tile(p, tile, acc, &lds[0][0], wave, wm, wn);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Forward products (both operands K-contiguous): tiles move global -> LDS by
+// DMA (global_load_lds_dwordx4, 16 bytes per lane straight into LDS), through
+// a ring of DS = 4 LDS stages issued three K tiles ahead.  No VGPR staging and
+// no LDS store instructions.  Each stage holds the A and B tiles unpadded
+// (64-byte rows) with 16-byte chunks XOR-swizzled by swz(row), which keeps the
+// fragment reads free of bank conflicts for 8- and 16-lane groups.
+// ---------------------------------------------------------------------------
+constexpr int DS = 4;
+constexpr int DSTAGE = (BM + BN) * BK;  // bf16 elements per stage
+
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+
+// Waits until at most N vector-memory instructions of this wave are in flight
+// and its LDS reads are done, then a workgroup barrier: the DMA of the tile
+// about to be read is complete in every wave.
+template <int N>
+__device__ __forceinline__ void dma_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | 0x70 | ((N >> 4) << 14));  // vmcnt(N) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+// DMA of one 256 x 32 operand tile: wave w issues row blocks 4w .. 4w+3 of 16
+// rows; lane l fetches chunk (l % 4) ^ swz(row) of row 16 b + l / 4, which lands
+// at LDS offset 16 l of the block, i.e. element row * 32 + 8 * (l % 4).
+__device__ __forceinline__ void dma_tile(const unsigned short* src, long long ld, int r0, int k0, unsigned short* stage) {
+    const int w = threadIdx.x / kWave;
+    const int l = threadIdx.x % kWave;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            __syncthreads();  // the previous block (or the K loop) is done with LDS
+    for (int i = 0; i < 4; ++i) {
+        const int blk = w * 4 + i;
+        const int row = 16 * blk + l / 4;
+        const unsigned short* g = src + static_cast<long long>(r0 + row) * ld + k0 + ((l % 4) ^ swz(row)) * 8;
+        __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)g,
+                                         (__attribute__((address_space(3))) void*)(stage + blk * 512), 16, 0, 0);
+    }
+}
+
+// Fragments of one K tile from a swizzled stage.  Row bases wm*128 + i*32 are
+// multiples of 32, so swz(row) = swz(lane % 32) and each lane's chunk offsets
+// are fixed: chunk 2 (l / 32) + s for MFMA step s.
+struct Frags {
+    bf16x8_t a[2][4], b[2][4];
+};
+
+__device__ __forceinline__ void read_frags(const unsigned short* stage, int wm, int wn, Frags& f) {
+    const int lane = threadIdx.x % kWave;
+    const int sw = swz(lane % 32);
+    const int off0 = 8 * ((2 * (lane / 32)) ^ sw);
+    const int off1 = 8 * ((2 * (lane / 32) + 1) ^ sw);
+    const unsigned short* la = stage + (wm * 128 + lane % 32) * BK;
+    const unsigned short* lb = stage + BM * BK + (wn * 128 + lane % 32) * BK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f.a[0][i] = *reinterpret_cast<const bf16x8_t*>(la + i * 32 * BK + off0);
+        f.a[1][i] = *reinterpret_cast<const bf16x8_t*>(la + i * 32 * BK + off1);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        f.b[0][j] = *reinterpret_cast<const bf16x8_t*>(lb + j * 32 * BK + off0);
+        f.b[1][j] = *reinterpret_cast<const bf16x8_t*>(lb + j * 32 * BK + off1);
+    }
+}
+
+__device__ __forceinline__ void mfma_frags(const Frags& f, f32x16_t (&acc)[4][4]) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[s][i], f.b[s][j], acc[i][j], 0, 0, 0);
+}
+
+// One step of the DMA pipeline: barrier (the DMA of the next tile has landed in
+// every wave, every wave is done with the stage `refill`), DMA of a later tile
+// into `refill`, the next tile's fragment reads, then this tile's MFMAs from
+// registers while those reads land.
+template <class Fetch>
+__device__ __forceinline__ void dma_step(Fetch&& fetch, int k_tile, unsigned short* refill, const unsigned short* next,
+                                         const Frags& cur, Frags& nxt, int wm, int wn, f32x16_t (&acc)[4][4]) {
+    dma_barrier<8>();
+    fetch(k_tile, refill);
+    read_frags(next, wm, wn, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_frags(cur, acc);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+__global__ __launch_bounds__(T, 1) void gemm_dma_kernel(Params p, int tiles_m, int tiles_n, int total) {
+    __shared__ __attribute__((aligned(16))) unsigned short lds[DS][DSTAGE];
+    static_assert(sizeof(lds) >= 4 * 32 * EP * sizeof(float), "epilogue staging must fit the K-loop LDS");
+
+    const int G = static_cast<int>(gridDim.x);
+    const int b = static_cast<int>(blockIdx.x);
+    const int slot = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
+    const int wave = threadIdx.x / kWave;
+    const int wm = wave / 2;
+    const int wn = wave % 2;
+
+    for (int id = slot; id < total; id += G) {
+        const Tile tile = tile_of(id, tiles_m, tiles_n, p.splits);
+        const unsigned short* A = static_cast<const unsigned short*>(p.a) + tile.batch * p.stride_a;
+        const unsigned short* B = static_cast<const unsigned short*>(p.b) + tile.batch * p.stride_b;
+        const int k_begin = tile.split * p.k_per_split;
+        const int k_end = min(p.k, k_begin + p.k_per_split);
+        const int nk = (k_end - k_begin) / BK;
+        // tiles past the end re-fetch the last tile into a stage nobody reads
+        const auto k_of = [&](int kt) { return k_begin + min(kt, nk - 1) * BK; };
+        const auto fetch = [&](int kt, unsigned short* stage) {
+            dma_tile(A, p.lda, tile.m0, k_of(kt), stage);
+            dma_tile(B, p.ldb, tile.n0, k_of(kt), stage + BM * BK);
+        };
+
+        f32x16_t acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    stage[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * EP + j * 32 + lane % 32] = acc[i][j][v];
-            __syncthreads();
-#pragma unroll 4
-            for (int r = 0; r < 16; ++r) {
-                const int row = 2 * r + lane / 32;
-                float4 val = *reinterpret_cast<const float4*>(stage + row * EP + 4 * c4);
-                const long long offset = static_cast<long long>(tile.m0 + wm * 128 + i * 32 + row) * ldd + col;
-                if (direct) {
-                    val = activate4(make_float4(val.x + bias4.x, val.y + bias4.y, val.z + bias4.z, val.w + bias4.w),
-                                    p.epilogue);
-                    if (C) {
-                        const float4 c = *reinterpret_cast<const float4*>(C + offset);
-                        val.x += p.beta * c.x;
-                        val.y += p.beta * c.y;
-                        val.z += p.beta * c.z;
-                        val.w += p.beta * c.w;
-                    }
-                    if (Dh)
-                        *reinterpret_cast<uint2*>(Dh + offset) =
-                            make_uint2(f32x2_to_bf16x2(val.x, val.y), f32x2_to_bf16x2(val.z, val.w));
-                }
-                *reinterpret_cast<float4*>(D + offset) = val;
-            }
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+        lds_barrier();  // the previous tile's epilogue is done with LDS
+        fetch(0, lds[0]);
+        fetch(1, lds[1]);
+        fetch(2, lds[2]);
+        // Step kt computes tile kt (stage kt % DS) from registers while reading
+        // tile kt + 1's fragments; its barrier waits for the DMA of tiles <= kt + 1
+        // (each wave has 8 DMA instructions per tile, so tile kt + 2's 8 may stay
+        // in flight) and for every wave to finish step kt - 1, whose stage
+        // ((kt + 3) % DS) then takes tile kt + 3.  nk is a multiple of 4.
+        Frags f0, f1;
+        dma_barrier<8>();
+        read_frags(lds[0], wm, wn, f0);
+        for (int kt = 0; kt < nk; kt += DS) {
+            dma_step(fetch, kt + 3, lds[3], lds[1], f0, f1, wm, wn, acc);
+            dma_step(fetch, kt + 4, lds[0], lds[2], f1, f0, wm, wn, acc);
+            dma_step(fetch, kt + 5, lds[1], lds[3], f0, f1, wm, wn, acc);
+            dma_step(fetch, kt + 6, lds[2], lds[0], f1, f0, wm, wn, acc);
         }
+        dma_barrier<0>();  // the redundant tail DMAs have landed and every wave is past its last reads
+        store_tile(p, tile, acc, &lds[0][0], wave, wm, wn);
     }
 }
 
@@ -331,7 +506,9 @@ void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream) {
     const int total = tiles_m * tiles_n * p.batch * p.splits;
     const dim3 grid(static_cast<unsigned>(std::min(total, compute_units())));
     const dim3 block(big::T);
-    if (ak && bk) hipLaunchKernelGGL((big::gemm_big_kernel<true, true>), grid, block, 0, stream, p, tiles_m, tiles_n, total);
+    const bool dma = ak && bk && p.k % (big::DS * big::BK) == 0 && p.k_per_split % (big::DS * big::BK) == 0;
+    if (dma) hipLaunchKernelGGL(big::gemm_dma_kernel, grid, block, 0, stream, p, tiles_m, tiles_n, total);
+    else if (ak && bk) hipLaunchKernelGGL((big::gemm_big_kernel<true, true>), grid, block, 0, stream, p, tiles_m, tiles_n, total);
     else if (ak && !bk) hipLaunchKernelGGL((big::gemm_big_kernel<true, false>), grid, block, 0, stream, p, tiles_m, tiles_n, total);
     else if (!ak && bk) hipLaunchKernelGGL((big::gemm_big_kernel<false, true>), grid, block, 0, stream, p, tiles_m, tiles_n, total);
     else hipLaunchKernelGGL((big::gemm_big_kernel<false, false>), grid, block, 0, stream, p, tiles_m, tiles_n, total);
