@@ -81,6 +81,24 @@ void* rl_adam_create(size_t count, const void* const* parameters, const void* co
                      void* learning_rate, double beta1, double beta2, double eps);
 int rl_adam_step(void* plan, void* stream);
 int rl_adam_destroy(void* plan);
+/* robolearn/cuda/kernels.cu:822-854: persistent device state for dynamic loss
+ * scaling (float scale, int growth tracker, int found_inf, int step_skipped,
+ * int64 attempted and skipped counters).  A step with found_inf set leaves
+ * weights, moments and timestep untouched and backs the scale off (floor
+ * 2^-126); growth_interval good steps in a row grow it.  Accepted on any plan
+ * with Adam state, the fused plan included. */
+int rl_adam_set_scaler(void* plan, void* float_scale, void* int_growth_tracker, void* int_found_inf,
+                       void* int_step_skipped, void* int64_attempted, void* int64_skipped, double growth_factor,
+                       double backoff_factor, int growth_interval);
+/* robolearn/cuda/kernels.cu:856-876: found_inf = 0, then g *= 1/scale over every
+ * gradient of the plan, raising found_inf on any non-finite value. */
+int rl_adam_unscale(void* plan, void* stream);
+
+/* robolearn/cuda/zero_kernels.cuh:53-116: grouped fp32 zero; spans sorted and
+ * disjoint, lengths in floats. */
+void* rl_zero_create(size_t count, const void* const* pointers, const size_t* lengths);
+int rl_zero_step(void* plan, void* stream);
+int rl_zero_destroy(void* plan);
 
 /* robolearn/cuda/flash_kernels.cuh:398-445 (shadows receive bf16 copies) */
 void* rl_flash_projection_create(size_t count, const void* const* first, const void* const* second,
@@ -123,6 +141,9 @@ int rl_rms_backward_ex(int ensemble, const float* x, const float* dy, const floa
                        long long member_stride, float eps, int accumulate_dx, int accumulate_dw, void* stream);
 /* fp32 -> bf16 RNE copy (weight shadows); counterpart of robolearn/cuda/kernels.cu:663-687. */
 int rl_cast_f32_bf16(const float* source, void* destination, long long count, void* stream);
+/* robolearn/cuda/kernels.cu:12, 663-687 under the reference's name: the 16-bit
+ * operand copy, which is bf16 (RNE) on this backend. */
+int rl_cast_f32_f16(const void* source, void* destination, size_t count, void* stream);
 /* Deterministic column sums; replaces robolearn/cuda/kernels.cu:237-251, 742-758. */
 int rl_bias_grad_ex(int ensemble, const float* dy, float* db, float* partial, int rows, int channels, int accumulate,
                     void* stream);
@@ -136,9 +157,21 @@ int rl_flash_bn_forward_with_bf16(const float* x, const float* w, const float* b
                                   float* running_var, float* mean, float* var, float* partial, float* y,
                                   void* half_output, int batch, int channels, float eps, float momentum,
                                   int training, int relu, void* stream);
+/* robolearn/cuda/flash_kernels.cuh:536-542 under the reference's name; half_output
+ * receives bf16. */
+int rl_flash_bn_forward_with_fp16(const float* x, const float* w, const float* b, float* running_mean,
+                                  float* running_var, float* mean, float* var, float* partial, float* y,
+                                  void* half_output, int batch, int channels, float eps, float momentum,
+                                  int training, int relu, void* stream);
 int rl_flash_bn_backward(const float* x, const float* dy, const float* y, const float* w, const float* mean,
                          const float* var, float* partial, float* sums, float* dx, float* dw, float* db, int batch,
                          int channels, float eps, int training, int relu, void* stream);
+/* robolearn/cuda/flash_kernels.cuh:577-584 under the reference's name; half_dx
+ * receives the bf16 rounding of the final (accumulated) dx. */
+int rl_flash_bn_backward_with_fp16(const float* x, const float* dy, const float* y, const float* w,
+                                   const float* mean, const float* var, float* partial, float* sums, float* dx,
+                                   float* dw, float* db, void* half_dx, int batch, int channels, float eps,
+                                   int training, int relu, void* stream);
 int rl_flash_bn_backward_controlled(const float* x, const float* dy, const float* y, const float* w,
                                     const float* mean, const float* var, float* partial, float* sums, float* dx,
                                     float* dw, float* db, void* half_dx, int overwrite_dx, int batch, int channels,

@@ -50,6 +50,11 @@ SIGNATURES = {
     "rl_adam_create": (c_void, [c_size, PP, PP, PP, PP, P, P, P, c_double, c_double, c_double]),
     "rl_adam_step": (c_int, [P, P]),
     "rl_adam_destroy": (c_int, [P]),
+    "rl_adam_set_scaler": (c_int, [P] * 7 + [c_double, c_double, c_int]),
+    "rl_adam_unscale": (c_int, [P, P]),
+    "rl_zero_create": (c_void, [c_size, PP, P]),
+    "rl_zero_step": (c_int, [P, P]),
+    "rl_zero_destroy": (c_int, [P]),
     "rl_flash_projection_create": (c_void, [c_size, PP, PP, P, P]),
     "rl_flash_projection_create_with_shadows": (c_void, [c_size, PP, PP, P, P, PP]),
     "rl_flash_projection_step": (c_int, [P, P]),
@@ -66,9 +71,12 @@ SIGNATURES = {
     "rl_rms_forward_ex": (c_int, [c_int, P, P, P, P, P, c_int, c_int, c_ll, c_float, P]),
     "rl_rms_backward_ex": (c_int, [c_int, P, P, P, P, P, P, P, P, c_int, c_int, c_ll, c_float, c_int, c_int, P]),
     "rl_cast_f32_bf16": (c_int, [P, P, c_ll, P]),
+    "rl_cast_f32_f16": (c_int, [P, P, c_size, P]),
     "rl_bias_grad_ex": (c_int, [c_int, P, P, P, c_int, c_int, c_int, P]),
     "rl_flash_bn_forward": (c_int, [P] * 9 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),
     "rl_flash_bn_forward_with_bf16": (c_int, [P] * 10 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),
+    "rl_flash_bn_forward_with_fp16": (c_int, [P] * 10 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),
+    "rl_flash_bn_backward_with_fp16": (c_int, [P] * 12 + [c_int, c_int, c_float, c_int, c_int, P]),
     "rl_flash_bn_backward": (c_int, [P] * 11 + [c_int, c_int, c_float, c_int, c_int, P]),
     "rl_flash_bn_backward_controlled": (c_int, [P] * 12 + [c_int, c_int, c_int, c_float, c_int, c_int, P]),
     "rl_flash_rms_forward": (c_int, [P, P, P, P, c_int, c_int, c_float, P]),

@@ -1055,12 +1055,38 @@ RL_API int rl_flash_bn_forward_with_bf16(const float* x, const float* w, const f
     });
 }
 
+// robolearn/cuda/flash_kernels.cuh:536-542 under the reference's symbol name.
+// This backend's 16-bit operand format is bf16 (RNE), so half_output receives
+// bf16 bit patterns; the caller allocates it as a 16-bit bf16 buffer.
+RL_API int rl_flash_bn_forward_with_fp16(const float* x, const float* w, const float* b, float* running_mean,
+                                         float* running_var, float* mean, float* var, float* partial, float* y,
+                                         void* half_output, int batch, int channels, float eps, float momentum,
+                                         int training, int relu, void* stream) noexcept {
+    return rl_flash_bn_forward_with_bf16(x, w, b, running_mean, running_var, mean, var, partial, y, half_output, batch,
+                                         channels, eps, momentum, training, relu, stream);
+}
+
 RL_API int rl_flash_bn_backward(const float* x, const float* dy, const float* y, const float* w, const float* mean,
                                 const float* var, float* partial, float* sums, float* dx, float* dw, float* db,
                                 int batch, int channels, float eps, int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_backward", [&] {
         rl::bn_backward(1, x, 0, dy, y, w, nullptr, mean, var, partial, sums, dx, dw, db, nullptr, batch, channels,
                         eps, training, relu, 1, 1, rl::as_stream(stream));
+    });
+}
+
+// robolearn/cuda/flash_kernels.cuh:577-584 under the reference's symbol name;
+// half_dx receives the bf16 rounding of the final dx (accumulating form).
+RL_API int rl_flash_bn_backward_with_fp16(const float* x, const float* dy, const float* y, const float* w,
+                                          const float* mean, const float* var, float* partial, float* sums, float* dx,
+                                          float* dw, float* db, void* half_dx, int batch, int channels, float eps,
+                                          int training, int relu, void* stream) noexcept {
+    return rl::guarded("rl_flash_bn_backward_with_fp16", [&] {
+        rl::require(half_dx != nullptr, "16-bit BN input adjoint must be nonnull.");
+        rl::require(dx != nullptr, "16-bit BN input adjoint requires an fp32 input adjoint.");
+        rl::bn_backward(1, x, 0, dy, y, w, nullptr, mean, var, partial, sums, dx, dw, db,
+                        static_cast<unsigned short*>(half_dx), batch, channels, eps, training, relu, 1, 1,
+                        rl::as_stream(stream));
     });
 }
 
@@ -1132,6 +1158,20 @@ RL_API int rl_cast_f32_bf16(const float* source, void* destination, long long co
         rl::require(source && destination && count > 0, "Cast needs buffers and a positive count.");
         hipLaunchKernelGGL(rl::norm::cast_bf16, dim3(rl::norm::elementwise_blocks(count)), dim3(256), 0,
                            rl::as_stream(stream), source, static_cast<unsigned short*>(destination), count);
+        rl::check_launch("Launch cast");
+    });
+}
+
+// robolearn/cuda/kernels.cu:663-687 under the reference's symbol name: the
+// 16-bit operand copy, bf16 (RNE) on this backend.
+RL_API int rl_cast_f32_f16(const void* source, void* destination, std::size_t count, void* stream) noexcept {
+    return rl::guarded("rl_cast_f32_f16", [&] {
+        rl::require(source && destination && count > 0 && rl::aligned(source, alignof(float)) &&
+                        rl::aligned(destination, 2) && count <= static_cast<std::size_t>(std::numeric_limits<long long>::max()),
+                    "16-bit conversion requires nonempty aligned buffers.");
+        hipLaunchKernelGGL(rl::norm::cast_bf16, dim3(rl::norm::elementwise_blocks(static_cast<long long>(count))),
+                           dim3(256), 0, rl::as_stream(stream), static_cast<const float*>(source),
+                           static_cast<unsigned short*>(destination), static_cast<long long>(count));
         rl::check_launch("Launch cast");
     });
 }

@@ -22,6 +22,7 @@
 // step is graph-capturable.
 #include "common.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <memory>
 #include <vector>
@@ -81,9 +82,8 @@ __device__ double schedule_value(const Schedule& s, double step) {
     return s.peak * (value / s.peak);
 }
 
-__global__ void prepare(float* timestep, float* lr, Schedule schedule, double beta1, double beta2, int form,
-                        const int* skip, Scalars* out) {
-    if (skip && skip[0]) return;
+__device__ __forceinline__ void prepare_body(float* timestep, float* lr, Schedule schedule, double beta1, double beta2,
+                                             int form, Scalars* out) {
     const float t = timestep[0] + 1.0f;
     timestep[0] = t;
     double lr_used = lr[0];
@@ -104,6 +104,41 @@ __global__ void prepare(float* timestep, float* lr, Schedule schedule, double be
     }
     out[0] = s;
 }
+
+__global__ void prepare(float* timestep, float* lr, Schedule schedule, double beta1, double beta2, int form,
+                        const int* skip, Scalars* out) {
+    if (skip && skip[0]) return;
+    prepare_body(timestep, lr, schedule, beta1, beta2, form, out);
+}
+
+// Dynamic loss scaling around an Adam step (robolearn/cuda/kernels.cu:356-405):
+// a step whose unscaled gradients held a non-finite value is skipped and the
+// scale backs off (floored at 2^-126); otherwise the step runs and the scale
+// grows by growth_factor every growth_interval successful steps.
+__global__ void scaled_prepare(float* timestep, float* lr, Schedule schedule, double beta1, double beta2, int form,
+                               float* loss_scale, int* growth_tracker, const int* found_inf, int* step_skipped,
+                               long long* attempted, long long* skipped, float growth_factor, float backoff_factor,
+                               int growth_interval, Scalars* out) {
+    attempted[0] += 1;
+    step_skipped[0] = found_inf[0] != 0;
+    if (step_skipped[0]) {
+        skipped[0] += 1;
+        growth_tracker[0] = 0;
+        loss_scale[0] = fmaxf(loss_scale[0] * backoff_factor, 0x1p-126f);
+        return;
+    }
+    prepare_body(timestep, lr, schedule, beta1, beta2, form, out);
+    const int growth = growth_tracker[0] + 1;
+    if (growth >= growth_interval) {
+        const float increased = loss_scale[0] * growth_factor;
+        if (isfinite(increased)) loss_scale[0] = increased;
+        growth_tracker[0] = 0;
+    } else {
+        growth_tracker[0] = growth;
+    }
+}
+
+__global__ void reset_flag(int* flag) { flag[0] = 0; }
 
 struct StepArgs {
     const Tensor* tensors;
@@ -268,6 +303,76 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepArgs a) {
     }
 }
 
+// Gradient unscale and overflow check (robolearn/cuda/kernels.cu:358-376):
+// g <- g * (1 / scale); found_inf is raised when a gradient, its unscaled
+// value or the scale is non-finite, or the scale is not positive.  Every
+// writer stores the same value 1, so the flag needs no atomic and the result
+// does not depend on wave order.  Same work decomposition as step_kernel.
+__device__ bool unscale_span(float* g, long long length, float inverse, bool bad_scale) {
+    const int lane = threadIdx.x % kWave;
+    bool bad = false;
+    for (long long i = lane; i < length; i += kWave) {
+        const float gradient = g[i];
+        const float unscaled = gradient * inverse;
+        bad = bad || !isfinite(gradient) || !isfinite(unscaled) || bad_scale;
+        g[i] = unscaled;
+    }
+    return bad;
+}
+
+__global__ __launch_bounds__(kThreads) void unscale_kernel(const Tensor* tensors, const Work* work, int work_count,
+                                                           const float* loss_scale, int* found_inf) {
+    const int item = static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x) / kWave;
+    if (item >= work_count) return;
+    const Work w = work[item];
+    const Tensor t = tensors[w.tensor];
+    const float scale = loss_scale[0];
+    const float inverse = 1.0f / scale;
+    const bool bad_scale = !isfinite(scale) || !(scale > 0.0f);
+    long long offset, length;
+    if (t.kind == kPlain) {
+        offset = static_cast<long long>(w.unit) * kChunk;
+        length = min(static_cast<long long>(kChunk), t.cols - offset);
+    } else {
+        offset = static_cast<long long>(w.unit) * t.cols;
+        length = t.cols;
+    }
+    bool bad = unscale_span(const_cast<float*>(t.part[0].g) + offset, length, inverse, bad_scale);
+    if (t.kind == kBatchNormPair) bad = unscale_span(const_cast<float*>(t.part[1].g) + offset, length, inverse, bad_scale) || bad;
+    if (bad) found_inf[0] = 1;
+}
+
+// Grouped zero of fp32 spans (robolearn/cuda/zero_kernels.cuh:38-48): one
+// 256-thread workgroup per span chunk of up to kZeroChunk floats, 16-byte
+// stores where the chunk start allows.
+constexpr unsigned kZeroChunk = 4096;
+
+struct ZeroBlock {
+    float* pointer;
+    unsigned length;
+};
+
+__global__ __launch_bounds__(kThreads) void zero_kernel(const ZeroBlock* blocks) {
+    const ZeroBlock block = blocks[blockIdx.x];
+    unsigned head = 0;
+    if (reinterpret_cast<std::uintptr_t>(block.pointer) % 16 == 0) {
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        f32x4* vectors = reinterpret_cast<f32x4*>(block.pointer);
+        const unsigned count = block.length / 4;
+        for (unsigned i = threadIdx.x; i < count; i += kThreads) vectors[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        head = count * 4;
+    }
+    for (unsigned i = head + threadIdx.x; i < block.length; i += kThreads) block.pointer[i] = 0.0f;
+}
+
+struct ZeroPlan {
+    ZeroBlock* blocks = nullptr;
+    unsigned count = 0;
+    ~ZeroPlan() {
+        if (blocks) (void)hipFree(blocks);
+    }
+};
+
 struct Plan {
     Tensor* tensors = nullptr;
     Work* work = nullptr;
@@ -282,6 +387,15 @@ struct Plan {
     int has_adam = 0;
     int has_projection = 0;
     int has_ema = 0;
+    // dynamic loss scaling (reference-compatible rl_adam_set_scaler); null when unused
+    float* loss_scale = nullptr;
+    int* growth_tracker = nullptr;
+    int* found_inf = nullptr;
+    int* step_skipped = nullptr;
+    long long* attempted_steps = nullptr;
+    long long* skipped_steps = nullptr;
+    float growth_factor = 2.0f, backoff_factor = 0.5f;
+    int growth_interval = 2000;
 
     ~Plan() {
         if (tensors) (void)hipFree(tensors);
@@ -334,7 +448,16 @@ std::unique_ptr<Plan> build(std::vector<Tensor> tensors) {
 void step(Plan* plan, int do_adam, int do_project, int do_ema, const int* skip, hipStream_t stream) {
     require(plan != nullptr, "Optimizer plan is null.");
     require(!do_adam || plan->has_adam, "This plan has no Adam state.");
-    if (do_adam) {
+    if (do_adam && plan->loss_scale) {
+        require(skip == nullptr, "A plan with dynamic loss scaling takes its skip flag from the scaler.");
+        hipLaunchKernelGGL(scaled_prepare, dim3(1), dim3(1), 0, stream, plan->timestep, plan->lr, plan->schedule,
+                           plan->beta1, plan->beta2, plan->form, plan->loss_scale, plan->growth_tracker,
+                           static_cast<const int*>(plan->found_inf), plan->step_skipped, plan->attempted_steps,
+                           plan->skipped_steps, plan->growth_factor, plan->backoff_factor, plan->growth_interval,
+                           plan->scalars);
+        check_launch("Launch optimizer scaled prepare");
+        skip = plan->step_skipped;
+    } else if (do_adam) {
         hipLaunchKernelGGL(prepare, dim3(1), dim3(1), 0, stream, plan->timestep, plan->lr, plan->schedule, plan->beta1,
                            plan->beta2, plan->form, skip, plan->scalars);
         check_launch("Launch optimizer prepare");
@@ -357,6 +480,16 @@ void step(Plan* plan, int do_adam, int do_project, int do_ema, const int* skip, 
     a.skip = skip;
     hipLaunchKernelGGL(step_kernel, dim3(ceil_div(plan->work_count, kWaves)), dim3(kThreads), 0, stream, a);
     check_launch("Launch fused optimizer step");
+}
+
+void unscale(Plan* plan, hipStream_t stream) {
+    require(plan != nullptr && plan->loss_scale != nullptr, "Unscale requires an Adam plan with dynamic loss scaling.");
+    hipLaunchKernelGGL(reset_flag, dim3(1), dim3(1), 0, stream, plan->found_inf);
+    check_launch("Launch loss-scale flag reset");
+    hipLaunchKernelGGL(unscale_kernel, dim3(ceil_div(plan->work_count, kWaves)), dim3(kThreads), 0, stream,
+                       static_cast<const Tensor*>(plan->tensors), static_cast<const Work*>(plan->work), plan->work_count,
+                       static_cast<const float*>(plan->loss_scale), plan->found_inf);
+    check_launch("Launch gradient unscale");
 }
 
 }  // namespace opt
@@ -513,6 +646,92 @@ RL_API int rl_adam_step(void* plan, void* stream) noexcept {
 RL_API int rl_adam_destroy(void* plan) noexcept {
     rl::clear_error();
     delete static_cast<Plan*>(plan);
+    return 0;
+}
+
+// robolearn/cuda/kernels.cu:822-854: attach persistent device state for
+// dynamic loss scaling.  Works on any plan with Adam state (the fused plan too).
+RL_API int rl_adam_set_scaler(void* plan, void* loss_scale, void* growth_tracker, void* found_inf, void* step_skipped,
+                              void* attempted_steps, void* skipped_steps, double growth_factor, double backoff_factor,
+                              int growth_interval) noexcept {
+    return rl::guarded("rl_adam_set_scaler", [&] {
+        rl::require(plan && loss_scale && growth_tracker && found_inf && step_skipped && attempted_steps && skipped_steps,
+                    "Dynamic loss scaling requires persistent device state.");
+        rl::require(rl::aligned(loss_scale, alignof(float)) && rl::aligned(growth_tracker, alignof(int)) &&
+                        rl::aligned(found_inf, alignof(int)) && rl::aligned(step_skipped, alignof(int)) &&
+                        rl::aligned(attempted_steps, alignof(long long)) && rl::aligned(skipped_steps, alignof(long long)),
+                    "Dynamic loss scaling state has invalid alignment.");
+        rl::require(std::isfinite(growth_factor) && growth_factor > 1.0 && std::isfinite(backoff_factor) &&
+                        backoff_factor > 0.0 && backoff_factor < 1.0 && growth_interval > 0,
+                    "Dynamic scale growth/backoff/interval are invalid.");
+        auto* p = static_cast<Plan*>(plan);
+        rl::require(p->has_adam, "Dynamic loss scaling needs a plan with Adam state.");
+        p->loss_scale = static_cast<float*>(loss_scale);
+        p->growth_tracker = static_cast<int*>(growth_tracker);
+        p->found_inf = static_cast<int*>(found_inf);
+        p->step_skipped = static_cast<int*>(step_skipped);
+        p->attempted_steps = static_cast<long long*>(attempted_steps);
+        p->skipped_steps = static_cast<long long*>(skipped_steps);
+        p->growth_factor = static_cast<float>(growth_factor);
+        p->backoff_factor = static_cast<float>(backoff_factor);
+        p->growth_interval = growth_interval;
+    });
+}
+
+// robolearn/cuda/kernels.cu:856-876: clear found_inf, then unscale and check
+// every gradient of the plan.  Call once after backward, before clipping/step.
+RL_API int rl_adam_unscale(void* plan, void* stream) noexcept {
+    return rl::guarded("rl_adam_unscale", [&] { rl::opt::unscale(static_cast<Plan*>(plan), rl::as_stream(stream)); });
+}
+
+// robolearn/cuda/zero_kernels.cuh:53-116: sorted, disjoint fp32 spans
+// (lengths in floats) cleared by one launch.  The descriptor table is copied
+// at creation; step only enqueues the kernel, so it is graph-capturable.
+RL_API void* rl_zero_create(std::size_t count, const void* const* pointers, const std::size_t* lengths) noexcept {
+    return rl::guarded_ptr("rl_zero_create", [&]() -> void* {
+        using rl::opt::ZeroBlock;
+        rl::require(count && pointers && lengths, "Zero plan requires nonempty host pointer/length tables.");
+        std::vector<ZeroBlock> blocks;
+        std::uintptr_t previous_end = 0;
+        for (std::size_t i = 0; i < count; ++i) {
+            const auto start = reinterpret_cast<std::uintptr_t>(pointers[i]);
+            rl::require(start && rl::aligned(pointers[i], alignof(float)) && lengths[i],
+                        "Zero plan requires aligned, nonempty fp32 spans.");
+            rl::require(lengths[i] <= (std::numeric_limits<std::uintptr_t>::max() - start) / sizeof(float),
+                        "Zero span pointer arithmetic overflows.");
+            rl::require(start >= previous_end, "Zero spans must be sorted and nonoverlapping.");
+            previous_end = start + lengths[i] * sizeof(float);
+            const std::size_t chunks = (lengths[i] - 1) / rl::opt::kZeroChunk + 1;
+            rl::require(chunks <= static_cast<std::size_t>(std::numeric_limits<int>::max()) - blocks.size(),
+                        "Zero plan block count exceeds the grid limit.");
+            float* base = static_cast<float*>(const_cast<void*>(pointers[i]));
+            for (std::size_t offset = 0; offset < lengths[i]; offset += rl::opt::kZeroChunk) {
+                const std::size_t remaining = lengths[i] - offset;
+                blocks.push_back({base + offset, static_cast<unsigned>(std::min<std::size_t>(remaining, rl::opt::kZeroChunk))});
+            }
+        }
+        auto plan = std::make_unique<rl::opt::ZeroPlan>();
+        rl::check_hip(hipMalloc(&plan->blocks, blocks.size() * sizeof(ZeroBlock)), "Allocate grouped-zero descriptors");
+        rl::check_hip(hipMemcpy(plan->blocks, blocks.data(), blocks.size() * sizeof(ZeroBlock), hipMemcpyHostToDevice),
+                      "Copy grouped-zero descriptors");
+        plan->count = static_cast<unsigned>(blocks.size());
+        return plan.release();
+    });
+}
+
+RL_API int rl_zero_step(void* plan, void* stream) noexcept {
+    return rl::guarded("rl_zero_step", [&] {
+        rl::require(plan != nullptr, "Zero plan is null.");
+        const auto* p = static_cast<const rl::opt::ZeroPlan*>(plan);
+        hipLaunchKernelGGL(rl::opt::zero_kernel, dim3(p->count), dim3(rl::opt::kThreads), 0, rl::as_stream(stream),
+                           static_cast<const rl::opt::ZeroBlock*>(p->blocks));
+        rl::check_launch("Launch grouped zero");
+    });
+}
+
+RL_API int rl_zero_destroy(void* plan) noexcept {
+    rl::clear_error();
+    delete static_cast<rl::opt::ZeroPlan*>(plan);
     return 0;
 }
 

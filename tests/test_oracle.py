@@ -309,3 +309,94 @@ def test_gaussian_kl_closed_form():
     expected = torch.distributions.kl_divergence(torch.distributions.Normal(old_mean, old_std),
                                                  torch.distributions.Normal(new_mean, new_std)).sum(-1)
     torch.testing.assert_close(kl, expected)
+
+
+# ---------------------------------------------------------------------------
+# native optimizer plans: Adam, loss scaling
+# ---------------------------------------------------------------------------
+from oracle import optim as OO  # noqa: E402
+
+
+def test_native_adam_matches_torch_adam():
+    rng = np.random.default_rng(3)
+    shapes = [(7,), (33, 5)]
+    params = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+    torch_params = [torch.tensor(p.copy(), requires_grad=True) for p in params]
+    adam = torch.optim.Adam(torch_params, lr=3e-3, betas=(0.9, 0.999), eps=1e-8)
+    m1 = [np.zeros_like(p) for p in params]
+    m2 = [np.zeros_like(p) for p in params]
+    state = {"timestep": np.float32(0)}
+    for _ in range(6):
+        grads = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+        OO.native_adam_step(params, grads, m1, m2, state, 3e-3, 0.9, 0.999, 1e-8)
+        for tp, g in zip(torch_params, grads):
+            tp.grad = torch.tensor(g)
+        adam.step()
+    assert state["timestep"] == 6
+    for p, tp in zip(params, torch_params):
+        np.testing.assert_allclose(p, tp.detach().numpy(), rtol=1e-6, atol=1e-7)
+
+
+def test_native_adam_first_step_closed_form():
+    g = np.array([3.0, -0.5, 1e-3, 0.0], np.float32)
+    p = np.zeros(4, np.float32)
+    OO.native_adam_step([p], [g.copy()], [np.zeros(4, np.float32)], [np.zeros(4, np.float32)],
+                        {"timestep": np.float32(0)}, 0.1, 0.9, 0.99, 1e-8)
+    np.testing.assert_allclose(p, -0.1 * g / (np.abs(g) + 1e-8), rtol=1e-5)
+
+
+def _torch_scale_sequence(found, scale, growth, backoff, interval):
+    s = torch.tensor([scale], dtype=torch.float32)
+    tracker = torch.zeros(1, dtype=torch.int32)
+    out = []
+    for f in found:
+        torch._amp_update_scale_(s, tracker, torch.tensor([float(f)]), growth, backoff, interval)
+        out.append((float(s[0]), int(tracker[0])))
+    return out
+
+
+def test_scaled_prepare_matches_torch_update_scale():
+    found = [0, 0, 1, 0, 0, 0, 1, 1, 0, 0, 0, 0, 0]
+    state = {"loss_scale": np.float32(65536.0), "growth_tracker": 0, "step_skipped": 0, "attempted": 0,
+             "skipped": 0}
+    expected = _torch_scale_sequence(found, 65536.0, 2.0, 0.5, 3)
+    for f, (scale, tracker) in zip(found, expected):
+        ran = OO.scaled_prepare(state, f, 2.0, 0.5, 3)
+        assert ran == (f == 0)
+        assert state["loss_scale"] == np.float32(scale) and state["growth_tracker"] == tracker
+    assert state["attempted"] == len(found) and state["skipped"] == sum(found)
+
+
+def test_scaled_prepare_floor_and_overflow_guard():
+    state = {"loss_scale": np.float32(2.0**-125), "growth_tracker": 0, "step_skipped": 0, "attempted": 0,
+             "skipped": 0}
+    for _ in range(4):
+        OO.scaled_prepare(state, 1, 2.0, 0.5, 1)
+    assert state["loss_scale"] == np.float32(2.0**-126)
+    state["loss_scale"] = np.float32(3.0e38)
+    OO.scaled_prepare(state, 0, 2.0, 0.5, 1)
+    assert state["loss_scale"] == np.float32(3.0e38) and state["growth_tracker"] == 0
+
+
+@pytest.mark.parametrize("poison", [None, np.inf, -np.inf, np.nan])
+def test_unscale_matches_torch_check(poison):
+    rng = np.random.default_rng(4)
+    grads = [rng.standard_normal(n).astype(np.float32) * 1024 for n in (5, 300)]
+    if poison is not None:
+        grads[1][17] = poison
+    torch_grads = [torch.tensor(g.copy()) for g in grads]
+    found_t = torch.zeros(1)
+    torch._amp_foreach_non_finite_check_and_unscale_(torch_grads, found_t, torch.tensor([1.0 / 1024]))
+    found = OO.unscale(grads, 1024.0)
+    assert found == int(found_t[0])
+    for g, t in zip(grads, torch_grads):
+        np.testing.assert_array_equal(np.isfinite(g), np.isfinite(t.numpy()))
+        np.testing.assert_array_equal(g[np.isfinite(g)], t.numpy()[np.isfinite(g)])
+
+
+def test_unscale_reference_only_cases():
+    # finite gradient whose unscaled value overflows; non-positive scale
+    assert OO.unscale([np.array([3.0e38], np.float32)], 0.5) == 1
+    assert OO.unscale([np.array([1.0], np.float32)], 0.0) == 1
+    assert OO.unscale([np.array([1.0], np.float32)], -2.0) == 1
+    assert OO.unscale([np.array([1.0, 2.0], np.float32)], 4.0) == 0
