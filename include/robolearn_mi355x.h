@@ -240,11 +240,11 @@ int rl_tanh_gaussian_backward(const float* head, const float* noise, const float
                               long long grad_rows, const float* dlog_probs, float* dhead, void* dhead_bf16,
                               long long rows, int action_dim, void* stream);
 /* Actor loss, entropy, mean action and their gradients (robolearn/flashsac/updates.py:105-137,
- * robolearn/warp/flashsac.py:109-153). */
+ * robolearn/warp/flashsac.py:109-153).  partial: 5 * ceil(total_rows / 256) + 1 floats. */
 int rl_actor_objective(const float* q0, const float* q1, const float* log_probs, const float* actions,
                        long long ld_actions, const float* replay_actions, const float* alpha, float bc_alpha,
                        long long batch, long long total_rows, int action_dim, float* metrics, float* dlog_probs,
-                       float* dq0, float* dq1, float* dactions_bc, void* stream);
+                       float* dq0, float* dq1, float* dactions_bc, float* partial, void* stream);
 /* Temperature loss and gradient (robolearn/flashsac/updates.py:297-326). */
 int rl_temperature_objective(const float* log_temp, const float* entropy, float target_entropy, float* grad,
                              float* metrics, void* stream);

@@ -98,7 +98,7 @@ SIGNATURES = {
     "rl_concat_columns": (c_int, [P, c_ll, c_ll, P, c_ll, c_int, P, c_ll, c_int, P]),
     "rl_tanh_gaussian_forward": (c_int, [P, P, P, c_ll, P, c_ll, c_int, c_int, P]),
     "rl_tanh_gaussian_backward": (c_int, [P, P, P, c_ll, c_ll, P, P, P, c_ll, c_int, P]),
-    "rl_actor_objective": (c_int, [P, P, P, P, c_ll, P, P, c_float, c_ll, c_ll, c_int, P, P, P, P, P, P]),
+    "rl_actor_objective": (c_int, [P, P, P, P, c_ll, P, P, c_float, c_ll, c_ll, c_int, P, P, P, P, P, P, P]),
     "rl_temperature_objective": (c_int, [P, P, c_float, P, P, P]),
     "rl_exp_scalar": (c_int, [P, P, P]),
     "rl_fill": (c_int, [P, c_ll, c_float, P]),

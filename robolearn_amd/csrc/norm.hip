@@ -87,21 +87,41 @@ __global__ __launch_bounds__(kThreads) void bn_moments(const float* x, long long
     }
 }
 
-// Combines chunk moments in order; writes batch mean / biased variance and
-// updates running statistics (lerp by momentum, unbiased variance).
-__global__ void bn_statistics(const float* partial, float* mean_out, float* var_out, float* running_mean,
-                              float* running_var, int rows, int channels, int chunks, int ensemble, float momentum,
-                              int update_running) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= ensemble * channels) return;
-    const int e = idx / channels;
-    const int c = idx % channels;
+// Combines the chunk moments of each (member, channel) column; writes batch
+// mean / biased variance and updates running statistics (lerp by momentum,
+// unbiased variance).  A workgroup covers kStatCols columns with kStatGroups
+// threads each: group g merges chunks g, g + kStatGroups, ... in order, then
+// group 0 merges the group results in order, so the result is deterministic
+// and each thread's dependent chain is chunks / kStatGroups merges long.
+constexpr int kStatCols = 32;
+constexpr int kStatGroups = 8;
+
+__global__ __launch_bounds__(kStatCols* kStatGroups) void bn_statistics(const float* partial, float* mean_out,
+                                                                        float* var_out, float* running_mean,
+                                                                        float* running_var, int rows, int channels,
+                                                                        int chunks, int ensemble, float momentum,
+                                                                        int update_running) {
+    const int col = threadIdx.x % kStatCols;
+    const int group = threadIdx.x / kStatCols;
+    const int idx = blockIdx.x * kStatCols + col;
+    const bool live = idx < ensemble * channels;
+    const int e = live ? idx / channels : 0;
+    const int c = live ? idx % channels : 0;
     float count = 0.0f, mean = 0.0f, m2 = 0.0f;
-    for (int k = 0; k < chunks; ++k) {
-        const float* in = partial + (static_cast<long long>(e) * chunks + k) * 2 * channels;
-        const float n = static_cast<float>(min(kChunk, rows - k * kChunk));
-        merge(count, mean, m2, n, in[c], in[channels + c]);
+    if (live) {
+        for (int k = group; k < chunks; k += kStatGroups) {
+            const float* in = partial + (static_cast<long long>(e) * chunks + k) * 2 * channels;
+            const float n = static_cast<float>(min(kChunk, rows - k * kChunk));
+            merge(count, mean, m2, n, in[c], in[channels + c]);
+        }
     }
+    __shared__ float s_count[kStatGroups][kStatCols], s_mean[kStatGroups][kStatCols], s_m2[kStatGroups][kStatCols];
+    s_count[group][col] = count;
+    s_mean[group][col] = mean;
+    s_m2[group][col] = m2;
+    __syncthreads();
+    if (group != 0 || !live) return;
+    for (int g = 1; g < kStatGroups; ++g) merge(count, mean, m2, s_count[g][col], s_mean[g][col], s_m2[g][col]);
     const float var = m2 / static_cast<float>(rows);
     mean_out[idx] = mean;
     var_out[idx] = var;
@@ -430,17 +450,33 @@ __global__ __launch_bounds__(kThreads) void bn_grad_partials(const float* x, lon
 }
 
 // sums[0][pc] = mean(dy'), sums[1][pc] = mean(dy' * xhat); dw (+)= sum(dy' xhat), db (+)= sum(dy').
-__global__ void bn_grad_reduce(const float* partial, float* sums, float* dw, float* db, int rows, int channels,
-                               int chunks, int ensemble, int accumulate) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= ensemble * channels) return;
-    const int e = idx / channels;
-    const int c = idx % channels;
+// Sums the chunk partials of each column (same decomposition and fixed order
+// as bn_statistics); sums = (mean dy', mean dy' xhat), dw/db (+)= the totals.
+__global__ __launch_bounds__(kStatCols* kStatGroups) void bn_grad_reduce(const float* partial, float* sums, float* dw,
+                                                                         float* db, int rows, int channels, int chunks,
+                                                                         int ensemble, int accumulate) {
+    const int col = threadIdx.x % kStatCols;
+    const int group = threadIdx.x / kStatCols;
+    const int idx = blockIdx.x * kStatCols + col;
+    const bool live = idx < ensemble * channels;
+    const int e = live ? idx / channels : 0;
+    const int c = live ? idx % channels : 0;
     float s0 = 0.0f, s1 = 0.0f;
-    for (int k = 0; k < chunks; ++k) {
-        const float* in = partial + (static_cast<long long>(e) * chunks + k) * 2 * channels;
-        s0 += in[c];
-        s1 += in[channels + c];
+    if (live) {
+        for (int k = group; k < chunks; k += kStatGroups) {
+            const float* in = partial + (static_cast<long long>(e) * chunks + k) * 2 * channels;
+            s0 += in[c];
+            s1 += in[channels + c];
+        }
+    }
+    __shared__ float s_0[kStatGroups][kStatCols], s_1[kStatGroups][kStatCols];
+    s_0[group][col] = s0;
+    s_1[group][col] = s1;
+    __syncthreads();
+    if (group != 0 || !live) return;
+    for (int g = 1; g < kStatGroups; ++g) {
+        s0 += s_0[g][col];
+        s1 += s_1[g][col];
     }
     sums[idx] = s0 / static_cast<float>(rows);
     sums[ensemble * channels + idx] = s1 / static_cast<float>(rows);
@@ -829,7 +865,8 @@ void bn_forward(int ensemble, const float* x, long long x_stride, const float* w
                                channels, chunks);
         }
         check_launch("Launch BN moments");
-        hipLaunchKernelGGL(norm::bn_statistics, dim3(ceil_div(ensemble * channels, 256)), dim3(256), 0, stream,
+        hipLaunchKernelGGL(norm::bn_statistics, dim3(ceil_div(ensemble * channels, norm::kStatCols)),
+                           dim3(norm::kStatCols * norm::kStatGroups), 0, stream,
                            partial, mean, var, running_mean, running_var, rows, channels, chunks, ensemble, momentum,
                            update_running && running_mean && running_var ? 1 : 0);
         check_launch("Launch BN statistics");
@@ -878,7 +915,8 @@ void bn_backward(int ensemble, const float* x, long long x_stride, const float* 
                                mean, var, partial, rows, channels, chunks, eps, relu);
         }
         check_launch("Launch BN gradient partials");
-        hipLaunchKernelGGL(norm::bn_grad_reduce, dim3(ceil_div(ensemble * channels, 256)), dim3(256), 0, stream,
+        hipLaunchKernelGGL(norm::bn_grad_reduce, dim3(ceil_div(ensemble * channels, norm::kStatCols)),
+                           dim3(norm::kStatCols * norm::kStatGroups), 0, stream,
                            partial, sums, dw, db, rows, channels, chunks, ensemble, accumulate_params);
         check_launch("Launch BN gradient reduce");
     }

@@ -158,16 +158,23 @@ __device__ __forceinline__ float softplus(float x) {
 }
 
 // head[r, :A] = mean, head[r, A:2A] = raw log-std (bias already added).
-// Writes actions (ld_actions stride), log pi and optionally std.
-__global__ void tanh_gaussian_forward(const float* head, const float* noise, float* actions, long long ld_actions,
-                                      float* log_probs, long long rows, int action_dim, int deterministic) {
-    const long long r = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
-    if (r >= rows) return;
+// Writes actions (ld_actions stride), log pi and optionally std.  One wave per
+// row (kPolicyRows rows per workgroup): lane j handles actions j, j + 64, ...
+// with coalesced loads, and log pi is a fixed-order wave sum.
+constexpr int kPolicyRows = 4;
+
+__global__ __launch_bounds__(kPolicyRows* kWave) void tanh_gaussian_forward(const float* head, const float* noise,
+                                                                           float* actions, long long ld_actions,
+                                                                           float* log_probs, long long rows,
+                                                                           int action_dim, int deterministic) {
+    const long long r = static_cast<long long>(blockIdx.x) * kPolicyRows + threadIdx.x / kWave;
+    if (r >= rows) return;  // wave-uniform
+    const int lane = threadIdx.x % kWave;
     const float* h = head + r * 2 * action_dim;
     const float half_log_two_pi = 0.91893853320467274178f;  // log(sqrt(2 pi))
     const float ln2 = 0.69314718055994530942f;
     float lp = 0.0f;
-    for (int j = 0; j < action_dim; ++j) {
+    for (int j = lane; j < action_dim; j += kWave) {
         const float mean = h[j];
         if (deterministic) {
             actions[r * ld_actions + j] = tanhf(mean);
@@ -183,112 +190,139 @@ __global__ void tanh_gaussian_forward(const float* head, const float* noise, flo
         const float correction = 2.0f * (ln2 - raw - softplus(-2.0f * raw));
         lp += log_normal - correction;
     }
-    if (log_probs && !deterministic) log_probs[r] = lp;
+    if (log_probs && !deterministic) {
+        lp = wave_sum(lp);
+        if (lane == 0) log_probs[r] = lp;
+    }
 }
 
 // Backward of the head given dL/da (rows < grad_rows, else zero) and dL/dlogpi.
-// dhead[r, :A] = dL/dmean, dhead[r, A:] = dL/draw_log_std.
+// dhead[r, :A] = dL/dmean, dhead[r, A:] = dL/draw_log_std.  One thread per
+// (row, action) element.
 __global__ void tanh_gaussian_backward(const float* head, const float* noise, const float* dactions,
                                        long long ld_dactions, long long grad_rows, const float* dlog_probs,
                                        float* dhead, unsigned short* dhead_bf16, long long rows, int action_dim) {
-    const long long r = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
-    if (r >= rows) return;
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= rows * action_dim) return;
+    const long long r = idx / action_dim;
+    const int j = static_cast<int>(idx - r * action_dim);
     const float* h = head + r * 2 * action_dim;
     const float dlp = dlog_probs ? dlog_probs[r] : 0.0f;
-    for (int j = 0; j < action_dim; ++j) {
-        const float mean = h[j];
-        const float t = tanhf(h[action_dim + j]);
-        const float log_std = -10.0f + 6.0f * (1.0f + t);
-        const float std = expf(log_std);
-        const float eps = noise[r * action_dim + j];
-        const float raw = mean + eps * std;
-        const float a = tanhf(raw);
-        const float da = (dactions && r < grad_rows) ? dactions[r * ld_dactions + j] : 0.0f;
-        const float g_raw = da * (1.0f - a * a) + dlp * 2.0f * a;
-        const float dstd = g_raw * eps - dlp / std;
-        const float dlog_std = dstd * std;
-        const float g_std = dlog_std * 6.0f * (1.0f - t * t);
-        if (dhead) {
-            dhead[r * 2 * action_dim + j] = g_raw;
-            dhead[r * 2 * action_dim + action_dim + j] = g_std;
-        }
-        if (dhead_bf16) {
-            dhead_bf16[r * 2 * action_dim + j] = f32_to_bf16_bits(g_raw);
-            dhead_bf16[r * 2 * action_dim + action_dim + j] = f32_to_bf16_bits(g_std);
-        }
+    const float mean = h[j];
+    const float t = tanhf(h[action_dim + j]);
+    const float log_std = -10.0f + 6.0f * (1.0f + t);
+    const float std = expf(log_std);
+    const float eps = noise[idx];
+    const float raw = mean + eps * std;
+    const float a = tanhf(raw);
+    const float da = (dactions && r < grad_rows) ? dactions[r * ld_dactions + j] : 0.0f;
+    const float g_raw = da * (1.0f - a * a) + dlp * 2.0f * a;
+    const float dstd = g_raw * eps - dlp / std;
+    const float dlog_std = dstd * std;
+    const float g_std = dlog_std * 6.0f * (1.0f - t * t);
+    if (dhead) {
+        dhead[r * 2 * action_dim + j] = g_raw;
+        dhead[r * 2 * action_dim + action_dim + j] = g_std;
+    }
+    if (dhead_bf16) {
+        dhead_bf16[r * 2 * action_dim + j] = f32_to_bf16_bits(g_raw);
+        dhead_bf16[r * 2 * action_dim + action_dim + j] = f32_to_bf16_bits(g_std);
     }
 }
 
-// Single-workgroup actor objective over the first `batch` rows:
+// Actor objective over the first `batch` rows:
 //   q = min(q0, q1); loss = mean(alpha logpi - q) [+ bc term];
 //   entropy = -mean(logpi); mean_action = mean(a).
-// Gradients: dlogpi (2B rows, zero past batch), dq [2, batch], daction_bc
-// (optional, batch x A) for the behaviour-cloning term.
-constexpr int kObjThreads = 1024;
+// Gradients: dlogpi (total_rows rows, zero past batch), dq [2, batch],
+// daction_bc (optional, batch x A) for the behaviour-cloning term.
+// objective_rows: one thread per row; each workgroup writes its kObjTerms
+// partial sums to partial[block * kObjTerms + term].  objective_finish adds
+// the partials in block order and writes the metrics and, for the bc term,
+// mean |q| to partial[blocks * kObjTerms]; bc_gradient then scales the
+// per-element differences by it.
+constexpr int kObjThreads = 256;
+constexpr int kObjTerms = 5;  // |q|, log pi, action, bc squared difference, alpha log pi - q
 
-__device__ float block_sum_1024(float v, float* s) {
-    s[threadIdx.x] = v;
-    __syncthreads();
-    for (int stride = kObjThreads / 2; stride > 0; stride >>= 1) {
-        if (static_cast<int>(threadIdx.x) < stride) s[threadIdx.x] += s[threadIdx.x + stride];
-        __syncthreads();
-    }
-    const float total = s[0];
-    __syncthreads();
-    return total;
-}
-
-__global__ __launch_bounds__(kObjThreads) void actor_objective(const float* q0, const float* q1, const float* log_probs,
-                                                               const float* actions, long long ld_actions,
-                                                               const float* replay_actions, const float* alpha,
-                                                               float bc_alpha, long long batch, long long total_rows,
-                                                               int action_dim, float* metrics, float* dlog_probs,
-                                                               float* dq0, float* dq1, float* dactions_bc) {
-    __shared__ float s[kObjThreads];
+__global__ __launch_bounds__(kObjThreads) void objective_rows(const float* q0, const float* q1, const float* log_probs,
+                                                              const float* actions, long long ld_actions,
+                                                              const float* replay_actions, const float* alpha,
+                                                              float bc_alpha, long long batch, long long total_rows,
+                                                              int action_dim, float* dlog_probs, float* dq0,
+                                                              float* dq1, float* partial) {
+    __shared__ float scratch[kObjThreads / kWave];
     const float a = alpha[0];
     const float inv = 1.0f / static_cast<float>(batch);
-    float qabs = 0.0f, lp_sum = 0.0f, act_sum = 0.0f, bc_sum = 0.0f;
-    for (long long i = threadIdx.x; i < batch; i += kObjThreads) {
-        const float q = fminf(q0[i], q1[i]);
-        qabs += fabsf(q);
-        lp_sum += log_probs[i];
-        for (int j = 0; j < action_dim; ++j) act_sum += actions[i * ld_actions + j];
-        if (bc_alpha > 0.0f) {
-            for (int j = 0; j < action_dim; ++j) {
-                const float d = actions[i * ld_actions + j] - replay_actions[i * action_dim + j];
-                bc_sum += d * d;
-            }
-        }
-    }
-    qabs = block_sum_1024(qabs, s) * inv;
-    lp_sum = block_sum_1024(lp_sum, s);
-    act_sum = block_sum_1024(act_sum, s);
-    bc_sum = block_sum_1024(bc_sum, s);
-    float loss_sum = 0.0f;
-    for (long long i = threadIdx.x; i < batch; i += kObjThreads) {
+    const long long row0 = static_cast<long long>(blockIdx.x) * kObjThreads;
+    const long long i = row0 + threadIdx.x;
+    float terms[kObjTerms] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (i < batch) {
         const float x0 = q0[i], x1 = q1[i];
         const float q = fminf(x0, x1);
-        loss_sum += a * log_probs[i] - q;
+        const float lp = log_probs[i];
+        terms[0] = fabsf(q);
+        terms[1] = lp;
+        terms[4] = a * lp - q;
         dlog_probs[i] = a * inv;
         dq0[i] = -inv * (x0 < x1 ? 1.0f : (x0 == x1 ? 0.5f : 0.0f));
         dq1[i] = -inv * (x1 < x0 ? 1.0f : (x0 == x1 ? 0.5f : 0.0f));
-        if (dactions_bc) {
-            for (int j = 0; j < action_dim; ++j) {
-                const float d = actions[i * ld_actions + j] - replay_actions[i * action_dim + j];
-                dactions_bc[i * action_dim + j] =
-                    bc_alpha > 0.0f ? bc_alpha * qabs * 2.0f * d / static_cast<float>(batch * action_dim) : 0.0f;
-            }
+    } else if (i < total_rows) {
+        dlog_probs[i] = 0.0f;
+    }
+    // this workgroup's rows of the action matrix, walked as one flat range
+    const long long rows_here = max(0LL, min(batch, row0 + kObjThreads) - row0);
+    const long long elements = rows_here * action_dim;
+    for (long long e = threadIdx.x; e < elements; e += kObjThreads) {
+        const long long r = row0 + e / action_dim;
+        const int j = static_cast<int>(e % action_dim);
+        const float v = actions[r * ld_actions + j];
+        terms[2] += v;
+        if (bc_alpha > 0.0f) {
+            const float d = v - replay_actions[r * action_dim + j];
+            terms[3] += d * d;
         }
     }
-    for (long long i = batch + threadIdx.x; i < total_rows; i += kObjThreads) dlog_probs[i] = 0.0f;
-    loss_sum = block_sum_1024(loss_sum, s);
-    if (threadIdx.x == 0) {
-        float loss = loss_sum * inv;
-        if (bc_alpha > 0.0f) loss += bc_alpha * qabs * (bc_sum / static_cast<float>(batch * action_dim));
-        metrics[0] = loss;
-        metrics[1] = -lp_sum * inv;
-        metrics[2] = act_sum / static_cast<float>(batch * action_dim);
+#pragma unroll
+    for (int t = 0; t < kObjTerms; ++t) {
+        const float total = block_sum<kObjThreads>(terms[t], scratch);
+        if (threadIdx.x == 0) partial[static_cast<long long>(blockIdx.x) * kObjTerms + t] = total;
     }
+}
+
+__global__ __launch_bounds__(kObjThreads) void objective_finish(const float* partial_in, int blocks, float bc_alpha,
+                                                                long long batch, int action_dim, float* metrics,
+                                                                float* qabs_out) {
+    __shared__ float scratch[kObjThreads / kWave];
+    float totals[kObjTerms];
+#pragma unroll
+    for (int t = 0; t < kObjTerms; ++t) {
+        float v = 0.0f;
+        for (int b = threadIdx.x; b < blocks; b += kObjThreads) v += partial_in[static_cast<long long>(b) * kObjTerms + t];
+        totals[t] = block_sum<kObjThreads>(v, scratch);
+    }
+    if (threadIdx.x != 0) return;
+    const float inv = 1.0f / static_cast<float>(batch);
+    const float qabs = totals[0] * inv;
+    const float count = static_cast<float>(batch * action_dim);
+    float loss = totals[4] * inv;
+    if (bc_alpha > 0.0f) loss += bc_alpha * qabs * (totals[3] / count);
+    metrics[0] = loss;
+    metrics[1] = -totals[1] * inv;
+    metrics[2] = totals[2] / count;
+    qabs_out[0] = qabs;
+}
+
+__global__ void bc_gradient(const float* actions, long long ld_actions, const float* replay_actions, float bc_alpha,
+                            const float* qabs, long long batch, int action_dim, float* dactions_bc) {
+    const long long idx = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= batch * action_dim) return;
+    if (!(bc_alpha > 0.0f)) {
+        dactions_bc[idx] = 0.0f;
+        return;
+    }
+    const long long r = idx / action_dim;
+    const int j = static_cast<int>(idx - r * action_dim);
+    const float d = actions[r * ld_actions + j] - replay_actions[idx];
+    dactions_bc[idx] = bc_alpha * qabs[0] * 2.0f * d / static_cast<float>(batch * action_dim);
 }
 
 // Temperature objective: value = exp(log_temp); loss = value (entropy - H*);
@@ -400,7 +434,8 @@ RL_API int rl_tanh_gaussian_forward(const float* head, const float* noise, float
     return rl::guarded("rl_tanh_gaussian_forward", [&] {
         rl::require(head && actions && rows > 0 && action_dim > 0 && (deterministic || noise),
                     "Policy forward needs head, noise and actions.");
-        hipLaunchKernelGGL(P::tanh_gaussian_forward, dim3(rl::ceil_div(rows, 256)), dim3(256), 0,
+        hipLaunchKernelGGL(P::tanh_gaussian_forward, dim3(rl::ceil_div(rows, P::kPolicyRows)),
+                           dim3(P::kPolicyRows * rl::kWave), 0,
                            rl::as_stream(stream), head, noise, actions, ld_actions, log_probs, rows, action_dim,
                            deterministic);
         rl::check_launch("Launch policy forward");
@@ -413,7 +448,7 @@ RL_API int rl_tanh_gaussian_backward(const float* head, const float* noise, cons
     return rl::guarded("rl_tanh_gaussian_backward", [&] {
         rl::require(head && noise && (dhead || dhead_bf16) && rows > 0 && action_dim > 0,
                     "Policy backward needs head, noise and an output.");
-        hipLaunchKernelGGL(P::tanh_gaussian_backward, dim3(rl::ceil_div(rows, 256)), dim3(256), 0,
+        hipLaunchKernelGGL(P::tanh_gaussian_backward, dim3(rl::ceil_div(rows * action_dim, 256)), dim3(256), 0,
                            rl::as_stream(stream), head, noise, dactions, ld_dactions, grad_rows, dlog_probs, dhead,
                            static_cast<unsigned short*>(dhead_bf16), rows, action_dim);
         rl::check_launch("Launch policy backward");
@@ -423,16 +458,28 @@ RL_API int rl_tanh_gaussian_backward(const float* head, const float* noise, cons
 RL_API int rl_actor_objective(const float* q0, const float* q1, const float* log_probs, const float* actions,
                               long long ld_actions, const float* replay_actions, const float* alpha, float bc_alpha,
                               long long batch, long long total_rows, int action_dim, float* metrics, float* dlog_probs,
-                              float* dq0, float* dq1, float* dactions_bc, void* stream) noexcept {
+                              float* dq0, float* dq1, float* dactions_bc, float* partial, void* stream) noexcept {
     return rl::guarded("rl_actor_objective", [&] {
-        rl::require(q0 && q1 && log_probs && actions && alpha && metrics && dlog_probs && dq0 && dq1,
-                    "Actor objective needs Q values, log-probs, actions, alpha and outputs.");
+        rl::require(q0 && q1 && log_probs && actions && alpha && metrics && dlog_probs && dq0 && dq1 && partial,
+                    "Actor objective needs Q values, log-probs, actions, alpha, outputs and partial scratch.");
         rl::require(batch > 0 && total_rows >= batch && action_dim > 0, "Actor objective shapes are invalid.");
         rl::require(bc_alpha <= 0.0f || replay_actions, "Behaviour cloning needs replay actions.");
-        hipLaunchKernelGGL(P::actor_objective, dim3(1), dim3(P::kObjThreads), 0, rl::as_stream(stream), q0, q1,
-                           log_probs, actions, ld_actions, replay_actions, alpha, bc_alpha, batch, total_rows,
-                           action_dim, metrics, dlog_probs, dq0, dq1, dactions_bc);
-        rl::check_launch("Launch actor objective");
+        const hipStream_t st = rl::as_stream(stream);
+        const unsigned blocks = rl::ceil_div(total_rows, P::kObjThreads);
+        hipLaunchKernelGGL(P::objective_rows, dim3(blocks), dim3(P::kObjThreads), 0, st, q0, q1, log_probs, actions,
+                           ld_actions, replay_actions, alpha, bc_alpha, batch, total_rows, action_dim, dlog_probs, dq0,
+                           dq1, partial);
+        rl::check_launch("Launch actor objective rows");
+        float* qabs = partial + static_cast<long long>(blocks) * P::kObjTerms;
+        hipLaunchKernelGGL(P::objective_finish, dim3(1), dim3(P::kObjThreads), 0, st, static_cast<const float*>(partial),
+                           static_cast<int>(blocks), bc_alpha, batch, action_dim, metrics, qabs);
+        rl::check_launch("Launch actor objective finish");
+        if (dactions_bc) {
+            hipLaunchKernelGGL(P::bc_gradient, dim3(rl::ceil_div(batch * action_dim, 256)), dim3(256), 0, st, actions,
+                               ld_actions, replay_actions, bc_alpha, static_cast<const float*>(qabs), batch,
+                               action_dim, dactions_bc);
+            rl::check_launch("Launch behaviour-cloning gradient");
+        }
     });
 }
 

@@ -234,6 +234,7 @@ class FlashSAC:
             self.alpha = z(1)
             self.temperature_grad_metrics = z(2)
             self.metrics_buffer = z(len(METRIC_KEYS))
+            self.objective_partial = z(5 * ((2 * B + 255) // 256) + 1)
             self.bias_partial = z(2 * K.chunks(2 * B) * max(2 * A, cfg.critic_num_bins))
             self.support = torch.linspace(cfg.critic_min_v, cfg.critic_max_v, cfg.critic_num_bins,
                                           dtype=torch.float32).to(dev)
@@ -509,7 +510,8 @@ class FlashSAC:
                      self.actions_all.data_ptr(), A, self.batch["action"].data_ptr(), self.alpha.data_ptr(),
                      float(cfg.actor_bc_alpha), B, 2 * B, A, self.metrics_buffer.data_ptr(),
                      self.dlog_probs.data_ptr(), self.dq.data_ptr(), self.dq[1].data_ptr(),
-                     self.dactions_bc.data_ptr() if cfg.actor_bc_alpha > 0 else None, K.stream())
+                     self.dactions_bc.data_ptr() if cfg.actor_bc_alpha > 0 else None,
+                     self.objective_partial.data_ptr(), K.stream())
         # critic backward to the action inputs (parameters frozen, BN in eval mode)
         bf = self.mode == K.BF16
         K.categorical_head_backward_q(self.logits, self.support, self.dq, None if bf else self.dlogits, rows=B,
