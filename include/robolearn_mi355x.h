@@ -47,14 +47,17 @@ int rl_plan_destroy(void* plan);
  * (mode 0: fp32 v_mfma_f32_32x32x2_f32, mode 1: bf16 v_mfma_f32_32x32x16_bf16).
  * A(m,k) = a_kcontig ? A[m*lda+k] : A[k*lda+m]; B(k,n) = b_kcontig ? B[n*ldb+k]
  * : B[k*ldb+n].  epilogue 0 none, 1 ReLU, 2 ELU.  splits > 1 reduces over K in
- * fixed order through workspace; d_bf16 (optional) receives a bf16 copy of D.  Serves the three plans of one Linear,
- * robolearn/cuda/linear.py:179-185, 341-360, and the ensemble einsum of
- * robolearn/flashsac/layers.py:174-186. */
+ * fixed order through workspace; d_bf16 (optional) receives a bf16 copy of D.
+ * moments (optional, needs ldd == n) receives the per-256-row-chunk column
+ * (mean, M2) of D in rl_bn_forward_ex's partial layout [batch][ceil(m/256)][2][n],
+ * from the GEMM epilogue when the 256x256 bf16 kernel runs the product.
+ * Serves the three plans of one Linear, robolearn/cuda/linear.py:179-185,
+ * 341-360, and the ensemble einsum of robolearn/flashsac/layers.py:174-186. */
 int rl_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int m, int n, int k, int batch,
             const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
             const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
             float beta, int epilogue, int splits, float* workspace, size_t workspace_bytes, void* d_bf16,
-            void* stream);
+            float* moments, void* stream);
 size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, int splits);
 
 /* ---- optimizer ---------------------------------------------------------- */
@@ -121,11 +124,12 @@ int rl_flash_ema_destroy(void* plan);
  * residual is added after the ReLU (fuses robolearn/flashsac/layers.py:105-113);
  * y or y_bf16 may be NULL (at least one output).
  * Replaces robolearn/cuda/flash_kernels.cuh:500-543 for the stacked critics of
- * robolearn/flashsac/layers.py:189-222.  partial: ensemble*2*ceil(rows/256)*channels. */
+ * robolearn/flashsac/layers.py:189-222.  partial: ensemble*2*ceil(rows/256)*channels;
+ * moments_ready: partial already holds x's chunk moments (rl_gemm's moments output). */
 int rl_bn_forward_ex(int ensemble, const float* x, long long x_stride, const float* w, const float* b,
                      float* running_mean, float* running_var, float* mean, float* var, float* partial,
                      const float* residual, float* y, void* y_bf16, int rows, int channels, float eps,
-                     float momentum, int training, int relu, int update_running, void* stream);
+                     float momentum, int training, int relu, int update_running, int moments_ready, void* stream);
 /* y == NULL with relu recomputes the ReLU mask from x, the statistics and (w, b).
  * sums: 2*ensemble*channels.  Replaces flash_kernels.cuh:545-609. */
 int rl_bn_backward_ex(int ensemble, const float* x, long long x_stride, const float* dy, const float* y,

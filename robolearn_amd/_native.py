@@ -32,7 +32,7 @@ SIGNATURES = {
     "rl_last_error": (c_char_p, []),
     # dense
     "rl_gemm": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, P, c_ll, c_ll, P, c_ll, c_ll,
-                        P, P, c_ll, c_ll, P, c_ll, c_float, c_int, c_int, P, c_size, P, P]),
+                        P, P, c_ll, c_ll, P, c_ll, c_float, c_int, c_int, P, c_size, P, P, P]),
     "rl_gemm_workspace": (c_size, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "rl_plan_create": (c_void, [c_int] * 10 + [c_size]),
     "rl_plan_create_mixed": (c_void, [c_int] * 11 + [c_size]),
@@ -65,7 +65,7 @@ SIGNATURES = {
     "rl_flash_ema_destroy": (c_int, [P]),
     # normalization
     "rl_bn_forward_ex": (c_int, [c_int, P, c_ll, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_float, c_float, c_int,
-                                 c_int, c_int, P]),
+                                 c_int, c_int, c_int, P]),
     "rl_bn_backward_ex": (c_int, [c_int, P, c_ll, P, P, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_float, c_int,
                                   c_int, c_int, c_int, P]),
     "rl_rms_forward_ex": (c_int, [c_int, P, P, P, P, P, c_int, c_int, c_ll, c_float, P]),

@@ -309,7 +309,7 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
              const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
              const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
              float beta, int epilogue, int splits, float* workspace, std::size_t workspace_bytes, hipStream_t stream,
-             unsigned short* d_bf16) {
+             unsigned short* d_bf16, float* moments) {
     require(mode == 0 || mode == 1, "GEMM mode must be 0 (fp32) or 1 (bf16 operands).");
     require(!(mode == 0 && (a_bf16 || b_bf16)), "fp32 GEMM mode requires fp32 operands.");
     require(m > 0 && n > 0 && k > 0 && batch > 0, "GEMM dimensions must be positive.");
@@ -318,6 +318,8 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     require(epilogue >= 0 && epilogue <= 2, "Unknown GEMM epilogue.");
     require(splits >= 1, "GEMM split count must be positive.");
     require(static_cast<long long>(m) * n <= std::numeric_limits<int>::max(), "GEMM output exceeds 2^31 elements.");
+    require(!moments || (ldd == n && aligned(moments, 16)),
+            "GEMM output moments need a row-contiguous output (ldd == n) and 16-byte aligned storage.");
     gemm::Params p{};
     p.a = a;
     p.b = b;
@@ -360,6 +362,11 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     } else {
         p.d = d;
     }
+    // Column moments come from the 256x256 kernel's epilogue when it runs this
+    // product in direct mode with the identity epilogue; otherwise from a pass over D.
+    const bool fused_moments = moments && mode == 1 && splits == 1 && !bias && epilogue == 0 && beta == 0.0f &&
+                               gemm::big_eligible(p, a_bf16, b_bf16);
+    p.moments = fused_moments ? moments : nullptr;
     if (mode == 0) gemm::launch_mode<0>(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
     else gemm::launch_bf16(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
     check_launch("Launch GEMM");
@@ -370,6 +377,7 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
                            stride_d, stride_bias, m, n, batch, splits, beta, epilogue);
         check_launch("Launch split-K reduction");
     }
+    if (moments && !fused_moments) bn_chunk_moments(batch, d, stride_d, moments, m, n, stream);
     return 0;
 }
 
@@ -379,11 +387,11 @@ RL_API int rl_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kconti
                    const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
                    const float* c, float* d, long long ldd, long long stride_d, const float* bias,
                    long long stride_bias, float beta, int epilogue, int splits, float* workspace,
-                   std::size_t workspace_bytes, void* d_bf16, void* stream) noexcept {
+                   std::size_t workspace_bytes, void* d_bf16, float* moments, void* stream) noexcept {
     return rl::guarded("rl_gemm", [&] {
         rl::run_gemm(mode, a_bf16, b_bf16, a_kcontig, b_kcontig, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
                      d, ldd, stride_d, bias, stride_bias, beta, epilogue, splits, workspace, workspace_bytes,
-                     rl::as_stream(stream), static_cast<unsigned short*>(d_bf16));
+                     rl::as_stream(stream), static_cast<unsigned short*>(d_bf16), moments);
     });
 }
 

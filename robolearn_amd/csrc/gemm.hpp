@@ -31,6 +31,7 @@ struct Params {
     int epilogue;        // Epilogue (direct mode only)
     int a_vec, b_vec;    // 16-byte vector loads allowed
     unsigned short* d_bf16;  // optional bf16 copy of the output (direct mode only)
+    float* moments;      // optional per-256-row-chunk (mean, M2) of D: [batch][m / 256][2][n]
 };
 
 __device__ __forceinline__ float apply_epilogue(float v, int epilogue) {
@@ -47,4 +48,18 @@ bool big_eligible(const Params& p, int a_bf16, int b_bf16);
 void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream);
 
 }  // namespace gemm
+
+// Row-major batched GEMM with optional split-K, bf16 copy and output column
+// moments (gemm.hip); the argument contract is rl_gemm's.
+int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int m, int n, int k, int batch,
+             const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
+             const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
+             float beta, int epilogue, int splits, float* workspace, std::size_t workspace_bytes, hipStream_t stream,
+             unsigned short* d_bf16, float* moments);
+
+// Per-256-row-chunk column moments of a row-major [ensemble][rows][channels]
+// fp32 tensor into partial[e][chunk][2][channels] (norm.hip).
+void bn_chunk_moments(int ensemble, const float* x, long long x_stride, float* partial, int rows, int channels,
+                      hipStream_t stream);
+
 }  // namespace rl

@@ -199,6 +199,19 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Chan's pairwise merge of (count, mean, M2) column moments, four columns at once.
+__device__ __forceinline__ void merge4(float& count, float4& mean, float4& m2, float count_b, float4 mean_b,
+                                       float4 m2_b) {
+    const float total = count + count_b;
+    const float fb = count_b / total;
+    const float fab = count * count_b / total;
+    const float4 d = make_float4(mean_b.x - mean.x, mean_b.y - mean.y, mean_b.z - mean.z, mean_b.w - mean.w);
+    mean = make_float4(mean.x + d.x * fb, mean.y + d.y * fb, mean.z + d.z * fb, mean.w + d.w * fb);
+    m2 = make_float4(m2.x + m2_b.x + d.x * d.x * fab, m2.y + m2_b.y + d.y * d.y * fab, m2.z + m2_b.z + d.z * d.z * fab,
+                     m2.w + m2_b.w + d.w * d.w * fab);
+    count = total;
+}
+
 // Writes one finished 256x256 tile: D = act(acc + bias) + beta C (and the bf16
 // copy) in direct mode, the raw partial tile in split-K mode.  `lds` must hold
 // 4 x 32 x EP floats and be free; the caller's last LDS reads must be complete.
@@ -222,6 +235,15 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
     float4 bias4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (direct && p.bias) bias4 = *reinterpret_cast<const float4*>(p.bias + tile.batch * p.stride_bias + col);
     float* stage = static_cast<float*>(lds) + wave * 32 * EP;
+    // Column moments for a BatchNorm that consumes D (identity epilogue only):
+    // the tile's 256 rows are one 256-row statistics chunk.  Each lane sees 4
+    // columns x 16 rows of every staged 32-row block: exact two-pass moments of
+    // those 16 rows (the second pass rereads the staged block), merged over the
+    // 4 blocks, then with lane l ^ 32 (the other row parity) and with the wave of
+    // the other row half, always in the same order.
+    const bool moments = direct && p.moments != nullptr;
+    float count = 0.0f;
+    float4 mean = make_float4(0.0f, 0.0f, 0.0f, 0.0f), m2 = mean;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         lds_barrier();  // the previous block (or the K loop) is done with LDS
@@ -231,6 +253,27 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
             for (int v = 0; v < 16; ++v)
                 stage[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * EP + j * 32 + lane % 32] = acc[i][j][v];
         lds_barrier();
+        if (moments) {
+            float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int r = 0; r < 16; ++r) {
+                const float4 v = *reinterpret_cast<const float4*>(stage + (2 * r + lane / 32) * EP + 4 * c4);
+                s = make_float4(s.x + v.x, s.y + v.y, s.z + v.z, s.w + v.w);
+            }
+            const float4 bm = make_float4(s.x * (1.0f / 16), s.y * (1.0f / 16), s.z * (1.0f / 16), s.w * (1.0f / 16));
+            float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int r = 0; r < 16; ++r) {
+                const float4 v = *reinterpret_cast<const float4*>(stage + (2 * r + lane / 32) * EP + 4 * c4);
+                const float4 d = make_float4(v.x - bm.x, v.y - bm.y, v.z - bm.z, v.w - bm.w);
+                q = make_float4(q.x + d.x * d.x, q.y + d.y * d.y, q.z + d.z * d.z, q.w + d.w * d.w);
+            }
+            if (i == 0) {
+                count = 16.0f;
+                mean = bm;
+                m2 = q;
+            } else {
+                merge4(count, mean, m2, 16.0f, bm, q);
+            }
+        }
 #pragma unroll 4
         for (int r = 0; r < 16; ++r) {
             const int row = 2 * r + lane / 32;
@@ -251,6 +294,35 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
                         make_uint2(f32x2_to_bf16x2(val.x, val.y), f32x2_to_bf16x2(val.z, val.w));
             }
             *reinterpret_cast<float4*>(D + offset) = val;
+        }
+    }
+    if (moments) {
+        // lanes l < 32 hold rows of parity 0, l >= 32 parity 1: merge parity 0 first
+        const float4 om = make_float4(__shfl_xor(mean.x, 32), __shfl_xor(mean.y, 32), __shfl_xor(mean.z, 32),
+                                      __shfl_xor(mean.w, 32));
+        const float4 oq = make_float4(__shfl_xor(m2.x, 32), __shfl_xor(m2.y, 32), __shfl_xor(m2.z, 32),
+                                      __shfl_xor(m2.w, 32));
+        if (lane >= 32) {
+            float4 t = mean, u = m2;
+            mean = om;
+            m2 = oq;
+            merge4(count, mean, m2, 64.0f, t, u);
+        } else {
+            merge4(count, mean, m2, 64.0f, om, oq);
+        }
+        float* xs = static_cast<float*>(lds);  // [2][2][256]: (mean, M2) of each row half
+        lds_barrier();                          // every wave is done with its staging
+        if (wm == 1 && lane < 32) {
+            *reinterpret_cast<float4*>(xs + wn * 128 + 4 * c4) = mean;
+            *reinterpret_cast<float4*>(xs + BN + wn * 128 + 4 * c4) = m2;
+        }
+        lds_barrier();
+        if (wm == 0 && lane < 32) {
+            merge4(count, mean, m2, 128.0f, *reinterpret_cast<const float4*>(xs + wn * 128 + 4 * c4),
+                   *reinterpret_cast<const float4*>(xs + BN + wn * 128 + 4 * c4));
+            float* out = p.moments + (static_cast<long long>(tile.batch) * (p.m / BM) + tile.m0 / BM) * 2 * p.n + col;
+            *reinterpret_cast<float4*>(out) = mean;
+            *reinterpret_cast<float4*>(out + p.n) = m2;
         }
     }
 }
@@ -323,7 +395,7 @@ __global__ __launch_bounds__(T, 1) void gemm_big_kernel(Params p, int tiles_m, i
 // ---------------------------------------------------------------------------
 // Forward products (both operands K-contiguous): tiles move global -> LDS by
 // DMA (global_load_lds_dwordx4, 16 bytes per lane straight into LDS), through
-// a ring of DS = 4 LDS stages issued three K tiles ahead.  No VGPR staging and
+// a ring of DS = 4 LDS stages issued four K tiles ahead.  No VGPR staging and
 // no LDS store instructions.  Each stage holds the A and B tiles unpadded
 // (64-byte rows) with 16-byte chunks XOR-swizzled by swz(row), which keeps the
 // fragment reads free of bank conflicts for 8- and 16-lane groups.
@@ -401,11 +473,12 @@ __device__ __forceinline__ void mfma_frags(const Frags& f, f32x16_t (&acc)[4][4]
 // One step of the DMA pipeline: barrier (the DMA of the next tile has landed in
 // every wave, every wave is done with the stage `refill`), DMA of a later tile
 // into `refill`, the next tile's fragment reads, then this tile's MFMAs from
-// registers while those reads land.
+// registers while those reads land.  Two later tiles (16 DMA instructions per
+// wave) may still be in flight at the barrier.
 template <class Fetch>
 __device__ __forceinline__ void dma_step(Fetch&& fetch, int k_tile, unsigned short* refill, const unsigned short* next,
                                          const Frags& cur, Frags& nxt, int wm, int wn, f32x16_t (&acc)[4][4]) {
-    dma_barrier<8>();
+    dma_barrier<16>();
     fetch(k_tile, refill);
     read_frags(next, wm, wn, nxt);
     __builtin_amdgcn_sched_barrier(0);
@@ -450,19 +523,21 @@ __global__ __launch_bounds__(T, 1) void gemm_dma_kernel(Params p, int tiles_m, i
         fetch(0, lds[0]);
         fetch(1, lds[1]);
         fetch(2, lds[2]);
-        // Step kt computes tile kt (stage kt % DS) from registers while reading
-        // tile kt + 1's fragments; its barrier waits for the DMA of tiles <= kt + 1
-        // (each wave has 8 DMA instructions per tile, so tile kt + 2's 8 may stay
-        // in flight) and for every wave to finish step kt - 1, whose stage
-        // ((kt + 3) % DS) then takes tile kt + 3.  nk is a multiple of 4.
+        fetch(3, lds[3]);
+        // Step kt computes tile kt from registers while reading tile kt + 1's
+        // fragments (stage (kt + 1) % DS).  Its barrier waits for the DMA of tiles
+        // <= kt + 1 (each wave has 8 DMA instructions per tile, so those of tiles
+        // kt + 2 and kt + 3 may stay in flight) and for every wave's reads of
+        // stage kt % DS, issued in step kt - 1, which then takes tile kt + 4.
+        // nk is a multiple of 4.
         Frags f0, f1;
-        dma_barrier<8>();
+        dma_barrier<24>();
         read_frags(lds[0], wm, wn, f0);
         for (int kt = 0; kt < nk; kt += DS) {
-            dma_step(fetch, kt + 3, lds[3], lds[1], f0, f1, wm, wn, acc);
-            dma_step(fetch, kt + 4, lds[0], lds[2], f1, f0, wm, wn, acc);
-            dma_step(fetch, kt + 5, lds[1], lds[3], f0, f1, wm, wn, acc);
-            dma_step(fetch, kt + 6, lds[2], lds[0], f1, f0, wm, wn, acc);
+            dma_step(fetch, kt + 4, lds[0], lds[1], f0, f1, wm, wn, acc);
+            dma_step(fetch, kt + 5, lds[1], lds[2], f1, f0, wm, wn, acc);
+            dma_step(fetch, kt + 6, lds[2], lds[3], f0, f1, wm, wn, acc);
+            dma_step(fetch, kt + 7, lds[3], lds[0], f1, f0, wm, wn, acc);
         }
         dma_barrier<0>();  // the redundant tail DMAs have landed and every wave is past its last reads
         store_tile(p, tile, acc, &lds[0][0], wave, wm, wn);

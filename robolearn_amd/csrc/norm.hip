@@ -842,10 +842,26 @@ inline unsigned elementwise_blocks(long long total) {
 
 int chunks_for(int rows) { return (rows + norm::kChunk - 1) / norm::kChunk; }
 
+// Per-256-row-chunk (mean, M2) of every column: partial[e][chunk][2][channels].
+void bn_chunk_moments(int ensemble, const float* x, long long x_stride, float* partial, int rows, int channels,
+                      hipStream_t stream) {
+    const int chunks = chunks_for(rows);
+    if (channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && aligned(partial, 16)) {
+        const dim3 grid(ceil_div(channels / 4, norm::kVecCols), chunks, ensemble);
+        hipLaunchKernelGGL(norm::bn_moments_vec, grid, dim3(norm::kThreads), 0, stream, x, x_stride, partial, rows,
+                           channels, chunks);
+    } else {
+        const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
+        hipLaunchKernelGGL(norm::bn_moments, grid, dim3(norm::kThreads), 0, stream, x, x_stride, partial, rows,
+                           channels, chunks);
+    }
+    check_launch("Launch BN moments");
+}
+
 void bn_forward(int ensemble, const float* x, long long x_stride, const float* w, const float* b, float* running_mean,
                 float* running_var, float* mean, float* var, float* partial, const float* residual, float* y,
                 unsigned short* y_bf16, int rows, int channels, float eps, float momentum, int training, int relu,
-                int update_running, hipStream_t stream) {
+                int update_running, int moments_ready, hipStream_t stream) {
     require(ensemble > 0 && rows > 0 && channels > 0, "BatchNorm dimensions must be positive.");
     require(static_cast<long long>(rows) * channels <= std::numeric_limits<int>::max(), "BatchNorm exceeds 2^31 elements.");
     require(std::isfinite(eps) && eps >= 0.0f && std::isfinite(momentum), "BatchNorm eps/momentum are invalid.");
@@ -855,16 +871,7 @@ void bn_forward(int ensemble, const float* x, long long x_stride, const float* w
     if (training) {
         require(mean && var && partial, "Training BatchNorm requires mean, var and partial scratch.");
         const int chunks = chunks_for(rows);
-        if (channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && aligned(partial, 16)) {
-            const dim3 grid(ceil_div(channels / 4, norm::kVecCols), chunks, ensemble);
-            hipLaunchKernelGGL(norm::bn_moments_vec, grid, dim3(norm::kThreads), 0, stream, x, x_stride, partial, rows,
-                               channels, chunks);
-        } else {
-            const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
-            hipLaunchKernelGGL(norm::bn_moments, grid, dim3(norm::kThreads), 0, stream, x, x_stride, partial, rows,
-                               channels, chunks);
-        }
-        check_launch("Launch BN moments");
+        if (!moments_ready) bn_chunk_moments(ensemble, x, x_stride, partial, rows, channels, stream);
         hipLaunchKernelGGL(norm::bn_statistics, dim3(ceil_div(ensemble * channels, norm::kStatCols)),
                            dim3(norm::kStatCols * norm::kStatGroups), 0, stream,
                            partial, mean, var, running_mean, running_var, rows, channels, chunks, ensemble, momentum,
@@ -1023,11 +1030,12 @@ void bias_grad(int ensemble, const float* dy, float* db, float* partial, int row
 RL_API int rl_bn_forward_ex(int ensemble, const float* x, long long x_stride, const float* w, const float* b,
                             float* running_mean, float* running_var, float* mean, float* var, float* partial,
                             const float* residual, float* y, void* y_bf16, int rows, int channels, float eps,
-                            float momentum, int training, int relu, int update_running, void* stream) noexcept {
+                            float momentum, int training, int relu, int update_running, int moments_ready,
+                            void* stream) noexcept {
     return rl::guarded("rl_bn_forward_ex", [&] {
         rl::bn_forward(ensemble, x, x_stride, w, b, running_mean, running_var, mean, var, partial, residual, y,
                        static_cast<unsigned short*>(y_bf16), rows, channels, eps, momentum, training, relu,
-                       update_running, rl::as_stream(stream));
+                       update_running, moments_ready, rl::as_stream(stream));
     });
 }
 
@@ -1077,7 +1085,7 @@ RL_API int rl_flash_bn_forward(const float* x, const float* w, const float* b, f
                                float momentum, int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_forward", [&] {
         rl::bn_forward(1, x, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y, nullptr, batch, channels,
-                       eps, momentum, training, relu, 1, rl::as_stream(stream));
+                       eps, momentum, training, relu, 1, 0, rl::as_stream(stream));
     });
 }
 
@@ -1089,7 +1097,7 @@ RL_API int rl_flash_bn_forward_with_bf16(const float* x, const float* w, const f
         rl::require(half_output != nullptr, "bf16 BN output must be nonnull.");
         rl::bn_forward(1, x, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y,
                        static_cast<unsigned short*>(half_output), batch, channels, eps, momentum, training, relu, 1,
-                       rl::as_stream(stream));
+                       0, rl::as_stream(stream));
     });
 }
 

@@ -8,7 +8,7 @@
 // columns its m.  input_dtype 1 means 16-bit operands in memory, which on
 // MI355X are bf16 (RNE) instead of fp16; input_dtype 2 keeps fp32 storage and
 // rounds operands to bf16 on load.  Split-K uses the caller's workspace.
-#include "common.hpp"
+#include "gemm.hpp"
 
 #include <cmath>
 #include <memory>
@@ -17,11 +17,6 @@
 namespace rl {
 thread_local char last_error[512] = "";
 
-int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int m, int n, int k, int batch,
-             const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
-             const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
-             float beta, int epilogue, int splits, float* workspace, std::size_t workspace_bytes, hipStream_t stream,
-             unsigned short* d_bf16);
 }
 
 extern "C" std::size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, int splits) noexcept;
@@ -141,7 +136,7 @@ RL_API int rl_plan_run(void* opaque, const void* a, const void* b, const void* c
         rl::run_gemm(plan->mode, bf, bf, a_kcontig, b_kcontig, plan->n, plan->m, plan->k, 1, b, plan->ldb, 0, a,
                      plan->lda, 0, static_cast<const float*>(c), static_cast<float*>(d), plan->ldd, 0,
                      plan->use_bias ? static_cast<const float*>(bias) : nullptr, 0, beta, 0, plan->splits,
-                     static_cast<float*>(workspace), workspace_bytes, rl::as_stream(stream), nullptr);
+                     static_cast<float*>(workspace), workspace_bytes, rl::as_stream(stream), nullptr, nullptr);
     });
 }
 

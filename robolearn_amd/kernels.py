@@ -40,26 +40,29 @@ def _is_bf16(tensor: torch.Tensor) -> int:
 def gemm(
     a, b, d, *, m, n, k, batch=1, a_kcontig, b_kcontig, lda, ldb, ldd, stride_a=0, stride_b=0, stride_d=0,
     c=None, beta=0.0, bias=None, stride_bias=0, epilogue=None, mode=FP32, splits=1, workspace=None, d_bf16=None,
+    moments=None,
 ):
-    """Row-major batched D = act(op(A) op(B) + bias) + beta * C (optional bf16 copy of D)."""
+    """Row-major batched D = act(op(A) op(B) + bias) + beta * C (optional bf16 copy of D and
+    per-256-row-chunk column moments of D for a following BatchNorm)."""
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _native.call(
         "rl_gemm", mode, _is_bf16(a), _is_bf16(b), int(a_kcontig), int(b_kcontig), m, n, k, batch, ptr(a), lda,
         stride_a, ptr(b), ldb, stride_b, ptr(c), ptr(d), ldd, stride_d, ptr(bias), stride_bias, float(beta),
-        EPILOGUES[epilogue], splits, ptr(workspace), ws_bytes, ptr(d_bf16), stream(),
+        EPILOGUES[epilogue], splits, ptr(workspace), ws_bytes, ptr(d_bf16), ptr(moments), stream(),
     )
 
 
 def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None, bias=None, epilogue=None,
-                   mode=FP32, c=None, beta=0.0, d_bf16=None):
-    """y[e] = act(x[e] w[e]^T + bias[e]) (+ beta c); x_stride 0 broadcasts x."""
+                   mode=FP32, c=None, beta=0.0, d_bf16=None, moments=None):
+    """y[e] = act(x[e] w[e]^T + bias[e]) (+ beta c); x_stride 0 broadcasts x; moments receives
+    y's per-256-row-chunk column moments (the BatchNorm partial layout)."""
     if x_stride is None:
         x_stride = rows * in_dim
     _check(w, ensemble * out_dim * in_dim, "weight", w.dtype)
     _check(y, ensemble * rows * out_dim, "output")
     gemm(x, w, y, m=rows, n=out_dim, k=in_dim, batch=ensemble, a_kcontig=True, b_kcontig=True, lda=in_dim,
          ldb=in_dim, ldd=out_dim, stride_a=x_stride, stride_b=out_dim * in_dim, stride_d=rows * out_dim, bias=bias,
-         stride_bias=out_dim, epilogue=epilogue, mode=mode, c=c, beta=beta, d_bf16=d_bf16)
+         stride_bias=out_dim, epilogue=epilogue, mode=mode, c=c, beta=beta, d_bf16=d_bf16, moments=moments)
 
 
 def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=FP32, c=None, beta=0.0,
@@ -103,13 +106,15 @@ def linear_backward_weight(dy, x, dw, *, rows, in_dim, out_dim, ensemble=1, x_st
 # ---------------------------------------------------------------------------
 def bn_forward(x, w, b, running_mean, running_var, mean, var, partial, y, *, rows, channels, ensemble=1,
                x_stride=None, eps=1e-5, momentum=0.01, training=True, relu=False, update_running=True, y_bf16=None,
-               residual=None):
-    """y = act(BN(x)) [+ residual]; x_stride 0 broadcasts one input to every member."""
+               residual=None, moments_ready=False):
+    """y = act(BN(x)) [+ residual]; x_stride 0 broadcasts one input to every member.
+
+    moments_ready: partial already holds x's chunk moments (written by the producing GEMM)."""
     if x_stride is None:
         x_stride = rows * channels
     _native.call("rl_bn_forward_ex", ensemble, ptr(x), x_stride, ptr(w), ptr(b), ptr(running_mean), ptr(running_var),
                  ptr(mean), ptr(var), ptr(partial), ptr(residual), ptr(y), ptr(y_bf16), rows, channels, eps, momentum,
-                 int(training), int(relu), int(update_running), stream())
+                 int(training), int(relu), int(update_running), int(moments_ready), stream())
 
 
 def bn_backward(x, dy, y, w, mean, var, partial, sums, dx, dw, db, *, rows, channels, ensemble=1, x_stride=None,

@@ -274,21 +274,23 @@ class Trunk:
                d_bf16=self.stream_h[0])
         for i in range(self.blocks):
             pre = f"encoder.{i}"
+            # in training the GEMM also writes the BatchNorm's chunk moments of its output
+            moments = self.partial if training else None
             K.linear_forward(self.op(self.stream[i], self.stream_h[i]), w[f"{pre}.w1{self.linear}"], self.u1[i],
-                             rows=rows, in_dim=h, out_dim=4 * h, ensemble=E, mode=mode)
+                             rows=rows, in_dim=h, out_dim=4 * h, ensemble=E, mode=mode, moments=moments)
             mean, var = self.stats[pre + ".norm1"]
             K.bn_forward(self.u1[i], p[pre + ".norm1.weight"], p[pre + ".norm1.bias"],
                          running[pre + ".norm1.running_mean"], running[pre + ".norm1.running_var"], mean, var,
                          self.partial, self.r1[i], rows=rows, channels=4 * h, ensemble=E, training=training,
-                         relu=True, update_running=update_running, y_bf16=self.r1_h[i])
+                         relu=True, update_running=update_running, y_bf16=self.r1_h[i], moments_ready=training)
             K.linear_forward(self.op(self.r1[i], self.r1_h[i]), w[f"{pre}.w2{self.linear}"], self.u2[i], rows=rows,
-                             in_dim=4 * h, out_dim=h, ensemble=E, mode=mode)
+                             in_dim=4 * h, out_dim=h, ensemble=E, mode=mode, moments=moments)
             mean, var = self.stats[pre + ".norm2"]
             K.bn_forward(self.u2[i], p[pre + ".norm2.weight"], p[pre + ".norm2.bias"],
                          running[pre + ".norm2.running_mean"], running[pre + ".norm2.running_var"], mean, var,
                          self.partial, self.stream[i + 1], rows=rows, channels=h, ensemble=E, training=training,
                          relu=True, update_running=update_running, residual=self.stream[i],
-                         y_bf16=self.stream_h[i + 1])
+                         y_bf16=self.stream_h[i + 1], moments_ready=training)
 
     def post_norm(self, p, *, rows, row0, count):
         """RMSNorm of rows [row0, row0 + count) of the last block output into z (same rows)."""

@@ -253,3 +253,59 @@ def test_big_tile_bf16_gemm_layouts(gpu, a_kcontig, b_kcontig, batch, m, n, k, s
            epilogue="relu", c=c.to(gpu), beta=1.0)
     expected = torch.relu(ref + bias.double()[:, None, :]) + c.double()
     torch.testing.assert_close(d.cpu().double(), expected, rtol=1e-5, atol=1e-5 * math.sqrt(k))
+
+
+def _chunk_moments(d):
+    """Per-256-row-chunk column (mean, M2) in float64: [batch][chunk][2][n]."""
+    batch, m, n = d.shape
+    out = []
+    for e in range(batch):
+        rows = []
+        for r0 in range(0, m, 256):
+            x = d[e, r0:r0 + 256].double()
+            mean = x.mean(0)
+            rows.append(torch.stack([mean, ((x - mean) ** 2).sum(0)]))
+        out.append(torch.stack(rows))
+    return torch.stack(out)
+
+
+# (batch, m, n, k, splits, a_kcontig, b_kcontig): the first three run the
+# epilogue path of the 256x256 kernel (DMA and register-staged), the rest the
+# separate pass (split-K, a ragged M, fp32-sized shapes the big kernel rejects).
+MOMENT_SHAPES = [(2, 512, 256, 256, 1, True, True), (1, 1024, 512, 192, 1, True, False),
+                 (2, 768, 256, 128, 1, False, False), (2, 1024, 512, 1024, 4, True, True),
+                 (2, 300, 256, 64, 1, True, True), (1, 512, 96, 64, 1, True, True)]
+
+
+@pytest.mark.parametrize("batch,m,n,k,splits,a_kcontig,b_kcontig", MOMENT_SHAPES)
+def test_gemm_output_moments_match_chunk_moments(gpu, batch, m, n, k, splits, a_kcontig, b_kcontig):
+    print(f"case moments batch={batch} m={m} n={n} k={k} splits={splits} a_k={a_kcontig} b_k={b_kcontig}", flush=True)
+    g = torch.Generator().manual_seed(7 * m + n)
+    a = (torch.randn(batch, m, k, generator=g) + 0.5).to(torch.bfloat16)
+    b = torch.randn(batch, n, k, generator=g).to(torch.bfloat16)
+    a_mem = a if a_kcontig else a.transpose(1, 2).contiguous()
+    b_mem = b if b_kcontig else b.transpose(1, 2).contiguous()
+    workspace = torch.empty(splits * batch * m * n * 4, dtype=torch.uint8, device=gpu) if splits > 1 else None
+    d = torch.empty(batch, m, n, device=gpu)
+    chunks = (m + 255) // 256
+    moments = torch.full((batch, chunks, 2, n), float("nan"), device=gpu)
+    K.gemm(a_mem.to(gpu), b_mem.to(gpu), d, m=m, n=n, k=k, batch=batch, a_kcontig=a_kcontig, b_kcontig=b_kcontig,
+           lda=k if a_kcontig else m, ldb=k if b_kcontig else n, ldd=n, stride_a=m * k, stride_b=n * k,
+           stride_d=m * n, mode=K.BF16, splits=splits, workspace=workspace, moments=moments)
+    torch.cuda.synchronize()
+    expected = _chunk_moments(d.cpu())
+    got = moments.cpu().double()
+    torch.testing.assert_close(got[:, :, 0], expected[:, :, 0], rtol=1e-5, atol=1e-4)
+    torch.testing.assert_close(got[:, :, 1], expected[:, :, 1], rtol=1e-5, atol=1e-3)
+    # the BatchNorm consuming them gives the statistics of its own moments pass
+    w, bb = torch.rand(batch, n, device=gpu) + 0.5, torch.randn(batch, n, device=gpu)
+    outs = []
+    for ready in (True, False):
+        mean, var = torch.zeros(batch, n, device=gpu), torch.zeros(batch, n, device=gpu)
+        partial = moments.clone() if ready else torch.zeros_like(moments)
+        y = torch.empty(batch, m, n, device=gpu)
+        K.bn_forward(d, w, bb, torch.zeros(batch, n, device=gpu), torch.ones(batch, n, device=gpu), mean, var,
+                     partial, y, rows=m, channels=n, ensemble=batch, relu=True, moments_ready=ready)
+        outs.append((mean.cpu(), var.cpu(), y.cpu()))
+    for x0, x1 in zip(*outs):
+        torch.testing.assert_close(x0, x1, rtol=1e-5, atol=1e-5)
