@@ -362,6 +362,9 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     } else {
         p.d = d;
     }
+    p.out_vec = n % 4 == 0 && aligned(p.d, 16) && (splits > 1 || (ldd % 4 == 0 && stride_d % 4 == 0)) &&
+                (splits > 1 || ((!bias || (aligned(bias, 16) && stride_bias % 4 == 0)) &&
+                                (beta == 0.0f || aligned(c, 16)) && (!d_bf16 || aligned(d_bf16, 8))));
     // Column moments come from the 256x256 kernel's epilogue when it runs this
     // product in direct mode with the identity epilogue; otherwise from a pass over D.
     const bool fused_moments = moments && mode == 1 && splits == 1 && !bias && epilogue == 0 && beta == 0.0f &&

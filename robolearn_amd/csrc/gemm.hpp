@@ -32,7 +32,17 @@ struct Params {
     int a_vec, b_vec;    // 16-byte vector loads allowed
     unsigned short* d_bf16;  // optional bf16 copy of the output (direct mode only)
     float* moments;      // optional per-256-row-chunk (mean, M2) of D: [batch][m / 256][2][n]
+    int out_vec;         // 16-byte output stores allowed (n, ldd, strides multiple of 4; aligned outputs)
 };
+
+// Wave-local LDS fence: this wave's LDS operations are complete and the
+// compiler may not move memory accesses across it.  Enough for LDS regions
+// that only this wave touches (LDS executes a wave's operations in order).
+__device__ __forceinline__ void lds_fence() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt unconstrained
+    asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ float apply_epilogue(float v, int epilogue) {
     if (epilogue == 1) return v > 0.0f ? v : 0.0f;

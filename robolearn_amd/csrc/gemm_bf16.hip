@@ -156,9 +156,70 @@ struct Loader {
     }
 };
 
+// Epilogue through LDS with 16-byte stores (n, ldd multiple of 4, aligned
+// outputs): each wave stages one 32 x 64 block of its 128 x 64 outputs at a
+// time and writes it back row-wise, four 256-byte row segments per wave
+// instruction, and the bf16 copy as 8-byte stores.  `lds` must be free and
+// hold 4 x 32 x kStagePitch floats; each wave's staging block is its own, so
+// the blocks need only wave-local fences.
+constexpr int kStagePitch = 68;
+
+__device__ __forceinline__ void store_tile_vec(const Params& p, const f32x16_t (&acc)[4][2], float* lds, int batch,
+                                               int split, int m0, int n0, int wave, int wm, int wn) {
+    const int lane = threadIdx.x % kWave;
+    const bool direct = p.splits == 1;
+    float* D = p.d + (direct ? batch * p.stride_d
+                             : (static_cast<long long>(split) * p.batch + batch) * static_cast<long long>(p.m) * p.n);
+    const long long ldd = direct ? p.ldd : p.n;
+    const float* C = (direct && p.beta != 0.0f) ? p.c + batch * p.stride_d : nullptr;
+    unsigned short* Dh = (direct && p.d_bf16) ? p.d_bf16 + batch * p.stride_d : nullptr;
+    const int c4 = lane % 16;
+    const int col = n0 + wn * 64 + 4 * c4;
+    const bool col_ok = col < p.n;
+    float4 bias4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (direct && p.bias && col_ok) bias4 = *reinterpret_cast<const float4*>(p.bias + batch * p.stride_bias + col);
+    float* stage = lds + wave * 32 * kStagePitch;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        lds_fence();  // this wave's reads of the previous block are done
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+                stage[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * kStagePitch + j * 32 + lane % 32] = acc[i][j][v];
+        lds_fence();
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int row = 4 * r + lane / 16;
+            const int grow = m0 + wm * 128 + i * 32 + row;
+            if (grow >= p.m || !col_ok) continue;
+            float4 val = *reinterpret_cast<const float4*>(stage + row * kStagePitch + 4 * c4);
+            const long long offset = static_cast<long long>(grow) * ldd + col;
+            if (direct) {
+                val.x = apply_epilogue(val.x + bias4.x, p.epilogue);
+                val.y = apply_epilogue(val.y + bias4.y, p.epilogue);
+                val.z = apply_epilogue(val.z + bias4.z, p.epilogue);
+                val.w = apply_epilogue(val.w + bias4.w, p.epilogue);
+                if (C) {
+                    const float4 c = *reinterpret_cast<const float4*>(C + offset);
+                    val.x += p.beta * c.x;
+                    val.y += p.beta * c.y;
+                    val.z += p.beta * c.z;
+                    val.w += p.beta * c.w;
+                }
+                if (Dh)
+                    *reinterpret_cast<uint2*>(Dh + offset) =
+                        make_uint2(f32x2_to_bf16x2(val.x, val.y), f32x2_to_bf16x2(val.z, val.w));
+            }
+            *reinterpret_cast<float4*>(D + offset) = val;
+        }
+    }
+}
+
 template <typename SA, typename SB, bool AK, bool BK>
 __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) unsigned short lds[2][(kBM + kBN) * kPitch];
+    static_assert(sizeof(lds) >= 4 * 32 * kStagePitch * sizeof(float), "epilogue staging must fit the K-loop LDS");
 
     const int split = static_cast<int>(blockIdx.z) % p.splits;
     const int batch = static_cast<int>(blockIdx.z) / p.splits;
@@ -234,6 +295,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(Params p) {
 
     // Accumulator layout of a 32x32 MFMA tile: lane l holds column l % 32 and
     // rows 8 * (v / 4) + 4 * (l / 32) + v % 4 for v = 0..15.
+    if (p.out_vec) {
+        store_tile_vec(p, acc, reinterpret_cast<float*>(&lds[0][0]), batch, split, m0, n0, wave, wm, wn);
+        return;
+    }
     const bool direct = p.splits == 1;
     float* D = p.d + (direct ? batch * p.stride_d
                              : (static_cast<long long>(split) * p.batch + batch) * static_cast<long long>(p.m) * p.n);

@@ -246,13 +246,16 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
     float4 mean = make_float4(0.0f, 0.0f, 0.0f, 0.0f), m2 = mean;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        lds_barrier();  // the previous block (or the K loop) is done with LDS
+        // the K loop's LDS (shared by all waves) is free; later blocks reuse
+        // this wave's own staging, which needs only a wave-local fence
+        if (i == 0) lds_barrier();
+        else lds_fence();
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v)
                 stage[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * EP + j * 32 + lane % 32] = acc[i][j][v];
-        lds_barrier();
+        lds_fence();
         if (moments) {
             float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             for (int r = 0; r < 16; ++r) {

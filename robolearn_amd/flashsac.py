@@ -504,7 +504,8 @@ class FlashSAC:
         cn.forward(cp, self.critic_w, self.critic_running, self.critic_in_actor, rows=B, x_stride=0, training=False)
         cn.post_norm(cp, rows=B, row0=0, count=B)
         K.linear_forward(cn.z_op, self.critic_w["predictor.w.weight"], self.logits, rows=B, in_dim=cn.h,
-                         out_dim=bins, ensemble=2, x_stride=B * cn.h, bias=cp["predictor.bias"], mode=self.mode)
+                         out_dim=bins, ensemble=2, x_stride=B * cn.h, bias=cp["predictor.bias"], mode=self.mode,
+                         workspace=self.workspace)
         K.categorical_head_forward(self.logits, self.support, self.q, rows=B, bins=bins, ensemble=2)
         _native.call("rl_actor_objective", self.q.data_ptr(), self.q[1].data_ptr(), self.log_probs_all.data_ptr(),
                      self.actions_all.data_ptr(), A, self.batch["action"].data_ptr(), self.alpha.data_ptr(),
@@ -571,12 +572,13 @@ class FlashSAC:
         cn.post_norm(self.target_p, rows=2 * B, row0=B, count=B)
         K.linear_forward(cn.z_op.view(-1)[B * cn.h:], self.target_w["predictor.w.weight"], self.target_logits,
                          rows=B, in_dim=cn.h, out_dim=bins, ensemble=2, x_stride=2 * B * cn.h,
-                         bias=self.target_p["predictor.bias"], mode=self.mode)
+                         bias=self.target_p["predictor.bias"], mode=self.mode, workspace=self.workspace)
         # online critic, training mode; head on the current-observation half
         cn.forward(cp, self.critic_w, self.critic_running, self.critic_in, rows=2 * B, x_stride=0, training=True)
         cn.post_norm(cp, rows=2 * B, row0=0, count=B)
         K.linear_forward(cn.z_op, self.critic_w["predictor.w.weight"], self.logits, rows=B, in_dim=cn.h,
-                         out_dim=bins, ensemble=2, x_stride=2 * B * cn.h, bias=cp["predictor.bias"], mode=self.mode)
+                         out_dim=bins, ensemble=2, x_stride=2 * B * cn.h, bias=cp["predictor.bias"], mode=self.mode,
+                         workspace=self.workspace)
         K.td_cross_entropy(self.target_logits, None, B, self.logits, None, B, self.support, self.reward_used,
                            self.batch["terminated"], self.batch["discount"], self.next_log_probs, self.alpha,
                            min_v=cfg.critic_min_v, max_v=cfg.critic_max_v, batch=B, bins=bins, scale=1.0 / (2 * B),

@@ -52,17 +52,36 @@ def gemm(
     )
 
 
+def forward_split_count(m, n, k, batch, mode):
+    """K splits for a product whose output tiles cannot fill the GPU (a narrow
+    head over a long K): at least 256 workgroups, each split >= 256 of K."""
+    tm = 256 if mode == BF16 else 128
+    tiles = ((m + tm - 1) // tm) * ((n + 127) // 128) * batch
+    ktiles = (k + 31) // 32
+    splits = 1
+    while tiles * splits < 256 and splits * 2 <= max(1, ktiles // 8) and splits < 16:
+        splits *= 2
+    return splits
+
+
 def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None, bias=None, epilogue=None,
-                   mode=FP32, c=None, beta=0.0, d_bf16=None, moments=None):
+                   mode=FP32, c=None, beta=0.0, d_bf16=None, moments=None, workspace=None):
     """y[e] = act(x[e] w[e]^T + bias[e]) (+ beta c); x_stride 0 broadcasts x; moments receives
-    y's per-256-row-chunk column moments (the BatchNorm partial layout)."""
+    y's per-256-row-chunk column moments (the BatchNorm partial layout).  With a workspace,
+    a product too small to fill the GPU is split over K (fixed-order reduction)."""
     if x_stride is None:
         x_stride = rows * in_dim
     _check(w, ensemble * out_dim * in_dim, "weight", w.dtype)
     _check(y, ensemble * rows * out_dim, "output")
+    splits = forward_split_count(rows, out_dim, in_dim, ensemble, mode) if workspace is not None else 1
+    if splits > 1:
+        need = _native.load().rl_gemm_workspace(mode, rows, out_dim, in_dim, ensemble, splits)
+        if need > workspace.numel() * workspace.element_size():
+            splits = 1
     gemm(x, w, y, m=rows, n=out_dim, k=in_dim, batch=ensemble, a_kcontig=True, b_kcontig=True, lda=in_dim,
          ldb=in_dim, ldd=out_dim, stride_a=x_stride, stride_b=out_dim * in_dim, stride_d=rows * out_dim, bias=bias,
-         stride_bias=out_dim, epilogue=epilogue, mode=mode, c=c, beta=beta, d_bf16=d_bf16, moments=moments)
+         stride_bias=out_dim, epilogue=epilogue, mode=mode, c=c, beta=beta, d_bf16=d_bf16, moments=moments,
+         splits=splits, workspace=workspace if splits > 1 else None)
 
 
 def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=FP32, c=None, beta=0.0,
