@@ -59,6 +59,10 @@ int rl_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int 
             float beta, int epilogue, int splits, float* workspace, size_t workspace_bytes, void* d_bf16,
             float* moments, void* stream);
 size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, int splits);
+/* dst[b][c][r] = src[b][r][c] over 16-bit elements (bf16 weight copies transposed
+ * so the input-gradient product reads both operands K-contiguously).  No
+ * reference counterpart: part of the MI355X operand layout. */
+int rl_transpose16(const void* src, void* dst, int batch, int rows, int cols, void* stream);
 
 /* ---- optimizer ---------------------------------------------------------- */
 /* One pass fusing Adam (form 0: torch.optim.Adam as robolearn/flashsac/agent.py:64-65;

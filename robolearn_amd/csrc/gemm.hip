@@ -301,6 +301,30 @@ void launch_mode(const Params& p, int a_bf16, int b_bf16, bool ak, bool bk, hipS
     else launch_layout<Mode, H, H>(p, ak, bk, stream);
 }
 
+// dst[b][c][r] = src[b][r][c] for 16-bit elements: 64 x 64 tiles through LDS,
+// coalesced 2-byte reads along c and writes along r.  Grid (col tiles, row
+// tiles, batch).
+__global__ __launch_bounds__(256) void transpose16(const unsigned short* src, unsigned short* dst, int rows, int cols) {
+    __shared__ unsigned short tile[64][65];
+    const long long base = static_cast<long long>(blockIdx.z) * rows * cols;
+    const int r0 = static_cast<int>(blockIdx.y) * 64;
+    const int c0 = static_cast<int>(blockIdx.x) * 64;
+    const int t = static_cast<int>(threadIdx.x);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = i * 4 + t / 64;
+        const int c = t % 64;
+        if (r0 + r < rows && c0 + c < cols) tile[r][c] = src[base + static_cast<long long>(r0 + r) * cols + c0 + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int c = i * 4 + t / 64;
+        const int r = t % 64;
+        if (r0 + r < rows && c0 + c < cols) dst[base + static_cast<long long>(c0 + c) * rows + r0 + r] = tile[r][c];
+    }
+}
+
 }  // namespace gemm
 
 // Row-major batched GEMM with optional split-K.  See the header for the
@@ -407,4 +431,18 @@ RL_API std::size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, i
     splits = (ktiles + per - 1) / per;
     if (splits <= 1) return 0;
     return static_cast<std::size_t>(splits) * batch * m * n * sizeof(float);
+}
+
+// Batched transpose of 16-bit matrices (bf16 weight copies laid out K-contiguous
+// for the input-gradient product); no reference counterpart.
+RL_API int rl_transpose16(const void* src, void* dst, int batch, int rows, int cols, void* stream) noexcept {
+    return rl::guarded("rl_transpose16", [&] {
+        rl::require(src && dst && src != dst, "Transpose needs distinct source and destination buffers.");
+        rl::require(batch > 0 && rows > 0 && cols > 0 && batch <= 65535 && (rows + 63) / 64 <= 65535,
+                    "Transpose dimensions are invalid.");
+        const dim3 grid(rl::ceil_div(cols, 64), rl::ceil_div(rows, 64), static_cast<unsigned>(batch));
+        hipLaunchKernelGGL(rl::gemm::transpose16, grid, dim3(256), 0, rl::as_stream(stream),
+                           static_cast<const unsigned short*>(src), static_cast<unsigned short*>(dst), rows, cols);
+        rl::check_launch("Launch transpose");
+    });
 }

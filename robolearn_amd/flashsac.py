@@ -188,6 +188,11 @@ class FlashSAC:
             self.target_p = self.critic.targets()
             self.critic_w = self.critic.shadows() or self.critic_p
             self.target_w = self.critic.target_shadows() or self.target_p
+            # transposed bf16 block weights: the input-gradient products read both operands K-contiguously
+            self.actor.enable_transposed([f"encoder.{i}.w{j}.w.weight" for i in range(cfg.actor_num_blocks)
+                                          for j in (1, 2)])
+            self.critic.enable_transposed([f"encoder.{i}.w{j}.weight" for i in range(cfg.critic_num_blocks)
+                                           for j in (1, 2)])
             self.actor.refresh_shadows()
             self.critic.refresh_shadows()
             # optimizers
@@ -521,6 +526,7 @@ class FlashSAC:
                                 rows=B, in_dim=cn.h, out_dim=bins, ensemble=2, mode=self.mode)
         cn.post_norm_backward(cp, None, rows=B, row0=0, count=B)
         cn.backward(cp, self.critic_w, self.critic_running, None, self.critic_in_actor, rows=B, x_stride=0,
+                    wt=self.critic.transposed,
                     training=False, workspace=self.workspace, input_grad=self.critic_dx)
         _native.call("rl_add", self.critic_dx[0].data_ptr(), self.critic_dx[1].data_ptr(), B * I, K.stream())
         if cfg.actor_bc_alpha > 0:
@@ -540,6 +546,7 @@ class FlashSAC:
                                 mode=self.mode)
         net.post_norm_backward(p, g, rows=2 * B, row0=0, count=2 * B)
         net.backward(p, self.actor_w, self.actor_running, g, self.actor_in, rows=2 * B, x_stride=0, training=True,
+                     wt=self.actor.transposed,
                      workspace=self.workspace)
         if apply_optimizer:
             self.actor_optimizer.step()
@@ -596,6 +603,7 @@ class FlashSAC:
                stride_d=2 * B * cn.h, mode=self.mode)
         cn.post_norm_backward(cp, cg, rows=2 * B, row0=0, count=B)
         cn.backward(cp, self.critic_w, self.critic_running, cg, self.critic_in, rows=2 * B, x_stride=0, training=True,
+                    wt=self.critic.transposed,
                     workspace=self.workspace)
         if apply_optimizer:
             self.critic_optimizer.step()

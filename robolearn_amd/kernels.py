@@ -85,12 +85,26 @@ def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None,
 
 
 def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=FP32, c=None, beta=0.0,
-                          d_bf16=None):
-    """dx[e] = dy[e] w[e] (+ beta c)."""
+                          d_bf16=None, wt=None):
+    """dx[e] = dy[e] w[e] (+ beta c).  wt: optional [ensemble, in_dim, out_dim] transposed copy of w,
+    which lets both operands be read K-contiguously."""
     _check(dx, ensemble * rows * in_dim, "input gradient")
+    if wt is not None:
+        _check(wt, ensemble * out_dim * in_dim, "transposed weight", wt.dtype)
+        gemm(dy, wt, dx, m=rows, n=in_dim, k=out_dim, batch=ensemble, a_kcontig=True, b_kcontig=True, lda=out_dim,
+             ldb=out_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=out_dim * in_dim, stride_d=rows * in_dim,
+             mode=mode, c=c, beta=beta, d_bf16=d_bf16)
+        return
     gemm(dy, w, dx, m=rows, n=in_dim, k=out_dim, batch=ensemble, a_kcontig=True, b_kcontig=False, lda=out_dim,
          ldb=in_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=out_dim * in_dim, stride_d=rows * in_dim,
          mode=mode, c=c, beta=beta, d_bf16=d_bf16)
+
+
+def transpose16(src, dst, *, batch, rows, cols):
+    """dst[b] = src[b]^T for 16-bit [batch, rows, cols] -> [batch, cols, rows]."""
+    _check(src, batch * rows * cols, "transpose source", src.dtype)
+    _check(dst, batch * rows * cols, "transpose destination", dst.dtype)
+    _native.call("rl_transpose16", ptr(src), ptr(dst), batch, rows, cols, stream())
 
 
 def split_count(m, n, k, batch, mode):

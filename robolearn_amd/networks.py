@@ -63,12 +63,34 @@ class FlatStore:
         self.target_shadow = (torch.zeros(self.size, dtype=torch.bfloat16, device=device)
                               if shadows and target else None)
 
+        # transposed bf16 copies of selected [E, out, in] weights, [E, in, out]
+        self.transposed = OrderedDict()
+
+    def enable_transposed(self, names):
+        """Keep [E, in, out] transposed bf16 copies of these weights (input-gradient operands)."""
+        if self.shadow is None:
+            return
+        for name in names:
+            e, o, i = self._matrix_dims(name)
+            self.transposed[name] = torch.zeros(e, i, o, dtype=torch.bfloat16, device=self.param.device)
+
+    def _matrix_dims(self, name):
+        shape = self.shapes[name]
+        o, i = shape[-2], shape[-1]
+        return _numel(shape) // (o * i), o, i
+
+    def refresh_transposed(self):
+        for name, dst in self.transposed.items():
+            e, o, i = self._matrix_dims(name)
+            K.transpose16(self.view(self.shadow, name), dst, batch=e, rows=o, cols=i)
+
     def refresh_shadows(self):
         """Re-derive the bf16 copies from the fp32 masters (after init or a checkpoint load)."""
         if self.shadow is not None:
             K.cast_bf16(self.param, self.shadow)
         if self.target_shadow is not None:
             K.cast_bf16(self.target, self.target_shadow)
+        self.refresh_transposed()
 
     def view(self, buffer, name):
         offset = self.offsets[name]
@@ -178,6 +200,8 @@ class FusedOptimizer:
         project = self.project if project is None else project
         ema = self.ema if ema is None else ema
         _native.call("rl_fused_optimizer_step", self.handle, int(adam), int(project), int(ema), None, K.stream())
+        if adam or project:
+            self.store.refresh_transposed()
 
     def close(self):
         if getattr(self, "handle", None):
@@ -317,12 +341,14 @@ class Trunk:
         if self.bf and self.blocks == 0:
             K.cast_bf16(self.d_stream.view(-1)[: self.E * rows * self.h], self.d_stream_h)
 
-    def backward(self, p, w, running, g, x, *, rows, x_stride, training, workspace, input_grad=None):
+    def backward(self, p, w, running, g, x, *, rows, x_stride, training, workspace, input_grad=None, wt=None):
         """Backward from self.d_stream (gradient of the last block output).
 
         g: gradient views (None for a frozen network: only input gradients).
         input_grad: optional [E, rows, in_dim] buffer receiving dL/dx per member.
+        wt: optional transposed block weights ([E, in, out], bf16) for the input-gradient products.
         """
+        wt = wt or {}
         E, h, mode = self.E, self.h, self.mode
         for i in reversed(range(self.blocks)):
             pre = f"encoder.{i}"
@@ -333,7 +359,7 @@ class Trunk:
                           training=training, relu=True, b=p[pre + ".norm2.bias"], dx_bf16=self.d_u2_h)
             d_u2 = self.op(self.d_u2, self.d_u2_h)
             K.linear_backward_input(d_u2, w[f"{pre}.w2{self.linear}"], self.d_r1, rows=rows, in_dim=4 * h,
-                                    out_dim=h, ensemble=E, mode=mode)
+                                    out_dim=h, ensemble=E, mode=mode, wt=wt.get(f"{pre}.w2{self.linear}"))
             if g is not None:
                 K.linear_backward_weight(d_u2, self.op(self.r1[i], self.r1_h[i]), g[f"{pre}.w2{self.linear}"],
                                          rows=rows, in_dim=4 * h, out_dim=h, ensemble=E, mode=mode,
@@ -346,7 +372,7 @@ class Trunk:
             d_r1 = self.op(self.d_r1, self.d_r1_h)
             K.linear_backward_input(d_r1, w[f"{pre}.w1{self.linear}"], self.d_stream, rows=rows, in_dim=h,
                                     out_dim=4 * h, ensemble=E, mode=mode, c=self.d_stream, beta=1.0,
-                                    d_bf16=self.d_stream_h)
+                                    d_bf16=self.d_stream_h, wt=wt.get(f"{pre}.w1{self.linear}"))
             if g is not None:
                 K.linear_backward_weight(d_r1, self.op(self.stream[i], self.stream_h[i]), g[f"{pre}.w1{self.linear}"],
                                          rows=rows, in_dim=h, out_dim=4 * h, ensemble=E, mode=mode,

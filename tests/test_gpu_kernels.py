@@ -309,3 +309,33 @@ def test_gemm_output_moments_match_chunk_moments(gpu, batch, m, n, k, splits, a_
         outs.append((mean.cpu(), var.cpu(), y.cpu()))
     for x0, x1 in zip(*outs):
         torch.testing.assert_close(x0, x1, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("batch,rows,cols", [(1, 64, 64), (2, 1024, 4096), (3, 100, 37), (1, 1, 130)])
+def test_transpose16_is_exact(gpu, batch, rows, cols):
+    print(f"case transpose16 batch={batch} rows={rows} cols={cols}", flush=True)
+    g = torch.Generator().manual_seed(rows * cols)
+    src = torch.randn(batch, rows, cols, generator=g).to(torch.bfloat16).to(gpu)
+    dst = torch.zeros(batch, cols, rows, dtype=torch.bfloat16, device=gpu)
+    K.transpose16(src, dst, batch=batch, rows=rows, cols=cols)
+    torch.cuda.synchronize()
+    assert torch.equal(dst.cpu(), src.cpu().transpose(1, 2))
+
+
+def test_input_gradient_with_transposed_weight(gpu):
+    print("case linear_backward_input wt", flush=True)
+    g = torch.Generator().manual_seed(11)
+    E, rows, in_dim, out_dim = 2, 512, 1024, 4096
+    dy = torch.randn(E, rows, out_dim, generator=g).to(torch.bfloat16).to(gpu)
+    w = torch.randn(E, out_dim, in_dim, generator=g).to(torch.bfloat16).to(gpu)
+    wt = torch.empty(E, in_dim, out_dim, dtype=torch.bfloat16, device=gpu)
+    K.transpose16(w, wt, batch=E, rows=out_dim, cols=in_dim)
+    dx0 = torch.empty(E, rows, in_dim, device=gpu)
+    dx1 = torch.empty(E, rows, in_dim, device=gpu)
+    K.linear_backward_input(dy, w, dx0, rows=rows, in_dim=in_dim, out_dim=out_dim, ensemble=E, mode=K.BF16)
+    K.linear_backward_input(dy, w, dx1, rows=rows, in_dim=in_dim, out_dim=out_dim, ensemble=E, mode=K.BF16, wt=wt)
+    ref = torch.matmul(dy.cpu().double(), w.cpu().double())
+    # fp32 accumulation over K = 4096 unit-scale products: tolerance as in the other bf16 GEMM tests
+    tol = 1e-5 * math.sqrt(out_dim)
+    torch.testing.assert_close(dx1.cpu().double(), ref, rtol=1e-5, atol=tol)
+    torch.testing.assert_close(dx0.cpu(), dx1.cpu(), rtol=1e-5, atol=tol)
