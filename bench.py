@@ -29,7 +29,7 @@ import time
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
-TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_bf16_critic_fwd_g1_traffic.md"
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_dma_critic_fwd_g1_traffic.md"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3

@@ -10,5 +10,5 @@ missing.
 
 Each function cites the reference file:line it follows.  Parity status of each
 function (how it is pinned) is recorded in the module docstrings of
-``oracle.flashsac`` and ``oracle.ppo``.
+``oracle.flashsac``, ``oracle.ppo`` and ``oracle.optim``.
 """
