@@ -1,4 +1,5 @@
-// Dense layer GEMMs on CDNA4 matrix cores.
+// fp32 dense-layer GEMMs on CDNA4 matrix cores (the fp32 mode: PPO MLPs and
+// fp32 FlashSAC configurations; bf16 products run in gemm_bf16*.hip).
 //
 // One row-major kernel family covers the three products of a bias-free
 // Linear layer (the reference's CudaLinear plans, robolearn/cuda/linear.py:179-185):
@@ -7,13 +8,15 @@
 //   weight   dW[N,K] = dY[R,N]^T . X[R,K]     (A M-contiguous, B N-contiguous)
 // batched over a leading ensemble index (the stacked twin critics).
 //
-// Mode 0 computes with v_mfma_f32_32x32x2_f32 (fp32 operands), mode 1 with
-// v_mfma_f32_32x32x16_bf16 (operands rounded to bf16 when staged into LDS,
-// fp32 accumulation).  A 256-thread workgroup owns a 128x128 output tile as
-// 2x2 waves of 64x64; each wave holds 2x2 32x32 accumulators.  Operands are
-// staged through LDS in [row][k] order so each lane reads its K-slice with one
-// or two 16-byte LDS loads; the K order inside a tile is permuted identically
-// for both operands, which leaves the dot products unchanged.
+// v_mfma_f32_32x32x2_f32 is 64 cycles per 2048 MACs, so these products are
+// bound by MFMA issue, not by operand traffic: what matters is that every SIMD
+// has independent work.  A 256-thread workgroup owns a T x T output tile as
+// 2x2 waves of (T/2) x (T/2), i.e. (T/64)^2 32x32 accumulators per wave.  T =
+// 64 for the small-row-count products of the PPO update (4x the workgroups of
+// T = 128, so every CU gets several), T = 128 for large ones.  Operands are
+// staged through LDS in [row][k] order, 16 K per step, so each lane reads its
+// K-slice with two 16-byte LDS loads; the K order inside a step is permuted
+// identically for both operands, which leaves the dot products unchanged.
 #include "gemm.hpp"
 
 #include <cmath>
@@ -22,114 +25,83 @@
 namespace rl {
 namespace gemm {
 
-template <typename T> struct Src;
-template <> struct Src<float> {
-    static __device__ __forceinline__ float load(const float* p) { return *p; }
-};
-template <> struct Src<unsigned short> {
-    static __device__ __forceinline__ float load(const unsigned short* p) { return bf16_bits_to_f32(*p); }
-};
+constexpr int kFp32K = 16;              // K per LDS step
+constexpr int kFp32Pitch = kFp32K + 4;  // floats per LDS row
 
-template <int Mode> struct Lds;
-template <> struct Lds<0> {
-    using T = float;
-    static constexpr int KT = 16;
-    static constexpr int Pitch = KT + 4;
-    static __device__ __forceinline__ T cvt(float v) { return v; }
-};
-template <> struct Lds<1> {
-    using T = unsigned short;
-    static constexpr int KT = 32;
-    static constexpr int Pitch = KT + 8;
-    static __device__ __forceinline__ T cvt(float v) { return f32_to_bf16_bits(v); }
-};
-
-// Loads one 128 x KT operand tile into registers, already converted to the
-// LDS element type, and later stores it.  Element (r, k) of the operand is
-// src[r * ld + k] when KContig, else src[k * ld + r].
-template <int Mode, typename S, bool KContig>
+// Loads one Rows x 16 operand tile into registers and later stores it to LDS.
+// Element (r, k) of the operand is src[r * ld + k] when KContig, else
+// src[k * ld + r].
+template <bool KContig, int Rows>
 struct TileLoader {
-    using L = Lds<Mode>;
-    using T = typename L::T;
-    static constexpr int KT = L::KT;
-    static constexpr int VecElems = 16 / sizeof(S);
-    static constexpr int VecPerRow = KT / VecElems;
-    static constexpr int PerThread = KContig ? (kTile * VecPerRow) / kThreads : 1;
-    static constexpr int Count = KContig ? PerThread * VecElems : KT / 2;
-    T regs[Count];
+    static constexpr int VecPerRow = kFp32K / 4;
+    static constexpr int PerThread = KContig ? Rows * VecPerRow / kThreads : 1;
+    static constexpr int Groups = kThreads / Rows;      // M/N-contiguous: k groups per tile
+    static constexpr int KPer = kFp32K / Groups;        // k values per thread
+    static constexpr int Count = KContig ? PerThread * 4 : KPer;
+    static_assert(KContig ? PerThread >= 1 : (KPer >= 1 && kFp32K % Groups == 0), "tile/thread mismatch");
+    float regs[Count];
 
-    __device__ __forceinline__ void load(const S* src, long long ld, int r0, int k0, int rows, int ks, bool vec) {
+    __device__ __forceinline__ void load(const float* src, long long ld, int r0, int k0, int rows, int ks, bool vec) {
         const int t = threadIdx.x;
         if constexpr (KContig) {
 #pragma unroll
             for (int i = 0; i < PerThread; ++i) {
                 const int v = i * kThreads + t;
                 const int r = r0 + v / VecPerRow;
-                const int k = k0 + (v % VecPerRow) * VecElems;
-                const S* p = src + static_cast<long long>(r) * ld + k;
-                if (r < rows && vec && k + VecElems <= ks) {
-                    if constexpr (sizeof(S) == 4) {
-                        const float4 x = *reinterpret_cast<const float4*>(p);
-                        regs[i * VecElems + 0] = L::cvt(x.x);
-                        regs[i * VecElems + 1] = L::cvt(x.y);
-                        regs[i * VecElems + 2] = L::cvt(x.z);
-                        regs[i * VecElems + 3] = L::cvt(x.w);
-                    } else {
-                        const u16x8_t x = *reinterpret_cast<const u16x8_t*>(p);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) regs[i * VecElems + e] = L::cvt(bf16_bits_to_f32(x[e]));
-                    }
+                const int k = k0 + (v % VecPerRow) * 4;
+                const float* q = src + static_cast<long long>(r) * ld + k;
+                if (r < rows && vec && k + 4 <= ks) {
+                    const float4 x = *reinterpret_cast<const float4*>(q);
+                    regs[i * 4 + 0] = x.x;
+                    regs[i * 4 + 1] = x.y;
+                    regs[i * 4 + 2] = x.z;
+                    regs[i * 4 + 3] = x.w;
                 } else {
 #pragma unroll
-                    for (int e = 0; e < VecElems; ++e)
-                        regs[i * VecElems + e] = (r < rows && k + e < ks) ? L::cvt(Src<S>::load(p + e)) : L::cvt(0.0f);
+                    for (int e = 0; e < 4; ++e) regs[i * 4 + e] = (r < rows && k + e < ks) ? q[e] : 0.0f;
                 }
             }
         } else {
-            const int r = r0 + t % kTile;
-            const int kb = k0 + (t / kTile) * (KT / 2);
+            const int r = r0 + t % Rows;
+            const int kb = k0 + (t / Rows) * KPer;
             const bool rv = r < rows;
 #pragma unroll
-            for (int e = 0; e < KT / 2; ++e) {
+            for (int e = 0; e < KPer; ++e) {
                 const int k = kb + e;
-                regs[e] = (rv && k < ks) ? L::cvt(Src<S>::load(src + static_cast<long long>(k) * ld + r)) : L::cvt(0.0f);
+                regs[e] = (rv && k < ks) ? src[static_cast<long long>(k) * ld + r] : 0.0f;
             }
         }
     }
 
-    __device__ __forceinline__ void store(T* lds) const {
+    __device__ __forceinline__ void store(float* lds) const {
         const int t = threadIdx.x;
         if constexpr (KContig) {
 #pragma unroll
             for (int i = 0; i < PerThread; ++i) {
                 const int v = i * kThreads + t;
-                T* q = lds + (v / VecPerRow) * L::Pitch + (v % VecPerRow) * VecElems;
-#pragma unroll
-                for (int e = 0; e < VecElems; ++e) q[e] = regs[i * VecElems + e];
+                *reinterpret_cast<float4*>(lds + (v / VecPerRow) * kFp32Pitch + (v % VecPerRow) * 4) =
+                    make_float4(regs[i * 4 + 0], regs[i * 4 + 1], regs[i * 4 + 2], regs[i * 4 + 3]);
             }
         } else {
-            T* q = lds + (t % kTile) * L::Pitch + (t / kTile) * (KT / 2);
+            float* q = lds + (t % Rows) * kFp32Pitch + (t / Rows) * KPer;
 #pragma unroll
-            for (int e = 0; e < KT / 2; ++e) q[e] = regs[e];
+            for (int e = 0; e < KPer; ++e) q[e] = regs[e];
         }
     }
 };
 
-template <int Mode, typename SA, typename SB, bool AK, bool BK>
+template <int T, bool AK, bool BK>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
-    using L = Lds<Mode>;
-    using T = typename L::T;
-    constexpr int KT = L::KT;
-    constexpr int Pitch = L::Pitch;
-    __shared__ __attribute__((aligned(16))) T sa[kTile * Pitch];
-    __shared__ __attribute__((aligned(16))) T sb[kTile * Pitch];
+    constexpr int WB = T / 64;  // 32x32 accumulator blocks per wave and dimension
+    __shared__ __attribute__((aligned(16))) float sa[T * kFp32Pitch];
+    __shared__ __attribute__((aligned(16))) float sb[T * kFp32Pitch];
 
     const int split = static_cast<int>(blockIdx.z) % p.splits;
     const int batch = static_cast<int>(blockIdx.z) / p.splits;
-    const SA* A = static_cast<const SA*>(p.a) + batch * p.stride_a;
-    const SB* B = static_cast<const SB*>(p.b) + batch * p.stride_b;
-    const int m0 = static_cast<int>(blockIdx.y) * kTile;
-    const int n0 = static_cast<int>(blockIdx.x) * kTile;
+    const float* A = static_cast<const float*>(p.a) + batch * p.stride_a;
+    const float* B = static_cast<const float*>(p.b) + batch * p.stride_b;
+    const int m0 = static_cast<int>(blockIdx.y) * T;
+    const int n0 = static_cast<int>(blockIdx.x) * T;
     const int k_begin = split * p.k_per_split;
     const int k_end = min(p.k, k_begin + p.k_per_split);
 
@@ -138,16 +110,16 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
     const int wm = wave / 2;
     const int wn = wave % 2;
 
-    f32x16_t acc[2][2];
+    f32x16_t acc[WB][WB];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WB; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WB; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    TileLoader<Mode, SA, AK> la;
-    TileLoader<Mode, SB, BK> lb;
+    TileLoader<AK, T> la;
+    TileLoader<BK, T> lb;
     const bool avec = p.a_vec != 0;
     const bool bvec = p.b_vec != 0;
 
@@ -160,57 +132,34 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
     }
     __syncthreads();
 
-    for (int k0 = k_begin; k0 < k_end; k0 += KT) {
-        const bool more = k0 + KT < k_end;
+    for (int k0 = k_begin; k0 < k_end; k0 += kFp32K) {
+        const bool more = k0 + kFp32K < k_end;
         if (more) {
-            la.load(A, p.lda, m0, k0 + KT, p.m, k_end, avec);
-            lb.load(B, p.ldb, n0, k0 + KT, p.n, k_end, bvec);
+            la.load(A, p.lda, m0, k0 + kFp32K, p.m, k_end, avec);
+            lb.load(B, p.ldb, n0, k0 + kFp32K, p.n, k_end, bvec);
         }
-        if constexpr (Mode == 1) {
-            bf16x8_t af[2][2], bfr[2][2];
+        float4 af[WB][2], bfr[WB][2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const T* q = sa + (wm * 64 + i * 32 + lane % 32) * Pitch + (lane / 32) * 16;
-                af[i][0] = *reinterpret_cast<const bf16x8_t*>(q);
-                af[i][1] = *reinterpret_cast<const bf16x8_t*>(q + 8);
-            }
+        for (int i = 0; i < WB; ++i) {
+            const float* q = sa + (wm * (T / 2) + i * 32 + lane % 32) * kFp32Pitch + (lane / 32) * 8;
+            af[i][0] = *reinterpret_cast<const float4*>(q);
+            af[i][1] = *reinterpret_cast<const float4*>(q + 4);
+        }
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const T* q = sb + (wn * 64 + j * 32 + lane % 32) * Pitch + (lane / 32) * 16;
-                bfr[j][0] = *reinterpret_cast<const bf16x8_t*>(q);
-                bfr[j][1] = *reinterpret_cast<const bf16x8_t*>(q + 8);
-            }
+        for (int j = 0; j < WB; ++j) {
+            const float* q = sb + (wn * (T / 2) + j * 32 + lane % 32) * kFp32Pitch + (lane / 32) * 8;
+            bfr[j][0] = *reinterpret_cast<const float4*>(q);
+            bfr[j][1] = *reinterpret_cast<const float4*>(q + 4);
+        }
 #pragma unroll
-            for (int s = 0; s < 2; ++s)
+        for (int s = 0; s < 8; ++s) {
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < WB; ++i) {
+                const float a = s < 4 ? af[i][0][s] : af[i][1][s - 4];
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][s], bfr[j][s], acc[i][j], 0, 0, 0);
-        } else {
-            float4 af[2][2], bfr[2][2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const T* q = sa + (wm * 64 + i * 32 + lane % 32) * Pitch + (lane / 32) * 8;
-                af[i][0] = *reinterpret_cast<const float4*>(q);
-                af[i][1] = *reinterpret_cast<const float4*>(q + 4);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const T* q = sb + (wn * 64 + j * 32 + lane % 32) * Pitch + (lane / 32) * 8;
-                bfr[j][0] = *reinterpret_cast<const float4*>(q);
-                bfr[j][1] = *reinterpret_cast<const float4*>(q + 4);
-            }
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const float a = s < 4 ? af[i][0][s] : af[i][1][s - 4];
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const float b = s < 4 ? bfr[j][0][s] : bfr[j][1][s - 4];
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
-                    }
+                for (int j = 0; j < WB; ++j) {
+                    const float b = s < 4 ? bfr[j][0][s] : bfr[j][1][s - 4];
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
                 }
             }
         }
@@ -231,15 +180,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
     const float* bias = p.bias ? p.bias + batch * p.stride_bias : nullptr;
     const float* C = p.c ? p.c + batch * p.stride_d : nullptr;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < WB; ++i) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = n0 + wn * 64 + j * 32 + lane % 32;
+        for (int j = 0; j < WB; ++j) {
+            const int col = n0 + wn * (T / 2) + j * 32 + lane % 32;
             if (col >= p.n) continue;
             const float bcol = (direct && bias) ? bias[col] : 0.0f;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * 64 + i * 32 + 8 * (v / 4) + 4 * (lane / 32) + (v % 4);
+                const int row = m0 + wm * (T / 2) + i * 32 + 8 * (v / 4) + 4 * (lane / 32) + (v % 4);
                 if (row >= p.m) continue;
                 const long long offset = static_cast<long long>(row) * ldd + col;
                 float* out = D + offset;
@@ -277,28 +226,30 @@ __global__ void splitk_reduce(const float* work, float* d, unsigned short* d_bf1
     }
 }
 
-template <int Mode, typename SA, typename SB, bool AK, bool BK>
-void launch_typed(const Params& p, hipStream_t stream) {
-    const dim3 grid(ceil_div(p.n, kTile), ceil_div(p.m, kTile), static_cast<unsigned>(p.batch * p.splits));
-    hipLaunchKernelGGL((gemm_kernel<Mode, SA, SB, AK, BK>), grid, dim3(kThreads), 0, stream, p);
+// Output tile edge for an fp32 product: 64 unless 128-wide tiles would still
+// give every SIMD several waves of work.
+int fp32_tile(const Params& p) {
+    const long long big = static_cast<long long>(ceil_div(p.m, 128)) * ceil_div(p.n, 128) * p.batch * p.splits;
+    return big >= 2048 ? 128 : 64;
 }
 
-template <int Mode, typename SA, typename SB>
-void launch_layout(const Params& p, bool ak, bool bk, hipStream_t stream) {
-    if (ak && bk) launch_typed<Mode, SA, SB, true, true>(p, stream);
-    else if (ak && !bk) launch_typed<Mode, SA, SB, true, false>(p, stream);
-    else if (!ak && bk) launch_typed<Mode, SA, SB, false, true>(p, stream);
-    else launch_typed<Mode, SA, SB, false, false>(p, stream);
+template <int T, bool AK, bool BK>
+void launch_fp32_tiled(const Params& p, hipStream_t stream) {
+    const dim3 grid(ceil_div(p.n, T), ceil_div(p.m, T), static_cast<unsigned>(p.batch * p.splits));
+    hipLaunchKernelGGL((gemm_kernel<T, AK, BK>), grid, dim3(kThreads), 0, stream, p);
 }
 
-template <int Mode>
-void launch_mode(const Params& p, int a_bf16, int b_bf16, bool ak, bool bk, hipStream_t stream) {
-    using F = float;
-    using H = unsigned short;
-    if (!a_bf16 && !b_bf16) launch_layout<Mode, F, F>(p, ak, bk, stream);
-    else if (!a_bf16 && b_bf16) launch_layout<Mode, F, H>(p, ak, bk, stream);
-    else if (a_bf16 && !b_bf16) launch_layout<Mode, H, F>(p, ak, bk, stream);
-    else launch_layout<Mode, H, H>(p, ak, bk, stream);
+template <bool AK, bool BK>
+void launch_fp32_layout(const Params& p, hipStream_t stream) {
+    if (fp32_tile(p) == 128) launch_fp32_tiled<128, AK, BK>(p, stream);
+    else launch_fp32_tiled<64, AK, BK>(p, stream);
+}
+
+void launch_fp32(const Params& p, bool ak, bool bk, hipStream_t stream) {
+    if (ak && bk) launch_fp32_layout<true, true>(p, stream);
+    else if (ak && !bk) launch_fp32_layout<true, false>(p, stream);
+    else if (!ak && bk) launch_fp32_layout<false, true>(p, stream);
+    else launch_fp32_layout<false, false>(p, stream);
 }
 
 // dst[b][c][r] = src[b][r][c] for 16-bit elements: 64 x 64 tiles through LDS,
@@ -394,7 +345,7 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     const bool fused_moments = moments && mode == 1 && splits == 1 && !bias && epilogue == 0 && beta == 0.0f &&
                                gemm::big_eligible(p, a_bf16, b_bf16);
     p.moments = fused_moments ? moments : nullptr;
-    if (mode == 0) gemm::launch_mode<0>(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
+    if (mode == 0) gemm::launch_fp32(p, a_kcontig != 0, b_kcontig != 0, stream);
     else gemm::launch_bf16(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
     check_launch("Launch GEMM");
     if (splits > 1) {

@@ -108,12 +108,21 @@ def transpose16(src, dst, *, batch, rows, cols):
 
 
 def split_count(m, n, k, batch, mode):
-    """K splits so that a weight-gradient product puts at least two workgroups on each of the 256 CUs."""
-    tm = 256 if mode == BF16 else 128
-    tiles = ((m + tm - 1) // tm) * ((n + 127) // 128) * batch
-    ktiles = (k + 31) // 32
+    """K splits for a weight-gradient product (small output, K = rows).
+
+    bf16: at least two 256x128-tile workgroups per CU, each split >= 512 of K.
+    fp32: the MFMA-issue-bound fp32 kernel runs 64x64 tiles for such products;
+    at least 1024 workgroups (four per CU), each split >= 64 of K."""
     splits = 1
-    while tiles * splits < 512 and splits * 2 <= max(1, ktiles // 16) and splits < 64:
+    if mode == BF16:
+        tiles = ((m + 255) // 256) * ((n + 127) // 128) * batch
+        ktiles = (k + 31) // 32
+        while tiles * splits < 512 and splits * 2 <= max(1, ktiles // 16) and splits < 64:
+            splits *= 2
+        return splits
+    tiles = ((m + 63) // 64) * ((n + 63) // 64) * batch
+    steps = (k + 15) // 16
+    while tiles * splits < 1024 and splits * 2 <= max(1, steps // 4) and splits < 256:
         splits *= 2
     return splits
 
