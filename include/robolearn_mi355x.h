@@ -46,7 +46,8 @@ int rl_plan_destroy(void* plan);
 /* Row-major batched D[b] = act(op(A[b]) op(B[b]) + bias[b]) + beta C[b] on MFMA
  * (mode 0: fp32 v_mfma_f32_32x32x2_f32, mode 1: bf16 v_mfma_f32_32x32x16_bf16).
  * A(m,k) = a_kcontig ? A[m*lda+k] : A[k*lda+m]; B(k,n) = b_kcontig ? B[n*ldb+k]
- * : B[k*ldb+n].  epilogue 0 none, 1 ReLU, 2 ELU.  splits > 1 reduces over K in
+ * : B[k*ldb+n].  epilogue 0 none, 1 ReLU, 2 ELU, 3 ELU gradient (mode 0 only:
+ * D = AB * elu'(C) with C the ELU outputs, beta 0, no bias).  splits > 1 reduces over K in
  * fixed order through workspace; d_bf16 (optional) receives a bf16 copy of D.
  * moments (optional, needs ldd == n) receives the per-256-row-chunk column
  * (mean, M2) of D in rl_bn_forward_ex's partial layout [batch][ceil(m/256)][2][n],

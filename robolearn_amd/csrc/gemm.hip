@@ -193,8 +193,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
                 const long long offset = static_cast<long long>(row) * ldd + col;
                 float* out = D + offset;
                 if (direct) {
-                    float value = apply_epilogue(acc[i][j][v] + bcol, p.epilogue);
-                    if (p.beta != 0.0f) value += p.beta * C[offset];
+                    float value;
+                    if (p.epilogue == kEluGrad) {
+                        value = acc[i][j][v] * elu_grad_from_output(C[offset]);
+                    } else {
+                        value = apply_epilogue(acc[i][j][v] + bcol, p.epilogue);
+                        if (p.beta != 0.0f) value += p.beta * C[offset];
+                    }
                     *out = value;
                     if (p.d_bf16) p.d_bf16[batch * p.stride_d + offset] = f32_to_bf16_bits(value);
                 } else {
@@ -217,13 +222,59 @@ __global__ void splitk_reduce(const float* work, float* d, unsigned short* d_bf1
         const int b = static_cast<int>(idx / (static_cast<long long>(m) * n));
         float value = 0.0f;
         for (int s = 0; s < splits; ++s) value += work[(static_cast<long long>(s) * batch + b) * m * n + static_cast<long long>(row) * n + col];
-        if (bias) value += bias[b * stride_bias + col];
-        value = apply_epilogue(value, epilogue);
         const long long offset = b * stride_d + static_cast<long long>(row) * ldd + col;
-        if (beta != 0.0f) value += beta * c[offset];
+        if (epilogue == kEluGrad) {
+            value *= elu_grad_from_output(c[offset]);
+        } else {
+            if (bias) value += bias[b * stride_bias + col];
+            value = apply_epilogue(value, epilogue);
+            if (beta != 0.0f) value += beta * c[offset];
+        }
         d[offset] = value;
         if (d_bf16) d_bf16[offset] = f32_to_bf16_bits(value);
     }
+}
+
+// Same reduction for many splits: a workgroup covers kReduceCols consecutive
+// outputs with kReduceGroups threads each; group g adds splits g, g + G, ...
+// in order and group 0 adds the group sums in order, so the result is fixed
+// and each thread's chain is splits / G loads long.
+constexpr int kReduceGroups = 8;
+constexpr int kReduceCols = 256 / kReduceGroups;
+
+__global__ __launch_bounds__(256) void splitk_reduce_grouped(const float* work, float* d, unsigned short* d_bf16,
+                                                             const float* c, const float* bias, long long ldd,
+                                                             long long stride_d, long long stride_bias, int m, int n,
+                                                             int batch, int splits, float beta, int epilogue) {
+    __shared__ float part[kReduceGroups][kReduceCols];
+    const long long total = static_cast<long long>(batch) * m * n;
+    const int e = threadIdx.x % kReduceCols;
+    const int g = threadIdx.x / kReduceCols;
+    const long long idx = static_cast<long long>(blockIdx.x) * kReduceCols + e;
+    const long long plane = static_cast<long long>(m) * n;
+    float value = 0.0f;
+    if (idx < total) {
+        const int b = static_cast<int>(idx / plane);
+        const long long within = idx - b * plane;
+        for (int s = g; s < splits; s += kReduceGroups) value += work[(static_cast<long long>(s) * batch + b) * plane + within];
+    }
+    part[g][e] = value;
+    __syncthreads();
+    if (g != 0 || idx >= total) return;
+    for (int k = 1; k < kReduceGroups; ++k) value += part[k][e];
+    const int col = static_cast<int>(idx % n);
+    const int row = static_cast<int>((idx / n) % m);
+    const int b = static_cast<int>(idx / plane);
+    const long long offset = b * stride_d + static_cast<long long>(row) * ldd + col;
+    if (epilogue == kEluGrad) {
+        value *= elu_grad_from_output(c[offset]);
+    } else {
+        if (bias) value += bias[b * stride_bias + col];
+        value = apply_epilogue(value, epilogue);
+        if (beta != 0.0f) value += beta * c[offset];
+    }
+    d[offset] = value;
+    if (d_bf16) d_bf16[offset] = f32_to_bf16_bits(value);
 }
 
 // Output tile edge for an fp32 product: 64 unless 128-wide tiles would still
@@ -290,7 +341,9 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     require(m > 0 && n > 0 && k > 0 && batch > 0, "GEMM dimensions must be positive.");
     require(a && b && d, "GEMM operands must be nonnull.");
     require(std::isfinite(beta) && (beta == 0.0f || c), "Nonzero beta requires C; beta must be finite.");
-    require(epilogue >= 0 && epilogue <= 2, "Unknown GEMM epilogue.");
+    require(epilogue >= 0 && epilogue <= 3, "Unknown GEMM epilogue.");
+    require(epilogue != 3 || (mode == 0 && c && beta == 0.0f && !bias),
+            "The ELU-gradient epilogue needs fp32 mode, the ELU outputs as C, beta 0 and no bias.");
     require(splits >= 1, "GEMM split count must be positive.");
     require(static_cast<long long>(m) * n <= std::numeric_limits<int>::max(), "GEMM output exceeds 2^31 elements.");
     require(!moments || (ldd == n && aligned(moments, 16)),
@@ -351,8 +404,13 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     if (splits > 1) {
         const long long total = static_cast<long long>(batch) * m * n;
         const unsigned blocks = static_cast<unsigned>(std::min<long long>((total + 255) / 256, 4096));
-        hipLaunchKernelGGL(gemm::splitk_reduce, dim3(blocks), dim3(256), 0, stream, workspace, d, d_bf16, c, bias, ldd,
-                           stride_d, stride_bias, m, n, batch, splits, beta, epilogue);
+        if (splits >= 2 * gemm::kReduceGroups && total <= (1LL << 22))
+            hipLaunchKernelGGL(gemm::splitk_reduce_grouped, dim3(ceil_div(total, gemm::kReduceCols)), dim3(256), 0,
+                               stream, workspace, d, d_bf16, c, bias, ldd, stride_d, stride_bias, m, n, batch, splits,
+                               beta, epilogue);
+        else
+            hipLaunchKernelGGL(gemm::splitk_reduce, dim3(blocks), dim3(256), 0, stream, workspace, d, d_bf16, c, bias,
+                               ldd, stride_d, stride_bias, m, n, batch, splits, beta, epilogue);
         check_launch("Launch split-K reduction");
     }
     if (moments && !fused_moments) bn_chunk_moments(batch, d, stride_d, moments, m, n, stream);

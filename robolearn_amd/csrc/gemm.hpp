@@ -13,7 +13,12 @@ typedef unsigned short u16x8_t __attribute__((ext_vector_type(8)));
 constexpr int kThreads = 256;
 constexpr int kTile = 128;
 
-enum Epilogue : int { kNone = 0, kRelu = 1, kElu = 2 };
+// kEluGrad (fp32 mode only): D = (A B) * elu'(C), where C holds the ELU
+// outputs y and elu'(z) = 1 for y > 0, y + 1 otherwise (the input-gradient
+// product of an ELU layer with the activation backward fused in).
+enum Epilogue : int { kNone = 0, kRelu = 1, kElu = 2, kEluGrad = 3 };
+
+__device__ __forceinline__ float elu_grad_from_output(float y) { return y > 0.0f ? 1.0f : y + 1.0f; }
 
 struct Params {
     const void* a;

@@ -11,7 +11,7 @@ from . import _native
 
 FP32 = 0
 BF16 = 1
-EPILOGUES = {None: 0, "relu": 1, "elu": 2}
+EPILOGUES = {None: 0, "relu": 1, "elu": 2, "elu_grad": 3}
 
 
 def stream() -> int:
@@ -85,9 +85,10 @@ def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None,
 
 
 def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=FP32, c=None, beta=0.0,
-                          d_bf16=None, wt=None):
+                          d_bf16=None, wt=None, epilogue=None):
     """dx[e] = dy[e] w[e] (+ beta c).  wt: optional [ensemble, in_dim, out_dim] transposed copy of w,
-    which lets both operands be read K-contiguously."""
+    which lets both operands be read K-contiguously.  epilogue "elu_grad" (fp32) multiplies by
+    elu'(c), c holding the ELU outputs of the layer below."""
     _check(dx, ensemble * rows * in_dim, "input gradient")
     if wt is not None:
         _check(wt, ensemble * out_dim * in_dim, "transposed weight", wt.dtype)
@@ -97,7 +98,7 @@ def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=
         return
     gemm(dy, w, dx, m=rows, n=in_dim, k=out_dim, batch=ensemble, a_kcontig=True, b_kcontig=False, lda=out_dim,
          ldb=in_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=out_dim * in_dim, stride_d=rows * in_dim,
-         mode=mode, c=c, beta=beta, d_bf16=d_bf16)
+         mode=mode, c=c, beta=beta, d_bf16=d_bf16, epilogue=epilogue)
 
 
 def transpose16(src, dst, *, batch, rows, cols):

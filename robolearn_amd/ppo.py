@@ -182,9 +182,9 @@ class WarpPPO:
                                      out_dim=out_dim, mode=K.FP32, workspace=self.workspace)
             K.bias_grad(d, g[f"{prefix}.{i}.bias"], self.partial, rows=rows, channels=out_dim)
             if i > 0:
-                K.linear_backward_input(d, w, dbufs[i], rows=rows, in_dim=widths[i], out_dim=out_dim, mode=K.FP32)
-                _native.call("rl_elu_backward", dbufs[i].data_ptr(), hidden[i - 1].data_ptr(), dbufs[i].numel(),
-                             K.stream())
+                # input gradient with the ELU backward of the layer below fused in
+                K.linear_backward_input(d, w, dbufs[i], rows=rows, in_dim=widths[i], out_dim=out_dim, mode=K.FP32,
+                                        c=hidden[i - 1], epilogue="elu_grad")
                 d = dbufs[i]
                 out_dim = widths[i]
 

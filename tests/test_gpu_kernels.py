@@ -339,3 +339,17 @@ def test_input_gradient_with_transposed_weight(gpu):
     tol = 1e-5 * math.sqrt(out_dim)
     torch.testing.assert_close(dx1.cpu().double(), ref, rtol=1e-5, atol=tol)
     torch.testing.assert_close(dx0.cpu(), dx1.cpu(), rtol=1e-5, atol=tol)
+
+
+@pytest.mark.parametrize("m,n,k,splits", [(300, 130, 77, 1), (2048, 512, 256, 1), (96, 64, 4096, 16)])
+def test_fp32_elu_gradient_epilogue(gpu, m, n, k, splits):
+    print(f"case elu_grad epilogue m={m} n={n} k={k} splits={splits}", flush=True)
+    g = torch.Generator().manual_seed(m + n + k)
+    a, b = torch.randn(m, k, generator=g), torch.randn(k, n, generator=g)
+    y = torch.nn.functional.elu(torch.randn(m, n, generator=g))
+    d = torch.empty(m, n, device=gpu)
+    workspace = torch.empty(splits * m * n * 4, dtype=torch.uint8, device=gpu) if splits > 1 else None
+    K.gemm(a.to(gpu), b.to(gpu), d, m=m, n=n, k=k, a_kcontig=True, b_kcontig=False, lda=k, ldb=n, ldd=n,
+           c=y.to(gpu), epilogue="elu_grad", mode=K.FP32, splits=splits, workspace=workspace)
+    expected = (a.double() @ b.double()) * torch.where(y > 0, torch.ones_like(y), y + 1).double()
+    torch.testing.assert_close(d.cpu().double(), expected, rtol=1e-4, atol=1e-4 * math.sqrt(k))
