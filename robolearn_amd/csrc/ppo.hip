@@ -140,29 +140,26 @@ struct GatherArgs {
     float *b_obs, *b_actions, *b_log_probs, *b_values, *b_advantages, *b_returns, *b_means, *b_stds;
 };
 
-__global__ void gather_kernel(GatherArgs a) {
-    const long long r = blockIdx.y;
-    if (r >= a.rows) return;
+// One wave per sampled row (kGatherRows rows per workgroup): coalesced copies
+// of the row's observation, action, mean and std vectors, then its scalars.
+constexpr int kGatherRows = 4;
+
+__global__ __launch_bounds__(kGatherRows* kWave) void gather_kernel(GatherArgs a) {
+    const long long r = static_cast<long long>(blockIdx.x) * kGatherRows + threadIdx.x / kWave;
+    if (r >= a.rows) return;  // wave-uniform
+    const int lane = threadIdx.x % kWave;
     const long long k = a.indices[a.offset + r];
-    const int width = a.obs_dim + 3 * a.action_dim + 4;
-    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < width; j += gridDim.x * blockDim.x) {
-        if (j < a.obs_dim) a.b_obs[r * a.obs_ld + j] = a.obs[k * a.obs_dim + j];
-        else if (j < a.obs_dim + a.action_dim) {
-            const int c = j - a.obs_dim;
-            a.b_actions[r * a.action_dim + c] = a.actions[k * a.action_dim + c];
-        } else if (j < a.obs_dim + 2 * a.action_dim) {
-            const int c = j - a.obs_dim - a.action_dim;
-            a.b_means[r * a.action_dim + c] = a.means[k * a.action_dim + c];
-        } else if (j < a.obs_dim + 3 * a.action_dim) {
-            const int c = j - a.obs_dim - 2 * a.action_dim;
-            a.b_stds[r * a.action_dim + c] = a.stds[k * a.action_dim + c];
-        } else {
-            const int f = j - a.obs_dim - 3 * a.action_dim;
-            if (f == 0) a.b_log_probs[r] = a.log_probs[k];
-            else if (f == 1) a.b_values[r] = a.values[k];
-            else if (f == 2) a.b_advantages[r] = a.advantages[k];
-            else a.b_returns[r] = a.returns[k];
-        }
+    for (int j = lane; j < a.obs_dim; j += kWave) a.b_obs[r * a.obs_ld + j] = a.obs[k * a.obs_dim + j];
+    for (int c = lane; c < a.action_dim; c += kWave) {
+        a.b_actions[r * a.action_dim + c] = a.actions[k * a.action_dim + c];
+        a.b_means[r * a.action_dim + c] = a.means[k * a.action_dim + c];
+        a.b_stds[r * a.action_dim + c] = a.stds[k * a.action_dim + c];
+    }
+    if (lane == 0) {
+        a.b_log_probs[r] = a.log_probs[k];
+        a.b_values[r] = a.values[k];
+        a.b_advantages[r] = a.advantages[k];
+        a.b_returns[r] = a.returns[k];
     }
 }
 
@@ -440,15 +437,14 @@ RL_API int rl_ppo_gather(const int* indices, long long offset, long long rows, i
                          float* b_obs, float* b_actions, float* b_log_probs, float* b_values, float* b_advantages,
                          float* b_returns, float* b_means, float* b_stds, void* stream) noexcept {
     return rl::guarded("rl_ppo_gather", [&] {
-        rl::require(indices && rows > 0 && rows <= 65535 * 4 && obs_dim > 0 && action_dim > 0 && obs_ld >= obs_dim,
+        rl::require(indices && rows > 0 && rows <= (1LL << 32) && obs_dim > 0 && action_dim > 0 && obs_ld >= obs_dim,
                     "PPO gather shapes are invalid.");
-        rl::require(rows <= 65535, "PPO gather supports at most 65535 rows per launch.");
+
         Q::GatherArgs a{indices, offset, rows, obs_dim, action_dim, obs_ld, obs, actions, log_probs, values, advantages,
                         returns, means, stds, b_obs, b_actions, b_log_probs, b_values, b_advantages, b_returns, b_means,
                         b_stds};
-        const int width = obs_dim + 3 * action_dim + 4;
-        hipLaunchKernelGGL(Q::gather_kernel, dim3(rl::ceil_div(width, 256), static_cast<unsigned>(rows)), dim3(256), 0,
-                           rl::as_stream(stream), a);
+        hipLaunchKernelGGL(Q::gather_kernel, dim3(rl::ceil_div(rows, Q::kGatherRows)), dim3(Q::kGatherRows * rl::kWave),
+                           0, rl::as_stream(stream), a);
         rl::check_launch("Launch PPO gather");
     });
 }

@@ -65,12 +65,14 @@ def forward_split_count(m, n, k, batch, mode):
 
 
 def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None, bias=None, epilogue=None,
-                   mode=FP32, c=None, beta=0.0, d_bf16=None, moments=None, workspace=None):
+                   mode=FP32, c=None, beta=0.0, d_bf16=None, moments=None, workspace=None, x_ld=None):
     """y[e] = act(x[e] w[e]^T + bias[e]) (+ beta c); x_stride 0 broadcasts x; moments receives
     y's per-256-row-chunk column moments (the BatchNorm partial layout).  With a workspace,
-    a product too small to fill the GPU is split over K (fixed-order reduction)."""
+    a product too small to fill the GPU is split over K (fixed-order reduction).  x_ld: row
+    pitch of x (default in_dim)."""
+    x_ld = x_ld or in_dim
     if x_stride is None:
-        x_stride = rows * in_dim
+        x_stride = rows * x_ld
     _check(w, ensemble * out_dim * in_dim, "weight", w.dtype)
     _check(y, ensemble * rows * out_dim, "output")
     splits = forward_split_count(rows, out_dim, in_dim, ensemble, mode) if workspace is not None else 1
@@ -78,7 +80,7 @@ def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None,
         need = _native.load().rl_gemm_workspace(mode, rows, out_dim, in_dim, ensemble, splits)
         if need > workspace.numel() * workspace.element_size():
             splits = 1
-    gemm(x, w, y, m=rows, n=out_dim, k=in_dim, batch=ensemble, a_kcontig=True, b_kcontig=True, lda=in_dim,
+    gemm(x, w, y, m=rows, n=out_dim, k=in_dim, batch=ensemble, a_kcontig=True, b_kcontig=True, lda=x_ld,
          ldb=in_dim, ldd=out_dim, stride_a=x_stride, stride_b=out_dim * in_dim, stride_d=rows * out_dim, bias=bias,
          stride_bias=out_dim, epilogue=epilogue, mode=mode, c=c, beta=beta, d_bf16=d_bf16, moments=moments,
          splits=splits, workspace=workspace if splits > 1 else None)
@@ -129,10 +131,12 @@ def split_count(m, n, k, batch, mode):
 
 
 def linear_backward_weight(dy, x, dw, *, rows, in_dim, out_dim, ensemble=1, x_stride=None, mode=FP32,
-                           workspace=None, beta=0.0):
-    """dw[e] = dy[e]^T x[e] (+ beta dw), split-K over rows when the tile grid is small."""
+                           workspace=None, beta=0.0, x_ld=None):
+    """dw[e] = dy[e]^T x[e] (+ beta dw), split-K over rows when the tile grid is small.
+    x_ld: row pitch of x (default in_dim)."""
+    x_ld = x_ld or in_dim
     if x_stride is None:
-        x_stride = rows * in_dim
+        x_stride = rows * x_ld
     _check(dw, ensemble * out_dim * in_dim, "weight gradient")
     splits = split_count(out_dim, in_dim, rows, ensemble, mode) if workspace is not None else 1
     if splits > 1:
@@ -140,7 +144,7 @@ def linear_backward_weight(dy, x, dw, *, rows, in_dim, out_dim, ensemble=1, x_st
         if need > workspace.numel() * workspace.element_size():
             splits = 1
     gemm(dy, x, dw, m=out_dim, n=in_dim, k=rows, batch=ensemble, a_kcontig=False, b_kcontig=False, lda=out_dim,
-         ldb=in_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=x_stride, stride_d=out_dim * in_dim, mode=mode,
+         ldb=x_ld, ldd=in_dim, stride_a=rows * out_dim, stride_b=x_stride, stride_d=out_dim * in_dim, mode=mode,
          splits=splits, workspace=workspace if splits > 1 else None, c=dw if beta else None, beta=beta)
 
 

@@ -107,7 +107,10 @@ class WarpPPO:
             self._seed = torch.tensor([cfg.seed], dtype=torch.int32, device=dev)
             self._stats = z(2)
             self._perm = torch.zeros(N, dtype=torch.int32, device=dev)
-            self.b_obs = z(M, O)
+            # minibatch observations with 16-byte aligned rows (zero pad columns) so the
+            # first layer's products read them with vector loads
+            self.obs_ld = (O + 3) // 4 * 4
+            self.b_obs = z(M, self.obs_ld)
             self.b_actions, self.b_means, self.b_stds = z(M, A), z(M, A), z(M, A)
             self.b_log_probs, self.b_values, self.b_advantages, self.b_returns = z(M), z(M), z(M), z(M)
             widths = (O, *cfg.hidden_dims)
@@ -158,19 +161,20 @@ class WarpPPO:
         p = self.store.params()
         return p[f"{prefix}.{i}.weight"], p[f"{prefix}.{i}.bias"]
 
-    def _mlp_forward(self, prefix, x, rows, hidden, out):
-        """Linear + ELU hidden layers (ELU fused in the GEMM epilogue), linear output."""
+    def _mlp_forward(self, prefix, x, rows, hidden, out, x_ld=None):
+        """Linear + ELU hidden layers (ELU fused in the GEMM epilogue), linear output.
+        x_ld: row pitch of x (default the observation width)."""
         widths = (self.observation_dim, *self.config.hidden_dims)
         inputs = x
         for i, width in enumerate(self.config.hidden_dims):
             w, b = self._layer(prefix, i)
             K.linear_forward(inputs, w, hidden[i], rows=rows, in_dim=widths[i], out_dim=width, bias=b,
-                             epilogue="elu", mode=K.FP32)
+                             epilogue="elu", mode=K.FP32, x_ld=x_ld if i == 0 else None)
             inputs = hidden[i]
         w, b = self._layer(prefix, self.layers - 1)
         K.linear_forward(inputs, w, out, rows=rows, in_dim=widths[-1], out_dim=out.shape[1], bias=b, mode=K.FP32)
 
-    def _mlp_backward(self, prefix, x, rows, hidden, dout, dbufs):
+    def _mlp_backward(self, prefix, x, rows, hidden, dout, dbufs, x_ld=None):
         widths = (self.observation_dim, *self.config.hidden_dims)
         g = self.grads
         d = dout
@@ -179,7 +183,8 @@ class WarpPPO:
             w, _ = self._layer(prefix, i)
             inputs = x if i == 0 else hidden[i - 1]
             K.linear_backward_weight(d, inputs, g[f"{prefix}.{i}.weight"], rows=rows, in_dim=widths[i],
-                                     out_dim=out_dim, mode=K.FP32, workspace=self.workspace)
+                                     out_dim=out_dim, mode=K.FP32, workspace=self.workspace,
+                                     x_ld=x_ld if i == 0 else None)
             K.bias_grad(d, g[f"{prefix}.{i}.bias"], self.partial, rows=rows, channels=out_dim)
             if i > 0:
                 # input gradient with the ELU backward of the layer below fused in
@@ -202,19 +207,19 @@ class WarpPPO:
     def _minibatch(self, offset: int):
         cfg = self.config
         M, A, O = self.mini_batch_size, self.action_dim, self.observation_dim
-        _native.call("rl_ppo_gather", self._perm.data_ptr(), offset, M, O, A, O, self.observations.data_ptr(),
+        _native.call("rl_ppo_gather", self._perm.data_ptr(), offset, M, O, A, self.obs_ld, self.observations.data_ptr(),
                      self.actions.data_ptr(), self.log_probs.data_ptr(), self.values.data_ptr(),
                      self.advantages.data_ptr(), self.returns.data_ptr(), self.means.data_ptr(),
                      self.stds.data_ptr(), self.b_obs.data_ptr(), self.b_actions.data_ptr(),
                      self.b_log_probs.data_ptr(), self.b_values.data_ptr(), self.b_advantages.data_ptr(),
                      self.b_returns.data_ptr(), self.b_means.data_ptr(), self.b_stds.data_ptr(), K.stream())
-        self._mlp_forward("actor", self.b_obs, M, self.actor_h, self.mean)
+        self._mlp_forward("actor", self.b_obs, M, self.actor_h, self.mean, x_ld=self.obs_ld)
         std_type = int(cfg.std_type == "scalar")
         _native.call("rl_ppo_kl_adapt", self.mean.data_ptr(), A, self.distribution_parameter.data_ptr(),
                      self.b_means.data_ptr(), self.b_stds.data_ptr(), M, A, std_type, float(cfg.std_range[0]),
                      float(cfg.std_range[1]), float(cfg.desired_kl), int(cfg.schedule == "adaptive"),
                      self.partial.data_ptr(), self.kl.data_ptr(), self.lr.data_ptr(), K.stream())
-        self._mlp_forward("critic", self.b_obs, M, self.critic_h, self.value)
+        self._mlp_forward("critic", self.b_obs, M, self.critic_h, self.value, x_ld=self.obs_ld)
         _native.call("rl_ppo_loss", self.mean.data_ptr(), A, self.value.data_ptr(),
                      self.distribution_parameter.data_ptr(), self.b_actions.data_ptr(), self.b_log_probs.data_ptr(),
                      self.b_values.data_ptr(), self.b_advantages.data_ptr(), self.b_returns.data_ptr(), M, A, std_type,
@@ -223,8 +228,8 @@ class WarpPPO:
                      int(cfg.clip_value), self.dmean.data_ptr(), self.dvalue.data_ptr(), self.dstd_rows.data_ptr(),
                      self.row_terms.data_ptr(), self.totals.data_ptr(), K.stream())
         K.bias_grad(self.dstd_rows, self.grads["std"], self.partial, rows=M, channels=A)
-        self._mlp_backward("actor", self.b_obs, M, self.actor_h, self.dmean, self.actor_d)
-        self._mlp_backward("critic", self.b_obs, M, self.critic_h, self.dvalue, self.critic_d)
+        self._mlp_backward("actor", self.b_obs, M, self.actor_h, self.dmean, self.actor_d, x_ld=self.obs_ld)
+        self._mlp_backward("critic", self.b_obs, M, self.critic_h, self.dvalue, self.critic_d, x_ld=self.obs_ld)
         for (start, end), norm in zip(self.group_ranges, self.group_norms):
             grad = self.store.grad[start:end]
             _native.call("rl_sum_squares", grad.data_ptr(), grad.numel(), self.norm_partial.data_ptr(),
