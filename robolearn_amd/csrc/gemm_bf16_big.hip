@@ -36,6 +36,7 @@ constexpr int EP = 136;  // epilogue staging pitch in floats (32 x 136 x 4 B per
 // Plain vector types (HIP's uint4 is a class the optimizer cannot always keep in registers).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ unsigned int low_halves(unsigned int a, unsigned int b) { return (a & 0xFFFFu) | (b << 16); }
 __device__ __forceinline__ unsigned int high_halves(unsigned int a, unsigned int b) {
@@ -293,10 +294,12 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
                     val.w += p.beta * c.w;
                 }
                 if (Dh)
-                    *reinterpret_cast<uint2*>(Dh + offset) =
-                        make_uint2(f32x2_to_bf16x2(val.x, val.y), f32x2_to_bf16x2(val.z, val.w));
+                    __builtin_nontemporal_store((u32x2){f32x2_to_bf16x2(val.x, val.y), f32x2_to_bf16x2(val.z, val.w)},
+                                                reinterpret_cast<u32x2*>(Dh + offset));
             }
-            *reinterpret_cast<float4*>(D + offset) = val;
+            // streaming stores: nothing in this kernel rereads D, and the tile
+            // rounds write far more than the L2 holds
+            __builtin_nontemporal_store((f32x4){val.x, val.y, val.z, val.w}, reinterpret_cast<f32x4*>(D + offset));
         }
     }
     if (moments) {
