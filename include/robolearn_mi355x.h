@@ -52,13 +52,17 @@ int rl_plan_destroy(void* plan);
  * moments (optional, needs ldd == n) receives the per-256-row-chunk column
  * (mean, M2) of D in rl_bn_forward_ex's partial layout [batch][ceil(m/256)][2][n],
  * from the GEMM epilogue when the 256x256 bf16 kernel runs the product.
+ * a_sums (optional, mode 0 only) receives the row sums of op(A) over K,
+ * [batch][m]: the bias gradient of a weight-gradient product dW = dY^T X.
+ * With splits > 1 the workspace holds splits*batch*m*n floats, plus splits*batch*m
+ * with a_sums (rl_gemm_workspace returns the larger size).
  * Serves the three plans of one Linear, robolearn/cuda/linear.py:179-185,
  * 341-360, and the ensemble einsum of robolearn/flashsac/layers.py:174-186. */
 int rl_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int m, int n, int k, int batch,
             const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
             const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
             float beta, int epilogue, int splits, float* workspace, size_t workspace_bytes, void* d_bf16,
-            float* moments, void* stream);
+            float* moments, float* a_sums, void* stream);
 size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, int splits);
 /* dst[b][c][r] = src[b][r][c] over 16-bit elements (bf16 weight copies transposed
  * so the input-gradient product reads both operands K-contiguously).  No

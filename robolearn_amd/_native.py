@@ -32,7 +32,7 @@ SIGNATURES = {
     "rl_last_error": (c_char_p, []),
     # dense
     "rl_gemm": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, P, c_ll, c_ll, P, c_ll, c_ll,
-                        P, P, c_ll, c_ll, P, c_ll, c_float, c_int, c_int, P, c_size, P, P, P]),
+                        P, P, c_ll, c_ll, P, c_ll, c_float, c_int, c_int, P, c_size, P, P, P, P]),
     "rl_gemm_workspace": (c_size, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "rl_transpose16": (c_int, [P, P, c_int, c_int, c_int, P]),
     "rl_plan_create": (c_void, [c_int] * 10 + [c_size]),

@@ -122,6 +122,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
     TileLoader<BK, T> lb;
     const bool avec = p.a_vec != 0;
     const bool bvec = p.b_vec != 0;
+    // Row sums of op(A) over this split's K (the bias gradient of a weight-
+    // gradient product), by the workgroups of the first N tile: thread t adds
+    // kFp32K * T / 256 staged values of row t / (256 / T) per step.
+    constexpr int SumLanes = kThreads / T;
+    constexpr int SumPer = kFp32K / SumLanes;
+    const bool row_sums = p.a_sums != nullptr && blockIdx.x == 0;
+    float a_sum = 0.0f;
 
     // B is indexed (n, k) when BK else (k, n); the loader wants (row=n, k).
     if (k_begin < k_end) {
@@ -151,6 +158,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
             bfr[j][0] = *reinterpret_cast<const float4*>(q);
             bfr[j][1] = *reinterpret_cast<const float4*>(q + 4);
         }
+        if (row_sums) {
+            const float* q = sa + (threadIdx.x / SumLanes) * kFp32Pitch + (threadIdx.x % SumLanes) * SumPer;
+#pragma unroll
+            for (int e = 0; e < SumPer; ++e) a_sum += q[e];
+        }
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
 #pragma unroll
@@ -169,6 +181,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
             lb.store(sb);
         }
         __syncthreads();
+    }
+
+    if (row_sums) {
+        // the SumLanes partial sums of a row sit in adjacent lanes: fixed-order butterfly
+#pragma unroll
+        for (int offset = 1; offset < SumLanes; offset <<= 1) a_sum += __shfl_xor(a_sum, offset);
+        const int r = m0 + static_cast<int>(threadIdx.x) / SumLanes;
+        if (threadIdx.x % SumLanes == 0 && r < p.m)
+            p.a_sums[(static_cast<long long>(split) * p.batch + batch) * p.m + r] = a_sum;
     }
 
     // Accumulator layout of a 32x32 MFMA tile: lane l holds column l % 32 and
@@ -335,7 +356,7 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
              const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
              const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
              float beta, int epilogue, int splits, float* workspace, std::size_t workspace_bytes, hipStream_t stream,
-             unsigned short* d_bf16, float* moments) {
+             unsigned short* d_bf16, float* moments, float* a_sums) {
     require(mode == 0 || mode == 1, "GEMM mode must be 0 (fp32) or 1 (bf16 operands).");
     require(!(mode == 0 && (a_bf16 || b_bf16)), "fp32 GEMM mode requires fp32 operands.");
     require(m > 0 && n > 0 && k > 0 && batch > 0, "GEMM dimensions must be positive.");
@@ -346,6 +367,7 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
             "The ELU-gradient epilogue needs fp32 mode, the ELU outputs as C, beta 0 and no bias.");
     require(splits >= 1, "GEMM split count must be positive.");
     require(static_cast<long long>(m) * n <= std::numeric_limits<int>::max(), "GEMM output exceeds 2^31 elements.");
+    require(!a_sums || mode == 0, "Row sums of A are produced by the fp32 GEMM family only.");
     require(!moments || (ldd == n && aligned(moments, 16)),
             "GEMM output moments need a row-contiguous output (ldd == n) and 16-byte aligned storage.");
     gemm::Params p{};
@@ -379,16 +401,19 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     p.a_vec = aligned(a, 16) && (lda * a_elem) % 16 == 0 && (stride_a * a_elem) % 16 == 0;
     p.b_vec = aligned(b, 16) && (ldb * b_elem) % 16 == 0 && (stride_b * b_elem) % 16 == 0;
     if (splits > 1) {
-        const std::size_t need = static_cast<std::size_t>(splits) * batch * m * n * sizeof(float);
+        const std::size_t need = static_cast<std::size_t>(splits) * batch *
+                                 (static_cast<std::size_t>(m) * n + (a_sums ? m : 0)) * sizeof(float);
         require(workspace && workspace_bytes >= need && aligned(workspace, 16),
                 "Split-K GEMM workspace is null, misaligned or too small.");
         p.d = workspace;
+        p.a_sums = a_sums ? workspace + static_cast<std::size_t>(splits) * batch * m * n : nullptr;
         p.c = nullptr;
         p.beta = 0.0f;
         p.epilogue = 0;
         p.d_bf16 = nullptr;
     } else {
         p.d = d;
+        p.a_sums = a_sums;
     }
     p.out_vec = n % 4 == 0 && aligned(p.d, 16) && (splits > 1 || (ldd % 4 == 0 && stride_d % 4 == 0)) &&
                 (splits > 1 || ((!bias || (aligned(bias, 16) && stride_bias % 4 == 0)) &&
@@ -412,6 +437,22 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
             hipLaunchKernelGGL(gemm::splitk_reduce, dim3(blocks), dim3(256), 0, stream, workspace, d, d_bf16, c, bias,
                                ldd, stride_d, stride_bias, m, n, batch, splits, beta, epilogue);
         check_launch("Launch split-K reduction");
+        if (a_sums) {
+            // [splits][batch][m] partial row sums -> [batch][m], fixed order
+            const float* work = workspace + static_cast<std::size_t>(splits) * batch * m * n;
+            if (splits >= 2 * gemm::kReduceGroups)
+                hipLaunchKernelGGL(gemm::splitk_reduce_grouped, dim3(ceil_div(static_cast<long long>(batch) * m,
+                                                                               gemm::kReduceCols)),
+                                   dim3(256), 0, stream, work, a_sums, nullptr, nullptr, nullptr,
+                                   static_cast<long long>(m), static_cast<long long>(m), 0LL, 1, m, batch, splits, 0.0f,
+                                   0);
+            else
+                hipLaunchKernelGGL(gemm::splitk_reduce, dim3(ceil_div(static_cast<long long>(batch) * m, 256)),
+                                   dim3(256), 0, stream, work, a_sums, nullptr, nullptr, nullptr,
+                                   static_cast<long long>(m), static_cast<long long>(m), 0LL, 1, m, batch, splits, 0.0f,
+                                   0);
+            check_launch("Launch row-sum reduction");
+        }
     }
     if (moments && !fused_moments) bn_chunk_moments(batch, d, stride_d, moments, m, n, stream);
     return 0;
@@ -423,11 +464,12 @@ RL_API int rl_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kconti
                    const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
                    const float* c, float* d, long long ldd, long long stride_d, const float* bias,
                    long long stride_bias, float beta, int epilogue, int splits, float* workspace,
-                   std::size_t workspace_bytes, void* d_bf16, float* moments, void* stream) noexcept {
+                   std::size_t workspace_bytes, void* d_bf16, float* moments, float* a_sums,
+                   void* stream) noexcept {
     return rl::guarded("rl_gemm", [&] {
         rl::run_gemm(mode, a_bf16, b_bf16, a_kcontig, b_kcontig, m, n, k, batch, a, lda, stride_a, b, ldb, stride_b, c,
                      d, ldd, stride_d, bias, stride_bias, beta, epilogue, splits, workspace, workspace_bytes,
-                     rl::as_stream(stream), static_cast<unsigned short*>(d_bf16), moments);
+                     rl::as_stream(stream), static_cast<unsigned short*>(d_bf16), moments, a_sums);
     });
 }
 
@@ -439,7 +481,8 @@ RL_API std::size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, i
     const int per = (ktiles + splits - 1) / splits;
     splits = (ktiles + per - 1) / per;
     if (splits <= 1) return 0;
-    return static_cast<std::size_t>(splits) * batch * m * n * sizeof(float);
+    // D partials plus the row-sum partials of A
+    return static_cast<std::size_t>(splits) * batch * (static_cast<std::size_t>(m) * n + m) * sizeof(float);
 }
 
 // Batched transpose of 16-bit matrices (bf16 weight copies laid out K-contiguous

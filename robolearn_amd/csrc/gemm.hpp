@@ -38,6 +38,7 @@ struct Params {
     unsigned short* d_bf16;  // optional bf16 copy of the output (direct mode only)
     float* moments;      // optional per-256-row-chunk (mean, M2) of D: [batch][m / 256][2][n]
     int out_vec;         // 16-byte output stores allowed (n, ldd, strides multiple of 4; aligned outputs)
+    float* a_sums;       // optional sum over this split's K of each row of op(A): [splits][batch][m] (fp32 family)
 };
 
 // Wave-local LDS fence: this wave's LDS operations are complete and the
@@ -70,7 +71,7 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
              const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
              const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
              float beta, int epilogue, int splits, float* workspace, std::size_t workspace_bytes, hipStream_t stream,
-             unsigned short* d_bf16, float* moments);
+             unsigned short* d_bf16, float* moments, float* a_sums);
 
 // Per-256-row-chunk column moments of a row-major [ensemble][rows][channels]
 // fp32 tensor into partial[e][chunk][2][channels] (norm.hip).

@@ -136,7 +136,7 @@ RL_API int rl_plan_run(void* opaque, const void* a, const void* b, const void* c
         rl::run_gemm(plan->mode, bf, bf, a_kcontig, b_kcontig, plan->n, plan->m, plan->k, 1, b, plan->ldb, 0, a,
                      plan->lda, 0, static_cast<const float*>(c), static_cast<float*>(d), plan->ldd, 0,
                      plan->use_bias ? static_cast<const float*>(bias) : nullptr, 0, beta, 0, plan->splits,
-                     static_cast<float*>(workspace), workspace_bytes, rl::as_stream(stream), nullptr, nullptr);
+                     static_cast<float*>(workspace), workspace_bytes, rl::as_stream(stream), nullptr, nullptr, nullptr);
     });
 }
 

@@ -40,15 +40,16 @@ def _is_bf16(tensor: torch.Tensor) -> int:
 def gemm(
     a, b, d, *, m, n, k, batch=1, a_kcontig, b_kcontig, lda, ldb, ldd, stride_a=0, stride_b=0, stride_d=0,
     c=None, beta=0.0, bias=None, stride_bias=0, epilogue=None, mode=FP32, splits=1, workspace=None, d_bf16=None,
-    moments=None,
+    moments=None, a_sums=None,
 ):
-    """Row-major batched D = act(op(A) op(B) + bias) + beta * C (optional bf16 copy of D and
-    per-256-row-chunk column moments of D for a following BatchNorm)."""
+    """Row-major batched D = act(op(A) op(B) + bias) + beta * C (optional bf16 copy of D,
+    per-256-row-chunk column moments of D for a following BatchNorm, and, fp32 mode, the
+    row sums of op(A) over K)."""
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _native.call(
         "rl_gemm", mode, _is_bf16(a), _is_bf16(b), int(a_kcontig), int(b_kcontig), m, n, k, batch, ptr(a), lda,
         stride_a, ptr(b), ldb, stride_b, ptr(c), ptr(d), ldd, stride_d, ptr(bias), stride_bias, float(beta),
-        EPILOGUES[epilogue], splits, ptr(workspace), ws_bytes, ptr(d_bf16), ptr(moments), stream(),
+        EPILOGUES[epilogue], splits, ptr(workspace), ws_bytes, ptr(d_bf16), ptr(moments), ptr(a_sums), stream(),
     )
 
 
@@ -131,9 +132,14 @@ def split_count(m, n, k, batch, mode):
 
 
 def linear_backward_weight(dy, x, dw, *, rows, in_dim, out_dim, ensemble=1, x_stride=None, mode=FP32,
-                           workspace=None, beta=0.0, x_ld=None):
+                           workspace=None, beta=0.0, x_ld=None, bias_grad=None):
     """dw[e] = dy[e]^T x[e] (+ beta dw), split-K over rows when the tile grid is small.
-    x_ld: row pitch of x (default in_dim)."""
+    x_ld: row pitch of x (default in_dim).  bias_grad (fp32 mode): receives sum_rows dy[e]
+    from the same product (overwritten)."""
+    if bias_grad is not None:
+        if mode != FP32:
+            raise ValueError("The fused bias gradient needs the fp32 GEMM family.")
+        _check(bias_grad, ensemble * out_dim, "bias gradient")
     x_ld = x_ld or in_dim
     if x_stride is None:
         x_stride = rows * x_ld
@@ -145,7 +151,8 @@ def linear_backward_weight(dy, x, dw, *, rows, in_dim, out_dim, ensemble=1, x_st
             splits = 1
     gemm(dy, x, dw, m=out_dim, n=in_dim, k=rows, batch=ensemble, a_kcontig=False, b_kcontig=False, lda=out_dim,
          ldb=x_ld, ldd=in_dim, stride_a=rows * out_dim, stride_b=x_stride, stride_d=out_dim * in_dim, mode=mode,
-         splits=splits, workspace=workspace if splits > 1 else None, c=dw if beta else None, beta=beta)
+         splits=splits, workspace=workspace if splits > 1 else None, c=dw if beta else None, beta=beta,
+         a_sums=bias_grad)
 
 
 # ---------------------------------------------------------------------------

@@ -182,10 +182,10 @@ class WarpPPO:
         for i in reversed(range(self.layers)):
             w, _ = self._layer(prefix, i)
             inputs = x if i == 0 else hidden[i - 1]
+            # weight gradient; the bias gradient (row sums of d^T) comes from the same product
             K.linear_backward_weight(d, inputs, g[f"{prefix}.{i}.weight"], rows=rows, in_dim=widths[i],
                                      out_dim=out_dim, mode=K.FP32, workspace=self.workspace,
-                                     x_ld=x_ld if i == 0 else None)
-            K.bias_grad(d, g[f"{prefix}.{i}.bias"], self.partial, rows=rows, channels=out_dim)
+                                     x_ld=x_ld if i == 0 else None, bias_grad=g[f"{prefix}.{i}.bias"])
             if i > 0:
                 # input gradient with the ELU backward of the layer below fused in
                 K.linear_backward_input(d, w, dbufs[i], rows=rows, in_dim=widths[i], out_dim=out_dim, mode=K.FP32,

@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol():
 def test_status_convention_reports_validation_errors():
     with pytest.raises(RuntimeError, match="positive"):
         _native.call("rl_gemm", 0, 0, 0, 1, 1, 0, 4, 4, 1, 1, 4, 0, 1, 4, 0, None, 1, 4, 0, None, 0, 0.0, 0, 1, None,
-                     0, None, None, None)
+                     0, None, None, None, None)
     assert "GEMM" in _native.last_error()
     handle = _native.load().rl_plan_create(0, 4, 4, 0, 0, 4, 4, 4, 0, 0, 0)
     assert not handle and "positive" in _native.last_error()

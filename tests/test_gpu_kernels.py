@@ -353,3 +353,19 @@ def test_fp32_elu_gradient_epilogue(gpu, m, n, k, splits):
            c=y.to(gpu), epilogue="elu_grad", mode=K.FP32, splits=splits, workspace=workspace)
     expected = (a.double() @ b.double()) * torch.where(y > 0, torch.ones_like(y), y + 1).double()
     torch.testing.assert_close(d.cpu().double(), expected, rtol=1e-4, atol=1e-4 * math.sqrt(k))
+
+
+@pytest.mark.parametrize("rows,in_dim,out_dim,use_ws", [(300, 70, 37, False), (24576, 123, 512, True),
+                                                         (24576, 128, 1, True), (5000, 256, 128, True)])
+def test_fp32_weight_gradient_with_fused_bias_gradient(gpu, rows, in_dim, out_dim, use_ws):
+    print(f"case dW+db rows={rows} in={in_dim} out={out_dim} ws={use_ws}", flush=True)
+    g = torch.Generator().manual_seed(rows + in_dim)
+    dy, x = torch.randn(rows, out_dim, generator=g), torch.randn(rows, in_dim, generator=g)
+    dw = torch.empty(out_dim, in_dim, device=gpu)
+    db = torch.full((out_dim,), float("nan"), device=gpu)
+    workspace = torch.empty(256 << 20, dtype=torch.uint8, device=gpu) if use_ws else None
+    K.linear_backward_weight(dy.to(gpu), x.to(gpu), dw, rows=rows, in_dim=in_dim, out_dim=out_dim, mode=K.FP32,
+                             workspace=workspace, bias_grad=db)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(dw.cpu().double(), dy.double().t() @ x.double(), rtol=1e-4, atol=1e-4 * math.sqrt(rows))
+    torch.testing.assert_close(db.cpu().double(), dy.double().sum(0), rtol=1e-4, atol=1e-4 * math.sqrt(rows))
