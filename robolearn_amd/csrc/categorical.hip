@@ -15,7 +15,8 @@
 //   Native    robolearn/cuda/categorical_kernels.cuh:35-176.
 //
 // One wavefront owns one row (K <= 512; kernels are instantiated for 1, 2, 4
-// or 8 bins per lane).  The projection is deterministic and reproduces the
+// or 8 bins per lane); the fused TD target + cross-entropy uses 16-lane row
+// groups instead for K <= 128.  The projection is deterministic and reproduces the
 // reference's per-bin summation order: every lane owns its target bins and adds
 // the source bins that land there in source order, so no atomics are involved.
 #include "common.hpp"
@@ -362,6 +363,308 @@ __global__ __launch_bounds__(kThreads) void td_cross_entropy(TargetArgs a, const
     }
 }
 
+// ---------------------------------------------------------------------------
+// Row-group variant of td_cross_entropy for K <= 128 bins (the FlashSAC heads
+// use 101): 16 lanes, one DPP row, own one table row, so a wavefront works on
+// four rows and every reduction is a four-step DPP butterfly inside the row
+// (no cross-row readlanes).  Lane l holds bins j = l + 16 i, i < PL.  The
+// projection adds, per target bin, the lower-bin masses and then the upper-bin
+// masses in source order, as run pieces over contiguous source blocks (a full
+// scan when a row's bin indices are not monotone); one wavefront per
+// workgroup keeps the per-row LDS small enough for several waves per SIMD.
+// ---------------------------------------------------------------------------
+constexpr int kGroup = 16;
+constexpr int kGroupRows = kWave / kGroup;     // table rows per workgroup (one wavefront)
+constexpr int kGroupBins = 128;                 // widest row of the variant
+
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppMirror>(v);
+    return v;
+}
+
+__device__ __forceinline__ float group_max(float v) {
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppMirror>(v));
+    return v;
+}
+
+template <int PL>
+__device__ __forceinline__ void group_load(const float* row, const float* bias, int bins, int l, float* x) {
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+        const int j = min(l + kGroup * i, bins - 1);
+        x[i] = row[j] + (bias ? bias[j] : 0.0f);
+        if (l + kGroup * i >= bins) x[i] = -INFINITY;
+    }
+}
+
+// log_softmax of a row, its probabilities (one exponential per bin: p = e / s
+// with e = exp(x - max)) and the expectation over the support z.
+template <int PL>
+__device__ __forceinline__ void group_log_softmax(const float* x, const float* z, int bins, int l, float* lp, float* p,
+                                                  float& q) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) m = fmaxf(m, x[i]);
+    m = group_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+        p[i] = l + kGroup * i < bins ? expf(x[i] - m) : 0.0f;
+        s += p[i];
+    }
+    s = group_sum(s);
+    const float lse = logf(s);
+    const float inv = 1.0f / s;
+    float e = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+        lp[i] = x[i] - m - lse;
+        p[i] *= inv;
+        e += p[i] * z[i];
+    }
+    q = group_sum(e);
+}
+
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Per-row LDS of the projection.  probs is read before the first fence and
+// lower_start written after it; the masses serve the non-monotone scan and the
+// run pieces the monotone path, never both in one wave, so each pair shares
+// storage.
+struct GroupRowLds {
+    union {
+        float probs[kGroupBins + 1];   // selected critic's probabilities, by source bin
+        int lower_start[kGroupBins + 1];  // first source whose lower bin is >= k (monotone rows)
+    };
+    int upper_start[kGroupBins + 1];   // first source whose upper bin is >= k
+    int lower[kGroupBins];             // per-source target bins
+    int upper[kGroupBins];
+    union {
+        float lower_mass[kGroupBins];  // per-source masses (non-monotone scan)
+        float lower_piece[kGroupBins]; // lower-bin mass of the run piece starting at this source
+    };
+    union {
+        float upper_mass[kGroupBins];
+        float upper_piece[kGroupBins];
+    };
+};
+
+// Lower/upper target bins and masses of source bin j (updates.py:60-79).
+struct TwoHot {
+    int lower, upper;
+    float lower_mass, upper_mass;
+};
+
+__device__ __forceinline__ TwoHot two_hot(const TargetArgs& a, const RowInputs& in, float z, float p, int bins) {
+    float v = in.reward + (in.discount * (z - in.entropy)) * in.not_done;
+    v = fminf(fmaxf(v, a.min_v), a.max_v);
+    const float b = (v - a.min_v) / a.width;
+    int lower = static_cast<int>(floorf(b));
+    lower = min(max(lower, 0), bins - 1);
+    const float frac = b - static_cast<float>(lower);
+    return TwoHot{lower, min(lower + 1, bins - 1), p * (1.0f - frac), p * frac};
+}
+
+template <int PL>
+__global__ __launch_bounds__(kWave) void td_cross_entropy_rows(TargetArgs a, const float* target_logits,
+                                                                  const float* target_bias, long long target_rows,
+                                                                  const float* online_logits, const float* online_bias,
+                                                                  long long online_rows, long long batch, float scale,
+                                                                  float* target_out, float* dlogits,
+                                                                  unsigned short* dlogits_bf16, float* loss_rows,
+                                                                  float* entropy_rows, float* q_next) {
+    __shared__ GroupRowLds lds[kGroupRows];
+    const int group = static_cast<int>(threadIdx.x) / kGroup;
+    const int l = static_cast<int>(threadIdx.x) % kGroup;
+    const long long row_raw = static_cast<long long>(blockIdx.x) * kGroupRows + group;
+    const bool live = row_raw < batch;
+    const long long row = live ? row_raw : batch - 1;  // rows past the batch compute on a copy and store nothing
+    const int bins = a.bins;
+    GroupRowLds& sh = lds[group];
+
+    float x0[PL], x1[PL], o0[PL], o1[PL], z[PL];
+    group_load<PL>(target_logits + row * bins, target_bias, bins, l, x0);
+    group_load<PL>(target_logits + (target_rows + row) * bins, target_bias ? target_bias + bins : nullptr, bins, l, x1);
+    group_load<PL>(online_logits + row * bins, online_bias, bins, l, o0);
+    group_load<PL>(online_logits + (online_rows + row) * bins, online_bias ? online_bias + bins : nullptr, bins, l, o1);
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+        const int j = l + kGroup * i;
+        z[i] = j < bins ? a.support[min(j, bins - 1)] : 0.0f;
+    }
+    const RowInputs in = load_row_inputs(a, row);
+
+    float lp0[PL], lp1[PL], p0[PL], p1[PL];
+    float q0, q1;
+    group_log_softmax<PL>(x0, z, bins, l, lp0, p0, q0);
+    group_log_softmax<PL>(x1, z, bins, l, lp1, p1, q1);
+    const bool second = q1 < q0;
+
+    // Two-hot projection.  The selected probabilities go to LDS by source bin;
+    // lane l then owns the source block [l c, l c + c), c = ceil(K / 16).  For a
+    // row whose bin indices are non-decreasing in the source (always, unless the
+    // discount is negative), the sources of target bin k are one contiguous run,
+    // so each lane sums its piece of every run in source order and target k adds
+    // the pieces of its run in block order.  That is the reference's per-bin sum
+    // (lower-bin masses, then upper-bin masses) split into at most
+    // ceil(run / c) + 1 ordered pieces, and no lane walks more than its block
+    // plus one piece per block of a long run.
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+        const int j = l + kGroup * i;
+        if (j < bins) sh.probs[j] = second ? p1[i] : p0[i];
+    }
+    wave_lds_fence();
+    const int c = (bins + kGroup - 1) / kGroup;
+    const int jb = min(bins, l * c);
+    const int je = min(bins, jb + c);
+    TwoHot h[PL];
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+        const int j = jb + i;
+        if (j < je) {
+            h[i] = two_hot(a, in, a.support[j], sh.probs[j], bins);
+            sh.lower[j] = h[i].lower;
+            sh.upper[j] = h[i].upper;
+            sh.lower_mass[j] = h[i].lower_mass;
+            sh.upper_mass[j] = h[i].upper_mass;
+        }
+    }
+    wave_lds_fence();
+    // bins of the source before this block, as its owner computed them
+    const int prev_lower = jb > 0 ? sh.lower[jb - 1] : -1;
+    const int prev_upper = jb > 0 ? sh.upper[jb - 1] : -1;
+    bool monotone = true;
+    {
+        int pl = prev_lower, pu = prev_upper;
+#pragma unroll
+        for (int i = 0; i < PL; ++i) {
+            if (jb + i < je) {
+                monotone = monotone && h[i].lower >= pl && h[i].upper >= pu;
+                pl = h[i].lower;
+                pu = h[i].upper;
+            }
+        }
+    }
+    monotone = __all(monotone);  // wave-wide: a non-monotone row sends its wave's rows to the scan
+    float t[PL];
+    if (monotone) {
+        // run starts: source j starts the runs of targets (lower[j - 1], lower[j]]
+        int pl = prev_lower, pu = prev_upper;
+        float piece_lo = 0.0f, piece_hi = 0.0f;
+        int start_lo = jb, start_hi = jb;
+#pragma unroll
+        for (int i = 0; i < PL; ++i) {
+            const int j = jb + i;
+            if (j < je) {
+                for (int k = pl + 1; k <= h[i].lower; ++k) sh.lower_start[k] = j;
+                for (int k = pu + 1; k <= h[i].upper; ++k) sh.upper_start[k] = j;
+                if (j > jb && h[i].lower != pl) {
+                    sh.lower_piece[start_lo] = piece_lo;
+                    piece_lo = 0.0f;
+                    start_lo = j;
+                }
+                if (j > jb && h[i].upper != pu) {
+                    sh.upper_piece[start_hi] = piece_hi;
+                    piece_hi = 0.0f;
+                    start_hi = j;
+                }
+                piece_lo += h[i].lower_mass;
+                piece_hi += h[i].upper_mass;
+                pl = h[i].lower;
+                pu = h[i].upper;
+            }
+        }
+        if (jb < je) {
+            sh.lower_piece[start_lo] = piece_lo;
+            sh.upper_piece[start_hi] = piece_hi;
+        }
+        if (je == bins && jb < je) {  // the last block closes every later target's (empty) run
+            for (int k = pl + 1; k <= bins; ++k) sh.lower_start[k] = bins;
+            for (int k = pu + 1; k <= bins; ++k) sh.upper_start[k] = bins;
+        }
+        wave_lds_fence();
+#pragma unroll
+        for (int i = 0; i < PL; ++i) {
+            const int k = l + kGroup * i;
+            float sum = 0.0f;
+            if (k < bins) {
+                for (int pass = 0; pass < 2; ++pass) {
+                    const int* starts = pass == 0 ? sh.lower_start : sh.upper_start;
+                    const float* pieces = pass == 0 ? sh.lower_piece : sh.upper_piece;
+                    const int r0 = max(starts[k], 0), r1 = min(starts[k + 1], bins);
+                    if (r0 < r1) {
+                        sum += pieces[r0];
+                        for (int j = (r0 / c + 1) * c; j < r1; j += c) sum += pieces[j];
+                    }
+                }
+            }
+            t[i] = sum;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < PL; ++i) {
+            const int k = l + kGroup * i;
+            float sum = 0.0f;
+            if (k < bins) {
+                for (int j = 0; j < bins; ++j)
+                    if (sh.lower[j] == k) sum += sh.lower_mass[j];
+                for (int j = 0; j < bins; ++j)
+                    if (sh.upper[j] == k) sum += sh.upper_mass[j];
+            }
+            t[i] = sum;
+        }
+    }
+    float tsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) tsum += t[i];
+    tsum = group_sum(tsum);
+    if (live && target_out) {
+#pragma unroll
+        for (int i = 0; i < PL; ++i) {
+            const int j = l + kGroup * i;
+            if (j < bins) target_out[row * bins + j] = t[i];
+        }
+    }
+#pragma unroll
+    for (int member = 0; member < 2; ++member) {
+        const long long orow = member * online_rows + row;
+        float lp[PL], pm[PL];
+        float q;
+        group_log_softmax<PL>(member == 0 ? o0 : o1, z, bins, l, lp, pm, q);
+        float ce = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PL; ++i) {
+            const int j = l + kGroup * i;
+            if (j < bins) {
+                ce -= t[i] * lp[i];
+                const float g = scale * (pm[i] * tsum - t[i]);
+                if (live && dlogits) dlogits[orow * bins + j] = g;
+                if (live && dlogits_bf16) dlogits_bf16[orow * bins + j] = f32_to_bf16_bits(g);
+            }
+        }
+        ce = group_sum(ce);
+        if (live && l == 0) loss_rows[member * batch + row] = ce;
+    }
+    if (live && l == 0) {
+        entropy_rows[row] = in.entropy;
+        if (q_next) {
+            q_next[row] = q0;
+            q_next[batch + row] = q1;
+        }
+    }
+}
+
 // Reference-compatible target kernel (categorical_kernels.cuh:87-114): q is
 // [2, 2B], log_probs [2, 2B, K]; the next-observation half is used.  The
 // maximum entropy bonus is an order-independent atomic float maximum, so the
@@ -526,12 +829,25 @@ RL_API int rl_categorical_td_cross_entropy(const float* target_logits, const flo
         rl::require(target_rows >= batch && online_rows >= batch, "Member row strides must cover the batch.");
         rl::cat::TargetArgs a{support, reward, terminated, discount, next_log_probs, alpha, min_v, max_v,
                               static_cast<float>((static_cast<double>(max_v) - min_v) / (bins - 1)), bins};
-        rl::cat::dispatch_bins<rl::cat::TdCrossEntropy>(bins, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
-                                                        rl::as_stream(stream), a, target_logits, target_bias,
-                                                        target_rows, online_logits, online_bias, online_rows, batch,
-                                                        scale, target_out, dlogits,
-                                                        static_cast<unsigned short*>(dlogits_bf16), loss_rows,
-                                                        entropy_rows, q_next);
+        unsigned short* dh = static_cast<unsigned short*>(dlogits_bf16);
+        if (bins <= rl::cat::kGroupBins) {
+            const dim3 grid(rl::ceil_div(batch, rl::cat::kGroupRows));
+            const hipStream_t st = rl::as_stream(stream);
+#define RL_TD_ROWS(PL)                                                                                                \
+    hipLaunchKernelGGL(rl::cat::td_cross_entropy_rows<PL>, grid, dim3(rl::kWave), 0, st, a, target_logits,             \
+                       target_bias, target_rows, online_logits, online_bias, online_rows, batch, scale, target_out,    \
+                       dlogits, dh, loss_rows, entropy_rows, q_next)
+            if (bins <= 2 * rl::cat::kGroup) RL_TD_ROWS(2);
+            else if (bins <= 4 * rl::cat::kGroup) RL_TD_ROWS(4);
+            else RL_TD_ROWS(8);
+#undef RL_TD_ROWS
+        } else {
+            rl::cat::dispatch_bins<rl::cat::TdCrossEntropy>(bins, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
+                                                            rl::as_stream(stream), a, target_logits, target_bias,
+                                                            target_rows, online_logits, online_bias, online_rows,
+                                                            batch, scale, target_out, dlogits, dh, loss_rows,
+                                                            entropy_rows, q_next);
+        }
         rl::check_launch("Launch TD cross-entropy");
     });
 }
