@@ -16,7 +16,9 @@ Prints ONE JSON line: value = FlashSAC updates/sec on the GPU, with
   ppo           PPO update ms at configs[3] (one captured graph per update, fp32
                 MFMA roofline, CPU oracle on one epoch scaled to five),
   kernel_sweep  configs[4]: fused categorical target + CE, fused optimizer and
-                RMSNorm at their sweep shapes against the HBM roofline.
+                RMSNorm at their sweep shapes against the HBM roofline, plus the
+                replay ingest (n-step commit) and return statistics of one
+                vector step at the G1 collection shape.
 """
 
 import argparse
@@ -372,6 +374,45 @@ def kernel_sweep() -> list:
     lines.append(_hbm_line("rms_backward (rms_backward_fused + column_reduce)", ms,
                            3 * rows * channels * 4 + rows * 4,
                            "65536 x 1024: read x, dy (and ms), write dx; weight gradient reduced in fixed order"))
+    del x, dy, y, dx, partial
+
+    # (d) replay ingest of one vector step at the G1 collection shape: 4096 environments,
+    # obs 123, action 37, n_step 3, into a 1,048,576-row ring; then the return statistics
+    from robolearn_amd import _native
+
+    envs, obs_dim, act_dim, n_step, capacity = 4096, 123, 37, 3, 1 << 20
+    step_in = [torch.randn(envs, obs_dim, generator=g, device=device),
+               torch.rand(envs, act_dim, generator=g, device=device) * 2 - 1,
+               torch.randn(envs, generator=g, device=device),
+               (torch.rand(envs, generator=g, device=device) < 0.005).float(),
+               torch.zeros(envs, device=device),
+               torch.randn(envs, obs_dim, generator=g, device=device)]
+    pending = [torch.zeros(n_step, envs, obs_dim, device=device), torch.zeros(n_step, envs, act_dim, device=device),
+               torch.zeros(n_step, envs, obs_dim, device=device), torch.zeros(n_step, envs, 3, device=device)]
+    store = [torch.zeros(capacity, obs_dim, device=device), torch.zeros(capacity, act_dim, device=device),
+             *[torch.zeros(capacity, device=device) for _ in range(3)],
+             torch.zeros(capacity, obs_dim, device=device), torch.zeros(capacity, device=device)]
+    counters = torch.zeros(3, dtype=torch.long, device=device)
+
+    def ingest():
+        _native.call("rl_replay_ingest", envs, obs_dim, act_dim, n_step, capacity, 0.99,
+                     *[t.data_ptr() for t in step_in], *[t.data_ptr() for t in pending],
+                     *[t.data_ptr() for t in store], counters.data_ptr(), K.stream())
+
+    row = 2 * obs_dim + act_dim
+    ingest_bytes = envs * 4 * ((row + 3) * 2 + (row + 3 * (n_step - 1)) + (row + 4))
+    ms = _time_launches(ingest)
+    lines.append(_hbm_line("replay_ingest (ingest_kernel + advance_kernel)", ms, ingest_bytes,
+                           "4096 envs, obs 123, act 37, n_step 3: stage the step, commit the oldest n-step return; "
+                           "two launches, latency-bound at this size"))
+    returns, maximum = torch.zeros(envs, device=device), torch.zeros(1, device=device)
+    running = torch.tensor([0.0, 1.0, 0.0], device=device)
+    ms = _time_launches(lambda: _native.call("rl_reward_stats_update", envs, 0.99, step_in[2].data_ptr(),
+                                             step_in[3].data_ptr(), step_in[4].data_ptr(), returns.data_ptr(),
+                                             maximum.data_ptr(), running.data_ptr(), K.stream()))
+    lines.append(_hbm_line("reward_stats_update", ms, envs * 4 * 5,
+                           "4096 envs: per-environment returns, running max and RunningMeanStd merge; "
+                           "one workgroup, latency-bound"))
     return lines
 
 

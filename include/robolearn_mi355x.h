@@ -269,6 +269,31 @@ int rl_advance_counters(long long* counters, int actor, void* stream);
 /* robolearn/flashsac/_utils/reward_normalization.py:28-38 */
 int rl_scale_rewards(float* rewards, long long n, const float* var, const float* r_max, float g_max, float eps,
                      void* stream);
+/* Replay ingest of one vector step (replaces TorchUniformBuffer.add,
+ * robolearn/flashsac/replay.py:107-174, and the Warp staging kernels
+ * _copy_pending/_commit_pending/_advance_replay, robolearn/warp/_flash_replay.py:26-113).
+ * Inputs are [E] / [E, O] / [E, A] fp32 rows, done flags as 0/1 floats.  The
+ * staging ring is pending_observation / pending_next_observation [n, E, O],
+ * pending_action [n, E, A] and pending_scalars [n, E, 3] (reward, terminated,
+ * truncated).  Once n - 1 earlier steps are staged, the oldest is committed at
+ * ring row (counters[1] + e) % capacity with its n-step reward, discount,
+ * terminal flags and bootstrap observation; counters = int64 [additions,
+ * position, count] on the device.  Two launches, no allocation, no host read:
+ * capturable. */
+int rl_replay_ingest(long long num_envs, int obs_dim, int action_dim, int n_step, long long capacity, float gamma,
+                     const float* observation, const float* action, const float* reward, const float* terminated,
+                     const float* truncated, const float* next_observation, float* pending_observation,
+                     float* pending_action, float* pending_next_observation, float* pending_scalars,
+                     float* observation_store, float* action_store, float* reward_store, float* terminated_store,
+                     float* truncated_store, float* next_observation_store, float* discount_store,
+                     long long* counters, void* stream);
+/* Return statistics for reward normalization (replaces
+ * RewardNormalizer.update_reward_stats, robolearn/flashsac/_utils/reward_normalization.py:14-25, 108-122,
+ * with RunningMeanStd.update :42-66, 187-197; Warp _update_returns/_return_variance/
+ * _update_running_moments, robolearn/warp/_flash_replay.py:347-390).  returns [E],
+ * maximum [1], running = [mean, var, count]; one workgroup, fixed-order sums. */
+int rl_reward_stats_update(long long num_envs, float gamma, const float* reward, const float* terminated,
+                           const float* truncated, float* returns, float* maximum, float* running, void* stream);
 
 /* ---- PPO ------------------------------------------------------------------ */
 /* robolearn/warp/ppo.py:101-133 */

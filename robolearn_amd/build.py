@@ -14,7 +14,7 @@ PACKAGE = Path(__file__).resolve().parent
 SOURCE_DIR = PACKAGE / "csrc"
 BUILD_DIR = PACKAGE / "_build"
 LIBRARY = PACKAGE / "librl_mi355x.so"
-SOURCES = ("plan.hip", "gemm.hip", "gemm_bf16.hip", "gemm_bf16_big.hip", "optimizer.hip", "norm.hip", "categorical.hip", "policy.hip", "ppo.hip")
+SOURCES = ("plan.hip", "gemm.hip", "gemm_bf16.hip", "gemm_bf16_big.hip", "optimizer.hip", "norm.hip", "categorical.hip", "policy.hip", "ppo.hip", "replay.hip")
 ARCH = os.environ.get("ROBOLEARN_AMD_ARCH", "gfx950")
 
 FLAGS = [

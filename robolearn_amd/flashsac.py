@@ -247,11 +247,16 @@ class FlashSAC:
             # replay storage (device ring) and reward normalizer state
             self.capacity = cfg.buffer_max_length
             self.replay = None
-            self.num_in_buffer = torch.zeros(1, dtype=torch.long, device=dev)
+            self.replay_counters = torch.zeros(3, dtype=torch.long, device=dev)  # additions, position, count
+            self.pending = None
+            self._host_additions = 0
             self._num_in_buffer_host = 0
             self._replay_position = 0
-            self.reward_var = torch.ones(1, device=dev)
+            # return statistics (reward_normalization.py:75-105): G_r per environment,
+            # running max |G_r| and RunningMeanStd [mean, var, count]
+            self.reward_returns = torch.zeros(num_envs, device=dev)
             self.reward_max = torch.zeros(1, device=dev)
+            self.reward_running = torch.tensor([0.0, 1.0, 0.0], device=dev)
             self.gather_error = torch.zeros(1, dtype=torch.int32, device=dev)
         self.metrics = {key: self.metrics_buffer[i: i + 1] for i, key in enumerate(METRIC_KEYS)}
 
@@ -318,8 +323,8 @@ class FlashSAC:
             arrays[f"optimizer.{label}.lr"] = optimizer.lr
         arrays["log_temperature"] = self.log_temperature
         arrays["update_counters"] = self.update_counters
-        arrays["normalizer.var"] = self.reward_var
-        arrays["normalizer.max"] = self.reward_max
+        arrays["normalizer.maximum"] = self.reward_max
+        arrays["normalizer.running"] = self.reward_running
         return arrays
 
     def state_dict(self, include_replay: bool = True) -> dict:
@@ -328,10 +333,14 @@ class FlashSAC:
         state = {key: value.detach().cpu().numpy().copy() for key, value in self._state_arrays().items()}
         state["replay.num_in_buffer"] = np.array([self._num_in_buffer_host], dtype=np.int64)
         state["replay.position"] = np.array([self._replay_position], dtype=np.int64)
+        state["replay.counters"] = self.replay_counters.cpu().numpy().copy()
+        state["normalizer.returns"] = self.reward_returns.cpu().numpy().copy()
         if include_replay and self.replay is not None:
             n = self._num_in_buffer_host
             for key, value in self.replay.items():
                 state[f"replay.{key}"] = value[:n].cpu().numpy()
+            for key, value in self.pending.items():
+                state[f"replay.pending.{key}"] = value.cpu().numpy()
         state["replay_storage_included"] = np.array([include_replay and self.replay is not None], dtype=np.bool_)
         return state
 
@@ -344,12 +353,27 @@ class FlashSAC:
                 raise ValueError(f"Checkpoint array {key} is missing or has the wrong shape.")
         for key, array in arrays.items():
             array.copy_(torch.as_tensor(np.asarray(state[key])).to(array.dtype))
+        returns = state.get("normalizer.returns")
+        if returns is not None and tuple(np.asarray(returns).shape) == tuple(self.reward_returns.shape):
+            self.reward_returns.copy_(torch.as_tensor(np.asarray(returns)))
+        else:
+            self.reward_returns.zero_()
         self.actor.refresh_shadows()
         self.critic.refresh_shadows()
         if bool(np.asarray(state.get("replay_storage_included", [False]))[0]):
             n = int(np.asarray(state["replay.num_in_buffer"])[0])
             self.load_replay({key: state[f"replay.{key}"] for key in BATCH_KEYS}, count=n,
                              position=int(np.asarray(state["replay.position"])[0]))
+            staged = [f"replay.pending.{key}" for key in self.pending]
+            if all(key in state for key in staged):
+                shapes_match = all(tuple(np.asarray(state[f"replay.pending.{key}"]).shape) == tuple(value.shape)
+                                   for key, value in self.pending.items())
+                if shapes_match:  # same environment count: continue the n-step staging exactly
+                    for key, value in self.pending.items():
+                        value.copy_(torch.as_tensor(np.asarray(state[f"replay.pending.{key}"])))
+                    additions = int(np.asarray(state["replay.counters"])[0])
+                    self.replay_counters[0] = additions
+                    self._host_additions = additions
         self._update_step = int(np.asarray(state["update_counters"])[0])
 
     def save(self, path, *, include_replay: bool = False) -> None:
@@ -379,11 +403,20 @@ class FlashSAC:
             raise ValueError("Checkpoint observation/action dimensions differ from this agent.")
         with np.load(directory / "agent.npz", allow_pickle=False) as archive:
             state = dict(archive)
-        if not self.cfg.load_optimizer:
+        current = None
+        if not self.cfg.load_optimizer or not self.cfg.load_reward_normalizer:
             current = self.state_dict(include_replay=False)
+        if not self.cfg.load_optimizer:
             for key in current:
                 if key.startswith("optimizer.") or key == "update_counters":
                     state[key] = current[key]
+        if not self.cfg.load_reward_normalizer:
+            for key in current:
+                if key.startswith("normalizer."):
+                    state[key] = current[key]
+        elif self.cfg.normalize_reward:
+            # a loaded normalizer restarts its per-environment returns (agent.py:570-572)
+            state.pop("normalizer.returns", None)
         self.load_state_dict(state)
 
     # ------------------------------------------------------------------
@@ -392,14 +425,23 @@ class FlashSAC:
     def _ensure_replay(self):
         if self.replay is None:
             c, dev = self.capacity, self.device
+            o, a = self.critic_observation_dim, self.action_dim
             self.replay = {
-                "observation": torch.zeros(c, self.critic_observation_dim, device=dev),
-                "action": torch.zeros(c, self.action_dim, device=dev),
+                "observation": torch.zeros(c, o, device=dev),
+                "action": torch.zeros(c, a, device=dev),
                 "reward": torch.zeros(c, device=dev),
                 "terminated": torch.zeros(c, device=dev),
                 "truncated": torch.zeros(c, device=dev),
-                "next_observation": torch.zeros(c, self.critic_observation_dim, device=dev),
+                "next_observation": torch.zeros(c, o, device=dev),
                 "discount": torch.zeros(c, device=dev),
+            }
+            # n-step staging ring (robolearn/warp/_flash_replay.py:200-209): slot = additions % n_step
+            n, e = self.cfg.n_step, self.num_envs
+            self.pending = {
+                "observation": torch.zeros(n, e, o, device=dev),
+                "action": torch.zeros(n, e, a, device=dev),
+                "next_observation": torch.zeros(n, e, o, device=dev),
+                "scalars": torch.zeros(n, e, 3, device=dev),  # reward, terminated, truncated
             }
 
     @torch.no_grad()
@@ -416,25 +458,50 @@ class FlashSAC:
                 self.replay[key][:n].shape))
         self._num_in_buffer_host = n
         self._replay_position = (position if position is not None else n) % self.capacity
-        self.num_in_buffer.fill_(n)
+        # the n-step staging restarts empty, as after TorchUniformBuffer.load (replay.py:238-240)
+        self._host_additions = 0
+        self.replay_counters.copy_(torch.tensor([0, self._replay_position, n], dtype=torch.long))
 
     @torch.no_grad()
     def observe(self, observations, actions, rewards, terminated, truncated, next_observations) -> None:
-        """Store one vector step of pre-reset transitions (one-step returns, discount gamma)."""
-        if self.cfg.n_step != 1:
-            raise NotImplementedError("n-step replay commits are not part of this learner build; use n_step=1.")
+        """Store one vector step of pre-reset transitions (agent.py:587-598 -> process_transition :457-468).
+
+        The step is staged on the device and, once n_step steps are staged, the
+        oldest is committed with its n-step return (replay.py:107-174); with
+        reward normalization the return statistics advance too
+        (reward_normalization.py:108-122).  Both run as HIP kernels on the
+        current stream; no host read."""
         self._ensure_replay()
-        n = observations.shape[0]
-        idx = (torch.arange(n, device=self.device) + self._replay_position) % self.capacity
-        for key, value in (("observation", observations), ("action", actions), ("reward", rewards),
-                           ("terminated", terminated), ("truncated", truncated),
-                           ("next_observation", next_observations)):
-            self.replay[key][idx] = torch.as_tensor(value, device=self.device).to(torch.float32).reshape(
-                self.replay[key][idx].shape)
-        self.replay["discount"][idx] = self.cfg.gamma
-        self._replay_position = (self._replay_position + n) % self.capacity
-        self._num_in_buffer_host = min(self._num_in_buffer_host + n, self.capacity)
-        self.num_in_buffer.fill_(self._num_in_buffer_host)
+        e, o, a = self.num_envs, self.critic_observation_dim, self.action_dim
+        fields = []
+        for value, shape in ((observations, (e, o)), (actions, (e, a)), (rewards, (e,)), (terminated, (e,)),
+                             (truncated, (e,)), (next_observations, (e, o))):
+            tensor = torch.as_tensor(value, device=self.device)
+            if tensor.numel() != math.prod(shape):
+                raise ValueError(f"observe() expects {e} environments with fields shaped {shape}.")
+            fields.append(tensor.to(torch.float32).reshape(shape).contiguous())
+        obs, act, rew, term, trunc, next_obs = fields
+        r, p = self.replay, self.pending
+        _native.call("rl_replay_ingest", e, o, a, self.cfg.n_step, self.capacity, float(self.cfg.gamma),
+                     obs.data_ptr(), act.data_ptr(), rew.data_ptr(), term.data_ptr(), trunc.data_ptr(),
+                     next_obs.data_ptr(), p["observation"].data_ptr(), p["action"].data_ptr(),
+                     p["next_observation"].data_ptr(), p["scalars"].data_ptr(), r["observation"].data_ptr(),
+                     r["action"].data_ptr(), r["reward"].data_ptr(), r["terminated"].data_ptr(),
+                     r["truncated"].data_ptr(), r["next_observation"].data_ptr(), r["discount"].data_ptr(),
+                     self.replay_counters.data_ptr(), K.stream())
+        if self.cfg.normalize_reward:
+            _native.call("rl_reward_stats_update", e, float(self.cfg.gamma), rew.data_ptr(), term.data_ptr(),
+                         trunc.data_ptr(), self.reward_returns.data_ptr(), self.reward_max.data_ptr(),
+                         self.reward_running.data_ptr(), K.stream())
+        if self._host_additions >= self.cfg.n_step - 1:
+            self._replay_position = (self._replay_position + e) % self.capacity
+            self._num_in_buffer_host = min(self._num_in_buffer_host + e, self.capacity)
+        self._host_additions += 1
+
+    def process_transition(self, transition: dict) -> None:
+        """Reference-named entry (agent.py:457-468): a transition dict with the observe() fields."""
+        self.observe(transition["observation"], transition["action"], transition["reward"],
+                     transition["terminated"], transition["truncated"], transition["next_observation"])
 
     @property
     def ready(self) -> bool:
@@ -480,7 +547,7 @@ class FlashSAC:
 
     def _sample(self):
         B = self.batch_size
-        K.sample_indices(self.indices, seed=self.cfg.seed * 7919 + 1, count=self.num_in_buffer,
+        K.sample_indices(self.indices, seed=self.cfg.seed * 7919 + 1, count=self.replay_counters[2:3],
                          counter=self.update_counters, stream_id=1)
         b, r = self.batch, self.replay
         _native.call("rl_replay_gather", self.indices.data_ptr(), B, self.capacity, self.critic_observation_dim,
@@ -618,7 +685,7 @@ class FlashSAC:
         self._pack_inputs()
         if normalize_reward and self.cfg.normalize_reward:
             self.reward_used.copy_(self.batch["reward"])
-            _native.call("rl_scale_rewards", self.reward_used.data_ptr(), B, self.reward_var.data_ptr(),
+            _native.call("rl_scale_rewards", self.reward_used.data_ptr(), B, self.reward_running[1:2].data_ptr(),
                          self.reward_max.data_ptr(), float(self.cfg.normalized_G_max), 1e-8, K.stream())
         else:
             self.reward_used.copy_(self.batch["reward"])

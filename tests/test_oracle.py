@@ -400,3 +400,90 @@ def test_unscale_reference_only_cases():
     assert OO.unscale([np.array([1.0], np.float32)], 0.0) == 1
     assert OO.unscale([np.array([1.0], np.float32)], -2.0) == 1
     assert OO.unscale([np.array([1.0, 2.0], np.float32)], 4.0) == 0
+
+
+# ---------------------------------------------------------------------------
+# replay ingest (n-step commit) and reward statistics
+# ---------------------------------------------------------------------------
+from oracle import replay as OR  # noqa: E402
+
+
+def test_n_step_replay_known_answer():
+    """The reference's known answer, tests/test_flashsac.py:197-231."""
+    replay = OR.NStepReplay(1, 1, n_step=3, gamma=0.5, capacity=16)
+    for step, rewards in enumerate(([1.0, 1.0, 1.0], [2.0, 2.0, 2.0], [100.0, 4.0, 100.0])):
+        replay.add([[step * 10.0], [step * 10.0 + 1], [step * 10.0 + 2]], np.zeros((3, 1)), rewards,
+                   [False, False, step == 1], [step == 1, False, False],
+                   [[(step + 1) * 10.0], [(step + 1) * 10.0 + 1], [(step + 1) * 10.0 + 2]])
+    batch = replay.sample([0, 1, 2])
+    np.testing.assert_array_equal(batch["reward"], [2.0, 3.0, 2.0])
+    np.testing.assert_array_equal(batch["next_observation"], [[20.0], [31.0], [22.0]])
+    np.testing.assert_array_equal(batch["discount"], [0.25, 0.125, 0.25])
+    np.testing.assert_array_equal(batch["terminated"], [0.0, 0.0, 1.0])
+    np.testing.assert_array_equal(batch["truncated"], [1.0, 0.0, 0.0])
+    target = batch["reward"] + batch["discount"] * (1.0 - batch["terminated"]) * batch["next_observation"][:, 0]
+    np.testing.assert_allclose(target, [7.0, 6.875, 2.0])
+    assert replay.count == 3 and replay.position == 3
+
+
+def _random_step(rng, envs, obs_dim, action_dim, done_prob):
+    return dict(observation=rng.standard_normal((envs, obs_dim)).astype(np.float32),
+                action=rng.uniform(-1, 1, (envs, action_dim)).astype(np.float32),
+                reward=rng.standard_normal(envs).astype(np.float32),
+                terminated=(rng.random(envs) < done_prob).astype(np.float32),
+                truncated=(rng.random(envs) < done_prob).astype(np.float32),
+                next_observation=rng.standard_normal((envs, obs_dim)).astype(np.float32))
+
+
+@pytest.mark.parametrize("n_step", [1, 2, 3, 5])
+def test_n_step_replay_matches_brute_force(n_step):
+    rng = np.random.default_rng(n_step)
+    envs, obs_dim, action_dim, capacity, gamma = 7, 3, 2, 40, 0.9
+    replay = OR.NStepReplay(obs_dim, action_dim, n_step, gamma, capacity)
+    history = []
+    for step in range(15):
+        t = _random_step(rng, envs, obs_dim, action_dim, done_prob=0.3)
+        history.append(t)
+        position = replay.position
+        replay.add(**t)
+        if step < n_step - 1:
+            assert replay.count == 0
+            continue
+        rows = (np.arange(envs) + position) % capacity
+        expected = OR.brute_force_commit(history, n_step, gamma)
+        got = replay.sample(rows)
+        np.testing.assert_allclose(got["reward"], expected["reward"], rtol=1e-6, atol=1e-6)
+        np.testing.assert_allclose(got["discount"], expected["discount"], rtol=1e-6)
+        np.testing.assert_array_equal(got["terminated"], expected["terminated"])
+        np.testing.assert_array_equal(got["truncated"], expected["truncated"])
+        np.testing.assert_array_equal(got["next_observation"], np.stack(expected["next_observation"]))
+        np.testing.assert_array_equal(got["observation"], history[-n_step]["observation"])
+        np.testing.assert_array_equal(got["action"], history[-n_step]["action"])
+    assert replay.count == min(capacity, envs * (15 - n_step + 1))
+
+
+def test_reward_stats_closed_forms():
+    rng = np.random.default_rng(3)
+    envs, gamma, steps = 9, 0.97, 12
+    stats = OR.RewardStats(envs, gamma)
+    returns = np.zeros(envs)
+    seen, previous_vars = [], []
+    for _ in range(steps):
+        reward = rng.standard_normal(envs).astype(np.float32)
+        term = (rng.random(envs) < 0.2).astype(np.float32)
+        trunc = (rng.random(envs) < 0.1).astype(np.float32)
+        previous_vars.append(float(stats.running[1]))
+        stats.update(reward, term, trunc)
+        done = (term != 0) | (trunc != 0)
+        returns = np.where(done, 0.0, gamma * returns) + reward
+        seen.append(returns.copy())
+        np.testing.assert_allclose(stats.returns, returns, rtol=1e-5, atol=1e-6)
+        values = np.concatenate(seen)
+        assert stats.maximum[0] == pytest.approx(np.abs(values).max(), rel=1e-6)
+        assert stats.running[2] == len(values)
+        assert stats.running[0] == pytest.approx(values.mean(), rel=1e-5, abs=1e-6)
+        total_squares = ((values - values.mean()) ** 2).sum() + 1e-4 * sum(previous_vars)
+        assert stats.running[1] * len(values) == pytest.approx(total_squares, rel=1e-5)
+    scaled = stats.scale(np.array([1.0, -2.0], np.float32), g_max=5.0)
+    denominator = max(math.sqrt(stats.running[1] + 1e-8), stats.maximum[0] / 5.0)
+    np.testing.assert_allclose(scaled, np.array([1.0, -2.0]) / denominator, rtol=1e-6)
