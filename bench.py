@@ -17,8 +17,9 @@ Prints ONE JSON line: value = FlashSAC updates/sec on the GPU, with
                 MFMA roofline, CPU oracle on one epoch scaled to five),
   kernel_sweep  configs[4]: fused categorical target + CE, fused optimizer and
                 RMSNorm at their sweep shapes against the HBM roofline, plus the
-                replay ingest (n-step commit) and return statistics of one
-                vector step at the G1 collection shape.
+                replay ingest (n-step commit), return statistics and act()
+                (fp32 actor + exploration repeat) of one vector step at the G1
+                collection shape.
 """
 
 import argparse
@@ -413,6 +414,25 @@ def kernel_sweep() -> list:
     lines.append(_hbm_line("reward_stats_update", ms, envs * 4 * 5,
                            "4096 envs: per-environment returns, running max and RunningMeanStd merge; "
                            "one workgroup, latency-bound"))
+    del store, pending
+
+    # (e) act(training=True) at the G1 collection shape: fp32 eval-mode actor (256 x 2 blocks) over
+    # 4096 environments plus the exploration-noise repeat; the critics are irrelevant here and kept small
+    from robolearn_amd.flashsac import FlashSAC
+
+    act_cfg = FlashSACConfig(actor_hidden_dim=256, actor_num_blocks=2, critic_hidden_dim=32, critic_num_blocks=1,
+                             sample_batch_size=256, buffer_max_length=1024, buffer_min_length=256)
+    actor_agent = FlashSAC(obs_dim, act_dim, num_envs=envs, cfg=act_cfg)
+    observations = torch.randn(envs, obs_dim, generator=g, device=device)
+    ms = _time_launches(lambda: actor_agent.act(observations, training=True))
+    h = act_cfg.actor_hidden_dim
+    flops = 2 * envs * (obs_dim * h + act_cfg.actor_num_blocks * 2 * h * 4 * h + h * 2 * act_dim)
+    achieved = flops / (ms * 1e-3) / 1e12
+    lines.append({"kernel": "act (fp32 actor forward + exploration repeat)", "ms": round(ms, 4),
+                  "flops": int(flops), "bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS,
+                  "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
+                  "detail": "4096 envs, obs 123, act 37, actor 256 x 2 blocks, fp32 (the reference acts in fp32); "
+                            "small products, launch-bound"})
     return lines
 
 

@@ -269,6 +269,16 @@ int rl_advance_counters(long long* counters, int actor, void* stream);
 /* robolearn/flashsac/_utils/reward_normalization.py:28-38 */
 int rl_scale_rewards(float* rewards, long long n, const float* var, const float* r_max, float g_max, float eps,
                      void* stream);
+/* Exploration-noise repeats for act(training) (replaces the repeat logic of
+ * _sample_flashsac_actions, robolearn/flashsac/agent.py:159-214, and the Warp kernels
+ * _exploration_repeat/_exploration_actions, robolearn/warp/flashsac.py:269-299).
+ * state = int32 [count, length, refresh] (start [0, 1, 0]); cdf = truncated zeta
+ * CDF [max_n]; cached_noise [count] keeps its values until a new repeat length
+ * is drawn.  uniform (one value) and fresh_noise ([count]) are optional injected
+ * draws; NULL uses Philox keyed by seed and the device draw counter `step`. */
+int rl_exploration_noise(unsigned long long seed, long long* step, const float* cdf, int max_n, int* state,
+                         float* cached_noise, long long count, const float* uniform, const float* fresh_noise,
+                         void* stream);
 /* Replay ingest of one vector step (replaces TorchUniformBuffer.add,
  * robolearn/flashsac/replay.py:107-174, and the Warp staging kernels
  * _copy_pending/_commit_pending/_advance_replay, robolearn/warp/_flash_replay.py:26-113).

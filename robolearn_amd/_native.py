@@ -106,6 +106,7 @@ SIGNATURES = {
     "rl_add": (c_int, [P, P, c_ll, P]),
     "rl_advance_counters": (c_int, [P, c_int, P]),
     "rl_scale_rewards": (c_int, [P, c_ll, P, P, c_float, c_float, P]),
+    "rl_exploration_noise": (c_int, [c_ull, P, P, c_int, P, P, c_ll, P, P, P]),
     "rl_replay_ingest": (c_int, [c_ll, c_int, c_int, c_int, c_ll, c_float] + [P] * 6 + [P] * 4 + [P] * 7
                          + [P, P]),
     "rl_reward_stats_update": (c_int, [c_ll, c_float, P, P, P, P, P, P, P]),

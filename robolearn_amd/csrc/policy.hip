@@ -357,6 +357,72 @@ __global__ void advance_counters(long long* counters, int actor) {
     counters[2] += actor;
 }
 
+// Exploration-noise repeats (robolearn/flashsac/agent.py:159-214, Warp
+// _exploration_repeat/_exploration_actions, robolearn/warp/flashsac.py:269-299).
+// state = int32 [count, length, refresh].  A call whose count is 0 or has
+// reached length draws a new repeat length n ~ truncated zeta (the first k with
+// u < cdf[k], plus one; when no entry exceeds u the length is 1, which is what
+// torch.argmax returns for an all-false mask) and asks for fresh noise; count
+// then advances.  The draw counter `step` is advanced here; exploration_noise
+// uses the value this kernel read.
+constexpr unsigned int kRepeatStream = 41;
+constexpr unsigned int kExplorationStream = 37;
+
+__global__ void exploration_repeat(unsigned long long seed, long long* step, const float* cdf, int max_n, int* state,
+                                   const float* uniform) {
+    if (blockIdx.x != 0 || threadIdx.x != 0) return;
+    const unsigned long long draw = static_cast<unsigned long long>(step[0]);
+    float u;
+    if (uniform) {
+        u = uniform[0];
+    } else {
+        const uint4 c = make_uint4(0u, static_cast<unsigned int>(draw), static_cast<unsigned int>(draw >> 32),
+                                   kRepeatStream);
+        u = uniform01(philox4x32_10(c, make_uint2(static_cast<unsigned int>(seed),
+                                                  static_cast<unsigned int>(seed >> 32))).x);
+    }
+    int length = 1;
+    for (int k = 0; k < max_n; ++k) {
+        if (u < cdf[k]) {
+            length = k + 1;
+            break;
+        }
+    }
+    const int count = state[0];
+    const bool reset = count == 0 || count >= state[1];
+    if (reset) state[1] = length;
+    state[0] = (reset ? 0 : count) + 1;
+    state[2] = reset ? 1 : 0;
+    step[0] = static_cast<long long>(draw + 1);
+}
+
+// cached[i] <- a fresh N(0, 1) draw (or fresh[i] when given) if this call refreshed
+// the noise; otherwise the previous noise is kept.  Four variates per thread.
+__global__ void exploration_noise(unsigned long long seed, const long long* step, const int* state, float* cached,
+                                  long long n, const float* fresh) {
+    const long long block = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
+    const long long first = block * 4;
+    if (first >= n || state[2] == 0) return;
+    if (fresh) {
+        for (long long i = first; i < min(first + 4, n); ++i) cached[i] = fresh[i];
+        return;
+    }
+    const unsigned long long draw = static_cast<unsigned long long>(step[0] - 1);  // the repeat kernel's draw
+    const uint4 c = make_uint4(static_cast<unsigned int>(block), static_cast<unsigned int>(draw),
+                               static_cast<unsigned int>(draw >> 32), kExplorationStream);
+    const uint4 r = philox4x32_10(c, make_uint2(static_cast<unsigned int>(seed), static_cast<unsigned int>(seed >> 32)));
+    const float two_pi = 6.28318530717958647692f;
+    const float r0 = sqrtf(-2.0f * logf(uniform_open0(r.x)));
+    const float r1 = sqrtf(-2.0f * logf(uniform_open0(r.z)));
+    float s0, c0, s1, c1;
+    sincosf(two_pi * uniform01(r.y), &s0, &c0);
+    sincosf(two_pi * uniform01(r.w), &s1, &c1);
+    const float v[4] = {r0 * c0, r0 * s0, r1 * c1, r1 * s1};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (first + i < n) cached[first + i] = v[i];
+}
+
 // rewards[i] *= 1 / max(sqrt(var + eps), G_r_max / G_max) (reward_normalization.py:28-38).
 __global__ void scale_rewards(float* rewards, long long n, const float* var, const float* r_max, float g_max, float eps) {
     const long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x;
@@ -393,6 +459,21 @@ RL_API int rl_replay_sample_indices(unsigned long long seed, const long long* co
         hipLaunchKernelGGL(P::sample_indices, dim3(rl::ceil_div(n, 256)), dim3(256), 0, rl::as_stream(stream), seed,
                            counter, stream_id, count, fixed_count, idx, n);
         rl::check_launch("Launch index sampling");
+    });
+}
+
+RL_API int rl_exploration_noise(unsigned long long seed, long long* step, const float* cdf, int max_n, int* state,
+                                float* cached_noise, long long count, const float* uniform, const float* fresh_noise,
+                                void* stream) noexcept {
+    return rl::guarded("rl_exploration_noise", [&] {
+        rl::require(step && cdf && state && cached_noise && max_n > 0 && count > 0,
+                    "Exploration noise needs the draw counter, the zeta CDF, the repeat state and the noise buffer.");
+        hipStream_t st = rl::as_stream(stream);
+        hipLaunchKernelGGL(P::exploration_repeat, dim3(1), dim3(1), 0, st, seed, step, cdf, max_n, state, uniform);
+        rl::check_launch("Launch exploration repeat");
+        hipLaunchKernelGGL(P::exploration_noise, dim3(rl::ceil_div((count + 3) / 4, 256)), dim3(256), 0, st, seed,
+                           step, state, cached_noise, count, fresh_noise);
+        rl::check_launch("Launch exploration noise");
     });
 }
 

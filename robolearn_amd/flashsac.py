@@ -258,6 +258,15 @@ class FlashSAC:
             self.reward_max = torch.zeros(1, device=dev)
             self.reward_running = torch.tensor([0.0, 1.0, 0.0], device=dev)
             self.gather_error = torch.zeros(1, dtype=torch.int32, device=dev)
+            # exploration-noise repeats (agent.py:159-214): truncated zeta CDF, [count, length, refresh],
+            # the held noise of the num_envs acting rows and the device draw counter
+            lengths = torch.arange(1, cfg.actor_noise_zeta_max + 1, dtype=torch.float32)
+            pmf = lengths ** (-cfg.actor_noise_zeta_mu)
+            self.zeta_cdf = torch.cumsum(pmf / torch.sum(pmf), dim=0).to(dev)
+            self.exploration_state = torch.tensor([0, 1, 0], dtype=torch.int32, device=dev)
+            self.exploration_step = torch.zeros(1, dtype=torch.long, device=dev)
+            self.exploration_noise = torch.zeros(num_envs, action_dim, device=dev)
+            self._act_nets = {}
         self.metrics = {key: self.metrics_buffer[i: i + 1] for i, key in enumerate(METRIC_KEYS)}
 
     # ------------------------------------------------------------------
@@ -513,25 +522,55 @@ class FlashSAC:
     # ------------------------------------------------------------------
     # inference
     # ------------------------------------------------------------------
+    def _act_net(self, n: int):
+        """fp32 eval-mode actor for n acting rows (the reference acts in fp32 under AMP too,
+        robolearn/warp/flashsac.py:571-575), with its own activations and output buffers."""
+        if n not in self._act_nets:
+            cfg = self.cfg
+            net = Trunk(ensemble=1, in_dim=self.observation_dim, hidden=cfg.actor_hidden_dim,
+                        blocks=cfg.actor_num_blocks, max_rows=n, device=self.device, mode=K.FP32,
+                        prefix_linear=".w.weight")
+            head = torch.empty(n, 2 * self.action_dim, device=self.device)
+            actions = torch.empty(n, self.action_dim, device=self.device)
+            self._act_nets[n] = (net, head, actions)
+        return self._act_nets[n]
+
     @torch.no_grad()
     def act(self, observations: torch.Tensor, training: bool = True) -> torch.Tensor:
-        """Actor inference in eval mode; training draws Gaussian exploration noise (repeat logic not modelled)."""
-        obs = torch.as_tensor(observations, device=self.device, dtype=torch.float32)[:, : self.observation_dim]
-        obs = obs.contiguous()
+        """Normalized actions from the eval-mode actor (agent.py:583-585 -> sample_actions :414-455).
+
+        Deterministic inference returns tanh(mean) and leaves the exploration
+        state alone.  Training acts over exactly num_envs rows and holds one
+        Gaussian noise draw for a truncated-zeta number of calls
+        (agent.py:180-214); the repeat state and the draws stay on the device."""
+        obs = torch.as_tensor(observations, device=self.device, dtype=torch.float32)
+        if obs.dim() != 2 or obs.shape[1] < self.observation_dim:
+            raise ValueError("act() expects [rows, obs] observations with the actor's observation prefix.")
+        obs = obs[:, : self.observation_dim].contiguous()
         n = obs.shape[0]
-        if n > 2 * self.batch_size:
-            raise ValueError("act() supports at most 2 * sample_batch_size rows.")
-        net, p = self.actor_net, self.actor_p
-        net.forward(p, self.actor_w, self.actor_running, obs, rows=n, x_stride=0, training=False)
-        net.post_norm(p, rows=n, row0=0, count=n)
-        head = torch.empty(n, 2 * self.action_dim, device=self.device)
-        K.linear_forward(net.z_op, self.head_w_op, head, rows=n, in_dim=net.h, out_dim=2 * self.action_dim,
-                         bias=self.head_b, mode=self.mode)
-        actions = torch.empty(n, self.action_dim, device=self.device)
-        noise = torch.randn(n, self.action_dim, device=self.device) if training else None
-        K.tanh_gaussian_forward(head, noise, actions, None, rows=n, action_dim=self.action_dim,
-                                deterministic=not training)
-        return actions
+        if training and n != self.num_envs:
+            raise ValueError("Training action batches must match num_envs.")
+        A = self.action_dim
+        net, head, actions = self._act_net(n)
+        p = self.actor_p
+        with torch.cuda.device(self.device):
+            net.forward(p, p, self.actor_running, obs, rows=n, x_stride=0, training=False)
+            net.post_norm(p, rows=n, row0=0, count=n)
+            K.linear_forward(net.z, self.head_w, head, rows=n, in_dim=net.h, out_dim=2 * A, bias=self.head_b,
+                             mode=K.FP32)
+            noise = None
+            if training:
+                _native.call("rl_exploration_noise", self.cfg.seed * 7919 + 37, self.exploration_step.data_ptr(),
+                             self.zeta_cdf.data_ptr(), self.cfg.actor_noise_zeta_max,
+                             self.exploration_state.data_ptr(), self.exploration_noise.data_ptr(), n * A, None, None,
+                             K.stream())
+                noise = self.exploration_noise
+            K.tanh_gaussian_forward(head, noise, actions, None, rows=n, action_dim=A, deterministic=not training)
+            return actions.clone()
+
+    def sample_actions(self, interaction_step: int, prev_transition: dict, training: bool) -> torch.Tensor:
+        """Reference-named entry (agent.py:414-455): acts on prev_transition["next_observation"]."""
+        return self.act(prev_transition["next_observation"], training=training)
 
     # ------------------------------------------------------------------
     # the update

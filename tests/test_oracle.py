@@ -487,3 +487,50 @@ def test_reward_stats_closed_forms():
     scaled = stats.scale(np.array([1.0, -2.0], np.float32), g_max=5.0)
     denominator = max(math.sqrt(stats.running[1] + 1e-8), stats.maximum[0] / 5.0)
     np.testing.assert_allclose(scaled, np.array([1.0, -2.0]) / denominator, rtol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# exploration-noise repeats (agent.py:159-214)
+# ---------------------------------------------------------------------------
+from oracle import explore as OX  # noqa: E402
+
+
+@pytest.mark.parametrize("mu,max_n", [(2.0, 16), (0.0, 5), (1.5, 1)])
+def test_zeta_cdf_closed_form(mu, max_n):
+    cdf = OX.zeta_cdf(mu, max_n)
+    harmonic = np.cumsum([k ** (-mu) for k in range(1, max_n + 1)])
+    np.testing.assert_allclose(cdf.numpy(), harmonic / harmonic[-1], rtol=1e-6)
+    if mu == 0.0:
+        np.testing.assert_allclose(cdf.numpy(), np.arange(1, max_n + 1) / max_n, rtol=1e-6)
+
+
+def test_sample_length_brute_force_and_all_false_mask():
+    cdf = OX.zeta_cdf(2.0, 8)
+    for u in np.linspace(0.0, float(cdf[-1]) - 1e-6, 57):
+        assert OX.sample_length(float(u), cdf) == 1 + int((cdf.numpy() <= np.float32(u)).sum())
+    # u beyond the last entry: the mask is all false and torch.argmax picks index 0
+    assert int(torch.argmax(torch.zeros(8, dtype=torch.int32))) == 0
+    assert OX.sample_length(float(cdf[-1]), cdf) == 1
+
+
+def test_exploration_refresh_schedule():
+    cdf = OX.zeta_cdf(0.0, 4)  # uniform lengths 1..4: u in [(L-1)/4, L/4) gives L
+    lengths = [3, 1, 4, 2, 2, 1]
+    state = OX.Exploration((2, 3))
+    refresh_at, t = set(), 0
+    for length in lengths:
+        refresh_at.add(t)
+        t += length
+    schedule = iter(lengths)
+    u_for = {L: (L - 0.5) / 4.0 for L in range(1, 5)}
+    held = None
+    for step in range(sum(lengths)):
+        fresh = torch.full((2, 3), float(step))
+        u = u_for[next(schedule)] if step in refresh_at else 0.9
+        refreshed = state.step(u, fresh, cdf)
+        assert refreshed == (step in refresh_at), step
+        if refreshed:
+            held = fresh
+        torch.testing.assert_close(state.noise, held)
+    mean, std = torch.zeros(2, 3), torch.full((2, 3), 0.5)
+    torch.testing.assert_close(state.actions(mean, std), torch.tanh(0.5 * held))
