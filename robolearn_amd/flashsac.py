@@ -385,7 +385,18 @@ class FlashSAC:
                     self._host_additions = additions
         self._update_step = int(np.asarray(state["update_counters"])[0])
 
-    def save(self, path, *, include_replay: bool = False) -> None:
+    def save(self, path, *, include_replay: bool = False, format: str = "native") -> None:
+        """Checkpoint directory: "native" (config.json + agent.npz, optional replay) or "torch", the
+        reference's Torch layout (robolearn/flashsac/agent.py:529-551), readable by its load()."""
+        if format == "torch":
+            from . import torch_checkpoint
+
+            torch_checkpoint.save(self, path)
+            if include_replay:
+                torch_checkpoint.save_replay_buffer(self, path)
+            return
+        if format != "native":
+            raise ValueError("format must be 'native' or 'torch'.")
         directory = Path(path)
         directory.mkdir(parents=True, exist_ok=True)
         metadata = {
@@ -404,7 +415,13 @@ class FlashSAC:
             np.savez(stream, **state)
 
     def load(self, path) -> None:
+        """Load a native checkpoint, or a Torch-layout one (actor.pt beside config.json)."""
         directory = Path(path)
+        if (directory / "actor.pt").exists():
+            from . import torch_checkpoint
+
+            torch_checkpoint.load(self, directory)
+            return
         metadata = json.loads((directory / "config.json").read_text())
         if metadata.get("format") != "robolearn-mi355x-flashsac-v1":
             raise ValueError("Unrecognized FlashSAC checkpoint format.")
@@ -427,6 +444,19 @@ class FlashSAC:
             # a loaded normalizer restarts its per-environment returns (agent.py:570-572)
             state.pop("normalizer.returns", None)
         self.load_state_dict(state)
+
+    def save_replay_buffer(self, path) -> None:
+        """replay_buffer.pt in the reference layout (agent.py:553-554, replay.py:196-216)."""
+        from . import torch_checkpoint
+
+        torch_checkpoint.save_replay_buffer(self, path)
+
+    def load_replay_buffer(self, path) -> None:
+        """Restore replay_buffer.pt (agent.py:575-576, replay.py:218-240)."""
+        from . import torch_checkpoint
+
+        self._ensure_replay()
+        torch_checkpoint.load_replay_buffer(self, path)
 
     # ------------------------------------------------------------------
     # replay
