@@ -200,13 +200,13 @@ def ppo_rollout(agent, seed=0):
     n = agent.batch_size
     torch.manual_seed(seed)
     obs = torch.randn(n, agent.observation_dim, device=agent.device)
-    agent.act(obs)
-    actions, log_probs, _, means, stds = agent._act
+    actions = agent.act(obs)
+    sampled = agent._act_state(n)
     agent.observations.copy_(obs)
     agent.actions.copy_(actions)
-    agent.log_probs.copy_(log_probs)
-    agent.means.copy_(means)
-    agent.stds.copy_(stds)
+    agent.log_probs.copy_(sampled["log_probs"])
+    agent.means.copy_(sampled["mean"])
+    agent.stds.copy_(sampled["std"].expand(n, -1))
     agent.values.copy_(torch.randn(n, device=agent.device))
     agent.next_values.copy_(torch.randn(n, device=agent.device))
     agent.rewards.copy_(torch.randn(n, device=agent.device))
@@ -433,6 +433,34 @@ def kernel_sweep() -> list:
                   "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
                   "detail": "4096 envs, obs 123, act 37, actor 256 x 2 blocks, fp32 (the reference acts in fp32); "
                             "small products, launch-bound"})
+    del actor_agent
+
+    # (f) PPO rollout step at the c3 collection shape: act() (actor + critic MLPs, Philox noise, sampling)
+    # then store() (critic MLP on the next observations, rollout row copies)
+    from robolearn_amd.ppo import WarpPPO
+
+    pcfg = ppo_config()
+    ppo = WarpPPO(PPO_C3["obs"], PPO_C3["act"], PPO_C3["envs"], PPO_C3["horizon"], pcfg)
+    n = PPO_C3["envs"]
+    obs_now = torch.randn(n, PPO_C3["obs"], generator=g, device=device)
+    obs_next = torch.randn(n, PPO_C3["obs"], generator=g, device=device)
+    rewards = torch.randn(n, generator=g, device=device)
+    flags = torch.zeros(n, dtype=torch.int32, device=device)
+
+    def rollout_step():
+        ppo.act(obs_now)
+        ppo.store(0, obs_now, rewards, flags, flags, obs_next)
+
+    ms = _time_launches(rollout_step)
+    widths = (PPO_C3["obs"], *PPO_C3["hidden"])
+    mlp = lambda out: sum(2 * n * a * b for a, b in zip(widths, widths[1:] + (out,)))  # noqa: E731
+    flops = mlp(PPO_C3["act"]) + 2 * mlp(1)
+    achieved = flops / (ms * 1e-3) / 1e12
+    lines.append({"kernel": "ppo rollout step (act + store)", "ms": round(ms, 4), "flops": int(flops),
+                  "bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                  "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
+                  "detail": "4096 envs, obs 123, act 37, 512-256-128 ELU, fp32: three MLP forwards, sampling and "
+                            "the rollout row copies; launch-bound"})
     return lines
 
 

@@ -312,6 +312,24 @@ int rl_gae(int horizon, int num_envs, float gamma, float lambda, int current_tim
            float* advantages, float* returns, void* stream);
 /* robolearn/warp/ppo.py:136-159 (fixed-order two-pass) */
 int rl_normalize_advantages(float* advantages, long long n, int sample_std, float* stats, void* stream);
+/* Rollout action sampling (replaces WarpPPO.act's _sample kernel,
+ * robolearn/warp/ppo.py:26-58, 488-507): actions = mean + std * noise with std =
+ * exp(p) or clamp(p, min_std, max_std), log-probs, values = value[:, 0], and
+ * the sampled std vector.  noise NULL = deterministic; counter (optional) is
+ * advanced by one. */
+int rl_ppo_sample(const float* mean, long long ld_mean, const float* value, long long ld_value,
+                  const float* parameter, int scalar_std, float min_std, float max_std, const float* noise,
+                  long long rows, int action_dim, float* actions, float* log_probs, float* values, float* sampled_std,
+                  long long* counter, void* stream);
+/* Rollout store of one step (replaces WarpPPO.store's _store kernel,
+ * robolearn/warp/ppo.py:61-99, 509-550): row step * E + i of each rollout buffer. */
+int rl_ppo_store(int step, long long num_envs, int obs_dim, int action_dim, const float* observations,
+                 const float* actions, const float* log_probs, const float* values, const float* rewards,
+                 const int* terminated, const int* truncated, const float* next_values, long long ld_next_values,
+                 const float* mean, long long ld_mean, const float* sampled_std, float* rollout_obs,
+                 float* rollout_actions, float* rollout_log_probs, float* rollout_values, float* rollout_rewards,
+                 int* rollout_terminated, int* rollout_truncated, float* rollout_next_values, float* rollout_means,
+                 float* rollout_stds, void* stream);
 /* Keyed Feistel permutation with cycle walking; replaces _shuffle_keys +
  * radix_sort_pairs, robolearn/warp/ppo.py:162-169, 595-603. */
 int rl_permutation(long long n, unsigned long long seed, const int* seed_counter, long long* perm64, int* perm32,

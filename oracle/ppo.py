@@ -9,13 +9,15 @@ Follows robolearn/warp/ppo.py:
                                  clipped value / entropy loss (:255-310),
                                  gradient clipping (:241-252, 676-693), Adam
   _mlp :313-350                  Linear + ELU/Tanh MLPs, U(+-1/sqrt(fan_in)) init
+  _sample :26-58                 rollout actions, log-probs and values (sample)
 with the Torch formulas of the reference's own parity harness
 (examples/diagnose_ppo_update.py:75-162), including torch.optim.Adam.
 
 Parity pinning: GAE, advantage normalization and the loss with its gradients
 are pinned by the reference's known-answer tests (tests/test_warp_ppo.py:23-119,
 restated in tests/test_oracle.py); the KL expression by the closed form of the
-Gaussian KL; Adam by torch.optim.Adam itself.  Combined (non-separate)
+Gaussian KL; Adam by torch.optim.Adam itself; the rollout log-prob by
+torch.distributions.Normal.log_prob of the same actions.  Combined (non-separate)
 gradient clipping follows Warp-NN's Adam ``max_norm`` option, whose source is
 not in the reference tree: parity unpinned for that mode (the separate-group
 mode's formula is visible at ppo.py:249-252 and is the one the tests use).
@@ -97,6 +99,16 @@ def std_of(parameter, cfg):
     if cfg.std_type == "scalar":
         return parameter.clamp(*cfg.std_range)
     return torch.exp(parameter)
+
+
+def sample(mean, value, parameter, noise, cfg):
+    """Rollout sampling, ppo.py:26-58: actions = mean + std * noise, the Gaussian log-prob summed over
+    action dimensions (log std = p for "log", log(clamp(p)) for "scalar"), values = value[:, 0]."""
+    std = std_of(parameter, cfg)
+    log_std = torch.log(std) if cfg.std_type == "scalar" else parameter
+    actions = mean + std * noise
+    log_probs = (-0.5 * (noise * noise + 2.0 * log_std + math.log(2.0 * math.pi))).sum(-1)
+    return actions, log_probs, value[:, 0], std
 
 
 def loss_terms(mean, value, parameter, actions, old_log_probs, old_values, advantages, returns, cfg):

@@ -107,6 +107,8 @@ SIGNATURES = {
     "rl_advance_counters": (c_int, [P, c_int, P]),
     "rl_scale_rewards": (c_int, [P, c_ll, P, P, c_float, c_float, P]),
     "rl_exploration_noise": (c_int, [c_ull, P, P, c_int, P, P, c_ll, P, P, P]),
+    "rl_ppo_sample": (c_int, [P, c_ll, P, c_ll, P, c_int, c_float, c_float, P, c_ll, c_int, P, P, P, P, P, P]),
+    "rl_ppo_store": (c_int, [c_int, c_ll, c_int, c_int] + [P] * 8 + [c_ll, P, c_ll, P] + [P] * 10 + [P]),
     "rl_replay_ingest": (c_int, [c_ll, c_int, c_int, c_int, c_ll, c_float] + [P] * 6 + [P] * 4 + [P] * 7
                          + [P, P]),
     "rl_reward_stats_update": (c_int, [c_ll, c_float, P, P, P, P, P, P, P]),

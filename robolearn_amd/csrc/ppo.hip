@@ -382,10 +382,156 @@ __global__ void elu_backward_kernel(float* dx, const float* y, long long n) {
         dx[i] *= y[i] > 0.0f ? 1.0f : y[i] + 1.0f;
 }
 
+// Rollout action sampling (robolearn/warp/ppo.py:26-58 _sample, called by act
+// :488-507): per action dimension std = exp(p) ("log") or clamp(p, lo, hi)
+// ("scalar"), actions = mean + std * noise, log_prob = sum_j -(noise^2 +
+// 2 log std + ln 2 pi) / 2, values = value[:, 0], sampled_std = std.  One wave
+// per environment row, lanes over the action dimensions.  noise == nullptr is
+// the deterministic case (zero noise).  The draw counter of the noise is
+// advanced here, after the launch that drew with it.
+struct SampleArgs {
+    const float* mean;
+    long long ld_mean;
+    const float* value;
+    long long ld_value;
+    const float* parameter;
+    const float* noise;
+    long long rows;
+    int action_dim;
+    int scalar_std;
+    float min_std, max_std;
+    float* actions;
+    float* log_probs;
+    float* values;
+    float* sampled_std;
+    long long* counter;
+};
+
+__global__ __launch_bounds__(kGatherRows* kWave) void rollout_sample(SampleArgs a) {
+    if (a.counter && blockIdx.x == 0 && threadIdx.x == 0) a.counter[0] += 1;
+    const long long r = static_cast<long long>(blockIdx.x) * kGatherRows + threadIdx.x / kWave;
+    if (r >= a.rows) return;  // wave-uniform
+    const int lane = threadIdx.x % kWave;
+    constexpr float kLogTwoPi = 1.8378770664093453f;
+    float log_prob = 0.0f;
+    for (int j = lane; j < a.action_dim; j += kWave) {
+        const float p = a.parameter[j];
+        const float std = a.scalar_std ? fminf(fmaxf(p, a.min_std), a.max_std) : expf(p);
+        const float log_std = a.scalar_std ? logf(std) : p;
+        const float noise = a.noise ? a.noise[r * a.action_dim + j] : 0.0f;
+        a.actions[r * a.action_dim + j] = a.mean[r * a.ld_mean + j] + std * noise;
+        log_prob -= 0.5f * (noise * noise + 2.0f * log_std + kLogTwoPi);
+        if (r == 0) a.sampled_std[j] = std;
+    }
+    log_prob = wave_sum(log_prob);
+    if (lane == 0) {
+        a.log_probs[r] = log_prob;
+        a.values[r] = a.value[r * a.ld_value];
+    }
+}
+
+// Rollout store of step t (robolearn/warp/ppo.py:61-99 _store, called by store
+// :509-550): row k = t E + i of every rollout buffer takes environment i's
+// observation, sampled action, log-prob, value, reward, done flags, bootstrap
+// value of the pre-reset next observation, mean and the sampled std.
+struct StoreArgs {
+    long long row0;  // t * E
+    long long num_envs;
+    int obs_dim, action_dim;
+    const float* observations;
+    const float* actions;
+    const float* log_probs;
+    const float* values;
+    const float* rewards;
+    const int* terminated;
+    const int* truncated;
+    const float* next_values;
+    long long ld_next_values;
+    const float* mean;
+    long long ld_mean;
+    const float* sampled_std;
+    float* rollout_obs;
+    float* rollout_actions;
+    float* rollout_log_probs;
+    float* rollout_values;
+    float* rollout_rewards;
+    int* rollout_terminated;
+    int* rollout_truncated;
+    float* rollout_next_values;
+    float* rollout_means;
+    float* rollout_stds;
+};
+
+__global__ __launch_bounds__(kGatherRows* kWave) void rollout_store(StoreArgs a) {
+    const long long i = static_cast<long long>(blockIdx.x) * kGatherRows + threadIdx.x / kWave;
+    if (i >= a.num_envs) return;  // wave-uniform
+    const int lane = threadIdx.x % kWave;
+    const long long k = a.row0 + i;
+    for (int j = lane; j < a.obs_dim; j += kWave) a.rollout_obs[k * a.obs_dim + j] = a.observations[i * a.obs_dim + j];
+    for (int j = lane; j < a.action_dim; j += kWave) {
+        a.rollout_actions[k * a.action_dim + j] = a.actions[i * a.action_dim + j];
+        a.rollout_means[k * a.action_dim + j] = a.mean[i * a.ld_mean + j];
+        a.rollout_stds[k * a.action_dim + j] = a.sampled_std[j];
+    }
+    if (lane == 0) {
+        a.rollout_log_probs[k] = a.log_probs[i];
+        a.rollout_values[k] = a.values[i];
+        a.rollout_rewards[k] = a.rewards[i];
+        a.rollout_terminated[k] = a.terminated[i];
+        a.rollout_truncated[k] = a.truncated[i];
+        a.rollout_next_values[k] = a.next_values[i * a.ld_next_values];
+    }
+}
+
 }  // namespace ppo
 }  // namespace rl
 
 namespace Q = rl::ppo;
+
+RL_API int rl_ppo_sample(const float* mean, long long ld_mean, const float* value, long long ld_value,
+                         const float* parameter, int scalar_std, float min_std, float max_std, const float* noise,
+                         long long rows, int action_dim, float* actions, float* log_probs, float* values,
+                         float* sampled_std, long long* counter, void* stream) noexcept {
+    return rl::guarded("rl_ppo_sample", [&] {
+        rl::require(mean && value && parameter && actions && log_probs && values && sampled_std,
+                    "PPO sampling needs the mean, value, distribution parameter and outputs.");
+        rl::require(rows > 0 && action_dim > 0 && ld_mean >= action_dim && ld_value >= 1,
+                    "PPO sampling shapes are invalid.");
+        Q::SampleArgs a{mean, ld_mean, value, ld_value, parameter, noise, rows, action_dim, scalar_std, min_std,
+                        max_std, actions, log_probs, values, sampled_std, counter};
+        hipLaunchKernelGGL(Q::rollout_sample, dim3(rl::ceil_div(rows, Q::kGatherRows)),
+                           dim3(Q::kGatherRows * rl::kWave), 0, rl::as_stream(stream), a);
+        rl::check_launch("Launch PPO rollout sampling");
+    });
+}
+
+RL_API int rl_ppo_store(int step, long long num_envs, int obs_dim, int action_dim, const float* observations,
+                        const float* actions, const float* log_probs, const float* values, const float* rewards,
+                        const int* terminated, const int* truncated, const float* next_values,
+                        long long ld_next_values, const float* mean, long long ld_mean, const float* sampled_std,
+                        float* rollout_obs, float* rollout_actions, float* rollout_log_probs, float* rollout_values,
+                        float* rollout_rewards, int* rollout_terminated, int* rollout_truncated,
+                        float* rollout_next_values, float* rollout_means, float* rollout_stds,
+                        void* stream) noexcept {
+    return rl::guarded("rl_ppo_store", [&] {
+        rl::require(step >= 0 && num_envs > 0 && obs_dim > 0 && action_dim > 0 && ld_mean >= action_dim &&
+                        ld_next_values >= 1,
+                    "PPO store shapes are invalid.");
+        rl::require(observations && actions && log_probs && values && rewards && terminated && truncated &&
+                        next_values && mean && sampled_std,
+                    "PPO store needs every per-step input.");
+        rl::require(rollout_obs && rollout_actions && rollout_log_probs && rollout_values && rollout_rewards &&
+                        rollout_terminated && rollout_truncated && rollout_next_values && rollout_means && rollout_stds,
+                    "PPO store needs every rollout buffer.");
+        Q::StoreArgs a{static_cast<long long>(step) * num_envs, num_envs, obs_dim, action_dim, observations, actions,
+                       log_probs, values, rewards, terminated, truncated, next_values, ld_next_values, mean, ld_mean,
+                       sampled_std, rollout_obs, rollout_actions, rollout_log_probs, rollout_values, rollout_rewards,
+                       rollout_terminated, rollout_truncated, rollout_next_values, rollout_means, rollout_stds};
+        hipLaunchKernelGGL(Q::rollout_store, dim3(rl::ceil_div(num_envs, Q::kGatherRows)),
+                           dim3(Q::kGatherRows * rl::kWave), 0, rl::as_stream(stream), a);
+        rl::check_launch("Launch PPO rollout store");
+    });
+}
 
 RL_API int rl_gae(int horizon, int num_envs, float gamma, float lambda, int current_timeout_bootstrap,
                   const float* rewards, const float* values, const float* next_values, const int* terminated,

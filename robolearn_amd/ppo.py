@@ -72,11 +72,11 @@ class WarpPPO:
         with torch.cuda.device(dev):
             # actor tensors + std parameter form clipping group 0, critic tensors group 1
             order = [[n for n, _ in actor] + ["std"], [n for n, _ in critic]]
-            self.store = FlatStore(shapes, dev, groups=[[n] for n in order[0]] + [[n] for n in order[1]])
+            self.flat = FlatStore(shapes, dev, groups=[[n] for n in order[0]] + [[n] for n in order[1]])
             self.names = [n for n, _ in actor] + [n for n, _ in critic] + ["std"]
-            views = self.store.params()
+            views = self.flat.params()
             self.parameters = [views[n] for n in self.names]
-            self.grads = self.store.grads()
+            self.grads = self.flat.grads()
             rng = np.random.default_rng(cfg.seed)
             for n, shape in actor + critic:
                 bound = 1.0 / math.sqrt(shape[-1] if n.endswith("weight") else shapes[n[:-4] + "weight"][-1])
@@ -88,10 +88,10 @@ class WarpPPO:
                 self.log_std = self.distribution_parameter
             else:
                 self.std_param = self.distribution_parameter
-            first_critic = self.store.offsets[critic[0][0]]
-            self.group_ranges = [(0, first_critic), (first_critic, self.store.size)]
+            first_critic = self.flat.offsets[critic[0][0]]
+            self.group_ranges = [(0, first_critic), (first_critic, self.flat.size)]
             if not cfg.separate_grad_clipping:
-                self.group_ranges = [(0, self.store.size)]
+                self.group_ranges = [(0, self.flat.size)]
             self.timestep = torch.zeros(1, device=dev)
             self.lr = torch.full((1,), float(cfg.learning_rate), device=dev)
             self._make_optimizer()
@@ -130,15 +130,17 @@ class WarpPPO:
             self.kl = z(1)
             max_width = max(A, 1, *cfg.hidden_dims)
             self.partial = z(max(K.chunks(M) * max_width, (M + 15) // 16))  # column / KL partial sums
-            self.norm_partial = z((self.store.size + 4095) // 4096 + 1)
+            self.norm_partial = z((self.flat.size + 4095) // 4096 + 1)
             self.group_norms = [z(1) for _ in self.group_ranges]
             self.workspace = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
-            self._act_mean = None
+            self._act_buffers = {}
+            self._act_rows = 0
+            self._act_counter = torch.zeros(1, dtype=torch.long, device=dev)  # Philox draw counter of act()
         self._update_graph = None
 
     def _make_optimizer(self):
         n = len(self.names)
-        store = self.store
+        store = self.flat
         ptrs = lambda buf: _native.pointer_array([store.view(buf, name).data_ptr() for name in self.names])  # noqa
         rows = [1] * n
         cols = [int(np.prod(store.shapes[name])) for name in self.names]
@@ -158,7 +160,7 @@ class WarpPPO:
 
     # ------------------------------------------------------------------
     def _layer(self, prefix, i):
-        p = self.store.params()
+        p = self.flat.params()
         return p[f"{prefix}.{i}.weight"], p[f"{prefix}.{i}.bias"]
 
     def _mlp_forward(self, prefix, x, rows, hidden, out, x_ld=None):
@@ -231,7 +233,7 @@ class WarpPPO:
         self._mlp_backward("actor", self.b_obs, M, self.actor_h, self.dmean, self.actor_d, x_ld=self.obs_ld)
         self._mlp_backward("critic", self.b_obs, M, self.critic_h, self.dvalue, self.critic_d, x_ld=self.obs_ld)
         for (start, end), norm in zip(self.group_ranges, self.group_norms):
-            grad = self.store.grad[start:end]
+            grad = self.flat.grad[start:end]
             _native.call("rl_sum_squares", grad.data_ptr(), grad.numel(), self.norm_partial.data_ptr(),
                          norm.data_ptr(), K.stream())
             _native.call("rl_clip_by_norm", grad.data_ptr(), grad.numel(), norm.data_ptr(),
@@ -272,43 +274,72 @@ class WarpPPO:
             self._update_graph.replay()
 
     # ------------------------------------------------------------------
+    def _act_state(self, n: int):
+        """Per-row-count buffers of act(): MLP activations, mean, value, noise and the sampled outputs."""
+        if n not in self._act_buffers:
+            z = lambda *s: torch.zeros(*s, device=self.device)  # noqa: E731
+            A = self.action_dim
+            self._act_buffers[n] = dict(hidden=[z(n, w) for w in self.config.hidden_dims], mean=z(n, A),
+                                        value=z(n, 1), noise=z(n, A), actions=z(n, A), log_probs=z(n), values=z(n),
+                                        std=z(A), next_value=z(n, 1))
+        return self._act_buffers[n]
+
     @torch.no_grad()
     def act(self, observations, deterministic: bool = False):
-        """Gaussian actions from the actor mean and the distribution parameter (rollout helper)."""
-        obs = torch.as_tensor(observations, device=self.device, dtype=torch.float32).contiguous()
+        """Gaussian actions from the actor mean and the distribution parameter (ppo.py:488-507).
+
+        The MLPs run on the fp32 MFMA GEMMs; the noise is a Philox draw keyed by
+        the seed and a device counter, and rl_ppo_sample forms the actions,
+        log-probs, values and sampled std (ppo.py:26-58) for store()."""
+        obs = torch.as_tensor(observations, device=self.device, dtype=torch.float32)
+        if obs.dim() != 2 or obs.shape[1] != self.observation_dim:
+            raise ValueError("act() expects [rows, observation_dim] observations.")
+        obs = obs.contiguous()
         n = obs.shape[0]
-        hidden = [torch.empty(n, w, device=self.device) for w in self.config.hidden_dims]
-        mean = torch.empty(n, self.action_dim, device=self.device)
-        value = torch.empty(n, 1, device=self.device)
-        self._mlp_forward("actor", obs, n, hidden, mean)
-        self._mlp_forward("critic", obs, n, hidden, value)
-        p = self.distribution_parameter
-        std = p.clamp(*self.config.std_range) if self.config.std_type == "scalar" else torch.exp(p)
-        noise = torch.zeros_like(mean) if deterministic else torch.randn_like(mean)
-        actions = mean + std * noise
-        log_std = torch.log(std)
-        self._act = (actions, (-0.5 * (noise * noise + 2 * log_std + math.log(2 * math.pi))).sum(1), value[:, 0],
-                     mean, std.expand_as(mean).contiguous())
-        return actions
+        b = self._act_state(n)
+        cfg = self.config
+        with torch.cuda.device(self.device):
+            self._mlp_forward("actor", obs, n, b["hidden"], b["mean"])
+            self._mlp_forward("critic", obs, n, b["hidden"], b["value"])
+            noise = None
+            if not deterministic:
+                K.philox_normal(b["noise"], seed=cfg.seed * 7919 + 53, counter=self._act_counter, stream_id=53)
+                noise = b["noise"]
+            _native.call("rl_ppo_sample", b["mean"].data_ptr(), self.action_dim, b["value"].data_ptr(), 1,
+                         self.distribution_parameter.data_ptr(), int(cfg.std_type == "scalar"),
+                         float(cfg.std_range[0]), float(cfg.std_range[1]),
+                         noise.data_ptr() if noise is not None else None, n, self.action_dim,
+                         b["actions"].data_ptr(), b["log_probs"].data_ptr(), b["values"].data_ptr(),
+                         b["std"].data_ptr(), self._act_counter.data_ptr() if noise is not None else None, K.stream())
+        self._act_rows = n
+        return b["actions"].clone()
 
     @torch.no_grad()
     def store(self, step, observations, rewards, terminated, truncated, next_observations) -> None:
+        """Store the last sampled action and bootstrap from the pre-reset next observation (ppo.py:509-550)."""
         if not 0 <= step < self.horizon:
             raise ValueError("step must be within the rollout horizon.")
-        actions, log_probs, values, mean, std = self._act
         n = self.num_envs
-        sl = slice(step * n, (step + 1) * n)
-        hidden = [torch.empty(n, w, device=self.device) for w in self.config.hidden_dims]
-        next_value = torch.empty(n, 1, device=self.device)
-        self._mlp_forward("critic", torch.as_tensor(next_observations, device=self.device).float().contiguous(), n,
-                          hidden, next_value)
-        self.observations[sl] = torch.as_tensor(observations, device=self.device).float()
-        self.actions[sl], self.log_probs[sl], self.values[sl] = actions, log_probs, values
-        self.means[sl], self.stds[sl] = mean, std
-        self.rewards[sl] = torch.as_tensor(rewards, device=self.device).float()
-        self.terminated[sl] = torch.as_tensor(terminated, device=self.device).int()
-        self.truncated[sl] = torch.as_tensor(truncated, device=self.device).int()
-        self.next_values[sl] = next_value[:, 0]
+        if self._act_rows != n:
+            raise RuntimeError("store() needs a preceding act() over num_envs observations.")
+        b = self._act_state(n)
+        dev = self.device
+        obs = torch.as_tensor(observations, device=dev, dtype=torch.float32).reshape(n, self.observation_dim)
+        next_obs = torch.as_tensor(next_observations, device=dev, dtype=torch.float32).reshape(n, self.observation_dim)
+        rewards = torch.as_tensor(rewards, device=dev, dtype=torch.float32).reshape(n).contiguous()
+        terminated = torch.as_tensor(terminated, device=dev).reshape(n).to(torch.int32).contiguous()
+        truncated = torch.as_tensor(truncated, device=dev).reshape(n).to(torch.int32).contiguous()
+        obs, next_obs = obs.contiguous(), next_obs.contiguous()
+        with torch.cuda.device(dev):
+            self._mlp_forward("critic", next_obs, n, b["hidden"], b["next_value"])
+            _native.call("rl_ppo_store", int(step), n, self.observation_dim, self.action_dim, obs.data_ptr(),
+                         b["actions"].data_ptr(), b["log_probs"].data_ptr(), b["values"].data_ptr(),
+                         rewards.data_ptr(), terminated.data_ptr(), truncated.data_ptr(), b["next_value"].data_ptr(),
+                         1, b["mean"].data_ptr(), self.action_dim, b["std"].data_ptr(),
+                         self.observations.data_ptr(), self.actions.data_ptr(), self.log_probs.data_ptr(),
+                         self.values.data_ptr(), self.rewards.data_ptr(), self.terminated.data_ptr(),
+                         self.truncated.data_ptr(), self.next_values.data_ptr(), self.means.data_ptr(),
+                         self.stds.data_ptr(), K.stream())
 
     def health_metrics(self) -> dict:
         parameter = self.distribution_parameter.detach().cpu().numpy()
@@ -328,7 +359,7 @@ class WarpPPO:
 
     def state_dict(self) -> dict:
         torch.cuda.synchronize(self.device)
-        m1, m2 = self.store.moments()
+        m1, m2 = self.flat.moments()
         state = {f"parameter_{i}": p.detach().cpu().numpy().copy() for i, p in enumerate(self.parameters)}
         state.update({f"adam_m1_{i}": m1[n].cpu().numpy().copy() for i, n in enumerate(self.names)})
         state.update({f"adam_m2_{i}": m2[n].cpu().numpy().copy() for i, n in enumerate(self.names)})
@@ -339,7 +370,7 @@ class WarpPPO:
 
     @torch.no_grad()
     def load_state_dict(self, state: dict) -> None:
-        m1, m2 = self.store.moments()
+        m1, m2 = self.flat.moments()
         arrays = {f"parameter_{i}": p for i, p in enumerate(self.parameters)}
         arrays.update({f"adam_m1_{i}": m1[n] for i, n in enumerate(self.names)})
         arrays.update({f"adam_m2_{i}": m2[n] for i, n in enumerate(self.names)})

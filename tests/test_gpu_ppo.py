@@ -181,3 +181,65 @@ def test_captured_update_matches_eager_and_checkpoint_preserves_graph(gpu, tmp_p
     eager.update(capture=False)
     for expected, actual in zip(eager.parameters, captured.parameters):
         np.testing.assert_allclose(actual.cpu().numpy(), expected.cpu().numpy(), rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("std_type", ["log", "scalar"])
+def test_rollout_act_and_store_match_oracle(gpu, std_type):
+    """act() (ppo.py:26-58, 488-507) and store() (ppo.py:61-99, 509-550) against oracle.ppo.sample with the
+    device's own noise draw read back; the rollout rows land where update() reads them."""
+    print(f"case PPO rollout act/store std_type={std_type}", flush=True)
+    cfg = PPOConfig(hidden_dims=(16, 8), activation="elu", std_type=std_type, epochs=1, num_mini_batches=2)
+    E, T, O, A = 8, 3, 5, 3
+    agent = _agent(O, A, E, T, cfg)
+    state = agent.state_dict()
+    params = [torch.as_tensor(state[f"parameter_{i}"]).double() for i in range(len(agent.parameters))]
+    layers = 2 * (len(cfg.hidden_dims) + 1)
+    actor, critic, parameter = params[:layers], params[layers:2 * layers], params[-1]
+    if std_type == "scalar":  # spread the std parameter across the clamp range
+        parameter = torch.tensor([0.005, 0.7, 5.0], dtype=torch.float64)
+        agent.distribution_parameter.copy_(parameter.float())
+        parameter = parameter.float().double()
+    g = torch.Generator().manual_seed(11)
+    expected = {k: [] for k in ("observations", "actions", "log_probs", "values", "rewards", "terminated",
+                                "truncated", "next_values", "means")}
+    for t in range(T):
+        obs, next_obs = torch.randn(E, O, generator=g), torch.randn(E, O, generator=g)
+        rewards = torch.randn(E, generator=g)
+        terminated = (torch.rand(E, generator=g) < 0.3).int()
+        truncated = (torch.rand(E, generator=g) < 0.2).int()
+        actions = agent.act(obs.to(gpu)).cpu().double()
+        sampled = agent._act_state(E)
+        noise = sampled["noise"].cpu().double()
+        mean = OP.mlp(obs.double(), actor, "elu")
+        value = OP.mlp(obs.double(), critic, "elu")
+        exp_actions, exp_lp, exp_values, exp_std = OP.sample(mean, value, parameter, noise, cfg)
+        torch.testing.assert_close(actions, exp_actions, rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(sampled["log_probs"].cpu().double(), exp_lp, rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(sampled["values"].cpu().double(), exp_values, rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(sampled["std"].cpu().double(), exp_std, rtol=1e-6, atol=0)
+        agent.store(t, obs.to(gpu), rewards.to(gpu), terminated.to(gpu), truncated.to(gpu), next_obs.to(gpu))
+        for key, value_ in (("observations", obs.double()), ("actions", actions), ("log_probs", exp_lp),
+                            ("values", exp_values), ("rewards", rewards.double()),
+                            ("terminated", terminated.double()), ("truncated", truncated.double()),
+                            ("next_values", OP.mlp(next_obs.double(), critic, "elu")[:, 0]), ("means", mean)):
+            expected[key].append(value_)
+    torch.cuda.synchronize()
+    for key, parts in expected.items():
+        got = getattr(agent, key).cpu().double()
+        torch.testing.assert_close(got, torch.cat(parts), rtol=1e-5, atol=1e-5, msg=key)
+    torch.testing.assert_close(agent.stds.cpu().double(), exp_std.expand(E * T, A), rtol=1e-6, atol=0)
+    np.testing.assert_array_equal(agent.observations.cpu().numpy(), torch.cat(expected["observations"]).numpy())
+    # deterministic acting uses the mean and leaves the draw counter alone
+    counter = agent._act_counter.item()
+    obs = torch.randn(E, O, generator=g)
+    torch.testing.assert_close(agent.act(obs.to(gpu), deterministic=True).cpu().double(),
+                               OP.mlp(obs.double(), actor, "elu"), rtol=1e-5, atol=1e-5)
+    assert agent._act_counter.item() == counter == T
+    # the device draws are standard normal and change with every call
+    big = _agent(O, A, 4096, 1, cfg)
+    big.act(torch.randn(4096, O, generator=g).to(gpu))
+    first = big._act_state(4096)["noise"].clone()
+    big.act(torch.randn(4096, O, generator=g).to(gpu))
+    second = big._act_state(4096)["noise"]
+    assert abs(first.mean().item()) < 0.03 and abs(first.std().item() - 1.0) < 0.03
+    assert not torch.equal(first, second)

@@ -534,3 +534,19 @@ def test_exploration_refresh_schedule():
         torch.testing.assert_close(state.noise, held)
     mean, std = torch.zeros(2, 3), torch.full((2, 3), 0.5)
     torch.testing.assert_close(state.actions(mean, std), torch.tanh(0.5 * held))
+
+
+@pytest.mark.parametrize("std_type", ["log", "scalar"])
+def test_ppo_rollout_sample_log_prob_matches_normal(std_type):
+    cfg = PPOConfig(std_type=std_type)
+    g = torch.Generator().manual_seed(8)
+    mean, noise = torch.randn(6, 5, generator=g, dtype=torch.float64), torch.randn(6, 5, generator=g, dtype=torch.float64)
+    value = torch.randn(6, 1, generator=g, dtype=torch.float64)
+    parameter = torch.randn(5, generator=g, dtype=torch.float64) * 0.5 + (0.0 if std_type == "log" else 0.6)
+    actions, log_probs, values, std = OP.sample(mean, value, parameter, noise, cfg)
+    expected_std = torch.exp(parameter) if std_type == "log" else parameter.clamp(*cfg.std_range)
+    torch.testing.assert_close(std, expected_std)
+    torch.testing.assert_close(actions, mean + expected_std * noise)
+    reference = torch.distributions.Normal(mean, expected_std).log_prob(actions).sum(-1)
+    torch.testing.assert_close(log_probs, reference, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(values, value[:, 0])
