@@ -52,8 +52,9 @@ int rl_plan_destroy(void* plan);
  * moments (optional, needs ldd == n) receives the per-256-row-chunk column
  * (mean, M2) of D in rl_bn_forward_ex's partial layout [batch][ceil(m/256)][2][n],
  * from the GEMM epilogue when the 256x256 bf16 kernel runs the product.
- * a_sums (optional, mode 0 only) receives the row sums of op(A) over K,
- * [batch][m]: the bias gradient of a weight-gradient product dW = dY^T X.
+ * a_sums (optional, mode 0 only, bias NULL) receives the row sums of op(A) over
+ * K in the bias layout, member e at a_sums + e * stride_bias (m when stride_bias
+ * is 0): the bias gradient of a weight-gradient product dW = dY^T X.
  * With splits > 1 the workspace holds splits*batch*m*n floats, plus splits*batch*m
  * with a_sums (rl_gemm_workspace returns the larger size).
  * Serves the three plans of one Linear, robolearn/cuda/linear.py:179-185,

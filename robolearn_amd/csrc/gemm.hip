@@ -189,7 +189,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
         for (int offset = 1; offset < SumLanes; offset <<= 1) a_sum += __shfl_xor(a_sum, offset);
         const int r = m0 + static_cast<int>(threadIdx.x) / SumLanes;
         if (threadIdx.x % SumLanes == 0 && r < p.m)
-            p.a_sums[(static_cast<long long>(split) * p.batch + batch) * p.m + r] = a_sum;
+            p.a_sums[(p.splits == 1 ? batch * p.sums_stride
+                                     : (static_cast<long long>(split) * p.batch + batch) * p.m) + r] = a_sum;
     }
 
     // Accumulator layout of a 32x32 MFMA tile: lane l holds column l % 32 and
@@ -367,7 +368,9 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
             "The ELU-gradient epilogue needs fp32 mode, the ELU outputs as C, beta 0 and no bias.");
     require(splits >= 1, "GEMM split count must be positive.");
     require(static_cast<long long>(m) * n <= std::numeric_limits<int>::max(), "GEMM output exceeds 2^31 elements.");
-    require(!a_sums || mode == 0, "Row sums of A are produced by the fp32 GEMM family only.");
+    require(!a_sums || (mode == 0 && !bias), "Row sums of A are produced by the fp32 GEMM family, without a bias.");
+    // the row sums take the bias layout: member e at a_sums + e * stride_bias (m when stride_bias is 0)
+    const long long sums_stride = stride_bias > 0 ? stride_bias : m;
     require(!moments || (ldd == n && aligned(moments, 16)),
             "GEMM output moments need a row-contiguous output (ldd == n) and 16-byte aligned storage.");
     gemm::Params p{};
@@ -414,6 +417,7 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     } else {
         p.d = d;
         p.a_sums = a_sums;
+        p.sums_stride = sums_stride;
     }
     p.out_vec = n % 4 == 0 && aligned(p.d, 16) && (splits > 1 || (ldd % 4 == 0 && stride_d % 4 == 0)) &&
                 (splits > 1 || ((!bias || (aligned(bias, 16) && stride_bias % 4 == 0)) &&
@@ -444,13 +448,11 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
                 hipLaunchKernelGGL(gemm::splitk_reduce_grouped, dim3(ceil_div(static_cast<long long>(batch) * m,
                                                                                gemm::kReduceCols)),
                                    dim3(256), 0, stream, work, a_sums, nullptr, nullptr, nullptr,
-                                   static_cast<long long>(m), static_cast<long long>(m), 0LL, 1, m, batch, splits, 0.0f,
-                                   0);
+                                   static_cast<long long>(m), sums_stride, 0LL, 1, m, batch, splits, 0.0f, 0);
             else
                 hipLaunchKernelGGL(gemm::splitk_reduce, dim3(ceil_div(static_cast<long long>(batch) * m, 256)),
                                    dim3(256), 0, stream, work, a_sums, nullptr, nullptr, nullptr,
-                                   static_cast<long long>(m), static_cast<long long>(m), 0LL, 1, m, batch, splits, 0.0f,
-                                   0);
+                                   static_cast<long long>(m), sums_stride, 0LL, 1, m, batch, splits, 0.0f, 0);
             check_launch("Launch row-sum reduction");
         }
     }

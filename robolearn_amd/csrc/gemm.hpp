@@ -39,6 +39,7 @@ struct Params {
     float* moments;      // optional per-256-row-chunk (mean, M2) of D: [batch][m / 256][2][n]
     int out_vec;         // 16-byte output stores allowed (n, ldd, strides multiple of 4; aligned outputs)
     float* a_sums;       // optional sum over this split's K of each row of op(A): [splits][batch][m] (fp32 family)
+    long long sums_stride;  // direct mode: elements between batch members of a_sums
 };
 
 // Wave-local LDS fence: this wave's LDS operations are complete and the

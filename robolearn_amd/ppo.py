@@ -114,10 +114,18 @@ class WarpPPO:
             self.b_actions, self.b_means, self.b_stds = z(M, A), z(M, A), z(M, A)
             self.b_log_probs, self.b_values, self.b_advantages, self.b_returns = z(M), z(M), z(M), z(M)
             widths = (O, *cfg.hidden_dims)
-            self.actor_h = [z(M, w) for w in cfg.hidden_dims]
-            self.critic_h = [z(M, w) for w in cfg.hidden_dims]
-            self.actor_d = [z(M, w) for w in widths]
-            self.critic_d = [z(M, w) for w in widths]
+            # hidden activations and input gradients of both MLPs as [2, M, width] pairs (actor, critic), so
+            # each hidden layer of the two networks runs as one batch-2 product
+            self.h_pair = [z(2, M, w) for w in cfg.hidden_dims]
+            self.d_pair = [z(2, M, w) for w in widths]
+            self.actor_h = [h[0] for h in self.h_pair]
+            self.critic_h = [h[1] for h in self.h_pair]
+            # element offsets from each actor hidden-layer tensor to the critic's (batch strides of the pairs)
+            offsets = self.flat.offsets
+            self.w_stride = [offsets[f"critic.{i}.weight"] - offsets[f"actor.{i}.weight"]
+                             for i in range(len(cfg.hidden_dims))]
+            self.b_stride = [offsets[f"critic.{i}.bias"] - offsets[f"actor.{i}.bias"]
+                             for i in range(len(cfg.hidden_dims))]
             self.mean = z(M, A)
             self.value = z(M, 1)
             self.dmean = z(M, A)
@@ -176,24 +184,62 @@ class WarpPPO:
         w, b = self._layer(prefix, self.layers - 1)
         K.linear_forward(inputs, w, out, rows=rows, in_dim=widths[-1], out_dim=out.shape[1], bias=b, mode=K.FP32)
 
-    def _mlp_backward(self, prefix, x, rows, hidden, dout, dbufs, x_ld=None):
-        widths = (self.observation_dim, *self.config.hidden_dims)
+    def _joint_forward(self, rows):
+        """Both MLPs on the minibatch observations: each hidden layer is one batch-2 product over
+        the actor and critic weights (Linear + bias + ELU in the GEMM epilogue), then the two
+        output layers (mean, value)."""
+        hidden = self.config.hidden_dims
+        widths = (self.observation_dim, *hidden)
+        for i, width in enumerate(hidden):
+            w, b = self._layer("actor", i)
+            first = i == 0
+            K.gemm(self.b_obs if first else self.h_pair[i - 1], w, self.h_pair[i], m=rows, n=width, k=widths[i],
+                   batch=2, a_kcontig=True, b_kcontig=True, lda=self.obs_ld if first else widths[i], ldb=widths[i],
+                   ldd=width, stride_a=0 if first else rows * widths[i], stride_b=self.w_stride[i],
+                   stride_d=rows * width, bias=b, stride_bias=self.b_stride[i], epilogue="elu", mode=K.FP32)
+        last = self.layers - 1
+        for member, (prefix, out) in enumerate((("actor", self.mean), ("critic", self.value))):
+            w, b = self._layer(prefix, last)
+            h = self.h_pair[-1][member] if hidden else self.b_obs
+            K.linear_forward(h, w, out, rows=rows, in_dim=widths[-1], out_dim=out.shape[1], bias=b, mode=K.FP32,
+                             x_ld=None if hidden else self.obs_ld)
+
+    def _joint_backward(self, rows):
+        """Weight, bias and input gradients of both MLPs: the output layers one network at a time,
+        the hidden layers as batch-2 products (the ELU backward of the layer below fused into each
+        input-gradient epilogue; bias gradients as row sums of the weight-gradient products)."""
+        hidden = self.config.hidden_dims
+        widths = (self.observation_dim, *hidden)
         g = self.grads
-        d = dout
-        out_dim = dout.shape[1]
-        for i in reversed(range(self.layers)):
-            w, _ = self._layer(prefix, i)
-            inputs = x if i == 0 else hidden[i - 1]
-            # weight gradient; the bias gradient (row sums of d^T) comes from the same product
-            K.linear_backward_weight(d, inputs, g[f"{prefix}.{i}.weight"], rows=rows, in_dim=widths[i],
-                                     out_dim=out_dim, mode=K.FP32, workspace=self.workspace,
-                                     x_ld=x_ld if i == 0 else None, bias_grad=g[f"{prefix}.{i}.bias"])
-            if i > 0:
-                # input gradient with the ELU backward of the layer below fused in
-                K.linear_backward_input(d, w, dbufs[i], rows=rows, in_dim=widths[i], out_dim=out_dim, mode=K.FP32,
-                                        c=hidden[i - 1], epilogue="elu_grad")
-                d = dbufs[i]
-                out_dim = widths[i]
+        last = self.layers - 1
+        for member, (prefix, dout) in enumerate((("actor", self.dmean), ("critic", self.dvalue))):
+            w, _ = self._layer(prefix, last)
+            h = self.h_pair[last - 1][member] if last > 0 else self.b_obs
+            K.linear_backward_weight(dout, h, g[f"{prefix}.{last}.weight"], rows=rows, in_dim=widths[-1],
+                                     out_dim=dout.shape[1], mode=K.FP32, workspace=self.workspace,
+                                     x_ld=None if last > 0 else self.obs_ld, bias_grad=g[f"{prefix}.{last}.bias"])
+            if last > 0:
+                K.linear_backward_input(dout, w, self.d_pair[last][member], rows=rows, in_dim=widths[-1],
+                                        out_dim=dout.shape[1], mode=K.FP32, c=h, epilogue="elu_grad")
+        for i in reversed(range(last)):
+            out_dim, in_dim = hidden[i], widths[i]
+            d = self.d_pair[i + 1]
+            first = i == 0
+            inputs = self.b_obs if first else self.h_pair[i - 1]
+            splits = K.split_count(out_dim, in_dim, rows, 2, K.FP32)
+            if splits > 1 and _native.load().rl_gemm_workspace(K.FP32, out_dim, in_dim, rows, 2, splits) > \
+                    self.workspace.numel():
+                splits = 1
+            K.gemm(d, inputs, g[f"actor.{i}.weight"], m=out_dim, n=in_dim, k=rows, batch=2, a_kcontig=False,
+                   b_kcontig=False, lda=out_dim, ldb=self.obs_ld if first else in_dim, ldd=in_dim,
+                   stride_a=rows * out_dim, stride_b=0 if first else rows * in_dim, stride_d=self.w_stride[i],
+                   mode=K.FP32, splits=splits, workspace=self.workspace if splits > 1 else None,
+                   a_sums=g[f"actor.{i}.bias"], stride_bias=self.b_stride[i])
+            if not first:
+                w, _ = self._layer("actor", i)
+                K.gemm(d, w, self.d_pair[i], m=rows, n=in_dim, k=out_dim, batch=2, a_kcontig=True, b_kcontig=False,
+                       lda=out_dim, ldb=in_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=self.w_stride[i],
+                       stride_d=rows * in_dim, mode=K.FP32, c=self.h_pair[i - 1], epilogue="elu_grad")
 
     # ------------------------------------------------------------------
     def compute_returns(self) -> None:
@@ -215,13 +261,12 @@ class WarpPPO:
                      self.stds.data_ptr(), self.b_obs.data_ptr(), self.b_actions.data_ptr(),
                      self.b_log_probs.data_ptr(), self.b_values.data_ptr(), self.b_advantages.data_ptr(),
                      self.b_returns.data_ptr(), self.b_means.data_ptr(), self.b_stds.data_ptr(), K.stream())
-        self._mlp_forward("actor", self.b_obs, M, self.actor_h, self.mean, x_ld=self.obs_ld)
+        self._joint_forward(M)
         std_type = int(cfg.std_type == "scalar")
         _native.call("rl_ppo_kl_adapt", self.mean.data_ptr(), A, self.distribution_parameter.data_ptr(),
                      self.b_means.data_ptr(), self.b_stds.data_ptr(), M, A, std_type, float(cfg.std_range[0]),
                      float(cfg.std_range[1]), float(cfg.desired_kl), int(cfg.schedule == "adaptive"),
                      self.partial.data_ptr(), self.kl.data_ptr(), self.lr.data_ptr(), K.stream())
-        self._mlp_forward("critic", self.b_obs, M, self.critic_h, self.value, x_ld=self.obs_ld)
         _native.call("rl_ppo_loss", self.mean.data_ptr(), A, self.value.data_ptr(),
                      self.distribution_parameter.data_ptr(), self.b_actions.data_ptr(), self.b_log_probs.data_ptr(),
                      self.b_values.data_ptr(), self.b_advantages.data_ptr(), self.b_returns.data_ptr(), M, A, std_type,
@@ -230,8 +275,7 @@ class WarpPPO:
                      int(cfg.clip_value), self.dmean.data_ptr(), self.dvalue.data_ptr(), self.dstd_rows.data_ptr(),
                      self.row_terms.data_ptr(), self.totals.data_ptr(), K.stream())
         K.bias_grad(self.dstd_rows, self.grads["std"], self.partial, rows=M, channels=A)
-        self._mlp_backward("actor", self.b_obs, M, self.actor_h, self.dmean, self.actor_d, x_ld=self.obs_ld)
-        self._mlp_backward("critic", self.b_obs, M, self.critic_h, self.dvalue, self.critic_d, x_ld=self.obs_ld)
+        self._joint_backward(M)
         for (start, end), norm in zip(self.group_ranges, self.group_norms):
             grad = self.flat.grad[start:end]
             _native.call("rl_sum_squares", grad.data_ptr(), grad.numel(), self.norm_partial.data_ptr(),
