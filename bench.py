@@ -13,8 +13,9 @@ Prints ONE JSON line: value = FlashSAC updates/sec on the GPU, with
   update_roofline  two-term serial roofline of the whole update,
   cpu_baseline  the CPU oracle (PyTorch-CPU restatement of the reference update,
                 fp32) timed on this host's cores on one update of the same shape,
-  ppo           PPO update ms at configs[3] (one captured graph per update, fp32
-                MFMA roofline, CPU oracle on one epoch scaled to five),
+  ppo           PPO update ms at configs[3] (one captured graph per update;
+                fp32-accurate products on the bf16 matrix cores, roofline at
+                the bf16 peak / 6; CPU oracle on one epoch scaled to five),
   kernel_sweep  configs[4]: fused categorical target + CE, fused optimizer and
                 RMSNorm at their sweep shapes against the HBM roofline, plus the
                 replay ingest (n-step commit), return statistics and act()
@@ -218,6 +219,7 @@ def bench_ppo(steps: int, warmup: int, with_cpu: bool) -> dict:
     """PPO update ms at c3: one captured graph (GAE, permutation, 5 epochs x 4 minibatches) per update."""
     import torch
 
+    from robolearn_amd import kernels as K
     from robolearn_amd.ppo import WarpPPO
 
     cfg = ppo_config()
@@ -237,6 +239,9 @@ def bench_ppo(steps: int, warmup: int, with_cpu: bool) -> dict:
     ms = start.elapsed_time(end) / steps
     flops = ppo_flops(cfg)
     achieved = flops / (ms * 1e-3) / 1e12
+    split = agent.gemm_mode == K.FP32_SPLIT
+    # fp32-accurate products on the bf16 matrix cores cost six bf16 products per fp32 product
+    peak = BF16_PEAK_TFLOPS / 6.0 if split else FP32_PEAK_TFLOPS
     result = {
         "metric": "PPO update ms", "value": round(ms, 4), "unit": "ms/update", "higher_is_better": False,
         "dtype": "fp32", "steps": steps, "warmup": warmup,
@@ -244,8 +249,10 @@ def bench_ppo(steps: int, warmup: int, with_cpu: bool) -> dict:
                    "obs_dim": PPO_C3["obs"], "act_dim": PPO_C3["act"], "hidden": list(cfg.hidden_dims),
                    "activation": cfg.activation, "epochs": cfg.epochs, "minibatches": cfg.num_mini_batches,
                    "schedule": cfg.schedule, "desired_kl": cfg.desired_kl},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "flops_per_update": flops},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
+                     "frac": round(achieved / peak, 4), "flops_per_update": flops,
+                     "products": ("fp32-accurate: three-piece bf16 splits, 6 bf16 MFMA products per fp32 product; "
+                                  "peak = bf16 dense peak / 6") if split else "v_mfma_f32_32x32x2_f32"},
         "cpu_baseline": None,
     }
     if with_cpu:

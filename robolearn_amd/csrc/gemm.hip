@@ -17,6 +17,17 @@
 // staged through LDS in [row][k] order, 16 K per step, so each lane reads its
 // K-slice with two 16-byte LDS loads; the K order inside a step is permuted
 // identically for both operands, which leaves the dot products unchanged.
+//
+// Mode 2 runs the same products on the bf16 matrix cores at fp32 accuracy:
+// every operand value x is split exactly into three bf16 pieces
+// x = x0 + x1 + x2 (x0 = bf16(x), x1 = bf16(x - x0), x2 = bf16(x - x0 - x1),
+// each difference exact in fp32) when the tile is staged in LDS, and each 16-K
+// step issues six v_mfma_f32_32x32x16_bf16 for a0b0 + a0b1 + a1b0 + a0b2 + a1b1
+// + a2b0.  The pieces carry 3 x 8 significant bits and the three dropped
+// cross terms are below 2^-26 of the product, so a product is as accurate as
+// an fp32 one; the matrix-core time per 16-K step is 6 x 32 cycles instead of
+// 8 x 64 (v_mfma_f32_32x32x2_f32).  Staging, tiles and epilogues are shared
+// with mode 0.
 #include "gemm.hpp"
 
 #include <cmath>
@@ -27,6 +38,19 @@ namespace gemm {
 
 constexpr int kFp32K = 16;              // K per LDS step
 constexpr int kFp32Pitch = kFp32K + 4;  // floats per LDS row
+constexpr int kSplitPitch = kFp32K + 8; // bf16 per LDS row of a split plane (48 bytes: 16-lane reads hit distinct banks)
+
+// x = x0 + x1 + x2 in bf16 pieces (round to nearest even at each step; both
+// differences are exact in fp32).
+__device__ __forceinline__ void split3(float x, unsigned short& h0, unsigned short& h1, unsigned short& h2) {
+    const __bf16 b0 = static_cast<__bf16>(x);
+    const float r1 = x - static_cast<float>(b0);
+    const __bf16 b1 = static_cast<__bf16>(r1);
+    const float r2 = r1 - static_cast<float>(b1);
+    h0 = __builtin_bit_cast(unsigned short, b0);
+    h1 = __builtin_bit_cast(unsigned short, b1);
+    h2 = __builtin_bit_cast(unsigned short, static_cast<__bf16>(r2));
+}
 
 // Loads one Rows x 16 operand tile into registers and later stores it to LDS.
 // Element (r, k) of the operand is src[r * ld + k] when KContig, else
@@ -88,20 +112,76 @@ struct TileLoader {
             for (int e = 0; e < KPer; ++e) q[e] = regs[e];
         }
     }
+
+    // Mode 2: the three bf16 planes of the tile, plane p at lds + p * Rows * kSplitPitch.
+    __device__ __forceinline__ void store_split(unsigned short* lds) const {
+        constexpr int Plane = Rows * kSplitPitch;
+        const int t = threadIdx.x;
+        if constexpr (KContig) {
+#pragma unroll
+            for (int i = 0; i < PerThread; ++i) {
+                const int v = i * kThreads + t;
+                const int offset = (v / VecPerRow) * kSplitPitch + (v % VecPerRow) * 4;
+                unsigned short h[3][4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) split3(regs[i * 4 + e], h[0][e], h[1][e], h[2][e]);
+#pragma unroll
+                for (int q = 0; q < 3; ++q)
+                    *reinterpret_cast<uint2*>(lds + q * Plane + offset) =
+                        make_uint2(h[q][0] | (static_cast<unsigned int>(h[q][1]) << 16),
+                                   h[q][2] | (static_cast<unsigned int>(h[q][3]) << 16));
+            }
+        } else {
+            const int offset = (t % Rows) * kSplitPitch + (t / Rows) * KPer;
+#pragma unroll
+            for (int e = 0; e < KPer; ++e) {
+                unsigned short h0, h1, h2;
+                split3(regs[e], h0, h1, h2);
+                lds[offset + e] = h0;
+                lds[Plane + offset + e] = h1;
+                lds[2 * Plane + offset + e] = h2;
+            }
+        }
+    }
+
+    // Sum of this thread's staged values (row sums of an M-contiguous operand).
+    __device__ __forceinline__ float sum() const {
+        float total = 0.0f;
+#pragma unroll
+        for (int e = 0; e < Count; ++e) total += regs[e];
+        return total;
+    }
 };
 
-template <int T, bool AK, bool BK>
+template <int T, bool AK, bool BK, bool Split>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
     constexpr int WB = T / 64;  // 32x32 accumulator blocks per wave and dimension
-    __shared__ __attribute__((aligned(16))) float sa[T * kFp32Pitch];
-    __shared__ __attribute__((aligned(16))) float sb[T * kFp32Pitch];
+    constexpr int Plane = T * kSplitPitch;  // bf16 per split plane
+    constexpr int StageBytes = Split ? 3 * Plane * 2 : T * kFp32Pitch * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char sa_raw[StageBytes];
+    __shared__ __attribute__((aligned(16))) unsigned char sb_raw[StageBytes];
+    float* sa = reinterpret_cast<float*>(sa_raw);
+    float* sb = reinterpret_cast<float*>(sb_raw);
+    unsigned short* ha = reinterpret_cast<unsigned short*>(sa_raw);
+    unsigned short* hb = reinterpret_cast<unsigned short*>(sb_raw);
 
-    const int split = static_cast<int>(blockIdx.z) % p.splits;
-    const int batch = static_cast<int>(blockIdx.z) / p.splits;
+    // XCD-aware tile order: workgroups are dispatched round-robin over the 8
+    // XCDs in linear (x fastest) order, so logical tile id (w % 8) * (G / 8) +
+    // w / 8 gives each XCD a contiguous range of tiles; the N tiles of one M
+    // panel then share that XCD's L2 instead of fetching the panel once per XCD.
+    const unsigned nx = gridDim.x, ny = gridDim.y;
+    const unsigned groups = nx * ny * gridDim.z;
+    unsigned w = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+    if (groups % 8 == 0) w = (w % 8) * (groups / 8) + w / 8;
+    const int bx = static_cast<int>(w % nx);
+    const int by = static_cast<int>((w / nx) % ny);
+    const int bz = static_cast<int>(w / (nx * ny));
+    const int split = bz % p.splits;
+    const int batch = bz / p.splits;
     const float* A = static_cast<const float*>(p.a) + batch * p.stride_a;
     const float* B = static_cast<const float*>(p.b) + batch * p.stride_b;
-    const int m0 = static_cast<int>(blockIdx.y) * T;
-    const int n0 = static_cast<int>(blockIdx.x) * T;
+    const int m0 = by * T;
+    const int n0 = bx * T;
     const int k_begin = split * p.k_per_split;
     const int k_end = min(p.k, k_begin + p.k_per_split);
 
@@ -127,15 +207,27 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
     // kFp32K * T / 256 staged values of row t / (256 / T) per step.
     constexpr int SumLanes = kThreads / T;
     constexpr int SumPer = kFp32K / SumLanes;
-    const bool row_sums = p.a_sums != nullptr && blockIdx.x == 0;
+    const bool row_sums = p.a_sums != nullptr && bx == 0;
     float a_sum = 0.0f;
 
     // B is indexed (n, k) when BK else (k, n); the loader wants (row=n, k).
+    // Mode 2 takes the row sums from the staged fp32 registers (M-contiguous A only).
+    const auto stage = [&]() {
+        if constexpr (Split) {
+            la.store_split(ha);
+            lb.store_split(hb);
+            if constexpr (!AK) {
+                if (row_sums) a_sum += la.sum();
+            }
+        } else {
+            la.store(sa);
+            lb.store(sb);
+        }
+    };
     if (k_begin < k_end) {
         la.load(A, p.lda, m0, k_begin, p.m, k_end, avec);
         lb.load(B, p.ldb, n0, k_begin, p.n, k_end, bvec);
-        la.store(sa);
-        lb.store(sb);
+        stage();
     }
     __syncthreads();
 
@@ -144,6 +236,40 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
         if (more) {
             la.load(A, p.lda, m0, k0 + kFp32K, p.m, k_end, avec);
             lb.load(B, p.ldb, n0, k0 + kFp32K, p.n, k_end, bvec);
+        }
+        if constexpr (Split) {
+            bf16x8_t af[WB][3], bf[WB][3];
+            const int koff = 8 * (lane / 32);
+#pragma unroll
+            for (int i = 0; i < WB; ++i) {
+                const int off = (wm * (T / 2) + i * 32 + lane % 32) * kSplitPitch + koff;
+#pragma unroll
+                for (int q = 0; q < 3; ++q) af[i][q] = *reinterpret_cast<const bf16x8_t*>(ha + q * Plane + off);
+            }
+#pragma unroll
+            for (int j = 0; j < WB; ++j) {
+                const int off = (wn * (T / 2) + j * 32 + lane % 32) * kSplitPitch + koff;
+#pragma unroll
+                for (int q = 0; q < 3; ++q) bf[j][q] = *reinterpret_cast<const bf16x8_t*>(hb + q * Plane + off);
+            }
+#pragma unroll
+            for (int i = 0; i < WB; ++i) {
+#pragma unroll
+                for (int j = 0; j < WB; ++j) {
+                    f32x16_t c = acc[i][j];
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][0], bf[j][0], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][0], bf[j][1], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][1], bf[j][0], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][0], bf[j][2], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][1], bf[j][1], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][2], bf[j][0], c, 0, 0, 0);
+                    acc[i][j] = c;
+                }
+            }
+            __syncthreads();
+            if (more) stage();
+            __syncthreads();
+            continue;
         }
         float4 af[WB][2], bfr[WB][2];
 #pragma unroll
@@ -176,14 +302,26 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
             }
         }
         __syncthreads();
-        if (more) {
-            la.store(sa);
-            lb.store(sb);
-        }
+        if (more) stage();
         __syncthreads();
     }
 
-    if (row_sums) {
+    if (Split && !AK && row_sums) {
+        // thread t holds the partial sum of row t % T over its k group t / T: add the groups in order
+        float* part = sa;
+        part[threadIdx.x] = a_sum;
+        __syncthreads();
+        const int t = static_cast<int>(threadIdx.x);
+        if (t < T) {
+            float total = part[t];
+#pragma unroll
+            for (int g = 1; g < kThreads / T; ++g) total += part[g * T + t];
+            const int r = m0 + t;
+            if (r < p.m)
+                p.a_sums[(p.splits == 1 ? batch * p.sums_stride
+                                         : (static_cast<long long>(split) * p.batch + batch) * p.m) + r] = total;
+        }
+    } else if (row_sums) {
         // the SumLanes partial sums of a row sit in adjacent lanes: fixed-order butterfly
 #pragma unroll
         for (int offset = 1; offset < SumLanes; offset <<= 1) a_sum += __shfl_xor(a_sum, offset);
@@ -306,23 +444,30 @@ int fp32_tile(const Params& p) {
     return big >= 2048 ? 128 : 64;
 }
 
-template <int T, bool AK, bool BK>
+template <int T, bool AK, bool BK, bool Split>
 void launch_fp32_tiled(const Params& p, hipStream_t stream) {
     const dim3 grid(ceil_div(p.n, T), ceil_div(p.m, T), static_cast<unsigned>(p.batch * p.splits));
-    hipLaunchKernelGGL((gemm_kernel<T, AK, BK>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((gemm_kernel<T, AK, BK, Split>), grid, dim3(kThreads), 0, stream, p);
 }
 
-template <bool AK, bool BK>
+template <bool AK, bool BK, bool Split>
 void launch_fp32_layout(const Params& p, hipStream_t stream) {
-    if (fp32_tile(p) == 128) launch_fp32_tiled<128, AK, BK>(p, stream);
-    else launch_fp32_tiled<64, AK, BK>(p, stream);
+    if (fp32_tile(p) == 128) launch_fp32_tiled<128, AK, BK, Split>(p, stream);
+    else launch_fp32_tiled<64, AK, BK, Split>(p, stream);
 }
 
-void launch_fp32(const Params& p, bool ak, bool bk, hipStream_t stream) {
-    if (ak && bk) launch_fp32_layout<true, true>(p, stream);
-    else if (ak && !bk) launch_fp32_layout<true, false>(p, stream);
-    else if (!ak && bk) launch_fp32_layout<false, true>(p, stream);
-    else launch_fp32_layout<false, false>(p, stream);
+template <bool Split>
+void launch_fp32_mode(const Params& p, bool ak, bool bk, hipStream_t stream) {
+    if (ak && bk) launch_fp32_layout<true, true, Split>(p, stream);
+    else if (ak && !bk) launch_fp32_layout<true, false, Split>(p, stream);
+    else if (!ak && bk) launch_fp32_layout<false, true, Split>(p, stream);
+    else launch_fp32_layout<false, false, Split>(p, stream);
+}
+
+// split: mode 2 (three-piece bf16 products); row sums of a K-contiguous A stay on mode 0
+void launch_fp32(const Params& p, bool ak, bool bk, bool split, hipStream_t stream) {
+    if (split && !(p.a_sums && ak)) launch_fp32_mode<true>(p, ak, bk, stream);
+    else launch_fp32_mode<false>(p, ak, bk, stream);
 }
 
 // dst[b][c][r] = src[b][r][c] for 16-bit elements: 64 x 64 tiles through LDS,
@@ -358,17 +503,17 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
              const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
              float beta, int epilogue, int splits, float* workspace, std::size_t workspace_bytes, hipStream_t stream,
              unsigned short* d_bf16, float* moments, float* a_sums) {
-    require(mode == 0 || mode == 1, "GEMM mode must be 0 (fp32) or 1 (bf16 operands).");
-    require(!(mode == 0 && (a_bf16 || b_bf16)), "fp32 GEMM mode requires fp32 operands.");
+    require(mode >= 0 && mode <= 2, "GEMM mode must be 0 (fp32), 1 (bf16 operands) or 2 (fp32 on bf16 pieces).");
+    require(!(mode != 1 && (a_bf16 || b_bf16)), "fp32 GEMM modes require fp32 operands.");
     require(m > 0 && n > 0 && k > 0 && batch > 0, "GEMM dimensions must be positive.");
     require(a && b && d, "GEMM operands must be nonnull.");
     require(std::isfinite(beta) && (beta == 0.0f || c), "Nonzero beta requires C; beta must be finite.");
     require(epilogue >= 0 && epilogue <= 3, "Unknown GEMM epilogue.");
-    require(epilogue != 3 || (mode == 0 && c && beta == 0.0f && !bias),
+    require(epilogue != 3 || (mode != 1 && c && beta == 0.0f && !bias),
             "The ELU-gradient epilogue needs fp32 mode, the ELU outputs as C, beta 0 and no bias.");
     require(splits >= 1, "GEMM split count must be positive.");
     require(static_cast<long long>(m) * n <= std::numeric_limits<int>::max(), "GEMM output exceeds 2^31 elements.");
-    require(!a_sums || (mode == 0 && !bias), "Row sums of A are produced by the fp32 GEMM family, without a bias.");
+    require(!a_sums || (mode != 1 && !bias), "Row sums of A are produced by the fp32 GEMM family, without a bias.");
     // the row sums take the bias layout: member e at a_sums + e * stride_bias (m when stride_bias is 0)
     const long long sums_stride = stride_bias > 0 ? stride_bias : m;
     require(!moments || (ldd == n && aligned(moments, 16)),
@@ -427,7 +572,7 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     const bool fused_moments = moments && mode == 1 && splits == 1 && !bias && epilogue == 0 && beta == 0.0f &&
                                gemm::big_eligible(p, a_bf16, b_bf16);
     p.moments = fused_moments ? moments : nullptr;
-    if (mode == 0) gemm::launch_fp32(p, a_kcontig != 0, b_kcontig != 0, stream);
+    if (mode != 1) gemm::launch_fp32(p, a_kcontig != 0, b_kcontig != 0, mode == 2, stream);
     else gemm::launch_bf16(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
     check_launch("Launch GEMM");
     if (splits > 1) {

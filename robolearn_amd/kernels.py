@@ -11,6 +11,9 @@ from . import _native
 
 FP32 = 0
 BF16 = 1
+# fp32 operands and results with the products formed on the bf16 matrix cores from exact
+# three-piece bf16 splits of every operand value (fp32-accurate)
+FP32_SPLIT = 2
 EPILOGUES = {None: 0, "relu": 1, "elu": 2, "elu_grad": 3}
 
 
@@ -137,7 +140,7 @@ def linear_backward_weight(dy, x, dw, *, rows, in_dim, out_dim, ensemble=1, x_st
     x_ld: row pitch of x (default in_dim).  bias_grad (fp32 mode): receives sum_rows dy[e]
     from the same product (overwritten)."""
     if bias_grad is not None:
-        if mode != FP32:
+        if mode == BF16:
             raise ValueError("The fused bias gradient needs the fp32 GEMM family.")
         _check(bias_grad, ensemble * out_dim, "bias gradient")
     x_ld = x_ld or in_dim

@@ -35,7 +35,12 @@ class WarpPPO:
     """PPO learner with the reference's WarpPPO interface, backed by HIP kernels."""
 
     def __init__(self, observation_dim: int, action_dim: int, num_envs: int, horizon: int,
-                 config: PPOConfig | None = None, device: str = "cuda"):
+                 config: PPOConfig | None = None, device: str = "cuda", gemm_mode: int = K.FP32_SPLIT):
+        """gemm_mode: K.FP32_SPLIT (default; fp32-accurate products on the bf16 matrix cores from
+        exact three-piece splits) or K.FP32 (the fp32 matrix-core instruction)."""
+        if gemm_mode not in (K.FP32, K.FP32_SPLIT):
+            raise ValueError("gemm_mode must be K.FP32 or K.FP32_SPLIT.")
+        self.gemm_mode = gemm_mode
         self.config = cfg = config or PPOConfig()
         if min(observation_dim, action_dim, num_envs, horizon, cfg.epochs, *cfg.hidden_dims) < 1:
             raise ValueError("Dimensions, horizon, and epochs must be positive.")
@@ -179,10 +184,10 @@ class WarpPPO:
         for i, width in enumerate(self.config.hidden_dims):
             w, b = self._layer(prefix, i)
             K.linear_forward(inputs, w, hidden[i], rows=rows, in_dim=widths[i], out_dim=width, bias=b,
-                             epilogue="elu", mode=K.FP32, x_ld=x_ld if i == 0 else None)
+                             epilogue="elu", mode=self.gemm_mode, x_ld=x_ld if i == 0 else None)
             inputs = hidden[i]
         w, b = self._layer(prefix, self.layers - 1)
-        K.linear_forward(inputs, w, out, rows=rows, in_dim=widths[-1], out_dim=out.shape[1], bias=b, mode=K.FP32)
+        K.linear_forward(inputs, w, out, rows=rows, in_dim=widths[-1], out_dim=out.shape[1], bias=b, mode=self.gemm_mode)
 
     def _joint_forward(self, rows):
         """Both MLPs on the minibatch observations: each hidden layer is one batch-2 product over
@@ -196,12 +201,12 @@ class WarpPPO:
             K.gemm(self.b_obs if first else self.h_pair[i - 1], w, self.h_pair[i], m=rows, n=width, k=widths[i],
                    batch=2, a_kcontig=True, b_kcontig=True, lda=self.obs_ld if first else widths[i], ldb=widths[i],
                    ldd=width, stride_a=0 if first else rows * widths[i], stride_b=self.w_stride[i],
-                   stride_d=rows * width, bias=b, stride_bias=self.b_stride[i], epilogue="elu", mode=K.FP32)
+                   stride_d=rows * width, bias=b, stride_bias=self.b_stride[i], epilogue="elu", mode=self.gemm_mode)
         last = self.layers - 1
         for member, (prefix, out) in enumerate((("actor", self.mean), ("critic", self.value))):
             w, b = self._layer(prefix, last)
             h = self.h_pair[-1][member] if hidden else self.b_obs
-            K.linear_forward(h, w, out, rows=rows, in_dim=widths[-1], out_dim=out.shape[1], bias=b, mode=K.FP32,
+            K.linear_forward(h, w, out, rows=rows, in_dim=widths[-1], out_dim=out.shape[1], bias=b, mode=self.gemm_mode,
                              x_ld=None if hidden else self.obs_ld)
 
     def _joint_backward(self, rows):
@@ -216,30 +221,30 @@ class WarpPPO:
             w, _ = self._layer(prefix, last)
             h = self.h_pair[last - 1][member] if last > 0 else self.b_obs
             K.linear_backward_weight(dout, h, g[f"{prefix}.{last}.weight"], rows=rows, in_dim=widths[-1],
-                                     out_dim=dout.shape[1], mode=K.FP32, workspace=self.workspace,
+                                     out_dim=dout.shape[1], mode=self.gemm_mode, workspace=self.workspace,
                                      x_ld=None if last > 0 else self.obs_ld, bias_grad=g[f"{prefix}.{last}.bias"])
             if last > 0:
                 K.linear_backward_input(dout, w, self.d_pair[last][member], rows=rows, in_dim=widths[-1],
-                                        out_dim=dout.shape[1], mode=K.FP32, c=h, epilogue="elu_grad")
+                                        out_dim=dout.shape[1], mode=self.gemm_mode, c=h, epilogue="elu_grad")
         for i in reversed(range(last)):
             out_dim, in_dim = hidden[i], widths[i]
             d = self.d_pair[i + 1]
             first = i == 0
             inputs = self.b_obs if first else self.h_pair[i - 1]
-            splits = K.split_count(out_dim, in_dim, rows, 2, K.FP32)
-            if splits > 1 and _native.load().rl_gemm_workspace(K.FP32, out_dim, in_dim, rows, 2, splits) > \
+            splits = K.split_count(out_dim, in_dim, rows, 2, self.gemm_mode)
+            if splits > 1 and _native.load().rl_gemm_workspace(self.gemm_mode, out_dim, in_dim, rows, 2, splits) > \
                     self.workspace.numel():
                 splits = 1
             K.gemm(d, inputs, g[f"actor.{i}.weight"], m=out_dim, n=in_dim, k=rows, batch=2, a_kcontig=False,
                    b_kcontig=False, lda=out_dim, ldb=self.obs_ld if first else in_dim, ldd=in_dim,
                    stride_a=rows * out_dim, stride_b=0 if first else rows * in_dim, stride_d=self.w_stride[i],
-                   mode=K.FP32, splits=splits, workspace=self.workspace if splits > 1 else None,
+                   mode=self.gemm_mode, splits=splits, workspace=self.workspace if splits > 1 else None,
                    a_sums=g[f"actor.{i}.bias"], stride_bias=self.b_stride[i])
             if not first:
                 w, _ = self._layer("actor", i)
                 K.gemm(d, w, self.d_pair[i], m=rows, n=in_dim, k=out_dim, batch=2, a_kcontig=True, b_kcontig=False,
                        lda=out_dim, ldb=in_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=self.w_stride[i],
-                       stride_d=rows * in_dim, mode=K.FP32, c=self.h_pair[i - 1], epilogue="elu_grad")
+                       stride_d=rows * in_dim, mode=self.gemm_mode, c=self.h_pair[i - 1], epilogue="elu_grad")
 
     # ------------------------------------------------------------------
     def compute_returns(self) -> None:

@@ -369,3 +369,60 @@ def test_fp32_weight_gradient_with_fused_bias_gradient(gpu, rows, in_dim, out_di
     torch.cuda.synchronize()
     torch.testing.assert_close(dw.cpu().double(), dy.double().t() @ x.double(), rtol=1e-4, atol=1e-4 * math.sqrt(rows))
     torch.testing.assert_close(db.cpu().double(), dy.double().sum(0), rtol=1e-4, atol=1e-4 * math.sqrt(rows))
+
+
+SPLIT_SHAPES = [(1, 5, 7, 3), (2, 130, 129, 40), (2, 257, 96, 160), (1, 300, 37, 123), (2, 2048, 512, 256)]
+
+
+@pytest.mark.parametrize("batch,rows,out_dim,in_dim", SPLIT_SHAPES)
+def test_fp32_split_products_are_fp32_accurate(gpu, batch, rows, out_dim, in_dim):
+    """Mode 2 (products on the bf16 matrix cores from exact three-piece splits) against float64,
+    with the same error budget as the fp32 matrix-core path (mode 0) on the same inputs: forward
+    with bias + ELU, input gradient with the ELU-gradient epilogue, weight gradient with the
+    bias-gradient row sums, direct and split over K."""
+    print(f"case fp32 split batch={batch} rows={rows} out={out_dim} in={in_dim}", flush=True)
+    x = _rand(batch, rows, in_dim, seed=21)
+    w = _rand(batch, out_dim, in_dim, seed=22, scale=0.2)
+    dy = _rand(batch, rows, out_dim, seed=23)
+    bias = _rand(batch, out_dim, seed=24)
+    xd, wd, dyd, bd = (t.to(gpu) for t in (x, w, dy, bias))
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=gpu)
+    x64, w64, dy64 = x.double(), w.double(), dy.double()
+    ref_y = torch.nn.functional.elu(torch.einsum("bri,boi->bro", x64, w64) + bias.double()[:, None, :])
+    ref_dx = torch.einsum("bro,boi->bri", dy64, w64)
+    c = ref_y.float()  # ELU outputs of the layer below, for the ELU-gradient epilogue of a [rows, out] product
+    c64 = c.double()
+    elu_grad = torch.where(c64 > 0, torch.ones_like(c64), c64 + 1)
+    ref_dw = torch.einsum("bro,bri->boi", dy64, x64)
+    ref_db = dy64.sum(1)
+
+    def run(mode):
+        y = torch.empty(batch, rows, out_dim, device=gpu)
+        K.linear_forward(xd, wd, y, rows=rows, in_dim=in_dim, out_dim=out_dim, ensemble=batch, bias=bd,
+                         epilogue="elu", mode=mode)
+        # [rows, out] input-gradient-shaped product dy' = x' w'^T with the ELU-gradient epilogue
+        g = torch.empty(batch, rows, out_dim, device=gpu)
+        K.gemm(xd, wd, g, m=rows, n=out_dim, k=in_dim, batch=batch, a_kcontig=True, b_kcontig=True, lda=in_dim,
+               ldb=in_dim, ldd=out_dim, stride_a=rows * in_dim, stride_b=out_dim * in_dim, stride_d=rows * out_dim,
+               c=c.to(gpu), epilogue="elu_grad", mode=mode)
+        dx = torch.empty(batch, rows, in_dim, device=gpu)
+        K.linear_backward_input(dyd, wd, dx, rows=rows, in_dim=in_dim, out_dim=out_dim, ensemble=batch, mode=mode)
+        out = {"y": y, "g": g, "dx": dx}
+        for label, workspace in (("direct", None), ("split", ws)):
+            dw = torch.empty(batch, out_dim, in_dim, device=gpu)
+            db = torch.empty(batch, out_dim, device=gpu)
+            K.linear_backward_weight(dyd, xd, dw, rows=rows, in_dim=in_dim, out_dim=out_dim, ensemble=batch, mode=mode,
+                                     workspace=workspace, bias_grad=db)
+            out[f"dw_{label}"], out[f"db_{label}"] = dw, db
+        torch.cuda.synchronize()
+        return {k: v.cpu().double() for k, v in out.items()}
+
+    native, split = run(K.FP32), run(K.FP32_SPLIT)
+    refs = {"y": ref_y, "g": torch.einsum("bri,boi->bro", x64, w64) * elu_grad, "dx": ref_dx,
+            "dw_direct": ref_dw, "db_direct": ref_db, "dw_split": ref_dw, "db_split": ref_db}
+    for key, ref in refs.items():
+        scale = ref.abs().max().item() + 1e-30
+        err_native = (native[key] - ref).abs().max().item()
+        err_split = (split[key] - ref).abs().max().item()
+        assert err_split <= 4.0 * err_native + 2e-7 * scale, (key, err_split, err_native, scale)
+        assert err_split <= 2e-6 * scale, (key, err_split, scale)
