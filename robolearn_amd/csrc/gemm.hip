@@ -398,16 +398,21 @@ __global__ void splitk_reduce(const float* work, float* d, unsigned short* d_bf1
 // Same reduction for many splits: a workgroup covers kReduceCols consecutive
 // outputs with kReduceGroups threads each; group g adds splits g, g + G, ...
 // in order and group 0 adds the group sums in order, so the result is fixed
-// and each thread's chain is splits / G loads long.
+// and each thread's chain is splits / G loads long.  With sums != nullptr the
+// index space continues past D with the batch * m row sums of A
+// ([splits][batch][m] partials in sums_work), written at b * sums_stride + r.
 constexpr int kReduceGroups = 8;
 constexpr int kReduceCols = 256 / kReduceGroups;
 
 __global__ __launch_bounds__(256) void splitk_reduce_grouped(const float* work, float* d, unsigned short* d_bf16,
                                                              const float* c, const float* bias, long long ldd,
                                                              long long stride_d, long long stride_bias, int m, int n,
-                                                             int batch, int splits, float beta, int epilogue) {
+                                                             int batch, int splits, float beta, int epilogue,
+                                                             const float* sums_work = nullptr, float* sums = nullptr,
+                                                             long long sums_stride = 0) {
     __shared__ float part[kReduceGroups][kReduceCols];
     const long long total = static_cast<long long>(batch) * m * n;
+    const long long extra = sums ? static_cast<long long>(batch) * m : 0;
     const int e = threadIdx.x % kReduceCols;
     const int g = threadIdx.x / kReduceCols;
     const long long idx = static_cast<long long>(blockIdx.x) * kReduceCols + e;
@@ -417,11 +422,19 @@ __global__ __launch_bounds__(256) void splitk_reduce_grouped(const float* work, 
         const int b = static_cast<int>(idx / plane);
         const long long within = idx - b * plane;
         for (int s = g; s < splits; s += kReduceGroups) value += work[(static_cast<long long>(s) * batch + b) * plane + within];
+    } else if (idx < total + extra) {
+        const long long j = idx - total;  // b * m + r
+        for (int s = g; s < splits; s += kReduceGroups) value += sums_work[static_cast<long long>(s) * batch * m + j];
     }
     part[g][e] = value;
     __syncthreads();
-    if (g != 0 || idx >= total) return;
+    if (g != 0 || idx >= total + extra) return;
     for (int k = 1; k < kReduceGroups; ++k) value += part[k][e];
+    if (idx >= total) {
+        const long long j = idx - total;
+        sums[(j / m) * sums_stride + j % m] = value;
+        return;
+    }
     const int col = static_cast<int>(idx % n);
     const int row = static_cast<int>((idx / n) % m);
     const int b = static_cast<int>(idx / plane);
@@ -578,25 +591,29 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     if (splits > 1) {
         const long long total = static_cast<long long>(batch) * m * n;
         const unsigned blocks = static_cast<unsigned>(std::min<long long>((total + 255) / 256, 4096));
-        if (splits >= 2 * gemm::kReduceGroups && total <= (1LL << 22))
-            hipLaunchKernelGGL(gemm::splitk_reduce_grouped, dim3(ceil_div(total, gemm::kReduceCols)), dim3(256), 0,
-                               stream, workspace, d, d_bf16, c, bias, ldd, stride_d, stride_bias, m, n, batch, splits,
-                               beta, epilogue);
+        const bool grouped = splits >= 2 * gemm::kReduceGroups && total <= (1LL << 22);
+        const float* sums_work = workspace + static_cast<std::size_t>(splits) * batch * m * n;
+        if (grouped)  // the row sums of A ride in the same launch
+            hipLaunchKernelGGL(gemm::splitk_reduce_grouped,
+                               dim3(ceil_div(total + (a_sums ? static_cast<long long>(batch) * m : 0),
+                                             gemm::kReduceCols)),
+                               dim3(256), 0, stream, workspace, d, d_bf16, c, bias, ldd, stride_d, stride_bias, m, n,
+                               batch, splits, beta, epilogue, a_sums ? sums_work : nullptr, a_sums, sums_stride);
         else
             hipLaunchKernelGGL(gemm::splitk_reduce, dim3(blocks), dim3(256), 0, stream, workspace, d, d_bf16, c, bias,
                                ldd, stride_d, stride_bias, m, n, batch, splits, beta, epilogue);
         check_launch("Launch split-K reduction");
-        if (a_sums) {
-            // [splits][batch][m] partial row sums -> [batch][m], fixed order
-            const float* work = workspace + static_cast<std::size_t>(splits) * batch * m * n;
+        if (a_sums && !grouped) {
+            // [splits][batch][m] partial row sums -> a_sums, fixed order
             if (splits >= 2 * gemm::kReduceGroups)
                 hipLaunchKernelGGL(gemm::splitk_reduce_grouped, dim3(ceil_div(static_cast<long long>(batch) * m,
                                                                                gemm::kReduceCols)),
-                                   dim3(256), 0, stream, work, a_sums, nullptr, nullptr, nullptr,
-                                   static_cast<long long>(m), sums_stride, 0LL, 1, m, batch, splits, 0.0f, 0);
+                                   dim3(256), 0, stream, sums_work, a_sums, nullptr, nullptr, nullptr,
+                                   static_cast<long long>(m), sums_stride, 0LL, 1, m, batch, splits, 0.0f, 0, nullptr,
+                                   nullptr, 0LL);
             else
                 hipLaunchKernelGGL(gemm::splitk_reduce, dim3(ceil_div(static_cast<long long>(batch) * m, 256)),
-                                   dim3(256), 0, stream, work, a_sums, nullptr, nullptr, nullptr,
+                                   dim3(256), 0, stream, sums_work, a_sums, nullptr, nullptr, nullptr,
                                    static_cast<long long>(m), sums_stride, 0LL, 1, m, batch, splits, 0.0f, 0);
             check_launch("Launch row-sum reduction");
         }
