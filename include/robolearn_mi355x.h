@@ -44,15 +44,18 @@ int rl_plan_run(void* plan, const void* a, const void* b, const void* c, void* d
 int rl_plan_destroy(void* plan);
 
 /* Row-major batched D[b] = act(op(A[b]) op(B[b]) + bias[b]) + beta C[b] on MFMA
- * (mode 0: fp32 v_mfma_f32_32x32x2_f32, mode 1: bf16 v_mfma_f32_32x32x16_bf16).
+ * (mode 0: fp32 v_mfma_f32_32x32x2_f32, mode 1: bf16 v_mfma_f32_32x32x16_bf16,
+ * mode 2: fp32 operands and results with fp32-accurate products on the bf16 matrix
+ * cores: every operand value split exactly into three bf16 pieces, six partial
+ * products per 16-K step).
  * A(m,k) = a_kcontig ? A[m*lda+k] : A[k*lda+m]; B(k,n) = b_kcontig ? B[n*ldb+k]
- * : B[k*ldb+n].  epilogue 0 none, 1 ReLU, 2 ELU, 3 ELU gradient (mode 0 only:
+ * : B[k*ldb+n].  epilogue 0 none, 1 ReLU, 2 ELU, 3 ELU gradient (modes 0 and 2:
  * D = AB * elu'(C) with C the ELU outputs, beta 0, no bias).  splits > 1 reduces over K in
  * fixed order through workspace; d_bf16 (optional) receives a bf16 copy of D.
  * moments (optional, needs ldd == n) receives the per-256-row-chunk column
  * (mean, M2) of D in rl_bn_forward_ex's partial layout [batch][ceil(m/256)][2][n],
  * from the GEMM epilogue when the 256x256 bf16 kernel runs the product.
- * a_sums (optional, mode 0 only, bias NULL) receives the row sums of op(A) over
+ * a_sums (optional, modes 0 and 2, bias NULL) receives the row sums of op(A) over
  * K in the bias layout, member e at a_sums + e * stride_bias (m when stride_bias
  * is 0): the bias gradient of a weight-gradient product dW = dY^T X.
  * With splits > 1 the workspace holds splits*batch*m*n floats, plus splits*batch*m
