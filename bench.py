@@ -562,7 +562,7 @@ def main() -> int:
     torch.cuda.synchronize()
     kernel_ms = k0.elapsed_time(k1) / reps
     kernel_flops = 2.0 * 2 * rows * h * 4 * h
-    peak = BF16_PEAK_TFLOPS if agent.mode == K.BF16 else FP32_PEAK_TFLOPS
+    peak = {K.BF16: BF16_PEAK_TFLOPS, K.FP32_SPLIT: BF16_PEAK_TFLOPS / 6.0}.get(agent.mode, FP32_PEAK_TFLOPS)
     achieved = kernel_flops / (kernel_ms * 1e-3) / 1e12
     operand = "unsigned short" if agent.mode == K.BF16 else "float"
     shape = f"critic block-1 forward [2 x {rows} x {h}] . [{4 * h} x {h}]^T"

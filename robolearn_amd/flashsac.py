@@ -141,7 +141,9 @@ class FlashSAC:
         self.action_dim = action_dim
         self.num_envs = num_envs
         self.batch_size = B = cfg.sample_batch_size
-        self.mode = K.BF16 if cfg.use_amp else K.FP32
+        # fp32 configurations form their products on the bf16 matrix cores from exact three-piece
+        # splits (fp32-accurate, rl_gemm mode 2)
+        self.mode = K.BF16 if cfg.use_amp else K.FP32_SPLIT
         self.compute_dtype = "bfloat16" if cfg.use_amp else "float32"
         self._update_step = 0
         self._graphs = {}
@@ -558,7 +560,7 @@ class FlashSAC:
         if n not in self._act_nets:
             cfg = self.cfg
             net = Trunk(ensemble=1, in_dim=self.observation_dim, hidden=cfg.actor_hidden_dim,
-                        blocks=cfg.actor_num_blocks, max_rows=n, device=self.device, mode=K.FP32,
+                        blocks=cfg.actor_num_blocks, max_rows=n, device=self.device, mode=K.FP32_SPLIT,
                         prefix_linear=".w.weight")
             head = torch.empty(n, 2 * self.action_dim, device=self.device)
             actions = torch.empty(n, self.action_dim, device=self.device)
@@ -587,7 +589,7 @@ class FlashSAC:
             net.forward(p, p, self.actor_running, obs, rows=n, x_stride=0, training=False)
             net.post_norm(p, rows=n, row0=0, count=n)
             K.linear_forward(net.z, self.head_w, head, rows=n, in_dim=net.h, out_dim=2 * A, bias=self.head_b,
-                             mode=K.FP32)
+                             mode=K.FP32_SPLIT)
             noise = None
             if training:
                 _native.call("rl_exploration_noise", self.cfg.seed * 7919 + 37, self.exploration_step.data_ptr(),
