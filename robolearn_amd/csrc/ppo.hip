@@ -242,21 +242,28 @@ struct LossArgs {
     int clip_value;
     float* dmean;             // [rows, A]
     float* dvalue;            // [rows]
-    float* dstd_rows;         // [rows, A] per-row std-parameter gradient
+    float* dstd_rows;         // [rows, A] per-row std-parameter gradient (when std_partial is null)
     float* partial;           // [4, blocks]: total, policy, value, entropy sums (already scaled by 1/rows)
+    // fused minibatch form: KL(N_old || N_new) sums in partial row 4 (old_mean, old_std given), and the
+    // std-parameter gradient as per-workgroup column sums in partial rows 5 .. 5 + A instead of dstd_rows
+    const float* old_mean;
+    const float* old_std;
+    bool fused;
 };
 
 // Clipped surrogate, clipped value and entropy terms of one row and their
 // gradients with respect to the mean, the value and the std parameter.
 __global__ __launch_bounds__(kRowThreads) void loss_kernel(LossArgs a) {
-    __shared__ float waves[4][kRowWaves];
+    __shared__ float waves[5][kRowWaves];
+    __shared__ float std_cols[kRowWaves][kWave];
     const float ln_two_pi = 1.8378770664093453f;
     const float entropy_const = 1.4189385332046727f;
     const float scale = 1.0f / static_cast<float>(a.rows);
     const float lo = 1.0f - a.clip_ratio, hi = 1.0f + a.clip_ratio;
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
-    float sums[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float sums[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    float std_col = 0.0f;  // fused form: this lane's std-gradient column (lane < A, A <= 64)
     for (int r = wave; r < kRowsPerBlock; r += kRowWaves) {
         const long long i = blockIdx.x * static_cast<long long>(kRowsPerBlock) + r;
         if (i >= a.rows) break;
@@ -312,23 +319,83 @@ __global__ __launch_bounds__(kRowThreads) void loss_kernel(LossArgs a) {
             const float inv_std = expf(-ls);
             const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * inv_std;
             a.dmean[i * a.action_dim + j] = dlp * residual * inv_std;
-            a.dstd_rows[i * a.action_dim + j] =
-                (dlp * (residual * residual - 1.0f) - scale * a.entropy_coefficient) * dls_dp;
+            const float dstd = (dlp * (residual * residual - 1.0f) - scale * a.entropy_coefficient) * dls_dp;
+            if (a.fused) {
+                std_col += dstd;
+                // KL(N_old || N_new) = log(s / s0) + (s0^2 + (m0 - m)^2) / (2 s^2) - 1/2 (ppo.py:207-230)
+                const float std = std_of(p, a.std_type, a.std_min, a.std_max);
+                const float ratio = a.old_std[i * a.action_dim + j] / std;
+                const float delta = (a.old_mean[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) / std;
+                sums[4] += 0.5f * (ratio * ratio + delta * delta - 1.0f) - logf(ratio);
+            } else {
+                a.dstd_rows[i * a.action_dim + j] = dstd;
+            }
         }
         sums[0] += scale * (policy_loss + a.value_coefficient * value_loss - a.entropy_coefficient * entropy);
         sums[1] += scale * policy_loss;
         sums[2] += scale * value_loss;
         sums[3] += scale * entropy;
     }
+    if (a.fused) {
+        sums[4] = wave_sum(sums[4]);  // lanes hold different action dimensions
+        std_cols[wave][lane] = std_col;
+    }
     if (lane == 0) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) waves[q][wave] = sums[q];
+        for (int q = 0; q < 5; ++q) waves[q][wave] = sums[q];
     }
     __syncthreads();
-    if (threadIdx.x < 4) {
+    const int terms = a.fused ? 5 : 4;
+    if (static_cast<int>(threadIdx.x) < terms) {
         float total = 0.0f;
         for (int w = 0; w < kRowWaves; ++w) total += waves[threadIdx.x][w];
         a.partial[threadIdx.x * static_cast<long long>(gridDim.x) + blockIdx.x] = total;
+    }
+    if (a.fused && static_cast<int>(threadIdx.x) < a.action_dim) {
+        float total = 0.0f;
+        for (int w = 0; w < kRowWaves; ++w) total += std_cols[w][threadIdx.x];
+        a.partial[(5 + threadIdx.x) * static_cast<long long>(gridDim.x) + blockIdx.x] = total;
+    }
+}
+
+// Fused minibatch finish: totals[q] = sum_b partial[q, b] (q < 4), the mean KL
+// and the adaptive learning-rate rule (ppo.py:233-238), and the std-parameter
+// gradient dstd[j] = sum_b partial[5 + j, b]; every sum in fixed order.
+constexpr int kFinishGroups = kThreads / kWave;
+
+__global__ __launch_bounds__(kThreads) void loss_finish(const float* partial, long long blocks, long long rows,
+                                                        int action_dim, float desired_kl, int adapt, float* totals,
+                                                        float* kl_out, float* lr, float* dstd) {
+    __shared__ float s[kThreads];
+    for (int q = 0; q < 5; ++q) {
+        float v = 0.0f;
+        for (long long i = threadIdx.x; i < blocks; i += kThreads) v += partial[q * blocks + i];
+        v = block_sum(v, s);
+        if (threadIdx.x == 0) {
+            if (q < 4) {
+                totals[q] = v;
+            } else {
+                const float kl = v / static_cast<float>(rows);
+                kl_out[0] = kl;
+                if (adapt) {
+                    if (kl > desired_kl * 2.0f) lr[0] = fmaxf(1.0e-5f, lr[0] / 1.5f);
+                    else if (kl < desired_kl / 2.0f && kl > 0.0f) lr[0] = fminf(1.0e-2f, lr[0] * 1.5f);
+                }
+            }
+        }
+    }
+    // std gradient: column j = t % 64, group g = t / 64 adds blocks g, g + G, ... in order
+    const int j = threadIdx.x % kWave;
+    const int g = threadIdx.x / kWave;
+    float v = 0.0f;
+    if (j < action_dim)
+        for (long long b = g; b < blocks; b += kFinishGroups) v += partial[(5 + j) * blocks + b];
+    s[threadIdx.x] = v;
+    __syncthreads();
+    if (g == 0 && j < action_dim) {
+        float total = s[j];
+        for (int q = 1; q < kFinishGroups; ++q) total += s[q * kWave + j];
+        dstd[j] = total;
     }
 }
 
@@ -630,12 +697,39 @@ RL_API int rl_ppo_loss(const float* mean, long long ld_mean, const float* value,
         rl::require(blocks <= (1LL << 30), "PPO loss row count is too large.");
         Q::LossArgs a{mean, ld_mean, value, std_param, actions, old_log_probs, old_values, advantages, returns, rows,
                       action_dim, std_type, std_min, std_max, clip_ratio, value_coefficient, entropy_coefficient,
-                      value_loss_scale, clip_value, dmean, dvalue, dstd_rows, row_terms};
+                      value_loss_scale, clip_value, dmean, dvalue, dstd_rows, row_terms, nullptr, nullptr, false};
         const hipStream_t st = rl::as_stream(stream);
         hipLaunchKernelGGL(Q::loss_kernel, dim3(static_cast<unsigned>(blocks)), dim3(Q::kRowThreads), 0, st, a);
         rl::check_launch("Launch PPO loss");
         hipLaunchKernelGGL(Q::sum_rows_kernel, dim3(1), dim3(Q::kThreads), 0, st, row_terms, blocks, 4, totals);
         rl::check_launch("Launch PPO loss reduction");
+    });
+}
+
+RL_API int rl_ppo_minibatch_loss(const float* mean, long long ld_mean, const float* value, const float* std_param,
+                                 const float* actions, const float* old_log_probs, const float* old_values,
+                                 const float* advantages, const float* returns, const float* old_mean,
+                                 const float* old_std, long long rows, int action_dim, int std_type, float std_min,
+                                 float std_max, float clip_ratio, float value_coefficient, float entropy_coefficient,
+                                 float value_loss_scale, int clip_value, float desired_kl, int adapt, float* dmean,
+                                 float* dvalue, float* dstd, float* partial, float* totals, float* kl, float* lr,
+                                 void* stream) noexcept {
+    return rl::guarded("rl_ppo_minibatch_loss", [&] {
+        rl::require(mean && value && std_param && actions && old_log_probs && old_values && advantages && returns &&
+                        old_mean && old_std && dmean && dvalue && dstd && partial && totals && kl && lr && rows > 0,
+                    "PPO minibatch loss needs every input and output buffer.");
+        rl::require(action_dim > 0 && action_dim <= rl::kWave, "PPO minibatch loss supports 1..64 action dimensions.");
+        const long long blocks = (rows + Q::kRowsPerBlock - 1) / Q::kRowsPerBlock;
+        rl::require(blocks <= (1LL << 30), "PPO loss row count is too large.");
+        Q::LossArgs a{mean, ld_mean, value, std_param, actions, old_log_probs, old_values, advantages, returns, rows,
+                      action_dim, std_type, std_min, std_max, clip_ratio, value_coefficient, entropy_coefficient,
+                      value_loss_scale, clip_value, dmean, dvalue, nullptr, partial, old_mean, old_std, true};
+        const hipStream_t st = rl::as_stream(stream);
+        hipLaunchKernelGGL(Q::loss_kernel, dim3(static_cast<unsigned>(blocks)), dim3(Q::kRowThreads), 0, st, a);
+        rl::check_launch("Launch PPO minibatch loss");
+        hipLaunchKernelGGL(Q::loss_finish, dim3(1), dim3(Q::kThreads), 0, st, partial, blocks, rows, action_dim,
+                           desired_kl, adapt, totals, kl, lr, dstd);
+        rl::check_launch("Launch PPO minibatch loss reduction");
     });
 }
 

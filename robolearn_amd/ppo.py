@@ -54,6 +54,8 @@ class WarpPPO:
             raise ValueError("timeout_bootstrap must be 'next' or 'current'.")
         if cfg.std_range[0] <= 0 or cfg.std_range[0] > cfg.std_range[1]:
             raise ValueError("std_range must contain positive increasing bounds.")
+        if action_dim > 64:
+            raise ValueError("The MI355X PPO loss kernels support at most 64 action dimensions.")
         if cfg.activation != "elu":
             raise NotImplementedError("The MI355X PPO path implements ELU activations (the G1 recipe).")
         if not torch.cuda.is_available():
@@ -135,8 +137,7 @@ class WarpPPO:
             self.value = z(M, 1)
             self.dmean = z(M, A)
             self.dvalue = z(M, 1)
-            self.dstd_rows = z(M, A)
-            self.row_terms = z(4, M)
+            self.loss_partial = z((5 + A) * ((M + 15) // 16))  # per-16-row-workgroup loss, KL, std-gradient sums
             self.totals = z(4)
             self.metrics = self.totals[1:]  # policy loss, value loss, entropy of the last minibatch
             self.loss = self.totals[:1]
@@ -267,19 +268,18 @@ class WarpPPO:
                      self.b_log_probs.data_ptr(), self.b_values.data_ptr(), self.b_advantages.data_ptr(),
                      self.b_returns.data_ptr(), self.b_means.data_ptr(), self.b_stds.data_ptr(), K.stream())
         self._joint_forward(M)
-        std_type = int(cfg.std_type == "scalar")
-        _native.call("rl_ppo_kl_adapt", self.mean.data_ptr(), A, self.distribution_parameter.data_ptr(),
-                     self.b_means.data_ptr(), self.b_stds.data_ptr(), M, A, std_type, float(cfg.std_range[0]),
-                     float(cfg.std_range[1]), float(cfg.desired_kl), int(cfg.schedule == "adaptive"),
-                     self.partial.data_ptr(), self.kl.data_ptr(), self.lr.data_ptr(), K.stream())
-        _native.call("rl_ppo_loss", self.mean.data_ptr(), A, self.value.data_ptr(),
+        # loss, its gradients, the pre-step KL with the adaptive learning rate and the std-parameter
+        # gradient: two launches (ppo.py:207-310)
+        _native.call("rl_ppo_minibatch_loss", self.mean.data_ptr(), A, self.value.data_ptr(),
                      self.distribution_parameter.data_ptr(), self.b_actions.data_ptr(), self.b_log_probs.data_ptr(),
-                     self.b_values.data_ptr(), self.b_advantages.data_ptr(), self.b_returns.data_ptr(), M, A, std_type,
+                     self.b_values.data_ptr(), self.b_advantages.data_ptr(), self.b_returns.data_ptr(),
+                     self.b_means.data_ptr(), self.b_stds.data_ptr(), M, A, int(cfg.std_type == "scalar"),
                      float(cfg.std_range[0]), float(cfg.std_range[1]), float(cfg.clip_ratio),
                      float(cfg.value_coefficient), float(cfg.entropy_coefficient), float(cfg.value_loss_scale),
-                     int(cfg.clip_value), self.dmean.data_ptr(), self.dvalue.data_ptr(), self.dstd_rows.data_ptr(),
-                     self.row_terms.data_ptr(), self.totals.data_ptr(), K.stream())
-        K.bias_grad(self.dstd_rows, self.grads["std"], self.partial, rows=M, channels=A)
+                     int(cfg.clip_value), float(cfg.desired_kl), int(cfg.schedule == "adaptive"),
+                     self.dmean.data_ptr(), self.dvalue.data_ptr(), self.grads["std"].data_ptr(),
+                     self.loss_partial.data_ptr(), self.totals.data_ptr(), self.kl.data_ptr(), self.lr.data_ptr(),
+                     K.stream())
         self._joint_backward(M)
         for (start, end), norm in zip(self.group_ranges, self.group_norms):
             grad = self.flat.grad[start:end]
