@@ -86,12 +86,16 @@ def gemm_flops(w: dict) -> float:
     return actor_phase + 2 * critic_phase
 
 
-def elementwise_bytes(w: dict) -> float:
-    """Approximate compulsory HBM bytes of the non-GEMM kernels for the same update pair."""
+def elementwise_bytes(w: dict, act_bytes: int = 4) -> float:
+    """Approximate compulsory HBM bytes of the non-GEMM kernels for the same update pair.
+
+    act_bytes: bytes per BatchNorm input / gradient element (2 when the bf16 path stores them
+    in bf16; its producing GEMM also writes the statistics, so the forward has no stats read)."""
     B, hc, ha, K = w["batch"], w["critic_hidden"], w["actor_hidden"], w["bins"]
     per_block = 2 * 2 * B * (4 * hc + hc)  # members x rows x channels of one critic block
-    bn_fwd = 3 * 4 * per_block * w["critic_blocks"]  # stats read + apply read + write
-    bn_bwd = 5 * 4 * per_block * w["critic_blocks"]
+    stats_read = 0 if act_bytes == 2 else 1
+    bn_fwd = (2 + stats_read) * act_bytes * per_block * w["critic_blocks"]  # (stats read +) apply read + write
+    bn_bwd = 5 * act_bytes * per_block * w["critic_blocks"]  # partials read x, dy; apply read x, dy, write dx
     critic_pass = bn_fwd
     critic_total = 2 * critic_pass * 2 + bn_bwd * 2 + bn_bwd  # 2 updates x (target + online) fwd, bwd
     actor_bytes = 10 * 4 * 2 * B * 5 * ha * w["actor_blocks"]
@@ -565,7 +569,8 @@ def main() -> int:
     peak = {K.BF16: BF16_PEAK_TFLOPS, K.FP32_SPLIT: BF16_PEAK_TFLOPS / 6.0}.get(agent.mode, FP32_PEAK_TFLOPS)
     achieved = kernel_flops / (kernel_ms * 1e-3) / 1e12
     operand = "unsigned short" if agent.mode == K.BF16 else "float"
-    shape = f"critic block-1 forward [2 x {rows} x {h}] . [{4 * h} x {h}]^T"
+    out_type = "bf16" if net.u1[0].dtype == torch.bfloat16 else "fp32"
+    shape = f"critic block-1 forward [2 x {rows} x {h}] . [{4 * h} x {h}]^T -> {out_type}"
     if agent.mode == K.BF16 and rows % 256 == 0 and (4 * h) % 256 == 0 and h % 128 == 0:
         kernel_name = f"gemm_dma_kernel {shape}"  # 256x256 tiles, DMA-fed (both operands K-contiguous)
     elif agent.mode == K.BF16:
@@ -574,7 +579,8 @@ def main() -> int:
         kernel_name = f"gemm_kernel<0, float, float, true, true> {shape}"
     traffic = args.traffic if args.traffic is not None else measured_traffic(kernel_name)
     operand_bytes = 2 if agent.mode == K.BF16 else 4
-    algorithmic_bytes = 2 * (rows * h + 4 * h * h) * operand_bytes + 2 * rows * 4 * h * 4
+    # the output is the BatchNorm input: bf16 in bf16 mode
+    algorithmic_bytes = 2 * (rows * h + 4 * h * h) * operand_bytes + 2 * rows * 4 * h * net.u1[0].element_size()
     roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": kernel_name,
                 "kernel_ms": round(kernel_ms, 4), "flops_per_launch": kernel_flops,
@@ -588,7 +594,7 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     flops = gemm_flops(w)
-    hbm_bytes = elementwise_bytes(w)
+    hbm_bytes = elementwise_bytes(w, 2 if agent.mode == K.BF16 else 4)
     t_roof_ms = (flops / (peak * 1e12) + hbm_bytes / (HBM_PEAK_GBS * 1e9)) * 1e3
     update_roofline = {"gemm_tflop_per_step": round(flops / 1e12, 3),
                        "elementwise_gb_per_step": round(hbm_bytes / 1e9, 3),

@@ -52,9 +52,11 @@ int rl_plan_destroy(void* plan);
  * : B[k*ldb+n].  epilogue 0 none, 1 ReLU, 2 ELU, 3 ELU gradient (modes 0 and 2:
  * D = AB * elu'(C) with C the ELU outputs, beta 0, no bias).  splits > 1 reduces over K in
  * fixed order through workspace; d_bf16 (optional) receives a bf16 copy of D.
+ * In mode 1, d may be NULL with d_bf16 set: the bf16 copy is then the only output.
  * moments (optional, needs ldd == n) receives the per-256-row-chunk column
  * (mean, M2) of D in rl_bn_forward_ex's partial layout [batch][ceil(m/256)][2][n],
- * from the GEMM epilogue when the 256x256 bf16 kernel runs the product.
+ * from the GEMM epilogue when the 256x256 bf16 kernel runs the product (of the
+ * bf16 values when d is NULL).
  * a_sums (optional, modes 0 and 2, bias NULL) receives the row sums of op(A) over
  * K in the bias layout, member e at a_sums + e * stride_bias (m when stride_bias
  * is 0): the bias gradient of a weight-gradient product dW = dY^T X.
@@ -133,20 +135,24 @@ int rl_flash_ema_step(void* plan, void* stream);
 int rl_flash_ema_destroy(void* plan);
 
 /* ---- normalization ------------------------------------------------------ */
-/* Ensemble BatchNorm; x_stride 0 broadcasts one input to every member; optional
+/* Ensemble BatchNorm; x_stride 0 broadcasts one input to every member; x_bf16:
+ * x holds bf16 values (channels and x_stride multiples of 4, 8-byte aligned),
+ * the layout of an autocast Linear output feeding the BatchNorm; optional
  * residual is added after the ReLU (fuses robolearn/flashsac/layers.py:105-113);
  * y or y_bf16 may be NULL (at least one output).
  * Replaces robolearn/cuda/flash_kernels.cuh:500-543 for the stacked critics of
  * robolearn/flashsac/layers.py:189-222.  partial: ensemble*2*ceil(rows/256)*channels;
  * moments_ready: partial already holds x's chunk moments (rl_gemm's moments output). */
-int rl_bn_forward_ex(int ensemble, const float* x, long long x_stride, const float* w, const float* b,
+int rl_bn_forward_ex(int ensemble, const void* x, int x_bf16, long long x_stride, const float* w, const float* b,
                      float* running_mean, float* running_var, float* mean, float* var, float* partial,
                      const float* residual, float* y, void* y_bf16, int rows, int channels, float eps,
                      float momentum, int training, int relu, int update_running, int moments_ready, void* stream);
 /* y == NULL with relu recomputes the ReLU mask from x, the statistics and (w, b).
+ * x_bf16 / dy_bf16: x / dy hold bf16 values (as in rl_bn_forward_ex); dx_bf16 may
+ * be the dy buffer itself (updated in place).
  * sums: 2*ensemble*channels.  Replaces flash_kernels.cuh:545-609. */
-int rl_bn_backward_ex(int ensemble, const float* x, long long x_stride, const float* dy, const float* y,
-                      const float* w, const float* b, const float* mean, const float* var, float* partial,
+int rl_bn_backward_ex(int ensemble, const void* x, int x_bf16, long long x_stride, const void* dy, int dy_bf16,
+                      const float* y, const float* w, const float* b, const float* mean, const float* var, float* partial,
                       float* sums, float* dx, float* dw, float* db, void* dx_bf16, int rows, int channels,
                       float eps, int training, int relu, int accumulate_dx, int accumulate_params, void* stream);
 /* RMSNorm over rows [0, rows) of each member (member_stride elements apart);

@@ -65,10 +65,10 @@ SIGNATURES = {
     "rl_flash_ema_step": (c_int, [P, P]),
     "rl_flash_ema_destroy": (c_int, [P]),
     # normalization
-    "rl_bn_forward_ex": (c_int, [c_int, P, c_ll, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_float, c_float, c_int,
-                                 c_int, c_int, c_int, P]),
-    "rl_bn_backward_ex": (c_int, [c_int, P, c_ll, P, P, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_float, c_int,
-                                  c_int, c_int, c_int, P]),
+    "rl_bn_forward_ex": (c_int, [c_int, P, c_int, c_ll, P, P, P, P, P, P, P, P, P, P, c_int, c_int, c_float,
+                                 c_float, c_int, c_int, c_int, c_int, P]),
+    "rl_bn_backward_ex": (c_int, [c_int, P, c_int, c_ll, P, c_int, P, P, P, P, P, P, P, P, P, P, P, c_int, c_int,
+                                  c_float, c_int, c_int, c_int, c_int, P]),
     "rl_rms_forward_ex": (c_int, [c_int, P, P, P, P, P, c_int, c_int, c_ll, c_float, P]),
     "rl_rms_backward_ex": (c_int, [c_int, P, P, P, P, P, P, P, P, c_int, c_int, c_ll, c_float, c_int, c_int, P]),
     "rl_cast_f32_bf16": (c_int, [P, P, c_ll, P]),

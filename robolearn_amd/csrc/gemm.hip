@@ -390,7 +390,7 @@ __global__ void splitk_reduce(const float* work, float* d, unsigned short* d_bf1
             value = apply_epilogue(value, epilogue);
             if (beta != 0.0f) value += beta * c[offset];
         }
-        d[offset] = value;
+        if (d) d[offset] = value;
         if (d_bf16) d_bf16[offset] = f32_to_bf16_bits(value);
     }
 }
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_grouped(const float* work, 
         value = apply_epilogue(value, epilogue);
         if (beta != 0.0f) value += beta * c[offset];
     }
-    d[offset] = value;
+    if (d) d[offset] = value;
     if (d_bf16) d_bf16[offset] = f32_to_bf16_bits(value);
 }
 
@@ -510,7 +510,7 @@ __global__ __launch_bounds__(256) void transpose16(const unsigned short* src, un
 }  // namespace gemm
 
 // Row-major batched GEMM with optional split-K.  See the header for the
-// argument contract.  Returns the workspace bytes needed when d == nullptr.
+// argument contract.  Returns 0.
 int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int m, int n, int k, int batch,
              const void* a, long long lda, long long stride_a, const void* b, long long ldb, long long stride_b,
              const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
@@ -519,7 +519,8 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     require(mode >= 0 && mode <= 2, "GEMM mode must be 0 (fp32), 1 (bf16 operands) or 2 (fp32 on bf16 pieces).");
     require(!(mode != 1 && (a_bf16 || b_bf16)), "fp32 GEMM modes require fp32 operands.");
     require(m > 0 && n > 0 && k > 0 && batch > 0, "GEMM dimensions must be positive.");
-    require(a && b && d, "GEMM operands must be nonnull.");
+    require(a && b && (d || (mode == 1 && d_bf16)),
+            "GEMM operands must be nonnull (bf16 mode may write the bf16 copy alone, with d null).");
     require(std::isfinite(beta) && (beta == 0.0f || c), "Nonzero beta requires C; beta must be finite.");
     require(epilogue >= 0 && epilogue <= 3, "Unknown GEMM epilogue.");
     require(epilogue != 3 || (mode != 1 && c && beta == 0.0f && !bias),
@@ -618,7 +619,10 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
             check_launch("Launch row-sum reduction");
         }
     }
-    if (moments && !fused_moments) bn_chunk_moments(batch, d, stride_d, moments, m, n, stream);
+    if (moments && !fused_moments) {
+        if (d) bn_chunk_moments(batch, d, 0, stride_d, moments, m, n, stream);
+        else bn_chunk_moments(batch, d_bf16, 1, stride_d, moments, m, n, stream);
+    }
     return 0;
 }
 

@@ -35,7 +35,7 @@ struct Params {
     float beta;          // D = act(AB + bias) + beta * C (direct mode only)
     int epilogue;        // Epilogue (direct mode only)
     int a_vec, b_vec;    // 16-byte vector loads allowed
-    unsigned short* d_bf16;  // optional bf16 copy of the output (direct mode only)
+    unsigned short* d_bf16;  // optional bf16 copy of the output (direct mode only; the only output when d is null)
     float* moments;      // optional per-256-row-chunk (mean, M2) of D: [batch][m / 256][2][n]
     int out_vec;         // 16-byte output stores allowed (n, ldd, strides multiple of 4; aligned outputs)
     float* a_sums;       // optional sum over this split's K of each row of op(A): [splits][batch][m] (fp32 family)
@@ -75,8 +75,8 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
              unsigned short* d_bf16, float* moments, float* a_sums);
 
 // Per-256-row-chunk column moments of a row-major [ensemble][rows][channels]
-// fp32 tensor into partial[e][chunk][2][channels] (norm.hip).
-void bn_chunk_moments(int ensemble, const float* x, long long x_stride, float* partial, int rows, int channels,
-                      hipStream_t stream);
+// fp32 (or, x_bf16, bf16) tensor into partial[e][chunk][2][channels] (norm.hip).
+void bn_chunk_moments(int ensemble, const void* x, int x_bf16, long long x_stride, float* partial, int rows,
+                      int channels, hipStream_t stream);
 
 }  // namespace rl

@@ -168,8 +168,11 @@ __device__ __forceinline__ void store_tile_vec(const Params& p, const f32x16_t (
                                                int split, int m0, int n0, int wave, int wm, int wn) {
     const int lane = threadIdx.x % kWave;
     const bool direct = p.splits == 1;
-    float* D = p.d + (direct ? batch * p.stride_d
-                             : (static_cast<long long>(split) * p.batch + batch) * static_cast<long long>(p.m) * p.n);
+    // direct mode with d null writes the bf16 copy alone
+    float* D = (direct && !p.d) ? nullptr
+                                : p.d + (direct ? batch * p.stride_d
+                                                : (static_cast<long long>(split) * p.batch + batch) *
+                                                      static_cast<long long>(p.m) * p.n);
     const long long ldd = direct ? p.ldd : p.n;
     const float* C = (direct && p.beta != 0.0f) ? p.c + batch * p.stride_d : nullptr;
     unsigned short* Dh = (direct && p.d_bf16) ? p.d_bf16 + batch * p.stride_d : nullptr;
@@ -211,7 +214,7 @@ __device__ __forceinline__ void store_tile_vec(const Params& p, const f32x16_t (
                     *reinterpret_cast<uint2*>(Dh + offset) =
                         make_uint2(f32x2_to_bf16x2(val.x, val.y), f32x2_to_bf16x2(val.z, val.w));
             }
-            *reinterpret_cast<float4*>(D + offset) = val;
+            if (D) *reinterpret_cast<float4*>(D + offset) = val;
         }
     }
 }
@@ -300,8 +303,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(Params p) {
         return;
     }
     const bool direct = p.splits == 1;
-    float* D = p.d + (direct ? batch * p.stride_d
-                             : (static_cast<long long>(split) * p.batch + batch) * static_cast<long long>(p.m) * p.n);
+    // direct mode with d null writes the bf16 copy alone
+    float* D = (direct && !p.d) ? nullptr
+                                : p.d + (direct ? batch * p.stride_d
+                                                : (static_cast<long long>(split) * p.batch + batch) *
+                                                      static_cast<long long>(p.m) * p.n);
     const long long ldd = direct ? p.ldd : p.n;
     const float* bias = p.bias ? p.bias + batch * p.stride_bias : nullptr;
     const float* C = p.c ? p.c + batch * p.stride_d : nullptr;
@@ -321,7 +327,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(Params p) {
                 if (direct) {
                     float value = apply_epilogue(acc[i][j][v] + bcol, p.epilogue);
                     if (p.beta != 0.0f) value += p.beta * C[offset];
-                    D[offset] = value;
+                    if (D) D[offset] = value;
                     if (Dh) Dh[offset] = f32_to_bf16_bits(value);
                 } else {
                     D[offset] = acc[i][j][v];

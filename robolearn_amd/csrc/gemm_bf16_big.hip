@@ -225,9 +225,11 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
     // holds column l % 32 and rows 8 (v / 4) + 4 (l / 32) + v % 4, v < 16)
     // and writes it back as 16-byte stores, two 512-byte row segments per
     // wave instruction.  The stores drain while the next tile starts.
-    float* D = p.d + (direct ? tile.batch * p.stride_d
-                             : (static_cast<long long>(tile.split) * p.batch + tile.batch) *
-                                   static_cast<long long>(p.m) * p.n);
+    // direct mode with d null writes the bf16 copy alone
+    float* D = (direct && !p.d) ? nullptr
+                                : p.d + (direct ? tile.batch * p.stride_d
+                                                : (static_cast<long long>(tile.split) * p.batch + tile.batch) *
+                                                      static_cast<long long>(p.m) * p.n);
     const long long ldd = direct ? p.ldd : p.n;
     const float* C = (direct && p.beta != 0.0f) ? p.c + tile.batch * p.stride_d : nullptr;
     unsigned short* Dh = (direct && p.d_bf16) ? p.d_bf16 + tile.batch * p.stride_d : nullptr;
@@ -243,6 +245,9 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
     // 4 blocks, then with lane l ^ 32 (the other row parity) and with the wave of
     // the other row half, always in the same order.
     const bool moments = direct && p.moments != nullptr;
+    // a bf16-only output takes the moments of the stored (rounded) values; the
+    // moments epilogue adds nothing to D, so the later rounding is exact
+    const bool round_stage = moments && !D;
     float count = 0.0f;
     float4 mean = make_float4(0.0f, 0.0f, 0.0f, 0.0f), m2 = mean;
 #pragma unroll
@@ -255,7 +260,8 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v)
-                stage[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * EP + j * 32 + lane % 32] = acc[i][j][v];
+                stage[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * EP + j * 32 + lane % 32] =
+                    round_stage ? bf16_bits_to_f32(f32_to_bf16_bits(acc[i][j][v])) : acc[i][j][v];
         lds_fence();
         if (moments) {
             float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -299,7 +305,8 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
             }
             // streaming stores: nothing in this kernel rereads D, and the tile
             // rounds write far more than the L2 holds
-            __builtin_nontemporal_store((f32x4){val.x, val.y, val.z, val.w}, reinterpret_cast<f32x4*>(D + offset));
+            if (D)
+                __builtin_nontemporal_store((f32x4){val.x, val.y, val.z, val.w}, reinterpret_cast<f32x4*>(D + offset));
         }
     }
     if (moments) {

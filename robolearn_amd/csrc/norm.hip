@@ -173,13 +173,21 @@ inline VecLayout vec_layout(long long rows, int channels, int ensemble) {
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+// four bf16 values (8-byte aligned) widened to fp32
+__device__ __forceinline__ float4 ld4(const unsigned short* p) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+}
 __device__ __forceinline__ void st4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
 __device__ __forceinline__ void st4_bf16(unsigned short* p, float4 v) {
     *reinterpret_cast<uint2*>(p) = make_uint2(f32x2_to_bf16x2(v.x, v.y), f32x2_to_bf16x2(v.z, v.w));
 }
 
-// bn_apply for channels % 4 == 0 with 16-byte aligned rows.
-__global__ __launch_bounds__(256) void bn_apply_vec(const float* x, long long x_stride, const float* mean,
+// bn_apply for channels % 4 == 0 with 16-byte aligned rows; XT is float or
+// unsigned short (bf16 bits, rows 8-byte aligned).
+template <typename XT>
+__global__ __launch_bounds__(256) void bn_apply_vec(const XT* x, long long x_stride, const float* mean,
                                                     const float* var, const float* w, const float* b,
                                                     const float* residual, float* y, unsigned short* y_bf16,
                                                     long long rows, int channels, float eps, int relu, int tpr) {
@@ -193,7 +201,7 @@ __global__ __launch_bounds__(256) void bn_apply_vec(const float* x, long long x_
     const float4 mu = ld4(mean + pc), va = ld4(var + pc), wv = ld4(w + pc), bv = ld4(b + pc);
     const float4 inv = make_float4(1.0f / sqrtf(va.x + eps), 1.0f / sqrtf(va.y + eps), 1.0f / sqrtf(va.z + eps),
                                    1.0f / sqrtf(va.w + eps));
-    const float* xe = x + e * x_stride;
+    const XT* xe = x + e * x_stride;
     const long long out_base = static_cast<long long>(e) * rows * channels;
 #pragma unroll 4
     for (int k = 0; k < kRowsPerThread; ++k) {
@@ -214,8 +222,11 @@ __global__ __launch_bounds__(256) void bn_apply_vec(const float* x, long long x_
     }
 }
 
-// bn_grad_apply for channels % 4 == 0 with 16-byte aligned rows.
-__global__ __launch_bounds__(256) void bn_grad_apply_vec(const float* x, long long x_stride, const float* dy,
+// bn_grad_apply for channels % 4 == 0 with 16-byte aligned rows; x and dy are
+// float or bf16 bits (XT, DT).  dx_bf16 may alias a bf16 dy: each element is
+// read and written by the same thread.
+template <typename XT, typename DT>
+__global__ __launch_bounds__(256) void bn_grad_apply_vec(const XT* x, long long x_stride, const DT* dy,
                                                          const float* y, const float* w, const float* b,
                                                          const float* mean, const float* var, const float* sums,
                                                          float* dx, unsigned short* dx_bf16, long long rows,
@@ -237,7 +248,7 @@ __global__ __launch_bounds__(256) void bn_grad_apply_vec(const float* x, long lo
         s0 = ld4(sums + pc);
         s1 = ld4(sums + ensemble * channels + pc);
     }
-    const float* xe = x + e * x_stride;
+    const XT* xe = x + e * x_stride;
     const long long out_base = static_cast<long long>(e) * rows * channels;
     const float4 winv = make_float4(wv.x * inv.x, wv.y * inv.y, wv.z * inv.z, wv.w * inv.w);
 #pragma unroll 4
@@ -275,7 +286,8 @@ __global__ __launch_bounds__(256) void bn_grad_apply_vec(const float* x, long lo
     }
 }
 
-// float4 variants of bn_moments / bn_grad_partials for channels % 4 == 0: a
+// float4 variants of bn_moments / bn_grad_partials for channels % 4 == 0 (x and
+// dy fp32 or bf16 bits): a
 // workgroup covers 64 channels (16 float4 columns) x one 256-row chunk, 16 row
 // groups of 16 rows; each thread keeps its rows in registers.
 constexpr int kVecCols = 16;                     // float4 columns per workgroup
@@ -286,7 +298,8 @@ __device__ __forceinline__ float4 f4(float v) { return make_float4(v, v, v, v); 
 
 // Chunk moments with a two-pass mean / M2 per thread, then a fixed-order merge
 // of the row groups.
-__global__ __launch_bounds__(kThreads) void bn_moments_vec(const float* x, long long x_stride, float* partial, int rows,
+template <typename XT>
+__global__ __launch_bounds__(kThreads) void bn_moments_vec(const XT* x, long long x_stride, float* partial, int rows,
                                                            int channels, int chunks) {
     const int e = blockIdx.z;
     const int q = blockIdx.x * kVecCols + threadIdx.x % kVecCols;
@@ -295,7 +308,7 @@ __global__ __launch_bounds__(kThreads) void bn_moments_vec(const float* x, long 
     const int r0 = chunk * kChunk + group;
     const int r_end = min(rows, (chunk + 1) * kChunk);
     const bool live = 4 * q < channels;
-    const float* base = x + e * x_stride + 4 * q;
+    const XT* base = x + e * x_stride + 4 * q;
     float4 v[kVecRows];
     float count = 0.0f;
     float4 mean = f4(0.0f);
@@ -343,7 +356,8 @@ __global__ __launch_bounds__(kThreads) void bn_moments_vec(const float* x, long 
     }
 }
 
-__global__ __launch_bounds__(kThreads) void bn_grad_partials_vec(const float* x, long long x_stride, const float* dy,
+template <typename XT, typename DT>
+__global__ __launch_bounds__(kThreads) void bn_grad_partials_vec(const XT* x, long long x_stride, const DT* dy,
                                                                  const float* y, const float* w, const float* b,
                                                                  const float* mean, const float* var, float* partial,
                                                                  int rows, int channels, int chunks, float eps,
@@ -362,7 +376,7 @@ __global__ __launch_bounds__(kThreads) void bn_grad_partials_vec(const float* x,
         const float4 bv = b ? ld4(b + pc) : f4(0.0f);
         const float4 inv = make_float4(1.0f / sqrtf(va.x + eps), 1.0f / sqrtf(va.y + eps), 1.0f / sqrtf(va.z + eps),
                                        1.0f / sqrtf(va.w + eps));
-        const float* xe = x + e * x_stride + 4 * q;
+        const XT* xe = x + e * x_stride + 4 * q;
         const long long off = static_cast<long long>(e) * rows * channels + 4 * q;
 #pragma unroll 4
         for (int k = 0; k < kVecRows; ++k) {
@@ -843,24 +857,30 @@ inline unsigned elementwise_blocks(long long total) {
 int chunks_for(int rows) { return (rows + norm::kChunk - 1) / norm::kChunk; }
 
 // Per-256-row-chunk (mean, M2) of every column: partial[e][chunk][2][channels].
-void bn_chunk_moments(int ensemble, const float* x, long long x_stride, float* partial, int rows, int channels,
-                      hipStream_t stream) {
+// x_bf16: x holds bf16 bits (channels % 4 == 0, x_stride % 4 == 0, 8-byte aligned).
+void bn_chunk_moments(int ensemble, const void* x, int x_bf16, long long x_stride, float* partial, int rows,
+                      int channels, hipStream_t stream) {
     const int chunks = chunks_for(rows);
-    if (channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && aligned(partial, 16)) {
-        const dim3 grid(ceil_div(channels / 4, norm::kVecCols), chunks, ensemble);
-        hipLaunchKernelGGL(norm::bn_moments_vec, grid, dim3(norm::kThreads), 0, stream, x, x_stride, partial, rows,
-                           channels, chunks);
+    const dim3 vec_grid(ceil_div(channels / 4, norm::kVecCols), chunks, ensemble);
+    if (x_bf16) {
+        require(channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 8) && aligned(partial, 16),
+                "bf16 BatchNorm input needs channels and strides in multiples of 4 and 8-byte alignment.");
+        hipLaunchKernelGGL(norm::bn_moments_vec<unsigned short>, vec_grid, dim3(norm::kThreads), 0, stream,
+                           static_cast<const unsigned short*>(x), x_stride, partial, rows, channels, chunks);
+    } else if (channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && aligned(partial, 16)) {
+        hipLaunchKernelGGL(norm::bn_moments_vec<float>, vec_grid, dim3(norm::kThreads), 0, stream,
+                           static_cast<const float*>(x), x_stride, partial, rows, channels, chunks);
     } else {
         const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
-        hipLaunchKernelGGL(norm::bn_moments, grid, dim3(norm::kThreads), 0, stream, x, x_stride, partial, rows,
-                           channels, chunks);
+        hipLaunchKernelGGL(norm::bn_moments, grid, dim3(norm::kThreads), 0, stream, static_cast<const float*>(x),
+                           x_stride, partial, rows, channels, chunks);
     }
     check_launch("Launch BN moments");
 }
 
-void bn_forward(int ensemble, const float* x, long long x_stride, const float* w, const float* b, float* running_mean,
-                float* running_var, float* mean, float* var, float* partial, const float* residual, float* y,
-                unsigned short* y_bf16, int rows, int channels, float eps, float momentum, int training, int relu,
+void bn_forward(int ensemble, const void* x, int x_bf16, long long x_stride, const float* w, const float* b,
+                float* running_mean, float* running_var, float* mean, float* var, float* partial,
+                const float* residual, float* y, unsigned short* y_bf16, int rows, int channels, float eps, float momentum, int training, int relu,
                 int update_running, int moments_ready, hipStream_t stream) {
     require(ensemble > 0 && rows > 0 && channels > 0, "BatchNorm dimensions must be positive.");
     require(static_cast<long long>(rows) * channels <= std::numeric_limits<int>::max(), "BatchNorm exceeds 2^31 elements.");
@@ -871,7 +891,7 @@ void bn_forward(int ensemble, const float* x, long long x_stride, const float* w
     if (training) {
         require(mean && var && partial, "Training BatchNorm requires mean, var and partial scratch.");
         const int chunks = chunks_for(rows);
-        if (!moments_ready) bn_chunk_moments(ensemble, x, x_stride, partial, rows, channels, stream);
+        if (!moments_ready) bn_chunk_moments(ensemble, x, x_bf16, x_stride, partial, rows, channels, stream);
         hipLaunchKernelGGL(norm::bn_statistics, dim3(ceil_div(ensemble * channels, norm::kStatCols)),
                            dim3(norm::kStatCols * norm::kStatGroups), 0, stream,
                            partial, mean, var, running_mean, running_var, rows, channels, chunks, ensemble, momentum,
@@ -883,22 +903,31 @@ void bn_forward(int ensemble, const float* x, long long x_stride, const float* w
         require(running_mean && running_var, "Eval BatchNorm requires running statistics.");
     }
     const long long total = static_cast<long long>(ensemble) * rows * channels;
-    const bool vec = channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && (!y || aligned(y, 16)) &&
-                     (!y_bf16 || aligned(y_bf16, 8)) && (!residual || aligned(residual, 16)) &&
-                     aligned(use_mean, 16) && aligned(use_var, 16) && aligned(w, 16) && aligned(b, 16);
+    const bool vec = channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, x_bf16 ? 8 : 16) &&
+                     (!y || aligned(y, 16)) && (!y_bf16 || aligned(y_bf16, 8)) &&
+                     (!residual || aligned(residual, 16)) && aligned(use_mean, 16) && aligned(use_var, 16) &&
+                     aligned(w, 16) && aligned(b, 16);
+    require(vec || !x_bf16, "bf16 BatchNorm input needs channels and strides in multiples of 4 and aligned buffers.");
     if (vec) {
         const norm::VecLayout layout = norm::vec_layout(rows, channels, ensemble);
-        hipLaunchKernelGGL(norm::bn_apply_vec, layout.grid, dim3(256), 0, stream, x, x_stride, use_mean, use_var, w, b,
-                           residual, y, y_bf16, static_cast<long long>(rows), channels, eps, relu, layout.tpr);
+        if (x_bf16)
+            hipLaunchKernelGGL(norm::bn_apply_vec<unsigned short>, layout.grid, dim3(256), 0, stream,
+                               static_cast<const unsigned short*>(x), x_stride, use_mean, use_var, w, b, residual, y,
+                               y_bf16, static_cast<long long>(rows), channels, eps, relu, layout.tpr);
+        else
+            hipLaunchKernelGGL(norm::bn_apply_vec<float>, layout.grid, dim3(256), 0, stream,
+                               static_cast<const float*>(x), x_stride, use_mean, use_var, w, b, residual, y, y_bf16,
+                               static_cast<long long>(rows), channels, eps, relu, layout.tpr);
     } else {
-        hipLaunchKernelGGL(norm::bn_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream, x, x_stride,
-                           use_mean, use_var, w, b, residual, y, y_bf16, static_cast<long long>(rows), channels,
-                           ensemble, eps, relu);
+        hipLaunchKernelGGL(norm::bn_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream,
+                           static_cast<const float*>(x), x_stride, use_mean, use_var, w, b, residual, y, y_bf16,
+                           static_cast<long long>(rows), channels, ensemble, eps, relu);
     }
     check_launch("Launch BN apply");
 }
 
-void bn_backward(int ensemble, const float* x, long long x_stride, const float* dy, const float* y, const float* w,
+void bn_backward(int ensemble, const void* x, int x_bf16, long long x_stride, const void* dy, int dy_bf16,
+                 const float* y, const float* w,
                  const float* b, const float* mean, const float* var, float* partial, float* sums, float* dx, float* dw,
                  float* db,
                  unsigned short* dx_bf16, int rows, int channels, float eps, int training, int relu,
@@ -907,19 +936,36 @@ void bn_backward(int ensemble, const float* x, long long x_stride, const float* 
     require(x && dy && w && mean && var, "BatchNorm backward requires x, dy, weight and statistics.");
     require(!relu || y || b, "ReLU BatchNorm backward requires the output or the bias to recompute it.");
     require(!accumulate_dx || dx, "Accumulating BN input adjoints requires the fp32 adjoint.");
+    const bool narrow = x_bf16 || dy_bf16;
+    // vector kernels: 16-byte fp32 rows, 8-byte bf16 rows
+    const bool vec_inputs = channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, x_bf16 ? 8 : 16) &&
+                            aligned(dy, dy_bf16 ? 8 : 16) && (!y || aligned(y, 16)) && aligned(w, 16) &&
+                            (!b || aligned(b, 16)) && aligned(mean, 16) && aligned(var, 16);
+    require(vec_inputs || !narrow,
+            "bf16 BatchNorm backward inputs need channels and strides in multiples of 4 and aligned buffers.");
     const bool need_sums = training || dw || db;
     if (need_sums) {
         require(partial && sums, "BatchNorm backward requires partial and sums scratch.");
+        require(!narrow || aligned(partial, 16), "BatchNorm partial scratch must be 16-byte aligned.");
         const int chunks = chunks_for(rows);
-        if (channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && aligned(dy, 16) && (!y || aligned(y, 16)) &&
-            aligned(w, 16) && (!b || aligned(b, 16)) && aligned(mean, 16) && aligned(var, 16) && aligned(partial, 16)) {
+        if (vec_inputs && aligned(partial, 16)) {
             const dim3 grid(ceil_div(channels / 4, norm::kVecCols), chunks, ensemble);
-            hipLaunchKernelGGL(norm::bn_grad_partials_vec, grid, dim3(norm::kThreads), 0, stream, x, x_stride, dy, y, w,
-                               b, mean, var, partial, rows, channels, chunks, eps, relu);
+            const auto launch = [&](auto xt, auto dt) {
+                using XT = decltype(xt);
+                using DT = decltype(dt);
+                hipLaunchKernelGGL((norm::bn_grad_partials_vec<XT, DT>), grid, dim3(norm::kThreads), 0, stream,
+                                   static_cast<const XT*>(x), x_stride, static_cast<const DT*>(dy), y, w, b, mean, var,
+                                   partial, rows, channels, chunks, eps, relu);
+            };
+            if (x_bf16 && dy_bf16) launch((unsigned short)0, (unsigned short)0);
+            else if (x_bf16) launch((unsigned short)0, 0.0f);
+            else if (dy_bf16) launch(0.0f, (unsigned short)0);
+            else launch(0.0f, 0.0f);
         } else {
             const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
-            hipLaunchKernelGGL(norm::bn_grad_partials, grid, dim3(norm::kThreads), 0, stream, x, x_stride, dy, y, w, b,
-                               mean, var, partial, rows, channels, chunks, eps, relu);
+            hipLaunchKernelGGL(norm::bn_grad_partials, grid, dim3(norm::kThreads), 0, stream,
+                               static_cast<const float*>(x), x_stride, static_cast<const float*>(dy), y, w, b, mean,
+                               var, partial, rows, channels, chunks, eps, relu);
         }
         check_launch("Launch BN gradient partials");
         hipLaunchKernelGGL(norm::bn_grad_reduce, dim3(ceil_div(ensemble * channels, norm::kStatCols)),
@@ -929,19 +975,28 @@ void bn_backward(int ensemble, const float* x, long long x_stride, const float* 
     }
     if (dx || dx_bf16) {
         const long long total = static_cast<long long>(ensemble) * rows * channels;
-        const bool vec = channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, 16) && aligned(dy, 16) &&
-                         (!y || aligned(y, 16)) && (!dx || aligned(dx, 16)) && (!dx_bf16 || aligned(dx_bf16, 8)) &&
-                         aligned(w, 16) && (!b || aligned(b, 16)) && aligned(mean, 16) && aligned(var, 16) &&
+        const bool vec = vec_inputs && (!dx || aligned(dx, 16)) && (!dx_bf16 || aligned(dx_bf16, 8)) &&
                          (!training || (aligned(sums, 16) && (ensemble * channels) % 4 == 0));
+        require(vec || !narrow, "bf16 BatchNorm backward outputs need aligned buffers and 4-aligned statistics.");
         if (vec) {
             const norm::VecLayout layout = norm::vec_layout(rows, channels, ensemble);
-            hipLaunchKernelGGL(norm::bn_grad_apply_vec, layout.grid, dim3(256), 0, stream, x, x_stride, dy, y, w, b,
-                               mean, var, sums, dx, dx_bf16, static_cast<long long>(rows), channels, ensemble, eps,
-                               training, relu, accumulate_dx, layout.tpr);
+            const auto launch = [&](auto xt, auto dt) {
+                using XT = decltype(xt);
+                using DT = decltype(dt);
+                hipLaunchKernelGGL((norm::bn_grad_apply_vec<XT, DT>), layout.grid, dim3(256), 0, stream,
+                                   static_cast<const XT*>(x), x_stride, static_cast<const DT*>(dy), y, w, b, mean, var,
+                                   sums, dx, dx_bf16, static_cast<long long>(rows), channels, ensemble, eps, training,
+                                   relu, accumulate_dx, layout.tpr);
+            };
+            if (x_bf16 && dy_bf16) launch((unsigned short)0, (unsigned short)0);
+            else if (x_bf16) launch((unsigned short)0, 0.0f);
+            else if (dy_bf16) launch(0.0f, (unsigned short)0);
+            else launch(0.0f, 0.0f);
         } else {
-            hipLaunchKernelGGL(norm::bn_grad_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream, x,
-                               x_stride, dy, y, w, b, mean, var, sums, dx, dx_bf16, static_cast<long long>(rows),
-                               channels, ensemble, eps, training, relu, accumulate_dx);
+            hipLaunchKernelGGL(norm::bn_grad_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream,
+                               static_cast<const float*>(x), x_stride, static_cast<const float*>(dy), y, w, b, mean,
+                               var, sums, dx, dx_bf16, static_cast<long long>(rows), channels, ensemble, eps,
+                               training, relu, accumulate_dx);
         }
         check_launch("Launch BN gradient apply");
     }
@@ -1027,25 +1082,25 @@ void bias_grad(int ensemble, const float* dy, float* db, float* partial, int row
 // Batched entry points (ensemble-aware; x_stride 0 broadcasts one input to
 // every member, as the critic embedder does with its shared input).
 // ---------------------------------------------------------------------------
-RL_API int rl_bn_forward_ex(int ensemble, const float* x, long long x_stride, const float* w, const float* b,
+RL_API int rl_bn_forward_ex(int ensemble, const void* x, int x_bf16, long long x_stride, const float* w, const float* b,
                             float* running_mean, float* running_var, float* mean, float* var, float* partial,
                             const float* residual, float* y, void* y_bf16, int rows, int channels, float eps,
                             float momentum, int training, int relu, int update_running, int moments_ready,
                             void* stream) noexcept {
     return rl::guarded("rl_bn_forward_ex", [&] {
-        rl::bn_forward(ensemble, x, x_stride, w, b, running_mean, running_var, mean, var, partial, residual, y,
+        rl::bn_forward(ensemble, x, x_bf16, x_stride, w, b, running_mean, running_var, mean, var, partial, residual, y,
                        static_cast<unsigned short*>(y_bf16), rows, channels, eps, momentum, training, relu,
                        update_running, moments_ready, rl::as_stream(stream));
     });
 }
 
-RL_API int rl_bn_backward_ex(int ensemble, const float* x, long long x_stride, const float* dy, const float* y,
-                             const float* w, const float* b, const float* mean, const float* var, float* partial,
-                             float* sums, float* dx, float* dw, float* db, void* dx_bf16, int rows, int channels,
+RL_API int rl_bn_backward_ex(int ensemble, const void* x, int x_bf16, long long x_stride, const void* dy,
+                             int dy_bf16, const float* y, const float* w, const float* b, const float* mean,
+                             const float* var, float* partial, float* sums, float* dx, float* dw, float* db, void* dx_bf16, int rows, int channels,
                              float eps, int training, int relu, int accumulate_dx, int accumulate_params,
                              void* stream) noexcept {
     return rl::guarded("rl_bn_backward_ex", [&] {
-        rl::bn_backward(ensemble, x, x_stride, dy, y, w, b, mean, var, partial, sums, dx, dw, db,
+        rl::bn_backward(ensemble, x, x_bf16, x_stride, dy, dy_bf16, y, w, b, mean, var, partial, sums, dx, dw, db,
                         static_cast<unsigned short*>(dx_bf16), rows, channels, eps, training, relu, accumulate_dx,
                         accumulate_params, rl::as_stream(stream));
     });
@@ -1084,7 +1139,7 @@ RL_API int rl_flash_bn_forward(const float* x, const float* w, const float* b, f
                                float* mean, float* var, float* partial, float* y, int batch, int channels, float eps,
                                float momentum, int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_forward", [&] {
-        rl::bn_forward(1, x, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y, nullptr, batch, channels,
+        rl::bn_forward(1, x, 0, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y, nullptr, batch, channels,
                        eps, momentum, training, relu, 1, 0, rl::as_stream(stream));
     });
 }
@@ -1095,7 +1150,7 @@ RL_API int rl_flash_bn_forward_with_bf16(const float* x, const float* w, const f
                                          int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_forward_with_bf16", [&] {
         rl::require(half_output != nullptr, "bf16 BN output must be nonnull.");
-        rl::bn_forward(1, x, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y,
+        rl::bn_forward(1, x, 0, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y,
                        static_cast<unsigned short*>(half_output), batch, channels, eps, momentum, training, relu, 1,
                        0, rl::as_stream(stream));
     });
@@ -1116,7 +1171,7 @@ RL_API int rl_flash_bn_backward(const float* x, const float* dy, const float* y,
                                 const float* var, float* partial, float* sums, float* dx, float* dw, float* db,
                                 int batch, int channels, float eps, int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_backward", [&] {
-        rl::bn_backward(1, x, 0, dy, y, w, nullptr, mean, var, partial, sums, dx, dw, db, nullptr, batch, channels,
+        rl::bn_backward(1, x, 0, 0, dy, 0, y, w, nullptr, mean, var, partial, sums, dx, dw, db, nullptr, batch, channels,
                         eps, training, relu, 1, 1, rl::as_stream(stream));
     });
 }
@@ -1130,7 +1185,7 @@ RL_API int rl_flash_bn_backward_with_fp16(const float* x, const float* dy, const
     return rl::guarded("rl_flash_bn_backward_with_fp16", [&] {
         rl::require(half_dx != nullptr, "16-bit BN input adjoint must be nonnull.");
         rl::require(dx != nullptr, "16-bit BN input adjoint requires an fp32 input adjoint.");
-        rl::bn_backward(1, x, 0, dy, y, w, nullptr, mean, var, partial, sums, dx, dw, db,
+        rl::bn_backward(1, x, 0, 0, dy, 0, y, w, nullptr, mean, var, partial, sums, dx, dw, db,
                         static_cast<unsigned short*>(half_dx), batch, channels, eps, training, relu, 1, 1,
                         rl::as_stream(stream));
     });
@@ -1141,7 +1196,7 @@ RL_API int rl_flash_bn_backward_controlled(const float* x, const float* dy, cons
                                            float* dw, float* db, void* half_dx, int overwrite_dx, int batch,
                                            int channels, float eps, int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_backward_controlled", [&] {
-        rl::bn_backward(1, x, 0, dy, y, w, nullptr, mean, var, partial, sums, dx, dw, db,
+        rl::bn_backward(1, x, 0, 0, dy, 0, y, w, nullptr, mean, var, partial, sums, dx, dw, db,
                         static_cast<unsigned short*>(half_dx), batch, channels, eps, training, relu,
                         overwrite_dx ? 0 : 1, 1, rl::as_stream(stream));
     });

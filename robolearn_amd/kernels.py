@@ -47,7 +47,12 @@ def gemm(
 ):
     """Row-major batched D = act(op(A) op(B) + bias) + beta * C (optional bf16 copy of D,
     per-256-row-chunk column moments of D for a following BatchNorm, and, fp32 mode, the
-    row sums of op(A) over K)."""
+    row sums of op(A) over K).  A bfloat16 d (bf16 mode) receives D rounded to bf16 as the
+    only output."""
+    if d is not None and d.dtype == torch.bfloat16:
+        if d_bf16 is not None or mode != BF16:
+            raise ValueError("A bfloat16 output is the bf16-mode product's only output.")
+        d, d_bf16 = None, d
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _native.call(
         "rl_gemm", mode, _is_bf16(a), _is_bf16(b), int(a_kcontig), int(b_kcontig), m, n, k, batch, ptr(a), lda,
@@ -78,7 +83,7 @@ def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None,
     if x_stride is None:
         x_stride = rows * x_ld
     _check(w, ensemble * out_dim * in_dim, "weight", w.dtype)
-    _check(y, ensemble * rows * out_dim, "output")
+    _check(y, ensemble * rows * out_dim, "output", y.dtype)
     splits = forward_split_count(rows, out_dim, in_dim, ensemble, mode) if workspace is not None else 1
     if splits > 1:
         need = _native.load().rl_gemm_workspace(mode, rows, out_dim, in_dim, ensemble, splits)
@@ -95,7 +100,7 @@ def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=
     """dx[e] = dy[e] w[e] (+ beta c).  wt: optional [ensemble, in_dim, out_dim] transposed copy of w,
     which lets both operands be read K-contiguously.  epilogue "elu_grad" (fp32) multiplies by
     elu'(c), c holding the ELU outputs of the layer below."""
-    _check(dx, ensemble * rows * in_dim, "input gradient")
+    _check(dx, ensemble * rows * in_dim, "input gradient", dx.dtype)
     if wt is not None:
         _check(wt, ensemble * out_dim * in_dim, "transposed weight", wt.dtype)
         gemm(dy, wt, dx, m=rows, n=in_dim, k=out_dim, batch=ensemble, a_kcontig=True, b_kcontig=True, lda=out_dim,
@@ -164,25 +169,27 @@ def linear_backward_weight(dy, x, dw, *, rows, in_dim, out_dim, ensemble=1, x_st
 def bn_forward(x, w, b, running_mean, running_var, mean, var, partial, y, *, rows, channels, ensemble=1,
                x_stride=None, eps=1e-5, momentum=0.01, training=True, relu=False, update_running=True, y_bf16=None,
                residual=None, moments_ready=False):
-    """y = act(BN(x)) [+ residual]; x_stride 0 broadcasts one input to every member.
+    """y = act(BN(x)) [+ residual]; x_stride 0 broadcasts one input to every member; x may
+    be float32 or bfloat16.
 
     moments_ready: partial already holds x's chunk moments (written by the producing GEMM)."""
     if x_stride is None:
         x_stride = rows * channels
-    _native.call("rl_bn_forward_ex", ensemble, ptr(x), x_stride, ptr(w), ptr(b), ptr(running_mean), ptr(running_var),
-                 ptr(mean), ptr(var), ptr(partial), ptr(residual), ptr(y), ptr(y_bf16), rows, channels, eps, momentum,
-                 int(training), int(relu), int(update_running), int(moments_ready), stream())
+    _native.call("rl_bn_forward_ex", ensemble, ptr(x), _is_bf16(x), x_stride, ptr(w), ptr(b), ptr(running_mean),
+                 ptr(running_var), ptr(mean), ptr(var), ptr(partial), ptr(residual), ptr(y), ptr(y_bf16), rows,
+                 channels, eps, momentum, int(training), int(relu), int(update_running), int(moments_ready), stream())
 
 
 def bn_backward(x, dy, y, w, mean, var, partial, sums, dx, dw, db, *, rows, channels, ensemble=1, x_stride=None,
                 eps=1e-5, training=True, relu=False, accumulate_dx=False, accumulate_params=False, dx_bf16=None,
                 b=None):
-    """BN backward; with relu and y=None the ReLU mask is recomputed from x and (w, b)."""
+    """BN backward; with relu and y=None the ReLU mask is recomputed from x and (w, b).  x and
+    dy may be float32 or bfloat16; dx_bf16 may be dy itself (updated in place)."""
     if x_stride is None:
         x_stride = rows * channels
-    _native.call("rl_bn_backward_ex", ensemble, ptr(x), x_stride, ptr(dy), ptr(y), ptr(w), ptr(b), ptr(mean),
-                 ptr(var), ptr(partial), ptr(sums), ptr(dx), ptr(dw), ptr(db), ptr(dx_bf16), rows, channels, eps,
-                 int(training), int(relu), int(accumulate_dx), int(accumulate_params), stream())
+    _native.call("rl_bn_backward_ex", ensemble, ptr(x), _is_bf16(x), x_stride, ptr(dy), _is_bf16(dy), ptr(y), ptr(w),
+                 ptr(b), ptr(mean), ptr(var), ptr(partial), ptr(sums), ptr(dx), ptr(dw), ptr(db), ptr(dx_bf16), rows,
+                 channels, eps, int(training), int(relu), int(accumulate_dx), int(accumulate_params), stream())
 
 
 def rms_forward(x, w, ms, y, *, rows, channels, ensemble=1, eps=1e-6, member_stride=0, y_bf16=None):

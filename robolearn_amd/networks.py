@@ -240,13 +240,21 @@ class Trunk:
         def full(*shape):
             return None if self.bf else buf(*shape)
 
+        # BatchNorm inputs and their gradients: bf16 in bf16 mode, as the Linear
+        # outputs an autocast forward feeds the BatchNorm (the BN kernels need
+        # channels in multiples of 4 for bf16 rows)
+        narrow = self.bf and h % 4 == 0
+
+        def pre_norm(*shape):
+            return torch.zeros(*shape, dtype=torch.bfloat16, device=device) if narrow else buf(*shape)
+
         self.y0, self.y0_h = full(E, R, in_dim), half(E, R, in_dim)
         self.stream = [buf(E, R, h) for _ in range(blocks + 1)]
         self.stream_h = [half(E, R, h) for _ in range(blocks + 1)]
-        self.u1 = [buf(E, R, 4 * h) for _ in range(blocks)]
+        self.u1 = [pre_norm(E, R, 4 * h) for _ in range(blocks)]
         self.r1 = [full(E, R, 4 * h) for _ in range(blocks)]
         self.r1_h = [half(E, R, 4 * h) for _ in range(blocks)]
-        self.u2 = [buf(E, R, h) for _ in range(blocks)]
+        self.u2 = [pre_norm(E, R, h) for _ in range(blocks)]
         self.z, self.z_h = full(E, R, h), half(E, R, h)
         self.ms = buf(E * R)
         self.stats = {}
@@ -254,7 +262,10 @@ class Trunk:
             self.stats[name] = (buf(E, width), buf(E, width))
         self.d_stream, self.d_stream_h = buf(E, R, h), half(E, R, h)
         self.d_u2, self.d_u2_h = full(E, R, h), half(E, R, h)
-        self.d_r1, self.d_r1_h = buf(E, R, 4 * h), half(E, R, 4 * h)
+        # in bf16 mode the product writes the ReLU-BN gradient in bf16 and the BN
+        # backward turns it into the input gradient in place
+        self.d_r1 = pre_norm(E, R, 4 * h)
+        self.d_r1_h = self.d_r1 if narrow else half(E, R, 4 * h)
         self.dy0 = buf(E, R, in_dim)
         self.dz = buf(E, R, h)
         widest = max(4 * h, in_dim)

@@ -311,6 +311,88 @@ def test_gemm_output_moments_match_chunk_moments(gpu, batch, m, n, k, splits, a_
         torch.testing.assert_close(x0, x1, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("batch,m,n,k,splits,a_kcontig,b_kcontig", MOMENT_SHAPES)
+def test_bf16_only_gemm_output(gpu, batch, m, n, k, splits, a_kcontig, b_kcontig):
+    """A bfloat16 output is the bf16 copy of the fp32 product, bit for bit, and its moments
+    are those of the rounded values."""
+    print(f"case bf16-only batch={batch} m={m} n={n} k={k} splits={splits} a_k={a_kcontig} b_k={b_kcontig}",
+          flush=True)
+    g = torch.Generator().manual_seed(5 * m + n)
+    a = (torch.randn(batch, m, k, generator=g) + 0.5).to(torch.bfloat16)
+    b = torch.randn(batch, n, k, generator=g).to(torch.bfloat16)
+    a_mem = (a if a_kcontig else a.transpose(1, 2).contiguous()).to(gpu)
+    b_mem = (b if b_kcontig else b.transpose(1, 2).contiguous()).to(gpu)
+    workspace = torch.empty(splits * batch * m * n * 4, dtype=torch.uint8, device=gpu) if splits > 1 else None
+    chunks = (m + 255) // 256
+    args = dict(m=m, n=n, k=k, batch=batch, a_kcontig=a_kcontig, b_kcontig=b_kcontig, lda=k if a_kcontig else m,
+                ldb=k if b_kcontig else n, ldd=n, stride_a=m * k, stride_b=n * k, stride_d=m * n, mode=K.BF16,
+                splits=splits, workspace=workspace)
+    d = torch.empty(batch, m, n, device=gpu)
+    copy = torch.empty(batch, m, n, dtype=torch.bfloat16, device=gpu)
+    K.gemm(a_mem, b_mem, d, d_bf16=copy, **args)
+    only = torch.full((batch, m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+    moments = torch.full((batch, chunks, 2, n), float("nan"), device=gpu)
+    K.gemm(a_mem, b_mem, only, moments=moments, **args)
+    torch.cuda.synchronize()
+    assert torch.equal(only.cpu().view(torch.int16), copy.cpu().view(torch.int16))
+    expected = _chunk_moments(only.cpu().float())
+    got = moments.cpu().double()
+    torch.testing.assert_close(got[:, :, 0], expected[:, :, 0], rtol=1e-5, atol=1e-4)
+    torch.testing.assert_close(got[:, :, 1], expected[:, :, 1], rtol=1e-5, atol=1e-3)
+
+
+def test_bf16_only_output_needs_bf16_mode(gpu):
+    x = torch.randn(64, 32, device=gpu)
+    w = torch.randn(16, 32, device=gpu)
+    with pytest.raises(ValueError, match="bf16-mode"):
+        K.linear_forward(x, w, torch.empty(64, 16, dtype=torch.bfloat16, device=gpu), rows=64, in_dim=32,
+                         out_dim=16, mode=K.FP32)
+
+
+@pytest.mark.parametrize("ensemble,rows,channels,relu", [(2, 777, 132, True), (1, 512, 1024, True),
+                                                         (2, 300, 64, False)])
+def test_batchnorm_bf16_inputs_match_fp32_path(gpu, ensemble, rows, channels, relu):
+    """bf16 x and dy give the fp32 path's results on the same (widened) values, bit for bit,
+    and the input gradient may overwrite a bf16 dy in place."""
+    print(f"case bn bf16 inputs ensemble={ensemble} rows={rows} channels={channels} relu={relu}", flush=True)
+    x_h = (_rand(ensemble, rows, channels, seed=20, scale=2.0) + 0.5).to(torch.bfloat16).to(gpu)
+    dy_h = _rand(ensemble, rows, channels, seed=21).to(torch.bfloat16).to(gpu)
+    x_f, dy_f = x_h.float(), dy_h.float()
+    w = (_rand(ensemble, channels, seed=22).abs() + 0.5).to(gpu)
+    b = _rand(ensemble, channels, seed=23).to(gpu)
+    results = []
+    for x, dy in ((x_f, dy_f), (x_h, dy_h.clone())):
+        rm, rv = torch.zeros(ensemble, channels, device=gpu), torch.ones(ensemble, channels, device=gpu)
+        mean, var = torch.empty(ensemble, channels, device=gpu), torch.empty(ensemble, channels, device=gpu)
+        partial = torch.empty(ensemble * 2 * K.chunks(rows) * channels, device=gpu)
+        y = torch.empty(ensemble, rows, channels, device=gpu)
+        y_h = torch.empty(ensemble, rows, channels, dtype=torch.bfloat16, device=gpu)
+        K.bn_forward(x, w, b, rm, rv, mean, var, partial, y, rows=rows, channels=channels, ensemble=ensemble,
+                     relu=relu, y_bf16=y_h)
+        sums = torch.empty(2 * ensemble * channels, device=gpu)
+        dw, db = torch.empty_like(mean), torch.empty_like(mean)
+        if dy.dtype == torch.bfloat16:
+            dx, dx_h = None, dy  # in place over the bf16 gradient
+        else:
+            dx, dx_h = torch.empty_like(y), torch.empty_like(y_h)
+        K.bn_backward(x, dy, None, w, mean, var, partial, sums, dx, dw, db, rows=rows, channels=channels,
+                      ensemble=ensemble, relu=relu, b=b, dx_bf16=dx_h)
+        results.append([t.cpu() for t in (y, y_h, mean, var, rm, rv, dw, db, dx_h)])
+    names = ("y", "y_bf16", "mean", "var", "running_mean", "running_var", "dw", "db", "dx_bf16")
+    for name, ref, got in zip(names, *results):
+        assert torch.equal(ref.view(torch.int32) if ref.dtype == torch.float32 else ref.view(torch.int16),
+                           got.view(torch.int32) if got.dtype == torch.float32 else got.view(torch.int16)), name
+
+
+def test_batchnorm_bf16_input_needs_vector_layout(gpu):
+    x = torch.zeros(1, 64, 6, dtype=torch.bfloat16, device=gpu)
+    w, b = torch.ones(1, 6, device=gpu), torch.zeros(1, 6, device=gpu)
+    with pytest.raises(RuntimeError, match="bf16 BatchNorm"):
+        K.bn_forward(x, w, b, torch.zeros(1, 6, device=gpu), torch.ones(1, 6, device=gpu),
+                     torch.empty(1, 6, device=gpu), torch.empty(1, 6, device=gpu),
+                     torch.empty(2 * 6, device=gpu), torch.empty(1, 64, 6, device=gpu), rows=64, channels=6)
+
+
 @pytest.mark.parametrize("batch,rows,cols", [(1, 64, 64), (2, 1024, 4096), (3, 100, 37), (1, 1, 130)])
 def test_transpose16_is_exact(gpu, batch, rows, cols):
     print(f"case transpose16 batch={batch} rows={rows} cols={cols}", flush=True)
