@@ -240,14 +240,13 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
     float* stage = static_cast<float*>(lds) + wave * 32 * EP;
     // Column moments for a BatchNorm that consumes D (identity epilogue only):
     // the tile's 256 rows are one 256-row statistics chunk.  Each lane sees 4
-    // columns x 16 rows of every staged 32-row block: exact two-pass moments of
-    // those 16 rows (the second pass rereads the staged block), merged over the
-    // 4 blocks, then with lane l ^ 32 (the other row parity) and with the wave of
-    // the other row half, always in the same order.
+    // columns x 16 rows of every staged 32-row block as it stores them: sums of
+    // the values shifted by the block's first row give the moments of those 16
+    // rows, merged over the 4 blocks, then with lane l ^ 32 (the other row
+    // parity) and with the wave of the other row half, always in the same order.
     const bool moments = direct && p.moments != nullptr;
-    // a bf16-only output takes the moments of the stored (rounded) values; the
-    // moments epilogue adds nothing to D, so the later rounding is exact
-    const bool round_stage = moments && !D;
+    // a bf16-only output takes the moments of the stored (rounded) values
+    const bool round_moments = moments && !D;
     float count = 0.0f;
     float4 mean = make_float4(0.0f, 0.0f, 0.0f, 0.0f), m2 = mean;
 #pragma unroll
@@ -260,30 +259,9 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v)
-                stage[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * EP + j * 32 + lane % 32] =
-                    round_stage ? bf16_bits_to_f32(f32_to_bf16_bits(acc[i][j][v])) : acc[i][j][v];
+                stage[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * EP + j * 32 + lane % 32] = acc[i][j][v];
         lds_fence();
-        if (moments) {
-            float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            for (int r = 0; r < 16; ++r) {
-                const float4 v = *reinterpret_cast<const float4*>(stage + (2 * r + lane / 32) * EP + 4 * c4);
-                s = make_float4(s.x + v.x, s.y + v.y, s.z + v.z, s.w + v.w);
-            }
-            const float4 bm = make_float4(s.x * (1.0f / 16), s.y * (1.0f / 16), s.z * (1.0f / 16), s.w * (1.0f / 16));
-            float4 q = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            for (int r = 0; r < 16; ++r) {
-                const float4 v = *reinterpret_cast<const float4*>(stage + (2 * r + lane / 32) * EP + 4 * c4);
-                const float4 d = make_float4(v.x - bm.x, v.y - bm.y, v.z - bm.z, v.w - bm.w);
-                q = make_float4(q.x + d.x * d.x, q.y + d.y * d.y, q.z + d.z * d.z, q.w + d.w * d.w);
-            }
-            if (i == 0) {
-                count = 16.0f;
-                mean = bm;
-                m2 = q;
-            } else {
-                merge4(count, mean, m2, 16.0f, bm, q);
-            }
-        }
+        float4 shift = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s1 = shift, s2 = shift;
 #pragma unroll 4
         for (int r = 0; r < 16; ++r) {
             const int row = 2 * r + lane / 32;
@@ -299,14 +277,39 @@ __device__ __forceinline__ void store_tile(const Params& p, const Tile& tile, f3
                     val.z += p.beta * c.z;
                     val.w += p.beta * c.w;
                 }
-                if (Dh)
-                    __builtin_nontemporal_store((u32x2){f32x2_to_bf16x2(val.x, val.y), f32x2_to_bf16x2(val.z, val.w)},
-                                                reinterpret_cast<u32x2*>(Dh + offset));
+                if (Dh) {
+                    const u32x2 packed = {f32x2_to_bf16x2(val.x, val.y), f32x2_to_bf16x2(val.z, val.w)};
+                    __builtin_nontemporal_store(packed, reinterpret_cast<u32x2*>(Dh + offset));
+                    if (round_moments)
+                        val = make_float4(__uint_as_float(packed.x << 16), __uint_as_float(packed.x & 0xffff0000u),
+                                          __uint_as_float(packed.y << 16), __uint_as_float(packed.y & 0xffff0000u));
+                }
+            }
+            if (moments) {  // identity epilogue: val is the stored value
+                if (r == 0) shift = val;
+                const float4 d = make_float4(val.x - shift.x, val.y - shift.y, val.z - shift.z, val.w - shift.w);
+                s1 = make_float4(s1.x + d.x, s1.y + d.y, s1.z + d.z, s1.w + d.w);
+                s2 = make_float4(s2.x + d.x * d.x, s2.y + d.y * d.y, s2.z + d.z * d.z, s2.w + d.w * d.w);
             }
             // streaming stores: nothing in this kernel rereads D, and the tile
             // rounds write far more than the L2 holds
             if (D)
                 __builtin_nontemporal_store((f32x4){val.x, val.y, val.z, val.w}, reinterpret_cast<f32x4*>(D + offset));
+        }
+        if (moments) {
+            const float4 bm = make_float4(shift.x + s1.x * (1.0f / 16), shift.y + s1.y * (1.0f / 16),
+                                          shift.z + s1.z * (1.0f / 16), shift.w + s1.w * (1.0f / 16));
+            const float4 q = make_float4(fmaxf(s2.x - s1.x * s1.x * (1.0f / 16), 0.0f),
+                                         fmaxf(s2.y - s1.y * s1.y * (1.0f / 16), 0.0f),
+                                         fmaxf(s2.z - s1.z * s1.z * (1.0f / 16), 0.0f),
+                                         fmaxf(s2.w - s1.w * s1.w * (1.0f / 16), 0.0f));
+            if (i == 0) {
+                count = 16.0f;
+                mean = bm;
+                m2 = q;
+            } else {
+                merge4(count, mean, m2, 16.0f, bm, q);
+            }
         }
     }
     if (moments) {

@@ -358,44 +358,35 @@ __global__ __launch_bounds__(kRowThreads) void loss_kernel(LossArgs a) {
     }
 }
 
-// Fused minibatch finish: totals[q] = sum_b partial[q, b] (q < 4), the mean KL
-// and the adaptive learning-rate rule (ppo.py:233-238), and the std-parameter
-// gradient dstd[j] = sum_b partial[5 + j, b]; every sum in fixed order.
-constexpr int kFinishGroups = kThreads / kWave;
-
+// Fused minibatch finish over partial [5 + action_dim][blocks]: totals[q] =
+// sum_b partial[q, b] (q < 4), the mean KL from column 4 and the adaptive
+// learning-rate rule (ppo.py:233-238), and the std-parameter gradient dstd[j] =
+// sum_b partial[5 + j, b].  One wave per column: lane l adds blocks l, l + 64,
+// ... in order, then the fixed lane reduction of wave_sum.
 __global__ __launch_bounds__(kThreads) void loss_finish(const float* partial, long long blocks, long long rows,
                                                         int action_dim, float desired_kl, int adapt, float* totals,
                                                         float* kl_out, float* lr, float* dstd) {
-    __shared__ float s[kThreads];
-    for (int q = 0; q < 5; ++q) {
+    const int lane = threadIdx.x % kWave;
+    const int columns = 5 + action_dim;
+    for (int q = threadIdx.x / kWave; q < columns; q += kThreads / kWave) {  // wave-uniform
+        const float* column = partial + q * blocks;
         float v = 0.0f;
-        for (long long i = threadIdx.x; i < blocks; i += kThreads) v += partial[q * blocks + i];
-        v = block_sum(v, s);
-        if (threadIdx.x == 0) {
-            if (q < 4) {
-                totals[q] = v;
-            } else {
-                const float kl = v / static_cast<float>(rows);
-                kl_out[0] = kl;
-                if (adapt) {
-                    if (kl > desired_kl * 2.0f) lr[0] = fmaxf(1.0e-5f, lr[0] / 1.5f);
-                    else if (kl < desired_kl / 2.0f && kl > 0.0f) lr[0] = fminf(1.0e-2f, lr[0] * 1.5f);
-                }
+#pragma unroll 8
+        for (long long b = lane; b < blocks; b += kWave) v += column[b];
+        v = wave_sum(v);
+        if (lane != 0) continue;
+        if (q < 4) {
+            totals[q] = v;
+        } else if (q == 4) {
+            const float kl = v / static_cast<float>(rows);
+            kl_out[0] = kl;
+            if (adapt) {
+                if (kl > desired_kl * 2.0f) lr[0] = fmaxf(1.0e-5f, lr[0] / 1.5f);
+                else if (kl < desired_kl / 2.0f && kl > 0.0f) lr[0] = fminf(1.0e-2f, lr[0] * 1.5f);
             }
+        } else {
+            dstd[q - 5] = v;
         }
-    }
-    // std gradient: column j = t % 64, group g = t / 64 adds blocks g, g + G, ... in order
-    const int j = threadIdx.x % kWave;
-    const int g = threadIdx.x / kWave;
-    float v = 0.0f;
-    if (j < action_dim)
-        for (long long b = g; b < blocks; b += kFinishGroups) v += partial[(5 + j) * blocks + b];
-    s[threadIdx.x] = v;
-    __syncthreads();
-    if (g == 0 && j < action_dim) {
-        float total = s[j];
-        for (int q = 1; q < kFinishGroups; ++q) total += s[q * kWave + j];
-        dstd[j] = total;
     }
 }
 
