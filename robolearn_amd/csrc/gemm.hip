@@ -395,6 +395,48 @@ __global__ void splitk_reduce(const float* work, float* d, unsigned short* d_bf1
     }
 }
 
+// splitk_reduce on four consecutive outputs of a row per thread (n, ldd and the
+// strides multiples of 4; d, c, bias 16-byte and d_bf16 8-byte aligned).
+__global__ void splitk_reduce_vec(const float* work, float* d, unsigned short* d_bf16, const float* c,
+                                  const float* bias, long long ldd, long long stride_d, long long stride_bias, int m,
+                                  int n, int batch, int splits, float beta, int epilogue) {
+    const int n4 = n / 4;
+    const long long total = static_cast<long long>(batch) * m * n4;
+    const long long plane = static_cast<long long>(m) * n;
+    for (long long idx = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; idx < total;
+         idx += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const int col = 4 * static_cast<int>(idx % n4);
+        const int row = static_cast<int>((idx / n4) % m);
+        const int b = static_cast<int>(idx / (static_cast<long long>(m) * n4));
+        const long long within = static_cast<long long>(row) * n + col;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int s = 0; s < splits; ++s) {
+            const float4 w = *reinterpret_cast<const float4*>(work + (static_cast<long long>(s) * batch + b) * plane + within);
+            v = make_float4(v.x + w.x, v.y + w.y, v.z + w.z, v.w + w.w);
+        }
+        const long long offset = b * stride_d + static_cast<long long>(row) * ldd + col;
+        if (epilogue == kEluGrad) {
+            const float4 y = *reinterpret_cast<const float4*>(c + offset);
+            v = make_float4(v.x * elu_grad_from_output(y.x), v.y * elu_grad_from_output(y.y),
+                            v.z * elu_grad_from_output(y.z), v.w * elu_grad_from_output(y.w));
+        } else {
+            if (bias) {
+                const float4 bv = *reinterpret_cast<const float4*>(bias + b * stride_bias + col);
+                v = make_float4(v.x + bv.x, v.y + bv.y, v.z + bv.z, v.w + bv.w);
+            }
+            v = make_float4(apply_epilogue(v.x, epilogue), apply_epilogue(v.y, epilogue),
+                            apply_epilogue(v.z, epilogue), apply_epilogue(v.w, epilogue));
+            if (beta != 0.0f) {
+                const float4 cv = *reinterpret_cast<const float4*>(c + offset);
+                v = make_float4(v.x + beta * cv.x, v.y + beta * cv.y, v.z + beta * cv.z, v.w + beta * cv.w);
+            }
+        }
+        if (d) *reinterpret_cast<float4*>(d + offset) = v;
+        if (d_bf16)
+            *reinterpret_cast<uint2*>(d_bf16 + offset) = make_uint2(f32x2_to_bf16x2(v.x, v.y), f32x2_to_bf16x2(v.z, v.w));
+    }
+}
+
 // Same reduction for many splits: a workgroup covers kReduceCols consecutive
 // outputs with kReduceGroups threads each; group g adds splits g, g + G, ...
 // in order and group 0 adds the group sums in order, so the result is fixed
@@ -600,6 +642,12 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
                                              gemm::kReduceCols)),
                                dim3(256), 0, stream, workspace, d, d_bf16, c, bias, ldd, stride_d, stride_bias, m, n,
                                batch, splits, beta, epilogue, a_sums ? sums_work : nullptr, a_sums, sums_stride);
+        else if (n % 4 == 0 && ldd % 4 == 0 && stride_d % 4 == 0 && aligned(d, 16) && aligned(d_bf16, 8) &&
+                 (!c || aligned(c, 16)) && (!bias || (aligned(bias, 16) && stride_bias % 4 == 0)))
+            hipLaunchKernelGGL(gemm::splitk_reduce_vec,
+                               dim3(static_cast<unsigned>(std::min<long long>((total / 4 + 255) / 256, 4096))),
+                               dim3(256), 0, stream, workspace, d, d_bf16, c, bias, ldd, stride_d, stride_bias, m, n,
+                               batch, splits, beta, epilogue);
         else
             hipLaunchKernelGGL(gemm::splitk_reduce, dim3(blocks), dim3(256), 0, stream, workspace, d, d_bf16, c, bias,
                                ldd, stride_d, stride_bias, m, n, batch, splits, beta, epilogue);

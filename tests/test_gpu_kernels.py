@@ -66,6 +66,33 @@ def test_gemm_epilogues_beta_and_broadcast(gpu):
         torch.testing.assert_close(y.cpu().double(), ref, rtol=1e-5, atol=1e-5)
 
 
+# split-K reductions with every direct-mode epilogue: 4-aligned outputs take the
+# float4 reduction, n = 70 the scalar one; 32 splits over a small output the grouped one
+@pytest.mark.parametrize("mode", [K.FP32, K.FP32_SPLIT, K.BF16])
+@pytest.mark.parametrize("rows,n,k,splits", [(512, 256, 512, 3), (200, 70, 512, 4), (64, 32, 4096, 32)])
+def test_split_k_reduction_epilogues(gpu, mode, rows, n, k, splits):
+    print(f"case split-K epilogues mode={mode} rows={rows} n={n} k={k} splits={splits}", flush=True)
+    x = _rand(2, rows, k, seed=31)
+    w = _rand(2, n, k, seed=32, scale=0.05)
+    bias = _rand(2, n, seed=33)
+    c = _rand(2, rows, n, seed=34)
+    if mode == K.BF16:
+        x, w = x.to(torch.bfloat16), w.to(torch.bfloat16)
+    xd, wd, bd, cd = x.to(gpu), w.to(gpu), bias.to(gpu), c.to(gpu)
+    workspace = torch.empty(splits * 2 * rows * n * 4, dtype=torch.uint8, device=gpu)
+    product = torch.bmm(x.double(), w.double().transpose(1, 2).contiguous())
+    tol = dict(rtol=1e-2, atol=1e-2) if mode == K.BF16 else dict(rtol=1e-5, atol=1e-5 * math.sqrt(k))
+    for epilogue, fn in (("relu", torch.relu), ("elu", torch.nn.functional.elu)):
+        y = torch.empty(2, rows, n, device=gpu)
+        y_h = torch.empty(2, rows, n, dtype=torch.bfloat16, device=gpu)
+        K.gemm(xd, wd, y, m=rows, n=n, k=k, batch=2, a_kcontig=True, b_kcontig=True, lda=k, ldb=k, ldd=n,
+               stride_a=rows * k, stride_b=n * k, stride_d=rows * n, bias=bd, stride_bias=n, epilogue=epilogue,
+               c=cd, beta=0.5, mode=mode, splits=splits, workspace=workspace, d_bf16=y_h)
+        ref = fn(product + bias.double()[:, None, :]) + 0.5 * c.double()
+        torch.testing.assert_close(y.cpu().double(), ref, **tol)
+        assert torch.equal(y_h.cpu().view(torch.int16), y.cpu().to(torch.bfloat16).view(torch.int16))
+
+
 def test_bf16_operand_tensors(gpu):
     rows, k, n = 96, 128, 64
     x = _rand(rows, k, seed=8).to(torch.bfloat16)
@@ -423,7 +450,8 @@ def test_input_gradient_with_transposed_weight(gpu):
     torch.testing.assert_close(dx0.cpu(), dx1.cpu(), rtol=1e-5, atol=tol)
 
 
-@pytest.mark.parametrize("m,n,k,splits", [(300, 130, 77, 1), (2048, 512, 256, 1), (96, 64, 4096, 16)])
+@pytest.mark.parametrize("m,n,k,splits", [(300, 130, 77, 1), (2048, 512, 256, 1), (96, 64, 4096, 16),
+                                          (2048, 512, 1024, 4), (300, 130, 1024, 4)])
 def test_fp32_elu_gradient_epilogue(gpu, m, n, k, splits):
     print(f"case elu_grad epilogue m={m} n={n} k={k} splits={splits}", flush=True)
     g = torch.Generator().manual_seed(m + n + k)
