@@ -549,6 +549,41 @@ __global__ __launch_bounds__(256) void transpose16(const unsigned short* src, un
     }
 }
 
+// transpose16 with 8-byte accesses for rows and cols in multiples of 4 and
+// 8-byte aligned buffers: a load covers 4 columns of one source row, a store 4
+// source rows of one column (one destination row segment).
+__global__ __launch_bounds__(256) void transpose16_vec(const unsigned short* src, unsigned short* dst, int rows,
+                                                       int cols) {
+    __shared__ unsigned short tile[64][66];
+    const long long base = static_cast<long long>(blockIdx.z) * rows * cols;
+    const int r0 = static_cast<int>(blockIdx.y) * 64;
+    const int c0 = static_cast<int>(blockIdx.x) * 64;
+    const int t = static_cast<int>(threadIdx.x);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = i * 16 + t / 16;
+        const int c = 4 * (t % 16);
+        if (r0 + r < rows && c0 + c < cols) {  // cols % 4 == 0: the whole group is in range
+            const uint2 v = *reinterpret_cast<const uint2*>(src + base + static_cast<long long>(r0 + r) * cols + c0 + c);
+            tile[r][c] = static_cast<unsigned short>(v.x & 0xffffu);
+            tile[r][c + 1] = static_cast<unsigned short>(v.x >> 16);
+            tile[r][c + 2] = static_cast<unsigned short>(v.y & 0xffffu);
+            tile[r][c + 3] = static_cast<unsigned short>(v.y >> 16);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = i * 16 + t / 16;
+        const int r = 4 * (t % 16);
+        if (r0 + r < rows && c0 + c < cols) {  // rows % 4 == 0: rows r .. r + 3 are in range
+            const uint2 v = make_uint2(static_cast<unsigned>(tile[r][c]) | (static_cast<unsigned>(tile[r + 1][c]) << 16),
+                                       static_cast<unsigned>(tile[r + 2][c]) | (static_cast<unsigned>(tile[r + 3][c]) << 16));
+            *reinterpret_cast<uint2*>(dst + base + static_cast<long long>(c0 + c) * rows + r0 + r) = v;
+        }
+    }
+}
+
 }  // namespace gemm
 
 // Row-major batched GEMM with optional split-K.  See the header for the
@@ -709,8 +744,10 @@ RL_API int rl_transpose16(const void* src, void* dst, int batch, int rows, int c
         rl::require(batch > 0 && rows > 0 && cols > 0 && batch <= 65535 && (rows + 63) / 64 <= 65535,
                     "Transpose dimensions are invalid.");
         const dim3 grid(rl::ceil_div(cols, 64), rl::ceil_div(rows, 64), static_cast<unsigned>(batch));
-        hipLaunchKernelGGL(rl::gemm::transpose16, grid, dim3(256), 0, rl::as_stream(stream),
-                           static_cast<const unsigned short*>(src), static_cast<unsigned short*>(dst), rows, cols);
+        const bool vec = rows % 4 == 0 && cols % 4 == 0 && rl::aligned(src, 8) && rl::aligned(dst, 8);
+        hipLaunchKernelGGL(vec ? rl::gemm::transpose16_vec : rl::gemm::transpose16, grid, dim3(256), 0,
+                           rl::as_stream(stream), static_cast<const unsigned short*>(src),
+                           static_cast<unsigned short*>(dst), rows, cols);
         rl::check_launch("Launch transpose");
     });
 }

@@ -420,7 +420,8 @@ def test_batchnorm_bf16_input_needs_vector_layout(gpu):
                      torch.empty(2 * 6, device=gpu), torch.empty(1, 64, 6, device=gpu), rows=64, channels=6)
 
 
-@pytest.mark.parametrize("batch,rows,cols", [(1, 64, 64), (2, 1024, 4096), (3, 100, 37), (1, 1, 130)])
+@pytest.mark.parametrize("batch,rows,cols", [(1, 64, 64), (2, 1024, 4096), (3, 100, 37), (1, 1, 130), (2, 100, 36),
+                                             (1, 132, 260)])
 def test_transpose16_is_exact(gpu, batch, rows, cols):
     print(f"case transpose16 batch={batch} rows={rows} cols={cols}", flush=True)
     g = torch.Generator().manual_seed(rows * cols)
