@@ -109,10 +109,21 @@ __global__ __launch_bounds__(kStatCols* kStatGroups) void bn_statistics(const fl
     const int c = live ? idx % channels : 0;
     float count = 0.0f, mean = 0.0f, m2 = 0.0f;
     if (live) {
-        for (int k = group; k < chunks; k += kStatGroups) {
-            const float* in = partial + (static_cast<long long>(e) * chunks + k) * 2 * channels;
-            const float n = static_cast<float>(min(kChunk, rows - k * kChunk));
-            merge(count, mean, m2, n, in[c], in[channels + c]);
+        // chunks group, group + G, ... merged in order; four chunks' loads are
+        // issued ahead of their merges
+        for (int k0 = group; k0 < chunks; k0 += 4 * kStatGroups) {
+            float cm[4], cq[4], cn[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int k = k0 + u * kStatGroups;
+                const bool ok = k < chunks;
+                const float* in = partial + (static_cast<long long>(e) * chunks + (ok ? k : 0)) * 2 * channels;
+                cm[u] = ok ? in[c] : 0.0f;
+                cq[u] = ok ? in[channels + c] : 0.0f;
+                cn[u] = ok ? static_cast<float>(min(kChunk, rows - k * kChunk)) : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) merge(count, mean, m2, cn[u], cm[u], cq[u]);
         }
     }
     __shared__ float s_count[kStatGroups][kStatCols], s_mean[kStatGroups][kStatCols], s_m2[kStatGroups][kStatCols];
@@ -477,6 +488,7 @@ __global__ __launch_bounds__(kStatCols* kStatGroups) void bn_grad_reduce(const f
     const int c = live ? idx % channels : 0;
     float s0 = 0.0f, s1 = 0.0f;
     if (live) {
+#pragma unroll 4
         for (int k = group; k < chunks; k += kStatGroups) {
             const float* in = partial + (static_cast<long long>(e) * chunks + k) * 2 * channels;
             s0 += in[c];
