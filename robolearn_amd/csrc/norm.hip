@@ -184,6 +184,14 @@ inline VecLayout vec_layout(long long rows, int channels, int ensemble) {
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+// 16-byte load when ok, zeros otherwise.  A branch: a conditional expression
+// over float4 lvalues compiles to a select between the global address and a
+// private zero, which turns the load into four flat dword loads.
+__device__ __forceinline__ float4 ld4_if(bool ok, const float* p) {
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (ok) v = *reinterpret_cast<const float4*>(p);
+    return v;
+}
 // four bf16 values (8-byte aligned) widened to fp32
 __device__ __forceinline__ float4 ld4(const unsigned short* p) {
     const uint2 u = *reinterpret_cast<const uint2*>(p);
@@ -608,7 +616,7 @@ __global__ __launch_bounds__(256) void rms_forward_vec(const float* x, const flo
 #pragma unroll
     for (int i = 0; i < V; ++i) {
         const int c = 4 * (lane + kWave * i);
-        v[i] = c < channels ? *reinterpret_cast<const float4*>(x + base + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[i] = ld4_if(c < channels, x + base + c);
         s += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
     }
     s = wave_sum(s) / static_cast<float>(channels);
@@ -643,10 +651,9 @@ __global__ __launch_bounds__(256) void rms_dx_vec(const float* x, const float* d
 #pragma unroll
     for (int i = 0; i < V; ++i) {
         const int c = 4 * (lane + kWave * i);
-        const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        xv[i] = c < channels ? *reinterpret_cast<const float4*>(x + base + c) : zero;
-        const float4 g = c < channels ? *reinterpret_cast<const float4*>(dy + base + c) : zero;
-        const float4 wv = c < channels ? *reinterpret_cast<const float4*>(we + c) : zero;
+        xv[i] = ld4_if(c < channels, x + base + c);
+        const float4 g = ld4_if(c < channels, dy + base + c);
+        const float4 wv = ld4_if(c < channels, we + c);
         gw[i] = make_float4(g.x * wv.x, g.y * wv.y, g.z * wv.z, g.w * wv.w);
         s += gw[i].x * xv[i].x + gw[i].y * xv[i].y + gw[i].z * xv[i].z + gw[i].w * xv[i].w;
     }
@@ -694,7 +701,7 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void rms_backward_fused(const 
 #pragma unroll
     for (int i = 0; i < V; ++i) {
         const int c = 4 * (lane + kWave * i);
-        wv[i] = c < channels ? *reinterpret_cast<const float4*>(we + c) : zero;
+        wv[i] = ld4_if(c < channels, we + c);
         acc[i] = zero;
     }
     const int r_end = min(rows, (chunk + 1) * kChunk);
@@ -709,8 +716,8 @@ __global__ __launch_bounds__(kFusedWaves * kWave) void rms_backward_fused(const 
             for (int i = 0; i < V; ++i) {
                 const int c = 4 * (lane + kWave * i);
                 const bool ok = live && c < channels;
-                xv[q][i] = ok ? *reinterpret_cast<const float4*>(x + base + c) : zero;
-                gv[q][i] = ok ? *reinterpret_cast<const float4*>(dy + base + c) : zero;
+                xv[q][i] = ld4_if(ok, x + base + c);
+                gv[q][i] = ld4_if(ok, dy + base + c);
             }
         }
 #pragma unroll
