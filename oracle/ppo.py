@@ -17,11 +17,15 @@ Parity pinning: GAE, advantage normalization and the loss with its gradients
 are pinned by the reference's known-answer tests (tests/test_warp_ppo.py:23-119,
 restated in tests/test_oracle.py); the KL expression by the closed form of the
 Gaussian KL; Adam by torch.optim.Adam itself; the rollout log-prob by
-torch.distributions.Normal.log_prob of the same actions.  Combined (non-separate)
-gradient clipping follows Warp-NN's Adam ``max_norm`` option, whose source is
-not in the reference tree: parity unpinned for that mode (the separate-group
-mode's formula is visible at ppo.py:249-252 and is the one the tests use).
-The minibatch permutation is injected (the device one is read back).
+torch.distributions.Normal.log_prob of the same actions.  Gradient clipping
+(``clip_gradients``) is pinned by its closed form in tests/test_oracle.py: below
+the threshold the gradients are unchanged, above it the post-clip norm is
+max_norm ||g|| / (||g|| + 1e-6), for one group and for the combined group.
+The combined (non-separate) mode applies that rule to all parameters as one
+group, standing in for Warp-NN's Adam ``max_norm`` option, whose source is not
+in the reference tree (warp-nn 0.4.0, uv.lock:1244-1245): where Warp-NN places
+its epsilon stays parity unpinned.  The minibatch permutation is injected (the
+device one is read back).
 """
 
 import math
@@ -138,6 +142,13 @@ def gaussian_kl(old_mean, old_std, mean, std):
     return (0.5 * (ratio * ratio + delta * delta - 1.0) - torch.log(ratio)).sum(-1)
 
 
+def clip_gradients(params, max_norm: float) -> float:
+    """g <- g * min(1, max_norm / (||g|| + 1e-6)) over one group (robolearn/warp/ppo.py:241-252,
+    676-693, the separate-group form; the combined form clips all parameters as one group with the
+    same rule, as Warp-NN's Adam(max_norm) is used at ppo.py:431-437).  Returns ||g|| before clipping."""
+    return float(torch.nn.utils.clip_grad_norm_(params, max_norm))
+
+
 class PPOOracle:
     def __init__(self, observation_dim, action_dim, num_envs, horizon, cfg, parameters, dtype=torch.float64):
         self.cfg = cfg
@@ -189,10 +200,10 @@ class PPOOracle:
                 self.optimizer.zero_grad()
                 loss.backward()
                 if cfg.separate_grad_clipping:
-                    torch.nn.utils.clip_grad_norm_(self.actor + [self.std_parameter], cfg.max_grad_norm)
-                    torch.nn.utils.clip_grad_norm_(self.critic, cfg.max_grad_norm)
+                    clip_gradients(self.actor + [self.std_parameter], cfg.max_grad_norm)
+                    clip_gradients(self.critic, cfg.max_grad_norm)
                 else:
-                    torch.nn.utils.clip_grad_norm_(self.params, cfg.max_grad_norm)
+                    clip_gradients(self.params, cfg.max_grad_norm)
                 self.optimizer.step()
                 self.last.update(loss=loss.item(), policy_loss=policy.item(), value_loss=value_loss.item(),
                                  entropy=entropy.item())

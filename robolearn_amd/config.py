@@ -55,32 +55,28 @@ class FlashSACConfig:
     load_reward_normalizer: bool = True
 
     def __post_init__(self):
-        if (
-            min(
-                self.buffer_max_length,
-                self.buffer_min_length,
-                self.sample_batch_size,
-                self.n_step,
-                self.actor_update_period,
-                self.learning_rate_decay_step,
-            )
-            <= 0
-        ):
-            raise ValueError("Buffer sizes, batch size, horizons, and update periods must be positive.")
-        if self.buffer_min_length > self.buffer_max_length:
-            raise ValueError("Replay warmup cannot exceed buffer capacity.")
-        if not 0 <= self.gamma <= 1:
-            raise ValueError("gamma must be in [0, 1].")
-        if self.critic_num_bins < 2 or self.critic_min_v >= self.critic_max_v:
-            raise ValueError("The categorical critic needs at least two bins and an increasing support.")
+        # Same acceptance conditions as robolearn/flashsac/config.py:59-79, checked field by field
+        # so the message names the offending field.
+        for field_name in ("buffer_max_length", "buffer_min_length", "sample_batch_size", "n_step",
+                           "actor_update_period", "learning_rate_decay_step"):
+            if getattr(self, field_name) <= 0:
+                raise ValueError(f"FlashSACConfig.{field_name} must be a positive integer, "
+                                 f"got {getattr(self, field_name)}.")
+        if self.buffer_max_length < self.buffer_min_length:
+            raise ValueError(f"FlashSACConfig.buffer_min_length ({self.buffer_min_length}) is larger than the "
+                             f"replay capacity buffer_max_length ({self.buffer_max_length}).")
+        if self.gamma < 0 or self.gamma > 1:
+            raise ValueError(f"FlashSACConfig.gamma={self.gamma} lies outside [0, 1].")
+        if self.critic_num_bins < 2:
+            raise ValueError(f"FlashSACConfig.critic_num_bins={self.critic_num_bins}: a categorical critic "
+                             "needs two or more bins.")
+        if not self.critic_min_v < self.critic_max_v:
+            raise ValueError(f"FlashSACConfig value support [{self.critic_min_v}, {self.critic_max_v}] "
+                             "is empty or reversed.")
 
-    @property
-    def device_type(self) -> str:
-        return self.device
-
-    @property
-    def buffer_device_type(self) -> str:
-        return self.buffer_device or self.device
+    # Device accessors of the reference config (robolearn/flashsac/config.py:81-87).
+    device_type = property(lambda self: self.device)
+    buffer_device_type = property(lambda self: self.buffer_device if self.buffer_device else self.device)
 
 
 @dataclass(frozen=True)

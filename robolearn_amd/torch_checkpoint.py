@@ -161,6 +161,13 @@ def load(agent, path) -> None:
     metadata = json.loads((directory / "config.json").read_text())
     if metadata["observation_dim"] != agent.observation_dim or metadata["action_dim"] != agent.action_dim:
         raise ValueError("Checkpoint observation/action dimensions differ from this agent.")
+    # agent.py:532 records the critic width only for asymmetric observations; a mismatch
+    # would surface in the reference as a shape error on the critic embedder
+    saved_critic_dim = metadata.get("critic_observation_dim")
+    expected_critic_dim = agent.critic_observation_dim if cfg.asymmetric_observation else None
+    if saved_critic_dim != expected_critic_dim:
+        raise ValueError(f"Checkpoint critic_observation_dim {saved_critic_dim} differs from this agent's "
+                         f"{expected_critic_dim}.")
     state = agent.state_dict(include_replay=False)
 
     def put(key, value):
@@ -224,7 +231,11 @@ def load(agent, path) -> None:
         counters = np.asarray(state["update_counters"]).copy()
         counters[0] = int(agent_state["update_step"])
         state["update_counters"] = counters
-    if cfg.normalize_reward and cfg.load_reward_normalizer and (directory / "reward_normalizer.pt").exists():
+    if cfg.normalize_reward and cfg.load_reward_normalizer:
+        # the reference opens reward_normalizer.pt unconditionally here (agent.py:570-572)
+        if not (directory / "reward_normalizer.pt").exists():
+            raise FileNotFoundError(f"{directory / 'reward_normalizer.pt'} is missing; set load_reward_normalizer="
+                                    "False to keep this agent's reward statistics.")
         normalizer = _load(directory / "reward_normalizer.pt")
         put("normalizer.maximum", torch.as_tensor(normalizer["G_r_max"]).reshape(1))
         put("normalizer.running", torch.stack([torch.as_tensor(normalizer[k]).reshape(()).float()

@@ -302,6 +302,34 @@ def test_ppo_loss_and_gradients_match_reference_known_answer():
         np.testing.assert_allclose(grad.numpy(), numerical, atol=1e-7, rtol=1e-6)
 
 
+@pytest.mark.parametrize("scale", [1e-3, 0.5, 3.0, 40.0])
+def test_ppo_gradient_clipping_closed_form(scale):
+    """clip_gradients (robolearn/warp/ppo.py:241-252, 676-693): unchanged below the threshold; above it
+    g * max_norm / (||g|| + 1e-6), so the post-clip norm is max_norm ||g|| / (||g|| + 1e-6).  Checked for
+    one group and for the combined group of several tensors (the c3 default)."""
+    g = torch.Generator().manual_seed(int(scale * 1000))
+    max_norm = 1.0
+    shapes = [(7, 3), (3,), (5, 7), (1,)]
+    params = [torch.nn.Parameter(torch.randn(s, generator=g, dtype=torch.float64)) for s in shapes]
+    grads = [torch.randn(s, generator=g, dtype=torch.float64) for s in shapes]
+    total = math.sqrt(sum(float((x * x).sum()) for x in grads))
+    grads = [x * (scale / total) for x in grads]
+    norm = math.sqrt(sum(float((x * x).sum()) for x in grads))
+    for p, x in zip(params, grads):
+        p.grad = x.clone()
+    returned = OP.clip_gradients(params, max_norm)
+    assert returned == pytest.approx(norm, rel=1e-12)
+    after = math.sqrt(sum(float((p.grad * p.grad).sum()) for p in params))
+    if norm + 1e-6 <= max_norm:
+        for p, x in zip(params, grads):
+            assert torch.equal(p.grad, x)
+    else:
+        assert after == pytest.approx(max_norm * norm / (norm + 1e-6), rel=1e-12)
+        coefficient = max_norm / (norm + 1e-6)
+        for p, x in zip(params, grads):
+            torch.testing.assert_close(p.grad, x * coefficient, rtol=1e-14, atol=0)
+
+
 def test_gaussian_kl_closed_form():
     old_mean, new_mean = torch.tensor([[0.3]]), torch.tensor([[-0.1]])
     old_std, new_std = torch.tensor([[0.7]]), torch.tensor([[1.2]])
