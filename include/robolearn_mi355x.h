@@ -186,6 +186,16 @@ int rl_flash_bn_forward_with_fp16(const float* x, const float* w, const float* b
                                   float* running_var, float* mean, float* var, float* partial, float* y,
                                   void* half_output, int batch, int channels, float eps, float momentum,
                                   int training, int relu, void* stream);
+/* No counterpart in the reference: rl_flash_bn_forward for callers that cannot
+ * allocate (code under stream capture, serving loops, harnesses that forbid
+ * hipMalloc).  The chunk moments that rl_flash_bn_forward keeps in the caller's
+ * `partial` live in a static device array of 2^21 floats (8 MiB) that each GPU
+ * holds until the process ends; training mode needs 2 * ceil(batch / 256) *
+ * channels <= 2^21 and refuses larger shapes with -1 before any launch.  No
+ * hipMalloc, no hipFree.  Calls that overlap on one GPU share the array and race. */
+int rl_flash_bn_forward_static(const float* x, const float* w, const float* b, float* running_mean,
+                               float* running_var, float* mean, float* var, float* y, int batch, int channels,
+                               float eps, float momentum, int training, int relu, void* stream);
 int rl_flash_bn_backward(const float* x, const float* dy, const float* y, const float* w, const float* mean,
                          const float* var, float* partial, float* sums, float* dx, float* dw, float* db, int batch,
                          int channels, float eps, int training, int relu, void* stream);

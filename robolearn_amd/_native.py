@@ -77,6 +77,7 @@ SIGNATURES = {
     "rl_flash_bn_forward": (c_int, [P] * 9 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),
     "rl_flash_bn_forward_with_bf16": (c_int, [P] * 10 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),
     "rl_flash_bn_forward_with_fp16": (c_int, [P] * 10 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),
+    "rl_flash_bn_forward_static": (c_int, [P] * 8 + [c_int, c_int, c_float, c_float, c_int, c_int, P]),
     "rl_flash_bn_backward_with_fp16": (c_int, [P] * 12 + [c_int, c_int, c_float, c_int, c_int, P]),
     "rl_flash_bn_backward": (c_int, [P] * 11 + [c_int, c_int, c_float, c_int, c_int, P]),
     "rl_flash_bn_backward_controlled": (c_int, [P] * 12 + [c_int, c_int, c_int, c_float, c_int, c_int, P]),

@@ -20,6 +20,7 @@
 
 #include <cmath>
 #include <initializer_list>
+#include <mutex>
 
 namespace rl {
 namespace norm {
@@ -1160,6 +1161,65 @@ RL_API int rl_flash_bn_forward(const float* x, const float* w, const float* b, f
     return rl::guarded("rl_flash_bn_forward", [&] {
         rl::bn_forward(1, x, 0, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y, nullptr, batch, channels,
                        eps, momentum, training, relu, 1, 0, rl::as_stream(stream));
+    });
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation BatchNorm forward for callers that cannot allocate (code under
+// stream capture, serving loops, harnesses that forbid hipMalloc).  The chunk
+// moments that rl_flash_bn_forward keeps in the caller's `partial` live in
+// this file-scope device array instead.  Every GPU holds its own copy of the
+// array for the life of the process; host code reaches it only through the
+// device address hipGetSymbolAddress returns (looked up once per device), never
+// through the symbol itself.  The moments are fully written before they are
+// read, so nothing needs clearing.  Calls that overlap on one GPU share the
+// array and race.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr long long kScratchFloats = 2LL << 20;  // 8 MiB: 2 * ceil(batch / 256) * channels floats at most
+constexpr int kMaxDevices = 64;
+
+__device__ __align__(256) float scratch[kScratchFloats];
+
+std::mutex scratch_mutex;
+float* scratch_address[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, resolved on first use.
+float* device_scratch() {
+    int device = -1;
+    rl::check_hip(hipGetDevice(&device), "Query the current device");
+    rl::require(device >= 0 && device < kMaxDevices, "Device ordinal outside the no-allocation scratch table.");
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (!scratch_address[device]) {
+        void* address = nullptr;
+        rl::check_hip(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)), "Resolve the BatchNorm scratch array");
+        rl::require(address != nullptr, "The BatchNorm scratch array has no device address.");
+        scratch_address[device] = static_cast<float*>(address);
+    }
+    return scratch_address[device];
+}
+
+}  // namespace
+
+RL_API int rl_flash_bn_forward_static(const float* x, const float* w, const float* b, float* running_mean,
+                                      float* running_var, float* mean, float* var, float* y, int batch, int channels,
+                                      float eps, float momentum, int training, int relu, void* stream) noexcept {
+    return rl::guarded("rl_flash_bn_forward_static", [&] {
+        float* partial = nullptr;
+        if (training) {
+            rl::require(batch > 0 && channels > 0, "BatchNorm dimensions must be positive.");
+            const long long need = 2LL * rl::chunks_for(batch) * channels;
+            if (need > kScratchFloats) {
+                rl::set_error("rl_flash_bn_forward_static: batch %d x channels %d needs %lld scratch floats "
+                              "(2 * ceil(batch / 256) * channels); the static scratch holds %lld.",
+                              batch, channels, need, kScratchFloats);
+                throw rl::Failure{};
+            }
+            partial = device_scratch();
+        }
+        rl::bn_forward(1, x, 0, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y, nullptr, batch,
+                       channels, eps, momentum, training, relu, 1, 0, rl::as_stream(stream));
     });
 }
 
