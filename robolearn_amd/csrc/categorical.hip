@@ -870,14 +870,37 @@ RL_API int rl_flash_categorical_forward(const void* raw, const void* bias, const
     });
 }
 
+namespace rl {
+namespace cat {
+// dbias[j] += sum over rows of scratch[row][j]: one workgroup per bin, a strided
+// per-thread sum then a fixed-order tree (the reference's bias_gradient shape,
+// robolearn/cuda/kernels.cu:237-251).
+__global__ __launch_bounds__(256) void bias_accumulate(const float* scratch, float* dbias, long long rows, int bins) {
+    __shared__ float partial[256];
+    const int j = blockIdx.x;
+    float s = 0.0f;
+    for (long long r = threadIdx.x; r < rows; r += 256) s += scratch[r * bins + j];
+    partial[threadIdx.x] = s;
+    __syncthreads();
+    for (int offset = 128; offset > 0; offset >>= 1) {
+        if (static_cast<int>(threadIdx.x) < offset) partial[threadIdx.x] += partial[threadIdx.x + offset];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) dbias[j] += partial[0];
+}
+}  // namespace cat
+}  // namespace rl
+
 // Scratch receives the per-row logit gradients (batch x bins) whenever dbias
-// is requested; the bias gradient is accumulated from it in fixed row order.
+// is requested; the bias gradient is then accumulated from it (dbias += column
+// sums), as the reference entry point does.  draw accumulates too.
 RL_API int rl_flash_categorical_backward(const void* log_probs, const void* support, const void* dlog_probs,
                                          const void* dvalues, void* scratch, void* draw, void* dbias, int batch,
                                          int bins, void* stream) noexcept {
     return rl::guarded("rl_flash_categorical_backward", [&] {
-        rl::require(log_probs && support && (draw || dbias) && (!dbias || scratch) && batch >= 1 && bins >= 2,
-                    "Categorical backward requires FP32 buffers, gradients and valid dimensions.");
+        rl::require(log_probs && support && (draw || dbias) && (!dbias || scratch) && batch >= 1 && bins >= 2 &&
+                        bins <= kMaxBins,
+                    "Categorical backward requires FP32 buffers, gradients and 2..512 bins.");
         const hipStream_t st = rl::as_stream(stream);
         hipLaunchKernelGGL(rl::cat::head_backward, dim3(rl::ceil_div(batch, rl::cat::kWaves)), dim3(rl::cat::kThreads),
                            0, st, static_cast<const float*>(log_probs), static_cast<const float*>(support),
@@ -885,8 +908,13 @@ RL_API int rl_flash_categorical_backward(const void* log_probs, const void* supp
                            static_cast<float*>(draw), dbias ? static_cast<float*>(scratch) : nullptr,
                            static_cast<long long>(batch), bins, 1);
         rl::check_launch("Launch categorical backward");
+        if (dbias) {
+            hipLaunchKernelGGL(rl::cat::bias_accumulate, dim3(bins), dim3(256), 0, st,
+                               static_cast<const float*>(scratch), static_cast<float*>(dbias),
+                               static_cast<long long>(batch), bins);
+            rl::check_launch("Launch categorical bias gradient");
+        }
     });
-    // dbias accumulation is issued by rl_bias_grad on the scratch rows.
 }
 
 RL_API int rl_flash_categorical_target(const void* q, const void* log_probs, const void* reward,

@@ -208,7 +208,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
     constexpr int SumLanes = kThreads / T;
     constexpr int SumPer = kFp32K / SumLanes;
     const bool row_sums = p.a_sums != nullptr && bx == 0;
-    float a_sum = 0.0f;
+    // compensated (Kahan) accumulation: bias gradients are sums over thousands of
+    // rows whose terms largely cancel, where plain sequential fp32 sums lose digits
+    float a_sum = 0.0f, a_comp = 0.0f;
+    const auto add_sum = [&](float x) {
+        const float y = x - a_comp;
+        const float t = a_sum + y;
+        a_comp = (t - a_sum) - y;
+        a_sum = t;
+    };
 
     // B is indexed (n, k) when BK else (k, n); the loader wants (row=n, k).
     // Mode 2 takes the row sums from the staged fp32 registers (M-contiguous A only).
@@ -217,7 +225,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
             la.store_split(ha);
             lb.store_split(hb);
             if constexpr (!AK) {
-                if (row_sums) a_sum += la.sum();
+                if (row_sums) {
+#pragma unroll
+                    for (int e = 0; e < decltype(la)::Count; ++e) add_sum(la.regs[e]);
+                }
             }
         } else {
             la.store(sa);
@@ -287,7 +298,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
         if (row_sums) {
             const float* q = sa + (threadIdx.x / SumLanes) * kFp32Pitch + (threadIdx.x % SumLanes) * SumPer;
 #pragma unroll
-            for (int e = 0; e < SumPer; ++e) a_sum += q[e];
+            for (int e = 0; e < SumPer; ++e) add_sum(q[e]);
         }
 #pragma unroll
         for (int s = 0; s < 8; ++s) {

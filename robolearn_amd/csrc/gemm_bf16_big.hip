@@ -560,6 +560,281 @@ __global__ __launch_bounds__(T, 1) void gemm_dma_kernel(Params p, int tiles_m, i
     }
 }
 
+// ---------------------------------------------------------------------------
+// Forward products, eight-wave form: the same 256x256 output tile, now split
+// over 8 waves (two per SIMD) of 128x64 outputs each, 64-deep K tiles (one
+// full 128-byte row segment per operand row, so each DMA fetches whole cache
+// lines) in two 64 KB LDS stages.  With two waves per SIMD the matrix core of a
+// SIMD is fed by one wave while the other waits on LDS, and within a wave the
+// fragments of the next 16-deep sub-step are read while the MFMAs of the
+// current one run.  The epilogue stages each wave's 32x64 blocks through LDS
+// and writes 8 consecutive columns per lane (32-byte fp32 / 16-byte bf16 row
+// pieces); per-column BatchNorm chunk moments are accumulated from the stored
+// values, merged across the 8 lane groups of a wave with butterflies (the lower
+// lane always first) and across the two row halves of the tile through LDS.
+// ---------------------------------------------------------------------------
+namespace wide {
+
+constexpr int NW = 8;                 // waves per workgroup
+constexpr int WTM = 128, WTN = 64;    // wave tile
+constexpr int MI = WTM / 32, NJ = WTN / 32;
+constexpr int BK = 64;                // K depth per stage
+constexpr int CPR = BK / 8;           // 16-byte chunks per LDS row
+constexpr int RPI = 64 / CPR;         // rows per DMA instruction
+constexpr int IPW = 4 * CPR / NW;     // DMA instructions per operand per wave per stage
+constexpr int STAGE = (BM + BN) * BK; // bf16 elements per stage
+constexpr int EP = WTN + 4;           // epilogue staging pitch (floats)
+constexpr int LPR = WTN / 8;          // lanes per staged row (8 floats each)
+constexpr int RPP = kWave / LPR;      // staged rows per pass
+static_assert(NW * 32 * EP * 4 <= 2 * STAGE * 2, "epilogue staging fits the two stages");
+
+// Chunk slot of a 16-byte k chunk in LDS row `row`: rows r and r + 1 differ in
+// their 128-byte bank alignment and rows r ^ 2i in the XOR, so the 16 rows that
+// one ds_read_b128 phase touches hit 16 distinct 4-bank groups.
+__device__ __forceinline__ int slot_of(int row) { return (row >> 1) & 7; }
+
+__device__ __forceinline__ void fetch(const unsigned short* A, const unsigned short* B, long long lda, long long ldb,
+                                      int m0, int n0, int k0, unsigned short* stage, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+        const int q = wave * IPW + j;
+        const int row = q * RPI + lane / CPR;
+        const int chunk = (lane % CPR) ^ slot_of(row);
+        __builtin_amdgcn_global_load_lds(
+            (__attribute__((address_space(1))) void*)(A + static_cast<long long>(m0 + row) * lda + k0 + chunk * 8),
+            (__attribute__((address_space(3))) void*)(stage + q * 512), 16, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+        const int q = wave * IPW + j;
+        const int row = q * RPI + lane / CPR;
+        const int chunk = (lane % CPR) ^ slot_of(row);
+        __builtin_amdgcn_global_load_lds(
+            (__attribute__((address_space(1))) void*)(B + static_cast<long long>(n0 + row) * ldb + k0 + chunk * 8),
+            (__attribute__((address_space(3))) void*)(stage + BM * BK + q * 512), 16, 0, 0);
+    }
+}
+
+// Chan merge of (count, mean, M2) of 8 columns: first (in place) with second.
+__device__ __forceinline__ void merge8(float& count, float (&mean)[8], float (&m2)[8], float count_b,
+                                       const float (&mean_b)[8], const float (&m2_b)[8]) {
+    const float total = count + count_b;
+    const float fb = count_b / total;
+    const float fab = count * count_b / total;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float d = mean_b[e] - mean[e];
+        mean[e] += d * fb;
+        m2[e] += m2_b[e] + d * d * fab;
+    }
+    count = total;
+}
+
+__global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int tiles_m, int tiles_n, int total) {
+    __shared__ __attribute__((aligned(16))) unsigned short lds[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) float exchange[2 * BN];  // (mean, M2) of the second row half
+    const int G = static_cast<int>(gridDim.x);
+    const int b = static_cast<int>(blockIdx.x);
+    const int slot = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int wm = wave / (BN / WTN);
+    const int wn = wave % (BN / WTN);
+    const int sw = slot_of(lane % 32);
+    const bool direct = p.splits == 1;
+
+    for (int id = slot; id < total; id += G) {
+        const Tile tile = big::tile_of(id, tiles_m, tiles_n, p.splits);
+        const unsigned short* A = static_cast<const unsigned short*>(p.a) + tile.batch * p.stride_a;
+        const unsigned short* B = static_cast<const unsigned short*>(p.b) + tile.batch * p.stride_b;
+        const int k_begin = tile.split * p.k_per_split;
+        const int k_end = min(p.k, k_begin + p.k_per_split);
+        const int nk = (k_end - k_begin) / BK;
+
+        f32x16_t acc[MI][NJ];
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+        big::lds_barrier();  // the previous tile's epilogue is done with LDS
+        fetch(A, B, p.lda, p.ldb, tile.m0, tile.n0, k_begin, lds, wave, lane);
+        for (int kt = 0; kt < nk; ++kt) {
+            // the DMA of K tile kt has landed in every wave, and every wave is done
+            // reading the stage that K tile kt + 1 now refills (it held kt - 1)
+            big::dma_barrier<0>();
+            const int next = min(kt + 1, nk - 1);  // the tail refetches the last tile into a stage nobody reads
+            fetch(A, B, p.lda, p.ldb, tile.m0, tile.n0, k_begin + next * BK, lds + ((kt + 1) & 1) * STAGE, wave, lane);
+            const unsigned short* stage = lds + (kt & 1) * STAGE;
+            const unsigned short* la = stage + (wm * WTM + lane % 32) * BK;
+            const unsigned short* lb = stage + BM * BK + (wn * WTN + lane % 32) * BK;
+            bf16x8_t af[2][MI], bfr[2][NJ];
+            const auto read = [&](int s, bf16x8_t (&fa)[MI], bf16x8_t (&fb)[NJ]) {
+                const int off = 8 * ((2 * s + lane / 32) ^ sw);
+#pragma unroll
+                for (int i = 0; i < MI; ++i) fa[i] = *reinterpret_cast<const bf16x8_t*>(la + i * 32 * BK + off);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) fb[j] = *reinterpret_cast<const bf16x8_t*>(lb + j * 32 * BK + off);
+            };
+            read(0, af[0], bfr[0]);
+#pragma unroll
+            for (int s = 0; s < BK / 16; ++s) {
+                if (s + 1 < BK / 16) read(s + 1, af[(s + 1) & 1], bfr[(s + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s & 1][i], bfr[s & 1][j], acc[i][j], 0,
+                                                                           0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        big::dma_barrier<0>();  // the tail DMA has landed and every wave is past its last fragment reads
+
+        // ---- epilogue
+        float* D = (direct && !p.d) ? nullptr
+                                    : p.d + (direct ? tile.batch * p.stride_d
+                                                    : (static_cast<long long>(tile.split) * p.batch + tile.batch) *
+                                                          static_cast<long long>(p.m) * p.n);
+        const long long ldd = direct ? p.ldd : p.n;
+        const float* C = (direct && p.beta != 0.0f) ? p.c + tile.batch * p.stride_d : nullptr;
+        unsigned short* Dh = (direct && p.d_bf16) ? p.d_bf16 + tile.batch * p.stride_d : nullptr;
+        const int col = tile.n0 + wn * WTN + (lane % LPR) * 8;
+        float bias8[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if (direct && p.bias) {
+            const float* bp = p.bias + tile.batch * p.stride_bias + col;
+            const float4 b0 = *reinterpret_cast<const float4*>(bp);
+            const float4 b1 = *reinterpret_cast<const float4*>(bp + 4);
+            bias8[0] = b0.x, bias8[1] = b0.y, bias8[2] = b0.z, bias8[3] = b0.w;
+            bias8[4] = b1.x, bias8[5] = b1.y, bias8[6] = b1.z, bias8[7] = b1.w;
+        }
+        const bool moments = direct && p.moments != nullptr;
+        const bool round_moments = moments && !D;  // a bf16-only output takes the moments of the stored values
+        float shift[8], s1[8], s2[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) shift[e] = s1[e] = s2[e] = 0.0f;
+        float* stagef = reinterpret_cast<float*>(lds) + wave * 32 * EP;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            if (i) lds_fence();  // this wave's reads of the previous block are done
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    stagef[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * EP + j * 32 + lane % 32] = acc[i][j][v];
+            lds_fence();
+#pragma unroll
+            for (int pass = 0; pass < 32 / RPP; ++pass) {
+                const int r = pass * RPP + lane / LPR;
+                const f32x4 x0 = *reinterpret_cast<const f32x4*>(stagef + r * EP + (lane % LPR) * 8);
+                const f32x4 x1 = *reinterpret_cast<const f32x4*>(stagef + r * EP + (lane % LPR) * 8 + 4);
+                float val[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                const long long offset = static_cast<long long>(tile.m0 + wm * WTM + i * 32 + r) * ldd + col;
+                if (direct) {
+                    float4 lo = activate4(make_float4(val[0] + bias8[0], val[1] + bias8[1], val[2] + bias8[2],
+                                                      val[3] + bias8[3]), p.epilogue);
+                    float4 hi = activate4(make_float4(val[4] + bias8[4], val[5] + bias8[5], val[6] + bias8[6],
+                                                      val[7] + bias8[7]), p.epilogue);
+                    val[0] = lo.x, val[1] = lo.y, val[2] = lo.z, val[3] = lo.w;
+                    val[4] = hi.x, val[5] = hi.y, val[6] = hi.z, val[7] = hi.w;
+                    if (C) {
+                        const float4 c0 = *reinterpret_cast<const float4*>(C + offset);
+                        const float4 c1 = *reinterpret_cast<const float4*>(C + offset + 4);
+                        val[0] += p.beta * c0.x, val[1] += p.beta * c0.y, val[2] += p.beta * c0.z;
+                        val[3] += p.beta * c0.w, val[4] += p.beta * c1.x, val[5] += p.beta * c1.y;
+                        val[6] += p.beta * c1.z, val[7] += p.beta * c1.w;
+                    }
+                    if (Dh) {
+                        const u32x4 packed = {f32x2_to_bf16x2(val[0], val[1]), f32x2_to_bf16x2(val[2], val[3]),
+                                              f32x2_to_bf16x2(val[4], val[5]), f32x2_to_bf16x2(val[6], val[7])};
+                        __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(Dh + offset));
+                        if (round_moments) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                val[2 * e] = __uint_as_float(packed[e] << 16);
+                                val[2 * e + 1] = __uint_as_float(packed[e] & 0xffff0000u);
+                            }
+                        }
+                    }
+                }
+                if (moments) {  // identity epilogue: val holds the stored values
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        if (i == 0 && pass == 0) shift[e] = val[e];
+                        const float d = val[e] - shift[e];
+                        s1[e] += d;
+                        s2[e] += d * d;
+                    }
+                }
+                if (D) {
+                    __builtin_nontemporal_store((f32x4){val[0], val[1], val[2], val[3]},
+                                                reinterpret_cast<f32x4*>(D + offset));
+                    __builtin_nontemporal_store((f32x4){val[4], val[5], val[6], val[7]},
+                                                reinterpret_cast<f32x4*>(D + offset + 4));
+                }
+            }
+        }
+        if (moments) {
+            // this lane's 16 rows -> (mean, M2), then butterflies over the 8 lane groups of the
+            // same columns (partners lane ^ 8, ^ 16, ^ 32; the lower lane's moments go first)
+            constexpr float rows = 32 / RPP * MI;
+            float count = rows, mean[8], m2[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                mean[e] = shift[e] + s1[e] * (1.0f / rows);
+                m2[e] = fmaxf(s2[e] - s1[e] * s1[e] * (1.0f / rows), 0.0f);
+            }
+#pragma unroll
+            for (int offset = LPR; offset < kWave; offset *= 2) {
+                float om[8], oq[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    om[e] = __shfl_xor(mean[e], offset);
+                    oq[e] = __shfl_xor(m2[e], offset);
+                }
+                if (lane & offset) {
+                    float tm[8], tq[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        tm[e] = mean[e], tq[e] = m2[e];
+                        mean[e] = om[e], m2[e] = oq[e];
+                    }
+                    merge8(count, mean, m2, count, tm, tq);
+                } else {
+                    merge8(count, mean, m2, count, om, oq);
+                }
+            }
+            if (wm == 1 && lane < LPR) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    exchange[wn * WTN + (lane % LPR) * 8 + e] = mean[e];
+                    exchange[BN + wn * WTN + (lane % LPR) * 8 + e] = m2[e];
+                }
+            }
+            big::lds_barrier();
+            if (wm == 0 && lane < LPR) {
+                float bm[8], bq[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    bm[e] = exchange[wn * WTN + (lane % LPR) * 8 + e];
+                    bq[e] = exchange[BN + wn * WTN + (lane % LPR) * 8 + e];
+                }
+                merge8(count, mean, m2, count, bm, bq);
+                float* out = p.moments + (static_cast<long long>(tile.batch) * (p.m / BM) + tile.m0 / BM) * 2 * p.n + col;
+                *reinterpret_cast<float4*>(out) = make_float4(mean[0], mean[1], mean[2], mean[3]);
+                *reinterpret_cast<float4*>(out + 4) = make_float4(mean[4], mean[5], mean[6], mean[7]);
+                *reinterpret_cast<float4*>(out + p.n) = make_float4(m2[0], m2[1], m2[2], m2[3]);
+                *reinterpret_cast<float4*>(out + p.n + 4) = make_float4(m2[4], m2[5], m2[6], m2[7]);
+            }
+        }
+    }
+}
+
+}  // namespace wide
+
 }  // namespace big
 
 bool big_eligible(const Params& p, int a_bf16, int b_bf16) {
@@ -598,7 +873,13 @@ void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(std::min(total, compute_units())));
     const dim3 block(big::T);
     const bool dma = ak && bk && p.k % (big::DS * big::BK) == 0 && p.k_per_split % (big::DS * big::BK) == 0;
-    if (dma) hipLaunchKernelGGL(big::gemm_dma_kernel, grid, block, 0, stream, p, tiles_m, tiles_n, total);
+    // the eight-wave kernel writes the bf16 copy as 16-byte pieces of 8 columns
+    const bool wide = ak && bk && p.k % (2 * big::wide::BK) == 0 && p.k_per_split % (2 * big::wide::BK) == 0 &&
+                      (!p.d_bf16 || (aligned(p.d_bf16, 16) && p.ldd % 8 == 0 && p.stride_d % 8 == 0));
+    if (wide)
+        hipLaunchKernelGGL(big::wide::gemm_wide_kernel, grid, dim3(big::wide::NW * kWave), 0, stream, p, tiles_m,
+                           tiles_n, total);
+    else if (dma) hipLaunchKernelGGL(big::gemm_dma_kernel, grid, block, 0, stream, p, tiles_m, tiles_n, total);
     else if (ak && bk) hipLaunchKernelGGL((big::gemm_big_kernel<true, true>), grid, block, 0, stream, p, tiles_m, tiles_n, total);
     else if (ak && !bk) hipLaunchKernelGGL((big::gemm_big_kernel<true, false>), grid, block, 0, stream, p, tiles_m, tiles_n, total);
     else if (!ak && bk) hipLaunchKernelGGL((big::gemm_big_kernel<false, true>), grid, block, 0, stream, p, tiles_m, tiles_n, total);

@@ -21,6 +21,7 @@
 // every replay.
 #include "common.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 namespace rl {
@@ -112,16 +113,22 @@ struct GatherArgs {
     int* error;
 };
 
+// One thread per (row, column) of the concatenated row [obs | next_obs | action |
+// reward, terminated, truncated, discount], grid-stride over batch * width so the
+// batch size has no launch-shape limit.  An index outside [0, capacity) raises
+// *error and reads row 0 instead.
 __global__ void gather_kernel(GatherArgs a) {
-    const long long i = blockIdx.y;
-    if (i >= a.batch) return;
-    long long k = a.idx[i];
-    if (k < 0 || k >= a.capacity) {
-        if (threadIdx.x == 0 && blockIdx.x == 0 && a.error) atomicExch(a.error, 1);
-        k = 0;
-    }
     const int width = 2 * a.obs_dim + a.action_dim + 4;
-    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < width; j += gridDim.x * blockDim.x) {
+    const long long total = a.batch * width;
+    const long long step = static_cast<long long>(gridDim.x) * blockDim.x;
+    for (long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; t < total; t += step) {
+        const long long i = t / width;
+        const int j = static_cast<int>(t - i * width);
+        long long k = a.idx[i];
+        if (k < 0 || k >= a.capacity) {
+            if (j == 0 && a.error) atomicExch(a.error, 1);
+            k = 0;
+        }
         if (j < a.obs_dim) a.out_obs[i * a.obs_dim + j] = a.obs[k * a.obs_dim + j];
         else if (j < 2 * a.obs_dim) {
             const int c = j - a.obs_dim;
@@ -487,13 +494,13 @@ RL_API int rl_replay_gather(const long long* idx, long long batch, long long cap
         rl::require(obs && next_obs && action && reward && terminated && discount && out_obs && out_next_obs &&
                         out_action && out_reward && out_terminated && out_discount,
                     "Gather needs every storage and output field.");
-        rl::require(batch <= 65535, "Gather batch must not exceed 65535 rows per launch.");
         P::GatherArgs a{idx, batch, obs, next_obs, action, reward, terminated, truncated, discount, out_obs,
                         out_next_obs, out_action, out_reward, out_terminated, out_truncated, out_discount, obs_dim,
                         action_dim, capacity, error};
-        const int width = 2 * obs_dim + action_dim + 4;
-        hipLaunchKernelGGL(P::gather_kernel, dim3(rl::ceil_div(width, 256), static_cast<unsigned>(batch)), dim3(256), 0,
-                           rl::as_stream(stream), a);
+        const long long total = batch * (2LL * obs_dim + action_dim + 4);
+        const long long blocks = std::min<long long>((total + 255) / 256, 1LL << 20);
+        hipLaunchKernelGGL(P::gather_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, rl::as_stream(stream),
+                           a);
         rl::check_launch("Launch replay gather");
     });
 }

@@ -68,8 +68,6 @@ class WarpPPO:
         if cfg.num_mini_batches < 1 or N % cfg.num_mini_batches:
             raise ValueError("num_mini_batches must be positive and divide the rollout batch size.")
         self.mini_batch_size = M = N // cfg.num_mini_batches
-        if M > 65535:
-            raise ValueError("Minibatches above 65535 rows are not supported by the gather kernel.")
         O, A = observation_dim, action_dim
         self.layers = len(cfg.hidden_dims) + 1
         actor = _mlp_shapes("actor", O, A, cfg.hidden_dims)
