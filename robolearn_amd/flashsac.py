@@ -108,13 +108,16 @@ class FlashSAC:
 
     ``update`` performs one critic update; the first update and every
     ``actor_update_period`` thereafter also update the actor and temperature.
-    ``cfg.use_amp`` selects bf16 operands for the dense-layer GEMMs.
+    ``cfg.use_amp`` selects bf16 operands for the dense-layer GEMMs; with it,
+    ``bf16_activations`` (default True) also stores the BatchNorm inputs and the
+    ReLU-BatchNorm gradients in bf16, the layout an autocast Linear hands its
+    BatchNorm, and False keeps those activations fp32.
     """
 
     def __init__(self, observation_dim: int, action_dim: int, num_envs: int = 1, cfg: FlashSACConfig | None = None,
                  critic_observation_dim: int | None = None, *, optimized_linear_backward: bool = True,
                  dense_backend: str = "hip", fused_updates: bool = True, cuda_autotune: bool = False,
-                 fresh_training_gradients: bool = False):
+                 fresh_training_gradients: bool = False, bf16_activations: bool = True):
         cfg = cfg or FlashSACConfig()
         if min(observation_dim, action_dim, num_envs) < 1:
             raise ValueError("Observation, action and environment dimensions must be positive.")
@@ -203,9 +206,12 @@ class FlashSAC:
             self.temperature_optimizer = FusedOptimizer(self.temperature, cfg, plain=True)
             # networks / activations
             self.actor_net = Trunk(ensemble=1, in_dim=Oa, hidden=ha, blocks=cfg.actor_num_blocks, max_rows=2 * B,
-                                   device=dev, mode=self.mode, prefix_linear=".w.weight")
+                                   device=dev, mode=self.mode, prefix_linear=".w.weight",
+                                   bf16_activations=bf16_activations)
             self.critic_net = Trunk(ensemble=2, in_dim=I, hidden=hc, blocks=cfg.critic_num_blocks, max_rows=2 * B,
-                                    device=dev, mode=self.mode, prefix_linear=".weight")
+                                    device=dev, mode=self.mode, prefix_linear=".weight",
+                                    bf16_activations=bf16_activations)
+            self.bf16_activations = bf and bf16_activations
             self.workspace = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
             z = lambda *s: torch.zeros(*s, device=dev)  # noqa: E731
             self.batch = {"observation": z(B, Oc), "action": z(B, A), "reward": z(B), "terminated": z(B),
@@ -387,9 +393,14 @@ class FlashSAC:
                     self._host_additions = additions
         self._update_step = int(np.asarray(state["update_counters"])[0])
 
-    def save(self, path, *, include_replay: bool = False, format: str = "native") -> None:
-        """Checkpoint directory: "native" (config.json + agent.npz, optional replay) or "torch", the
-        reference's Torch layout (robolearn/flashsac/agent.py:529-551), readable by its load()."""
+    default_checkpoint_format = "native"
+
+    def save(self, path, *, include_replay: bool = False, format: str | None = None) -> None:
+        """Checkpoint directory: "native" (config.json + agent.npz, optional replay), "torch", the
+        reference's Torch layout (robolearn/flashsac/agent.py:529-551), or "warp", the reference Warp
+        learner's robolearn-warp-flashsac-v1 arrays (robolearn/warp/flashsac.py:1169-1195); each is
+        readable by the matching reference load()."""
+        format = format or self.default_checkpoint_format
         if format == "torch":
             from . import torch_checkpoint
 
@@ -397,8 +408,13 @@ class FlashSAC:
             if include_replay:
                 torch_checkpoint.save_replay_buffer(self, path)
             return
+        if format == "warp":
+            from . import warp_checkpoint
+
+            warp_checkpoint.save(self, path, include_replay=include_replay)
+            return
         if format != "native":
-            raise ValueError("format must be 'native' or 'torch'.")
+            raise ValueError("format must be 'native', 'torch' or 'warp'.")
         directory = Path(path)
         directory.mkdir(parents=True, exist_ok=True)
         metadata = {
@@ -417,7 +433,8 @@ class FlashSAC:
             np.savez(stream, **state)
 
     def load(self, path) -> None:
-        """Load a native checkpoint, or a Torch-layout one (actor.pt beside config.json)."""
+        """Load a native checkpoint, a Warp-format one (its config.json format tag) or a Torch-layout
+        one (actor.pt beside config.json), in place: captured graphs keep their buffers."""
         directory = Path(path)
         if (directory / "actor.pt").exists():
             from . import torch_checkpoint
@@ -425,6 +442,11 @@ class FlashSAC:
             torch_checkpoint.load(self, directory)
             return
         metadata = json.loads((directory / "config.json").read_text())
+        if metadata.get("format") == "robolearn-warp-flashsac-v1":
+            from . import warp_checkpoint
+
+            warp_checkpoint.load(self, directory)
+            return
         if metadata.get("format") != "robolearn-mi355x-flashsac-v1":
             raise ValueError("Unrecognized FlashSAC checkpoint format.")
         if metadata["observation_dim"] != self.observation_dim or metadata["action_dim"] != self.action_dim:
@@ -829,16 +851,37 @@ class FlashSAC:
                     self.launch_update(phase)
                 self._graphs[phase] = graph
 
+    def _pair_phases(self) -> tuple:
+        period = self.cfg.actor_update_period
+        return tuple((self._update_step + i) % period == 0 for i in range(2))
+
     def capture_pair(self) -> "torch.cuda.CUDAGraph":
-        """One graph holding an actor-phase update followed by a critic-only update (update-to-data 2)."""
+        """One graph holding the next two updates (update-to-data 2), with the actor phases that the
+        current update step gives them: an actor-phase update then a critic-only update when the step
+        is even and actor_update_period is 2.  Replay it through ``update_pair``, which keeps the host
+        update step in line with the device counters."""
         self.prepare(capture=False)
-        if "pair" not in self._graphs:
+        phases = self._pair_phases()
+        key = ("pair",) + phases
+        if key not in self._graphs:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                self.launch_update(True)
-                self.launch_update(False)
-            self._graphs["pair"] = graph
-        return self._graphs["pair"]
+                for phase in phases:
+                    self.launch_update(phase)
+            self._graphs[key] = graph
+        return self._graphs[key]
+
+    def update_pair(self, *, tensor_metrics: bool = False) -> dict:
+        """Two updates in one graph replay (the update-to-data-2 step of robolearn/warp/flashsac.py:1033-1048
+        called twice).  The metrics are those of the second update plus, when only the first was an actor
+        phase, the first update's actor and temperature metrics."""
+        if not self.ready:
+            raise RuntimeError("Replay has not reached buffer_min_length.")
+        phases = self._pair_phases()
+        with torch.cuda.device(self.device):
+            self.capture_pair().replay()
+        self._update_step += 2
+        return self._metrics(any(phases), tensor_metrics)
 
     def update(self, *, tensor_metrics: bool = False, capture: bool = True) -> dict:
         if not self.ready:
@@ -868,4 +911,8 @@ class FlashSAC:
         return result
 
 
-WarpFlashSAC = FlashSAC
+class WarpFlashSAC(FlashSAC):
+    """The reference's WarpFlashSAC entry point (robolearn/warp/flashsac.py:340-353): the same
+    learner, whose save() writes the Warp learner's robolearn-warp-flashsac-v1 checkpoint."""
+
+    default_checkpoint_format = "warp"

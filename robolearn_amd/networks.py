@@ -224,7 +224,8 @@ class Trunk:
     the residual stream, the BN backward inputs).
     """
 
-    def __init__(self, *, ensemble, in_dim, hidden, blocks, max_rows, device, mode, prefix_linear):
+    def __init__(self, *, ensemble, in_dim, hidden, blocks, max_rows, device, mode, prefix_linear,
+                 bf16_activations=True):
         self.E, self.in_dim, self.h, self.blocks, self.R = ensemble, in_dim, hidden, blocks, max_rows
         self.mode = mode
         self.bf = mode == K.BF16
@@ -242,8 +243,10 @@ class Trunk:
 
         # BatchNorm inputs and their gradients: bf16 in bf16 mode, as the Linear
         # outputs an autocast forward feeds the BatchNorm (the BN kernels need
-        # channels in multiples of 4 for bf16 rows)
-        narrow = self.bf and h % 4 == 0
+        # channels in multiples of 4 for bf16 rows); bf16_activations=False keeps
+        # them fp32 (bf16 GEMM operands with fp32 activations)
+        narrow = self.bf and bf16_activations and h % 4 == 0
+        self.bf16_activations = narrow
 
         def pre_norm(*shape):
             return torch.zeros(*shape, dtype=torch.bfloat16, device=device) if narrow else buf(*shape)
