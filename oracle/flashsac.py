@@ -270,8 +270,17 @@ def critic_support(d: Dims, dtype=torch.float32) -> torch.Tensor:
     return torch.linspace(d.min_v, d.max_v, d.bins, dtype=torch.float32).to(dtype)
 
 
-def critic_forward(p, s, observations, actions, training: bool, d: Dims):
-    """FlashSACDoubleCritic.forward (networks.py:97-110); returns (q [2, R], log_probs [2, R, K])."""
+def _relu_margin(x, margins):
+    """Per row, the smallest |ReLU input| relative to the row's largest (how near a rounding flip is)."""
+    if margins is not None:
+        with torch.no_grad():
+            scale = x.abs().amax(dim=-1, keepdim=True).clamp_min(1e-30)
+            margins.append((x.abs() / scale).amin(dim=-1))
+
+
+def critic_forward(p, s, observations, actions, training: bool, d: Dims, margins: list | None = None):
+    """FlashSACDoubleCritic.forward (networks.py:97-110); returns (q [2, R], log_probs [2, R, K]).
+    margins (optional): receives one [2, R] tensor per ReLU, see _relu_margin."""
     x = torch.cat((observations, actions), dim=-1)
     x = x.unsqueeze(0).expand(2, -1, -1)
     x = _ensemble_bn(x, p, s, "embedder.norm", training)
@@ -280,9 +289,11 @@ def critic_forward(p, s, observations, actions, training: bool, d: Dims):
         residual = x
         x = torch.einsum("nbi,noi->nbo", x, p[f"encoder.{b}.w1.weight"])
         x = _ensemble_bn(x, p, s, f"encoder.{b}.norm1", training)
+        _relu_margin(x, margins)
         x = F.relu(x)
         x = torch.einsum("nbi,noi->nbo", x, p[f"encoder.{b}.w2.weight"])
         x = _ensemble_bn(x, p, s, f"encoder.{b}.norm2", training)
+        _relu_margin(x, margins)
         x = F.relu(x)
         x = x + residual
     rms = torch.sqrt(torch.mean(x * x, dim=-1, keepdim=True) + RMS_EPS)
@@ -477,7 +488,9 @@ def update(state: OracleState, batch: dict, actor_noise: torch.Tensor, next_nois
             actor_loss = actor_loss + cfg.actor_bc_alpha * q_abs * ((actions - b["action"]) ** 2).mean()
         entropy = -log_probs.mean()
         mean_action = actions.mean()
-        grads = torch.autograd.grad(actor_loss, actor_params)
+        grads = torch.autograd.grad(actor_loss, actor_params + [actions_all])
+        record["actor_dactions"] = grads[-1].detach().clone()  # the loss's gradient at the tanh outputs
+        grads = grads[:-1]
         record["actor_grads"] = OrderedDict((k, g.detach().clone()) for k, g in zip(state.actor.keys(), grads))
         record["actor_actions"] = actions_all.detach().clone()
         record["actor_log_probs"] = log_probs_all.detach().clone()

@@ -165,10 +165,9 @@ class PPOOracle:
         self.learning_rate = cfg.learning_rate
         self.last = {}
 
-    def update(self, rollout: dict, permutation) -> dict:
-        """One launch_update (ppo.py:586-695) on a fixed rollout and permutation."""
+    def prepare(self, rollout: dict):
+        """GAE and advantage normalization of a rollout (ppo.py:101-159); keeps the arrays."""
         cfg = self.cfg
-        dt = self.dtype
         data = {k: torch.as_tensor(np.asarray(v)) for k, v in rollout.items()}
         advantages, returns = gae(data["rewards"], data["values"], data["next_values"], data["terminated"],
                                   data["truncated"], self.horizon, self.num_envs, cfg.gamma, cfg.gae_lambda,
@@ -176,38 +175,67 @@ class PPOOracle:
         if cfg.normalize_advantages:
             advantages = normalize(advantages, cfg.advantage_sample_std)
         self.advantages, self.returns = advantages.clone(), returns.clone()
-        obs = data["observations"].to(dt)
+        self._data = data
+        self._obs = data["observations"].to(self.dtype)
+
+    def minibatch_step(self, idx) -> None:
+        """One minibatch of launch_update (ppo.py:586-695) on the prepared rollout: the pre-step KL and
+        adaptive learning rate, the loss, backward, gradient clipping and the Adam step."""
+        cfg, dt, data = self.cfg, self.dtype, self._data
+        idx = torch.as_tensor(np.asarray(idx, dtype=np.int64))
+        mean = mlp(self._obs[idx], self.actor, cfg.activation)
+        if cfg.schedule == "adaptive":
+            with torch.no_grad():
+                kl = gaussian_kl(data["means"][idx].to(dt), data["stds"][idx].to(dt), mean,
+                                 std_of(self.std_parameter, cfg)).mean().item()
+                if kl > 2.0 * cfg.desired_kl:
+                    self.learning_rate = max(1.0e-5, self.learning_rate / 1.5)
+                elif 0.0 < kl < cfg.desired_kl / 2.0:
+                    self.learning_rate = min(1.0e-2, self.learning_rate * 1.5)
+                self.last["kl"] = kl
+            for group in self.optimizer.param_groups:
+                group["lr"] = self.learning_rate
+        value = mlp(self._obs[idx], self.critic, cfg.activation)
+        loss, policy, value_loss, entropy = loss_terms(
+            mean, value, self.std_parameter, data["actions"][idx].to(dt), data["log_probs"][idx].to(dt),
+            data["values"][idx].to(dt), self.advantages[idx].to(dt), self.returns[idx].to(dt), cfg)
+        self.optimizer.zero_grad()
+        loss.backward()
+        if cfg.separate_grad_clipping:
+            clip_gradients(self.actor + [self.std_parameter], cfg.max_grad_norm)
+            clip_gradients(self.critic, cfg.max_grad_norm)
+        else:
+            clip_gradients(self.params, cfg.max_grad_norm)
+        self.optimizer.step()
+        self.last.update(loss=loss.item(), policy_loss=policy.item(), value_loss=value_loss.item(),
+                         entropy=entropy.item())
+
+    def update(self, rollout: dict, permutation) -> dict:
+        """One launch_update (ppo.py:586-695) on a fixed rollout and permutation: the same permutation
+        for every epoch, minibatches in order."""
+        self.prepare(rollout)
         permutation = np.asarray(permutation, dtype=np.int64)
-        for _ in range(cfg.epochs):
-            for mb in range(cfg.num_mini_batches):
-                idx = torch.as_tensor(permutation[mb * self.mini_batch_size: (mb + 1) * self.mini_batch_size])
-                mean = mlp(obs[idx], self.actor, cfg.activation)
-                if cfg.schedule == "adaptive":
-                    with torch.no_grad():
-                        kl = gaussian_kl(data["means"][idx].to(dt), data["stds"][idx].to(dt), mean,
-                                         std_of(self.std_parameter, cfg)).mean().item()
-                        if kl > 2.0 * cfg.desired_kl:
-                            self.learning_rate = max(1.0e-5, self.learning_rate / 1.5)
-                        elif 0.0 < kl < cfg.desired_kl / 2.0:
-                            self.learning_rate = min(1.0e-2, self.learning_rate * 1.5)
-                        self.last["kl"] = kl
-                    for group in self.optimizer.param_groups:
-                        group["lr"] = self.learning_rate
-                value = mlp(obs[idx], self.critic, cfg.activation)
-                loss, policy, value_loss, entropy = loss_terms(
-                    mean, value, self.std_parameter, data["actions"][idx].to(dt), data["log_probs"][idx].to(dt),
-                    data["values"][idx].to(dt), advantages[idx].to(dt), returns[idx].to(dt), cfg)
-                self.optimizer.zero_grad()
-                loss.backward()
-                if cfg.separate_grad_clipping:
-                    clip_gradients(self.actor + [self.std_parameter], cfg.max_grad_norm)
-                    clip_gradients(self.critic, cfg.max_grad_norm)
-                else:
-                    clip_gradients(self.params, cfg.max_grad_norm)
-                self.optimizer.step()
-                self.last.update(loss=loss.item(), policy_loss=policy.item(), value_loss=value_loss.item(),
-                                 entropy=entropy.item())
+        size = self.mini_batch_size
+        for _ in range(self.cfg.epochs):
+            for mb in range(self.cfg.num_mini_batches):
+                self.minibatch_step(permutation[mb * size: (mb + 1) * size])
         return dict(self.last, learning_rate=self.learning_rate)
+
+    def set_state(self, parameters, moments, steps: int, learning_rate: float) -> None:
+        """Parameters, Adam moments, Adam step count and learning rate taken from another
+        implementation (to check one step from its state)."""
+        with torch.no_grad():
+            for p, value in zip(self.params, parameters):
+                p.copy_(torch.as_tensor(np.asarray(value)).reshape(p.shape).to(self.dtype))
+        for p, (m1, m2) in zip(self.params, moments):
+            self.optimizer.state[p] = {
+                "step": torch.tensor(float(steps)),
+                "exp_avg": torch.as_tensor(np.asarray(m1)).reshape(p.shape).to(self.dtype).clone(),
+                "exp_avg_sq": torch.as_tensor(np.asarray(m2)).reshape(p.shape).to(self.dtype).clone(),
+            }
+        self.learning_rate = float(learning_rate)
+        for group in self.optimizer.param_groups:
+            group["lr"] = self.learning_rate
 
     def moments(self):
         out = []

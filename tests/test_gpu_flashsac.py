@@ -118,14 +118,14 @@ def test_full_updates_match_oracle(gpu, steps):
             bound = 5e-7 + 0.02 * delta_ref.abs().max().item()
             err = (delta_gpu - delta_ref).abs()
             flips += int((err > bound).sum())
-            assert err.max().item() <= bound or (err > bound).float().mean().item() < 0.01, (step, key)
+            assert err.max().item() <= bound, (step, key, err.max().item(), bound)
         moments = state.moments()
         for label, store in (("actor", agent.actor), ("critic", agent.critic)):
             m1, m2 = store.moments()
             for name in store.shapes:
                 assert _tensor_rel(m1[name], moments[f"{label}.{name}.m1"]) < 1e-4, (step, label, name, "m1")
                 assert _tensor_rel(m2[name], moments[f"{label}.{name}.m2"]) < 1e-4, (step, label, name, "m2")
-        print(f"step {step}: parameter sign flips beyond the delta policy: {flips}")
+        print(f"step {step}: parameter elements beyond the delta policy: {flips}")
 
 
 def test_bf16_mode_losses_within_1e2(gpu):

@@ -243,3 +243,29 @@ def test_rollout_act_and_store_match_oracle(gpu, std_type):
     second = big._act_state(4096)["noise"]
     assert abs(first.mean().item()) < 0.03 and abs(first.std().item() - 1.0) < 0.03
     assert not torch.equal(first, second)
+
+
+@pytest.mark.parametrize("n,scale", [(1000, 1e-3), (232_522 + 227_841, 0.7), (460_363, 25.0), (5, 3.0)])
+def test_sum_squares_and_clip_closed_form(gpu, n, scale):
+    """rl_sum_squares + rl_clip_by_norm (robolearn/warp/ppo.py:241-252): below the threshold the gradient
+    is unchanged; above it g * max_norm / (||g|| + 1e-6), so the post-clip norm is
+    max_norm ||g|| / (||g|| + 1e-6).  The middle sizes are the c3 actor + critic parameter count, the
+    combined group of the default (non-separate) mode."""
+    print(f"case clip n={n} scale={scale}", flush=True)
+    g = torch.Generator().manual_seed(n)
+    grad = torch.randn(n, generator=g)
+    grad = grad * (scale / grad.double().norm().item())
+    device = grad.to(gpu)
+    partial = torch.empty((n + 4095) // 4096, device=gpu)
+    sum_squares = torch.empty(1, device=gpu)
+    _native.call("rl_sum_squares", device.data_ptr(), n, partial.data_ptr(), sum_squares.data_ptr(), K.stream())
+    _native.call("rl_clip_by_norm", device.data_ptr(), n, sum_squares.data_ptr(), 1.0, K.stream())
+    torch.cuda.synchronize()
+    norm = grad.double().norm().item()
+    assert sum_squares.item() == pytest.approx(norm * norm, rel=1e-5)
+    clipped = device.cpu().double()
+    if norm + 1e-6 <= 1.0:
+        assert torch.equal(device.cpu(), grad)
+    else:
+        assert clipped.norm().item() == pytest.approx(norm / (norm + 1e-6), rel=1e-5)
+        torch.testing.assert_close(clipped, grad.double() / (norm + 1e-6), rtol=1e-5, atol=1e-9)

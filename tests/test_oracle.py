@@ -330,6 +330,39 @@ def test_ppo_gradient_clipping_closed_form(scale):
             torch.testing.assert_close(p.grad, x * coefficient, rtol=1e-14, atol=0)
 
 
+def test_ppo_step_from_injected_state_continues_the_update():
+    """set_state + minibatch_step (the per-step check of the GPU update) continue a run exactly: an
+    update of 2 epochs x 2 minibatches equals its first three steps followed by the fourth step run
+    from the parameters, moments, step count and learning rate copied into a fresh oracle."""
+    cfg = PPOConfig(hidden_dims=(16, 8), epochs=2, num_mini_batches=2, schedule="adaptive", desired_kl=0.01)
+    envs, horizon, obs_dim, act_dim = 8, 4, 5, 3
+    n = envs * horizon
+    rng = np.random.default_rng(4)
+    rollout = dict(observations=rng.standard_normal((n, obs_dim)), actions=rng.standard_normal((n, act_dim)),
+                   means=rng.standard_normal((n, act_dim)) * 0.1, stds=np.full((n, act_dim), 1.1),
+                   values=rng.standard_normal(n), log_probs=rng.standard_normal(n) - 4.0,
+                   rewards=rng.standard_normal(n), next_values=rng.standard_normal(n),
+                   terminated=(rng.random(n) < 0.1).astype(np.int32), truncated=np.zeros(n, np.int32))
+    params = OP.init_parameters(obs_dim, act_dim, cfg)
+    permutation = rng.permutation(n)
+    full = OP.PPOOracle(obs_dim, act_dim, envs, horizon, cfg, params)
+    full.update(rollout, permutation)
+    first = OP.PPOOracle(obs_dim, act_dim, envs, horizon, cfg, params)
+    first.prepare(rollout)
+    half = n // 2
+    for idx in (permutation[:half], permutation[half:], permutation[:half]):
+        first.minibatch_step(idx)
+    second = OP.PPOOracle(obs_dim, act_dim, envs, horizon, cfg, params)
+    second.prepare(rollout)
+    second.set_state([p.detach() for p in first.params], first.moments(), 3, first.learning_rate)
+    second.minibatch_step(permutation[half:])
+    for a, b in zip(full.params, second.params):
+        assert torch.equal(a.detach(), b.detach())
+    for (a1, a2), (b1, b2) in zip(full.moments(), second.moments()):
+        assert torch.equal(a1, b1) and torch.equal(a2, b2)
+    assert full.learning_rate == second.learning_rate
+
+
 def test_gaussian_kl_closed_form():
     old_mean, new_mean = torch.tensor([[0.3]]), torch.tensor([[-0.1]])
     old_std, new_std = torch.tensor([[0.7]]), torch.tensor([[1.2]])
