@@ -583,10 +583,11 @@ constexpr int CPR = BK / 8;           // 16-byte chunks per LDS row
 constexpr int RPI = 64 / CPR;         // rows per DMA instruction
 constexpr int IPW = 4 * CPR / NW;     // DMA instructions per operand per wave per stage
 constexpr int STAGE = (BM + BN) * BK; // bf16 elements per stage
-constexpr int EP = WTN + 4;           // epilogue staging pitch (floats)
+constexpr int EP = WTN + 8;           // epilogue staging pitch (floats): the two half-waves' rows 4 apart
+                                      // start 32 banks apart
 constexpr int LPR = WTN / 8;          // lanes per staged row (8 floats each)
 constexpr int RPP = kWave / LPR;      // staged rows per pass
-static_assert(NW * 32 * EP * 4 <= 2 * STAGE * 2, "epilogue staging fits the two stages");
+static_assert(RPP == 8, "a pass stages acc[i][j][4q .. 4q + 3]: 8 rows");
 
 // Chunk slot of a 16-byte k chunk in LDS row `row`: rows r and r + 1 differ in
 // their 128-byte bank alignment and rows r ^ 2i in the XOR, so the 16 rows that
@@ -615,6 +616,29 @@ __device__ __forceinline__ void fetch(const unsigned short* A, const unsigned sh
     }
 }
 
+// 16-byte LDS read of `p` + OFF bytes, issued as inline assembly.  The compiler
+// orders its own LDS reads after every LDS DMA still in flight (it cannot prove
+// that a swizzled fragment read misses the stage a DMA is filling) and would
+// wait for the DMA just issued into the other stage; the kernel instead waits
+// for its DMA explicitly (vmcnt + barrier) and for these reads with explicit
+// lgkmcnt waits before the MFMAs that use them.
+template <int OFF>
+__device__ __forceinline__ bf16x8_t lds_read16(const unsigned short* p) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds_read offset is 16 bits");
+    const auto local = (__attribute__((address_space(3))) const unsigned short*)p;  // LDS byte offset
+    const unsigned address = (unsigned)(uintptr_t)local;
+    bf16x8_t v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(address), "i"(OFF));
+    return v;
+}
+
+// s_waitcnt lgkmcnt(N), leaving vmcnt and expcnt alone.
+template <int N>
+__device__ __forceinline__ void wait_lds_reads() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt is a 4-bit count");
+    __builtin_amdgcn_s_waitcnt(0xC07F | (N << 8));
+}
+
 // Chan merge of (count, mean, M2) of 8 columns: first (in place) with second.
 __device__ __forceinline__ void merge8(float& count, float (&mean)[8], float (&m2)[8], float count_b,
                                        const float (&mean_b)[8], const float (&m2_b)[8]) {
@@ -630,8 +654,22 @@ __device__ __forceinline__ void merge8(float& count, float (&mean)[8], float (&m
     count = total;
 }
 
+// SPP: 16-byte stores every lane issues per 8-row epilogue pass (2 for an fp32 D,
+// 1 for the bf16 copy).  BIAS: the product adds a bias (a kernel without one
+// issues no epilogue loads, whose registers the next tile's fragment reads
+// would otherwise wait on).  The next tile's first two K tiles are fetched before
+// the epilogue, so the waits for them may leave S = 16 SPP stores in flight
+// (vector-memory counts complete in issue order); the conditional moment
+// stores and the bias / C loads only make those waits stricter.
+template <int SPP, bool BIAS>
 __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int tiles_m, int tiles_n, int total) {
-    __shared__ __attribute__((aligned(16))) unsigned short lds[2 * STAGE];
+    constexpr int S = MI * (32 / RPP) * SPP;
+    static_assert(SPP >= 1 && 2 * IPW + S < 64, "vmcnt is a 6-bit count");
+    // the two stages are separate objects: the compiler can then tell a fragment read of one
+    // stage from a DMA into the other and does not make the read wait for that DMA
+    __shared__ __attribute__((aligned(16))) unsigned short stage0[STAGE];
+    __shared__ __attribute__((aligned(16))) unsigned short stage1[STAGE];
+    __shared__ __attribute__((aligned(16))) float staging[NW * RPP * EP];
     __shared__ __attribute__((aligned(16))) float exchange[2 * BN];  // (mean, M2) of the second row half
     const int G = static_cast<int>(gridDim.x);
     const int b = static_cast<int>(blockIdx.x);
@@ -643,13 +681,25 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
     const int sw = slot_of(lane % 32);
     const bool direct = p.splits == 1;
 
+    const auto fetch_tile = [&](const Tile& t, int kt, unsigned short* stage) {
+        const unsigned short* A = static_cast<const unsigned short*>(p.a) + t.batch * p.stride_a;
+        const unsigned short* B = static_cast<const unsigned short*>(p.b) + t.batch * p.stride_b;
+        fetch(A, B, p.lda, p.ldb, t.m0, t.n0, t.split * p.k_per_split + kt * BK, stage, wave, lane);
+    };
+    const auto k_tiles = [&](const Tile& t) {
+        const int k_begin = t.split * p.k_per_split;
+        return (min(p.k, k_begin + p.k_per_split) - k_begin) / BK;  // even, >= 2: K splits are multiples of 128
+    };
+    if (slot >= total) return;
+    Tile tile = big::tile_of(slot, tiles_m, tiles_n, p.splits);
+    fetch_tile(tile, 0, stage0);
+    fetch_tile(tile, 1, stage1);
+    bool first = true;
+    float* stagef = staging + wave * RPP * EP;
+
     for (int id = slot; id < total; id += G) {
-        const Tile tile = big::tile_of(id, tiles_m, tiles_n, p.splits);
-        const unsigned short* A = static_cast<const unsigned short*>(p.a) + tile.batch * p.stride_a;
-        const unsigned short* B = static_cast<const unsigned short*>(p.b) + tile.batch * p.stride_b;
-        const int k_begin = tile.split * p.k_per_split;
-        const int k_end = min(p.k, k_begin + p.k_per_split);
-        const int nk = (k_end - k_begin) / BK;
+        const Tile next = id + G < total ? big::tile_of(id + G, tiles_m, tiles_n, p.splits) : tile;
+        const int nk = k_tiles(tile);
 
         f32x16_t acc[MI][NJ];
 #pragma unroll
@@ -659,29 +709,42 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-        big::lds_barrier();  // the previous tile's epilogue is done with LDS
-        fetch(A, B, p.lda, p.ldb, tile.m0, tile.n0, k_begin, lds, wave, lane);
-        for (int kt = 0; kt < nk; ++kt) {
-            // the DMA of K tile kt has landed in every wave, and every wave is done
-            // reading the stage that K tile kt + 1 now refills (it held kt - 1)
-            big::dma_barrier<0>();
-            const int next = min(kt + 1, nk - 1);  // the tail refetches the last tile into a stage nobody reads
-            fetch(A, B, p.lda, p.ldb, tile.m0, tile.n0, k_begin + next * BK, lds + ((kt + 1) & 1) * STAGE, wave, lane);
-            const unsigned short* stage = lds + (kt & 1) * STAGE;
-            const unsigned short* la = stage + (wm * WTM + lane % 32) * BK;
-            const unsigned short* lb = stage + BM * BK + (wn * WTN + lane % 32) * BK;
-            bf16x8_t af[2][MI], bfr[2][NJ];
-            const auto read = [&](int s, bf16x8_t (&fa)[MI], bf16x8_t (&fb)[NJ]) {
-                const int off = 8 * ((2 * s + lane / 32) ^ sw);
-#pragma unroll
-                for (int i = 0; i < MI; ++i) fa[i] = *reinterpret_cast<const bf16x8_t*>(la + i * 32 * BK + off);
-#pragma unroll
-                for (int j = 0; j < NJ; ++j) fb[j] = *reinterpret_cast<const bf16x8_t*>(lb + j * 32 * BK + off);
-            };
-            read(0, af[0], bfr[0]);
+        bf16x8_t af[2][MI], bfr[2][NJ];
+        // MI + NJ = 6 reads per substep; fragments i / j sit 32 * BK elements (4 KiB) apart
+        static_assert(MI == 4 && NJ == 2, "the read sequence below");
+        const auto read = [&](const unsigned short* stage, int s, bf16x8_t (&fa)[MI], bf16x8_t (&fb)[NJ]) {
+            const int off = 8 * ((2 * s + lane / 32) ^ sw);
+            const unsigned short* la = stage + (wm * WTM + lane % 32) * BK + off;
+            const unsigned short* lb = stage + BM * BK + (wn * WTN + lane % 32) * BK + off;
+            fa[0] = lds_read16<0>(la);
+            fa[1] = lds_read16<64 * BK>(la);
+            fa[2] = lds_read16<128 * BK>(la);
+            fa[3] = lds_read16<192 * BK>(la);
+            fb[0] = lds_read16<0>(lb);
+            fb[1] = lds_read16<64 * BK>(lb);
+        };
+        // one K tile from `cur`; inside its last substep K tile kt + 1 (in `other`) has landed in every
+        // wave and every wave holds its last fragments of kt, so `cur` takes K tile kt + 2 and the first
+        // fragments of kt + 1 are read under this substep's MFMAs
+        const auto k_tile = [&](int kt, unsigned short* cur, const unsigned short* other) {
 #pragma unroll
             for (int s = 0; s < BK / 16; ++s) {
-                if (s + 1 < BK / 16) read(s + 1, af[(s + 1) & 1], bfr[(s + 1) & 1]);
+                if (s + 1 < BK / 16) {
+                    read(cur, s + 1, af[(s + 1) & 1], bfr[(s + 1) & 1]);
+                    wait_lds_reads<6>();  // substep s's fragments have landed; s + 1's may stay in flight
+                } else if (kt + 1 < nk) {
+                    // the barrier's lgkmcnt(0) also lands substep s's fragments
+                    if (kt == 0) {
+                        if (first) big::dma_barrier<0>();
+                        else big::dma_barrier<S>();
+                    } else {
+                        big::dma_barrier<0>();
+                    }
+                    if (kt + 2 < nk) fetch_tile(tile, kt + 2, cur);
+                    read(other, 0, af[0], bfr[0]);
+                } else {
+                    wait_lds_reads<0>();
+                }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
@@ -691,8 +754,30 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                                                                            0, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
+        };
+        // K tile 0 has landed in every wave (the previous epilogue's stores may still be in flight)
+        if (first) big::dma_barrier<2 * IPW>();
+        else big::dma_barrier<2 * IPW + S>();
+        read(stage0, 0, af[0], bfr[0]);
+        for (int kt = 0; kt < nk; kt += 2) {  // nk is even: K splits are multiples of 128
+            k_tile(kt, stage0, stage1);
+            k_tile(kt + 1, stage1, stage0);
         }
-        big::dma_barrier<0>();  // the tail DMA has landed and every wave is past its last fragment reads
+        // the bias is loaded before the next tile's DMA so that waiting for it leaves the DMA in flight
+        const int col = tile.n0 + wn * WTN + (lane % LPR) * 8;
+        float bias8[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if (BIAS && direct) {
+            const float* bp = p.bias + tile.batch * p.stride_bias + col;
+            const float4 b0 = *reinterpret_cast<const float4*>(bp);
+            const float4 b1 = *reinterpret_cast<const float4*>(bp + 4);
+            bias8[0] = b0.x, bias8[1] = b0.y, bias8[2] = b0.z, bias8[3] = b0.w;
+            bias8[4] = b1.x, bias8[5] = b1.y, bias8[6] = b1.z, bias8[7] = b1.w;
+        }
+        // every wave is past its last fragment reads: the next tile's first two K tiles may land
+        // (the last tile refetches itself into stages nobody reads; the kernel drains them at exit)
+        big::lds_barrier();
+        fetch_tile(next, 0, stage0);
+        fetch_tile(next, 1, stage1);
 
         // ---- epilogue
         float* D = (direct && !p.d) ? nullptr
@@ -702,35 +787,26 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
         const long long ldd = direct ? p.ldd : p.n;
         const float* C = (direct && p.beta != 0.0f) ? p.c + tile.batch * p.stride_d : nullptr;
         unsigned short* Dh = (direct && p.d_bf16) ? p.d_bf16 + tile.batch * p.stride_d : nullptr;
-        const int col = tile.n0 + wn * WTN + (lane % LPR) * 8;
-        float bias8[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        if (direct && p.bias) {
-            const float* bp = p.bias + tile.batch * p.stride_bias + col;
-            const float4 b0 = *reinterpret_cast<const float4*>(bp);
-            const float4 b1 = *reinterpret_cast<const float4*>(bp + 4);
-            bias8[0] = b0.x, bias8[1] = b0.y, bias8[2] = b0.z, bias8[3] = b0.w;
-            bias8[4] = b1.x, bias8[5] = b1.y, bias8[6] = b1.z, bias8[7] = b1.w;
-        }
         const bool moments = direct && p.moments != nullptr;
         const bool round_moments = moments && !D;  // a bf16-only output takes the moments of the stored values
         float shift[8], s1[8], s2[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) shift[e] = s1[e] = s2[e] = 0.0f;
-        float* stagef = reinterpret_cast<float*>(lds) + wave * 32 * EP;
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
-            if (i) lds_fence();  // this wave's reads of the previous block are done
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                    stagef[(8 * (v / 4) + 4 * (lane / 32) + (v % 4)) * EP + j * 32 + lane % 32] = acc[i][j][v];
-            lds_fence();
 #pragma unroll
             for (int pass = 0; pass < 32 / RPP; ++pass) {
+                // rows 8 pass .. 8 pass + 7 of the block: acc[i][j][4 pass + e] holds row 8 pass + 4 (lane / 32) + e
+                lds_fence();  // this wave's reads of the previous pass are done
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        stagef[(4 * (lane / 32) + e) * EP + j * 32 + lane % 32] = acc[i][j][4 * pass + e];
+                lds_fence();
                 const int r = pass * RPP + lane / LPR;
-                const f32x4 x0 = *reinterpret_cast<const f32x4*>(stagef + r * EP + (lane % LPR) * 8);
-                const f32x4 x1 = *reinterpret_cast<const f32x4*>(stagef + r * EP + (lane % LPR) * 8 + 4);
+                const f32x4 x0 = *reinterpret_cast<const f32x4*>(stagef + (lane / LPR) * EP + (lane % LPR) * 8);
+                const f32x4 x1 = *reinterpret_cast<const f32x4*>(stagef + (lane / LPR) * EP + (lane % LPR) * 8 + 4);
                 float val[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
                 const long long offset = static_cast<long long>(tile.m0 + wm * WTM + i * 32 + r) * ldd + col;
                 if (direct) {
@@ -830,7 +906,10 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                 *reinterpret_cast<float4*>(out + p.n + 4) = make_float4(m2[4], m2[5], m2[6], m2[7]);
             }
         }
+        tile = next;
+        first = false;
     }
+    big::dma_barrier<0>();  // no DMA into this workgroup's LDS outlives it
 }
 
 }  // namespace wide
@@ -876,9 +955,24 @@ void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream) {
     // the eight-wave kernel writes the bf16 copy as 16-byte pieces of 8 columns
     const bool wide = ak && bk && p.k % (2 * big::wide::BK) == 0 && p.k_per_split % (2 * big::wide::BK) == 0 &&
                       (!p.d_bf16 || (aligned(p.d_bf16, 16) && p.ldd % 8 == 0 && p.stride_d % 8 == 0));
-    if (wide)
-        hipLaunchKernelGGL(big::wide::gemm_wide_kernel, grid, dim3(big::wide::NW * kWave), 0, stream, p, tiles_m,
-                           tiles_n, total);
+    if (wide) {
+        // unconditional 16-byte stores per lane per epilogue pass: the fp32 D (split-K partials or a
+        // direct fp32 output) takes 2, the bf16 copy 1
+        const bool direct = p.splits == 1;
+        const int spp = ((!direct || p.d) ? 2 : 0) + ((direct && p.d_bf16) ? 1 : 0);
+        require(spp > 0, "The GEMM has no output.");
+        const dim3 wblock(big::wide::NW * kWave);
+        const bool bias = direct && p.bias;
+#define RL_WIDE(SPP, BIAS) \
+    hipLaunchKernelGGL((big::wide::gemm_wide_kernel<SPP, BIAS>), grid, wblock, 0, stream, p, tiles_m, tiles_n, total)
+        if (spp == 1 && bias) RL_WIDE(1, true);
+        else if (spp == 1) RL_WIDE(1, false);
+        else if (spp == 2 && bias) RL_WIDE(2, true);
+        else if (spp == 2) RL_WIDE(2, false);
+        else if (bias) RL_WIDE(3, true);
+        else RL_WIDE(3, false);
+#undef RL_WIDE
+    }
     else if (dma) hipLaunchKernelGGL(big::gemm_dma_kernel, grid, block, 0, stream, p, tiles_m, tiles_n, total);
     else if (ak && bk) hipLaunchKernelGGL((big::gemm_big_kernel<true, true>), grid, block, 0, stream, p, tiles_m, tiles_n, total);
     else if (ak && !bk) hipLaunchKernelGGL((big::gemm_big_kernel<true, false>), grid, block, 0, stream, p, tiles_m, tiles_n, total);
