@@ -1,26 +1,29 @@
 #!/usr/bin/env python3
 """Learner hot-path benchmark on one MI355X.
 
-Default workload ("g1"): one captured HIP graph per
-step holding two FlashSAC updates (update-to-data 2: an actor+critic update and
-a critic-only update) at batch 8192, obs 123, act 37, actor 256x2, twin critics
-1024x2, 101 bins on [-20, 20], bf16 dense operands with fp32 state; replay
-4096 envs x 256 steps of seeded synthetic transitions resident in HBM.
+Headline ("g1"): one captured HIP graph per step
+holding two FlashSAC updates (update-to-data 2: an actor+critic update and a
+critic-only update) at batch 8192, obs 123, act 37, actor 256x2, twin critics
+1024x2, 101 bins on [-20, 20], bf16 dense operands with fp32 state, BatchNorm
+inputs and ReLU-BN gradients stored in bf16; replay 4096 envs x 256 steps of
+seeded synthetic transitions resident in HBM.
 
 Prints ONE JSON line: value = FlashSAC updates/sec on the GPU, with
-  roofline      the dominant kernel (critic block-1 forward GEMM, bf16 MFMA)
-                timed live with HIP events on the stream it runs on,
-  update_roofline  two-term serial roofline of the whole update,
-  cpu_baseline  the CPU oracle (PyTorch-CPU restatement of the reference update,
-                fp32) timed on this host's cores on one update of the same shape,
-  ppo           PPO update ms at configs[3] (one captured graph per update;
-                fp32-accurate products on the bf16 matrix cores, roofline at
-                the bf16 peak / 6; CPU oracle on one epoch scaled to five),
-  kernel_sweep  configs[4]: fused categorical target + CE, fused optimizer and
-                RMSNorm at their sweep shapes against the HBM roofline, plus the
-                replay ingest (n-step commit), return statistics and act()
-                (fp32 actor + exploration repeat) of one vector step at the G1
-                collection shape.
+  roofline        the dominant kernel (critic block-1 forward GEMM, bf16 MFMA)
+                  timed live with HIP events on the stream it runs on; its HBM
+                  traffic and MFMA-busy share come from the committed rocprofv3
+                  summary only when that summary names the same kernel, shape and
+                  kernel-source fingerprint as this build,
+  update_roofline two-term serial roofline of the whole update,
+  workloads       the other configurations at 1 GPU: G1 with fp32 BatchNorm
+                  activations, configs[0] Cartpole (fp32) and configs[1] README in
+                  both modes, each with updates/s and its update roofline,
+  ppo             PPO update ms at configs[3] (one captured graph per update),
+                  against the published fp32 matrix peak,
+  kernel_sweep    configs[4]: the HBM-bound kernels at their sweep shapes,
+  cpu_baseline    the CPU oracle (PyTorch-CPU restatement of the reference update,
+                  fp32) at G1 on this host's cores; cpu_baselines holds c0, c1,
+                  c2 and c3 at all cores and at 8 threads with the CPU model.
 """
 
 import argparse
@@ -33,7 +36,7 @@ import time
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
-TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_dma_critic_fwd_g1_traffic.md"
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemm_wide_critic_fwd_g1_counters.md"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
@@ -104,33 +107,68 @@ def elementwise_bytes(w: dict, act_bytes: int = 4) -> float:
     return critic_total + actor_bytes + optimizer + 3 * 2 * B * K * 4 * 4
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary, if it covers this kernel.
+def source_fingerprint() -> str:
+    """First 16 hex digits of the SHA-256 of the HIP sources (names and bytes, sorted by name)."""
+    import hashlib
 
-    The summary holds a `kernel:` line naming the launch and a
-    `traffic_bytes_per_launch:` line (FETCH_SIZE + WRITE_SIZE, each scaled by a
-    plain copy of known size); a summary for another kernel or shape is ignored.
-    """
+    digest = hashlib.sha256()
+    for path in sorted((ROOT / "robolearn_amd" / "csrc").glob("*")):
+        if path.suffix in (".hip", ".hpp"):
+            digest.update(path.name.encode())
+            digest.update(path.read_bytes())
+    return digest.hexdigest()[:16]
+
+
+def measured_counters(kernel: str) -> dict:
+    """HBM bytes per launch and MFMA-busy share of `kernel` from the committed rocprofv3 --pmc summary.
+
+    The summary holds `kernel:`, `source:` (the kernel-source fingerprint of the build it
+    measured), `traffic_bytes_per_launch:` (FETCH_SIZE + WRITE_SIZE, each scaled by a plain copy
+    of known size) and `mfma_busy_percent:` lines; a summary of another kernel, shape or build
+    is ignored, so the numbers cannot go stale silently."""
     try:
         text = TRAFFIC_PROFILE.read_text()
     except OSError:
-        return None
-    named = re.search(r"^kernel: (.+)$", text, flags=re.M)
-    value = re.search(r"^traffic_bytes_per_launch: (\d+)$", text, flags=re.M)
-    if named is None or value is None or named.group(1).strip() != kernel:
-        return None
-    return int(value.group(1))
+        return {}
+    fields = dict(re.findall(r"^([a-z_]+): (.+)$", text, flags=re.M))
+    if fields.get("kernel", "").strip() != kernel or fields.get("source", "").strip() != source_fingerprint():
+        return {}
+    out = {}
+    if "traffic_bytes_per_launch" in fields:
+        out["traffic"] = int(fields["traffic_bytes_per_launch"])
+    if "mfma_busy_percent" in fields:
+        out["mfma_busy_percent"] = float(fields["mfma_busy_percent"])
+    return out
 
 
-def cpu_baseline(w: dict, cfg_kwargs: dict) -> dict:
-    """Time the CPU oracle (fp32) on one actor-phase update at the workload shape."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as stream:
+            for line in stream:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median(values):
+    values = sorted(values)
+    n = len(values)
+    return values[n // 2] if n % 2 else 0.5 * (values[n // 2 - 1] + values[n // 2])
+
+
+def cpu_flashsac(w: dict, cfg_kwargs: dict, threads: int, warmups: int, timed: int) -> dict:
+    """The CPU oracle (fp32) at the workload shape: `warmups` untimed then `timed` timed updates,
+    alternating actor-phase and critic-only updates as the UTD-2 step does; seconds per update is
+    the mean of the two phases' medians."""
     import torch
+
+    from dataclasses import replace
 
     from oracle import flashsac as O
     from robolearn_amd.config import FlashSACConfig
-    from dataclasses import replace
 
-    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     cfg = FlashSACConfig(**cfg_kwargs)
     cfg = replace(cfg, temp_target_entropy=O.target_entropy(w["act"], cfg.temp_target_sigma))
@@ -140,36 +178,84 @@ def cpu_baseline(w: dict, cfg_kwargs: dict) -> dict:
     B = w["batch"]
     batch = {
         "observation": torch.randn(B, w["obs"], generator=g), "next_observation": torch.randn(B, w["obs"], generator=g),
-        "action": torch.rand(B, w["act"], generator=g) * 2 - 1, "reward": torch.randn(B, generator=g),
+        "action": torch.rand(B, w["act"], generator=g) * 2 - 1,
+        "reward": torch.randn(B, generator=g) * w["reward_std"],
         "terminated": (torch.rand(B, generator=g) < w["done"]).float(), "discount": torch.full((B,), cfg.gamma),
     }
     noise = torch.randn(2 * B, w["act"], generator=g)
     next_noise = torch.randn(B, w["act"], generator=g)
-    O.update(state, batch, noise, next_noise, do_actor_update=False)  # warm-up (critic-only)
-    t0 = time.perf_counter()
-    O.update(state, batch, noise, next_noise, do_actor_update=True)
-    actor_seconds = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    O.update(state, batch, noise, next_noise, do_actor_update=False)
-    critic_seconds = time.perf_counter() - t0
-    per_update = 0.5 * (actor_seconds + critic_seconds)
-    model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as stream:
-            for line in stream:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {
-        "value": 1.0 / per_update,
-        "unit": "updates/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"oracle.flashsac (PyTorch CPU fp32) at the same shape: 1 critic-only warm-up, then 1 actor-phase "
-                   f"({actor_seconds:.2f} s) + 1 critic-only ({critic_seconds:.2f} s) update timed; {model}"),
-    }
+    times = {True: [], False: []}
+    for i in range(warmups + timed):
+        actor = i % 2 == 0
+        t0 = time.perf_counter()
+        O.update(state, batch, noise, next_noise, do_actor_update=actor)
+        if i >= warmups:
+            times[actor].append(time.perf_counter() - t0)
+    medians = [_median(v) for v in times.values() if v]
+    return {"seconds_per_update": sum(medians) / len(medians), "threads": threads, "warmups": warmups,
+            "timed_updates": timed,
+            "phases": {"actor_phase_s": _median(times[True]) if times[True] else None,
+                       "critic_only_s": _median(times[False]) if times[False] else None}}
+
+
+def cpu_ppo(threads: int, warmups: int, timed: int) -> dict:
+    """The CPU oracle (fp32) on full c3 PPO updates (GAE, 5 epochs x 4 minibatches) of one rollout."""
+    import numpy as np
+    import torch
+
+    from oracle import ppo as OP
+
+    torch.set_num_threads(threads)
+    cfg = ppo_config()
+    E, T, O_, A = PPO_C3["envs"], PPO_C3["horizon"], PPO_C3["obs"], PPO_C3["act"]
+    n = E * T
+    rng = np.random.default_rng(0)
+    rollout = dict(observations=rng.standard_normal((n, O_)).astype(np.float32),
+                   actions=rng.standard_normal((n, A)).astype(np.float32),
+                   means=rng.standard_normal((n, A)).astype(np.float32) * 0.1, stds=np.ones((n, A), np.float32),
+                   values=rng.standard_normal(n).astype(np.float32),
+                   log_probs=rng.standard_normal(n).astype(np.float32) - 40.0,
+                   rewards=rng.standard_normal(n).astype(np.float32),
+                   next_values=rng.standard_normal(n).astype(np.float32),
+                   terminated=(rng.random(n) < 1e-3).astype(np.int32), truncated=np.zeros(n, np.int32))
+    params = OP.init_parameters(O_, A, cfg)
+    permutation = rng.permutation(n)
+    times = []
+    for i in range(warmups + timed):
+        oracle = OP.PPOOracle(O_, A, E, T, cfg, params, dtype=torch.float32)
+        t0 = time.perf_counter()
+        oracle.update(rollout, permutation)
+        if i >= warmups:
+            times.append(time.perf_counter() - t0)
+    return {"seconds_per_update": _median(times), "threads": threads, "warmups": warmups, "timed_updates": timed}
+
+
+def cpu_baselines() -> dict:
+    """c0, c1 (fp32), c2 and c3 on the CPU oracle at all host cores and at 8 threads (the reference
+    harnesses pin 8: examples/benchmark_warp_flashsac.py:87, benchmark_official_flashsac.py:878).
+    3 warm-ups and the median of 5 where the time allows; c2 (about 15-25 s per update on 8-16 cores)
+    is capped at 1 warm-up + 2 timed updates (one of each phase) and c3 (about 5 s per update) at
+    1 + 3 and 1 + 2; the counts are recorded in each entry."""
+    all_cores = len(os.sched_getaffinity(0))
+    out = {"cpu_model": cpu_model(), "all_cores": all_cores, "configs": {}}
+    plans = {"c0_cartpole": ("cartpole", 3, 5, 3, 5), "c1_readme_fp32": ("readme", 3, 5, 2, 3),
+             "c2_g1": ("g1", 1, 2, 1, 2)}
+    for label, (name, warm_all, timed_all, warm_8, timed_8) in plans.items():
+        w = dict(WORKLOADS[name], amp=False)
+        kwargs = flashsac_config_kwargs(w)
+        entry = {}
+        for threads, warm, timed in ((all_cores, warm_all, timed_all), (min(8, all_cores), warm_8, timed_8)):
+            print(f"[bench] CPU oracle {label} at {threads} threads", file=sys.stderr, flush=True)
+            result = cpu_flashsac(w, kwargs, threads, warm, timed)
+            entry[f"threads_{threads}"] = dict(result, updates_per_s=1.0 / result["seconds_per_update"])
+        out["configs"][label] = entry
+    entry = {}
+    for threads, warm, timed in ((all_cores, 1, 3), (min(8, all_cores), 1, 2)):
+        print(f"[bench] CPU oracle c3_ppo at {threads} threads", file=sys.stderr, flush=True)
+        result = cpu_ppo(threads, warm, timed)
+        entry[f"threads_{threads}"] = dict(result, ms_per_update=1e3 * result["seconds_per_update"])
+    out["configs"]["c3_ppo"] = entry
+    return out
 
 
 PPO_C3 = dict(envs=4096, horizon=24, obs=123, act=37, hidden=(512, 256, 128))
@@ -197,30 +283,40 @@ def ppo_flops(cfg) -> float:
     return float(rows * total)
 
 
-def ppo_rollout(agent, seed=0):
-    """Synthetic c3 rollout on the device: obs, values ~ N(0,1); actions = mu(obs) + sigma*eps with their
-    Gaussian log-probs; rewards ~ N(0,1); terminated ~ Bernoulli(1/1000); no truncations."""
+def ppo_rollout(agent, seed=0, behaviour_shift=0.025):
+    """Synthetic c3 rollout on the device: obs, next values ~ N(0,1); actions = mu(obs) + sigma*eps with
+    their Gaussian log-probs and the critic's values from act(), the stored means and values shifted by
+    N(0, behaviour_shift^2) as a rollout a few updates old holds; rewards ~ N(0,1); terminated ~
+    Bernoulli(1/1000); no truncations."""
+    import math
+
     import torch
 
     n = agent.batch_size
-    torch.manual_seed(seed)
-    obs = torch.randn(n, agent.observation_dim, device=agent.device)
+    g = torch.Generator(device=agent.device).manual_seed(seed)
+    obs = torch.randn(n, agent.observation_dim, generator=g, device=agent.device)
     actions = agent.act(obs)
     sampled = agent._act_state(n)
+    means = sampled["mean"] + behaviour_shift * torch.randn(n, agent.action_dim, generator=g, device=agent.device)
+    std = sampled["std"].expand(n, -1)
+    log_probs = (-0.5 * (((actions - means) / std) ** 2 + 2.0 * torch.log(std) + math.log(2 * math.pi))).sum(-1)
     agent.observations.copy_(obs)
     agent.actions.copy_(actions)
-    agent.log_probs.copy_(sampled["log_probs"])
-    agent.means.copy_(sampled["mean"])
-    agent.stds.copy_(sampled["std"].expand(n, -1))
-    agent.values.copy_(torch.randn(n, device=agent.device))
-    agent.next_values.copy_(torch.randn(n, device=agent.device))
-    agent.rewards.copy_(torch.randn(n, device=agent.device))
-    agent.terminated.copy_((torch.rand(n, device=agent.device) < 1e-3).int())
+    agent.log_probs.copy_(log_probs)
+    agent.means.copy_(means)
+    agent.stds.copy_(std)
+    agent.values.copy_(sampled["values"] + behaviour_shift * torch.randn(n, generator=g, device=agent.device))
+    agent.next_values.copy_(torch.randn(n, generator=g, device=agent.device))
+    agent.rewards.copy_(torch.randn(n, generator=g, device=agent.device))
+    agent.terminated.copy_((torch.rand(n, generator=g, device=agent.device) < 1e-3).int())
     agent.truncated.zero_()
 
 
-def bench_ppo(steps: int, warmup: int, with_cpu: bool) -> dict:
-    """PPO update ms at c3: one captured graph (GAE, permutation, 5 epochs x 4 minibatches) per update."""
+def bench_ppo(steps: int, warmup: int) -> dict:
+    """PPO update ms at c3: one captured graph (GAE, permutation, 5 epochs x 4 minibatches) per update.
+    The roofline prices the fp32 product FLOPs against the published fp32 matrix peak (157.3 TFLOP/s);
+    the products run as fp32-accurate three-piece bf16 splits (6 bf16 MFMA products per fp32 product),
+    whose issued bf16 rate is reported beside it."""
     import torch
 
     from robolearn_amd import kernels as K
@@ -229,12 +325,11 @@ def bench_ppo(steps: int, warmup: int, with_cpu: bool) -> dict:
     cfg = ppo_config()
     agent = WarpPPO(PPO_C3["obs"], PPO_C3["act"], PPO_C3["envs"], PPO_C3["horizon"], cfg)
     ppo_rollout(agent)
-    initial = agent.state_dict() if with_cpu else None
     agent.update()  # captures the graph (after an eager warm-up that restores the state)
     for _ in range(warmup):
         agent.update()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start, end = _events()
     start.record()
     for _ in range(steps):
         agent.update()
@@ -244,51 +339,28 @@ def bench_ppo(steps: int, warmup: int, with_cpu: bool) -> dict:
     flops = ppo_flops(cfg)
     achieved = flops / (ms * 1e-3) / 1e12
     split = agent.gemm_mode == K.FP32_SPLIT
-    # fp32-accurate products on the bf16 matrix cores cost six bf16 products per fp32 product
-    peak = BF16_PEAK_TFLOPS / 6.0 if split else FP32_PEAK_TFLOPS
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "flops_per_update": flops,
+                "products": "fp32-accurate three-piece bf16 splits (6 bf16 MFMA products per fp32 product)"
+                if split else "v_mfma_f32_32x32x2_f32"}
+    if split:
+        roofline["issued_bf16_tflops"] = round(6 * achieved, 2)
+        roofline["issued_bf16_frac"] = round(6 * achieved / BF16_PEAK_TFLOPS, 4)
     result = {
         "metric": "PPO update ms", "value": round(ms, 4), "unit": "ms/update", "higher_is_better": False,
         "dtype": "fp32", "steps": steps, "warmup": warmup,
         "config": {"workload": "ppo_c3", "envs": PPO_C3["envs"], "horizon": PPO_C3["horizon"],
                    "obs_dim": PPO_C3["obs"], "act_dim": PPO_C3["act"], "hidden": list(cfg.hidden_dims),
                    "activation": cfg.activation, "epochs": cfg.epochs, "minibatches": cfg.num_mini_batches,
-                   "schedule": cfg.schedule, "desired_kl": cfg.desired_kl},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
-                     "frac": round(achieved / peak, 4), "flops_per_update": flops,
-                     "products": ("fp32-accurate: three-piece bf16 splits, 6 bf16 MFMA products per fp32 product; "
-                                  "peak = bf16 dense peak / 6") if split else "v_mfma_f32_32x32x2_f32"},
+                   "schedule": cfg.schedule, "desired_kl": cfg.desired_kl,
+                   "grad_clipping": "separate" if cfg.separate_grad_clipping else "combined"},
+        "roofline": roofline,
         "cpu_baseline": None,
     }
-    if with_cpu:
-        result["cpu_baseline"] = ppo_cpu_baseline(agent, initial)
     del agent
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     return result
-
-
-def ppo_cpu_baseline(agent, initial: dict) -> dict:
-    """The CPU oracle (fp32) on one epoch of the same rollout (4 minibatch steps), scaled to 5 epochs."""
-    import numpy as np
-    import torch
-
-    from oracle import ppo as OP
-
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
-    cfg = ppo_config(epochs=1)
-    rollout = {name: getattr(agent, name).cpu().numpy() for name in
-               ("observations", "actions", "means", "stds", "values", "log_probs", "rewards", "next_values",
-                "terminated", "truncated")}
-    layers = [initial[f"parameter_{i}"] for i in range(len(agent.parameters))]
-    oracle = OP.PPOOracle(PPO_C3["obs"], PPO_C3["act"], PPO_C3["envs"], PPO_C3["horizon"], cfg, layers,
-                          dtype=torch.float32)
-    permutation = np.random.default_rng(0).permutation(agent.batch_size)
-    t0 = time.perf_counter()
-    oracle.update(rollout, permutation)
-    seconds = time.perf_counter() - t0
-    epochs = ppo_config().epochs
-    return {"value": round(seconds * epochs * 1e3, 1), "unit": "ms/update", "cores": threads, "kind": "port",
-            "sample": f"oracle.ppo (PyTorch CPU fp32): GAE + 1 epoch x 4 minibatches timed ({seconds:.2f} s), "
-                      f"scaled x{epochs} epochs"}
 
 
 def _time_launches(launch, reps: int = 20) -> float:
@@ -475,44 +547,94 @@ def kernel_sweep() -> list:
     return lines
 
 
-def main() -> int:
-    parser = argparse.ArgumentParser(description=__doc__)
-    parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=5)
-    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="g1")
-    parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--no-extras", action="store_true",
-                        help="skip the PPO (c3) update timing and the HBM kernel sweep (c4)")
-    parser.add_argument("--calibration-copy-mb", type=int, default=0,
-                        help="after timing, run one plain device copy of this size (counter calibration)")
-    parser.add_argument("--traffic", type=float, default=None,
-                        help="HBM bytes per launch of the dominant kernel measured with rocprofv3 --pmc (reported)")
-    args = parser.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: the learner path is single-GPU (see DESIGN.md for sharding).",
-              file=sys.stderr)
-        return 2
+def flashsac_config_kwargs(w: dict) -> dict:
+    B = w["batch"]
+    capacity = w["envs"] * w["horizon"]
+    return dict(seed=0, normalize_reward=False, n_step=1, sample_batch_size=B, buffer_max_length=capacity,
+                buffer_min_length=B, actor_hidden_dim=w["actor_hidden"], actor_num_blocks=w["actor_blocks"],
+                critic_hidden_dim=w["critic_hidden"], critic_num_blocks=w["critic_blocks"],
+                critic_num_bins=w["bins"], critic_min_v=w["min_v"], critic_max_v=w["max_v"],
+                critic_target_update_tau=0.005, learning_rate_init=3e-4, learning_rate_peak=3e-4,
+                learning_rate_end=3e-4, gamma=0.99, use_amp=w["amp"], actor_update_period=2)
 
+
+def _events():
+    import torch
+
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def dominant_kernel(agent, w: dict, reps: int = 20, calibration_copy_mb: int = 0) -> dict:
+    """Critic block-1 forward GEMM [2 x 2B x h] . [4h x h]^T at the shape it runs with inside the
+    update, timed over `reps` launches with HIP events recorded on the stream it is launched on."""
+    import torch
+
+    from robolearn_amd import kernels as K
+
+    net = agent.critic_net
+    h, rows = net.h, 2 * w["batch"]
+    launch = lambda: K.linear_forward(net.op(net.stream[0], net.stream_h[0]),  # noqa: E731
+                                      agent.critic_w["encoder.0.w1.weight"], net.u1[0], rows=rows, in_dim=h,
+                                      out_dim=4 * h, ensemble=2, mode=agent.mode)
+    launch()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()  # kernels.stream() launches on torch's current stream
+    k0, k1 = _events()
+    k0.record(stream)
+    for _ in range(reps):
+        launch()
+    k1.record(stream)
+    torch.cuda.synchronize()
+    kernel_ms = k0.elapsed_time(k1) / reps
+    if calibration_copy_mb:
+        # one plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE counter readings
+        n = calibration_copy_mb * (1 << 20) // 4
+        src = torch.ones(n, device=net.u1[0].device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    flops = 2.0 * 2 * rows * h * 4 * h
+    bf16 = agent.mode == K.BF16
+    peak = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    out_type = "bf16" if net.u1[0].dtype == torch.bfloat16 else "fp32"
+    shape = f"critic block-1 forward [2 x {rows} x {h}] . [{4 * h} x {h}]^T -> {out_type}"
+    if bf16 and rows % 256 == 0 and (4 * h) % 256 == 0 and h % 128 == 0:
+        kernel = f"rl::gemm::big::wide::gemm_wide_kernel {shape}"  # 8 waves, 256x256 tiles, DMA-fed
+    elif bf16:
+        kernel = f"rl::gemm::gemm_bf16_kernel {shape}"
+    else:
+        kernel = f"rl::gemm::gemm_kernel {shape}"
+    operand_bytes = 2 if bf16 else 4
+    algorithmic_bytes = 2 * (rows * h + 4 * h * h) * operand_bytes + 2 * rows * 4 * h * net.u1[0].element_size()
+    counters = measured_counters(kernel)
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4), "traffic": counters.get("traffic"), "kernel": kernel,
+                "kernel_ms": round(kernel_ms, 4), "flops_per_launch": flops,
+                "algorithmic_bytes_per_launch": algorithmic_bytes, "source": source_fingerprint()}
+    if "mfma_busy_percent" in counters:
+        roofline["mfma_busy_percent"] = counters["mfma_busy_percent"]
+    return roofline
+
+
+def run_flashsac(name: str, steps: int, warmup: int, *, bf16_activations: bool = True, amp=None,
+                 dominant: bool = False, calibration_copy_mb: int = 0) -> dict:
+    """Updates/s of one workload: seeded synthetic replay resident in HBM, one captured graph per step
+    (UTD 2: actor-phase + critic-only update, device-side replay sampling inside the graph)."""
     import torch
 
     from robolearn_amd import kernels as K
     from robolearn_amd.config import FlashSACConfig
     from robolearn_amd.flashsac import FlashSAC
 
-    w = WORKLOADS[args.workload]
-    B = w["batch"]
-    capacity = w["envs"] * w["horizon"]
-    cfg_kwargs = dict(seed=0, normalize_reward=False, n_step=1, sample_batch_size=B, buffer_max_length=capacity,
-                      buffer_min_length=B, actor_hidden_dim=w["actor_hidden"], actor_num_blocks=w["actor_blocks"],
-                      critic_hidden_dim=w["critic_hidden"], critic_num_blocks=w["critic_blocks"],
-                      critic_num_bins=w["bins"], critic_min_v=w["min_v"], critic_max_v=w["max_v"],
-                      critic_target_update_tau=0.005, learning_rate_init=3e-4, learning_rate_peak=3e-4,
-                      learning_rate_end=3e-4, gamma=0.99, use_amp=w["amp"], actor_update_period=2)
-    cfg = FlashSACConfig(**cfg_kwargs)
+    w = dict(WORKLOADS[name])
+    if amp is not None:
+        w["amp"] = amp
+    cfg = FlashSACConfig(**flashsac_config_kwargs(w))
     device = torch.device("cuda:0")
-    torch.cuda.set_device(device)
-    agent = FlashSAC(w["obs"], w["act"], num_envs=w["envs"], cfg=cfg)
+    capacity = w["envs"] * w["horizon"]
+    agent = FlashSAC(w["obs"], w["act"], num_envs=w["envs"], cfg=cfg, bf16_activations=bf16_activations)
     g = torch.Generator(device=device).manual_seed(0)
     data = {
         "observation": torch.randn(capacity, w["obs"], generator=g, device=device),
@@ -525,117 +647,132 @@ def main() -> int:
     }
     agent.load_replay(data)
     del data
-    graph = agent.capture_pair() if w["utd"] == 2 else None
-    print(f"[bench] workload {args.workload}: captured update-to-data-{w['utd']} graph", file=sys.stderr, flush=True)
-
-    def step():
-        if graph is not None:
-            graph.replay()
-        else:
-            agent.update()
-
-    for _ in range(args.warmup):
-        step()
+    agent.capture_pair()
+    for _ in range(warmup):
+        agent.update_pair(tensor_metrics=True)
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start, end = _events()
     start.record()
-    for _ in range(args.steps):
-        step()
+    for _ in range(steps):
+        agent.update_pair(tensor_metrics=True)
     end.record()
     torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / args.steps
-    updates_per_second = w["utd"] * 1000.0 / ms_per_step
-    print(f"[bench] {ms_per_step:.3f} ms per step, {updates_per_second:.1f} updates/s", file=sys.stderr, flush=True)
-
-    # Dominant kernel: critic block-1 forward GEMM [2 x 2B x h] . [4h x h]^T (bf16 MFMA), timed live on the
-    # stream it is launched on, at the shape it runs with inside the update.
-    net = agent.critic_net
-    h = net.h
-    rows = 2 * B
-    reps = 20
-    launch = lambda: K.linear_forward(net.op(net.stream[0], net.stream_h[0]),  # noqa: E731
-                                      agent.critic_w["encoder.0.w1.weight"], net.u1[0], rows=rows, in_dim=h,
-                                      out_dim=4 * h, ensemble=2, mode=agent.mode)
-    launch()
-    torch.cuda.synchronize()
-    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    k0.record()
-    for _ in range(reps):
-        launch()
-    k1.record()
-    torch.cuda.synchronize()
-    kernel_ms = k0.elapsed_time(k1) / reps
-    kernel_flops = 2.0 * 2 * rows * h * 4 * h
-    peak = {K.BF16: BF16_PEAK_TFLOPS, K.FP32_SPLIT: BF16_PEAK_TFLOPS / 6.0}.get(agent.mode, FP32_PEAK_TFLOPS)
-    achieved = kernel_flops / (kernel_ms * 1e-3) / 1e12
-    operand = "unsigned short" if agent.mode == K.BF16 else "float"
-    out_type = "bf16" if net.u1[0].dtype == torch.bfloat16 else "fp32"
-    shape = f"critic block-1 forward [2 x {rows} x {h}] . [{4 * h} x {h}]^T -> {out_type}"
-    if agent.mode == K.BF16 and rows % 256 == 0 and (4 * h) % 256 == 0 and h % 128 == 0:
-        kernel_name = f"gemm_dma_kernel {shape}"  # 256x256 tiles, DMA-fed (both operands K-contiguous)
-    elif agent.mode == K.BF16:
-        kernel_name = f"gemm_bf16_kernel<{operand}, {operand}, true, true> {shape}"
-    else:
-        kernel_name = f"gemm_kernel<0, float, float, true, true> {shape}"
-    traffic = args.traffic if args.traffic is not None else measured_traffic(kernel_name)
-    operand_bytes = 2 if agent.mode == K.BF16 else 4
-    # the output is the BatchNorm input: bf16 in bf16 mode
-    algorithmic_bytes = 2 * (rows * h + 4 * h * h) * operand_bytes + 2 * rows * 4 * h * net.u1[0].element_size()
-    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": kernel_name,
-                "kernel_ms": round(kernel_ms, 4), "flops_per_launch": kernel_flops,
-                "algorithmic_bytes_per_launch": algorithmic_bytes}
-    if args.calibration_copy_mb:
-        # plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE counter readings
-        n = args.calibration_copy_mb * (1 << 20) // 4
-        src = torch.ones(n, device=device)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    ms_per_step = start.elapsed_time(end) / steps
+    bf16 = agent.mode == K.BF16
+    act_bytes = 2 if agent.bf16_activations else 4
     flops = gemm_flops(w)
-    hbm_bytes = elementwise_bytes(w, 2 if agent.mode == K.BF16 else 4)
+    hbm_bytes = elementwise_bytes(w, act_bytes)
+    peak = BF16_PEAK_TFLOPS if bf16 else FP32_PEAK_TFLOPS
     t_roof_ms = (flops / (peak * 1e12) + hbm_bytes / (HBM_PEAK_GBS * 1e9)) * 1e3
-    update_roofline = {"gemm_tflop_per_step": round(flops / 1e12, 3),
-                       "elementwise_gb_per_step": round(hbm_bytes / 1e9, 3),
-                       "t_roof_ms_per_step": round(t_roof_ms, 3),
-                       "frac": round(t_roof_ms / ms_per_step, 4)}
+    result = {
+        "workload": f"flashsac_{name}", "updates_per_s": round(2000.0 / ms_per_step, 3),
+        "ms_per_step": round(ms_per_step, 4), "steps": steps, "warmup": warmup,
+        "dtype": "bf16" if bf16 else "fp32",
+        "batchnorm_activations": "bf16" if agent.bf16_activations else "fp32",
+        "update_roofline": {"gemm_tflop_per_step": round(flops / 1e12, 4),
+                            "elementwise_gb_per_step": round(hbm_bytes / 1e9, 4), "peak_tflops": peak,
+                            "t_roof_ms_per_step": round(t_roof_ms, 4), "frac": round(t_roof_ms / ms_per_step, 4)},
+    }
+    if dominant:
+        result["roofline"] = dominant_kernel(agent, w, calibration_copy_mb=calibration_copy_mb)
+    del agent
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return result
 
-    ppo, sweep = None, None
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--workload", choices=sorted(WORKLOADS), default="g1")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-extras", action="store_true",
+                        help="headline only: skip the other workloads, PPO (c3) and the kernel sweep (c4)")
+    parser.add_argument("--calibration-copy-mb", type=int, default=0,
+                        help="after timing the dominant kernel, one plain device copy of this size "
+                             "(scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: every GPU box of this build has one GPU, and the learner "
+              "update runs on one GPU.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    torch.cuda.set_device(0)
+    w = WORKLOADS[args.workload]
+    head = run_flashsac(args.workload, args.steps, args.warmup, dominant=True,
+                        calibration_copy_mb=args.calibration_copy_mb)
+    print(f"[bench] {args.workload}: {head['ms_per_step']:.3f} ms per step, {head['updates_per_s']:.1f} updates/s",
+          file=sys.stderr, flush=True)
+
+    others, ppo, sweep = None, None, None
     if not args.no_extras:
+        few = max(5, args.steps // 2)
+        others = []
+        plans = [("g1", dict(bf16_activations=False)), ("cartpole", {}), ("readme", {}),
+                 ("readme", dict(amp=True)), ("readme", dict(amp=True, bf16_activations=False))]
+        for name, kwargs in plans:
+            if name == args.workload and not kwargs:
+                continue
+            line = run_flashsac(name, few, 2, **kwargs)
+            others.append(line)
+            print(f"[bench] {line['workload']} {line['dtype']} (BatchNorm activations "
+                  f"{line['batchnorm_activations']}): {line['updates_per_s']:.1f} updates/s",
+                  file=sys.stderr, flush=True)
         print("[bench] PPO c3 update", file=sys.stderr, flush=True)
-        ppo = bench_ppo(max(5, args.steps // 2), 2, not args.no_cpu_baseline)
+        ppo = bench_ppo(max(5, args.steps // 2), 2)
         print("[bench] kernel sweep", file=sys.stderr, flush=True)
         sweep = kernel_sweep()
 
-    baseline = None
+    baselines, baseline = None, None
     if not args.no_cpu_baseline:
-        print("[bench] timing the CPU oracle baseline", file=sys.stderr, flush=True)
-        baseline = cpu_baseline(w, cfg_kwargs)
+        print("[bench] timing the CPU oracle baselines", file=sys.stderr, flush=True)
+        baselines = cpu_baselines()
+        label = {"g1": "c2_g1", "readme": "c1_readme_fp32", "cartpole": "c0_cartpole"}[args.workload]
+        entry = baselines["configs"][label][f"threads_{baselines['all_cores']}"]
+        baseline = {"value": round(entry["updates_per_s"], 4), "unit": "updates/s", "cores": entry["threads"],
+                    "kind": "port",
+                    "sample": f"oracle.flashsac (PyTorch CPU, fp32) at the {args.workload} shape on "
+                              f"{baselines['cpu_model']}: {entry['warmups']} warm-up + {entry['timed_updates']} "
+                              f"timed updates alternating actor-phase and critic-only; mean of the two phases' "
+                              f"medians"}
+        if ppo is not None:
+            c3 = baselines["configs"]["c3_ppo"][f"threads_{baselines['all_cores']}"]
+            ppo["cpu_baseline"] = {"value": round(c3["ms_per_update"], 1), "unit": "ms/update",
+                                   "cores": c3["threads"], "kind": "port",
+                                   "sample": f"oracle.ppo (PyTorch CPU, fp32): full c3 updates, "
+                                             f"{c3['warmups']} warm-up + median of {c3['timed_updates']}"}
 
+    B = w["batch"]
     result = {
         "metric": "FlashSAC updates/sec at batch 8192 (1 GPU)" if args.workload == "g1"
         else f"FlashSAC updates/sec at batch {B} (1 GPU)",
-        "value": round(updates_per_second, 3),
+        "value": head["updates_per_s"],
         "unit": "updates/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16" if w["amp"] else "fp32",
+        "dtype": head["dtype"],
         "data": "synthetic",
         "config": {"workload": f"flashsac_{args.workload}", "batch": B, "obs_dim": w["obs"], "act_dim": w["act"],
                    "actor": f"{w['actor_hidden']}x{w['actor_blocks']}",
                    "critic": f"2x {w['critic_hidden']}x{w['critic_blocks']}", "bins": w["bins"],
-                   "updates_per_step": w["utd"], "replay_rows": capacity, "parallelism": "single-gpu"},
-        "roofline": roofline,
-        "update_roofline": update_roofline,
+                   "updates_per_step": w["utd"], "replay_rows": w["envs"] * w["horizon"],
+                   "batchnorm_activations": head["batchnorm_activations"], "parallelism": "single-gpu"},
+        "roofline": head["roofline"],
+        "update_roofline": head["update_roofline"],
         "cpu_baseline": baseline,
+        "workloads": others,
         "ppo": ppo,
         "kernel_sweep": sweep,
+        "cpu_baselines": baselines,
     }
     print(json.dumps(result))
     return 0
