@@ -20,6 +20,7 @@
 #include "gemm.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace rl {
 namespace gemm {
@@ -178,14 +179,15 @@ __device__ __forceinline__ float4 activate4(float4 v, int epilogue) {
 
 // Logical tile id -> output tile.  Within a (batch, split) slice tiles go in
 // groups of GroupM M-tiles, M fastest, so consecutive ids share operand panels.
+template <int GM = GroupM>
 __device__ __forceinline__ Tile tile_of(int id, int tiles_m, int tiles_n, int splits) {
     const int per_slice = tiles_m * tiles_n;
     const int slice = id / per_slice;
     const int t = id % per_slice;
-    const int group = t / (GroupM * tiles_n);
-    const int first_m = group * GroupM;
-    const int group_m = min(tiles_m - first_m, GroupM);
-    const int local = t % (GroupM * tiles_n);
+    const int group = t / (GM * tiles_n);
+    const int first_m = group * GM;
+    const int group_m = min(tiles_m - first_m, GM);
+    const int local = t % (GM * tiles_n);
     return Tile{(first_m + local % group_m) * BM, (local / group_m) * BN, slice / splits, slice % splits};
 }
 
@@ -579,6 +581,7 @@ constexpr int NW = 8;                 // waves per workgroup
 constexpr int WTM = 128, WTN = 64;    // wave tile
 constexpr int MI = WTM / 32, NJ = WTN / 32;
 constexpr int BK = 64;                // K depth per stage
+constexpr int kGroupM = 4;            // M tiles per group of the tile order (4 measured faster than 8 here)
 constexpr int CPR = BK / 8;           // 16-byte chunks per LDS row
 constexpr int RPI = 64 / CPR;         // rows per DMA instruction
 constexpr int IPW = 4 * CPR / NW;     // DMA instructions per operand per wave per stage
@@ -614,6 +617,52 @@ __device__ __forceinline__ void fetch(const unsigned short* A, const unsigned sh
             (__attribute__((address_space(1))) void*)(B + static_cast<long long>(n0 + row) * ldb + k0 + chunk * 8),
             (__attribute__((address_space(3))) void*)(stage + BM * BK + q * 512), 16, 0, 0);
     }
+}
+
+// M/N-contiguous operands (a weight gradient dW = dY^T X reads both operands
+// along their rows): a stage holds 64 K rows x 256 M (N) of each operand, 512
+// bytes per K row, and the 16-byte M granule c of K row k sits in slot
+// c ^ tslot(k).  DMA instruction q of an operand fills K rows 2q and 2q + 1;
+// lane l loads the granule that belongs in slot l % 32 of row 2q + l / 32.
+__device__ __forceinline__ int tslot(int k) { return 4 * (k & 3); }
+
+__device__ __forceinline__ void fetch_mn(const unsigned short* A, const unsigned short* B, long long lda, long long ldb,
+                                         int m0, int n0, int k0, unsigned short* stage, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+        const int q = wave * IPW + j;
+        const int k = 2 * q + lane / 32;
+        const int granule = (lane % 32) ^ tslot(k);
+        __builtin_amdgcn_global_load_lds(
+            (__attribute__((address_space(1))) void*)(A + static_cast<long long>(k0 + k) * lda + m0 + granule * 8),
+            (__attribute__((address_space(3))) void*)(stage + q * 512), 16, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+        const int q = wave * IPW + j;
+        const int k = 2 * q + lane / 32;
+        const int granule = (lane % 32) ^ tslot(k);
+        __builtin_amdgcn_global_load_lds(
+            (__attribute__((address_space(1))) void*)(B + static_cast<long long>(k0 + k) * ldb + n0 + granule * 8),
+            (__attribute__((address_space(3))) void*)(stage + BM * BK + q * 512), 16, 0, 0);
+    }
+}
+static_assert(2 * IPW * NW == BK, "fetch_mn: two K rows per DMA instruction");
+
+// 8-byte transposing LDS read (ds_read_b64_tr_b16) of `p`, inline assembly for
+// the same reason as lds_read16 below.  In each 16-lane group, lane i receives
+// 16-bit element i % 4 of the 8-byte pieces that lanes i / 4, i / 4 + 4,
+// i / 4 + 8 and i / 4 + 12 address: with lane c addressing K row k0 + c / 4 at
+// M offset 4 (c % 4), lane i holds M offset i and K rows k0 .. k0 + 3.
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+template <int OFF>
+__device__ __forceinline__ u32x2_t lds_read8_tr(const unsigned short* p) {
+    static_assert(OFF >= 0 && OFF < 65536, "ds_read offset is 16 bits");
+    const auto local = (__attribute__((address_space(3))) const unsigned short*)p;  // LDS byte offset
+    const unsigned address = (unsigned)(uintptr_t)local;
+    u32x2_t v;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(address), "i"(OFF));
+    return v;
 }
 
 // 16-byte LDS read of `p` + OFF bytes, issued as inline assembly.  The compiler
@@ -654,14 +703,15 @@ __device__ __forceinline__ void merge8(float& count, float (&mean)[8], float (&m
     count = total;
 }
 
-// SPP: 16-byte stores every lane issues per 8-row epilogue pass (2 for an fp32 D,
-// 1 for the bf16 copy).  BIAS: the product adds a bias (a kernel without one
+// MN: both operands M/N-contiguous (fetch_mn, transposing fragment reads); else
+// both K-contiguous.  SPP: 16-byte stores every lane issues per 8-row epilogue
+// pass (2 for an fp32 D, 1 for the bf16 copy).  BIAS: the product adds a bias (a kernel without one
 // issues no epilogue loads, whose registers the next tile's fragment reads
 // would otherwise wait on).  The next tile's first two K tiles are fetched before
 // the epilogue, so the waits for them may leave S = 16 SPP stores in flight
 // (vector-memory counts complete in issue order); the conditional moment
 // stores and the bias / C loads only make those waits stricter.
-template <int SPP, bool BIAS>
+template <int SPP, bool BIAS, bool MN>
 __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int tiles_m, int tiles_n, int total) {
     constexpr int S = MI * (32 / RPP) * SPP;
     static_assert(SPP >= 1 && 2 * IPW + S < 64, "vmcnt is a 6-bit count");
@@ -684,21 +734,31 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
     const auto fetch_tile = [&](const Tile& t, int kt, unsigned short* stage) {
         const unsigned short* A = static_cast<const unsigned short*>(p.a) + t.batch * p.stride_a;
         const unsigned short* B = static_cast<const unsigned short*>(p.b) + t.batch * p.stride_b;
-        fetch(A, B, p.lda, p.ldb, t.m0, t.n0, t.split * p.k_per_split + kt * BK, stage, wave, lane);
+        if constexpr (MN) fetch_mn(A, B, p.lda, p.ldb, t.m0, t.n0, t.split * p.k_per_split + kt * BK, stage, wave, lane);
+        else fetch(A, B, p.lda, p.ldb, t.m0, t.n0, t.split * p.k_per_split + kt * BK, stage, wave, lane);
     };
+    // transposing reads (MN): lane l reads K rows 16 s + 8 (l / 32) + 4 r + (l % 16) / 4 of substep s,
+    // r = 0, 1, at M offset 16 ((l / 16) % 2) + 4 (l % 4) of each 32-wide fragment; the K row's slot
+    // swizzle is tslot = 4 ((l % 16) / 4) for every row this lane reads
+    // (the swizzle XOR acts on granule bits 2-3 only: fragment i of A sits 32 (i ^ tq) elements from
+    // fragment 0's granule group, fragment j of B at ((wn WTN / 8 + 4 j) ^ 4 tq) granules)
+    const int tq = (lane % 16) / 4;
+    const int t_low = 2 * ((lane / 16) % 2) + (lane % 4) / 2;
+    const int t_base_a = (8 * (lane / 32) + tq) * BM + ((wm * WTM) / 8 + t_low) * 8 + 4 * (lane % 2);
+    const int t_base_b = BM * BK + (8 * (lane / 32) + tq) * BN + t_low * 8 + 4 * (lane % 2);
     const auto k_tiles = [&](const Tile& t) {
         const int k_begin = t.split * p.k_per_split;
         return (min(p.k, k_begin + p.k_per_split) - k_begin) / BK;  // even, >= 2: K splits are multiples of 128
     };
     if (slot >= total) return;
-    Tile tile = big::tile_of(slot, tiles_m, tiles_n, p.splits);
+    Tile tile = big::tile_of<kGroupM>(slot, tiles_m, tiles_n, p.splits);
     fetch_tile(tile, 0, stage0);
     fetch_tile(tile, 1, stage1);
     bool first = true;
     float* stagef = staging + wave * RPP * EP;
 
     for (int id = slot; id < total; id += G) {
-        const Tile next = id + G < total ? big::tile_of(id + G, tiles_m, tiles_n, p.splits) : tile;
+        const Tile next = id + G < total ? big::tile_of<kGroupM>(id + G, tiles_m, tiles_n, p.splits) : tile;
         const int nk = k_tiles(tile);
 
         f32x16_t acc[MI][NJ];
@@ -710,9 +770,32 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
         bf16x8_t af[2][MI], bfr[2][NJ];
-        // MI + NJ = 6 reads per substep; fragments i / j sit 32 * BK elements (4 KiB) apart
+        // K-contiguous: MI + NJ = 6 reads per substep, fragments i / j 32 * BK elements (4 KiB) apart;
+        // MN: 2 (MI + NJ) = 12 transposing reads
         static_assert(MI == 4 && NJ == 2, "the read sequence below");
-        const auto read = [&](const unsigned short* stage, int s, bf16x8_t (&fa)[MI], bf16x8_t (&fb)[NJ]) {
+        constexpr int kReads = MN ? 2 * (MI + NJ) : MI + NJ;
+        const auto read = [&](const unsigned short* stage, auto s_const, bf16x8_t (&fa)[MI], bf16x8_t (&fb)[NJ]) {
+            constexpr int s = decltype(s_const)::value;
+            if constexpr (MN) {
+                // substep rows and the second 4-row half go in the instruction's offset field (bytes)
+                constexpr int kLo = 2 * 16 * s * BM, kHi = kLo + 2 * 4 * BM;
+                static_assert(BM == BN, "A and B rows share the offsets");
+#pragma unroll
+                for (int i = 0; i < MI; ++i) {
+                    const unsigned short* q = stage + t_base_a + 32 * (i ^ tq);
+                    const u32x2_t lo = lds_read8_tr<kLo>(q);
+                    const u32x2_t hi = lds_read8_tr<kHi>(q);
+                    fa[i] = __builtin_bit_cast(bf16x8_t, (u32x4){lo[0], lo[1], hi[0], hi[1]});
+                }
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    const unsigned short* q = stage + t_base_b + ((((wn * WTN) / 8 + 4 * j) ^ (4 * tq)) * 8);
+                    const u32x2_t lo = lds_read8_tr<kLo>(q);
+                    const u32x2_t hi = lds_read8_tr<kHi>(q);
+                    fb[j] = __builtin_bit_cast(bf16x8_t, (u32x4){lo[0], lo[1], hi[0], hi[1]});
+                }
+                return;
+            }
             const int off = 8 * ((2 * s + lane / 32) ^ sw);
             const unsigned short* la = stage + (wm * WTM + lane % 32) * BK + off;
             const unsigned short* lb = stage + BM * BK + (wn * WTN + lane % 32) * BK + off;
@@ -727,23 +810,25 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
         // wave and every wave holds its last fragments of kt, so `cur` takes K tile kt + 2 and the first
         // fragments of kt + 1 are read under this substep's MFMAs
         const auto k_tile = [&](int kt, unsigned short* cur, const unsigned short* other) {
-#pragma unroll
-            for (int s = 0; s < BK / 16; ++s) {
-                if (s + 1 < BK / 16) {
-                    read(cur, s + 1, af[(s + 1) & 1], bfr[(s + 1) & 1]);
-                    wait_lds_reads<6>();  // substep s's fragments have landed; s + 1's may stay in flight
-                } else if (kt + 1 < nk) {
-                    // the barrier's lgkmcnt(0) also lands substep s's fragments
-                    if (kt == 0) {
-                        if (first) big::dma_barrier<0>();
-                        else big::dma_barrier<S>();
-                    } else {
-                        big::dma_barrier<0>();
-                    }
-                    if (kt + 2 < nk) fetch_tile(tile, kt + 2, cur);
-                    read(other, 0, af[0], bfr[0]);
+            const auto substep = [&](auto s_const) {
+                constexpr int s = decltype(s_const)::value;
+                if constexpr (s + 1 < BK / 16) {
+                    read(cur, std::integral_constant<int, s + 1>{}, af[(s + 1) & 1], bfr[(s + 1) & 1]);
+                    wait_lds_reads<kReads>();  // substep s's fragments have landed; s + 1's may stay in flight
                 } else {
-                    wait_lds_reads<0>();
+                    if (kt + 1 < nk) {
+                        // the barrier's lgkmcnt(0) also lands substep s's fragments
+                        if (kt == 0) {
+                            if (first) big::dma_barrier<0>();
+                            else big::dma_barrier<S>();
+                        } else {
+                            big::dma_barrier<0>();
+                        }
+                        if (kt + 2 < nk) fetch_tile(tile, kt + 2, cur);
+                        read(other, std::integral_constant<int, 0>{}, af[0], bfr[0]);
+                    } else {
+                        wait_lds_reads<0>();
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -753,12 +838,17 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s & 1][i], bfr[s & 1][j], acc[i][j], 0,
                                                                            0, 0);
                 __builtin_amdgcn_sched_barrier(0);
-            }
+            };
+            static_assert(BK / 16 == 4, "four substeps per K tile");
+            substep(std::integral_constant<int, 0>{});
+            substep(std::integral_constant<int, 1>{});
+            substep(std::integral_constant<int, 2>{});
+            substep(std::integral_constant<int, 3>{});
         };
         // K tile 0 has landed in every wave (the previous epilogue's stores may still be in flight)
         if (first) big::dma_barrier<2 * IPW>();
         else big::dma_barrier<2 * IPW + S>();
-        read(stage0, 0, af[0], bfr[0]);
+        read(stage0, std::integral_constant<int, 0>{}, af[0], bfr[0]);
         for (int kt = 0; kt < nk; kt += 2) {  // nk is even: K splits are multiples of 128
             k_tile(kt, stage0, stage1);
             k_tile(kt + 1, stage1, stage0);
@@ -953,7 +1043,8 @@ void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream) {
     const dim3 block(big::T);
     const bool dma = ak && bk && p.k % (big::DS * big::BK) == 0 && p.k_per_split % (big::DS * big::BK) == 0;
     // the eight-wave kernel writes the bf16 copy as 16-byte pieces of 8 columns
-    const bool wide = ak && bk && p.k % (2 * big::wide::BK) == 0 && p.k_per_split % (2 * big::wide::BK) == 0 &&
+    // (both operands K-contiguous, or both M/N-contiguous: the weight gradients)
+    const bool wide = ak == bk && p.k % (2 * big::wide::BK) == 0 && p.k_per_split % (2 * big::wide::BK) == 0 &&
                       (!p.d_bf16 || (aligned(p.d_bf16, 16) && p.ldd % 8 == 0 && p.stride_d % 8 == 0));
     if (wide) {
         // unconditional 16-byte stores per lane per epilogue pass: the fp32 D (split-K partials or a
@@ -963,8 +1054,15 @@ void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream) {
         require(spp > 0, "The GEMM has no output.");
         const dim3 wblock(big::wide::NW * kWave);
         const bool bias = direct && p.bias;
-#define RL_WIDE(SPP, BIAS) \
-    hipLaunchKernelGGL((big::wide::gemm_wide_kernel<SPP, BIAS>), grid, wblock, 0, stream, p, tiles_m, tiles_n, total)
+#define RL_WIDE(SPP, BIAS)                                                                                           \
+    do {                                                                                                            \
+        if (ak)                                                                                                     \
+            hipLaunchKernelGGL((big::wide::gemm_wide_kernel<SPP, BIAS, false>), grid, wblock, 0, stream, p, tiles_m, \
+                               tiles_n, total);                                                                     \
+        else                                                                                                        \
+            hipLaunchKernelGGL((big::wide::gemm_wide_kernel<SPP, BIAS, true>), grid, wblock, 0, stream, p, tiles_m,  \
+                               tiles_n, total);                                                                     \
+    } while (0)
         if (spp == 1 && bias) RL_WIDE(1, true);
         else if (spp == 1) RL_WIDE(1, false);
         else if (spp == 2 && bias) RL_WIDE(2, true);

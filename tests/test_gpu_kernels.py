@@ -246,9 +246,10 @@ def test_td_cross_entropy_matches_oracle_projection(gpu, bins):
 # Shapes that take the 256x256-tile bf16 kernel (m, n multiples of 256, K ranges
 # multiples of 128): workgroup counts below and at multiples of 8 (the XCD
 # renumbering), more tiles than CUs (the persistent loop), partial M-tile groups,
-# split-K, and every operand layout.
+# split-K, and every operand layout (both K-contiguous and both M/N-contiguous
+# take the eight-wave DMA kernel, the mixed layouts the register-staged one).
 BIG_SHAPES = [(2, 512, 256, 128, 1), (2, 2560, 512, 256, 1), (1, 3072, 256, 128, 1), (2, 1024, 512, 1024, 4),
-              (2, 4096, 4096, 128, 1)]
+              (2, 4096, 4096, 128, 1), (1, 512, 256, 8192, 2)]  # the last: a weight gradient's long K, split
 
 
 @pytest.mark.parametrize("a_kcontig", [True, False])
