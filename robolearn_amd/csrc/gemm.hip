@@ -40,16 +40,22 @@ constexpr int kFp32K = 16;              // K per LDS step
 constexpr int kFp32Pitch = kFp32K + 4;  // floats per LDS row
 constexpr int kSplitPitch = kFp32K + 8; // bf16 per LDS row of a split plane (48 bytes: 16-lane reads hit distinct banks)
 
-// x = x0 + x1 + x2 in bf16 pieces (round to nearest even at each step; both
-// differences are exact in fp32).
-__device__ __forceinline__ void split3(float x, unsigned short& h0, unsigned short& h1, unsigned short& h2) {
-    const __bf16 b0 = static_cast<__bf16>(x);
-    const float r1 = x - static_cast<float>(b0);
-    const __bf16 b1 = static_cast<__bf16>(r1);
-    const float r2 = r1 - static_cast<float>(b1);
-    h0 = __builtin_bit_cast(unsigned short, b0);
-    h1 = __builtin_bit_cast(unsigned short, b1);
-    h2 = __builtin_bit_cast(unsigned short, static_cast<__bf16>(r2));
+// x = x0 + x1 + x2 exactly in bf16 pieces, two values at a time: x0 keeps x's
+// top 8 significant bits (bf16 by truncation), r1 = x - x0 is exact in fp32
+// (same exponent), x1 keeps r1's top 8 bits, and r2 = r1 - x1 has at most 8
+// significant bits left, so x2 = r2 is exact in bf16.  Each piece's bf16 bits
+// are the high half of its fp32 bits; one byte permute packs the pieces of a
+// and b into a plane word (a in the low half).
+__device__ __forceinline__ void split3_pair(float a, float b, unsigned& p0, unsigned& p1, unsigned& p2) {
+    constexpr unsigned kHigh = 0xFFFF0000u;
+    constexpr unsigned kHighHalves = 0x07060302u;  // bytes 2, 3 of the second operand, then of the first
+    const unsigned ua = __float_as_uint(a), ub = __float_as_uint(b);
+    const float ra = a - __uint_as_float(ua & kHigh), rb = b - __uint_as_float(ub & kHigh);
+    const unsigned ura = __float_as_uint(ra), urb = __float_as_uint(rb);
+    const float sa = ra - __uint_as_float(ura & kHigh), sb = rb - __uint_as_float(urb & kHigh);
+    p0 = __builtin_amdgcn_perm(ub, ua, kHighHalves);
+    p1 = __builtin_amdgcn_perm(urb, ura, kHighHalves);
+    p2 = __builtin_amdgcn_perm(__float_as_uint(sb), __float_as_uint(sa), kHighHalves);
 }
 
 // Loads one Rows x 16 operand tile into registers and later stores it to LDS.
@@ -122,24 +128,23 @@ struct TileLoader {
             for (int i = 0; i < PerThread; ++i) {
                 const int v = i * kThreads + t;
                 const int offset = (v / VecPerRow) * kSplitPitch + (v % VecPerRow) * 4;
-                unsigned short h[3][4];
+                unsigned w[3][2];
+                split3_pair(regs[i * 4 + 0], regs[i * 4 + 1], w[0][0], w[1][0], w[2][0]);
+                split3_pair(regs[i * 4 + 2], regs[i * 4 + 3], w[0][1], w[1][1], w[2][1]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) split3(regs[i * 4 + e], h[0][e], h[1][e], h[2][e]);
-#pragma unroll
-                for (int q = 0; q < 3; ++q)
-                    *reinterpret_cast<uint2*>(lds + q * Plane + offset) =
-                        make_uint2(h[q][0] | (static_cast<unsigned int>(h[q][1]) << 16),
-                                   h[q][2] | (static_cast<unsigned int>(h[q][3]) << 16));
+                for (int q = 0; q < 3; ++q) *reinterpret_cast<uint2*>(lds + q * Plane + offset) = make_uint2(w[q][0], w[q][1]);
             }
         } else {
+            // KPer consecutive K values of one row: packed into 4-byte words per plane
+            static_assert(KPer % 2 == 0 && kSplitPitch % 2 == 0, "pairs of K values share a word");
             const int offset = (t % Rows) * kSplitPitch + (t / Rows) * KPer;
 #pragma unroll
-            for (int e = 0; e < KPer; ++e) {
-                unsigned short h0, h1, h2;
-                split3(regs[e], h0, h1, h2);
-                lds[offset + e] = h0;
-                lds[Plane + offset + e] = h1;
-                lds[2 * Plane + offset + e] = h2;
+            for (int e = 0; e < KPer; e += 2) {
+                unsigned w0, w1, w2;
+                split3_pair(regs[e], regs[e + 1], w0, w1, w2);
+                *reinterpret_cast<unsigned*>(lds + offset + e) = w0;
+                *reinterpret_cast<unsigned*>(lds + Plane + offset + e) = w1;
+                *reinterpret_cast<unsigned*>(lds + 2 * Plane + offset + e) = w2;
             }
         }
     }

@@ -291,28 +291,38 @@ def test_ppo_c3_captured_update_matches_oracle(gpu):
     Adam's first step shifts -- the oracle itself ends at a 1.5^5 different learning rate in float32 and
     float64 on this rollout -- so the update is compared with the oracle run in float32, the
     reference's own precision (the Warp learner is fp32): the learning rate exactly (same rule
-    decisions), KL and losses 1e-3 relative, parameters 1e-4 relative to the tensor maximum.  The
-    float64 oracle's result is printed beside it."""
+    decisions), KL and losses within 1e-3 relative or 3x the float32-float64 difference of the same
+    metric, parameters within a 1e-2 sanity bound relative to the tensor maximum (the per-step
+    arithmetic is held by the teacher-forced test below).  The float64 oracle's result is printed
+    beside it."""
     print("case c3 PPO full captured update vs float32 oracle", flush=True)
     cfg = _c3_config()
     agent, oracle, result, rollout, permutation, initial = _c3_run(gpu, cfg, torch.float32)
     health = agent.health_metrics()
-    exact = OP.PPOOracle(123, 37, 4096, 24, cfg, [initial[f"parameter_{i}"] for i in range(len(agent.parameters))],
-                         dtype=torch.float64).update(rollout, permutation)
+    exact_oracle = OP.PPOOracle(123, 37, 4096, 24, cfg,
+                                [initial[f"parameter_{i}"] for i in range(len(agent.parameters))], dtype=torch.float64)
+    exact = exact_oracle.update(rollout, permutation)
     print(f"c3: MI355X kl {health['kl']:.6g} lr {health['learning_rate']:.6g}; float32 oracle kl {result['kl']:.6g} "
           f"lr {result['learning_rate']:.6g}; float64 oracle kl {exact['kl']:.6g} lr {exact['learning_rate']:.6g}",
           flush=True)
     assert health["learning_rate"] == pytest.approx(result["learning_rate"], rel=1e-6)
     for key in ("kl", "policy_loss", "value_loss", "entropy"):
-        assert health[key] == pytest.approx(result[key], rel=1e-3, abs=1e-6), key
+        # the last minibatch's metrics sit at the end of a chaotic 20-step trajectory: the GPU may differ
+        # from the float32 oracle by 1e-3 relative or by 3x what float32 and float64 differ by
+        allowed = max(1e-3 * abs(result[key]) + 1e-6, 3.0 * abs(result[key] - exact[key]))
+        assert abs(health[key] - result[key]) <= allowed, (key, health[key], result[key], exact[key])
     np.testing.assert_allclose(agent.advantages.cpu().numpy(), oracle.advantages.numpy(), atol=1e-5)
     state = agent.state_dict()
     worst = 0.0
-    for i, p in enumerate(oracle.params):
+    for i, (p, pe) in enumerate(zip(oracle.params, exact_oracle.params)):
         ref = p.detach().double()
-        rel = (torch.as_tensor(state[f"parameter_{i}"]).double() - ref).abs().max().item() / ref.abs().max().item()
+        scale = ref.abs().max().item()
+        rel = (torch.as_tensor(state[f"parameter_{i}"]).double() - ref).abs().max().item() / scale
+        chaos = (ref - pe.detach().double()).abs().max().item() / scale  # float32 vs float64, same update
         worst = max(worst, rel)
-        assert rel < 1e-2, (i, rel)  # sanity only: the fixed-schedule test below holds the arithmetic
+        # sanity only (the teacher-forced test below holds the arithmetic): 1e-2, or 3x the float32-float64
+        # difference where the trajectory's chaos is larger
+        assert rel < max(1e-2, 3.0 * chaos), (i, rel, chaos)
     print(f"c3 adaptive: worst parameter difference to the float32 oracle, relative to the tensor max {worst:.2e}",
           flush=True)
 
