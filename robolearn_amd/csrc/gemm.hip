@@ -36,9 +36,9 @@
 namespace rl {
 namespace gemm {
 
-constexpr int kFp32K = 16;              // K per LDS step
+constexpr int kFp32K = 32;              // K per LDS step: two 16-K MFMA substeps (16: 16.3 ms per c3 PPO update, 32: 15.4, 64: 21.1 -- occupancy 2)
 constexpr int kFp32Pitch = kFp32K + 4;  // floats per LDS row
-constexpr int kSplitPitch = kFp32K + 8; // bf16 per LDS row of a split plane (48 bytes: 16-lane reads hit distinct banks)
+constexpr int kSplitPitch = kFp32K + 8; // bf16 per LDS row of a split plane (80 bytes: row starts 20 banks apart)
 
 // x = x0 + x1 + x2 exactly in bf16 pieces, two values at a time: x0 keeps x's
 // top 8 significant bits (bf16 by truncation), r1 = x - x0 is exact in fp32
@@ -254,8 +254,10 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
             lb.load(B, p.ldb, n0, k0 + kFp32K, p.n, k_end, bvec);
         }
         if constexpr (Split) {
+#pragma unroll
+          for (int sub = 0; sub < kFp32K / 16; ++sub) {
             bf16x8_t af[WB][3], bf[WB][3];
-            const int koff = 8 * (lane / 32);
+            const int koff = 16 * sub + 8 * (lane / 32);
 #pragma unroll
             for (int i = 0; i < WB; ++i) {
                 const int off = (wm * (T / 2) + i * 32 + lane % 32) * kSplitPitch + koff;
@@ -282,23 +284,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
                     acc[i][j] = c;
                 }
             }
+          }
             __syncthreads();
             if (more) stage();
             __syncthreads();
             continue;
-        }
-        float4 af[WB][2], bfr[WB][2];
-#pragma unroll
-        for (int i = 0; i < WB; ++i) {
-            const float* q = sa + (wm * (T / 2) + i * 32 + lane % 32) * kFp32Pitch + (lane / 32) * 8;
-            af[i][0] = *reinterpret_cast<const float4*>(q);
-            af[i][1] = *reinterpret_cast<const float4*>(q + 4);
-        }
-#pragma unroll
-        for (int j = 0; j < WB; ++j) {
-            const float* q = sb + (wn * (T / 2) + j * 32 + lane % 32) * kFp32Pitch + (lane / 32) * 8;
-            bfr[j][0] = *reinterpret_cast<const float4*>(q);
-            bfr[j][1] = *reinterpret_cast<const float4*>(q + 4);
         }
         if (row_sums) {
             const float* q = sa + (threadIdx.x / SumLanes) * kFp32Pitch + (threadIdx.x % SumLanes) * SumPer;
@@ -306,14 +296,30 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
             for (int e = 0; e < SumPer; ++e) add_sum(q[e]);
         }
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int sub = 0; sub < kFp32K / 16; ++sub) {
+            float4 af[WB][2], bfr[WB][2];
 #pragma unroll
             for (int i = 0; i < WB; ++i) {
-                const float a = s < 4 ? af[i][0][s] : af[i][1][s - 4];
+                const float* q = sa + (wm * (T / 2) + i * 32 + lane % 32) * kFp32Pitch + 16 * sub + (lane / 32) * 8;
+                af[i][0] = *reinterpret_cast<const float4*>(q);
+                af[i][1] = *reinterpret_cast<const float4*>(q + 4);
+            }
 #pragma unroll
-                for (int j = 0; j < WB; ++j) {
-                    const float b = s < 4 ? bfr[j][0][s] : bfr[j][1][s - 4];
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
+            for (int j = 0; j < WB; ++j) {
+                const float* q = sb + (wn * (T / 2) + j * 32 + lane % 32) * kFp32Pitch + 16 * sub + (lane / 32) * 8;
+                bfr[j][0] = *reinterpret_cast<const float4*>(q);
+                bfr[j][1] = *reinterpret_cast<const float4*>(q + 4);
+            }
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+#pragma unroll
+                for (int i = 0; i < WB; ++i) {
+                    const float a = s < 4 ? af[i][0][s] : af[i][1][s - 4];
+#pragma unroll
+                    for (int j = 0; j < WB; ++j) {
+                        const float b = s < 4 ? bfr[j][0][s] : bfr[j][1][s - 4];
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
+                    }
                 }
             }
         }
