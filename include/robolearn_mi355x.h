@@ -354,14 +354,17 @@ int rl_ppo_store(int step, long long num_envs, int obs_dim, int action_dim, cons
  * entropy loss and its gradients (robolearn/warp/ppo.py:255-310), the KL of the
  * pre-step policy with the adaptive learning-rate rule (:207-238) and the
  * std-parameter gradient summed over rows.  partial needs (5 + A) * ceil(rows / 16)
- * floats; dstd [A] is overwritten; action_dim <= 64. */
-int rl_ppo_minibatch_loss(const float* mean, long long ld_mean, const float* value, const float* std_param,
-                          const float* actions, const float* old_log_probs, const float* old_values,
-                          const float* advantages, const float* returns, const float* old_mean, const float* old_std,
-                          long long rows, int action_dim, int std_type, float std_min, float std_max, float clip_ratio,
-                          float value_coefficient, float entropy_coefficient, float value_loss_scale, int clip_value,
-                          float desired_kl, int adapt, float* dmean, float* dvalue, float* dstd, float* partial,
-                          float* totals, float* kl, float* lr, void* stream);
+ * floats; dstd [A] is overwritten; action_dim <= 64.  value and dvalue are read and
+ * written at row pitches ld_value and ld_dvalue (the value head's column of a
+ * batched actor/critic head output). */
+int rl_ppo_minibatch_loss(const float* mean, long long ld_mean, const float* value, long long ld_value,
+                          const float* std_param, const float* actions, const float* old_log_probs,
+                          const float* old_values, const float* advantages, const float* returns, const float* old_mean,
+                          const float* old_std, long long rows, int action_dim, int std_type, float std_min,
+                          float std_max, float clip_ratio, float value_coefficient, float entropy_coefficient,
+                          float value_loss_scale, int clip_value, float desired_kl, int adapt, float* dmean,
+                          float* dvalue, long long ld_dvalue, float* dstd, float* partial, float* totals, float* kl,
+                          float* lr, void* stream);
 /* Keyed Feistel permutation with cycle walking; replaces _shuffle_keys +
  * radix_sort_pairs, robolearn/warp/ppo.py:162-169, 595-603. */
 int rl_permutation(long long n, unsigned long long seed, const int* seed_counter, long long* perm64, int* perm32,

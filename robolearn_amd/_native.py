@@ -122,8 +122,9 @@ SIGNATURES = {
     "rl_ppo_kl_adapt": (c_int, [P, c_ll, P, P, P, c_ll, c_int, c_int, c_float, c_float, c_float, c_int, P, P, P, P]),
     "rl_ppo_loss": (c_int, [P, c_ll, P, P, P, P, P, P, P, c_ll, c_int, c_int, c_float, c_float, c_float, c_float,
                             c_float, c_float, c_int, P, P, P, P, P, P]),
-    "rl_ppo_minibatch_loss": (c_int, [P, c_ll, P, P, P, P, P, P, P, P, P, c_ll, c_int, c_int, c_float, c_float,
-                                      c_float, c_float, c_float, c_float, c_int, c_float, c_int] + [P] * 7 + [P]),
+    "rl_ppo_minibatch_loss": (c_int, [P, c_ll, P, c_ll, P, P, P, P, P, P, P, P, c_ll, c_int, c_int, c_float,
+                                      c_float, c_float, c_float, c_float, c_float, c_int, c_float, c_int, P, P, c_ll]
+                              + [P] * 5 + [P]),
     "rl_sum_squares": (c_int, [P, c_ll, P, P, P]),
     "rl_clip_by_norm": (c_int, [P, c_ll, P, c_float, P]),
     "rl_elu_backward": (c_int, [P, P, c_ll, P]),

@@ -227,7 +227,8 @@ __global__ __launch_bounds__(kThreads) void kl_finish(const float* partial, int 
 struct LossArgs {
     const float* mean;
     long long ld_mean;
-    const float* value;       // critic output [rows, 1]
+    const float* value;       // critic output, row pitch ld_value
+    long long ld_value;
     const float* std_param;
     const float* actions;
     const float* old_log_probs;
@@ -241,7 +242,8 @@ struct LossArgs {
     float clip_ratio, value_coefficient, entropy_coefficient, value_loss_scale;
     int clip_value;
     float* dmean;             // [rows, A]
-    float* dvalue;            // [rows]
+    float* dvalue;            // row pitch ld_dvalue
+    long long ld_dvalue;
     float* dstd_rows;         // [rows, A] per-row std-parameter gradient (when std_partial is null)
     float* partial;           // [4, blocks]: total, policy, value, entropy sums (already scaled by 1/rows)
     // fused minibatch form: KL(N_old || N_new) sums in partial row 4 (old_mean, old_std given), and the
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(kRowThreads) void loss_kernel(LossArgs a) {
         float dratio;
         if (unclipped <= clipped) dratio = -adv;
         else dratio = (ratio > lo && ratio < hi) ? -adv : 0.0f;
-        const float v = a.value[i];
+        const float v = a.value[i * a.ld_value];
         const float error = v - a.returns[i];
         float value_loss = error * error;
         float dv = 2.0f * error;
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(kRowThreads) void loss_kernel(LossArgs a) {
         }
         value_loss = a.value_loss_scale * value_loss;
         dv *= a.value_loss_scale;
-        if (lane == 0) a.dvalue[i] = scale * a.value_coefficient * dv;
+        if (lane == 0) a.dvalue[i * a.ld_dvalue] = scale * a.value_coefficient * dv;
         const float dlp = scale * dratio * ratio;
         for (int j = lane; j < a.action_dim; j += kWave) {
             const float p = a.std_param[j];
@@ -686,9 +688,10 @@ RL_API int rl_ppo_loss(const float* mean, long long ld_mean, const float* value,
                     "PPO loss needs every input and output buffer.");
         const long long blocks = (rows + Q::kRowsPerBlock - 1) / Q::kRowsPerBlock;
         rl::require(blocks <= (1LL << 30), "PPO loss row count is too large.");
-        Q::LossArgs a{mean, ld_mean, value, std_param, actions, old_log_probs, old_values, advantages, returns, rows,
-                      action_dim, std_type, std_min, std_max, clip_ratio, value_coefficient, entropy_coefficient,
-                      value_loss_scale, clip_value, dmean, dvalue, dstd_rows, row_terms, nullptr, nullptr, false};
+        Q::LossArgs a{mean, ld_mean, value, 1, std_param, actions, old_log_probs, old_values, advantages, returns,
+                      rows, action_dim, std_type, std_min, std_max, clip_ratio, value_coefficient,
+                      entropy_coefficient, value_loss_scale, clip_value, dmean, dvalue, 1, dstd_rows, row_terms,
+                      nullptr, nullptr, false};
         const hipStream_t st = rl::as_stream(stream);
         hipLaunchKernelGGL(Q::loss_kernel, dim3(static_cast<unsigned>(blocks)), dim3(Q::kRowThreads), 0, st, a);
         rl::check_launch("Launch PPO loss");
@@ -697,14 +700,14 @@ RL_API int rl_ppo_loss(const float* mean, long long ld_mean, const float* value,
     });
 }
 
-RL_API int rl_ppo_minibatch_loss(const float* mean, long long ld_mean, const float* value, const float* std_param,
-                                 const float* actions, const float* old_log_probs, const float* old_values,
-                                 const float* advantages, const float* returns, const float* old_mean,
-                                 const float* old_std, long long rows, int action_dim, int std_type, float std_min,
-                                 float std_max, float clip_ratio, float value_coefficient, float entropy_coefficient,
-                                 float value_loss_scale, int clip_value, float desired_kl, int adapt, float* dmean,
-                                 float* dvalue, float* dstd, float* partial, float* totals, float* kl, float* lr,
-                                 void* stream) noexcept {
+RL_API int rl_ppo_minibatch_loss(const float* mean, long long ld_mean, const float* value, long long ld_value,
+                                 const float* std_param, const float* actions, const float* old_log_probs,
+                                 const float* old_values, const float* advantages, const float* returns,
+                                 const float* old_mean, const float* old_std, long long rows, int action_dim,
+                                 int std_type, float std_min, float std_max, float clip_ratio, float value_coefficient,
+                                 float entropy_coefficient, float value_loss_scale, int clip_value, float desired_kl,
+                                 int adapt, float* dmean, float* dvalue, long long ld_dvalue, float* dstd,
+                                 float* partial, float* totals, float* kl, float* lr, void* stream) noexcept {
     return rl::guarded("rl_ppo_minibatch_loss", [&] {
         rl::require(mean && value && std_param && actions && old_log_probs && old_values && advantages && returns &&
                         old_mean && old_std && dmean && dvalue && dstd && partial && totals && kl && lr && rows > 0,
@@ -712,9 +715,11 @@ RL_API int rl_ppo_minibatch_loss(const float* mean, long long ld_mean, const flo
         rl::require(action_dim > 0 && action_dim <= rl::kWave, "PPO minibatch loss supports 1..64 action dimensions.");
         const long long blocks = (rows + Q::kRowsPerBlock - 1) / Q::kRowsPerBlock;
         rl::require(blocks <= (1LL << 30), "PPO loss row count is too large.");
-        Q::LossArgs a{mean, ld_mean, value, std_param, actions, old_log_probs, old_values, advantages, returns, rows,
-                      action_dim, std_type, std_min, std_max, clip_ratio, value_coefficient, entropy_coefficient,
-                      value_loss_scale, clip_value, dmean, dvalue, nullptr, partial, old_mean, old_std, true};
+        rl::require(ld_value >= 1 && ld_dvalue >= 1, "PPO minibatch loss value pitches must be positive.");
+        Q::LossArgs a{mean, ld_mean, value, ld_value, std_param, actions, old_log_probs, old_values, advantages,
+                      returns, rows, action_dim, std_type, std_min, std_max, clip_ratio, value_coefficient,
+                      entropy_coefficient, value_loss_scale, clip_value, dmean, dvalue, ld_dvalue, nullptr, partial,
+                      old_mean, old_std, true};
         const hipStream_t st = rl::as_stream(stream);
         hipLaunchKernelGGL(Q::loss_kernel, dim3(static_cast<unsigned>(blocks)), dim3(Q::kRowThreads), 0, st, a);
         rl::check_launch("Launch PPO minibatch loss");

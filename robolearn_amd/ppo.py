@@ -72,12 +72,23 @@ class WarpPPO:
         self.layers = len(cfg.hidden_dims) + 1
         actor = _mlp_shapes("actor", O, A, cfg.hidden_dims)
         critic = _mlp_shapes("critic", O, 1, cfg.hidden_dims)
-        shapes = dict(actor + critic + [("std", (A,))])
+        # With hidden layers the two output layers run as one batch-2 product of A outputs: the
+        # value head's weight and bias are followed in the flat store by A - 1 zero rows (never
+        # optimized, never part of a named parameter), so member 1 of the batch is the value head
+        # padded to A outputs whose extra outputs and gradients are exactly zero.
+        last = self.layers - 1
+        self.batched_heads = bool(cfg.hidden_dims)
+        pads = {}
+        if self.batched_heads and A > 1:
+            pads = {f"critic.{last}.weight": (f"critic.{last}.weight_pad", (A - 1, cfg.hidden_dims[-1])),
+                    f"critic.{last}.bias": (f"critic.{last}.bias_pad", (A - 1,))}
+        shapes = dict(actor + critic + [("std", (A,))] + list(pads.values()))
         dev = self.device
         with torch.cuda.device(dev):
             # actor tensors + std parameter form clipping group 0, critic tensors group 1
             order = [[n for n, _ in actor] + ["std"], [n for n, _ in critic]]
-            self.flat = FlatStore(shapes, dev, groups=[[n] for n in order[0]] + [[n] for n in order[1]])
+            groups = [[n] for n in order[0]] + [[n] + ([pads[n][0]] if n in pads else []) for n in order[1]]
+            self.flat = FlatStore(shapes, dev, groups=groups)
             self.names = [n for n, _ in actor] + [n for n, _ in critic] + ["std"]
             views = self.flat.params()
             self.parameters = [views[n] for n in self.names]
@@ -131,10 +142,19 @@ class WarpPPO:
                              for i in range(len(cfg.hidden_dims))]
             self.b_stride = [offsets[f"critic.{i}.bias"] - offsets[f"actor.{i}.bias"]
                              for i in range(len(cfg.hidden_dims))]
-            self.mean = z(M, A)
-            self.value = z(M, 1)
-            self.dmean = z(M, A)
-            self.dvalue = z(M, 1)
+            if self.batched_heads:
+                # [2, M, A]: member 0 the mean, member 1 column 0 the value (columns 1.. stay zero in
+                # the gradient: the loss writes column 0 only)
+                self.head_out, self.head_grad = z(2, M, A), z(2, M, A)
+                self.mean, self.value = self.head_out[0], self.head_out[1]
+                self.dmean, self.dvalue = self.head_grad[0], self.head_grad[1]
+                self.value_ld = A
+                self.head_w_stride = offsets[f"critic.{last}.weight"] - offsets[f"actor.{last}.weight"]
+                self.head_b_stride = offsets[f"critic.{last}.bias"] - offsets[f"actor.{last}.bias"]
+            else:
+                self.mean, self.value = z(M, A), z(M, 1)
+                self.dmean, self.dvalue = z(M, A), z(M, 1)
+                self.value_ld = 1
             self.loss_partial = z((5 + A) * ((M + 15) // 16))  # per-16-row-workgroup loss, KL, std-gradient sums
             self.totals = z(4)
             self.metrics = self.totals[1:]  # policy loss, value loss, entropy of the last minibatch
@@ -202,11 +222,17 @@ class WarpPPO:
                    ldd=width, stride_a=0 if first else rows * widths[i], stride_b=self.w_stride[i],
                    stride_d=rows * width, bias=b, stride_bias=self.b_stride[i], epilogue="elu", mode=self.gemm_mode)
         last = self.layers - 1
+        if self.batched_heads:
+            w, b = self._layer("actor", last)
+            A, width = self.action_dim, widths[-1]
+            K.gemm(self.h_pair[-1], w, self.head_out, m=rows, n=A, k=width, batch=2, a_kcontig=True, b_kcontig=True,
+                   lda=width, ldb=width, ldd=A, stride_a=rows * width, stride_b=self.head_w_stride,
+                   stride_d=rows * A, bias=b, stride_bias=self.head_b_stride, mode=self.gemm_mode)
+            return
         for member, (prefix, out) in enumerate((("actor", self.mean), ("critic", self.value))):
             w, b = self._layer(prefix, last)
-            h = self.h_pair[-1][member] if hidden else self.b_obs
-            K.linear_forward(h, w, out, rows=rows, in_dim=widths[-1], out_dim=out.shape[1], bias=b, mode=self.gemm_mode,
-                             x_ld=None if hidden else self.obs_ld)
+            K.linear_forward(self.b_obs, w, out, rows=rows, in_dim=widths[-1], out_dim=out.shape[1], bias=b,
+                             mode=self.gemm_mode, x_ld=self.obs_ld)
 
     def _joint_backward(self, rows):
         """Weight, bias and input gradients of both MLPs: the output layers one network at a time,
@@ -216,15 +242,28 @@ class WarpPPO:
         widths = (self.observation_dim, *hidden)
         g = self.grads
         last = self.layers - 1
-        for member, (prefix, dout) in enumerate((("actor", self.dmean), ("critic", self.dvalue))):
-            w, _ = self._layer(prefix, last)
-            h = self.h_pair[last - 1][member] if last > 0 else self.b_obs
-            K.linear_backward_weight(dout, h, g[f"{prefix}.{last}.weight"], rows=rows, in_dim=widths[-1],
-                                     out_dim=dout.shape[1], mode=self.gemm_mode, workspace=self.workspace,
-                                     x_ld=None if last > 0 else self.obs_ld, bias_grad=g[f"{prefix}.{last}.bias"])
-            if last > 0:
-                K.linear_backward_input(dout, w, self.d_pair[last][member], rows=rows, in_dim=widths[-1],
-                                        out_dim=dout.shape[1], mode=self.gemm_mode, c=h, epilogue="elu_grad")
+        if self.batched_heads:
+            # both output layers as batch-2 products of A outputs (the value head zero-padded)
+            A, width = self.action_dim, widths[-1]
+            w, _ = self._layer("actor", last)
+            dw, db = g[f"actor.{last}.weight"], g[f"actor.{last}.bias"]
+            h = self.h_pair[last - 1]
+            splits = K.split_count(A, width, rows, 2, self.gemm_mode)
+            if splits > 1 and _native.load().rl_gemm_workspace(self.gemm_mode, A, width, rows, 2, splits) > \
+                    self.workspace.numel():
+                splits = 1
+            K.gemm(self.head_grad, h, dw, m=A, n=width, k=rows, batch=2, a_kcontig=False, b_kcontig=False, lda=A,
+                   ldb=width, ldd=width, stride_a=rows * A, stride_b=rows * width, stride_d=self.head_w_stride,
+                   mode=self.gemm_mode, splits=splits, workspace=self.workspace if splits > 1 else None, a_sums=db,
+                   stride_bias=self.head_b_stride)
+            K.gemm(self.head_grad, w, self.d_pair[last], m=rows, n=width, k=A, batch=2, a_kcontig=True,
+                   b_kcontig=False, lda=A, ldb=width, ldd=width, stride_a=rows * A, stride_b=self.head_w_stride,
+                   stride_d=rows * width, mode=self.gemm_mode, c=h, epilogue="elu_grad")
+        else:
+            for member, (prefix, dout) in enumerate((("actor", self.dmean), ("critic", self.dvalue))):
+                K.linear_backward_weight(dout, self.b_obs, g[f"{prefix}.{last}.weight"], rows=rows, in_dim=widths[-1],
+                                         out_dim=dout.shape[1], mode=self.gemm_mode, workspace=self.workspace,
+                                         x_ld=self.obs_ld, bias_grad=g[f"{prefix}.{last}.bias"])
         for i in reversed(range(last)):
             out_dim, in_dim = hidden[i], widths[i]
             d = self.d_pair[i + 1]
@@ -268,14 +307,14 @@ class WarpPPO:
         self._joint_forward(M)
         # loss, its gradients, the pre-step KL with the adaptive learning rate and the std-parameter
         # gradient: two launches (ppo.py:207-310)
-        _native.call("rl_ppo_minibatch_loss", self.mean.data_ptr(), A, self.value.data_ptr(),
+        _native.call("rl_ppo_minibatch_loss", self.mean.data_ptr(), A, self.value.data_ptr(), self.value_ld,
                      self.distribution_parameter.data_ptr(), self.b_actions.data_ptr(), self.b_log_probs.data_ptr(),
                      self.b_values.data_ptr(), self.b_advantages.data_ptr(), self.b_returns.data_ptr(),
                      self.b_means.data_ptr(), self.b_stds.data_ptr(), M, A, int(cfg.std_type == "scalar"),
                      float(cfg.std_range[0]), float(cfg.std_range[1]), float(cfg.clip_ratio),
                      float(cfg.value_coefficient), float(cfg.entropy_coefficient), float(cfg.value_loss_scale),
                      int(cfg.clip_value), float(cfg.desired_kl), int(cfg.schedule == "adaptive"),
-                     self.dmean.data_ptr(), self.dvalue.data_ptr(), self.grads["std"].data_ptr(),
+                     self.dmean.data_ptr(), self.dvalue.data_ptr(), self.value_ld, self.grads["std"].data_ptr(),
                      self.loss_partial.data_ptr(), self.totals.data_ptr(), self.kl.data_ptr(), self.lr.data_ptr(),
                      K.stream())
         self._joint_backward(M)
