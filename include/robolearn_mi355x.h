@@ -393,6 +393,11 @@ int rl_ppo_loss(const float* mean, long long ld_mean, const float* value, const 
 /* robolearn/warp/ppo.py:241-252 (fixed-order partials: ceil(n/4096) floats) */
 int rl_sum_squares(const float* x, long long n, float* partial, float* out, void* stream);
 int rl_clip_by_norm(float* g, long long n, const float* sum_squares, float max_norm, void* stream);
+/* rl_sum_squares followed by rl_clip_by_norm in two launches (the finishing sum
+ * is repeated by every clipping workgroup, in rl_sum_squares' order): g *=
+ * min(1, max_norm / (||g|| + 1e-6)), sum_squares receives ||g||^2; partial needs
+ * ceil(n / 4096) floats.  robolearn/warp/ppo.py:241-252, 676-693. */
+int rl_clip_grad_norm(float* g, long long n, float* partial, float* sum_squares, float max_norm, void* stream);
 /* ELU backward from the activation output (robolearn/warp/ppo.py:345). */
 int rl_elu_backward(float* dx, const float* y, long long n, void* stream);
 

@@ -127,6 +127,7 @@ SIGNATURES = {
                               + [P] * 5 + [P]),
     "rl_sum_squares": (c_int, [P, c_ll, P, P, P]),
     "rl_clip_by_norm": (c_int, [P, c_ll, P, c_float, P]),
+    "rl_clip_grad_norm": (c_int, [P, c_ll, P, P, c_float, P]),
     "rl_elu_backward": (c_int, [P, P, c_ll, P]),
 }
 

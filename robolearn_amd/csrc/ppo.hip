@@ -140,26 +140,58 @@ struct GatherArgs {
     float *b_obs, *b_actions, *b_log_probs, *b_values, *b_advantages, *b_returns, *b_means, *b_stds;
 };
 
-// One wave per sampled row (kGatherRows rows per workgroup): coalesced copies
-// of the row's observation, action, mean and std vectors, then its scalars.
+// kGatherRows sampled rows per wave, four waves per workgroup: the wave loads its
+// rows' indices at once, then issues every row's observation, action, mean and
+// std loads (coalesced within a row) before the first store, so one memory
+// round trip covers all of its rows; lanes 0 .. kGatherRows - 1 copy the rows'
+// scalars.
 constexpr int kGatherRows = 4;
+constexpr int kGatherWaves = 4;
 
-__global__ __launch_bounds__(kGatherRows* kWave) void gather_kernel(GatherArgs a) {
-    const long long r = static_cast<long long>(blockIdx.x) * kGatherRows + threadIdx.x / kWave;
-    if (r >= a.rows) return;  // wave-uniform
+__global__ __launch_bounds__(kGatherWaves* kWave) void gather_kernel(GatherArgs a) {
     const int lane = threadIdx.x % kWave;
-    const long long k = a.indices[a.offset + r];
-    for (int j = lane; j < a.obs_dim; j += kWave) a.b_obs[r * a.obs_ld + j] = a.obs[k * a.obs_dim + j];
-    for (int c = lane; c < a.action_dim; c += kWave) {
-        a.b_actions[r * a.action_dim + c] = a.actions[k * a.action_dim + c];
-        a.b_means[r * a.action_dim + c] = a.means[k * a.action_dim + c];
-        a.b_stds[r * a.action_dim + c] = a.stds[k * a.action_dim + c];
+    const long long r0 = (static_cast<long long>(blockIdx.x) * kGatherWaves + threadIdx.x / kWave) * kGatherRows;
+    if (r0 >= a.rows) return;  // wave-uniform
+    const long long mine = r0 + lane;
+    const long long kl = lane < kGatherRows && mine < a.rows ? a.indices[a.offset + mine] : 0;
+    long long k[kGatherRows];
+#pragma unroll
+    for (int i = 0; i < kGatherRows; ++i) k[i] = __shfl(kl, i);
+    constexpr int kObsPer = 4;  // observation values per lane and row (obs_dim <= 256)
+    float obs[kGatherRows][kObsPer], act[kGatherRows], mean[kGatherRows], std[kGatherRows];
+#pragma unroll
+    for (int i = 0; i < kGatherRows; ++i) {
+        const bool live = r0 + i < a.rows;
+#pragma unroll
+        for (int q = 0; q < kObsPer; ++q) {
+            const int j = lane + q * kWave;
+            obs[i][q] = live && j < a.obs_dim ? a.obs[k[i] * a.obs_dim + j] : 0.0f;
+        }
+        const bool c = live && lane < a.action_dim;
+        act[i] = c ? a.actions[k[i] * a.action_dim + lane] : 0.0f;
+        mean[i] = c ? a.means[k[i] * a.action_dim + lane] : 0.0f;
+        std[i] = c ? a.stds[k[i] * a.action_dim + lane] : 0.0f;
     }
-    if (lane == 0) {
-        a.b_log_probs[r] = a.log_probs[k];
-        a.b_values[r] = a.values[k];
-        a.b_advantages[r] = a.advantages[k];
-        a.b_returns[r] = a.returns[k];
+#pragma unroll
+    for (int i = 0; i < kGatherRows; ++i) {
+        const long long r = r0 + i;
+        if (r >= a.rows) break;
+#pragma unroll
+        for (int q = 0; q < kObsPer; ++q) {
+            const int j = lane + q * kWave;
+            if (j < a.obs_dim) a.b_obs[r * a.obs_ld + j] = obs[i][q];
+        }
+        if (lane < a.action_dim) {
+            a.b_actions[r * a.action_dim + lane] = act[i];
+            a.b_means[r * a.action_dim + lane] = mean[i];
+            a.b_stds[r * a.action_dim + lane] = std[i];
+        }
+    }
+    if (lane < kGatherRows && mine < a.rows) {
+        a.b_log_probs[mine] = a.log_probs[kl];
+        a.b_values[mine] = a.values[kl];
+        a.b_advantages[mine] = a.advantages[kl];
+        a.b_returns[mine] = a.returns[kl];
     }
 }
 
@@ -435,6 +467,22 @@ __global__ void clip_kernel(float* g, long long n, const float* sum_squares, flo
         g[i] *= coefficient;
 }
 
+// clip_kernel on sumsq_partials' output: every workgroup adds the partials in
+// sumsq_finish's order (so all see the same sum of squares, bitwise that of
+// sumsq_finish), workgroup 0 stores it, and each scales its grid-stride share.
+__global__ __launch_bounds__(kThreads) void clip_from_partials(float* g, long long n, const float* partial,
+                                                               long long blocks, float* sum_squares, float max_norm) {
+    __shared__ float s[kThreads];
+    float v = 0.0f;
+    for (long long i = threadIdx.x; i < blocks; i += kThreads) v += partial[i];
+    v = block_sum(v, s);
+    if (blockIdx.x == 0 && threadIdx.x == 0) sum_squares[0] = v;
+    const float coefficient = fminf(1.0f, max_norm / (sqrtf(v) + 1.0e-6f));
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<long long>(gridDim.x) * blockDim.x)
+        g[i] *= coefficient;
+}
+
 // dx *= elu'(y) = 1 if y > 0 else y + 1 (ELU with alpha 1, from its output).
 __global__ void elu_backward_kernel(float* dx, const float* y, long long n) {
     for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n;
@@ -645,12 +693,14 @@ RL_API int rl_ppo_gather(const int* indices, long long offset, long long rows, i
     return rl::guarded("rl_ppo_gather", [&] {
         rl::require(indices && rows > 0 && rows <= (1LL << 32) && obs_dim > 0 && action_dim > 0 && obs_ld >= obs_dim,
                     "PPO gather shapes are invalid.");
+        rl::require(obs_dim <= 4 * rl::kWave && action_dim <= rl::kWave,
+                    "PPO gather supports up to 256 observation and 64 action dimensions.");
 
         Q::GatherArgs a{indices, offset, rows, obs_dim, action_dim, obs_ld, obs, actions, log_probs, values, advantages,
                         returns, means, stds, b_obs, b_actions, b_log_probs, b_values, b_advantages, b_returns, b_means,
                         b_stds};
-        hipLaunchKernelGGL(Q::gather_kernel, dim3(rl::ceil_div(rows, Q::kGatherRows)), dim3(Q::kGatherRows * rl::kWave),
-                           0, rl::as_stream(stream), a);
+        hipLaunchKernelGGL(Q::gather_kernel, dim3(rl::ceil_div(rows, Q::kGatherRows * Q::kGatherWaves)),
+                           dim3(Q::kGatherWaves * rl::kWave), 0, rl::as_stream(stream), a);
         rl::check_launch("Launch PPO gather");
     });
 }
@@ -747,6 +797,21 @@ RL_API int rl_clip_by_norm(float* g, long long n, const float* sum_squares, floa
         rl::require(g && sum_squares && n > 0 && max_norm > 0, "Clipping needs buffers and a positive norm.");
         hipLaunchKernelGGL(Q::clip_kernel, dim3(static_cast<unsigned>(std::min<long long>((n + 255) / 256, 65536))),
                            dim3(256), 0, rl::as_stream(stream), g, n, sum_squares, max_norm);
+        rl::check_launch("Launch gradient clipping");
+    });
+}
+
+RL_API int rl_clip_grad_norm(float* g, long long n, float* partial, float* sum_squares, float max_norm,
+                             void* stream) noexcept {
+    return rl::guarded("rl_clip_grad_norm", [&] {
+        rl::require(g && partial && sum_squares && n > 0 && max_norm > 0,
+                    "Gradient-norm clipping needs buffers and a positive norm.");
+        const long long blocks = (n + 4095) / 4096;
+        const hipStream_t st = rl::as_stream(stream);
+        hipLaunchKernelGGL(Q::sumsq_partials, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st, g, n, partial);
+        rl::check_launch("Launch sum of squares");
+        hipLaunchKernelGGL(Q::clip_from_partials, dim3(static_cast<unsigned>(std::min<long long>((n + 255) / 256, 1024))),
+                           dim3(Q::kThreads), 0, st, g, n, partial, blocks, sum_squares, max_norm);
         rl::check_launch("Launch gradient clipping");
     });
 }

@@ -56,6 +56,8 @@ class WarpPPO:
             raise ValueError("std_range must contain positive increasing bounds.")
         if action_dim > 64:
             raise ValueError("The MI355X PPO loss kernels support at most 64 action dimensions.")
+        if observation_dim > 256:
+            raise ValueError("The MI355X PPO minibatch gather supports at most 256 observation dimensions.")
         if cfg.activation != "elu":
             raise NotImplementedError("The MI355X PPO path implements ELU activations (the G1 recipe).")
         if not torch.cuda.is_available():
@@ -320,10 +322,8 @@ class WarpPPO:
         self._joint_backward(M)
         for (start, end), norm in zip(self.group_ranges, self.group_norms):
             grad = self.flat.grad[start:end]
-            _native.call("rl_sum_squares", grad.data_ptr(), grad.numel(), self.norm_partial.data_ptr(),
-                         norm.data_ptr(), K.stream())
-            _native.call("rl_clip_by_norm", grad.data_ptr(), grad.numel(), norm.data_ptr(),
-                         float(cfg.max_grad_norm), K.stream())
+            _native.call("rl_clip_grad_norm", grad.data_ptr(), grad.numel(), self.norm_partial.data_ptr(),
+                         norm.data_ptr(), float(cfg.max_grad_norm), K.stream())
         _native.call("rl_fused_optimizer_step", self.optimizer_handle, 1, 0, 0, None, K.stream())
 
     def launch_update(self) -> None:

@@ -269,3 +269,23 @@ def test_sum_squares_and_clip_closed_form(gpu, n, scale):
     else:
         assert clipped.norm().item() == pytest.approx(norm / (norm + 1e-6), rel=1e-5)
         torch.testing.assert_close(clipped, grad.double() / (norm + 1e-6), rtol=1e-5, atol=1e-9)
+
+
+@pytest.mark.parametrize("n,scale", [(1000, 1e-3), (232_522 + 227_841, 0.7), (460_363, 25.0)])
+def test_fused_clip_equals_sum_squares_then_clip(gpu, n, scale):
+    """rl_clip_grad_norm (the update's two-launch form) leaves the same sum of squares and the same
+    clipped gradient, bit for bit, as rl_sum_squares followed by rl_clip_by_norm."""
+    print(f"case fused clip n={n} scale={scale}", flush=True)
+    g = torch.Generator().manual_seed(n + 1)
+    grad = torch.randn(n, generator=g)
+    grad = (grad * (scale / grad.double().norm().item())).float().to(gpu)
+    blocks = (n + 4095) // 4096
+    a, b = grad.clone(), grad.clone()
+    pa, pb = torch.empty(blocks, device=gpu), torch.empty(blocks, device=gpu)
+    sa, sb = torch.empty(1, device=gpu), torch.empty(1, device=gpu)
+    _native.call("rl_sum_squares", a.data_ptr(), n, pa.data_ptr(), sa.data_ptr(), K.stream())
+    _native.call("rl_clip_by_norm", a.data_ptr(), n, sa.data_ptr(), 1.0, K.stream())
+    _native.call("rl_clip_grad_norm", b.data_ptr(), n, pb.data_ptr(), sb.data_ptr(), 1.0, K.stream())
+    torch.cuda.synchronize()
+    assert torch.equal(sa, sb)
+    assert torch.equal(a, b)
