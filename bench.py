@@ -107,15 +107,18 @@ def elementwise_bytes(w: dict, act_bytes: int = 4) -> float:
     return critic_total + actor_bytes + optimizer + 3 * 2 * B * K * 4 * 4
 
 
+# the sources the dominant kernel (gemm_wide_kernel) is compiled from
+DOMINANT_SOURCES = ("common.hpp", "gemm.hpp", "gemm_bf16_big.hip")
+
+
 def source_fingerprint() -> str:
-    """First 16 hex digits of the SHA-256 of the HIP sources (names and bytes, sorted by name)."""
+    """First 16 hex digits of the SHA-256 of the dominant kernel's sources (names and bytes, in order)."""
     import hashlib
 
     digest = hashlib.sha256()
-    for path in sorted((ROOT / "robolearn_amd" / "csrc").glob("*")):
-        if path.suffix in (".hip", ".hpp"):
-            digest.update(path.name.encode())
-            digest.update(path.read_bytes())
+    for name in DOMINANT_SOURCES:
+        digest.update(name.encode())
+        digest.update((ROOT / "robolearn_amd" / "csrc" / name).read_bytes())
     return digest.hexdigest()[:16]
 
 
