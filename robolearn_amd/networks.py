@@ -384,9 +384,12 @@ class Trunk:
                           None if g is None else g[pre + ".norm1.bias"], rows=rows, channels=4 * h, ensemble=E,
                           training=training, relu=True, b=p[pre + ".norm1.bias"], dx_bf16=self.d_r1_h)
             d_r1 = self.op(self.d_r1, self.d_r1_h)
+            # the bf16 copy of d_stream is read only after the first block (by the embedder's
+            # products); the blocks above read the fp32 stream gradient
             K.linear_backward_input(d_r1, w[f"{pre}.w1{self.linear}"], self.d_stream, rows=rows, in_dim=h,
                                     out_dim=4 * h, ensemble=E, mode=mode, c=self.d_stream, beta=1.0,
-                                    d_bf16=self.d_stream_h, wt=wt.get(f"{pre}.w1{self.linear}"))
+                                    d_bf16=self.d_stream_h if i == 0 else None,
+                                    wt=wt.get(f"{pre}.w1{self.linear}"))
             if g is not None:
                 K.linear_backward_weight(d_r1, self.op(self.stream[i], self.stream_h[i]), g[f"{pre}.w1{self.linear}"],
                                          rows=rows, in_dim=h, out_dim=4 * h, ensemble=E, mode=mode,
