@@ -711,8 +711,18 @@ __device__ __forceinline__ void merge8(float& count, float (&mean)[8], float (&m
 // the epilogue, so the waits for them may leave S = 16 SPP stores in flight
 // (vector-memory counts complete in issue order); the conditional moment
 // stores and the bias / C loads only make those waits stricter.
-template <int SPP, bool BIAS, bool MN>
+// OUT selects the epilogue: kGeneral handles every Params combination; the plain
+// kinds (identity epilogue, no bias, no beta term) are compiled without the
+// branches and register moves of the general one, which at K = 1024 cost about a
+// fifth of the launch: kBf16 (direct, bf16 D only), kBf16Moments (the same plus
+// the BatchNorm chunk moments of the stored values) and kFp32 (fp32 D only:
+// split-K partials or a direct output without a bf16 copy or moments).
+enum Out { kGeneral = 0, kBf16 = 1, kBf16Moments = 2, kFp32 = 3 };
+
+template <int SPP, bool BIAS, bool MN, int OUT>
 __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int tiles_m, int tiles_n, int total) {
+    static_assert(OUT == kGeneral || !BIAS, "the plain epilogues add no bias");
+    static_assert(OUT == kGeneral || SPP == (OUT == kFp32 ? 2 : 1), "stores per pass of the plain epilogues");
     constexpr int S = MI * (32 / RPP) * SPP;
     static_assert(SPP >= 1 && 2 * IPW + S < 64, "vmcnt is a 6-bit count");
     // the two stages are separate objects: the compiler can then tell a fragment read of one
@@ -729,7 +739,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
     const int wm = wave / (BN / WTN);
     const int wn = wave % (BN / WTN);
     const int sw = slot_of(lane % 32);
-    const bool direct = p.splits == 1;
+    const bool direct = OUT == kBf16 || OUT == kBf16Moments || p.splits == 1;
 
     const auto fetch_tile = [&](const Tile& t, int kt, unsigned short* stage) {
         const unsigned short* A = static_cast<const unsigned short*>(p.a) + t.batch * p.stride_a;
@@ -870,15 +880,20 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
         fetch_tile(next, 1, stage1);
 
         // ---- epilogue
-        float* D = (direct && !p.d) ? nullptr
-                                    : p.d + (direct ? tile.batch * p.stride_d
-                                                    : (static_cast<long long>(tile.split) * p.batch + tile.batch) *
-                                                          static_cast<long long>(p.m) * p.n);
+        constexpr bool general = OUT == kGeneral;
+        constexpr bool bf16_only = OUT == kBf16 || OUT == kBf16Moments;
+        float* D = bf16_only ? nullptr
+                   : (general && direct && !p.d) ? nullptr
+                   : p.d + (direct ? tile.batch * p.stride_d
+                                   : (static_cast<long long>(tile.split) * p.batch + tile.batch) *
+                                         static_cast<long long>(p.m) * p.n);
         const long long ldd = direct ? p.ldd : p.n;
-        const float* C = (direct && p.beta != 0.0f) ? p.c + tile.batch * p.stride_d : nullptr;
-        unsigned short* Dh = (direct && p.d_bf16) ? p.d_bf16 + tile.batch * p.stride_d : nullptr;
-        const bool moments = direct && p.moments != nullptr;
-        const bool round_moments = moments && !D;  // a bf16-only output takes the moments of the stored values
+        const float* C = (general && direct && p.beta != 0.0f) ? p.c + tile.batch * p.stride_d : nullptr;
+        unsigned short* Dh = OUT == kFp32 ? nullptr
+                             : (bf16_only || (direct && p.d_bf16)) ? p.d_bf16 + tile.batch * p.stride_d : nullptr;
+        const bool moments = OUT == kBf16Moments || (general && direct && p.moments != nullptr);
+        // a bf16-only output takes the moments of the stored values
+        const bool round_moments = OUT == kBf16Moments || (general && moments && !D);
         float shift[8], s1[8], s2[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) shift[e] = s1[e] = s2[e] = 0.0f;
@@ -899,7 +914,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                 const f32x4 x1 = *reinterpret_cast<const f32x4*>(stagef + (lane / LPR) * EP + (lane % LPR) * 8 + 4);
                 float val[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
                 const long long offset = static_cast<long long>(tile.m0 + wm * WTM + i * 32 + r) * ldd + col;
-                if (direct) {
+                if (general && direct) {
                     float4 lo = activate4(make_float4(val[0] + bias8[0], val[1] + bias8[1], val[2] + bias8[2],
                                                       val[3] + bias8[3]), p.epilogue);
                     float4 hi = activate4(make_float4(val[4] + bias8[4], val[5] + bias8[5], val[6] + bias8[6],
@@ -913,16 +928,16 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                         val[3] += p.beta * c0.w, val[4] += p.beta * c1.x, val[5] += p.beta * c1.y;
                         val[6] += p.beta * c1.z, val[7] += p.beta * c1.w;
                     }
-                    if (Dh) {
-                        const u32x4 packed = {f32x2_to_bf16x2(val[0], val[1]), f32x2_to_bf16x2(val[2], val[3]),
-                                              f32x2_to_bf16x2(val[4], val[5]), f32x2_to_bf16x2(val[6], val[7])};
-                        __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(Dh + offset));
-                        if (round_moments) {
+                }
+                if (bf16_only || (direct && Dh)) {
+                    const u32x4 packed = {f32x2_to_bf16x2(val[0], val[1]), f32x2_to_bf16x2(val[2], val[3]),
+                                          f32x2_to_bf16x2(val[4], val[5]), f32x2_to_bf16x2(val[6], val[7])};
+                    __builtin_nontemporal_store(packed, reinterpret_cast<u32x4*>(Dh + offset));
+                    if (round_moments) {
 #pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                val[2 * e] = __uint_as_float(packed[e] << 16);
-                                val[2 * e + 1] = __uint_as_float(packed[e] & 0xffff0000u);
-                            }
+                        for (int e = 0; e < 4; ++e) {
+                            val[2 * e] = __uint_as_float(packed[e] << 16);
+                            val[2 * e + 1] = __uint_as_float(packed[e] & 0xffff0000u);
                         }
                     }
                 }
@@ -1054,21 +1069,29 @@ void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream) {
         require(spp > 0, "The GEMM has no output.");
         const dim3 wblock(big::wide::NW * kWave);
         const bool bias = direct && p.bias;
-#define RL_WIDE(SPP, BIAS)                                                                                           \
+        // the plain epilogues: identity activation, no bias, no beta term (split-K partials have none)
+        const bool plain = !direct || (!p.bias && p.beta == 0.0f && p.epilogue == 0);
+        int out = big::wide::kGeneral;
+        if (plain && direct && !p.d && p.d_bf16) out = p.moments ? big::wide::kBf16Moments : big::wide::kBf16;
+        else if (plain && (!direct || (p.d && !p.d_bf16 && !p.moments))) out = big::wide::kFp32;
+#define RL_WIDE(SPP, BIAS, OUT)                                                                                      \
     do {                                                                                                            \
         if (ak)                                                                                                     \
-            hipLaunchKernelGGL((big::wide::gemm_wide_kernel<SPP, BIAS, false>), grid, wblock, 0, stream, p, tiles_m, \
-                               tiles_n, total);                                                                     \
+            hipLaunchKernelGGL((big::wide::gemm_wide_kernel<SPP, BIAS, false, OUT>), grid, wblock, 0, stream, p,    \
+                               tiles_m, tiles_n, total);                                                            \
         else                                                                                                        \
-            hipLaunchKernelGGL((big::wide::gemm_wide_kernel<SPP, BIAS, true>), grid, wblock, 0, stream, p, tiles_m,  \
-                               tiles_n, total);                                                                     \
+            hipLaunchKernelGGL((big::wide::gemm_wide_kernel<SPP, BIAS, true, OUT>), grid, wblock, 0, stream, p,     \
+                               tiles_m, tiles_n, total);                                                            \
     } while (0)
-        if (spp == 1 && bias) RL_WIDE(1, true);
-        else if (spp == 1) RL_WIDE(1, false);
-        else if (spp == 2 && bias) RL_WIDE(2, true);
-        else if (spp == 2) RL_WIDE(2, false);
-        else if (bias) RL_WIDE(3, true);
-        else RL_WIDE(3, false);
+        if (out == big::wide::kBf16) RL_WIDE(1, false, big::wide::kBf16);
+        else if (out == big::wide::kBf16Moments) RL_WIDE(1, false, big::wide::kBf16Moments);
+        else if (out == big::wide::kFp32) RL_WIDE(2, false, big::wide::kFp32);
+        else if (spp == 1 && bias) RL_WIDE(1, true, big::wide::kGeneral);
+        else if (spp == 1) RL_WIDE(1, false, big::wide::kGeneral);
+        else if (spp == 2 && bias) RL_WIDE(2, true, big::wide::kGeneral);
+        else if (spp == 2) RL_WIDE(2, false, big::wide::kGeneral);
+        else if (bias) RL_WIDE(3, true, big::wide::kGeneral);
+        else RL_WIDE(3, false, big::wide::kGeneral);
 #undef RL_WIDE
     }
     else if (dma) hipLaunchKernelGGL(big::gemm_dma_kernel, grid, block, 0, stream, p, tiles_m, tiles_n, total);
