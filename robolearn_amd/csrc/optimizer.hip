@@ -163,6 +163,13 @@ __device__ __forceinline__ float adam_element(const StepArgs& a, const Scalars& 
     return p - s.a * ((m1 * s.b) / (sqrtf(m2 * s.c) + a.eps));
 }
 
+// Four bf16 copies as one 8-byte store (vec4 spans start at multiples of 4 elements).
+__device__ __forceinline__ void store_bf16x4(unsigned short* dst, float4 v) {
+    const unsigned lo = static_cast<unsigned>(f32_to_bf16_bits(v.x)) | (static_cast<unsigned>(f32_to_bf16_bits(v.y)) << 16);
+    const unsigned hi = static_cast<unsigned>(f32_to_bf16_bits(v.z)) | (static_cast<unsigned>(f32_to_bf16_bits(v.w)) << 16);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+}
+
 // Pass 1 over one contiguous span: optional Adam, returns the squared norm of
 // the resulting parameters.
 __device__ float update_span(const StepArgs& a, const Scalars& s, const Part& part, long long offset, long long length,
@@ -242,21 +249,9 @@ __device__ void finish_span(const StepArgs& a, const Part& part, long long offse
                 t.z = t.z + a.tau * (v.z - t.z);
                 t.w = t.w + a.tau * (v.w - t.w);
                 reinterpret_cast<float4*>(part.target + offset)[i] = t;
-                if (part.target_shadow) {
-                    unsigned short* ts = part.target_shadow + offset + 4 * i;
-                    ts[0] = f32_to_bf16_bits(t.x);
-                    ts[1] = f32_to_bf16_bits(t.y);
-                    ts[2] = f32_to_bf16_bits(t.z);
-                    ts[3] = f32_to_bf16_bits(t.w);
-                }
+                if (part.target_shadow) store_bf16x4(part.target_shadow + offset + 4 * i, t);
             }
-            if (part.shadow) {
-                unsigned short* sh = part.shadow + offset + 4 * i;
-                sh[0] = f32_to_bf16_bits(v.x);
-                sh[1] = f32_to_bf16_bits(v.y);
-                sh[2] = f32_to_bf16_bits(v.z);
-                sh[3] = f32_to_bf16_bits(v.w);
-            }
+            if (part.shadow) store_bf16x4(part.shadow + offset + 4 * i, v);
         }
     } else {
         for (long long i = lane; i < length; i += kWave) {
@@ -270,6 +265,67 @@ __device__ void finish_span(const StepArgs& a, const Part& part, long long offse
     }
 }
 
+// A unit row of up to 4 * kWave * R elements keeps its updated values in registers
+// between the Adam pass and the projection pass: each parameter is read and written
+// once.  The arithmetic is that of update_span and finish_span (mode 0).  R is 16
+// (rows up to 4096: the 4h -> h block weights) when the plan has such rows, else 4
+// (rows up to 1024), since the buffer's registers cost occupancy for short rows.
+template <int R>
+__device__ void unit_row_in_registers(const StepArgs& a, const Scalars& s, const Part& part, long long offset,
+                                      long long cols) {
+    constexpr int kRegRow = R;
+    const int lane = threadIdx.x % kWave;
+    const long long n4 = cols / 4;
+    float4* p = reinterpret_cast<float4*>(part.p + offset);
+    float4 v[kRegRow];
+    float sumsq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kRegRow; ++j) {
+        const long long i = lane + static_cast<long long>(j) * kWave;
+        if (i < n4) {
+            float4 pv = p[i];
+            if (a.do_adam) {
+                const float4 gv = reinterpret_cast<const float4*>(part.g + offset)[i];
+                float4 m1v = reinterpret_cast<float4*>(part.m1 + offset)[i];
+                float4 m2v = reinterpret_cast<float4*>(part.m2 + offset)[i];
+                pv.x = adam_element(a, s, pv.x, gv.x, m1v.x, m2v.x);
+                pv.y = adam_element(a, s, pv.y, gv.y, m1v.y, m2v.y);
+                pv.z = adam_element(a, s, pv.z, gv.z, m1v.z, m2v.z);
+                pv.w = adam_element(a, s, pv.w, gv.w, m1v.w, m2v.w);
+                reinterpret_cast<float4*>(part.m1 + offset)[i] = m1v;
+                reinterpret_cast<float4*>(part.m2 + offset)[i] = m2v;
+            }
+            v[j] = pv;
+            sumsq += pv.x * pv.x + pv.y * pv.y + pv.z * pv.z + pv.w * pv.w;
+        }
+    }
+    sumsq = wave_sum(sumsq);
+    const float factor = fmaxf(sqrtf(sumsq), 1.0e-8f);
+#pragma unroll
+    for (int j = 0; j < kRegRow; ++j) {
+        const long long i = lane + static_cast<long long>(j) * kWave;
+        if (i < n4) {
+            float4 x = v[j];
+            x.x = x.x / factor;
+            x.y = x.y / factor;
+            x.z = x.z / factor;
+            x.w = x.w / factor;
+            p[i] = x;
+            if (part.shadow) store_bf16x4(part.shadow + offset + 4 * i, x);
+            if (a.do_ema && part.target) {
+                float4 t = reinterpret_cast<float4*>(part.target + offset)[i];
+                t.x = t.x + a.tau * (x.x - t.x);
+                t.y = t.y + a.tau * (x.y - t.y);
+                t.z = t.z + a.tau * (x.z - t.z);
+                t.w = t.w + a.tau * (x.w - t.w);
+                reinterpret_cast<float4*>(part.target + offset)[i] = t;
+                if (part.target_shadow) store_bf16x4(part.target_shadow + offset + 4 * i, t);
+            }
+        }
+    }
+}
+
+template <int R>
 __global__ __launch_bounds__(kThreads) void step_kernel(StepArgs a) {
     if (a.skip && a.skip[0]) return;
     const int item = static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x) / kWave;
@@ -286,6 +342,10 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepArgs a) {
         return;
     }
     const long long offset = static_cast<long long>(w.unit) * t.cols;
+    if (t.kind == kUnitRow && vec4 && a.do_project && t.cols <= 4LL * kWave * R) {
+        unit_row_in_registers<R>(a, s, t.part[0], offset, t.cols);
+        return;
+    }
     float sumsq = update_span(a, s, t.part[0], offset, t.cols, vec4);
     if (t.kind == kBatchNormPair) sumsq += update_span(a, s, t.part[1], offset, t.cols, vec4);
     sumsq = wave_sum(sumsq);
@@ -387,6 +447,7 @@ struct Plan {
     int has_adam = 0;
     int has_projection = 0;
     int has_ema = 0;
+    int long_rows = 0;  // a vector unit row longer than 1024 elements: step_kernel<16>
     // dynamic loss scaling (reference-compatible rl_adam_set_scaler); null when unused
     float* loss_scale = nullptr;
     int* growth_tracker = nullptr;
@@ -406,7 +467,10 @@ struct Plan {
 
 bool all_aligned16(const Part& part) {
     auto ok = [](const void* q) { return q == nullptr || aligned(q, 16); };
-    return ok(part.p) && ok(part.g) && ok(part.m1) && ok(part.m2) && ok(part.target);
+    // bf16 copies take 8-byte stores of four elements
+    auto ok8 = [](const void* q) { return q == nullptr || aligned(q, 8); };
+    return ok(part.p) && ok(part.g) && ok(part.m1) && ok(part.m2) && ok(part.target) && ok8(part.shadow) &&
+           ok8(part.target_shadow);
 }
 
 std::unique_ptr<Plan> build(std::vector<Tensor> tensors) {
@@ -442,6 +506,8 @@ std::unique_ptr<Plan> build(std::vector<Tensor> tensors) {
               "Copy optimizer work table");
     check_hip(hipMemset(plan->scalars, 0, sizeof(Scalars)), "Clear optimizer scalars");
     plan->work_count = static_cast<int>(work.size());
+    for (const Tensor& t : tensors)
+        if (t.kind == kUnitRow && t.vec4 && t.cols > 1024) plan->long_rows = 1;
     return plan;
 }
 
@@ -478,7 +544,10 @@ void step(Plan* plan, int do_adam, int do_project, int do_ema, const int* skip, 
     a.do_project = do_project;
     a.do_ema = do_ema;
     a.skip = skip;
-    hipLaunchKernelGGL(step_kernel, dim3(ceil_div(plan->work_count, kWaves)), dim3(kThreads), 0, stream, a);
+    if (plan->long_rows)
+        hipLaunchKernelGGL(step_kernel<16>, dim3(ceil_div(plan->work_count, kWaves)), dim3(kThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL(step_kernel<4>, dim3(ceil_div(plan->work_count, kWaves)), dim3(kThreads), 0, stream, a);
     check_launch("Launch fused optimizer step");
 }
 

@@ -36,6 +36,11 @@ def _check(tensor: torch.Tensor, numel: int, name: str, dtype=torch.float32):
         raise ValueError(f"{name} holds {tensor.numel()} elements, {numel} are needed.")
 
 
+def _check_optional(tensor, numel: int, name: str, dtype=torch.float32):
+    if tensor is not None:
+        _check(tensor, numel, name, dtype)
+
+
 def _is_bf16(tensor: torch.Tensor) -> int:
     return 1 if tensor.dtype == torch.bfloat16 else 0
 
@@ -175,6 +180,11 @@ def bn_forward(x, w, b, running_mean, running_var, mean, var, partial, y, *, row
     moments_ready: partial already holds x's chunk moments (written by the producing GEMM)."""
     if x_stride is None:
         x_stride = rows * channels
+    # the kernels write whole rows of the dtype each output pointer is declared with
+    total = ensemble * rows * channels
+    _check_optional(y, total, "BatchNorm output")
+    _check_optional(y_bf16, total, "BatchNorm bf16 output", torch.bfloat16)
+    _check_optional(residual, total, "BatchNorm residual")
     _native.call("rl_bn_forward_ex", ensemble, ptr(x), _is_bf16(x), x_stride, ptr(w), ptr(b), ptr(running_mean),
                  ptr(running_var), ptr(mean), ptr(var), ptr(partial), ptr(residual), ptr(y), ptr(y_bf16), rows,
                  channels, eps, momentum, int(training), int(relu), int(update_running), int(moments_ready), stream())
@@ -187,6 +197,10 @@ def bn_backward(x, dy, y, w, mean, var, partial, sums, dx, dw, db, *, rows, chan
     dy may be float32 or bfloat16; dx_bf16 may be dy itself (updated in place)."""
     if x_stride is None:
         x_stride = rows * channels
+    total = ensemble * rows * channels
+    _check_optional(dx, total, "BatchNorm input gradient")
+    _check_optional(dx_bf16, total, "BatchNorm bf16 input gradient", torch.bfloat16)
+    _check_optional(y, total, "BatchNorm forward output")
     _native.call("rl_bn_backward_ex", ensemble, ptr(x), _is_bf16(x), x_stride, ptr(dy), _is_bf16(dy), ptr(y), ptr(w),
                  ptr(b), ptr(mean), ptr(var), ptr(partial), ptr(sums), ptr(dx), ptr(dw), ptr(db), ptr(dx_bf16), rows,
                  channels, eps, int(training), int(relu), int(accumulate_dx), int(accumulate_params), stream())
