@@ -127,14 +127,17 @@ def transpose16(src, dst, *, batch, rows, cols):
 def split_count(m, n, k, batch, mode):
     """K splits for a weight-gradient product (small output, K = rows).
 
-    bf16: at least two 256x128-tile workgroups per CU, each split >= 512 of K.
+    bf16: at least two 256x128-tile workgroups per CU, each split >= 512 of K; >= 256 of K
+    when the output does not tile by 256 (a narrow head or embedder: those products run on
+    the 256x128 kernel, whose workgroups are short enough that more of them pays).
     fp32: the MFMA-issue-bound fp32 kernel runs 64x64 tiles for such products;
     at least 1024 workgroups (four per CU), each split >= 64 of K."""
     splits = 1
     if mode == BF16:
         tiles = ((m + 255) // 256) * ((n + 127) // 128) * batch
         ktiles = (k + 31) // 32
-        while tiles * splits < 512 and splits * 2 <= max(1, ktiles // 16) and splits < 64:
+        min_ktiles = 16 if m % 256 == 0 and n % 256 == 0 else 8
+        while tiles * splits < 512 and splits * 2 <= max(1, ktiles // min_ktiles) and splits < 64:
             splits *= 2
         return splits
     tiles = ((m + 63) // 64) * ((n + 63) // 64) * batch
