@@ -403,6 +403,14 @@ __device__ __forceinline__ void group_load(const float* row, const float* bias, 
     }
 }
 
+// e^x for x <= 0 (softmax terms) as 2^(x log2 e) on the hardware base-2
+// exponential: relative error about |x| 2^-24 from rounding the product (below
+// 2e-6 for the logit spreads of a categorical head), x = -inf gives 0, and no
+// range reduction or overflow handling is needed.
+__device__ __forceinline__ float exp_nonpositive(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
 // log_softmax of a row, its probabilities (one exponential per bin: p = e / s
 // with e = exp(x - max)) and the expectation over the support z.
 template <int PL>
@@ -415,12 +423,14 @@ __device__ __forceinline__ void group_log_softmax(const float* x, const float* z
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < PL; ++i) {
-        p[i] = l + kGroup * i < bins ? expf(x[i] - m) : 0.0f;
+        p[i] = l + kGroup * i < bins ? exp_nonpositive(x[i] - m) : 0.0f;
         s += p[i];
     }
     s = group_sum(s);
-    const float lse = logf(s);
-    const float inv = 1.0f / s;
+    // s >= 1 (the maximum's own term): hardware log2 and reciprocal, each within
+    // about 1 ulp, are well inside the head's fp32 tolerances
+    const float lse = __builtin_amdgcn_logf(s) * 0.693147180559945309f;
+    const float inv = __builtin_amdgcn_rcpf(s);
     float e = 0.0f;
 #pragma unroll
     for (int i = 0; i < PL; ++i) {
@@ -437,19 +447,14 @@ __device__ __forceinline__ void wave_lds_fence() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Per-row LDS of the projection.  probs is read before the first fence and
-// lower_start written after it; the masses serve the non-monotone scan and the
-// run pieces the monotone path, never both in one wave, so each pair shares
-// storage.
+// Per-row LDS of the projection (1544 bytes, so LDS leaves room for four waves
+// per SIMD).  Source bin j's probability is read only by the lane that owns j,
+// before that lane writes j's lower mass; the masses serve the non-monotone scan
+// and the run pieces the monotone path, never both in one wave; so each group
+// shares storage.  Bin indices and run starts are at most 128: one byte each.
 struct GroupRowLds {
     union {
-        float probs[kGroupBins + 1];   // selected critic's probabilities, by source bin
-        int lower_start[kGroupBins + 1];  // first source whose lower bin is >= k (monotone rows)
-    };
-    int upper_start[kGroupBins + 1];   // first source whose upper bin is >= k
-    int lower[kGroupBins];             // per-source target bins
-    int upper[kGroupBins];
-    union {
+        float probs[kGroupBins];       // selected critic's probabilities, by source bin
         float lower_mass[kGroupBins];  // per-source masses (non-monotone scan)
         float lower_piece[kGroupBins]; // lower-bin mass of the run piece starting at this source
     };
@@ -457,7 +462,12 @@ struct GroupRowLds {
         float upper_mass[kGroupBins];
         float upper_piece[kGroupBins];
     };
+    unsigned char lower_start[kGroupBins + 4];  // first source whose lower bin is >= k (monotone rows)
+    unsigned char upper_start[kGroupBins + 4];  // first source whose upper bin is >= k
+    unsigned char lower[kGroupBins];            // per-source target bins
+    unsigned char upper[kGroupBins];
 };
+static_assert(sizeof(GroupRowLds) == 1544, "per-row LDS of the projection");
 
 // Lower/upper target bins and masses of source bin j (updates.py:60-79).
 struct TwoHot {
@@ -484,6 +494,7 @@ __global__ __launch_bounds__(kWave) void td_cross_entropy_rows(TargetArgs a, con
                                                                   unsigned short* dlogits_bf16, float* loss_rows,
                                                                   float* entropy_rows, float* q_next) {
     __shared__ GroupRowLds lds[kGroupRows];
+    __shared__ float support_lds[kGroupBins];  // the support by bin, for the block-layout projection
     const int group = static_cast<int>(threadIdx.x) / kGroup;
     const int l = static_cast<int>(threadIdx.x) % kGroup;
     const long long row_raw = static_cast<long long>(blockIdx.x) * kGroupRows + group;
@@ -503,6 +514,11 @@ __global__ __launch_bounds__(kWave) void td_cross_entropy_rows(TargetArgs a, con
         z[i] = j < bins ? a.support[min(j, bins - 1)] : 0.0f;
     }
     const RowInputs in = load_row_inputs(a, row);
+    if (group == 0) {
+#pragma unroll
+        for (int i = 0; i < PL; ++i)
+            if (l + kGroup * i < bins) support_lds[l + kGroup * i] = z[i];
+    }
 
     float lp0[PL], lp1[PL], p0[PL], p1[PL];
     float q0, q1;
@@ -526,6 +542,8 @@ __global__ __launch_bounds__(kWave) void td_cross_entropy_rows(TargetArgs a, con
     }
     wave_lds_fence();
     const int c = (bins + kGroup - 1) / kGroup;
+    // r / c for 0 <= r <= 128 and c <= 8 as (r * c_magic) >> 16, exact on that range
+    const int c_magic = (65536 + c - 1) / c;
     const int jb = min(bins, l * c);
     const int je = min(bins, jb + c);
     TwoHot h[PL];
@@ -533,7 +551,7 @@ __global__ __launch_bounds__(kWave) void td_cross_entropy_rows(TargetArgs a, con
     for (int i = 0; i < PL; ++i) {
         const int j = jb + i;
         if (j < je) {
-            h[i] = two_hot(a, in, a.support[j], sh.probs[j], bins);
+            h[i] = two_hot(a, in, support_lds[j], sh.probs[j], bins);
             sh.lower[j] = h[i].lower;
             sh.upper[j] = h[i].upper;
             sh.lower_mass[j] = h[i].lower_mass;
@@ -600,12 +618,12 @@ __global__ __launch_bounds__(kWave) void td_cross_entropy_rows(TargetArgs a, con
             float sum = 0.0f;
             if (k < bins) {
                 for (int pass = 0; pass < 2; ++pass) {
-                    const int* starts = pass == 0 ? sh.lower_start : sh.upper_start;
+                    const unsigned char* starts = pass == 0 ? sh.lower_start : sh.upper_start;
                     const float* pieces = pass == 0 ? sh.lower_piece : sh.upper_piece;
                     const int r0 = max(starts[k], 0), r1 = min(starts[k + 1], bins);
                     if (r0 < r1) {
                         sum += pieces[r0];
-                        for (int j = (r0 / c + 1) * c; j < r1; j += c) sum += pieces[j];
+                        for (int j = (((r0 * c_magic) >> 16) + 1) * c; j < r1; j += c) sum += pieces[j];
                     }
                 }
             }
@@ -839,6 +857,7 @@ RL_API int rl_categorical_td_cross_entropy(const float* target_logits, const flo
                        dlogits, dh, loss_rows, entropy_rows, q_next)
             if (bins <= 2 * rl::cat::kGroup) RL_TD_ROWS(2);
             else if (bins <= 4 * rl::cat::kGroup) RL_TD_ROWS(4);
+            else if (bins <= 7 * rl::cat::kGroup) RL_TD_ROWS(7);  // 101 bins: 112 lane slots instead of 128
             else RL_TD_ROWS(8);
 #undef RL_TD_ROWS
         } else {
