@@ -196,7 +196,7 @@ def test_rmsnorm_and_bias_grad(gpu, ensemble, rows, channels):
     torch.testing.assert_close(db.cpu().double(), dy.double().sum(1), rtol=1e-5, atol=1e-4)
 
 
-@pytest.mark.parametrize("bins", [21, 101, 160, 300])
+@pytest.mark.parametrize("bins", [21, 51, 80, 101, 112, 128, 160, 300])
 def test_td_cross_entropy_matches_oracle_projection(gpu, bins):
     """Fused min-Q target, two-hot projection, CE and d-logits against the oracle's
     categorical_td_target (robolearn/flashsac/updates.py:19-80, 254-257).  Rows mix
