@@ -693,6 +693,9 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-extras", action="store_true",
                         help="headline only: skip the other workloads, PPO (c3) and the kernel sweep (c4)")
+    parser.add_argument("--sweep-only", action="store_true",
+                        help="run only the configs[4] kernel sweep and print its lines as one JSON object "
+                             "(for rocprofv3 counter passes over the sweep kernels)")
     parser.add_argument("--calibration-copy-mb", type=int, default=0,
                         help="after timing the dominant kernel, one plain device copy of this size "
                              "(scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -705,6 +708,9 @@ def main() -> int:
     import torch
 
     torch.cuda.set_device(0)
+    if args.sweep_only:
+        print(json.dumps({"kernel_sweep": kernel_sweep()}))
+        return 0
     w = WORKLOADS[args.workload]
     head = run_flashsac(args.workload, args.steps, args.warmup, dominant=True,
                         calibration_copy_mb=args.calibration_copy_mb)
