@@ -210,34 +210,119 @@ def safe_tanh_log_det_jacobian(x: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
+# Parity-test hooks (the comparison needs them; the reference has no counterpart)
+# ---------------------------------------------------------------------------
+def round_bf16(x: torch.Tensor) -> torch.Tensor:
+    """Round to the nearest bfloat16 (ties to even), returned in x's dtype."""
+    return x.to(torch.bfloat16).to(x.dtype)
+
+
+class _Round(torch.autograd.Function):
+    """Identity or bf16 rounding in the forward and, independently, in the backward."""
+
+    @staticmethod
+    def forward(ctx, x, forward_round, backward_round):
+        ctx.backward_round = backward_round
+        return round_bf16(x) if forward_round else x.clone()
+
+    @staticmethod
+    def backward(ctx, grad):
+        return (round_bf16(grad) if ctx.backward_round else grad), None, None
+
+
+class Emulation:
+    """How one device update rounds, for parity tests of it.
+
+    relu_masks: one 0/1 tensor per ReLU, in execution order (per block norm1 then norm2, per
+        forward in update order: actor, eval critic, next-action actor, target critic, online
+        critic), shaped like that ReLU's input.  Each replaces the ReLU's pass/block decision with
+        the device's, so inputs within rounding of zero (passed on one side, blocked on the other)
+        do not enter the comparison; the forward value x * mask differs from relu(x) only on such
+        elements, by less than their rounding.
+    bf16: the bf16-operand mode: every dense product reads its operands rounded to bf16 (RNE) and
+        the gradient reaching its output rounded to bf16 (the device feeds both backward products
+        from a bf16 copy of it; bias gradients read the unrounded one).
+    bf16_activations: with bf16, the block products' outputs (the BatchNorm inputs) are stored in
+        bf16, and so is the gradient reaching the second block product's input (the ReLU-BatchNorm
+        gradient).
+    after_actor_phase: optional callable(state), run after the actor and temperature steps, before
+        the critic phase (a test loads the device's post-step actor, log-temperature and actor
+        BatchNorm statistics there, so the critic phase is compared from the same start).
+    """
+
+    def __init__(self, relu_masks=None, bf16: bool = False, bf16_activations: bool = False,
+                 after_actor_phase=None, record_masks: list | None = None,
+                 record_products: list | None = None):
+        self.relu_masks = list(relu_masks) if relu_masks is not None else None
+        self.bf16 = bf16
+        self.bf16_activations = bf16 and bf16_activations
+        self.after_actor_phase = after_actor_phase
+        self.record_masks = record_masks  # receives the natural decisions x > 0 when nothing is forced
+        self.record_products = record_products  # receives the block products' outputs (BatchNorm inputs)
+        self.used = 0
+
+    def relu(self, x: torch.Tensor) -> torch.Tensor:
+        if self.relu_masks is None:
+            if self.record_masks is not None:
+                self.record_masks.append((x.detach() > 0).clone())
+            return F.relu(x)
+        if self.used >= len(self.relu_masks):
+            raise ValueError("More ReLUs than forced masks.")
+        mask = torch.as_tensor(self.relu_masks[self.used])
+        self.used += 1
+        if tuple(mask.shape) != tuple(x.shape):
+            raise ValueError(f"Forced ReLU mask {tuple(mask.shape)} does not fit its input {tuple(x.shape)}.")
+        return x * mask.to(x.dtype)
+
+    def product(self, x, w, ensemble: bool, *, output_bf16: bool = False, input_grad_bf16: bool = False):
+        """x W^T (ensemble: per member), with the device's roundings in bf16 mode."""
+        if self.bf16:
+            x = _Round.apply(x, True, input_grad_bf16 and self.bf16_activations)
+            w = _Round.apply(w, True, False)
+        y = torch.einsum("nbi,noi->nbo", x, w) if ensemble else F.linear(x, w)
+        if self.bf16:
+            y = _Round.apply(y, output_bf16 and self.bf16_activations, True)
+        if output_bf16 and self.record_products is not None:
+            self.record_products.append(y.detach().clone())
+        return y
+
+
+def _emulation(emulation):
+    return emulation if emulation is not None else Emulation()
+
+
+# ---------------------------------------------------------------------------
 # Forward passes
 # ---------------------------------------------------------------------------
-def actor_forward(p, s, observations, training: bool, noise: torch.Tensor | None, d: Dims):
+def actor_forward(p, s, observations, training: bool, noise: torch.Tensor | None, d: Dims,
+                  emulation: Emulation | None = None):
     """FlashSACActor.forward (networks.py:50-61) with rsample noise injected.
 
     Returns (actions, log_prob, mean, std).  BN running statistics in ``s``
     are updated in place in training mode, as F.batch_norm does (layers.py:36-55).
+    ``emulation`` (parity tests only) applies a device's roundings and ReLU decisions.
     """
+    em = _emulation(emulation)
     x = F.batch_norm(observations, s["embedder.norm.running_mean"], s["embedder.norm.running_var"],
                      p["embedder.norm.weight"], p["embedder.norm.bias"], training=training, momentum=BN_MOMENTUM,
                      eps=BN_EPS)
-    x = F.linear(x, p["embedder.w.w.weight"])
+    x = em.product(x, p["embedder.w.w.weight"], False)
     for i in range(d.actor_blocks):
         residual = x
-        x = F.linear(x, p[f"encoder.{i}.w1.w.weight"])
+        x = em.product(x, p[f"encoder.{i}.w1.w.weight"], False, output_bf16=True)
         x = F.batch_norm(x, s[f"encoder.{i}.norm1.running_mean"], s[f"encoder.{i}.norm1.running_var"],
                          p[f"encoder.{i}.norm1.weight"], p[f"encoder.{i}.norm1.bias"], training=training,
                          momentum=BN_MOMENTUM, eps=BN_EPS)
-        x = F.relu(x)
-        x = F.linear(x, p[f"encoder.{i}.w2.w.weight"])
+        x = em.relu(x)
+        x = em.product(x, p[f"encoder.{i}.w2.w.weight"], False, output_bf16=True, input_grad_bf16=True)
         x = F.batch_norm(x, s[f"encoder.{i}.norm2.running_mean"], s[f"encoder.{i}.norm2.running_var"],
                          p[f"encoder.{i}.norm2.weight"], p[f"encoder.{i}.norm2.bias"], training=training,
                          momentum=BN_MOMENTUM, eps=BN_EPS)
-        x = F.relu(x)
+        x = em.relu(x)
         x = x + residual
     x = F.rms_norm(x, (d.actor_hidden,), p["post_norm.weight"], eps=RMS_EPS)
-    mean = F.linear(x, p["predictor.mean_w.w.weight"], p["predictor.mean_bias"])
-    raw_log_std = F.linear(x, p["predictor.std_w.w.weight"], p["predictor.std_bias"])
+    mean = em.product(x, p["predictor.mean_w.w.weight"], False) + p["predictor.mean_bias"]
+    raw_log_std = em.product(x, p["predictor.std_w.w.weight"], False) + p["predictor.std_bias"]
     log_std = LOG_STD_MIN + (LOG_STD_MAX - LOG_STD_MIN) * 0.5 * (1 + torch.tanh(raw_log_std))
     std = torch.exp(log_std)
     if noise is None:
@@ -278,27 +363,30 @@ def _relu_margin(x, margins):
             margins.append((x.abs() / scale).amin(dim=-1))
 
 
-def critic_forward(p, s, observations, actions, training: bool, d: Dims, margins: list | None = None):
+def critic_forward(p, s, observations, actions, training: bool, d: Dims, margins: list | None = None,
+                   emulation: Emulation | None = None):
     """FlashSACDoubleCritic.forward (networks.py:97-110); returns (q [2, R], log_probs [2, R, K]).
-    margins (optional): receives one [2, R] tensor per ReLU, see _relu_margin."""
+    margins (optional): receives one [2, R] tensor per ReLU, see _relu_margin.
+    ``emulation`` (parity tests only) applies a device's roundings and ReLU decisions."""
+    em = _emulation(emulation)
     x = torch.cat((observations, actions), dim=-1)
     x = x.unsqueeze(0).expand(2, -1, -1)
     x = _ensemble_bn(x, p, s, "embedder.norm", training)
-    x = torch.einsum("nbi,noi->nbo", x, p["embedder.w.weight"])
+    x = em.product(x, p["embedder.w.weight"], True)
     for b in range(d.critic_blocks):
         residual = x
-        x = torch.einsum("nbi,noi->nbo", x, p[f"encoder.{b}.w1.weight"])
+        x = em.product(x, p[f"encoder.{b}.w1.weight"], True, output_bf16=True)
         x = _ensemble_bn(x, p, s, f"encoder.{b}.norm1", training)
         _relu_margin(x, margins)
-        x = F.relu(x)
-        x = torch.einsum("nbi,noi->nbo", x, p[f"encoder.{b}.w2.weight"])
+        x = em.relu(x)
+        x = em.product(x, p[f"encoder.{b}.w2.weight"], True, output_bf16=True, input_grad_bf16=True)
         x = _ensemble_bn(x, p, s, f"encoder.{b}.norm2", training)
         _relu_margin(x, margins)
-        x = F.relu(x)
+        x = em.relu(x)
         x = x + residual
     rms = torch.sqrt(torch.mean(x * x, dim=-1, keepdim=True) + RMS_EPS)
     x = (x / rms) * p["post_norm.weight"].unsqueeze(1)
-    value = torch.einsum("nbi,noi->nbo", x, p["predictor.w.weight"]) + p["predictor.bias"].unsqueeze(1)
+    value = em.product(x, p["predictor.w.weight"], True) + p["predictor.bias"].unsqueeze(1)
     log_prob = F.log_softmax(value, dim=-1)
     q = torch.sum(torch.exp(log_prob) * critic_support(d, log_prob.dtype).reshape(1, 1, -1), dim=-1)
     return q, log_prob
@@ -451,14 +539,17 @@ def _adam_step(state: OracleState, name: str, params, grads):
 
 
 def update(state: OracleState, batch: dict, actor_noise: torch.Tensor, next_noise: torch.Tensor,
-           do_actor_update: bool | None = None, record: dict | None = None) -> dict:
+           do_actor_update: bool | None = None, record: dict | None = None,
+           emulation: Emulation | None = None) -> dict:
     """One FlashSAC update (agent.py:217-281 over updates.py:83-326).
 
     ``batch`` holds observation, action, reward, terminated, next_observation,
     discount (fp tensors, B rows).  ``record`` (optional) receives gradients
-    and intermediate tensors for parity tests.  Returns the reference metric
-    dictionary.
+    and intermediate tensors for parity tests; ``emulation`` (optional) applies
+    a device's roundings and ReLU decisions (parity tests).  Returns the
+    reference metric dictionary.
     """
+    em = emulation
     d, cfg = state.d, state.cfg
     dt = state.dtype
     if do_actor_update is None:
@@ -475,11 +566,11 @@ def update(state: OracleState, batch: dict, actor_noise: torch.Tensor, next_nois
         actor_params = list(state.actor.values())
         actions_all, log_probs_all, _, _ = actor_forward(state.actor, state.actor_buffers,
                                                          torch.cat([actor_obs, actor_next_obs], 0), True,
-                                                         actor_noise.to(dt), d)
+                                                         actor_noise.to(dt), d, emulation=em)
         actions = actions_all[:rows]
         log_probs = log_probs_all[:rows]
         critic_frozen = OrderedDict((k, v.detach()) for k, v in state.critic.items())
-        qs, _ = critic_forward(critic_frozen, state.critic_buffers, obs, actions, False, d)
+        qs, _ = critic_forward(critic_frozen, state.critic_buffers, obs, actions, False, d, emulation=em)
         q = torch.minimum(qs[0], qs[1])
         temp_value = torch.exp(state.log_temp).detach()
         actor_loss = (log_probs * temp_value - q).mean()
@@ -506,18 +597,20 @@ def update(state: OracleState, batch: dict, actor_noise: torch.Tensor, next_nois
         record["temperature_grad"] = grad.detach().clone()
         _adam_step(state, "temperature", [state.log_temp], [grad])
         info.update({"temperature/value": temperature_value.detach(), "temperature/loss": temperature_loss.detach()})
+        if em is not None and em.after_actor_phase is not None:
+            em.after_actor_phase(state)
 
     # update_critic (updates.py:169-284)
     with torch.no_grad():
         actor_eval = OrderedDict((k, v.detach()) for k, v in state.actor.items())
         next_actions, next_log_probs, _, _ = actor_forward(actor_eval, state.actor_buffers, actor_next_obs, False,
-                                                           next_noise.to(dt), d)
+                                                           next_noise.to(dt), d, emulation=em)
         temp_value = torch.exp(state.log_temp.detach())
         next_entropy = temp_value * next_log_probs
         obs_all = torch.cat([obs, next_obs], 0)
         act_all = torch.cat([b["action"], next_actions], 0)
         target_frozen = OrderedDict((k, v.detach()) for k, v in state.target.items())
-        qs_all, lp_all = critic_forward(target_frozen, state.target_buffers, obs_all, act_all, True, d)
+        qs_all, lp_all = critic_forward(target_frozen, state.target_buffers, obs_all, act_all, True, d, emulation=em)
         next_qs = qs_all[:, rows:]
         next_lp = select_min_q_log_probs(next_qs, lp_all[:, rows:])
         target_probs = categorical_td_target(next_lp, b["reward"], b["terminated"], next_entropy, b["discount"],
@@ -528,7 +621,7 @@ def update(state: OracleState, batch: dict, actor_noise: torch.Tensor, next_nois
     record["target_q"] = qs_all.clone()
     record["target_probs"] = target_probs.clone()
     critic_params = list(state.critic.values())
-    _, pred_lp = critic_forward(state.critic, state.critic_buffers, obs_all, act_all, True, d)
+    _, pred_lp = critic_forward(state.critic, state.critic_buffers, obs_all, act_all, True, d, emulation=em)
     ce = -(target_probs.unsqueeze(0) * pred_lp[:, :rows]).sum(dim=-1)
     critic_loss = ce.mean()
     grads = torch.autograd.grad(critic_loss, critic_params)

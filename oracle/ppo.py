@@ -142,6 +142,17 @@ def gaussian_kl(old_mean, old_std, mean, std):
     return (0.5 * (ratio * ratio + delta * delta - 1.0) - torch.log(ratio)).sum(-1)
 
 
+def adapt_learning_rate(learning_rate: float, kl: float, desired_kl: float) -> float:
+    """_adapt_learning_rate (robolearn/warp/ppo.py:233-238): lr / 1.5, floored at 1e-5, when the
+    minibatch KL exceeds twice the target; lr * 1.5, capped at 1e-2, when 0 < KL < target / 2; both
+    comparisons strict, otherwise unchanged."""
+    if kl > desired_kl * 2.0:
+        return max(1.0e-5, learning_rate / 1.5)
+    if kl < desired_kl / 2.0 and kl > 0.0:
+        return min(1.0e-2, learning_rate * 1.5)
+    return learning_rate
+
+
 def clip_gradients(params, max_norm: float) -> float:
     """g <- g * min(1, max_norm / (||g|| + 1e-6)) over one group (robolearn/warp/ppo.py:241-252,
     676-693, the separate-group form; the combined form clips all parameters as one group with the
@@ -188,10 +199,7 @@ class PPOOracle:
             with torch.no_grad():
                 kl = gaussian_kl(data["means"][idx].to(dt), data["stds"][idx].to(dt), mean,
                                  std_of(self.std_parameter, cfg)).mean().item()
-                if kl > 2.0 * cfg.desired_kl:
-                    self.learning_rate = max(1.0e-5, self.learning_rate / 1.5)
-                elif 0.0 < kl < cfg.desired_kl / 2.0:
-                    self.learning_rate = min(1.0e-2, self.learning_rate * 1.5)
+                self.learning_rate = adapt_learning_rate(self.learning_rate, kl, cfg.desired_kl)
                 self.last["kl"] = kl
             for group in self.optimizer.param_groups:
                 group["lr"] = self.learning_rate

@@ -16,11 +16,13 @@
 //
 // One wavefront owns one row (K <= 512; kernels are instantiated for 1, 2, 4
 // or 8 bins per lane); the fused TD target + cross-entropy uses 16-lane row
-// groups instead for K <= 128.  The projection is deterministic and reproduces the
+// groups instead for K <= 128, and wider rows take one workgroup per row
+// (the head forward and Q backward at any K, the projection up to 4096 bins).  The projection is deterministic and reproduces the
 // reference's per-bin summation order: every lane owns its target bins and adds
 // the source bins that land there in source order, so no atomics are involved.
 #include "common.hpp"
 
+#include <climits>
 #include <cmath>
 
 namespace rl {
@@ -740,6 +742,270 @@ __global__ __launch_bounds__(1024) void reduce_vector(const float* x, long long 
     if (threadIdx.x == 0) out[0] = op == 1 ? part[0] : part[0] * scale;
 }
 
+// ---------------------------------------------------------------------------
+// Wide rows: more bins than one wavefront's registers hold (K > 512).  One
+// workgroup of 256 threads per row, thread t owning bins j = t + 256 i; every
+// reduction is a fixed-order block reduction, so results are deterministic.
+// The log-softmax passes re-read the row (it stays in the L2).  The two-hot
+// projection keeps its tables in LDS, which bounds it at 4096 bins (the
+// reference's own limit, robolearn/cuda/categorical_kernels.cuh:164-166); the
+// head forward and Q backward take any width.
+// ---------------------------------------------------------------------------
+constexpr int kWideThreads = 256;
+constexpr int kWidePer = 16;                             // bins per thread in the projection
+constexpr int kWideTargetBins = kWideThreads * kWidePer;  // 4096
+
+__device__ __forceinline__ float wide_block_max(float value, float* scratch) {
+    value = wave_max(value);
+    const int wave = threadIdx.x / kWave;
+    __syncthreads();
+    if (threadIdx.x % kWave == 0) scratch[wave] = value;
+    __syncthreads();
+    float m = scratch[0];
+#pragma unroll
+    for (int w = 1; w < kWideThreads / kWave; ++w) m = fmaxf(m, scratch[w]);
+    return m;
+}
+
+// max m and log-sum-exp of x_j + b_j (lp_j = x_j + b_j - m - lse), and the
+// expectation Q = sum_j exp(lp_j) z_j when a support is given.
+struct WideStats {
+    float m, lse, q;
+};
+
+__device__ __forceinline__ WideStats wide_log_softmax(const float* row, const float* bias, const float* support,
+                                                      int bins, float* scratch) {
+    float m = -INFINITY;
+    for (int j = threadIdx.x; j < bins; j += kWideThreads) m = fmaxf(m, row[j] + (bias ? bias[j] : 0.0f));
+    m = wide_block_max(m, scratch);
+    float s = 0.0f;
+    for (int j = threadIdx.x; j < bins; j += kWideThreads) s += expf(row[j] + (bias ? bias[j] : 0.0f) - m);
+    const float lse = logf(block_sum<kWideThreads>(s, scratch));
+    float e = 0.0f;
+    if (support) {
+        for (int j = threadIdx.x; j < bins; j += kWideThreads)
+            e += expf(row[j] + (bias ? bias[j] : 0.0f) - m - lse) * support[j];
+        e = block_sum<kWideThreads>(e, scratch);
+    }
+    return WideStats{m, lse, e};
+}
+
+__global__ __launch_bounds__(kWideThreads) void wide_head_forward(const float* logits, const float* bias,
+                                                                  long long bias_stride, const float* support,
+                                                                  float* log_probs, float* values, long long rows,
+                                                                  int bins) {
+    __shared__ float scratch[kWideThreads / kWave];
+    const long long row = blockIdx.x;
+    const int e = static_cast<int>(row / rows);
+    const float* x = logits + row * bins;
+    const float* b = bias ? bias + e * bias_stride : nullptr;
+    const WideStats st = wide_log_softmax(x, b, support, bins, scratch);
+    if (log_probs)
+        for (int j = threadIdx.x; j < bins; j += kWideThreads)
+            log_probs[row * bins + j] = x[j] + (b ? b[j] : 0.0f) - st.m - st.lse;
+    if (threadIdx.x == 0) values[row] = st.q;
+}
+
+__global__ __launch_bounds__(kWideThreads) void wide_head_backward_q(const float* logits, const float* bias,
+                                                                     long long bias_stride, const float* support,
+                                                                     const float* dvalues, float* dlogits,
+                                                                     unsigned short* dlogits_bf16, long long rows,
+                                                                     int bins) {
+    __shared__ float scratch[kWideThreads / kWave];
+    const long long row = blockIdx.x;
+    const int e = static_cast<int>(row / rows);
+    const float* x = logits + row * bins;
+    const float* b = bias ? bias + e * bias_stride : nullptr;
+    const WideStats st = wide_log_softmax(x, b, support, bins, scratch);
+    const float dq = dvalues[row];
+    for (int j = threadIdx.x; j < bins; j += kWideThreads) {
+        const float lp = x[j] + (b ? b[j] : 0.0f) - st.m - st.lse;
+        const float g = dq * expf(lp) * (support[j] - st.q);
+        if (dlogits) dlogits[row * bins + j] = g;
+        if (dlogits_bf16) dlogits_bf16[row * bins + j] = f32_to_bf16_bits(g);
+    }
+}
+
+// LDS tables of the wide two-hot projection.
+struct WideTables {
+    unsigned short lower[kWideTargetBins];
+    unsigned short upper[kWideTargetBins];
+    float lower_mass[kWideTargetBins];
+    float upper_mass[kWideTargetBins];
+    float scratch[kWideThreads / kWave];
+};
+
+__device__ __forceinline__ int first_at_least_u16(const unsigned short* idx, int bins, int k) {
+    int lo = 0, hi = bins;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (static_cast<int>(idx[mid]) < k) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// The two-hot projection of project_row for a whole workgroup: probs[i] holds
+// p_j for j = threadIdx.x + 256 i; t is returned in the same layout.  Target
+// bin k receives its lower-bin masses in source order, then its upper-bin
+// masses in source order (updates.py:76-79); sources of bin k form a
+// contiguous range when the bin indices are non-decreasing, else every source
+// is scanned.
+__device__ __forceinline__ void wide_project(const TargetArgs& a, const RowInputs& in, const float* probs, float* t,
+                                             WideTables& tab) {
+    const int bins = a.bins;
+#pragma unroll
+    for (int i = 0; i < kWidePer; ++i) {
+        const int j = threadIdx.x + i * kWideThreads;
+        if (j < bins) {
+            const float z = a.support ? a.support[j] : a.min_v + static_cast<float>(j) * a.width;
+            float v = in.reward + (in.discount * (z - in.entropy)) * in.not_done;
+            v = fminf(fmaxf(v, a.min_v), a.max_v);
+            const float b = (v - a.min_v) / a.width;
+            int lower = static_cast<int>(floorf(b));
+            lower = min(max(lower, 0), bins - 1);
+            const int upper = min(lower + 1, bins - 1);
+            const float frac = b - static_cast<float>(lower);
+            tab.lower[j] = static_cast<unsigned short>(lower);
+            tab.upper[j] = static_cast<unsigned short>(upper);
+            tab.lower_mass[j] = probs[i] * (1.0f - frac);
+            tab.upper_mass[j] = probs[i] * frac;
+        }
+    }
+    __syncthreads();
+    bool monotone = true;
+#pragma unroll
+    for (int i = 0; i < kWidePer; ++i) {
+        const int j = threadIdx.x + i * kWideThreads;
+        if (j > 0 && j < bins)
+            monotone = monotone && tab.lower[j] >= tab.lower[j - 1] && tab.upper[j] >= tab.upper[j - 1];
+    }
+    if (__syncthreads_and(monotone)) {
+#pragma unroll
+        for (int i = 0; i < kWidePer; ++i) {
+            const int k = threadIdx.x + i * kWideThreads;
+            float sum = 0.0f;
+            if (k < bins) {
+                const int l0 = first_at_least_u16(tab.lower, bins, k);
+                const int l1 = first_at_least_u16(tab.lower, bins, k + 1);
+                for (int j = l0; j < l1; ++j) sum += tab.lower_mass[j];
+                const int u0 = first_at_least_u16(tab.upper, bins, k);
+                const int u1 = first_at_least_u16(tab.upper, bins, k + 1);
+                for (int j = u0; j < u1; ++j) sum += tab.upper_mass[j];
+            }
+            t[i] = sum;
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < kWidePer; ++i) {
+        const int k = threadIdx.x + i * kWideThreads;
+        float sum = 0.0f;
+        if (k < bins) {
+            for (int j = 0; j < bins; ++j)
+                if (tab.lower[j] == k) sum += tab.lower_mass[j];
+            for (int j = 0; j < bins; ++j)
+                if (tab.upper[j] == k) sum += tab.upper_mass[j];
+        }
+        t[i] = sum;
+    }
+}
+
+// td_cross_entropy for 512 < K <= 4096: one workgroup per row.
+__global__ __launch_bounds__(kWideThreads) void wide_td_cross_entropy(TargetArgs a, const float* target_logits,
+                                                                      const float* target_bias, long long target_rows,
+                                                                      const float* online_logits,
+                                                                      const float* online_bias, long long online_rows,
+                                                                      long long batch, float scale, float* target_out,
+                                                                      float* dlogits, unsigned short* dlogits_bf16,
+                                                                      float* loss_rows, float* entropy_rows,
+                                                                      float* q_next) {
+    __shared__ WideTables tab;
+    const long long row = blockIdx.x;
+    const int bins = a.bins;
+    const RowInputs in = load_row_inputs(a, row);
+    const float* x0 = target_logits + row * bins;
+    const float* x1 = target_logits + (target_rows + row) * bins;
+    const float* b1 = target_bias ? target_bias + bins : nullptr;
+    const WideStats s0 = wide_log_softmax(x0, target_bias, a.support, bins, tab.scratch);
+    const WideStats s1 = wide_log_softmax(x1, b1, a.support, bins, tab.scratch);
+    const bool second = s1.q < s0.q;
+    const float* xs = second ? x1 : x0;
+    const float* bs = second ? b1 : target_bias;
+    const WideStats& ss = second ? s1 : s0;
+    float probs[kWidePer], t[kWidePer];
+#pragma unroll
+    for (int i = 0; i < kWidePer; ++i) {
+        const int j = threadIdx.x + i * kWideThreads;
+        probs[i] = j < bins ? expf(xs[j] + (bs ? bs[j] : 0.0f) - ss.m - ss.lse) : 0.0f;
+    }
+    wide_project(a, in, probs, t, tab);
+    float tsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kWidePer; ++i)
+        if (threadIdx.x + i * kWideThreads < bins) tsum += t[i];
+    tsum = block_sum<kWideThreads>(tsum, tab.scratch);
+    if (target_out) {
+#pragma unroll
+        for (int i = 0; i < kWidePer; ++i) {
+            const int j = threadIdx.x + i * kWideThreads;
+            if (j < bins) target_out[row * bins + j] = t[i];
+        }
+    }
+#pragma unroll
+    for (int member = 0; member < 2; ++member) {
+        const long long orow = member * online_rows + row;
+        const float* o = online_logits + orow * bins;
+        const float* ob = online_bias ? online_bias + member * bins : nullptr;
+        const WideStats so = wide_log_softmax(o, ob, nullptr, bins, tab.scratch);
+        float ce = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kWidePer; ++i) {
+            const int j = threadIdx.x + i * kWideThreads;
+            if (j < bins) {
+                const float lp = o[j] + (ob ? ob[j] : 0.0f) - so.m - so.lse;
+                ce -= t[i] * lp;
+                const float g = scale * (expf(lp) * tsum - t[i]);
+                if (dlogits) dlogits[orow * bins + j] = g;
+                if (dlogits_bf16) dlogits_bf16[orow * bins + j] = f32_to_bf16_bits(g);
+            }
+        }
+        ce = block_sum<kWideThreads>(ce, tab.scratch);
+        if (threadIdx.x == 0) loss_rows[member * batch + row] = ce;
+    }
+    if (threadIdx.x == 0) {
+        entropy_rows[row] = in.entropy;
+        if (q_next) {
+            q_next[row] = s0.q;
+            q_next[batch + row] = s1.q;
+        }
+    }
+}
+
+// project_target for 512 < K <= 4096: one workgroup per row.
+__global__ __launch_bounds__(kWideThreads) void wide_project_target(TargetArgs a, const float* q,
+                                                                    const float* log_probs, long long batch,
+                                                                    float* target, float* maximum_entropy) {
+    __shared__ WideTables tab;
+    const long long row = blockIdx.x;
+    const int bins = a.bins;
+    const int selected = q[3 * batch + row] < q[batch + row] ? 1 : 0;
+    const float* src = log_probs + (static_cast<long long>(selected) * (2 * batch) + batch + row) * bins;
+    float probs[kWidePer], t[kWidePer];
+#pragma unroll
+    for (int i = 0; i < kWidePer; ++i) {
+        const int j = threadIdx.x + i * kWideThreads;
+        probs[i] = j < bins ? expf(src[j]) : 0.0f;
+    }
+    wide_project(a, load_row_inputs(a, row), probs, t, tab);
+#pragma unroll
+    for (int i = 0; i < kWidePer; ++i) {
+        const int j = threadIdx.x + i * kWideThreads;
+        if (j < bins) target[row * bins + j] = t[i];
+    }
+    if (threadIdx.x == 0) atomic_max_float(maximum_entropy, a.alpha[0] * a.next_log_probs[row]);
+}
+
 // Launches Kernel<PerLane> with the narrowest per-lane width that holds `bins`.
 template <template <int> class Launch, class... Args>
 void dispatch_bins(int bins, Args&&... args) {
@@ -806,11 +1072,18 @@ RL_API int rl_categorical_head_forward(const float* logits, const float* bias, l
                                        const float* support, float* log_probs, float* values, long long rows,
                                        int bins, int ensemble, void* stream) noexcept {
     return rl::guarded("rl_categorical_head_forward", [&] {
-        rl::require(logits && support && values && rows > 0 && bins >= 2 && bins <= kMaxBins && ensemble > 0,
-                    "Categorical head needs logits, support, values and 2..512 bins.");
-        rl::cat::dispatch_bins<rl::cat::HeadForward>(bins, dim3(rl::ceil_div(rows * ensemble, rl::cat::kWaves)),
-                                                     rl::as_stream(stream), logits, bias, bias_stride, support,
-                                                     log_probs, values, rows, bins, ensemble);
+        rl::require(logits && support && values && rows > 0 && bins >= 2 && ensemble > 0,
+                    "Categorical head needs logits, support, values and at least 2 bins.");
+        rl::require(rows * ensemble <= INT_MAX, "Categorical head row count is too large.");
+        if (bins > kMaxBins) {
+            hipLaunchKernelGGL(rl::cat::wide_head_forward, dim3(static_cast<unsigned>(rows * ensemble)),
+                               dim3(rl::cat::kWideThreads), 0, rl::as_stream(stream), logits, bias, bias_stride,
+                               support, log_probs, values, rows, bins);
+        } else {
+            rl::cat::dispatch_bins<rl::cat::HeadForward>(bins, dim3(rl::ceil_div(rows * ensemble, rl::cat::kWaves)),
+                                                         rl::as_stream(stream), logits, bias, bias_stride, support,
+                                                         log_probs, values, rows, bins, ensemble);
+        }
         rl::check_launch("Launch categorical head forward");
     });
 }
@@ -821,12 +1094,19 @@ RL_API int rl_categorical_head_backward_q(const float* logits, const float* bias
                                           void* stream) noexcept {
     return rl::guarded("rl_categorical_head_backward_q", [&] {
         rl::require(logits && support && dvalues && (dlogits || dlogits_bf16) && rows > 0 && bins >= 2 &&
-                        bins <= kMaxBins,
-                    "Categorical Q backward needs logits, support, dvalues, an output and 2..512 bins.");
-        rl::cat::dispatch_bins<rl::cat::HeadBackwardQ>(bins, dim3(rl::ceil_div(rows * ensemble, rl::cat::kWaves)),
-                                                       rl::as_stream(stream), logits, bias, bias_stride, support,
-                                                       dvalues, dlogits, static_cast<unsigned short*>(dlogits_bf16),
-                                                       rows, bins, ensemble);
+                        ensemble > 0,
+                    "Categorical Q backward needs logits, support, dvalues, an output and at least 2 bins.");
+        rl::require(rows * ensemble <= INT_MAX, "Categorical Q backward row count is too large.");
+        if (bins > kMaxBins) {
+            hipLaunchKernelGGL(rl::cat::wide_head_backward_q, dim3(static_cast<unsigned>(rows * ensemble)),
+                               dim3(rl::cat::kWideThreads), 0, rl::as_stream(stream), logits, bias, bias_stride,
+                               support, dvalues, dlogits, static_cast<unsigned short*>(dlogits_bf16), rows, bins);
+        } else {
+            rl::cat::dispatch_bins<rl::cat::HeadBackwardQ>(bins, dim3(rl::ceil_div(rows * ensemble, rl::cat::kWaves)),
+                                                           rl::as_stream(stream), logits, bias, bias_stride, support,
+                                                           dvalues, dlogits, static_cast<unsigned short*>(dlogits_bf16),
+                                                           rows, bins, ensemble);
+        }
         rl::check_launch("Launch categorical Q backward");
     });
 }
@@ -843,7 +1123,9 @@ RL_API int rl_categorical_td_cross_entropy(const float* target_logits, const flo
         rl::require(target_logits && online_logits && support && reward && terminated && discount && next_log_probs &&
                         alpha && (dlogits || dlogits_bf16) && loss_rows && entropy_rows,
                     "TD cross-entropy needs every input and output buffer.");
-        rl::require(batch > 0 && bins >= 2 && bins <= kMaxBins && min_v < max_v, "TD cross-entropy needs 2..512 bins.");
+        rl::require(batch > 0 && bins >= 2 && bins <= rl::cat::kWideTargetBins && min_v < max_v,
+                    "TD cross-entropy needs 2..4096 bins and min_v < max_v.");
+        rl::require(batch <= INT_MAX, "TD cross-entropy batch is too large.");
         rl::require(target_rows >= batch && online_rows >= batch, "Member row strides must cover the batch.");
         rl::cat::TargetArgs a{support, reward, terminated, discount, next_log_probs, alpha, min_v, max_v,
                               static_cast<float>((static_cast<double>(max_v) - min_v) / (bins - 1)), bins};
@@ -860,6 +1142,11 @@ RL_API int rl_categorical_td_cross_entropy(const float* target_logits, const flo
             else if (bins <= 7 * rl::cat::kGroup) RL_TD_ROWS(7);  // 101 bins: 112 lane slots instead of 128
             else RL_TD_ROWS(8);
 #undef RL_TD_ROWS
+        } else if (bins > kMaxBins) {
+            hipLaunchKernelGGL(rl::cat::wide_td_cross_entropy, dim3(static_cast<unsigned>(batch)),
+                               dim3(rl::cat::kWideThreads), 0, rl::as_stream(stream), a, target_logits, target_bias,
+                               target_rows, online_logits, online_bias, online_rows, batch, scale, target_out, dlogits,
+                               dh, loss_rows, entropy_rows, q_next);
         } else {
             rl::cat::dispatch_bins<rl::cat::TdCrossEntropy>(bins, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
                                                             rl::as_stream(stream), a, target_logits, target_bias,
@@ -877,14 +1164,22 @@ RL_API int rl_categorical_td_cross_entropy(const float* target_logits, const flo
 RL_API int rl_flash_categorical_forward(const void* raw, const void* bias, const void* support, void* log_probs,
                                         void* values, int batch, int bins, void* stream) noexcept {
     return rl::guarded("rl_flash_categorical_forward", [&] {
-        rl::require(raw && bias && support && log_probs && values && batch >= 1 && bins >= 2 && bins <= kMaxBins,
-                    "Categorical forward requires nonempty FP32 buffers and 2..512 bins.");
-        rl::cat::dispatch_bins<rl::cat::HeadForward>(bins, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
-                                                     rl::as_stream(stream), static_cast<const float*>(raw),
-                                                     static_cast<const float*>(bias), 0LL,
-                                                     static_cast<const float*>(support), static_cast<float*>(log_probs),
-                                                     static_cast<float*>(values), static_cast<long long>(batch), bins,
-                                                     1);
+        rl::require(raw && bias && support && log_probs && values && batch >= 1 && bins >= 2,
+                    "Categorical forward requires nonempty FP32 buffers and at least two bins.");
+        if (bins > kMaxBins) {
+            hipLaunchKernelGGL(rl::cat::wide_head_forward, dim3(static_cast<unsigned>(batch)),
+                               dim3(rl::cat::kWideThreads), 0, rl::as_stream(stream), static_cast<const float*>(raw),
+                               static_cast<const float*>(bias), 0LL, static_cast<const float*>(support),
+                               static_cast<float*>(log_probs), static_cast<float*>(values),
+                               static_cast<long long>(batch), bins);
+        } else {
+            rl::cat::dispatch_bins<rl::cat::HeadForward>(bins, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
+                                                         rl::as_stream(stream), static_cast<const float*>(raw),
+                                                         static_cast<const float*>(bias), 0LL,
+                                                         static_cast<const float*>(support),
+                                                         static_cast<float*>(log_probs), static_cast<float*>(values),
+                                                         static_cast<long long>(batch), bins, 1);
+        }
         rl::check_launch("Launch categorical forward");
     });
 }
@@ -917,9 +1212,8 @@ RL_API int rl_flash_categorical_backward(const void* log_probs, const void* supp
                                          const void* dvalues, void* scratch, void* draw, void* dbias, int batch,
                                          int bins, void* stream) noexcept {
     return rl::guarded("rl_flash_categorical_backward", [&] {
-        rl::require(log_probs && support && (draw || dbias) && (!dbias || scratch) && batch >= 1 && bins >= 2 &&
-                        bins <= kMaxBins,
-                    "Categorical backward requires FP32 buffers, gradients and 2..512 bins.");
+        rl::require(log_probs && support && (draw || dbias) && (!dbias || scratch) && batch >= 1 && bins >= 2,
+                    "Categorical backward requires FP32 buffers, gradients and valid dimensions.");
         const hipStream_t st = rl::as_stream(stream);
         hipLaunchKernelGGL(rl::cat::head_backward, dim3(rl::ceil_div(batch, rl::cat::kWaves)), dim3(rl::cat::kThreads),
                            0, st, static_cast<const float*>(log_probs), static_cast<const float*>(support),
@@ -942,18 +1236,27 @@ RL_API int rl_flash_categorical_target(const void* q, const void* log_probs, con
                                        float min_v, float max_v, void* stream) noexcept {
     return rl::guarded("rl_flash_categorical_target", [&] {
         rl::require(q && log_probs && reward && terminated && discount && next_log_probs && alpha && target &&
-                        maximum_entropy && batch >= 1 && bins >= 2 && bins <= kMaxBins && min_v < max_v,
-                    "Categorical target requires FP32 buffers, valid support and 2..512 bins.");
+                        maximum_entropy && batch >= 1 && bins >= 2 && bins <= rl::cat::kWideTargetBins &&
+                        min_v < max_v,
+                    "Categorical target requires FP32 buffers, valid support and 2..4096 bins.");
         // Support min_v + j * width, as the reference kernel builds it.
         rl::cat::TargetArgs a{nullptr, static_cast<const float*>(reward), static_cast<const float*>(terminated),
                               static_cast<const float*>(discount), static_cast<const float*>(next_log_probs),
                               static_cast<const float*>(alpha), min_v, max_v, (max_v - min_v) / static_cast<float>(bins - 1),
                               bins};
-        rl::cat::dispatch_bins<rl::cat::ProjectTarget>(bins, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
-                                                       rl::as_stream(stream), a, static_cast<const float*>(q),
-                                                       static_cast<const float*>(log_probs),
-                                                       static_cast<long long>(batch), static_cast<float*>(target),
-                                                       static_cast<float*>(maximum_entropy));
+        if (bins > kMaxBins) {
+            hipLaunchKernelGGL(rl::cat::wide_project_target, dim3(static_cast<unsigned>(batch)),
+                               dim3(rl::cat::kWideThreads), 0, rl::as_stream(stream), a,
+                               static_cast<const float*>(q), static_cast<const float*>(log_probs),
+                               static_cast<long long>(batch), static_cast<float*>(target),
+                               static_cast<float*>(maximum_entropy));
+        } else {
+            rl::cat::dispatch_bins<rl::cat::ProjectTarget>(bins, dim3(rl::ceil_div(batch, rl::cat::kWaves)),
+                                                           rl::as_stream(stream), a, static_cast<const float*>(q),
+                                                           static_cast<const float*>(log_probs),
+                                                           static_cast<long long>(batch), static_cast<float*>(target),
+                                                           static_cast<float*>(maximum_entropy));
+        }
         rl::check_launch("Launch categorical target");
     });
 }

@@ -195,6 +195,27 @@ __global__ __launch_bounds__(kGatherWaves* kWave) void gather_kernel(GatherArgs 
     }
 }
 
+// Rows wider than the register-batched kernel holds (obs_dim > 256 or
+// action_dim > 64): one wave per sampled row, lanes striding over the row.
+__global__ __launch_bounds__(kGatherWaves* kWave) void gather_rows_kernel(GatherArgs a) {
+    const int lane = threadIdx.x % kWave;
+    const long long r = static_cast<long long>(blockIdx.x) * kGatherWaves + threadIdx.x / kWave;
+    if (r >= a.rows) return;  // wave-uniform
+    const long long k = a.indices[a.offset + r];
+    for (int j = lane; j < a.obs_dim; j += kWave) a.b_obs[r * a.obs_ld + j] = a.obs[k * a.obs_dim + j];
+    for (int j = lane; j < a.action_dim; j += kWave) {
+        a.b_actions[r * a.action_dim + j] = a.actions[k * a.action_dim + j];
+        a.b_means[r * a.action_dim + j] = a.means[k * a.action_dim + j];
+        a.b_stds[r * a.action_dim + j] = a.stds[k * a.action_dim + j];
+    }
+    if (lane == 0) {
+        a.b_log_probs[r] = a.log_probs[k];
+        a.b_values[r] = a.values[k];
+        a.b_advantages[r] = a.advantages[k];
+        a.b_returns[r] = a.returns[k];
+    }
+}
+
 // Row-parallel passes over the minibatch: one wave per row (lanes over the
 // action dimensions), kRowsPerBlock rows per workgroup, per-workgroup sums in
 // fixed order, then one finishing workgroup that adds the partials in fixed
@@ -693,14 +714,16 @@ RL_API int rl_ppo_gather(const int* indices, long long offset, long long rows, i
     return rl::guarded("rl_ppo_gather", [&] {
         rl::require(indices && rows > 0 && rows <= (1LL << 32) && obs_dim > 0 && action_dim > 0 && obs_ld >= obs_dim,
                     "PPO gather shapes are invalid.");
-        rl::require(obs_dim <= 4 * rl::kWave && action_dim <= rl::kWave,
-                    "PPO gather supports up to 256 observation and 64 action dimensions.");
-
         Q::GatherArgs a{indices, offset, rows, obs_dim, action_dim, obs_ld, obs, actions, log_probs, values, advantages,
                         returns, means, stds, b_obs, b_actions, b_log_probs, b_values, b_advantages, b_returns, b_means,
                         b_stds};
-        hipLaunchKernelGGL(Q::gather_kernel, dim3(rl::ceil_div(rows, Q::kGatherRows * Q::kGatherWaves)),
-                           dim3(Q::kGatherWaves * rl::kWave), 0, rl::as_stream(stream), a);
+        if (obs_dim <= 4 * rl::kWave && action_dim <= rl::kWave) {
+            hipLaunchKernelGGL(Q::gather_kernel, dim3(rl::ceil_div(rows, Q::kGatherRows * Q::kGatherWaves)),
+                               dim3(Q::kGatherWaves * rl::kWave), 0, rl::as_stream(stream), a);
+        } else {
+            hipLaunchKernelGGL(Q::gather_rows_kernel, dim3(rl::ceil_div(rows, Q::kGatherWaves)),
+                               dim3(Q::kGatherWaves * rl::kWave), 0, rl::as_stream(stream), a);
+        }
         rl::check_launch("Launch PPO gather");
     });
 }

@@ -36,6 +36,12 @@ METRIC_KEYS = ("actor/loss", "actor/entropy", "actor/mean_action", "critic/loss"
 BATCH_KEYS = ("observation", "action", "reward", "terminated", "truncated", "next_observation", "discount")
 
 
+def target_entropy(action_dim: int, sigma: float) -> float:
+    """Temperature target: the differential entropy of an action_dim-dimensional Normal with standard
+    deviation sigma per dimension, 0.5 A ln(2 pi e sigma^2) (robolearn/flashsac/agent.py:329)."""
+    return 0.5 * action_dim * math.log(2.0 * math.pi * math.e * sigma**2)
+
+
 def actor_shapes(obs, act, h, blocks):
     from collections import OrderedDict
 
@@ -130,14 +136,13 @@ class FlashSAC:
             raise ValueError("Target EMA tau must lie in [0, 1].")
         if cfg.learning_rate_warmup_step < 0 or cfg.learning_rate_warmup_step >= cfg.learning_rate_decay_step:
             raise ValueError("Learning-rate warmup must be nonnegative and shorter than decay.")
-        if cfg.critic_num_bins > 512:
-            raise ValueError("The MI355X categorical kernels support at most 512 bins.")
+        if not 2 <= cfg.critic_num_bins <= 4096:
+            raise ValueError("The categorical TD projection supports 2 to 4096 bins (the reference native limit).")
         if not torch.cuda.is_available():
             raise RuntimeError("FlashSAC on MI355X requires a visible GPU; there is no CPU fallback.")
         _native.load()
-        target_entropy = 0.5 * action_dim * math.log(2.0 * math.pi * math.e * cfg.temp_target_sigma**2)
         self.cfg = self.config = replace(cfg, asymmetric_observation=critic_observation_dim is not None,
-                                         temp_target_entropy=target_entropy)
+                                         temp_target_entropy=target_entropy(action_dim, cfg.temp_target_sigma))
         self.device = torch.device(cfg.device if str(cfg.device).startswith("cuda") else "cuda:0")
         self.observation_dim = observation_dim
         self.critic_observation_dim = total_dim

@@ -56,8 +56,6 @@ class WarpPPO:
             raise ValueError("std_range must contain positive increasing bounds.")
         if action_dim > 64:
             raise ValueError("The MI355X PPO loss kernels support at most 64 action dimensions.")
-        if observation_dim > 256:
-            raise ValueError("The MI355X PPO minibatch gather supports at most 256 observation dimensions.")
         if cfg.activation != "elu":
             raise NotImplementedError("The MI355X PPO path implements ELU activations (the G1 recipe).")
         if not torch.cuda.is_available():

@@ -30,10 +30,14 @@ Layout (robolearn/warp/flashsac.py:1085-1239):
 
 Where the two implementations draw random numbers differently, the arrays keep
 their shapes: this backend draws from Philox streams keyed by the seed and its
-device counters (the update counters and the exploration step), so the Warp RNG
-state arrays are written as zeros and ignored on load, and the exploration step
-travels in an extra array ("mi355x.exploration_step") that the reference's
-loader skips (it reads only its own keys, flashsac.py:1132-1138).
+device counters (the update counters and the exploration step) and ignores the
+Warp RNG state arrays on load; the exploration step travels in an extra array
+("mi355x.exploration_step") that the reference's loader skips (it reads only its
+own keys, flashsac.py:1132-1138).  The Warp learner does read the RNG arrays and
+draws row i's noise from state i (flashsac.py:44-50), so they are written as the
+per-element states its constructor seeds (flashsac.py:495-501 with offsets 11,
+23, 37, 41; _flash_replay.py:216 for replay.rng), see warp_rng_states: every
+row and environment of a resumed Warp run gets its own stream.
 
 The order of the Adam moments is the module order of the networks: a module's
 own parameters in registration order, then its child modules in registration
@@ -57,6 +61,25 @@ FORMAT = "robolearn-warp-flashsac-v1"
 REPLAY_FIELDS = ("observation", "action", "reward", "terminated", "truncated", "next_observation", "discount")
 AMP_KEYS = (("loss_scale", np.float32), ("scale_growth_tracker", np.int32), ("found_inf", np.int32),
             ("step_skipped", np.int32), ("attempted_steps", np.int64), ("skipped_steps", np.int64))
+
+
+def _pcg_hash(state: np.ndarray) -> np.ndarray:
+    """The PCG-RXS-M-XS hash of Jarzynski and Olano, "Hash Functions for GPU Rendering", JCGT 9(3),
+    2020, on uint32 arrays (wrapping arithmetic)."""
+    state = state.astype(np.uint32)
+    b = state * np.uint32(747796405) + np.uint32(2891336453)
+    c = ((b >> ((b >> np.uint32(28)) + np.uint32(4))) ^ b) * np.uint32(277803737)
+    return (c >> np.uint32(22)) ^ c
+
+
+def warp_rng_states(seed: int, count: int) -> np.ndarray:
+    """uint32 generator states for elements 0 .. count - 1 as warp-lang's rand_init(seed, i) builds
+    them: the PCG hash of seed + hash(i), the composition warp-lang's open-source rand.h uses
+    (warp-lang 1.18.0, not in the reference tree or this image: the exact values are parity
+    unpinned; distinct per-element states are what the Warp learner's per-row draws need)."""
+    index = np.arange(count, dtype=np.uint32)
+    with np.errstate(over="ignore"):
+        return _pcg_hash(np.uint32(seed & 0xFFFFFFFF) + _pcg_hash(index))
 
 
 def warp_critic_name(torch_key: str) -> str:
@@ -172,15 +195,16 @@ def to_state(agent, include_replay: bool = True) -> dict:
     state["log_temperature"] = np.asarray(native["log_temperature"], np.float32).reshape(1)
     state["update_counters"] = np.asarray(native["update_counters"], np.int64)
     B, E = agent.batch_size, agent.num_envs
-    for key, size in (("rng.actor", 2 * B), ("rng.next", B), ("rng.exploration", E), ("rng.repeat", 1)):
-        state[key] = np.zeros(size, np.uint32)
+    for key, size, offset in (("rng.actor", 2 * B, 11), ("rng.next", B, 23), ("rng.exploration", E, 37),
+                              ("rng.repeat", 1, 41)):
+        state[key] = warp_rng_states(cfg.seed + offset, size)
     exploration = agent.exploration_state.cpu().numpy()
     state["exploration.repetition"] = exploration[:2].astype(np.int32)
     state["exploration.cached_noise"] = agent.exploration_noise.cpu().numpy().astype(np.float32)
     state["mi355x.exploration_step"] = agent.exploration_step.cpu().numpy().astype(np.int64)
     agent._ensure_replay()
     state["replay.counters"] = agent.replay_counters.cpu().numpy().astype(np.int64)
-    state["replay.rng"] = np.zeros(B, np.uint32)
+    state["replay.rng"] = warp_rng_states(cfg.seed, B)
     if include_replay:
         count = agent._num_in_buffer_host
         for field in REPLAY_FIELDS:

@@ -178,3 +178,31 @@ def test_checkpoint_roundtrip_preserves_graph(gpu, tmp_path):
         np.testing.assert_array_equal(saved[key], restored[key], err_msg=key)
     agent.update()  # the captured graph still points at the restored buffers
     torch.cuda.synchronize()
+
+
+def test_constructor_target_entropy_is_the_normal_entropy(gpu):
+    """cfg.temp_target_entropy of a constructed learner is A times the entropy of Normal(0, sigma)
+    (robolearn/flashsac/agent.py:329), for the configured temp_target_sigma."""
+    from robolearn_amd.flashsac import FlashSAC
+
+    for sigma in (0.15, 0.4):
+        agent = FlashSAC(OBS, ACT, cfg=_config(temp_target_sigma=sigma))
+        normal = ACT * torch.distributions.Normal(torch.tensor(0.0, dtype=torch.float64),
+                                                  torch.tensor(sigma, dtype=torch.float64)).entropy().item()
+        assert agent.cfg.temp_target_entropy == pytest.approx(normal, rel=1e-12)
+
+
+@pytest.mark.parametrize("bins", [1024, 4096])
+def test_wide_categorical_heads_match_oracle(gpu, bins):
+    """Critics with more bins than the register-row kernels hold take the one-workgroup-per-row
+    categorical kernels (head forward, Q backward, TD target + cross-entropy): an actor-phase update and
+    a critic-only update against the float64 oracle with the device's ReLU decisions, 1e-4."""
+    from parity import forced_update_check
+
+    print(f"case flashsac with {bins}-bin critics vs float64 oracle (forced ReLU decisions)", flush=True)
+    cfg = _config(critic_num_bins=bins)
+    agent, _ = _make(cfg)
+    for step, actor_phase in enumerate((True, False)):
+        batch, an, nn = _inputs(cfg, step)
+        forced_update_check(agent, batch, an, nn, bound=1e-4, label=f"{bins} bins update {step + 1}",
+                            actor_phase=actor_phase)

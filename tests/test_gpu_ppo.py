@@ -289,3 +289,105 @@ def test_fused_clip_equals_sum_squares_then_clip(gpu, n, scale):
     torch.cuda.synchronize()
     assert torch.equal(sa, sb)
     assert torch.equal(a, b)
+
+
+def _device_kl_adapt(lr, old_mean, desired_kl):
+    """rl_ppo_kl_adapt on one row with one action, unit old and new std (std_type 1, clamped): the
+    KL is 0.5 d^2 for d = old_mean, exact in fp32 for dyadic d.  Returns (kl, learning rate)."""
+    dev = torch.device("cuda:0")
+    mean = torch.zeros(1, 1, device=dev)
+    std_param = torch.ones(1, device=dev)
+    old_m = torch.full((1, 1), float(old_mean), device=dev)
+    old_s = torch.ones(1, 1, device=dev)
+    partial = torch.zeros(1, device=dev)
+    kl = torch.zeros(1, device=dev)
+    lr_t = torch.full((1,), float(lr), device=dev)
+    _native.call("rl_ppo_kl_adapt", mean.data_ptr(), 1, std_param.data_ptr(), old_m.data_ptr(), old_s.data_ptr(),
+                 1, 1, 1, 1e-3, 10.0, float(desired_kl), 1, partial.data_ptr(), kl.data_ptr(), lr_t.data_ptr(),
+                 K.stream())
+    torch.cuda.synchronize()
+    return kl.item(), lr_t.item()
+
+
+def test_adaptive_learning_rate_rule_known_answers_on_device(gpu):
+    """The device rule against hand-worked answers of robolearn/warp/ppo.py:233-238 (tests/test_oracle_pins.py
+    holds the same cases for the oracle).  With desired_kl 2^-6 both thresholds are dyadic (2 x target
+    = 0.5 * 0.25^2, target / 2 = 0.5 * 0.125^2), so KL lands exactly on them and the strict comparisons
+    are exercised; the desired_kl 0.01 cases sit away from the thresholds."""
+    f32 = np.float32
+    cases = [  # (lr, d, desired_kl, expected lr computed in fp32)
+        (1e-3, 0.25, 2.0 ** -6, f32(1e-3)),                                # KL == 2 target: unchanged
+        (1e-3, 0.25 * (1 + 2.0 ** -10), 2.0 ** -6, f32(1e-3) / f32(1.5)),  # just above: lowered
+        (1e-3, 0.25 * (1 - 2.0 ** -10), 2.0 ** -6, f32(1e-3)),             # just below: unchanged
+        (1e-3, 0.125, 2.0 ** -6, f32(1e-3)),                               # KL == target / 2: unchanged
+        (1e-3, 0.125 * (1 - 2.0 ** -10), 2.0 ** -6, f32(1e-3) * f32(1.5)),  # just below: raised
+        (1e-3, 0.0, 2.0 ** -6, f32(1e-3)),                                 # KL == 0: unchanged
+        (1e-3, math.sqrt(2 * 0.0025), 0.01, f32(1e-3) * f32(1.5)),         # KL 0.0025: raised
+        (1e-3, math.sqrt(2 * 0.01), 0.01, f32(1e-3)),                      # KL 0.01: unchanged
+        (1e-3, math.sqrt(2 * 0.03), 0.01, f32(1e-3) / f32(1.5)),           # KL 0.03: lowered
+        (1.2e-5, math.sqrt(2 * 0.03), 0.01, f32(1e-5)),                    # floor
+        (8e-3, math.sqrt(2 * 0.001), 0.01, f32(1e-2)),                     # cap
+    ]
+    for lr, d, desired, expected in cases:
+        kl, got = _device_kl_adapt(lr, d, desired)
+        # 0.5 (1 + d^2 - 1) cancels in fp32: absolute error about ulp(1) for small d, exact for dyadic d
+        assert kl == pytest.approx(0.5 * d * d, rel=1e-6, abs=2e-7), (lr, d, desired)
+        assert got == pytest.approx(float(expected), rel=1e-7, abs=0.0), (lr, d, desired, kl, got)
+        assert OP.adapt_learning_rate(float(f32(lr)), kl, desired) == pytest.approx(got, rel=1e-6), (lr, d, desired)
+
+
+@pytest.mark.parametrize("obs_dim, act_dim", [(123, 37), (310, 12), (40, 70)])
+def test_minibatch_gather_is_exact_for_narrow_and_wide_rows(gpu, obs_dim, act_dim):
+    """rl_ppo_gather copies the permuted rows bit for bit, in the register-batched layout (rows up to
+    256 observations and 64 actions) and the per-row strided one beyond it (robolearn/warp/ppo.py:172-204)."""
+    print(f"case ppo gather obs {obs_dim} act {act_dim}", flush=True)
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(obs_dim + act_dim)
+    n, rows, offset = 1000, 301, 37
+    obs_ld = (obs_dim + 3) // 4 * 4
+    src = {"obs": torch.randn(n, obs_dim, generator=g), "actions": torch.randn(n, act_dim, generator=g),
+           "means": torch.randn(n, act_dim, generator=g), "stds": torch.rand(n, act_dim, generator=g)}
+    for key in ("log_probs", "values", "advantages", "returns"):
+        src[key] = torch.randn(n, generator=g)
+    perm = torch.randperm(n, generator=g).to(torch.int32)
+    d = {k: v.to(dev) for k, v in src.items()}
+    out = {"obs": torch.full((rows, obs_ld), 7.0, device=dev)}
+    for key in ("actions", "means", "stds"):
+        out[key] = torch.zeros(rows, act_dim, device=dev)
+    for key in ("log_probs", "values", "advantages", "returns"):
+        out[key] = torch.zeros(rows, device=dev)
+    perm_d = perm.to(dev)
+    _native.call("rl_ppo_gather", perm_d.data_ptr(), offset, rows, obs_dim, act_dim, obs_ld, d["obs"].data_ptr(),
+                 d["actions"].data_ptr(), d["log_probs"].data_ptr(), d["values"].data_ptr(),
+                 d["advantages"].data_ptr(), d["returns"].data_ptr(), d["means"].data_ptr(), d["stds"].data_ptr(),
+                 out["obs"].data_ptr(), out["actions"].data_ptr(), out["log_probs"].data_ptr(),
+                 out["values"].data_ptr(), out["advantages"].data_ptr(), out["returns"].data_ptr(),
+                 out["means"].data_ptr(), out["stds"].data_ptr(), K.stream())
+    torch.cuda.synchronize()
+    idx = perm[offset: offset + rows].long()
+    got_obs = out["obs"].cpu()
+    assert torch.equal(got_obs[:, :obs_dim], src["obs"][idx])
+    assert torch.all(got_obs[:, obs_dim:] == 7.0)  # padding columns untouched
+    for key in ("actions", "means", "stds", "log_probs", "values", "advantages", "returns"):
+        assert torch.equal(out[key].cpu(), src[key][idx]), key
+
+
+def test_update_with_wide_observations_matches_oracle(gpu):
+    """A 310-observation policy (wider than the register-batched gather) against the oracle."""
+    print("case ppo update obs 310 vs oracle", flush=True)
+    cfg = _config()
+    agent = _agent(310, 3, 16, 4, cfg)
+    initial = agent.state_dict()
+    data = _rollout(agent)
+    agent.launch_update()
+    torch.cuda.synchronize()
+    permutation = agent._perm.cpu().numpy().astype(np.int64)
+    oracle = OP.PPOOracle(310, 3, 16, 4, cfg, [initial[f"parameter_{i}"] for i in range(len(agent.parameters))])
+    result = oracle.update(data, permutation)
+    state = agent.state_dict()
+    health = agent.health_metrics()
+    assert health["learning_rate"] == pytest.approx(result["learning_rate"], rel=1e-6)
+    assert health["policy_loss"] == pytest.approx(result["policy_loss"], rel=1e-4, abs=1e-6)
+    assert health["value_loss"] == pytest.approx(result["value_loss"], rel=1e-4, abs=1e-6)
+    for i, p in enumerate(oracle.params):
+        np.testing.assert_allclose(state[f"parameter_{i}"], p.detach().numpy(), atol=2e-4, rtol=0, err_msg=str(i))

@@ -1,21 +1,29 @@
 """FlashSAC at the README shape (obs 31, act 8, batch 2048, actor 256 x 1 block,
 critics 2 x 512 x 2 blocks, 101 bins on [-10, 10]) in both precision modes.
 
-* fp32 mode, one update: losses within 1e-4 relative of the float64 CPU oracle;
-  the frozen eval-mode critic's gradient at the actor's actions row by row
-  (1e-5; rows with a ReLU input within 1e-6 of zero are left out, at most 5 %);
-  the parameters as Adam's first step plus the projections from the GPU's own
-  gradients, 1e-6 relative; gradients and Adam moments reported beside the
-  reference's fp32 path on the same update (the float32 oracle with the rows
-  in the original and five permuted orders), with a 1e-2 sanity bound.  Near-
-  zero ReLU inputs flip with rounding and Adam's first step amplifies
-  near-zero gradients (tests/parity.py), so neither the float64 gradients
-  summed over rows nor the float64 parameters bound an fp32 update tightly:
-  the reference's own fp32 path misses the delta policy on thousands of
-  elements at this shape; the delta-policy counts of both are printed.
-* bf16-operand mode, one update: losses within 1e-2 relative of the oracle, with
-  fp32 activations (the configuration's stated layout, bf16_activations=False)
-  and with bf16 BatchNorm inputs and ReLU-BatchNorm gradients (the G1 layout).
+* fp32 mode, one update: the device's ReLU decisions (replayed exactly from the
+  BatchNorm inputs and statistics it stored, tests/parity.py) are forced into the
+  float64 oracle, and its post-step actor and temperature are loaded before the
+  critic phase, so inputs within rounding of zero, which either side passes or
+  blocks by rounding, and Adam's first step on gradients within rounding of zero
+  (tests/parity.py) do not enter the comparison: every actor, critic and
+  temperature gradient and every Adam moment within 1e-4 relative L2, metrics
+  1e-4 (or 3x the reference's own update run in float32 under the same
+  decisions, where that is larger: it is near 1e-5 here, so 1e-4 decides), the
+  frozen critic's action gradient 1e-5 over all rows, the parameters
+  as Adam's first step plus the projections from the GPU's own gradients (1e-6),
+  running statistics 1e-4 against the plain float64 oracle.
+* bf16-operand mode, one update, with fp32 activations (the configuration's
+  stated layout, bf16_activations=False) and with bf16 BatchNorm inputs and
+  ReLU-BatchNorm gradients (the G1 layout): losses within 1e-2 of the oracle, and
+  every gradient and moment within max(1e-3, 3x the float32 oracle's error) of
+  the float64 oracle run with the device's bf16 roundings
+  (oracle.flashsac.Emulation) and ReLU decisions.  The float32 oracle, the
+  reference's bf16 update at fp32 accumulation under the same roundings and
+  decisions, is itself 1-2 % away from float64 on the critic's gradients: a
+  value within fp32 accumulation error of a bf16 rounding midpoint rounds either
+  way, each rounding stage widens the spread, and the training-mode BatchNorm
+  backward cancels most of its input gradient.
 * 100-update drift, for both layouts: the bf16 mode and the fp32 mode run the same 100 updates
   (same initial weights, replay batches and noise); the relative parameter
   drift between them and the largest loss difference are reported (printed,
@@ -35,7 +43,7 @@ import torch
 from oracle import flashsac as O
 from robolearn_amd.config import FlashSACConfig
 
-from parity import compare, delta_stats, permuted
+from parity import delta_stats, forced_update_check
 
 pytestmark = pytest.mark.gpu
 
@@ -76,81 +84,28 @@ def _agent(cfg, state=None, bf16_activations=True):
 
 
 def test_readme_shape_one_update_matches_oracle(gpu):
-    print("case readme fp32 + bf16 one update vs float64 oracle", flush=True)
+    print("case readme fp32 + bf16 one update vs float64 oracle (device ReLU decisions forced)", flush=True)
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     cfg = _config()
     agent = _agent(cfg)
     state0 = agent.state_dict(include_replay=False)
     state0_t = {k: torch.as_tensor(v).double() for k, v in state0.items()}
-    oracle = O.OracleState(O.dims_from_config(OBS, ACT, agent.cfg), agent.cfg, dtype=torch.float64)
-    oracle.load_flat(dict(state0))
     store = _replay(cfg)
     batch, an, nn = _inputs(store, 0)
-    metrics = _run(agent, batch, an, nn)
-    exact = {}
-    info = O.update(oracle, batch, an, nn, record=exact)
-    for key, value in info.items():
-        assert metrics[key] == pytest.approx(float(value), rel=1e-4, abs=1e-6), key
-    # The frozen eval-mode critic's gradient at the actor's actions, row by row (the rows are independent
-    # through an eval-mode critic).  A ReLU input within 1e-6 of zero (relative to its row's largest)
-    # is passed or blocked by rounding, and one flip changes its row, so those rows are left out; they
-    # must stay rare.
-    before = O.OracleState(oracle.d, agent.cfg, dtype=torch.float64)
-    before.load_flat(dict(state0))
-    margins = []
-    with torch.no_grad():
-        O.critic_forward(before.critic, before.critic_buffers, torch.as_tensor(batch["observation"]).double(),
-                         exact["actor_actions"][:BATCH], False, before.d, margins=margins)
-    margin = torch.stack(margins).amin(dim=(0, 1))  # per row, over every ReLU of both critics
-    clean = margin > 1e-6
-    Oc, I = agent.critic_observation_dim, agent.critic_in_dim
-    dactions = agent.critic_dx[0].view(BATCH, I)[:, Oc:].cpu().double()  # both critics' sum, actor phase
+    # fp32: every gradient, the temperature gradient, every Adam moment and the metrics at 1e-4 relative
+    # L2 against float64 with the device's ReLU decisions and its post-step actor
+    worst, exact, _ = forced_update_check(agent, batch, an, nn, bound=1e-4, label="readme fp32")
+    print(f"readme fp32: worst error / 1e-4 = {worst:.3f}", flush=True)
+    # the frozen eval-mode critic's gradient at the actor's actions, every row
+    dactions = agent.critic_dx[0].view(BATCH, agent.critic_in_dim)[:, agent.critic_observation_dim:].cpu().double()
     reference = exact["actor_dactions"][:BATCH]
-    err = (dactions - reference)[clean]
-    scale = reference.abs().max().item()
-    print(f"readme fp32: action gradient through the eval critic, {int(clean.sum())} of {BATCH} rows clear of "
-          f"ReLU ties: max error {err.abs().max().item() / scale:.2e} of the largest entry, relative L2 "
-          f"{err.norm().item() / reference[clean].norm().item():.2e}", flush=True)
-    # each row meets 2 critics x 2 blocks x (4h + h) = 10,240 ReLU inputs; with about 3e-6 of them within
-    # 1e-6 of zero, about 3 % of rows are expected to be left out
-    assert int((~clean).sum()) <= BATCH // 20
-    assert err.abs().max().item() <= 1e-5 * scale
-    assert err.norm().item() <= 1e-5 * reference[clean].norm().item()
-    # Gradients and Adam moments against float64 beside the reference's own fp32 path on the same
-    # update (the oracle in float32, rows in the original and five permuted orders): reported, with
-    # a sanity bound.  Their sums over rows include the ReLU flips above (about 35 inputs within 1e-7
-    # of zero per update at this shape), so a single fp32 evaluation lands 1e-5 or 1e-3 away from
-    # float64 by which inputs its rounding flips.
-    ensemble, records = [], []
-    for seed in (None, 1, 2, 3, 4, 5):
-        fp32 = O.OracleState(oracle.d, agent.cfg, dtype=torch.float32)
-        fp32.load_flat(dict(state0))
-        record = {}
-        inputs = (batch, an, nn) if seed is None else permuted(batch, an, nn, seed)
-        O.update(fp32, *inputs, record=record)
-        ensemble.append(fp32)
-        records.append(record)
-    report = []
-    worst = compare("actor grad", {k: v.cpu() for k, v in agent.actor.grads().items()},
-                    [r["actor_grads"] for r in records], exact["actor_grads"], report, check=False)
-    worst = max(worst, compare("critic grad", {k: v.cpu() for k, v in agent.critic.grads().items()},
-                               [r["critic_grads"] for r in records], exact["critic_grads"], report, check=False))
-    gpu_moments = {}
-    for label, net in (("actor", agent.actor), ("critic", agent.critic)):
-        m1, m2 = net.moments()
-        for name in net.shapes:
-            gpu_moments[f"{label}.{name}.m1"] = m1[name].cpu()
-            gpu_moments[f"{label}.{name}.m2"] = m2[name].cpu()
-    m1, m2 = agent.temperature.moments()
-    gpu_moments["temperature.m1"], gpu_moments["temperature.m2"] = m1["log_temp"].cpu(), m2["log_temp"].cpu()
-    worst = max(worst, compare("Adam moments", gpu_moments, [run.moments() for run in ensemble], oracle.moments(),
-                               report, check=False))
-    for label, name, gpu_max, cpu_max, gpu_l2, cpu_l2 in report:
-        assert gpu_l2 < 1e-2, (label, name, gpu_l2)
-    # Adam's first step from the GPU's own gradients, in float64: -lr g / (|g| + eps) (bias-corrected
-    # moments m = g, v = g^2), then the unit projections; the step maps rounding-level gradient
-    # differences on near-zero elements to parameter changes of up to 2 lr, so the parameters are held
-    # to this step given the gradients checked above, not to the float64 trajectory
+    err = dactions - reference
+    print(f"readme fp32: action gradient through the eval critic: relative L2 "
+          f"{err.norm().item() / reference.norm().item():.2e}", flush=True)
+    assert err.norm().item() <= 1e-5 * reference.norm().item()
+    # Adam's first step from the GPU's own (checked) gradients, in float64: -lr g / (|g| + eps), then
+    # the unit projections.  The step maps gradients within rounding of zero to changes of up to
+    # 2 lr, so the parameters are held to this step given the gradients, not to the float64 ones.
     gpu_state = agent.state_dict(include_replay=False)
     lr = O.warmup_cosine(cfg.learning_rate_init, cfg.learning_rate_peak, cfg.learning_rate_end,
                          cfg.learning_rate_warmup_step, cfg.learning_rate_decay_step)(0)
@@ -164,25 +119,31 @@ def test_readme_shape_one_update_matches_oracle(gpu):
             got = torch.as_tensor(gpu_state[f"{label}.{name}"]).double().reshape(value.shape)
             err = (got - value).abs().max().item() / max(value.abs().max().item(), 1e-30)
             assert err < 1e-6, (label, name, err)
+    # the plain float64 oracle (no forcing) for the running statistics and the delta-policy report
+    oracle = O.OracleState(O.dims_from_config(OBS, ACT, agent.cfg), agent.cfg, dtype=torch.float64)
+    oracle.load_flat(dict(state0))
+    info = O.update(oracle, batch, an, nn)
     after = oracle.flat()
     for key, expected_value in after.items():
         if "running" in key:  # BN batch means are O(1e-10) in fp32: absolute floor
             err = (torch.as_tensor(gpu_state[key]).double() - expected_value).abs().max().item()
             assert err <= 1e-4 * expected_value.abs().max().item() + 1e-7, key
-    cpu_state = ensemble[0].flat()
+    fp32 = O.OracleState(oracle.d, agent.cfg, dtype=torch.float32)
+    fp32.load_flat(dict(state0))
+    O.update(fp32, batch, an, nn)
     beyond_gpu = sum(v[2] for v in delta_stats(state0_t, gpu_state, after).values())
-    beyond_cpu = sum(v[2] for v in delta_stats(state0_t, cpu_state, after).values())
-    report.sort(key=lambda r: -r[4])
-    print(f"readme fp32: worst GPU gradient/moment error / (3x the fp32 ensemble's, floor 1e-4) {worst:.3f}; "
-          f"delta-policy elements beyond: MI355X "
-          f"{beyond_gpu}, reference fp32 Torch {beyond_cpu}", flush=True)
-    for label, name, gpu_max, cpu_max, gpu_l2, cpu_l2 in report[:6]:
-        print(f"  {label:14s} {name:40s} rel L2 GPU {gpu_l2:.2e} fp32 Torch {cpu_l2:.2e}", flush=True)
-    # bf16-operand mode from the same weights, same inputs, in both activation layouts
+    beyond_cpu = sum(v[2] for v in delta_stats(state0_t, fp32.flat(), after).values())
+    print(f"readme fp32: delta-policy elements beyond (unforced float64 trajectory): MI355X {beyond_gpu}, "
+          f"reference fp32 Torch {beyond_cpu}", flush=True)
+    # bf16-operand mode from the same weights and inputs, in both activation layouts: losses within 1e-2
+    # of the fp32 oracle (north star), and every gradient and moment within max(1e-3, 3x the float32
+    # oracle's error) of the float64 oracle run with the device's bf16 roundings and ReLU decisions
     for bf16_activations in (False, True):
         agent16 = _agent(replace(cfg, use_amp=True), state0, bf16_activations=bf16_activations)
         assert agent16.bf16_activations == bf16_activations
-        metrics16 = _run(agent16, batch, an, nn)
+        worst16, _, _ = forced_update_check(agent16, batch, an, nn, bound=1e-3,
+                                            label=f"readme bf16 (bf16 activations {bf16_activations})")
+        metrics16 = agent16._metrics(True, False)
         for key, value in info.items():
             assert metrics16[key] == pytest.approx(float(value), rel=1e-2, abs=1e-3), (bf16_activations, key)
 

@@ -107,6 +107,10 @@ def test_warp_arrays_follow_the_reference_definition(gpu, tmp_path):
     for key, (shape, dtype) in expected.items():
         assert key in saved, key
         assert saved[key].shape == shape and saved[key].dtype == dtype, (key, saved[key].shape, saved[key].dtype)
+    # the Warp learner draws row i from state i (robolearn/warp/flashsac.py:44-50): distinct states
+    for key in ("rng.actor", "rng.next", "rng.exploration"):
+        assert len(np.unique(saved[key])) == saved[key].size, key
+    np.testing.assert_array_equal(saved["rng.actor"], WC.warp_rng_states(agent.cfg.seed + 11, 2 * B))
     # the module definition agrees with the one the loader validates against
     assert {k: v[0] for k, v in WC.state_keys(agent, include_replay=False).items()
             if not k.startswith("replay.")} == {k: v[0] for k, v in expected.items()}
