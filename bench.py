@@ -54,6 +54,9 @@ WORKLOADS = {
 }
 
 
+BLOCK_STEPS = 20  # graph replays per timing block
+
+
 def gemm_flops(w: dict) -> float:
     """Algorithmic GEMM FLOPs (2 M N K per product) of one actor-phase + one critic-only update.
 
@@ -145,14 +148,35 @@ def measured_counters(kernel: str) -> dict:
 
 
 def cpu_model() -> str:
+    """The host CPU as lscpu names it (model name, family/model/stepping, the BIOS model name when
+    present), falling back to /proc/cpuinfo."""
+    import subprocess
+
+    fields = {}
     try:
-        with open("/proc/cpuinfo") as stream:
-            for line in stream:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            key, _, value = line.partition(":")
+            fields[key.strip()] = value.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return "unknown"
+    name = fields.get("Model name")
+    if not name:
+        try:
+            with open("/proc/cpuinfo") as stream:
+                for line in stream:
+                    if line.startswith("model name"):
+                        name = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    parts = [name or "unknown"]
+    ids = [f"{k.lower()} {fields[k]}" for k in ("CPU family", "Model", "Stepping") if fields.get(k)]
+    if ids:
+        parts.append("(" + ", ".join(ids) + ")")
+    if fields.get("BIOS Model name") and fields["BIOS Model name"] != name:
+        parts.append(f"BIOS model name {fields['BIOS Model name']}")
+    return " ".join(parts)
 
 
 def _median(values):
@@ -654,13 +678,21 @@ def run_flashsac(name: str, steps: int, warmup: int, *, bf16_activations: bool =
     for _ in range(warmup):
         agent.update_pair(tensor_metrics=True)
     torch.cuda.synchronize()
-    start, end = _events()
-    start.record()
-    for _ in range(steps):
+    # timed: exactly `steps` graph replays between two synchronizations, with an event at every block
+    # boundary (blocks of `block` replays, no host wait inside the timed region); ms_per_step is the
+    # whole region's mean, and the median of the block means is reported beside it (the reference
+    # protocol, examples/benchmark_official_flashsac.py:422-429, 654-655)
+    block = max(1, min(BLOCK_STEPS, steps))
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range((steps + block - 1) // block + 1)]
+    marks[0].record()
+    for i in range(steps):
         agent.update_pair(tensor_metrics=True)
-    end.record()
+        if (i + 1) % block == 0 or i + 1 == steps:
+            marks[(i + block) // block].record()
     torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / steps
+    ms_per_step = marks[0].elapsed_time(marks[-1]) / steps
+    sizes = [min(block, steps - j * block) for j in range(len(marks) - 1)]
+    block_means = [marks[j].elapsed_time(marks[j + 1]) / sizes[j] for j in range(len(marks) - 1)]
     bf16 = agent.mode == K.BF16
     act_bytes = 2 if agent.bf16_activations else 4
     flops = gemm_flops(w)
@@ -670,6 +702,9 @@ def run_flashsac(name: str, steps: int, warmup: int, *, bf16_activations: bool =
     result = {
         "workload": f"flashsac_{name}", "updates_per_s": round(2000.0 / ms_per_step, 3),
         "ms_per_step": round(ms_per_step, 4), "steps": steps, "warmup": warmup,
+        "timing": {"block_steps": block, "blocks": len(block_means),
+                   "median_block_ms_per_step": round(_median(block_means), 4),
+                   "block_ms_per_step": [round(v, 4) for v in block_means]},
         "dtype": "bf16" if bf16 else "fp32",
         "batchnorm_activations": "bf16" if agent.bf16_activations else "fp32",
         "update_roofline": {"gemm_tflop_per_step": round(flops / 1e12, 4),
@@ -687,8 +722,8 @@ def run_flashsac(name: str, steps: int, warmup: int, *, bf16_activations: bool =
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--workload", choices=sorted(WORKLOADS), default="g1")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-extras", action="store_true",
@@ -719,7 +754,7 @@ def main() -> int:
 
     others, ppo, sweep = None, None, None
     if not args.no_extras:
-        few = max(5, args.steps // 2)
+        few = max(10, min(50, args.steps // 2))
         others = []
         plans = [("g1", dict(bf16_activations=False)), ("cartpole", {}), ("readme", {}),
                  ("readme", dict(amp=True)), ("readme", dict(amp=True, bf16_activations=False))]
@@ -732,7 +767,7 @@ def main() -> int:
                   f"{line['batchnorm_activations']}): {line['updates_per_s']:.1f} updates/s",
                   file=sys.stderr, flush=True)
         print("[bench] PPO c3 update", file=sys.stderr, flush=True)
-        ppo = bench_ppo(max(5, args.steps // 2), 2)
+        ppo = bench_ppo(max(5, min(20, args.steps // 5)), 2)
         print("[bench] kernel sweep", file=sys.stderr, flush=True)
         sweep = kernel_sweep()
 
@@ -765,6 +800,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": head["ms_per_step"],
+        "timing": head["timing"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -1,22 +1,32 @@
-// bf16 MFMA GEMM for the large dense-layer products: 256x256 output tiles, one
-// workgroup per CU.
+// bf16 MFMA GEMMs for the large dense-layer products: 256x256 output tiles,
+// one persistent workgroup per CU, bf16 operands whose shapes tile exactly
+// (m, n multiples of 256, 16-byte aligned rows).  Same row-major contract as
+// gemm_bf16.hip.  Three kernels:
 //
-// Same row-major contract as gemm_bf16.hip, for bf16 operands whose shapes
-// tile exactly (m, n multiples of 256, K ranges multiples of 64, 16-byte
-// aligned rows).  Designed around the latency of HBM/L2 on CDNA4:
-//   * 4 waves in a 2x2 grid, each owning 128x128 outputs as 4x4
-//     v_mfma_f32_32x32x16_bf16 accumulators (256 accumulator registers), so a
-//     K tile of 32 is 32 MFMAs per wave between barriers;
-//   * global loads run two K tiles ahead through two register stages while
-//     LDS is double-buffered, so a tile's loads have two tiles of MFMA work
-//     (about 2000 cycles) to land;
-//   * workgroups are renumbered so that each XCD (workgroups are dealt to the
-//     8 XCDs round-robin) receives one contiguous run of tiles, walked in
-//     groups of 8 M-tiles, which keeps each XCD's L2 working set to a few
-//     operand panels instead of all of A;
-//   * M/N-contiguous operands (the input- and weight-gradient products) are
-//     loaded as 16-byte vectors along their contiguous dimension and
-//     transposed in registers, so LDS always holds [row][k].
+//   * gemm_wide_kernel (namespace wide), the one that carries the G1 update:
+//     8 waves (two per SIMD) of 128x64 outputs as 4x2
+//     v_mfma_f32_32x32x16_bf16 accumulators; operands move global -> LDS by
+//     global_load_lds_dwordx4 (no register staging) into two 64-deep K stages
+//     of 64 KB, 16-byte chunks XOR-swizzled so each ds_read_b128 phase hits 16
+//     distinct bank groups; fragments of the next 16-deep sub-step are read
+//     (inline-asm ds_read_b128, explicit lgkmcnt waits) under the current
+//     sub-step's MFMAs, and the barrier that publishes K tile k + 1 sits in
+//     K tile k's last sub-step.  Both operands K-contiguous (forward products,
+//     input gradients through transposed weights) or both M/N-contiguous
+//     (weight gradients, fragments from the transposing ds_read_b64_tr_b16).
+//     The next tile's first two K tiles are fetched before the epilogue, which
+//     writes 8 columns per lane as 16/32-byte stores and, for a BatchNorm
+//     input, its per-column chunk moments; the epilogue is instantiated per
+//     output kind so the plain kinds carry no unused branches.
+//   * gemm_dma_kernel: 4 waves of 128x128 outputs, a ring of four 32-deep
+//     DMA stages; the K-contiguous products the wide kernel does not take
+//     (K a multiple of 64 but not 128, or an unaligned bf16 copy of D).
+//   * gemm_big_kernel: 4 waves, register-staged loads with the transposes in
+//     registers, for mixed operand layouts (one K-contiguous, one not).
+//
+// Workgroups are renumbered so that each XCD (workgroups are dealt to the 8
+// XCDs round-robin) receives one contiguous run of tiles, walked in groups of
+// a few M-tiles, which keeps each XCD's L2 working set to a few operand panels.
 #include "gemm.hpp"
 
 #include <algorithm>
