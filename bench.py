@@ -731,6 +731,10 @@ def main() -> int:
     parser.add_argument("--sweep-only", action="store_true",
                         help="run only the configs[4] kernel sweep and print its lines as one JSON object "
                              "(for rocprofv3 counter passes over the sweep kernels)")
+    parser.add_argument("--ppo-only", action="store_true",
+                        help="run only the configs[3] PPO update and print its line as one JSON object")
+    parser.add_argument("--bf16", action="store_true",
+                        help="bf16 operands for the headline workload (configs[1] README runs fp32 by default)")
     parser.add_argument("--calibration-copy-mb", type=int, default=0,
                         help="after timing the dominant kernel, one plain device copy of this size "
                              "(scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -746,9 +750,12 @@ def main() -> int:
     if args.sweep_only:
         print(json.dumps({"kernel_sweep": kernel_sweep()}))
         return 0
+    if args.ppo_only:
+        print(json.dumps({"ppo": bench_ppo(max(5, min(20, args.steps // 5)), 2)}))
+        return 0
     w = WORKLOADS[args.workload]
     head = run_flashsac(args.workload, args.steps, args.warmup, dominant=True,
-                        calibration_copy_mb=args.calibration_copy_mb)
+                        calibration_copy_mb=args.calibration_copy_mb, amp=True if args.bf16 else None)
     print(f"[bench] {args.workload}: {head['ms_per_step']:.3f} ms per step, {head['updates_per_s']:.1f} updates/s",
           file=sys.stderr, flush=True)
 

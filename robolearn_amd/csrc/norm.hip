@@ -21,6 +21,7 @@
 #include <cmath>
 #include <initializer_list>
 #include <mutex>
+#include <type_traits>
 
 namespace rl {
 namespace norm {
@@ -166,12 +167,18 @@ __global__ void bn_apply(const float* x, long long x_stride, const float* mean, 
 }
 
 // Layout of the vectorized elementwise BN kernels: a workgroup covers
-// `tpr` float4 columns x (256 / tpr) row groups, each thread kRowsPerThread rows
-// of one float4 column; per-channel constants are loaded once per thread.
-constexpr int kRowsPerThread = 16;
+// `tpr` float4 columns x (256 / tpr) row groups, each thread `rpt` rows of one
+// float4 column; per-channel constants are loaded once per thread.  A thread
+// issues the loads of all its rows before any arithmetic (rows past the end
+// read the last row and store nothing), so one memory round trip covers them;
+// rpt is 8 where that still gives every CU several workgroups, and shrinks to 2
+// for small layers so that the grid spreads over the GPU instead.
+constexpr int kMaxRowsPerThread = 8;
+constexpr int kMinWorkgroups = 2048;
 
 struct VecLayout {
     int tpr;    // threads per row (float4 columns per workgroup)
+    int rpt;    // rows per thread: 2, 4 or 8
     dim3 grid;
 };
 
@@ -180,8 +187,11 @@ inline VecLayout vec_layout(long long rows, int channels, int ensemble) {
     int tpr = 1;
     while (tpr < cols4 && tpr < 256) tpr *= 2;
     const long long groups = 256 / tpr;
-    const long long row_blocks = (rows + groups * kRowsPerThread - 1) / (groups * kRowsPerThread);
-    return VecLayout{tpr, dim3(ceil_div(cols4, tpr), static_cast<unsigned>(row_blocks), ensemble)};
+    const long long col_blocks = ceil_div(cols4, tpr);
+    int rpt = kMaxRowsPerThread;
+    const auto row_blocks = [&](int r) { return (rows + groups * r - 1) / (groups * r); };
+    while (rpt > 2 && col_blocks * row_blocks(rpt) * ensemble < kMinWorkgroups) rpt /= 2;
+    return VecLayout{tpr, rpt, dim3(static_cast<unsigned>(col_blocks), static_cast<unsigned>(row_blocks(rpt)), ensemble)};
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
@@ -205,8 +215,8 @@ __device__ __forceinline__ void st4_bf16(unsigned short* p, float4 v) {
 }
 
 // bn_apply for channels % 4 == 0 with 16-byte aligned rows; XT is float or
-// unsigned short (bf16 bits, rows 8-byte aligned).
-template <typename XT>
+// unsigned short (bf16 bits, rows 8-byte aligned).  RPT rows per thread.
+template <typename XT, int RPT>
 __global__ __launch_bounds__(256) void bn_apply_vec(const XT* x, long long x_stride, const float* mean,
                                                     const float* var, const float* w, const float* b,
                                                     const float* residual, float* y, unsigned short* y_bf16,
@@ -215,28 +225,31 @@ __global__ __launch_bounds__(256) void bn_apply_vec(const XT* x, long long x_str
     const int q = blockIdx.x * tpr + threadIdx.x % tpr;  // float4 column
     if (4 * q >= channels) return;
     const int groups = 256 / tpr;
-    const long long r0 = static_cast<long long>(blockIdx.y) * groups * kRowsPerThread + threadIdx.x / tpr;
+    const long long r0 = static_cast<long long>(blockIdx.y) * groups * RPT + threadIdx.x / tpr;
     const int c = 4 * q;
+    const XT* xe = x + e * x_stride;
+    const long long out_base = static_cast<long long>(e) * rows * channels;
+    float4 xv[RPT], rv[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const long long i = min(r0 + static_cast<long long>(k) * groups, rows - 1) * channels + c;
+        xv[k] = ld4(xe + i);
+        if (residual) rv[k] = ld4(residual + out_base + i);
+    }
     const int pc = e * channels + c;
     const float4 mu = ld4(mean + pc), va = ld4(var + pc), wv = ld4(w + pc), bv = ld4(b + pc);
     const float4 inv = make_float4(1.0f / sqrtf(va.x + eps), 1.0f / sqrtf(va.y + eps), 1.0f / sqrtf(va.z + eps),
                                    1.0f / sqrtf(va.w + eps));
-    const XT* xe = x + e * x_stride;
-    const long long out_base = static_cast<long long>(e) * rows * channels;
-#pragma unroll 4
-    for (int k = 0; k < kRowsPerThread; ++k) {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
         const long long r = r0 + static_cast<long long>(k) * groups;
         if (r >= rows) break;
         const long long i = r * channels + c;
-        const float4 xv = ld4(xe + i);
-        float4 v = make_float4(bn_value(xv.x, mu.x, inv.x, wv.x, bv.x), bn_value(xv.y, mu.y, inv.y, wv.y, bv.y),
-                               bn_value(xv.z, mu.z, inv.z, wv.z, bv.z), bn_value(xv.w, mu.w, inv.w, wv.w, bv.w));
+        float4 v = make_float4(bn_value(xv[k].x, mu.x, inv.x, wv.x, bv.x), bn_value(xv[k].y, mu.y, inv.y, wv.y, bv.y),
+                               bn_value(xv[k].z, mu.z, inv.z, wv.z, bv.z), bn_value(xv[k].w, mu.w, inv.w, wv.w, bv.w));
         if (relu) v = make_float4(v.x > 0.0f ? v.x : 0.0f, v.y > 0.0f ? v.y : 0.0f, v.z > 0.0f ? v.z : 0.0f,
                                   v.w > 0.0f ? v.w : 0.0f);
-        if (residual) {
-            const float4 rv = ld4(residual + out_base + i);
-            v = make_float4(v.x + rv.x, v.y + rv.y, v.z + rv.z, v.w + rv.w);
-        }
+        if (residual) v = make_float4(v.x + rv[k].x, v.y + rv[k].y, v.z + rv[k].z, v.w + rv[k].w);
         if (y) st4(y + out_base + i, v);
         if (y_bf16) st4_bf16(y_bf16 + out_base + i, v);
     }
@@ -244,8 +257,9 @@ __global__ __launch_bounds__(256) void bn_apply_vec(const XT* x, long long x_str
 
 // bn_grad_apply for channels % 4 == 0 with 16-byte aligned rows; x and dy are
 // float or bf16 bits (XT, DT).  dx_bf16 may alias a bf16 dy: each element is
-// read and written by the same thread.
-template <typename XT, typename DT>
+// read and written by the same thread, and every read comes first.  RPT rows
+// per thread, all loads issued before any arithmetic.
+template <typename XT, typename DT, int RPT>
 __global__ __launch_bounds__(256) void bn_grad_apply_vec(const XT* x, long long x_stride, const DT* dy,
                                                          const float* y, const float* w, const float* b,
                                                          const float* mean, const float* var, const float* sums,
@@ -256,8 +270,19 @@ __global__ __launch_bounds__(256) void bn_grad_apply_vec(const XT* x, long long 
     const int q = blockIdx.x * tpr + threadIdx.x % tpr;
     if (4 * q >= channels) return;
     const int groups = 256 / tpr;
-    const long long r0 = static_cast<long long>(blockIdx.y) * groups * kRowsPerThread + threadIdx.x / tpr;
+    const long long r0 = static_cast<long long>(blockIdx.y) * groups * RPT + threadIdx.x / tpr;
     const int c = 4 * q;
+    const XT* xe = x + e * x_stride;
+    const long long out_base = static_cast<long long>(e) * rows * channels;
+    // x and dy of every row are loaded before any arithmetic; a stored output (reference callers) and
+    // an accumulated dx are read in the loop
+    float4 xv[RPT], g[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const long long i = min(r0 + static_cast<long long>(k) * groups, rows - 1) * channels + c;
+        xv[k] = ld4(xe + i);
+        g[k] = ld4(dy + out_base + i);
+    }
     const int pc = e * channels + c;
     const float4 mu = ld4(mean + pc), va = ld4(var + pc), wv = ld4(w + pc);
     const float4 bv = b ? ld4(b + pc) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -268,34 +293,32 @@ __global__ __launch_bounds__(256) void bn_grad_apply_vec(const XT* x, long long 
         s0 = ld4(sums + pc);
         s1 = ld4(sums + ensemble * channels + pc);
     }
-    const XT* xe = x + e * x_stride;
-    const long long out_base = static_cast<long long>(e) * rows * channels;
     const float4 winv = make_float4(wv.x * inv.x, wv.y * inv.y, wv.z * inv.z, wv.w * inv.w);
-#pragma unroll 4
-    for (int k = 0; k < kRowsPerThread; ++k) {
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
         const long long r = r0 + static_cast<long long>(k) * groups;
         if (r >= rows) break;
         const long long i = r * channels + c;
-        const float4 xv = ld4(xe + i);
-        float4 g = ld4(dy + out_base + i);
+        float4 gk = g[k];
         if (relu) {
-            float4 out;
-            if (y) out = ld4(y + out_base + i);
-            else out = make_float4(bn_value(xv.x, mu.x, inv.x, wv.x, bv.x), bn_value(xv.y, mu.y, inv.y, wv.y, bv.y),
-                                   bn_value(xv.z, mu.z, inv.z, wv.z, bv.z), bn_value(xv.w, mu.w, inv.w, wv.w, bv.w));
-            if (!(out.x > 0.0f)) g.x = 0.0f;
-            if (!(out.y > 0.0f)) g.y = 0.0f;
-            if (!(out.z > 0.0f)) g.z = 0.0f;
-            if (!(out.w > 0.0f)) g.w = 0.0f;
+            const float4 out = y ? ld4(y + out_base + i)
+                                 : make_float4(bn_value(xv[k].x, mu.x, inv.x, wv.x, bv.x),
+                                               bn_value(xv[k].y, mu.y, inv.y, wv.y, bv.y),
+                                               bn_value(xv[k].z, mu.z, inv.z, wv.z, bv.z),
+                                               bn_value(xv[k].w, mu.w, inv.w, wv.w, bv.w));
+            if (!(out.x > 0.0f)) gk.x = 0.0f;
+            if (!(out.y > 0.0f)) gk.y = 0.0f;
+            if (!(out.z > 0.0f)) gk.z = 0.0f;
+            if (!(out.w > 0.0f)) gk.w = 0.0f;
         }
         float4 v;
         if (training) {
-            v = make_float4(winv.x * (g.x - s0.x - (xv.x - mu.x) * inv.x * s1.x),
-                            winv.y * (g.y - s0.y - (xv.y - mu.y) * inv.y * s1.y),
-                            winv.z * (g.z - s0.z - (xv.z - mu.z) * inv.z * s1.z),
-                            winv.w * (g.w - s0.w - (xv.w - mu.w) * inv.w * s1.w));
+            v = make_float4(winv.x * (gk.x - s0.x - (xv[k].x - mu.x) * inv.x * s1.x),
+                            winv.y * (gk.y - s0.y - (xv[k].y - mu.y) * inv.y * s1.y),
+                            winv.z * (gk.z - s0.z - (xv[k].z - mu.z) * inv.z * s1.z),
+                            winv.w * (gk.w - s0.w - (xv[k].w - mu.w) * inv.w * s1.w));
         } else {
-            v = make_float4(winv.x * g.x, winv.y * g.y, winv.z * g.z, winv.w * g.w);
+            v = make_float4(winv.x * gk.x, winv.y * gk.y, winv.z * gk.z, winv.w * gk.w);
         }
         if (accumulate) {
             const float4 o = ld4(dx + out_base + i);
@@ -328,15 +351,19 @@ __global__ __launch_bounds__(kThreads) void bn_moments_vec(const XT* x, long lon
     const int r0 = chunk * kChunk + group;
     const int r_end = min(rows, (chunk + 1) * kChunk);
     const bool live = 4 * q < channels;
-    const XT* base = x + e * x_stride + 4 * q;
+    // every load is issued before any arithmetic: a row or column outside the layer reads the
+    // last valid one and is masked afterwards
+    const XT* base = x + e * x_stride + 4 * (live ? q : channels / 4 - 1);
     float4 v[kVecRows];
+#pragma unroll
+    for (int k = 0; k < kVecRows; ++k)
+        v[k] = ld4(base + static_cast<long long>(min(r0 + k * kVecGroups, r_end - 1)) * channels);
     float count = 0.0f;
     float4 mean = f4(0.0f);
 #pragma unroll
     for (int k = 0; k < kVecRows; ++k) {
-        const int r = r0 + k * kVecGroups;
-        const bool ok = live && r < r_end;
-        v[k] = ok ? ld4(base + static_cast<long long>(r) * channels) : f4(0.0f);
+        const bool ok = live && r0 + k * kVecGroups < r_end;
+        if (!ok) v[k] = f4(0.0f);
         if (ok) {
             count += 1.0f;
             mean = make_float4(mean.x + v[k].x, mean.y + v[k].y, mean.z + v[k].z, mean.w + v[k].w);
@@ -391,33 +418,46 @@ __global__ __launch_bounds__(kThreads) void bn_grad_partials_vec(const XT* x, lo
     const bool live = 4 * q < channels;
     float4 s0 = f4(0.0f), s1 = f4(0.0f);
     if (live) {
+        const XT* xe = x + e * x_stride + 4 * q;
+        const long long off = static_cast<long long>(e) * rows * channels + 4 * q;
         const int pc = e * channels + 4 * q;
         const float4 mu = ld4(mean + pc), va = ld4(var + pc), wv = ld4(w + pc);
         const float4 bv = b ? ld4(b + pc) : f4(0.0f);
         const float4 inv = make_float4(1.0f / sqrtf(va.x + eps), 1.0f / sqrtf(va.y + eps), 1.0f / sqrtf(va.z + eps),
                                        1.0f / sqrtf(va.w + eps));
-        const XT* xe = x + e * x_stride + 4 * q;
-        const long long off = static_cast<long long>(e) * rows * channels + 4 * q;
-#pragma unroll 4
-        for (int k = 0; k < kVecRows; ++k) {
-            const int r = r0 + k * kVecGroups;
-            if (r >= r_end) break;
-            const long long i = static_cast<long long>(r) * channels;
-            const float4 xv = ld4(xe + i);
-            float4 g = ld4(dy + off + i);
-            if (relu) {
-                float4 out;
-                if (y) out = ld4(y + off + i);
-                else out = make_float4(bn_value(xv.x, mu.x, inv.x, wv.x, bv.x), bn_value(xv.y, mu.y, inv.y, wv.y, bv.y),
-                                       bn_value(xv.z, mu.z, inv.z, wv.z, bv.z), bn_value(xv.w, mu.w, inv.w, wv.w, bv.w));
-                if (!(out.x > 0.0f)) g.x = 0.0f;
-                if (!(out.y > 0.0f)) g.y = 0.0f;
-                if (!(out.z > 0.0f)) g.z = 0.0f;
-                if (!(out.w > 0.0f)) g.w = 0.0f;
+        // rows in batches of 8: a batch's x and dy loads are issued before its arithmetic (rows past
+        // the chunk read its last row); a stored output (reference callers) is read in the loop
+        constexpr int kBatch = 8;
+        static_assert(kVecRows % kBatch == 0, "whole batches");
+#pragma unroll
+        for (int k0 = 0; k0 < kVecRows; k0 += kBatch) {
+            float4 xv[kBatch], g[kBatch];
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const long long i = static_cast<long long>(min(r0 + (k0 + k) * kVecGroups, r_end - 1)) * channels;
+                xv[k] = ld4(xe + i);
+                g[k] = ld4(dy + off + i);
             }
-            s0 = make_float4(s0.x + g.x, s0.y + g.y, s0.z + g.z, s0.w + g.w);
-            s1 = make_float4(s1.x + g.x * ((xv.x - mu.x) * inv.x), s1.y + g.y * ((xv.y - mu.y) * inv.y),
-                             s1.z + g.z * ((xv.z - mu.z) * inv.z), s1.w + g.w * ((xv.w - mu.w) * inv.w));
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int r = r0 + (k0 + k) * kVecGroups;
+                if (r >= r_end) break;
+                float4 gk = g[k];
+                if (relu) {
+                    const float4 out = y ? ld4(y + off + static_cast<long long>(r) * channels)
+                                         : make_float4(bn_value(xv[k].x, mu.x, inv.x, wv.x, bv.x),
+                                                       bn_value(xv[k].y, mu.y, inv.y, wv.y, bv.y),
+                                                       bn_value(xv[k].z, mu.z, inv.z, wv.z, bv.z),
+                                                       bn_value(xv[k].w, mu.w, inv.w, wv.w, bv.w));
+                    if (!(out.x > 0.0f)) gk.x = 0.0f;
+                    if (!(out.y > 0.0f)) gk.y = 0.0f;
+                    if (!(out.z > 0.0f)) gk.z = 0.0f;
+                    if (!(out.w > 0.0f)) gk.w = 0.0f;
+                }
+                s0 = make_float4(s0.x + gk.x, s0.y + gk.y, s0.z + gk.z, s0.w + gk.w);
+                s1 = make_float4(s1.x + gk.x * ((xv[k].x - mu.x) * inv.x), s1.y + gk.y * ((xv[k].y - mu.y) * inv.y),
+                                 s1.z + gk.z * ((xv[k].z - mu.z) * inv.z), s1.w + gk.w * ((xv[k].w - mu.w) * inv.w));
+            }
         }
     }
     __shared__ float4 sa[kThreads], sb[kThreads];
@@ -930,14 +970,19 @@ void bn_forward(int ensemble, const void* x, int x_bf16, long long x_stride, con
     require(vec || !x_bf16, "bf16 BatchNorm input needs channels and strides in multiples of 4 and aligned buffers.");
     if (vec) {
         const norm::VecLayout layout = norm::vec_layout(rows, channels, ensemble);
-        if (x_bf16)
-            hipLaunchKernelGGL(norm::bn_apply_vec<unsigned short>, layout.grid, dim3(256), 0, stream,
-                               static_cast<const unsigned short*>(x), x_stride, use_mean, use_var, w, b, residual, y,
-                               y_bf16, static_cast<long long>(rows), channels, eps, relu, layout.tpr);
-        else
-            hipLaunchKernelGGL(norm::bn_apply_vec<float>, layout.grid, dim3(256), 0, stream,
-                               static_cast<const float*>(x), x_stride, use_mean, use_var, w, b, residual, y, y_bf16,
+        const auto launch = [&](auto xt, auto rpt) {
+            using XT = decltype(xt);
+            hipLaunchKernelGGL((norm::bn_apply_vec<XT, decltype(rpt)::value>), layout.grid, dim3(256), 0, stream,
+                               static_cast<const XT*>(x), x_stride, use_mean, use_var, w, b, residual, y, y_bf16,
                                static_cast<long long>(rows), channels, eps, relu, layout.tpr);
+        };
+        const auto by_rows = [&](auto xt) {
+            if (layout.rpt == 8) launch(xt, std::integral_constant<int, 8>{});
+            else if (layout.rpt == 4) launch(xt, std::integral_constant<int, 4>{});
+            else launch(xt, std::integral_constant<int, 2>{});
+        };
+        if (x_bf16) by_rows((unsigned short)0);
+        else by_rows(0.0f);
     } else {
         hipLaunchKernelGGL(norm::bn_apply, dim3(norm::elementwise_blocks(total)), dim3(256), 0, stream,
                            static_cast<const float*>(x), x_stride, use_mean, use_var, w, b, residual, y, y_bf16,
@@ -1000,13 +1045,18 @@ void bn_backward(int ensemble, const void* x, int x_bf16, long long x_stride, co
         require(vec || !narrow, "bf16 BatchNorm backward outputs need aligned buffers and 4-aligned statistics.");
         if (vec) {
             const norm::VecLayout layout = norm::vec_layout(rows, channels, ensemble);
-            const auto launch = [&](auto xt, auto dt) {
+            const auto launch_rows = [&](auto xt, auto dt, auto rpt) {
                 using XT = decltype(xt);
                 using DT = decltype(dt);
-                hipLaunchKernelGGL((norm::bn_grad_apply_vec<XT, DT>), layout.grid, dim3(256), 0, stream,
-                                   static_cast<const XT*>(x), x_stride, static_cast<const DT*>(dy), y, w, b, mean, var,
-                                   sums, dx, dx_bf16, static_cast<long long>(rows), channels, ensemble, eps, training,
-                                   relu, accumulate_dx, layout.tpr);
+                hipLaunchKernelGGL((norm::bn_grad_apply_vec<XT, DT, decltype(rpt)::value>), layout.grid, dim3(256), 0,
+                                   stream, static_cast<const XT*>(x), x_stride, static_cast<const DT*>(dy), y, w, b,
+                                   mean, var, sums, dx, dx_bf16, static_cast<long long>(rows), channels, ensemble, eps,
+                                   training, relu, accumulate_dx, layout.tpr);
+            };
+            const auto launch = [&](auto xt, auto dt) {
+                if (layout.rpt == 8) launch_rows(xt, dt, std::integral_constant<int, 8>{});
+                else if (layout.rpt == 4) launch_rows(xt, dt, std::integral_constant<int, 4>{});
+                else launch_rows(xt, dt, std::integral_constant<int, 2>{});
             };
             if (x_bf16 && dy_bf16) launch((unsigned short)0, (unsigned short)0);
             else if (x_bf16) launch((unsigned short)0, 0.0f);
