@@ -28,8 +28,6 @@ namespace norm {
 
 constexpr int kChunk = 256;
 constexpr int kThreads = 256;
-constexpr int kCols = 64;
-constexpr int kRowGroups = kThreads / kCols;
 
 // Normalized affine value; forward apply and the backward ReLU-mask recompute
 // both call this, so the mask is bitwise identical to the forward decision.
@@ -53,39 +51,85 @@ __device__ __forceinline__ void merge(float& count, float& mean, float& m2, floa
     count = total;
 }
 
-// partial[e][chunk][0..1][c] = (mean, m2) of the chunk's rows.
+// Per-column layout of the scalar BN passes (channels not a multiple of 4):
+// Cols columns per workgroup and kThreads / Cols row groups, so that narrow
+// layers (an embedder over a handful of observations) still spread a 256-row
+// chunk over the whole workgroup.
+inline int scalar_cols(int channels) { return channels >= 64 ? 64 : channels >= 16 ? 16 : channels >= 4 ? 4 : 1; }
+
+// Fixed-order tree over the row groups of a workgroup: after it, group 0 of
+// each column holds the merge of all groups (pairs g, g + stride, stride
+// halving), for (count, mean, m2) triples in LDS.
+template <int Cols>
+__device__ __forceinline__ void tree_merge(float* s_count, float* s_mean, float* s_m2) {
+    constexpr int Groups = kThreads / Cols;
+    const int group = threadIdx.x / Cols;
+#pragma unroll
+    for (int stride = Groups / 2; stride > 0; stride >>= 1) {
+        __syncthreads();
+        if (group < stride) {
+            const int t = threadIdx.x, u = threadIdx.x + stride * Cols;
+            float count = s_count[t], mean = s_mean[t], m2 = s_m2[t];
+            merge(count, mean, m2, s_count[u], s_mean[u], s_m2[u]);
+            s_count[t] = count;
+            s_mean[t] = mean;
+            s_m2[t] = m2;
+        }
+    }
+    __syncthreads();
+}
+
+// partial[e][chunk][0..1][c] = (mean, m2) of the chunk's rows.  Every load of a
+// thread's rows is issued first (rows past the chunk and columns past the layer
+// read the last valid ones and are masked), then a two-pass mean / M2.
+template <int Cols>
 __global__ __launch_bounds__(kThreads) void bn_moments(const float* x, long long x_stride, float* partial, int rows,
                                                        int channels, int chunks) {
+    constexpr int Groups = kThreads / Cols;
+    constexpr int Rows = kChunk / Groups;
     const int e = blockIdx.z;
-    const int c = blockIdx.x * kCols + threadIdx.x % kCols;
-    const int group = threadIdx.x / kCols;
+    const int c = blockIdx.x * Cols + threadIdx.x % Cols;
+    const int group = threadIdx.x / Cols;
     const int chunk = blockIdx.y;
-    const int r0 = chunk * kChunk;
-    const int r1 = min(rows, r0 + kChunk);
-    const float* base = x + e * x_stride;
-    float count = 0.0f, mean = 0.0f, m2 = 0.0f;
-    if (c < channels) {
-        for (int r = r0 + group; r < r1; r += kRowGroups) {
-            const float v = base[static_cast<long long>(r) * channels + c];
-            count += 1.0f;
-            const float delta = v - mean;
-            mean += delta / count;
-            m2 += delta * (v - mean);
+    const int r0 = chunk * kChunk + group;
+    const int r_end = min(rows, (chunk + 1) * kChunk);
+    const bool live = c < channels;
+    const float* base = x + e * x_stride + (live ? c : channels - 1);
+    // shifted sums (shift: the thread's first row), rows in batches of up to 16 whose loads are issued
+    // before their arithmetic; rows past the chunk and columns past the layer read the last valid ones
+    constexpr int Batch = Rows < 16 ? Rows : 16;
+    const float shift = base[static_cast<long long>(min(r0, r_end - 1)) * channels];
+    float count = 0.0f, s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int k0 = 0; k0 < Rows; k0 += Batch) {
+        float v[Batch];
+#pragma unroll
+        for (int k = 0; k < Batch; ++k)
+            v[k] = base[static_cast<long long>(min(r0 + (k0 + k) * Groups, r_end - 1)) * channels];
+#pragma unroll
+        for (int k = 0; k < Batch; ++k) {
+            if (live && r0 + (k0 + k) * Groups < r_end) {
+                const float d = v[k] - shift;
+                count += 1.0f;
+                s1 += d;
+                s2 += d * d;
+            }
         }
+    }
+    float mean = 0.0f, m2 = 0.0f;
+    if (count > 0.0f) {
+        mean = shift + s1 / count;
+        m2 = fmaxf(s2 - s1 * (s1 / count), 0.0f);
     }
     __shared__ float s_count[kThreads], s_mean[kThreads], s_m2[kThreads];
     s_count[threadIdx.x] = count;
     s_mean[threadIdx.x] = mean;
     s_m2[threadIdx.x] = m2;
-    __syncthreads();
-    if (group == 0 && c < channels) {
-        for (int g = 1; g < kRowGroups; ++g) {
-            const int t = g * kCols + threadIdx.x;
-            merge(count, mean, m2, s_count[t], s_mean[t], s_m2[t]);
-        }
+    tree_merge<Cols>(s_count, s_mean, s_m2);
+    if (group == 0 && live) {
         float* out = partial + (static_cast<long long>(e) * chunks + chunk) * 2 * channels;
-        out[c] = mean;
-        out[channels + c] = m2;
+        out[c] = s_mean[threadIdx.x];
+        out[channels + c] = s_m2[threadIdx.x];
     }
 }
 
@@ -477,49 +521,71 @@ __global__ __launch_bounds__(kThreads) void bn_grad_partials_vec(const XT* x, lo
 }
 
 // Backward partial sums per chunk: sum(dy'), sum(dy' * xhat) with dy' the
-// ReLU-masked output gradient.
+// ReLU-masked output gradient (scalar path, Cols columns per workgroup as
+// bn_moments; loads issued first, a fixed-order tree over the row groups).
+template <int Cols>
 __global__ __launch_bounds__(kThreads) void bn_grad_partials(const float* x, long long x_stride, const float* dy,
                                                              const float* y, const float* w, const float* b,
                                                              const float* mean, const float* var, float* partial,
                                                              int rows, int channels, int chunks, float eps, int relu) {
+    constexpr int Groups = kThreads / Cols;
+    constexpr int Rows = kChunk / Groups;
     const int e = blockIdx.z;
-    const int c = blockIdx.x * kCols + threadIdx.x % kCols;
-    const int group = threadIdx.x / kCols;
+    const int c = blockIdx.x * Cols + threadIdx.x % Cols;
+    const int group = threadIdx.x / Cols;
     const int chunk = blockIdx.y;
-    const int r0 = chunk * kChunk;
-    const int r1 = min(rows, r0 + kChunk);
-    const long long off = static_cast<long long>(e) * rows * channels;
+    const int r0 = chunk * kChunk + group;
+    const int r_end = min(rows, (chunk + 1) * kChunk);
+    const bool live = c < channels;
+    const int cc = live ? c : channels - 1;
+    const long long off = static_cast<long long>(e) * rows * channels + cc;
+    const float* xe = x + e * x_stride + cc;
     float s0 = 0.0f, s1 = 0.0f;
-    if (c < channels) {
-        const int pc = e * channels + c;
-        const float mu = mean[pc];
-        const float inv = 1.0f / sqrtf(var[pc] + eps);
-        const float wc = w[pc];
-        const float bc = b ? b[pc] : 0.0f;
-        for (int r = r0 + group; r < r1; r += kRowGroups) {
-            const long long i = static_cast<long long>(r) * channels + c;
-            const float xv = x[e * x_stride + i];
-            float g = dy[off + i];
+    const int pc = e * channels + cc;
+    const float mu = mean[pc];
+    const float inv = 1.0f / sqrtf(var[pc] + eps);
+    const float wc = w[pc];
+    const float bc = b ? b[pc] : 0.0f;
+    // rows in batches of up to 16 whose loads are issued before their arithmetic
+    constexpr int Batch = Rows < 16 ? Rows : 16;
+#pragma unroll
+    for (int k0 = 0; k0 < Rows; k0 += Batch) {
+        float xv[Batch], g[Batch];
+#pragma unroll
+        for (int k = 0; k < Batch; ++k) {
+            const long long i = static_cast<long long>(min(r0 + (k0 + k) * Groups, r_end - 1)) * channels;
+            xv[k] = xe[i];
+            g[k] = dy[off + i];
+        }
+#pragma unroll
+        for (int k = 0; k < Batch; ++k) {
+            const int r = r0 + (k0 + k) * Groups;
+            if (!live || r >= r_end) break;
+            float gk = g[k];
             if (relu) {
-                const float out = y ? y[off + i] : bn_value(xv, mu, inv, wc, bc);
-                if (!(out > 0.0f)) g = 0.0f;
+                const float out = y ? y[off + static_cast<long long>(r) * channels] : bn_value(xv[k], mu, inv, wc, bc);
+                if (!(out > 0.0f)) gk = 0.0f;
             }
-            s0 += g;
-            s1 += g * ((xv - mu) * inv);
+            s0 += gk;
+            s1 += gk * ((xv[k] - mu) * inv);
         }
     }
     __shared__ float sa[kThreads], sb[kThreads];
     sa[threadIdx.x] = s0;
     sb[threadIdx.x] = s1;
-    __syncthreads();
-    if (group == 0 && c < channels) {
-        for (int g = 1; g < kRowGroups; ++g) {
-            s0 += sa[g * kCols + threadIdx.x];
-            s1 += sb[g * kCols + threadIdx.x];
+#pragma unroll
+    for (int stride = Groups / 2; stride > 0; stride >>= 1) {
+        __syncthreads();
+        if (group < stride) {
+            sa[threadIdx.x] += sa[threadIdx.x + stride * Cols];
+            sb[threadIdx.x] += sb[threadIdx.x + stride * Cols];
         }
+    }
+    __syncthreads();
+    if (group == 0 && live) {
         float* out = partial + (static_cast<long long>(e) * chunks + chunk) * 2 * channels;
-        out[c] = s0;
-        out[channels + c] = s1;
+        out[c] = sa[threadIdx.x];
+        out[channels + c] = sb[threadIdx.x];
     }
 }
 
@@ -835,20 +901,37 @@ __global__ __launch_bounds__(kThreads) void column_partials(const float* dy, con
                                                             float* partial, int rows, int channels, int chunks,
                                                             long long member_stride, float eps, int mode) {
     constexpr int Groups = kThreads / Cols;
+    constexpr int Rows = kChunk / Groups;
     const int e = blockIdx.z;
     const int c = blockIdx.x * Cols + threadIdx.x % Cols;
     const int group = threadIdx.x / Cols;
     const int chunk = blockIdx.y;
-    const int r0 = chunk * kChunk;
-    const int r1 = min(rows, r0 + kChunk);
-    const long long off = static_cast<long long>(e) * member_stride;
+    const int r0 = chunk * kChunk + group;
+    const int r_end = min(rows, (chunk + 1) * kChunk);
+    const bool live = c < channels;
+    const long long off = static_cast<long long>(e) * member_stride + (live ? c : channels - 1);
+    // rows in batches of up to 16 whose loads are issued before the sums (rows past the chunk read its
+    // last row)
+    constexpr int Batch = Rows < 16 ? Rows : 16;
     float s = 0.0f;
-    if (c < channels) {
-#pragma unroll 4
-        for (int r = r0 + group; r < r1; r += Groups) {
-            const long long i = off + static_cast<long long>(r) * channels + c;
-            if (mode == 0) s += dy[i];
-            else s += dy[i] * x[i] * (1.0f / sqrtf(ms[static_cast<long long>(e) * rows + r] + eps));
+#pragma unroll
+    for (int k0 = 0; k0 < Rows; k0 += Batch) {
+        float d[Batch], xv[Batch], m[Batch];
+#pragma unroll
+        for (int k = 0; k < Batch; ++k) {
+            const int r = min(r0 + (k0 + k) * Groups, r_end - 1);
+            const long long i = off + static_cast<long long>(r) * channels;
+            d[k] = dy[i];
+            if (mode != 0) {
+                xv[k] = x[i];
+                m[k] = ms[static_cast<long long>(e) * rows + r];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < Batch; ++k) {
+            if (!live || r0 + (k0 + k) * Groups >= r_end) break;
+            if (mode == 0) s += d[k];
+            else s += d[k] * xv[k] * (1.0f / sqrtf(m[k] + eps));
         }
     }
     __shared__ float a[kThreads];
@@ -859,7 +942,7 @@ __global__ __launch_bounds__(kThreads) void column_partials(const float* dy, con
         if (group < stride) a[threadIdx.x] += a[threadIdx.x + stride * Cols];
         __syncthreads();
     }
-    if (group == 0 && c < channels) partial[(static_cast<long long>(e) * chunks + chunk) * channels + c] = a[threadIdx.x];
+    if (group == 0 && live) partial[(static_cast<long long>(e) * chunks + chunk) * channels + c] = a[threadIdx.x];
 }
 
 // One wave per output column: lanes stride over the chunk partials, then a
@@ -883,7 +966,10 @@ inline void column_sums(const float* dy, const float* x, const float* ms, float*
                         int channels, int ensemble, long long member_stride, float eps, int mode, int accumulate,
                         hipStream_t stream) {
     const int chunks = (rows + kChunk - 1) / kChunk;
-    const int cols = channels >= 64 ? 64 : channels >= 16 ? 16 : channels >= 4 ? 4 : 1;
+    // 64 columns per workgroup where that still gives every CU a workgroup, else narrower blocks
+    // (more workgroups, each thread fewer rows)
+    int cols = channels >= 64 ? 64 : channels >= 16 ? 16 : channels >= 4 ? 4 : 1;
+    while (cols > 4 && static_cast<long long>(ceil_div(channels, cols)) * chunks * ensemble < 256) cols /= 4;
     const dim3 grid(ceil_div(channels, cols), chunks, ensemble);
     switch (cols) {
         case 64:
@@ -931,9 +1017,21 @@ void bn_chunk_moments(int ensemble, const void* x, int x_bf16, long long x_strid
         hipLaunchKernelGGL(norm::bn_moments_vec<float>, vec_grid, dim3(norm::kThreads), 0, stream,
                            static_cast<const float*>(x), x_stride, partial, rows, channels, chunks);
     } else {
-        const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
-        hipLaunchKernelGGL(norm::bn_moments, grid, dim3(norm::kThreads), 0, stream, static_cast<const float*>(x),
-                           x_stride, partial, rows, channels, chunks);
+        const int cols = norm::scalar_cols(channels);
+        const dim3 grid(ceil_div(channels, cols), chunks, ensemble);
+        const float* xf = static_cast<const float*>(x);
+        if (cols == 64)
+            hipLaunchKernelGGL(norm::bn_moments<64>, grid, dim3(norm::kThreads), 0, stream, xf, x_stride, partial, rows,
+                               channels, chunks);
+        else if (cols == 16)
+            hipLaunchKernelGGL(norm::bn_moments<16>, grid, dim3(norm::kThreads), 0, stream, xf, x_stride, partial, rows,
+                               channels, chunks);
+        else if (cols == 4)
+            hipLaunchKernelGGL(norm::bn_moments<4>, grid, dim3(norm::kThreads), 0, stream, xf, x_stride, partial, rows,
+                               channels, chunks);
+        else
+            hipLaunchKernelGGL(norm::bn_moments<1>, grid, dim3(norm::kThreads), 0, stream, xf, x_stride, partial, rows,
+                               channels, chunks);
     }
     check_launch("Launch BN moments");
 }
@@ -1027,10 +1125,17 @@ void bn_backward(int ensemble, const void* x, int x_bf16, long long x_stride, co
             else if (dy_bf16) launch(0.0f, (unsigned short)0);
             else launch(0.0f, 0.0f);
         } else {
-            const dim3 grid(ceil_div(channels, norm::kCols), chunks, ensemble);
-            hipLaunchKernelGGL(norm::bn_grad_partials, grid, dim3(norm::kThreads), 0, stream,
-                               static_cast<const float*>(x), x_stride, static_cast<const float*>(dy), y, w, b, mean,
-                               var, partial, rows, channels, chunks, eps, relu);
+            const int cols = norm::scalar_cols(channels);
+            const dim3 grid(ceil_div(channels, cols), chunks, ensemble);
+            const auto launch = [&](auto cols_const) {
+                hipLaunchKernelGGL((norm::bn_grad_partials<decltype(cols_const)::value>), grid, dim3(norm::kThreads),
+                                   0, stream, static_cast<const float*>(x), x_stride, static_cast<const float*>(dy), y,
+                                   w, b, mean, var, partial, rows, channels, chunks, eps, relu);
+            };
+            if (cols == 64) launch(std::integral_constant<int, 64>{});
+            else if (cols == 16) launch(std::integral_constant<int, 16>{});
+            else if (cols == 4) launch(std::integral_constant<int, 4>{});
+            else launch(std::integral_constant<int, 1>{});
         }
         check_launch("Launch BN gradient partials");
         hipLaunchKernelGGL(norm::bn_grad_reduce, dim3(ceil_div(ensemble * channels, norm::kStatCols)),

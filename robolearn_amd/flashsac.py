@@ -218,6 +218,7 @@ class FlashSAC:
                                     bf16_activations=bf16_activations)
             self.bf16_activations = bf and bf16_activations
             self.workspace = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+            self.actor_net.workspace = self.critic_net.workspace = self.workspace
             z = lambda *s: torch.zeros(*s, device=dev)  # noqa: E731
             self.batch = {"observation": z(B, Oc), "action": z(B, A), "reward": z(B), "terminated": z(B),
                           "truncated": z(B), "next_observation": z(B, Oc), "discount": z(B)}

@@ -67,14 +67,36 @@ def gemm(
 
 
 def forward_split_count(m, n, k, batch, mode):
-    """K splits for a product whose output tiles cannot fill the GPU (a narrow
-    head over a long K): at least 256 workgroups, each split >= 256 of K."""
-    tm = 256 if mode == BF16 else 128
-    tiles = ((m + tm - 1) // tm) * ((n + 127) // 128) * batch
-    ktiles = (k + 31) // 32
+    """K splits for a forward or input-gradient product whose output tiles cannot fill the GPU (a
+    narrow head, or a narrow layer over a long K at a small batch).
+
+    bf16 (the heads): 256x128 tiles, at least 256 workgroups, each split >= 256 of K.  A bf16 block
+    product is not split even where its tiles leave CUs idle (README shape): the split loses the
+    BatchNorm moments of the 256x256 kernel's epilogue and adds a reduction, which measured slower.
+    fp32: 64x64 tiles, whose K loop is latency-bound when few workgroups share a CU; at least 1024
+    workgroups, each split >= 128 of K (four 32-deep steps)."""
     splits = 1
-    while tiles * splits < 256 and splits * 2 <= max(1, ktiles // 8) and splits < 16:
+    if mode == BF16:
+        tiles = ((m + 255) // 256) * ((n + 127) // 128) * batch
+        ktiles = (k + 31) // 32
+        while tiles * splits < 256 and splits * 2 <= max(1, ktiles // 8) and splits < 16:
+            splits *= 2
+        return splits
+    tiles = ((m + 63) // 64) * ((n + 63) // 64) * batch
+    while tiles * splits < 1024 and k // (2 * splits) >= 128 and splits < 16:
         splits *= 2
+    return splits
+
+
+def _split_for(m, n, k, batch, mode, workspace):
+    """forward_split_count, limited to what the workspace holds (1 without one)."""
+    if workspace is None:
+        return 1
+    splits = forward_split_count(m, n, k, batch, mode)
+    if splits > 1:
+        need = _native.load().rl_gemm_workspace(mode, m, n, k, batch, splits)
+        if need > workspace.numel() * workspace.element_size():
+            splits = 1
     return splits
 
 
@@ -89,11 +111,7 @@ def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None,
         x_stride = rows * x_ld
     _check(w, ensemble * out_dim * in_dim, "weight", w.dtype)
     _check(y, ensemble * rows * out_dim, "output", y.dtype)
-    splits = forward_split_count(rows, out_dim, in_dim, ensemble, mode) if workspace is not None else 1
-    if splits > 1:
-        need = _native.load().rl_gemm_workspace(mode, rows, out_dim, in_dim, ensemble, splits)
-        if need > workspace.numel() * workspace.element_size():
-            splits = 1
+    splits = _split_for(rows, out_dim, in_dim, ensemble, mode, workspace)
     gemm(x, w, y, m=rows, n=out_dim, k=in_dim, batch=ensemble, a_kcontig=True, b_kcontig=True, lda=x_ld,
          ldb=in_dim, ldd=out_dim, stride_a=x_stride, stride_b=out_dim * in_dim, stride_d=rows * out_dim, bias=bias,
          stride_bias=out_dim, epilogue=epilogue, mode=mode, c=c, beta=beta, d_bf16=d_bf16, moments=moments,
@@ -101,20 +119,23 @@ def linear_forward(x, w, y, *, rows, in_dim, out_dim, ensemble=1, x_stride=None,
 
 
 def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=FP32, c=None, beta=0.0,
-                          d_bf16=None, wt=None, epilogue=None):
+                          d_bf16=None, wt=None, epilogue=None, workspace=None):
     """dx[e] = dy[e] w[e] (+ beta c).  wt: optional [ensemble, in_dim, out_dim] transposed copy of w,
     which lets both operands be read K-contiguously.  epilogue "elu_grad" (fp32) multiplies by
-    elu'(c), c holding the ELU outputs of the layer below."""
+    elu'(c), c holding the ELU outputs of the layer below.  With a workspace, a product too small
+    to fill the GPU is split over K (fixed-order reduction)."""
     _check(dx, ensemble * rows * in_dim, "input gradient", dx.dtype)
+    splits = _split_for(rows, in_dim, out_dim, ensemble, mode, workspace)
+    ws = workspace if splits > 1 else None
     if wt is not None:
         _check(wt, ensemble * out_dim * in_dim, "transposed weight", wt.dtype)
         gemm(dy, wt, dx, m=rows, n=in_dim, k=out_dim, batch=ensemble, a_kcontig=True, b_kcontig=True, lda=out_dim,
              ldb=out_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=out_dim * in_dim, stride_d=rows * in_dim,
-             mode=mode, c=c, beta=beta, d_bf16=d_bf16)
+             mode=mode, c=c, beta=beta, d_bf16=d_bf16, splits=splits, workspace=ws)
         return
     gemm(dy, w, dx, m=rows, n=in_dim, k=out_dim, batch=ensemble, a_kcontig=True, b_kcontig=False, lda=out_dim,
          ldb=in_dim, ldd=in_dim, stride_a=rows * out_dim, stride_b=out_dim * in_dim, stride_d=rows * in_dim,
-         mode=mode, c=c, beta=beta, d_bf16=d_bf16, epilogue=epilogue)
+         mode=mode, c=c, beta=beta, d_bf16=d_bf16, epilogue=epilogue, splits=splits, workspace=ws)
 
 
 def transpose16(src, dst, *, batch, rows, cols):

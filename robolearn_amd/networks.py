@@ -231,6 +231,9 @@ class Trunk:
         self.bf = mode == K.BF16
         self.linear = prefix_linear  # name suffix of unit-linear weights (".w.weight" actor, ".weight" critic)
         E, R, h = ensemble, max_rows, hidden
+        # split-K partial sums for fp32 block products whose tile grid cannot fill the GPU (set by the
+        # owner; bf16 block products keep their fused BatchNorm moments instead)
+        self.workspace = None
 
         def buf(*shape):
             return torch.zeros(*shape, device=device)
@@ -315,14 +318,16 @@ class Trunk:
             # in training the GEMM also writes the BatchNorm's chunk moments of its output
             moments = self.partial if training else None
             K.linear_forward(self.op(self.stream[i], self.stream_h[i]), w[f"{pre}.w1{self.linear}"], self.u1[i],
-                             rows=rows, in_dim=h, out_dim=4 * h, ensemble=E, mode=mode, moments=moments)
+                             rows=rows, in_dim=h, out_dim=4 * h, ensemble=E, mode=mode, moments=moments,
+                             workspace=None if self.bf else self.workspace)
             mean, var = self.stats[pre + ".norm1"]
             K.bn_forward(self.u1[i], p[pre + ".norm1.weight"], p[pre + ".norm1.bias"],
                          running[pre + ".norm1.running_mean"], running[pre + ".norm1.running_var"], mean, var,
                          self.partial, self.r1[i], rows=rows, channels=4 * h, ensemble=E, training=training,
                          relu=True, update_running=update_running, y_bf16=self.r1_h[i], moments_ready=training)
             K.linear_forward(self.op(self.r1[i], self.r1_h[i]), w[f"{pre}.w2{self.linear}"], self.u2[i], rows=rows,
-                             in_dim=4 * h, out_dim=h, ensemble=E, mode=mode, moments=moments)
+                             in_dim=4 * h, out_dim=h, ensemble=E, mode=mode, moments=moments,
+                             workspace=None if self.bf else self.workspace)
             mean, var = self.stats[pre + ".norm2"]
             K.bn_forward(self.u2[i], p[pre + ".norm2.weight"], p[pre + ".norm2.bias"],
                          running[pre + ".norm2.running_mean"], running[pre + ".norm2.running_var"], mean, var,
@@ -373,7 +378,8 @@ class Trunk:
                           training=training, relu=True, b=p[pre + ".norm2.bias"], dx_bf16=self.d_u2_h)
             d_u2 = self.op(self.d_u2, self.d_u2_h)
             K.linear_backward_input(d_u2, w[f"{pre}.w2{self.linear}"], self.d_r1, rows=rows, in_dim=4 * h,
-                                    out_dim=h, ensemble=E, mode=mode, wt=wt.get(f"{pre}.w2{self.linear}"))
+                                    out_dim=h, ensemble=E, mode=mode, wt=wt.get(f"{pre}.w2{self.linear}"),
+                                    workspace=None if self.bf else workspace)
             if g is not None:
                 K.linear_backward_weight(d_u2, self.op(self.r1[i], self.r1_h[i]), g[f"{pre}.w2{self.linear}"],
                                          rows=rows, in_dim=4 * h, out_dim=h, ensemble=E, mode=mode,
@@ -389,7 +395,7 @@ class Trunk:
             K.linear_backward_input(d_r1, w[f"{pre}.w1{self.linear}"], self.d_stream, rows=rows, in_dim=h,
                                     out_dim=4 * h, ensemble=E, mode=mode, c=self.d_stream, beta=1.0,
                                     d_bf16=self.d_stream_h if i == 0 else None,
-                                    wt=wt.get(f"{pre}.w1{self.linear}"))
+                                    wt=wt.get(f"{pre}.w1{self.linear}"), workspace=None if self.bf else workspace)
             if g is not None:
                 K.linear_backward_weight(d_r1, self.op(self.stream[i], self.stream_h[i]), g[f"{pre}.w1{self.linear}"],
                                          rows=rows, in_dim=h, out_dim=4 * h, ensemble=E, mode=mode,
