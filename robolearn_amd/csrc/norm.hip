@@ -258,13 +258,67 @@ __device__ __forceinline__ void st4_bf16(unsigned short* p, float4 v) {
     *reinterpret_cast<uint2*>(p) = make_uint2(f32x2_to_bf16x2(v.x, v.y), f32x2_to_bf16x2(v.z, v.w));
 }
 
+// Statistics folded into the apply passes for layers of at most kFoldChunks
+// 256-row chunks (small batches), which saves the statistics and gradient-
+// reduce launches.  Every thread reduces its four columns' chunk partials in
+// chunk order, which is the order bn_statistics / bn_grad_reduce use for so
+// few chunks, so the results are the same bits; row group 0 of the first row
+// block writes the statistics, the running-statistics update and the
+// parameter gradients.
+constexpr int kFoldChunks = 8;
+
+struct Fold {
+    const float* partial;  // [E][chunks][2][C]
+    int chunks;
+    float* mean_out;       // forward: batch mean / biased variance (may be null in the backward)
+    float* var_out;
+    float* running_mean;   // forward: running statistics, updated when update_running
+    float* running_var;
+    float momentum;
+    int update_running;
+    float* dw;             // backward: parameter gradients (accumulate when accumulate_params)
+    float* db;
+    int accumulate_params;
+};
+
+// Chunk moments of columns c .. c + 3 merged in chunk order -> batch mean and biased variance.
+__device__ __forceinline__ void fold_moments(const Fold& f, int e, int c, int channels, long long rows, float4& mu,
+                                             float4& va) {
+    float n[4] = {0.0f, 0.0f, 0.0f, 0.0f}, m[4] = {0.0f, 0.0f, 0.0f, 0.0f}, q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = 0; k < f.chunks; ++k) {
+        const float* in = f.partial + (static_cast<long long>(e) * f.chunks + k) * 2 * channels;
+        const float4 cm = ld4(in + c), cq = ld4(in + channels + c);
+        const float cn = static_cast<float>(min(static_cast<long long>(kChunk), rows - static_cast<long long>(k) * kChunk));
+        merge(n[0], m[0], q[0], cn, cm.x, cq.x);
+        merge(n[1], m[1], q[1], cn, cm.y, cq.y);
+        merge(n[2], m[2], q[2], cn, cm.z, cq.z);
+        merge(n[3], m[3], q[3], cn, cm.w, cq.w);
+    }
+    const float r = static_cast<float>(rows);
+    mu = make_float4(m[0], m[1], m[2], m[3]);
+    va = make_float4(q[0] / r, q[1] / r, q[2] / r, q[3] / r);
+}
+
+// Sums of the chunk gradient partials of columns c .. c + 3 in chunk order.
+__device__ __forceinline__ void fold_sums(const Fold& f, int e, int c, int channels, float4& s0, float4& s1) {
+    s0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    s1 = s0;
+    for (int k = 0; k < f.chunks; ++k) {
+        const float* in = f.partial + (static_cast<long long>(e) * f.chunks + k) * 2 * channels;
+        const float4 a = ld4(in + c), g = ld4(in + channels + c);
+        s0 = make_float4(s0.x + a.x, s0.y + a.y, s0.z + a.z, s0.w + a.w);
+        s1 = make_float4(s1.x + g.x, s1.y + g.y, s1.z + g.z, s1.w + g.w);
+    }
+}
+
 // bn_apply for channels % 4 == 0 with 16-byte aligned rows; XT is float or
 // unsigned short (bf16 bits, rows 8-byte aligned).  RPT rows per thread.
-template <typename XT, int RPT>
+template <typename XT, int RPT, bool FOLD>
 __global__ __launch_bounds__(256) void bn_apply_vec(const XT* x, long long x_stride, const float* mean,
                                                     const float* var, const float* w, const float* b,
                                                     const float* residual, float* y, unsigned short* y_bf16,
-                                                    long long rows, int channels, float eps, int relu, int tpr) {
+                                                    long long rows, int channels, float eps, int relu, int tpr,
+                                                    Fold fold) {
     const int e = blockIdx.z;
     const int q = blockIdx.x * tpr + threadIdx.x % tpr;  // float4 column
     if (4 * q >= channels) return;
@@ -281,7 +335,28 @@ __global__ __launch_bounds__(256) void bn_apply_vec(const XT* x, long long x_str
         if (residual) rv[k] = ld4(residual + out_base + i);
     }
     const int pc = e * channels + c;
-    const float4 mu = ld4(mean + pc), va = ld4(var + pc), wv = ld4(w + pc), bv = ld4(b + pc);
+    float4 mu, va;
+    if constexpr (FOLD) {
+        fold_moments(fold, e, c, channels, rows, mu, va);
+        if (blockIdx.y == 0 && threadIdx.x < tpr) {
+            st4(fold.mean_out + pc, mu);
+            st4(fold.var_out + pc, va);
+            if (fold.update_running) {
+                const float f = rows > 1 ? static_cast<float>(rows) / static_cast<float>(rows - 1) : 1.0f;
+                const float4 rm = ld4(fold.running_mean + pc), rv0 = ld4(fold.running_var + pc);
+                const float mo = fold.momentum;
+                st4(fold.running_mean + pc, make_float4(rm.x + mo * (mu.x - rm.x), rm.y + mo * (mu.y - rm.y),
+                                                        rm.z + mo * (mu.z - rm.z), rm.w + mo * (mu.w - rm.w)));
+                const float4 ub = rows > 1 ? make_float4(va.x * f, va.y * f, va.z * f, va.w * f) : va;
+                st4(fold.running_var + pc, make_float4(rv0.x + mo * (ub.x - rv0.x), rv0.y + mo * (ub.y - rv0.y),
+                                                       rv0.z + mo * (ub.z - rv0.z), rv0.w + mo * (ub.w - rv0.w)));
+            }
+        }
+    } else {
+        mu = ld4(mean + pc);
+        va = ld4(var + pc);
+    }
+    const float4 wv = ld4(w + pc), bv = ld4(b + pc);
     const float4 inv = make_float4(1.0f / sqrtf(va.x + eps), 1.0f / sqrtf(va.y + eps), 1.0f / sqrtf(va.z + eps),
                                    1.0f / sqrtf(va.w + eps));
 #pragma unroll
@@ -303,13 +378,13 @@ __global__ __launch_bounds__(256) void bn_apply_vec(const XT* x, long long x_str
 // float or bf16 bits (XT, DT).  dx_bf16 may alias a bf16 dy: each element is
 // read and written by the same thread, and every read comes first.  RPT rows
 // per thread, all loads issued before any arithmetic.
-template <typename XT, typename DT, int RPT>
+template <typename XT, typename DT, int RPT, bool FOLD>
 __global__ __launch_bounds__(256) void bn_grad_apply_vec(const XT* x, long long x_stride, const DT* dy,
                                                          const float* y, const float* w, const float* b,
                                                          const float* mean, const float* var, const float* sums,
                                                          float* dx, unsigned short* dx_bf16, long long rows,
                                                          int channels, int ensemble, float eps, int training, int relu,
-                                                         int accumulate, int tpr) {
+                                                         int accumulate, int tpr, Fold fold) {
     const int e = blockIdx.z;
     const int q = blockIdx.x * tpr + threadIdx.x % tpr;
     if (4 * q >= channels) return;
@@ -333,7 +408,26 @@ __global__ __launch_bounds__(256) void bn_grad_apply_vec(const XT* x, long long 
     const float4 inv = make_float4(1.0f / sqrtf(va.x + eps), 1.0f / sqrtf(va.y + eps), 1.0f / sqrtf(va.z + eps),
                                    1.0f / sqrtf(va.w + eps));
     float4 s0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), s1 = s0;
-    if (training) {
+    if constexpr (FOLD) {
+        float4 t0, t1;
+        fold_sums(fold, e, c, channels, t0, t1);
+        if (blockIdx.y == 0 && threadIdx.x < tpr) {
+            const float a = fold.accumulate_params ? 1.0f : 0.0f;
+            if (fold.dw) {
+                const float4 o = fold.accumulate_params ? ld4(fold.dw + pc) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                st4(fold.dw + pc, make_float4(o.x * a + t1.x, o.y * a + t1.y, o.z * a + t1.z, o.w * a + t1.w));
+            }
+            if (fold.db) {
+                const float4 o = fold.accumulate_params ? ld4(fold.db + pc) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                st4(fold.db + pc, make_float4(o.x * a + t0.x, o.y * a + t0.y, o.z * a + t0.z, o.w * a + t0.w));
+            }
+        }
+        if (training) {
+            const float r = static_cast<float>(rows);
+            s0 = make_float4(t0.x / r, t0.y / r, t0.z / r, t0.w / r);
+            s1 = make_float4(t1.x / r, t1.y / r, t1.z / r, t1.w / r);
+        }
+    } else if (training) {
         s0 = ld4(sums + pc);
         s1 = ld4(sums + ensemble * channels + pc);
     }
@@ -560,14 +654,16 @@ __global__ __launch_bounds__(kThreads) void bn_grad_partials(const float* x, lon
 #pragma unroll
         for (int k = 0; k < Batch; ++k) {
             const int r = r0 + (k0 + k) * Groups;
-            if (!live || r >= r_end) break;
-            float gk = g[k];
-            if (relu) {
-                const float out = y ? y[off + static_cast<long long>(r) * channels] : bn_value(xv[k], mu, inv, wc, bc);
-                if (!(out > 0.0f)) gk = 0.0f;
+            if (live && r < r_end) {
+                float gk = g[k];
+                if (relu) {
+                    const float out = y ? y[off + static_cast<long long>(r) * channels]
+                                        : bn_value(xv[k], mu, inv, wc, bc);
+                    if (!(out > 0.0f)) gk = 0.0f;
+                }
+                s0 += gk;
+                s1 += gk * ((xv[k] - mu) * inv);
             }
-            s0 += gk;
-            s1 += gk * ((xv[k] - mu) * inv);
         }
     }
     __shared__ float sa[kThreads], sb[kThreads];
@@ -1046,38 +1142,51 @@ void bn_forward(int ensemble, const void* x, int x_bf16, long long x_stride, con
     require(x && w && b && (y || y_bf16), "BatchNorm requires x, weight, bias and an output.");
     const float* use_mean = running_mean;
     const float* use_var = running_var;
+    const bool vec = channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, x_bf16 ? 8 : 16) &&
+                     (!y || aligned(y, 16)) && (!y_bf16 || aligned(y_bf16, 8)) &&
+                     (!residual || aligned(residual, 16)) && aligned(w, 16) && aligned(b, 16) &&
+                     (training ? aligned(mean, 16) && aligned(var, 16)
+                               : aligned(running_mean, 16) && aligned(running_var, 16));
+    require(vec || !x_bf16, "bf16 BatchNorm input needs channels and strides in multiples of 4 and aligned buffers.");
+    const int chunks = chunks_for(rows);
+    // few chunks: the apply pass merges them itself (no statistics launch)
+    const bool fold = training && vec && chunks <= norm::kFoldChunks && aligned(partial, 16) &&
+                      (!running_mean || (aligned(running_mean, 16) && aligned(running_var, 16)));
+    norm::Fold folded{partial, chunks, mean, var, running_mean, running_var, momentum,
+                      update_running && running_mean && running_var ? 1 : 0, nullptr, nullptr, 0};
     if (training) {
         require(mean && var && partial, "Training BatchNorm requires mean, var and partial scratch.");
-        const int chunks = chunks_for(rows);
         if (!moments_ready) bn_chunk_moments(ensemble, x, x_bf16, x_stride, partial, rows, channels, stream);
-        hipLaunchKernelGGL(norm::bn_statistics, dim3(ceil_div(ensemble * channels, norm::kStatCols)),
-                           dim3(norm::kStatCols * norm::kStatGroups), 0, stream,
-                           partial, mean, var, running_mean, running_var, rows, channels, chunks, ensemble, momentum,
-                           update_running && running_mean && running_var ? 1 : 0);
-        check_launch("Launch BN statistics");
+        if (!fold) {
+            hipLaunchKernelGGL(norm::bn_statistics, dim3(ceil_div(ensemble * channels, norm::kStatCols)),
+                               dim3(norm::kStatCols * norm::kStatGroups), 0, stream,
+                               partial, mean, var, running_mean, running_var, rows, channels, chunks, ensemble,
+                               momentum, folded.update_running);
+            check_launch("Launch BN statistics");
+        }
         use_mean = mean;
         use_var = var;
     } else {
         require(running_mean && running_var, "Eval BatchNorm requires running statistics.");
     }
     const long long total = static_cast<long long>(ensemble) * rows * channels;
-    const bool vec = channels % 4 == 0 && x_stride % 4 == 0 && aligned(x, x_bf16 ? 8 : 16) &&
-                     (!y || aligned(y, 16)) && (!y_bf16 || aligned(y_bf16, 8)) &&
-                     (!residual || aligned(residual, 16)) && aligned(use_mean, 16) && aligned(use_var, 16) &&
-                     aligned(w, 16) && aligned(b, 16);
-    require(vec || !x_bf16, "bf16 BatchNorm input needs channels and strides in multiples of 4 and aligned buffers.");
     if (vec) {
         const norm::VecLayout layout = norm::vec_layout(rows, channels, ensemble);
-        const auto launch = [&](auto xt, auto rpt) {
+        const auto launch = [&](auto xt, auto rpt, auto fold_const) {
             using XT = decltype(xt);
-            hipLaunchKernelGGL((norm::bn_apply_vec<XT, decltype(rpt)::value>), layout.grid, dim3(256), 0, stream,
-                               static_cast<const XT*>(x), x_stride, use_mean, use_var, w, b, residual, y, y_bf16,
-                               static_cast<long long>(rows), channels, eps, relu, layout.tpr);
+            hipLaunchKernelGGL((norm::bn_apply_vec<XT, decltype(rpt)::value, decltype(fold_const)::value>),
+                               layout.grid, dim3(256), 0, stream, static_cast<const XT*>(x), x_stride, use_mean,
+                               use_var, w, b, residual, y, y_bf16, static_cast<long long>(rows), channels, eps, relu,
+                               layout.tpr, folded);
+        };
+        const auto by_fold = [&](auto xt, auto rpt) {
+            if (fold) launch(xt, rpt, std::true_type{});
+            else launch(xt, rpt, std::false_type{});
         };
         const auto by_rows = [&](auto xt) {
-            if (layout.rpt == 8) launch(xt, std::integral_constant<int, 8>{});
-            else if (layout.rpt == 4) launch(xt, std::integral_constant<int, 4>{});
-            else launch(xt, std::integral_constant<int, 2>{});
+            if (layout.rpt == 8) by_fold(xt, std::integral_constant<int, 8>{});
+            else if (layout.rpt == 4) by_fold(xt, std::integral_constant<int, 4>{});
+            else by_fold(xt, std::integral_constant<int, 2>{});
         };
         if (x_bf16) by_rows((unsigned short)0);
         else by_rows(0.0f);
@@ -1107,10 +1216,16 @@ void bn_backward(int ensemble, const void* x, int x_bf16, long long x_stride, co
     require(vec_inputs || !narrow,
             "bf16 BatchNorm backward inputs need channels and strides in multiples of 4 and aligned buffers.");
     const bool need_sums = training || dw || db;
+    const int chunks = chunks_for(rows);
+    // few chunks: the apply pass adds the chunk partials itself (no reduce launch)
+    const bool apply_vec = (dx || dx_bf16) && vec_inputs && (!dx || aligned(dx, 16)) &&
+                           (!dx_bf16 || aligned(dx_bf16, 8)) && (ensemble * channels) % 4 == 0;
+    const bool fold = need_sums && apply_vec && aligned(partial, 16) && chunks <= norm::kFoldChunks &&
+                      (!dw || aligned(dw, 16)) && (!db || aligned(db, 16));
+    const norm::Fold folded{partial, chunks, nullptr, nullptr, nullptr, nullptr, 0.0f, 0, dw, db, accumulate_params};
     if (need_sums) {
         require(partial && sums, "BatchNorm backward requires partial and sums scratch.");
         require(!narrow || aligned(partial, 16), "BatchNorm partial scratch must be 16-byte aligned.");
-        const int chunks = chunks_for(rows);
         if (vec_inputs && aligned(partial, 16)) {
             const dim3 grid(ceil_div(channels / 4, norm::kVecCols), chunks, ensemble);
             const auto launch = [&](auto xt, auto dt) {
@@ -1138,30 +1253,38 @@ void bn_backward(int ensemble, const void* x, int x_bf16, long long x_stride, co
             else launch(std::integral_constant<int, 1>{});
         }
         check_launch("Launch BN gradient partials");
-        hipLaunchKernelGGL(norm::bn_grad_reduce, dim3(ceil_div(ensemble * channels, norm::kStatCols)),
-                           dim3(norm::kStatCols * norm::kStatGroups), 0, stream,
-                           partial, sums, dw, db, rows, channels, chunks, ensemble, accumulate_params);
-        check_launch("Launch BN gradient reduce");
+        if (!fold) {
+            hipLaunchKernelGGL(norm::bn_grad_reduce, dim3(ceil_div(ensemble * channels, norm::kStatCols)),
+                               dim3(norm::kStatCols * norm::kStatGroups), 0, stream,
+                               partial, sums, dw, db, rows, channels, chunks, ensemble, accumulate_params);
+            check_launch("Launch BN gradient reduce");
+        }
     }
     if (dx || dx_bf16) {
         const long long total = static_cast<long long>(ensemble) * rows * channels;
-        const bool vec = vec_inputs && (!dx || aligned(dx, 16)) && (!dx_bf16 || aligned(dx_bf16, 8)) &&
-                         (!training || (aligned(sums, 16) && (ensemble * channels) % 4 == 0));
+        // a folded launch takes the vector apply, which adds the partials itself and reads no sums
+        const bool vec = fold || (vec_inputs && (!dx || aligned(dx, 16)) && (!dx_bf16 || aligned(dx_bf16, 8)) &&
+                                  (!training || (aligned(sums, 16) && (ensemble * channels) % 4 == 0)));
         require(vec || !narrow, "bf16 BatchNorm backward outputs need aligned buffers and 4-aligned statistics.");
         if (vec) {
             const norm::VecLayout layout = norm::vec_layout(rows, channels, ensemble);
-            const auto launch_rows = [&](auto xt, auto dt, auto rpt) {
+            const auto launch_rows = [&](auto xt, auto dt, auto rpt, auto fold_const) {
                 using XT = decltype(xt);
                 using DT = decltype(dt);
-                hipLaunchKernelGGL((norm::bn_grad_apply_vec<XT, DT, decltype(rpt)::value>), layout.grid, dim3(256), 0,
-                                   stream, static_cast<const XT*>(x), x_stride, static_cast<const DT*>(dy), y, w, b,
-                                   mean, var, sums, dx, dx_bf16, static_cast<long long>(rows), channels, ensemble, eps,
-                                   training, relu, accumulate_dx, layout.tpr);
+                hipLaunchKernelGGL((norm::bn_grad_apply_vec<XT, DT, decltype(rpt)::value, decltype(fold_const)::value>),
+                                   layout.grid, dim3(256), 0, stream, static_cast<const XT*>(x), x_stride,
+                                   static_cast<const DT*>(dy), y, w, b, mean, var, sums, dx, dx_bf16,
+                                   static_cast<long long>(rows), channels, ensemble, eps, training, relu, accumulate_dx,
+                                   layout.tpr, folded);
+            };
+            const auto by_fold = [&](auto xt, auto dt, auto rpt) {
+                if (fold) launch_rows(xt, dt, rpt, std::true_type{});
+                else launch_rows(xt, dt, rpt, std::false_type{});
             };
             const auto launch = [&](auto xt, auto dt) {
-                if (layout.rpt == 8) launch_rows(xt, dt, std::integral_constant<int, 8>{});
-                else if (layout.rpt == 4) launch_rows(xt, dt, std::integral_constant<int, 4>{});
-                else launch_rows(xt, dt, std::integral_constant<int, 2>{});
+                if (layout.rpt == 8) by_fold(xt, dt, std::integral_constant<int, 8>{});
+                else if (layout.rpt == 4) by_fold(xt, dt, std::integral_constant<int, 4>{});
+                else by_fold(xt, dt, std::integral_constant<int, 2>{});
             };
             if (x_bf16 && dy_bf16) launch((unsigned short)0, (unsigned short)0);
             else if (x_bf16) launch((unsigned short)0, 0.0f);
