@@ -339,6 +339,30 @@ def test_gemm_output_moments_match_chunk_moments(gpu, batch, m, n, k, splits, a_
         torch.testing.assert_close(x0, x1, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("batch,m,n,k,splits", [(2, 1024, 256, 1024, 8), (1, 1000, 128, 512, 2), (2, 64, 36, 256, 4)])
+def test_split_fp32_product_moments_match_chunk_moments(gpu, batch, m, n, k, splits):
+    """fp32-accurate products split over K reduce their partials and take the BatchNorm chunk moments of
+    the result in one pass: D against float64, the moments against the chunk moments of D."""
+    print(f"case fp32 split moments batch={batch} m={m} n={n} k={k} splits={splits}", flush=True)
+    g = torch.Generator().manual_seed(3 * m + k)
+    a = torch.randn(batch, m, k, generator=g) + 0.25
+    b = torch.randn(batch, n, k, generator=g)
+    workspace = torch.empty(splits * batch * (m * n + m) * 4, dtype=torch.uint8, device=gpu)
+    d = torch.empty(batch, m, n, device=gpu)
+    chunks = (m + 255) // 256
+    moments = torch.full((batch, chunks, 2, n), float("nan"), device=gpu)
+    K.gemm(a.to(gpu), b.to(gpu), d, m=m, n=n, k=k, batch=batch, a_kcontig=True, b_kcontig=True, lda=k, ldb=k,
+           ldd=n, stride_a=m * k, stride_b=n * k, stride_d=m * n, mode=K.FP32_SPLIT, splits=splits,
+           workspace=workspace, moments=moments)
+    torch.cuda.synchronize()
+    ref = a.double() @ b.double().transpose(1, 2)
+    torch.testing.assert_close(d.cpu().double(), ref, rtol=1e-5, atol=1e-4)
+    expected = _chunk_moments(d.cpu())
+    got = moments.cpu().double()
+    torch.testing.assert_close(got[:, :, 0], expected[:, :, 0], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(got[:, :, 1], expected[:, :, 1], rtol=1e-5, atol=1e-3)
+
+
 @pytest.mark.parametrize("batch,m,n,k,splits,a_kcontig,b_kcontig", MOMENT_SHAPES)
 def test_bf16_only_gemm_output(gpu, batch, m, n, k, splits, a_kcontig, b_kcontig):
     """A bfloat16 output is the bf16 copy of the fp32 product, bit for bit, and its moments
