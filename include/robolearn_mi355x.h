@@ -8,7 +8,8 @@
  *   - Run/step calls only enqueue work on the caller's stream (a hipStream_t
  *     passed as void*): no allocation, no synchronization, graph-capturable.
  *   - All device buffers are caller-owned; float arrays are fp32 unless a
- *     parameter says bf16 (stored as 16-bit bf16 bit patterns, RNE).
+ *     parameter says bf16 or fp16 (16-bit bf16 / IEEE binary16 bit patterns,
+ *     rounded to nearest even).
  *   - Row-major layouts; "ensemble" batches independent members (the twin
  *     critics) with member strides.
  * Paths below are relative to the reference tree.
@@ -30,8 +31,9 @@ const char* rl_last_error(void);
 /* Column-major D = op(A) op(B) + beta C (+ bias[m]); replaces
  * robolearn/cuda/kernels.cu:528-538 (create), :689 (workspace), :540 (autotune,
  * accepted as a no-op), :654 (metadata), :698-731 (run), :733 (destroy).
- * input_dtype: 0 fp32, 1 bf16 operands in memory (the reference's fp16), 2 fp32
- * stored with bf16 compute. */
+ * input_dtype: 0 fp32, 1 IEEE fp16 operands in memory (as the reference; fp16
+ * matrix cores, fp32 accumulation and output), and two precisions the reference
+ * lacks: 2 fp32 stored with bf16 compute, 3 bf16 operands in memory. */
 void* rl_plan_create(int m, int n, int k, int transa, int transb, int lda, int ldb, int ldd, int use_bias,
                      int allow_tf32, size_t workspace_limit);
 void* rl_plan_create_mixed(int m, int n, int k, int transa, int transb, int lda, int ldb, int ldd, int use_bias,
@@ -47,7 +49,9 @@ int rl_plan_destroy(void* plan);
  * (mode 0: fp32 v_mfma_f32_32x32x2_f32, mode 1: bf16 v_mfma_f32_32x32x16_bf16,
  * mode 2: fp32 operands and results with fp32-accurate products on the bf16 matrix
  * cores: every operand value split exactly into three bf16 pieces, six partial
- * products per 16-K step).
+ * products per 16-K step, mode 3: IEEE fp16 v_mfma_f32_32x32x16_f16).  In modes 1
+ * and 3, a_bf16 / b_bf16 mark an operand stored as 16-bit values of the mode's
+ * format (else fp32, rounded on load); mode 3 writes the fp32 D only.
  * A(m,k) = a_kcontig ? A[m*lda+k] : A[k*lda+m]; B(k,n) = b_kcontig ? B[n*ldb+k]
  * : B[k*ldb+n].  epilogue 0 none, 1 ReLU, 2 ELU, 3 ELU gradient (modes 0 and 2:
  * D = AB * elu'(C) with C the ELU outputs, beta 0, no bias).  splits > 1 reduces over K in
@@ -118,7 +122,7 @@ void* rl_zero_create(size_t count, const void* const* pointers, const size_t* le
 int rl_zero_step(void* plan, void* stream);
 int rl_zero_destroy(void* plan);
 
-/* robolearn/cuda/flash_kernels.cuh:398-445 (shadows receive bf16 copies) */
+/* robolearn/cuda/flash_kernels.cuh:398-445; shadows receive IEEE fp16 copies (:128) */
 void* rl_flash_projection_create(size_t count, const void* const* first, const void* const* second,
                                  const size_t* lengths, const int* kinds);
 void* rl_flash_projection_create_with_shadows(size_t count, const void* const* first, const void* const* second,
@@ -126,7 +130,8 @@ void* rl_flash_projection_create_with_shadows(size_t count, const void* const* f
 int rl_flash_projection_step(void* plan, void* stream);
 int rl_flash_projection_destroy(void* plan);
 
-/* robolearn/cuda/flash_kernels.cuh:447-498 */
+/* robolearn/cuda/flash_kernels.cuh:447-498; shadows receive IEEE fp16 copies of the
+ * new targets (:138) */
 void* rl_flash_ema_create(size_t count, const void* const* source, const void* const* target,
                           const size_t* lengths, float tau);
 void* rl_flash_ema_create_with_shadows(size_t count, const void* const* source, const void* const* target,
@@ -164,15 +169,16 @@ int rl_rms_backward_ex(int ensemble, const float* x, const float* dy, const floa
                        long long member_stride, float eps, int accumulate_dx, int accumulate_dw, void* stream);
 /* fp32 -> bf16 RNE copy (weight shadows); counterpart of robolearn/cuda/kernels.cu:663-687. */
 int rl_cast_f32_bf16(const float* source, void* destination, long long count, void* stream);
-/* robolearn/cuda/kernels.cu:12, 663-687 under the reference's name: the 16-bit
- * operand copy, which is bf16 (RNE) on this backend. */
+/* robolearn/cuda/kernels.cu:12, 663-687: fp32 -> IEEE fp16 (RNE) copy, the
+ * operands of rl_plan_create_mixed's input_dtype 1. */
 int rl_cast_f32_f16(const void* source, void* destination, size_t count, void* stream);
 /* Deterministic column sums; replaces robolearn/cuda/kernels.cu:237-251, 742-758. */
 int rl_bias_grad_ex(int ensemble, const float* dy, float* db, float* partial, int rows, int channels, int accumulate,
                     void* stream);
 
 /* Reference-signature entries: robolearn/cuda/flash_kernels.cuh:529-634 (fp16
- * side outputs become bf16), robolearn/cuda/kernels.cu:742. */
+ * side outputs are IEEE fp16, the exact rounding of the retained fp32 y or dx),
+ * robolearn/cuda/kernels.cu:742. */
 int rl_flash_bn_forward(const float* x, const float* w, const float* b, float* running_mean, float* running_var,
                         float* mean, float* var, float* partial, float* y, int batch, int channels, float eps,
                         float momentum, int training, int relu, void* stream);
@@ -180,8 +186,7 @@ int rl_flash_bn_forward_with_bf16(const float* x, const float* w, const float* b
                                   float* running_var, float* mean, float* var, float* partial, float* y,
                                   void* half_output, int batch, int channels, float eps, float momentum,
                                   int training, int relu, void* stream);
-/* robolearn/cuda/flash_kernels.cuh:536-542 under the reference's name; half_output
- * receives bf16. */
+/* robolearn/cuda/flash_kernels.cuh:536-542; half_output receives IEEE fp16. */
 int rl_flash_bn_forward_with_fp16(const float* x, const float* w, const float* b, float* running_mean,
                                   float* running_var, float* mean, float* var, float* partial, float* y,
                                   void* half_output, int batch, int channels, float eps, float momentum,
@@ -199,12 +204,14 @@ int rl_flash_bn_forward_static(const float* x, const float* w, const float* b, f
 int rl_flash_bn_backward(const float* x, const float* dy, const float* y, const float* w, const float* mean,
                          const float* var, float* partial, float* sums, float* dx, float* dw, float* db, int batch,
                          int channels, float eps, int training, int relu, void* stream);
-/* robolearn/cuda/flash_kernels.cuh:577-584 under the reference's name; half_dx
- * receives the bf16 rounding of the final (accumulated) dx. */
+/* robolearn/cuda/flash_kernels.cuh:589-596; half_dx receives the IEEE fp16
+ * rounding of the final (accumulated) dx. */
 int rl_flash_bn_backward_with_fp16(const float* x, const float* dy, const float* y, const float* w,
                                    const float* mean, const float* var, float* partial, float* sums, float* dx,
                                    float* dw, float* db, void* half_dx, int batch, int channels, float eps,
                                    int training, int relu, void* stream);
+/* robolearn/cuda/flash_kernels.cuh:598-609: dx required, overwritten when
+ * overwrite_dx is 1 (else accumulated); optional half_dx as above. */
 int rl_flash_bn_backward_controlled(const float* x, const float* dy, const float* y, const float* w,
                                     const float* mean, const float* var, float* partial, float* sums, float* dx,
                                     float* dw, float* db, void* half_dx, int overwrite_dx, int batch, int channels,

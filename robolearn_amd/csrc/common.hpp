@@ -119,6 +119,17 @@ __device__ __forceinline__ float bf16_bits_to_f32(unsigned short bits) {
     return __uint_as_float(static_cast<unsigned int>(bits) << 16);
 }
 
+// fp32 -> IEEE binary16 with round-to-nearest-even (v_cvt_f16_f32 under the
+// default rounding mode): subnormal results are kept, magnitudes past the
+// largest finite half become infinities and NaN stays NaN.
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ unsigned short f32_to_f16_bits(float value) {
+    return __builtin_bit_cast(unsigned short, static_cast<_Float16>(value));
+}
+__device__ __forceinline__ unsigned int f32x2_to_f16x2(float lo, float hi) {
+    return __builtin_bit_cast(unsigned int, __builtin_convertvector((f32x2_t){lo, hi}, f16x2_t));
+}
+
 // DPP lane permutations within a row of 16 lanes (GCN/CDNA DPP16 controls).
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]

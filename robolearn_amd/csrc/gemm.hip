@@ -615,18 +615,21 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
              const float* c, float* d, long long ldd, long long stride_d, const float* bias, long long stride_bias,
              float beta, int epilogue, int splits, float* workspace, std::size_t workspace_bytes, hipStream_t stream,
              unsigned short* d_bf16, float* moments, float* a_sums) {
-    require(mode >= 0 && mode <= 2, "GEMM mode must be 0 (fp32), 1 (bf16 operands) or 2 (fp32 on bf16 pieces).");
-    require(!(mode != 1 && (a_bf16 || b_bf16)), "fp32 GEMM modes require fp32 operands.");
+    require(mode >= 0 && mode <= 3,
+            "GEMM mode must be 0 (fp32), 1 (bf16 operands), 2 (fp32 on bf16 pieces) or 3 (fp16 operands).");
+    const bool half_mode = mode == 1 || mode == 3;  // 16-bit MFMA operands, K tiles of 32
+    require(half_mode || !(a_bf16 || b_bf16), "fp32 GEMM modes require fp32 operands.");
     require(m > 0 && n > 0 && k > 0 && batch > 0, "GEMM dimensions must be positive.");
     require(a && b && (d || (mode == 1 && d_bf16)),
             "GEMM operands must be nonnull (bf16 mode may write the bf16 copy alone, with d null).");
+    require(mode != 3 || (!d_bf16 && !moments), "The fp16 mode writes the fp32 output only.");
     require(std::isfinite(beta) && (beta == 0.0f || c), "Nonzero beta requires C; beta must be finite.");
     require(epilogue >= 0 && epilogue <= 3, "Unknown GEMM epilogue.");
-    require(epilogue != 3 || (mode != 1 && c && beta == 0.0f && !bias),
+    require(epilogue != 3 || (!half_mode && c && beta == 0.0f && !bias),
             "The ELU-gradient epilogue needs fp32 mode, the ELU outputs as C, beta 0 and no bias.");
     require(splits >= 1, "GEMM split count must be positive.");
     require(static_cast<long long>(m) * n <= std::numeric_limits<int>::max(), "GEMM output exceeds 2^31 elements.");
-    require(!a_sums || (mode != 1 && !bias), "Row sums of A are produced by the fp32 GEMM family, without a bias.");
+    require(!a_sums || (!half_mode && !bias), "Row sums of A are produced by the fp32 GEMM family, without a bias.");
     // the row sums take the bias layout: member e at a_sums + e * stride_bias (m when stride_bias is 0)
     const long long sums_stride = stride_bias > 0 ? stride_bias : m;
     require(!moments || (ldd == n && aligned(moments, 16)),
@@ -650,7 +653,7 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     p.beta = beta;
     p.epilogue = epilogue;
     p.d_bf16 = d_bf16;
-    const int kt = mode == 1 ? 32 : 16;
+    const int kt = half_mode ? 32 : 16;
     const int ktiles = (k + kt - 1) / kt;
     if (splits > ktiles) splits = ktiles;
     const int tiles_per_split = (ktiles + splits - 1) / splits;  // split boundaries are multiples of 32 in both modes
@@ -685,8 +688,9 @@ int run_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kcontig, int
     const bool fused_moments = moments && mode == 1 && splits == 1 && !bias && epilogue == 0 && beta == 0.0f &&
                                gemm::big_eligible(p, a_bf16, b_bf16);
     p.moments = fused_moments ? moments : nullptr;
-    if (mode != 1) gemm::launch_fp32(p, a_kcontig != 0, b_kcontig != 0, mode == 2, stream);
-    else gemm::launch_bf16(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
+    if (mode == 1) gemm::launch_bf16(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
+    else if (mode == 3) gemm::launch_f16(p, a_bf16, b_bf16, a_kcontig != 0, b_kcontig != 0, stream);
+    else gemm::launch_fp32(p, a_kcontig != 0, b_kcontig != 0, mode == 2, stream);
     check_launch("Launch GEMM");
     if (splits > 1) {
         const long long total = static_cast<long long>(batch) * m * n;
@@ -748,7 +752,7 @@ RL_API int rl_gemm(int mode, int a_bf16, int b_bf16, int a_kcontig, int b_kconti
 
 RL_API std::size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, int splits) noexcept {
     if (m <= 0 || n <= 0 || k <= 0 || batch <= 0 || splits <= 1) return 0;
-    const int kt = mode == 1 ? 32 : 16;
+    const int kt = (mode == 1 || mode == 3) ? 32 : 16;
     const int ktiles = (k + kt - 1) / kt;
     if (splits > ktiles) splits = ktiles;
     const int per = (ktiles + splits - 1) / splits;

@@ -59,6 +59,9 @@ __device__ __forceinline__ float apply_epilogue(float v, int epilogue) {
 
 // bf16 MFMA kernel family with 256x128 tiles (gemm_bf16.hip).
 void launch_bf16(const Params& p, int a_bf16, int b_bf16, bool ak, bool bk, hipStream_t stream);
+// The same tiles on IEEE fp16 operands (a_f16 / b_f16: 16-bit fp16 storage,
+// else fp32 rounded to fp16 on load).
+void launch_f16(const Params& p, int a_f16, int b_f16, bool ak, bool bk, hipStream_t stream);
 
 // 256x256-tile bf16 kernel for exactly tiling bf16 operands (gemm_bf16_big.hip).
 bool big_eligible(const Params& p, int a_bf16, int b_bf16);

@@ -15,6 +15,9 @@
 //     [row][k] and each lane reads its K-slice with 16-byte LDS loads;
 //   * fp32 sources are rounded to bf16 (RNE) on the way into LDS, bf16 sources
 //     are copied as-is; accumulation is fp32.
+// The F16 instantiations run the same schedule on IEEE fp16 operands
+// (v_mfma_f32_32x32x16_f16): 16-bit sources are fp16 bit patterns and fp32
+// sources are rounded to fp16 (RNE).
 #include "gemm.hpp"
 
 namespace rl {
@@ -38,11 +41,11 @@ __device__ __forceinline__ unsigned int high_halves(unsigned int a, unsigned int
 }
 
 // Loads a Rows x 32 operand tile (element (r, k) = KContig ? src[r*ld + k] :
-// src[k*ld + r]) as raw 16-byte vectors; store() converts to bf16 (hardware
-// RNE for fp32 sources), transposes M/N-contiguous vectors in registers and
-// writes LDS as [r][k] with pitch kPitch.  load() issues memory operations
+// src[k*ld + r]) as raw 16-byte vectors; store() converts fp32 sources to bf16
+// (fp16 when F16; hardware RNE), transposes M/N-contiguous vectors in
+// registers and writes LDS as [r][k] with pitch kPitch.  load() issues memory operations
 // only, so the loads stay in flight across the MFMA block that follows.
-template <typename S, bool KContig, int Rows>
+template <typename S, bool KContig, int Rows, bool F16>
 struct Loader {
     using V = typename Raw<S>::T;
     static constexpr int VE = 16 / static_cast<int>(sizeof(S));  // elements per 16-byte vector
@@ -107,6 +110,11 @@ struct Loader {
         }
     }
 
+    static __device__ __forceinline__ unsigned int pack(float lo, float hi) {
+        if constexpr (F16) return f32x2_to_f16x2(lo, hi);
+        else return f32x2_to_bf16x2(lo, hi);
+    }
+
     __device__ __forceinline__ void store(unsigned short* lds) const {
         const int t = threadIdx.x;
         if constexpr (KContig) {
@@ -115,8 +123,7 @@ struct Loader {
                 const int v = i * kThreads + t;
                 unsigned short* q = lds + (v / VPR) * kPitch + (v % VPR) * VE;
                 if constexpr (sizeof(S) == 4) {
-                    *reinterpret_cast<uint2*>(q) = make_uint2(f32x2_to_bf16x2(raw[i].x, raw[i].y),
-                                                              f32x2_to_bf16x2(raw[i].z, raw[i].w));
+                    *reinterpret_cast<uint2*>(q) = make_uint2(pack(raw[i].x, raw[i].y), pack(raw[i].z, raw[i].w));
                 } else {
                     *reinterpret_cast<uint4*>(q) = raw[i];
                 }
@@ -130,10 +137,10 @@ struct Loader {
             for (int j = 0; j < KR / 2; ++j) {
                 if constexpr (sizeof(S) == 4) {
                     const float4 a = raw[2 * j], b = raw[2 * j + 1];
-                    w[0][j] = f32x2_to_bf16x2(a.x, b.x);
-                    w[1][j] = f32x2_to_bf16x2(a.y, b.y);
-                    w[2][j] = f32x2_to_bf16x2(a.z, b.z);
-                    w[3][j] = f32x2_to_bf16x2(a.w, b.w);
+                    w[0][j] = pack(a.x, b.x);
+                    w[1][j] = pack(a.y, b.y);
+                    w[2][j] = pack(a.z, b.z);
+                    w[3][j] = pack(a.w, b.w);
                 } else {
                     const uint4 a = raw[2 * j], b = raw[2 * j + 1];
                     const unsigned int aw[4] = {a.x, a.y, a.z, a.w};
@@ -219,7 +226,20 @@ __device__ __forceinline__ void store_tile_vec(const Params& p, const f32x16_t (
     }
 }
 
-template <typename SA, typename SB, bool AK, bool BK>
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+// One 32x32x16 MFMA on 16-bit operand registers: bf16, or IEEE fp16 when F16.
+template <bool F16>
+__device__ __forceinline__ f32x16_t mfma16(u16x8_t a, u16x8_t b, f32x16_t c) {
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                      c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+template <typename SA, typename SB, bool AK, bool BK, bool F16>
 __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) unsigned short lds[2][(kBM + kBN) * kPitch];
     static_assert(sizeof(lds) >= 4 * 32 * kStagePitch * sizeof(float), "epilogue staging must fit the K-loop LDS");
@@ -246,8 +266,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(Params p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    Loader<SA, AK, kBM> la;
-    Loader<SB, BK, kBN> lb;
+    Loader<SA, AK, kBM, F16> la;
+    Loader<SB, BK, kBN, F16> lb;
     const bool avec = p.a_vec != 0;
     const bool bvec = p.b_vec != 0;
 
@@ -268,18 +288,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(Params p) {
         }
         const unsigned short* sa = lds[buffer];
         const unsigned short* sb = lds[buffer] + kBM * kPitch;
-        bf16x8_t af[4][2], bfr[2][2];
+        u16x8_t af[4][2], bfr[2][2];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const unsigned short* q = sa + (wm * 128 + i * 32 + lane % 32) * kPitch + (lane / 32) * 16;
-            af[i][0] = *reinterpret_cast<const bf16x8_t*>(q);
-            af[i][1] = *reinterpret_cast<const bf16x8_t*>(q + 8);
+            af[i][0] = *reinterpret_cast<const u16x8_t*>(q);
+            af[i][1] = *reinterpret_cast<const u16x8_t*>(q + 8);
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const unsigned short* q = sb + (wn * 64 + j * 32 + lane % 32) * kPitch + (lane / 32) * 16;
-            bfr[j][0] = *reinterpret_cast<const bf16x8_t*>(q);
-            bfr[j][1] = *reinterpret_cast<const bf16x8_t*>(q + 8);
+            bfr[j][0] = *reinterpret_cast<const u16x8_t*>(q);
+            bfr[j][1] = *reinterpret_cast<const u16x8_t*>(q + 8);
         }
 #pragma unroll
         for (int s = 0; s < 2; ++s)
@@ -287,7 +307,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(Params p) {
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][s], bfr[j][s], acc[i][j], 0, 0, 0);
+                    acc[i][j] = mfma16<F16>(af[i][s], bfr[j][s], acc[i][j]);
         if (more) {
             la.store(lds[buffer ^ 1]);
             lb.store(lds[buffer ^ 1] + kBM * kPitch);
@@ -337,18 +357,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf16_kernel(Params p) {
     }
 }
 
-template <typename SA, typename SB, bool AK, bool BK>
+template <typename SA, typename SB, bool AK, bool BK, bool F16>
 void launch_v2(const Params& p, hipStream_t stream) {
     const dim3 grid(ceil_div(p.n, kBN), ceil_div(p.m, kBM), static_cast<unsigned>(p.batch * p.splits));
-    hipLaunchKernelGGL((gemm_bf16_kernel<SA, SB, AK, BK>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((gemm_bf16_kernel<SA, SB, AK, BK, F16>), grid, dim3(kThreads), 0, stream, p);
 }
 
-template <typename SA, typename SB>
+template <typename SA, typename SB, bool F16 = false>
 void launch_layout_v2(const Params& p, bool ak, bool bk, hipStream_t stream) {
-    if (ak && bk) launch_v2<SA, SB, true, true>(p, stream);
-    else if (ak && !bk) launch_v2<SA, SB, true, false>(p, stream);
-    else if (!ak && bk) launch_v2<SA, SB, false, true>(p, stream);
-    else launch_v2<SA, SB, false, false>(p, stream);
+    if (ak && bk) launch_v2<SA, SB, true, true, F16>(p, stream);
+    else if (ak && !bk) launch_v2<SA, SB, true, false, F16>(p, stream);
+    else if (!ak && bk) launch_v2<SA, SB, false, true, F16>(p, stream);
+    else launch_v2<SA, SB, false, false, F16>(p, stream);
 }
 
 void launch_bf16(const Params& p, int a_bf16, int b_bf16, bool ak, bool bk, hipStream_t stream) {
@@ -362,6 +382,15 @@ void launch_bf16(const Params& p, int a_bf16, int b_bf16, bool ak, bool bk, hipS
     else if (!a_bf16 && b_bf16) launch_layout_v2<F, H>(p, ak, bk, stream);
     else if (a_bf16 && !b_bf16) launch_layout_v2<H, F>(p, ak, bk, stream);
     else launch_layout_v2<H, H>(p, ak, bk, stream);
+}
+
+void launch_f16(const Params& p, int a_f16, int b_f16, bool ak, bool bk, hipStream_t stream) {
+    using F = float;
+    using H = unsigned short;
+    if (!a_f16 && !b_f16) launch_layout_v2<F, F, true>(p, ak, bk, stream);
+    else if (!a_f16 && b_f16) launch_layout_v2<F, H, true>(p, ak, bk, stream);
+    else if (a_f16 && !b_f16) launch_layout_v2<H, F, true>(p, ak, bk, stream);
+    else launch_layout_v2<H, H, true>(p, ak, bk, stream);
 }
 
 }  // namespace gemm

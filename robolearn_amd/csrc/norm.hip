@@ -1374,6 +1374,9 @@ void bias_grad(int ensemble, const float* dy, float* db, float* partial, int row
                       0.0f, 0, accumulate, stream);
 }
 
+// fp32 -> 16-bit copy of count values (IEEE fp16 when f16, else bf16; RNE).
+void cast_to_16bit(const float* source, unsigned short* destination, long long count, bool f16, hipStream_t stream);
+
 }  // namespace rl
 
 // ---------------------------------------------------------------------------
@@ -1513,15 +1516,21 @@ RL_API int rl_flash_bn_forward_with_bf16(const float* x, const float* w, const f
     });
 }
 
-// robolearn/cuda/flash_kernels.cuh:536-542 under the reference's symbol name.
-// This backend's 16-bit operand format is bf16 (RNE), so half_output receives
-// bf16 bit patterns; the caller allocates it as a 16-bit bf16 buffer.
+// robolearn/cuda/flash_kernels.cuh:536-542: y and, in half_output, its IEEE fp16
+// (RNE) rounding.  The fp16 copy is a pass over the retained fp32 y after the
+// apply pass (the same values the reference rounds inside its apply kernel).
 RL_API int rl_flash_bn_forward_with_fp16(const float* x, const float* w, const float* b, float* running_mean,
                                          float* running_var, float* mean, float* var, float* partial, float* y,
                                          void* half_output, int batch, int channels, float eps, float momentum,
                                          int training, int relu, void* stream) noexcept {
-    return rl_flash_bn_forward_with_bf16(x, w, b, running_mean, running_var, mean, var, partial, y, half_output, batch,
-                                         channels, eps, momentum, training, relu, stream);
+    return rl::guarded("rl_flash_bn_forward_with_fp16", [&] {
+        rl::require(half_output != nullptr, "FP16 BN output must be nonnull.");
+        rl::require(y != nullptr && rl::aligned(half_output, 2), "FP16 BN output needs the fp32 y and 2-byte alignment.");
+        rl::bn_forward(1, x, 0, 0, w, b, running_mean, running_var, mean, var, partial, nullptr, y, nullptr, batch,
+                       channels, eps, momentum, training, relu, 1, 0, rl::as_stream(stream));
+        rl::cast_to_16bit(y, static_cast<unsigned short*>(half_output), static_cast<long long>(batch) * channels, true,
+                          rl::as_stream(stream));
+    });
 }
 
 RL_API int rl_flash_bn_backward(const float* x, const float* dy, const float* y, const float* w, const float* mean,
@@ -1533,29 +1542,39 @@ RL_API int rl_flash_bn_backward(const float* x, const float* dy, const float* y,
     });
 }
 
-// robolearn/cuda/flash_kernels.cuh:577-584 under the reference's symbol name;
-// half_dx receives the bf16 rounding of the final dx (accumulating form).
+// robolearn/cuda/flash_kernels.cuh:589-596: half_dx receives the IEEE fp16 (RNE)
+// rounding of the final dx (accumulating form), by a pass over dx after the
+// apply pass.
 RL_API int rl_flash_bn_backward_with_fp16(const float* x, const float* dy, const float* y, const float* w,
                                           const float* mean, const float* var, float* partial, float* sums, float* dx,
                                           float* dw, float* db, void* half_dx, int batch, int channels, float eps,
                                           int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_backward_with_fp16", [&] {
-        rl::require(half_dx != nullptr, "16-bit BN input adjoint must be nonnull.");
-        rl::require(dx != nullptr, "16-bit BN input adjoint requires an fp32 input adjoint.");
-        rl::bn_backward(1, x, 0, 0, dy, 0, y, w, nullptr, mean, var, partial, sums, dx, dw, db,
-                        static_cast<unsigned short*>(half_dx), batch, channels, eps, training, relu, 1, 1,
-                        rl::as_stream(stream));
+        rl::require(half_dx != nullptr, "FP16 BN input adjoint must be nonnull.");
+        rl::require(dx != nullptr && rl::aligned(half_dx, 2),
+                    "FP16 BN input adjoint requires aligned storage and an fp32 input adjoint.");
+        rl::bn_backward(1, x, 0, 0, dy, 0, y, w, nullptr, mean, var, partial, sums, dx, dw, db, nullptr, batch,
+                        channels, eps, training, relu, 1, 1, rl::as_stream(stream));
+        rl::cast_to_16bit(dx, static_cast<unsigned short*>(half_dx), static_cast<long long>(batch) * channels, true,
+                          rl::as_stream(stream));
     });
 }
 
+// robolearn/cuda/flash_kernels.cuh:598-609: dx overwritten (overwrite_dx 1) or
+// accumulated, and optionally its IEEE fp16 rounding in half_dx.
 RL_API int rl_flash_bn_backward_controlled(const float* x, const float* dy, const float* y, const float* w,
                                            const float* mean, const float* var, float* partial, float* sums, float* dx,
                                            float* dw, float* db, void* half_dx, int overwrite_dx, int batch,
                                            int channels, float eps, int training, int relu, void* stream) noexcept {
     return rl::guarded("rl_flash_bn_backward_controlled", [&] {
-        rl::bn_backward(1, x, 0, 0, dy, 0, y, w, nullptr, mean, var, partial, sums, dx, dw, db,
-                        static_cast<unsigned short*>(half_dx), batch, channels, eps, training, relu,
-                        overwrite_dx ? 0 : 1, 1, rl::as_stream(stream));
+        rl::require(dx != nullptr && (overwrite_dx == 0 || overwrite_dx == 1),
+                    "Controlled BN backward requires dx and a Boolean overwrite flag.");
+        rl::require(!half_dx || rl::aligned(half_dx, 2), "FP16 BN input adjoint requires aligned storage.");
+        rl::bn_backward(1, x, 0, 0, dy, 0, y, w, nullptr, mean, var, partial, sums, dx, dw, db, nullptr, batch,
+                        channels, eps, training, relu, overwrite_dx ? 0 : 1, 1, rl::as_stream(stream));
+        if (half_dx)
+            rl::cast_to_16bit(dx, static_cast<unsigned short*>(half_dx), static_cast<long long>(batch) * channels, true,
+                              rl::as_stream(stream));
     });
 }
 
@@ -1602,34 +1621,66 @@ RL_API int rl_bias_grad(const void* dy, void* db, int batch, int channels, void*
 
 namespace rl {
 namespace norm {
-__global__ void cast_bf16(const float* src, unsigned short* dst, long long n) {
+// fp32 -> 16-bit copies (bf16, or IEEE fp16 when F16; RNE): four values per
+// thread as a 16-byte load and an 8-byte store, the count % 4 tail by the first
+// threads of workgroup 0.
+template <bool F16>
+__device__ __forceinline__ unsigned short to_half(float v) {
+    if constexpr (F16) return f32_to_f16_bits(v);
+    else return f32_to_bf16_bits(v);
+}
+template <bool F16>
+__device__ __forceinline__ unsigned int to_half2(float lo, float hi) {
+    if constexpr (F16) return f32x2_to_f16x2(lo, hi);
+    else return f32x2_to_bf16x2(lo, hi);
+}
+template <bool F16>
+__global__ void cast16(const float* src, unsigned short* dst, long long n) {
     for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n;
          i += static_cast<long long>(gridDim.x) * blockDim.x)
-        dst[i] = f32_to_bf16_bits(src[i]);
+        dst[i] = to_half<F16>(src[i]);
+}
+template <bool F16>
+__global__ void cast16_vec(const float* src, unsigned short* dst, long long n) {
+    const long long n4 = n / 4;
+    for (long long i = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; i < n4;
+         i += static_cast<long long>(gridDim.x) * blockDim.x) {
+        const float4 v = reinterpret_cast<const float4*>(src)[i];
+        reinterpret_cast<uint2*>(dst)[i] = make_uint2(to_half2<F16>(v.x, v.y), to_half2<F16>(v.z, v.w));
+    }
+    const long long tail = 4 * n4 + threadIdx.x;
+    if (blockIdx.x == 0 && tail < n) dst[tail] = to_half<F16>(src[tail]);
 }
 }  // namespace norm
+
+void cast_to_16bit(const float* source, unsigned short* destination, long long count, bool f16, hipStream_t stream) {
+    const bool vec = aligned(source, 16) && aligned(destination, 8);
+    const dim3 grid(norm::elementwise_blocks(vec ? (count + 3) / 4 : count));
+    if (vec && f16) hipLaunchKernelGGL(norm::cast16_vec<true>, grid, dim3(256), 0, stream, source, destination, count);
+    else if (vec) hipLaunchKernelGGL(norm::cast16_vec<false>, grid, dim3(256), 0, stream, source, destination, count);
+    else if (f16) hipLaunchKernelGGL(norm::cast16<true>, grid, dim3(256), 0, stream, source, destination, count);
+    else hipLaunchKernelGGL(norm::cast16<false>, grid, dim3(256), 0, stream, source, destination, count);
+    check_launch("Launch cast");
+}
 }  // namespace rl
 
-// fp32 -> bf16 (RNE) copy; the MI355X counterpart of robolearn/cuda/kernels.cu:663-687.
+// fp32 -> bf16 (RNE) copy: the bf16 counterpart of robolearn/cuda/kernels.cu:663-687.
 RL_API int rl_cast_f32_bf16(const float* source, void* destination, long long count, void* stream) noexcept {
     return rl::guarded("rl_cast_f32_bf16", [&] {
-        rl::require(source && destination && count > 0, "Cast needs buffers and a positive count.");
-        hipLaunchKernelGGL(rl::norm::cast_bf16, dim3(rl::norm::elementwise_blocks(count)), dim3(256), 0,
-                           rl::as_stream(stream), source, static_cast<unsigned short*>(destination), count);
-        rl::check_launch("Launch cast");
+        rl::require(source && destination && count > 0 && rl::aligned(destination, 2),
+                    "Cast needs buffers, 2-byte aligned output and a positive count.");
+        rl::cast_to_16bit(source, static_cast<unsigned short*>(destination), count, false, rl::as_stream(stream));
     });
 }
 
-// robolearn/cuda/kernels.cu:663-687 under the reference's symbol name: the
-// 16-bit operand copy, bf16 (RNE) on this backend.
+// robolearn/cuda/kernels.cu:663-687: fp32 -> IEEE fp16 (RNE) copy, the
+// operand format of rl_plan_create_mixed's input_dtype 1.
 RL_API int rl_cast_f32_f16(const void* source, void* destination, std::size_t count, void* stream) noexcept {
     return rl::guarded("rl_cast_f32_f16", [&] {
         rl::require(source && destination && count > 0 && rl::aligned(source, alignof(float)) &&
                         rl::aligned(destination, 2) && count <= static_cast<std::size_t>(std::numeric_limits<long long>::max()),
-                    "16-bit conversion requires nonempty aligned buffers.");
-        hipLaunchKernelGGL(rl::norm::cast_bf16, dim3(rl::norm::elementwise_blocks(static_cast<long long>(count))),
-                           dim3(256), 0, rl::as_stream(stream), static_cast<const float*>(source),
-                           static_cast<unsigned short*>(destination), static_cast<long long>(count));
-        rl::check_launch("Launch cast");
+                    "FP16 conversion requires nonempty aligned buffers.");
+        rl::cast_to_16bit(static_cast<const float*>(source), static_cast<unsigned short*>(destination),
+                          static_cast<long long>(count), true, rl::as_stream(stream));
     });
 }

@@ -1,5 +1,7 @@
 // One coalesced pass that fuses Adam, the unit-norm weight projection, the
-// target EMA and bf16 operand shadows over every tensor of a network.
+// target EMA and 16-bit operand shadows over every tensor of a network (bf16
+// for the fused learner plans, IEEE fp16 for the reference projection and EMA
+// plans).
 //
 // Reference semantics:
 //   Adam          torch.optim.Adam single-tensor path, as called from
@@ -17,7 +19,7 @@
 // tensor, so the row norm needed by the projection is a wave reduction and no
 // inter-workgroup communication is needed.  Pass 1 reads p, g, m1, m2, writes
 // the moments and the unprojected parameter and accumulates the row's squared
-// norm; pass 2 rereads the row (resident in L2), scales it, writes it, its bf16
+// norm; pass 2 rereads the row (resident in L2), scales it, writes it, its 16-bit
 // shadow and the EMA target.  All scalar step state lives on the device, so a
 // step is graph-capturable.
 #include "common.hpp"
@@ -147,6 +149,7 @@ struct StepArgs {
     const Scalars* scalars;
     float beta1, beta2, one_minus_beta1, one_minus_beta2, eps, tau;
     int form, do_adam, do_project, do_ema;
+    int shadow_f16;      // shadows hold IEEE fp16 (the reference projection/EMA plans) instead of bf16
     const int* skip;
 };
 
@@ -163,11 +166,15 @@ __device__ __forceinline__ float adam_element(const StepArgs& a, const Scalars& 
     return p - s.a * ((m1 * s.b) / (sqrtf(m2 * s.c) + a.eps));
 }
 
-// Four bf16 copies as one 8-byte store (vec4 spans start at multiples of 4 elements).
-__device__ __forceinline__ void store_bf16x4(unsigned short* dst, float4 v) {
-    const unsigned lo = static_cast<unsigned>(f32_to_bf16_bits(v.x)) | (static_cast<unsigned>(f32_to_bf16_bits(v.y)) << 16);
-    const unsigned hi = static_cast<unsigned>(f32_to_bf16_bits(v.z)) | (static_cast<unsigned>(f32_to_bf16_bits(v.w)) << 16);
-    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+// The 16-bit shadow copy of one value (bf16, or IEEE fp16 for plans whose
+// shadows are fp16; RNE either way), and of four as one 8-byte store (vec4
+// spans start at multiples of 4 elements).
+__device__ __forceinline__ unsigned short shadow_bits(const StepArgs& a, float v) {
+    return a.shadow_f16 ? f32_to_f16_bits(v) : f32_to_bf16_bits(v);
+}
+__device__ __forceinline__ void store_shadow4(const StepArgs& a, unsigned short* dst, float4 v) {
+    *reinterpret_cast<uint2*>(dst) = a.shadow_f16 ? make_uint2(f32x2_to_f16x2(v.x, v.y), f32x2_to_f16x2(v.z, v.w))
+                                                  : make_uint2(f32x2_to_bf16x2(v.x, v.y), f32x2_to_bf16x2(v.z, v.w));
 }
 
 // Pass 1 over one contiguous span: optional Adam, returns the squared norm of
@@ -223,12 +230,12 @@ __device__ void finish_span(const StepArgs& a, const Part& part, long long offse
     float* p = part.p + offset;
     auto scale = [&](float v) { return mode == 0 ? v / factor : (mode == 1 ? v * factor : v); };
     auto tail = [&](long long i, float v) {
-        if (part.shadow) part.shadow[offset + i] = f32_to_bf16_bits(v);
+        if (part.shadow) part.shadow[offset + i] = shadow_bits(a, v);
         if (a.do_ema && part.target) {
             float t = part.target[offset + i];
             t = t + a.tau * (v - t);
             part.target[offset + i] = t;
-            if (part.target_shadow) part.target_shadow[offset + i] = f32_to_bf16_bits(t);
+            if (part.target_shadow) part.target_shadow[offset + i] = shadow_bits(a, t);
         }
     };
     if (vec4) {
@@ -249,9 +256,9 @@ __device__ void finish_span(const StepArgs& a, const Part& part, long long offse
                 t.z = t.z + a.tau * (v.z - t.z);
                 t.w = t.w + a.tau * (v.w - t.w);
                 reinterpret_cast<float4*>(part.target + offset)[i] = t;
-                if (part.target_shadow) store_bf16x4(part.target_shadow + offset + 4 * i, t);
+                if (part.target_shadow) store_shadow4(a, part.target_shadow + offset + 4 * i, t);
             }
-            if (part.shadow) store_bf16x4(part.shadow + offset + 4 * i, v);
+            if (part.shadow) store_shadow4(a, part.shadow + offset + 4 * i, v);
         }
     } else {
         for (long long i = lane; i < length; i += kWave) {
@@ -311,7 +318,7 @@ __device__ void unit_row_in_registers(const StepArgs& a, const Scalars& s, const
             x.z = x.z / factor;
             x.w = x.w / factor;
             p[i] = x;
-            if (part.shadow) store_bf16x4(part.shadow + offset + 4 * i, x);
+            if (part.shadow) store_shadow4(a, part.shadow + offset + 4 * i, x);
             if (a.do_ema && part.target) {
                 float4 t = reinterpret_cast<float4*>(part.target + offset)[i];
                 t.x = t.x + a.tau * (x.x - t.x);
@@ -319,7 +326,7 @@ __device__ void unit_row_in_registers(const StepArgs& a, const Scalars& s, const
                 t.z = t.z + a.tau * (x.z - t.z);
                 t.w = t.w + a.tau * (x.w - t.w);
                 reinterpret_cast<float4*>(part.target + offset)[i] = t;
-                if (part.target_shadow) store_bf16x4(part.target_shadow + offset + 4 * i, t);
+                if (part.target_shadow) store_shadow4(a, part.target_shadow + offset + 4 * i, t);
             }
         }
     }
@@ -448,6 +455,7 @@ struct Plan {
     int has_projection = 0;
     int has_ema = 0;
     int long_rows = 0;  // a vector unit row longer than 1024 elements: step_kernel<16>
+    int shadow_f16 = 0; // shadows are IEEE fp16 (reference projection/EMA plans), else bf16
     // dynamic loss scaling (reference-compatible rl_adam_set_scaler); null when unused
     float* loss_scale = nullptr;
     int* growth_tracker = nullptr;
@@ -467,7 +475,7 @@ struct Plan {
 
 bool all_aligned16(const Part& part) {
     auto ok = [](const void* q) { return q == nullptr || aligned(q, 16); };
-    // bf16 copies take 8-byte stores of four elements
+    // 16-bit copies take 8-byte stores of four elements
     auto ok8 = [](const void* q) { return q == nullptr || aligned(q, 8); };
     return ok(part.p) && ok(part.g) && ok(part.m1) && ok(part.m2) && ok(part.target) && ok8(part.shadow) &&
            ok8(part.target_shadow);
@@ -543,6 +551,7 @@ void step(Plan* plan, int do_adam, int do_project, int do_ema, const int* skip, 
     a.do_adam = do_adam;
     a.do_project = do_project;
     a.do_ema = do_ema;
+    a.shadow_f16 = plan->shadow_f16;
     a.skip = skip;
     if (plan->long_rows)
         hipLaunchKernelGGL(step_kernel<16>, dim3(ceil_div(plan->work_count, kWaves)), dim3(kThreads), 0, stream, a);
@@ -806,7 +815,8 @@ RL_API int rl_zero_destroy(void* plan) noexcept {
 
 // robolearn/cuda/flash_kernels.cuh:398-445: one descriptor per unit row
 // (kind 0), BN (weight, bias) pair (kind 1) or RMS scale (kind 2); optional
-// shadows receive the 16-bit copy (bf16 here) of the projected first vector.
+// shadows receive the IEEE fp16 (RNE) copy of the projected first vector, as
+// the reference's __half shadows (flash_kernels.cuh:128).
 static void* create_projection(std::size_t count, const void* const* first, const void* const* second,
                                const std::size_t* lengths, const int* kinds, const void* const* shadows) {
     rl::require(count && first && lengths && kinds, "Projection requires nonempty host tables.");
@@ -826,6 +836,7 @@ static void* create_projection(std::size_t count, const void* const* first, cons
     }
     auto plan = rl::opt::build(std::move(tensors));
     plan->has_projection = 1;
+    plan->shadow_f16 = 1;
     return plan.release();
 }
 
@@ -853,7 +864,9 @@ RL_API int rl_flash_projection_destroy(void* plan) noexcept {
     return 0;
 }
 
-// robolearn/cuda/flash_kernels.cuh:447-498: target = (1 - tau) target + tau source.
+// robolearn/cuda/flash_kernels.cuh:447-498: target = (1 - tau) target + tau source;
+// optional shadows receive the IEEE fp16 (RNE) copy of the new target
+// (flash_kernels.cuh:138).
 static void* create_ema(std::size_t count, const void* const* source, const void* const* target,
                         const std::size_t* lengths, float tau, const void* const* shadows) {
     rl::require(count && source && target && lengths, "EMA requires nonempty host tables.");
@@ -873,6 +886,7 @@ static void* create_ema(std::size_t count, const void* const* source, const void
     auto plan = rl::opt::build(std::move(tensors));
     plan->tau = tau;
     plan->has_ema = 1;
+    plan->shadow_f16 = 1;
     return plan.release();
 }
 

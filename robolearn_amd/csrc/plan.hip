@@ -5,9 +5,12 @@
 //
 // The column-major product is executed by the row-major kernel family as
 // D^T = op(B)^T . op(A)^T: rows of the row-major view are the reference's n,
-// columns its m.  input_dtype 1 means 16-bit operands in memory, which on
-// MI355X are bf16 (RNE) instead of fp16; input_dtype 2 keeps fp32 storage and
-// rounds operands to bf16 on load.  Split-K uses the caller's workspace.
+// columns its m.  input_dtype 1 means IEEE fp16 operands in memory, as the
+// reference's (the copies rl_cast_f32_f16 writes), multiplied on the fp16
+// matrix cores (v_mfma_f32_32x32x16_f16) with fp32 accumulation and output.
+// Two precisions the reference does not have: input_dtype 2 keeps fp32 storage
+// and rounds operands to bf16 on load, input_dtype 3 reads bf16 operands (the
+// copies rl_cast_f32_bf16 writes).  Split-K uses the caller's workspace.
 #include "gemm.hpp"
 
 #include <cmath>
@@ -25,14 +28,14 @@ namespace {
 
 struct DensePlan {
     int m, n, k, transa, transb, lda, ldb, ldd, use_bias;
-    int mode, operands_bf16, splits;
+    int mode, operands_16bit, splits;  // mode: rl_gemm's (0 fp32, 1 bf16, 3 fp16)
     std::size_t workspace_bytes;
     std::string metadata;
 };
 
 int choose_splits(int rows, int cols, int k, int mode) {
     const long long tiles = static_cast<long long>((rows + 127) / 128) * ((cols + 127) / 128);
-    const int kt = mode == 1 ? 32 : 16;
+    const int kt = mode == 0 ? 16 : 32;
     const int ktiles = (k + kt - 1) / kt;
     int splits = 1;
     while (tiles * splits < 256 && splits * 2 <= ktiles / 4 && splits < 64) splits *= 2;
@@ -45,7 +48,8 @@ void* create_plan(int m, int n, int k, int transa, int transb, int lda, int ldb,
     rl::require(m > 0 && n > 0 && k > 0, "Dense plan dimensions must be positive.");
     rl::require((transa == 0 || transa == 1) && (transb == 0 || transb == 1), "Transpose flags must be 0 or 1.");
     rl::require(lda >= (transa ? k : m) && ldb >= (transb ? n : k) && ldd >= m, "Leading dimensions are too small.");
-    rl::require(input_dtype >= 0 && input_dtype <= 2, "input_dtype must be 0 (fp32), 1 (bf16) or 2 (fp32 stored, bf16 compute).");
+    rl::require(input_dtype >= 0 && input_dtype <= 3,
+                "input_dtype must be 0 (fp32), 1 (fp16), 2 (fp32 stored, bf16 compute) or 3 (bf16).");
     auto plan = std::make_unique<DensePlan>();
     plan->m = m;
     plan->n = n;
@@ -56,8 +60,8 @@ void* create_plan(int m, int n, int k, int transa, int transb, int lda, int ldb,
     plan->ldb = ldb;
     plan->ldd = ldd;
     plan->use_bias = use_bias != 0;
-    plan->mode = input_dtype == 0 ? 0 : 1;
-    plan->operands_bf16 = input_dtype == 1;
+    plan->mode = input_dtype == 0 ? 0 : (input_dtype == 1 ? 3 : 1);
+    plan->operands_16bit = input_dtype == 1 || input_dtype == 3;
     int splits = choose_splits(n, m, k, plan->mode);
     std::size_t bytes = rl_gemm_workspace(plan->mode, n, m, k, 1, splits);
     while (splits > 1 && bytes > workspace_limit) {
@@ -66,7 +70,9 @@ void* create_plan(int m, int n, int k, int transa, int transb, int lda, int ldb,
     }
     plan->splits = splits;
     plan->workspace_bytes = bytes;
-    plan->metadata = "{\"kernel\":\"mfma_128x128\",\"mode\":\"" + std::string(plan->mode ? "bf16" : "fp32") +
+    const char* precision = plan->mode == 0 ? "fp32" : (plan->mode == 3 ? "fp16" : "bf16");
+    plan->metadata = "{\"kernel\":\"" + std::string(plan->mode ? "mfma_256x128" : "mfma_128x128") +
+                     "\",\"mode\":\"" + std::string(precision) +
                      "\",\"split_k\":" + std::to_string(splits) + ",\"workspace_bytes\":" + std::to_string(bytes) +
                      ",\"autotuned\":false}";
     return plan.release();
@@ -132,8 +138,8 @@ RL_API int rl_plan_run(void* opaque, const void* a, const void* b, const void* c
         // Row-major view: A_rm = op(B)^T (n x k), B_rm = op(A)^T, D_rm (n x m).
         const int a_kcontig = plan->transb == 0;
         const int b_kcontig = plan->transa == 1;
-        const int bf = plan->operands_bf16;
-        rl::run_gemm(plan->mode, bf, bf, a_kcontig, b_kcontig, plan->n, plan->m, plan->k, 1, b, plan->ldb, 0, a,
+        const int h = plan->operands_16bit;
+        rl::run_gemm(plan->mode, h, h, a_kcontig, b_kcontig, plan->n, plan->m, plan->k, 1, b, plan->ldb, 0, a,
                      plan->lda, 0, static_cast<const float*>(c), static_cast<float*>(d), plan->ldd, 0,
                      plan->use_bias ? static_cast<const float*>(bias) : nullptr, 0, beta, 0, plan->splits,
                      static_cast<float*>(workspace), workspace_bytes, rl::as_stream(stream), nullptr, nullptr, nullptr);

@@ -14,6 +14,9 @@ BF16 = 1
 # fp32 operands and results with the products formed on the bf16 matrix cores from exact
 # three-piece bf16 splits of every operand value (fp32-accurate)
 FP32_SPLIT = 2
+# IEEE fp16 operands on the fp16 matrix cores (float16 tensors as stored, float32 ones rounded to fp16 on
+# load), fp32 accumulation and output: the precision of the reference's mixed dense plans
+FP16 = 3
 EPILOGUES = {None: 0, "relu": 1, "elu": 2, "elu_grad": 3}
 
 
@@ -45,6 +48,16 @@ def _is_bf16(tensor: torch.Tensor) -> int:
     return 1 if tensor.dtype == torch.bfloat16 else 0
 
 
+def _operand_flag(tensor: torch.Tensor, mode: int) -> int:
+    """1 for a 16-bit operand (bfloat16 in the bf16 mode, float16 in the fp16 mode), 0 for float32."""
+    if tensor.dtype == torch.float32:
+        return 0
+    expected = torch.float16 if mode == FP16 else torch.bfloat16
+    if tensor.dtype != expected:
+        raise ValueError(f"GEMM mode {mode} takes float32 or {expected} operands, got {tensor.dtype}.")
+    return 1
+
+
 def gemm(
     a, b, d, *, m, n, k, batch=1, a_kcontig, b_kcontig, lda, ldb, ldd, stride_a=0, stride_b=0, stride_d=0,
     c=None, beta=0.0, bias=None, stride_bias=0, epilogue=None, mode=FP32, splits=1, workspace=None, d_bf16=None,
@@ -60,7 +73,7 @@ def gemm(
         d, d_bf16 = None, d
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     _native.call(
-        "rl_gemm", mode, _is_bf16(a), _is_bf16(b), int(a_kcontig), int(b_kcontig), m, n, k, batch, ptr(a), lda,
+        "rl_gemm", mode, _operand_flag(a, mode), _operand_flag(b, mode), int(a_kcontig), int(b_kcontig), m, n, k, batch, ptr(a), lda,
         stride_a, ptr(b), ldb, stride_b, ptr(c), ptr(d), ldd, stride_d, ptr(bias), stride_bias, float(beta),
         EPILOGUES[epilogue], splits, ptr(workspace), ws_bytes, ptr(d_bf16), ptr(moments), ptr(a_sums), stream(),
     )

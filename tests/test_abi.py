@@ -48,11 +48,17 @@ def test_status_convention_reports_validation_errors():
 
 def test_dense_plan_metadata_and_workspace_on_host():
     library = _native.load()
-    plan = _native.create("rl_plan_create_mixed", 1024, 8192, 160, 1, 0, 160, 160, 1024, 0, 0, 1, 64 << 20)
-    metadata = library.rl_plan_tuning_metadata(plan).decode()
-    assert '"mode":"bf16"' in metadata
-    assert library.rl_plan_workspace(plan) <= 64 << 20
-    assert library.rl_plan_destroy(plan) == 0
+    # input_dtype 1 is the reference's IEEE fp16; 3 (bf16 operands) and 2 (fp32 stored, bf16 compute) are this
+    # library's additions
+    for input_dtype, precision in ((1, "fp16"), (2, "bf16"), (3, "bf16")):
+        plan = _native.create("rl_plan_create_mixed", 1024, 8192, 160, 1, 0, 160, 160, 1024, 0, 0, input_dtype,
+                              64 << 20)
+        metadata = library.rl_plan_tuning_metadata(plan).decode()
+        assert f'"mode":"{precision}"' in metadata
+        assert library.rl_plan_workspace(plan) <= 64 << 20
+        assert library.rl_plan_destroy(plan) == 0
+    assert not library.rl_plan_create_mixed(64, 64, 64, 0, 0, 64, 64, 64, 0, 0, 4, 0)
+    assert "input_dtype" in _native.last_error()
 
 
 def test_exports_have_c_linkage():

@@ -103,6 +103,40 @@ def test_bf16_operand_tensors(gpu):
     torch.testing.assert_close(y.cpu().double(), ref, rtol=1e-5, atol=1e-4)
 
 
+# fp16 mode (the reference's mixed-plan precision): float16 operands as stored, float32 operands
+# rounded to fp16 on load; both layouts, an edge-tiled shape, split-K and the fused epilogue
+@pytest.mark.parametrize("a_dtype,b_dtype", [(torch.float16, torch.float16), (torch.float32, torch.float16),
+                                             (torch.float16, torch.float32), (torch.float32, torch.float32)])
+@pytest.mark.parametrize("a_kcontig,b_kcontig", [(True, True), (True, False), (False, True), (False, False)])
+@pytest.mark.parametrize("batch,m,n,k,splits", [(2, 300, 136, 200, 1), (1, 64, 96, 1024, 4)])
+def test_fp16_gemm_matches_rounded_operands(gpu, a_dtype, b_dtype, a_kcontig, b_kcontig, batch, m, n, k, splits):
+    print(f"case fp16 gemm {a_dtype}x{b_dtype} a_k={a_kcontig} b_k={b_kcontig} {batch}x{m}x{n}x{k} "
+          f"splits={splits}", flush=True)
+    g = torch.Generator().manual_seed(m + n + k + 2 * a_kcontig + b_kcontig)
+    a = torch.randn(batch, m, k, generator=g) * 4
+    b = torch.randn(batch, n, k, generator=g)
+    bias = torch.randn(batch, n, generator=g)
+    c = torch.randn(batch, m, n, generator=g)
+    a_mem = (a if a_kcontig else a.transpose(1, 2)).contiguous().to(a_dtype)
+    b_mem = (b if b_kcontig else b.transpose(1, 2)).contiguous().to(b_dtype)
+    ref = torch.einsum("bmk,bnk->bmn", a.to(torch.float16).double(), b.to(torch.float16).double())
+    scale = torch.einsum("bmk,bnk->bmn", a.to(torch.float16).double().abs(), b.to(torch.float16).double().abs())
+    workspace = torch.empty(splits * batch * (m * n + m) * 4, dtype=torch.uint8, device=gpu) if splits > 1 else None
+    d = torch.full((batch, m, n), float("nan"), device=gpu)
+    K.gemm(a_mem.to(gpu), b_mem.to(gpu), d, m=m, n=n, k=k, batch=batch, a_kcontig=a_kcontig, b_kcontig=b_kcontig,
+           lda=k if a_kcontig else m, ldb=k if b_kcontig else n, ldd=n, stride_a=m * k, stride_b=n * k,
+           stride_d=m * n, mode=K.FP16, splits=splits, workspace=workspace, bias=bias.to(gpu), stride_bias=n,
+           epilogue="relu", c=c.to(gpu), beta=0.5)
+    expected = torch.relu(ref + bias.double()[:, None, :]) + 0.5 * c.double()
+    # exact fp16 products, fp32 accumulation: a few fp32 ulps of the absolute-value product per term
+    err = (d.cpu().double() - expected).abs()
+    assert (err <= 2e-7 * scale * math.sqrt(k) + 1e-6).all(), err.max().item()
+    with pytest.raises(ValueError, match="float16"):
+        K.gemm(a_mem.to(torch.bfloat16).to(gpu), b_mem.to(gpu), d, m=m, n=n, k=k, batch=batch, a_kcontig=a_kcontig,
+               b_kcontig=b_kcontig, lda=k if a_kcontig else m, ldb=k if b_kcontig else n, ldd=n, stride_a=m * k,
+               stride_b=n * k, stride_d=m * n, mode=K.FP16)
+
+
 # channels 64, 160 and 1024 take the float4 elementwise kernels (160: a partial
 # column block), 5 and 130 the scalar ones
 @pytest.mark.parametrize("ensemble,rows,channels,relu", [(1, 1000, 5, False), (2, 777, 130, True), (2, 300, 64, True),

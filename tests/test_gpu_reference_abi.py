@@ -160,7 +160,8 @@ def test_projection_and_ema_plans_match_oracle(gpu):
     host = OrderedDict([("block.weight", torch.randn(rows, cols)), ("block.norm.weight", torch.randn(channels)),
                         ("block.norm.bias", torch.randn(channels)), ("post_norm.weight", torch.randn(channels) * 3)])
     dev = OrderedDict((k, v.to(gpu)) for k, v in host.items())
-    shadows = OrderedDict((k, torch.zeros(v.shape, dtype=torch.bfloat16, device=gpu)) for k, v in host.items())
+    # the reference's shadows are __half (flash_kernels.cuh:63-70, 128, 138): IEEE fp16
+    shadows = OrderedDict((k, torch.zeros(v.shape, dtype=torch.float16, device=gpu)) for k, v in host.items())
     first, second, lengths, kinds, shadow = [], [], [], [], []
     for r in range(rows):  # one descriptor per unit row (flash_kernels.cuh:398-445)
         first.append(dev["block.weight"][r].data_ptr()); second.append(None); lengths.append(cols); kinds.append(0)
@@ -174,9 +175,11 @@ def test_projection_and_ema_plans_match_oracle(gpu):
     target = OrderedDict((k, torch.randn_like(v)) for k, v in host.items())
     target_dev = OrderedDict((k, v.to(gpu)) for k, v in target.items())
     tau = 0.125
-    ema = N.create("rl_flash_ema_create", len(dev), N.pointer_array([v.data_ptr() for v in dev.values()]),
+    target_shadows = OrderedDict((k, torch.zeros(v.shape, dtype=torch.float16, device=gpu)) for k, v in host.items())
+    ema = N.create("rl_flash_ema_create_with_shadows", len(dev), N.pointer_array([v.data_ptr() for v in dev.values()]),
                    N.pointer_array([v.data_ptr() for v in target_dev.values()]),
-                   N.size_array([v.numel() for v in dev.values()]), tau)
+                   N.size_array([v.numel() for v in dev.values()]), tau,
+                   N.pointer_array([v.data_ptr() for v in target_shadows.values()]))
     try:
         N.call("rl_flash_projection_step", plan, STREAM)
         N.call("rl_flash_ema_step", ema, STREAM)
@@ -187,7 +190,9 @@ def test_projection_and_ema_plans_match_oracle(gpu):
             torch.testing.assert_close(dev[k].cpu(), host[k], rtol=1e-5, atol=1e-6)
             torch.testing.assert_close(target_dev[k].cpu(), target[k], rtol=1e-5, atol=1e-6)
         for k in ("block.weight", "block.norm.weight", "post_norm.weight"):
-            assert torch.equal(shadows[k], dev[k].to(torch.bfloat16)), k
+            assert torch.equal(shadows[k], dev[k].to(torch.float16)), k
+        for k in host:
+            assert torch.equal(target_shadows[k], target_dev[k].to(torch.float16)), k
         norms = dev["block.weight"].norm(dim=1)
         torch.testing.assert_close(norms, torch.ones_like(norms), rtol=1e-5, atol=1e-5)
     finally:
@@ -195,15 +200,51 @@ def test_projection_and_ema_plans_match_oracle(gpu):
         N.call("rl_flash_ema_destroy", ema)
 
 
-@pytest.mark.parametrize("count,offset", [(1, 0), (1001, 0), (4096, 1), (70001, 3)])
-def test_cast_f32_f16_writes_bf16(gpu, count, offset):
+# IEEE binary16 edge cases: ties to even, the largest finite half, the overflow threshold
+# (65520 rounds to infinity), subnormals down to half the smallest one, signed zero, infinities
+F16_EDGES = [1.0 + 2.0**-11, 1.0 + 3 * 2.0**-11, 65504.0, 65519.0, 65520.0, -65520.0, 1e6, 2.0**-14, 2.0**-24,
+             2.0**-25, 3 * 2.0**-26, 2.0**-26, -0.0, float("inf"), float("-inf"), 6.1e-5, 1e-8, -3.0e-7]
+
+
+@pytest.mark.parametrize("count,offset", [(1, 0), (3, 1), (1001, 0), (4096, 1), (70001, 3)])
+def test_cast_f32_f16_writes_ieee_half(gpu, count, offset):
+    """rl_cast_f32_f16 (kernels.cu:663-687, __float2half_rn): round-to-nearest-even IEEE fp16,
+    bit for bit against torch's float32 -> float16 conversion, on the vector path (16-byte aligned
+    source) and the element path, with the count % 4 tail."""
     source = torch.randn(count + offset, device=gpu) * 100
-    source[offset] = 1.0 + 2.0**-8  # a tie: round-to-nearest-even keeps 1.0
-    out = torch.zeros(count + offset, dtype=torch.bfloat16, device=gpu)
+    edges = torch.tensor(F16_EDGES, device=gpu)
+    source[offset:offset + min(count, len(edges))] = edges[:count]
+    if count > len(edges):
+        source[-1] = float("nan")
+    out = torch.zeros(count + offset, dtype=torch.float16, device=gpu)
     N.call("rl_cast_f32_f16", _ptr(source[offset:]), _ptr(out[offset:]), count, STREAM)
     torch.cuda.synchronize()
-    assert torch.equal(out[offset:], source[offset:].to(torch.bfloat16))
-    assert float(out[offset]) == 1.0
+    expected = source[offset:].to(torch.float16)
+    got = out[offset:]
+    nan = torch.isnan(expected)
+    assert torch.equal(torch.isnan(got), nan)
+    assert torch.equal(got[~nan].view(torch.int16), expected[~nan].view(torch.int16))
+    if count >= 7:
+        host = got[:7].cpu().double().tolist()
+        assert host[:2] == [1.0, 1.0 + 2.0**-9]  # ties to the even neighbour
+        assert host[2:5] == [65504.0, 65504.0, float("inf")] and host[5:7] == [float("-inf"), float("inf")]
+    if count >= 13:
+        host = got[7:13].cpu().double().tolist()
+        # 2^-25 is the tie between 0 and the smallest subnormal: even is 0
+        assert host == [2.0**-14, 2.0**-24, 0.0, 2.0**-24, 0.0, 0.0]
+        assert got[12].view(torch.int16).item() == -32768  # -0.0 keeps its sign
+
+
+@pytest.mark.parametrize("count", [1, 1001, 70001])
+def test_cast_f32_bf16_rounds_to_nearest_even(gpu, count):
+    source = torch.randn(count + 1, device=gpu) * 100
+    source[1] = 1.0 + 2.0**-8  # a tie: round-to-nearest-even keeps 1.0
+    out = torch.zeros(count + 1, dtype=torch.bfloat16, device=gpu)
+    for offset in (0, 1):
+        N.call("rl_cast_f32_bf16", _ptr(source[offset:]), _ptr(out[offset:]), count, STREAM)
+        torch.cuda.synchronize()
+        assert torch.equal(out[offset:offset + count], source[offset:offset + count].to(torch.bfloat16))
+    assert float(out[1]) == 1.0
 
 
 def test_batchnorm_16bit_side_outputs(gpu):
@@ -219,7 +260,7 @@ def test_batchnorm_16bit_side_outputs(gpu):
         mean, var = torch.zeros(channels, device=gpu), torch.zeros(channels, device=gpu)
         partial = torch.zeros(2 * chunks * channels, device=gpu)
         y = torch.zeros(batch, channels, device=gpu)
-        half = torch.zeros(batch, channels, dtype=torch.bfloat16, device=gpu)
+        half = torch.zeros(batch, channels, dtype=torch.float16, device=gpu)
         args = [_ptr(t) for t in (x, w, b, rm, rv, mean, var, partial, y)]
         if with_half:
             N.call("rl_flash_bn_forward_with_fp16", *args, _ptr(half), batch, channels, eps, momentum, 1, 1, STREAM)
@@ -229,7 +270,7 @@ def test_batchnorm_16bit_side_outputs(gpu):
         sums = torch.zeros(2 * channels, device=gpu)
         dx, dw, db = (torch.zeros(batch, channels, device=gpu), torch.zeros(channels, device=gpu),
                       torch.zeros(channels, device=gpu))
-        half_dx = torch.zeros(batch, channels, dtype=torch.bfloat16, device=gpu)
+        half_dx = torch.zeros(batch, channels, dtype=torch.float16, device=gpu)
         back = [_ptr(t) for t in (x, dy, y, w, mean, var, partial, sums, dx, dw, db)]
         if with_half:
             N.call("rl_flash_bn_backward_with_fp16", *back, _ptr(half_dx), batch, channels, eps, 1, 1, STREAM)
@@ -241,8 +282,34 @@ def test_batchnorm_16bit_side_outputs(gpu):
     y0, _, dx0, _, dw0, db0 = run(False)
     y1, half, dx1, half_dx, dw1, db1 = run(True)
     assert torch.equal(y0, y1) and torch.equal(dx0, dx1) and torch.equal(dw0, dw1) and torch.equal(db0, db1)
-    assert torch.equal(half, y1.to(torch.bfloat16))
-    assert torch.equal(half_dx, dx1.to(torch.bfloat16))
+    # flash_kernels.cuh:28: the 16-bit outputs are the exact IEEE fp16 rounding of the retained fp32 values
+    assert torch.equal(half, y1.to(torch.float16))
+    assert torch.equal(half_dx, dx1.to(torch.float16))
     with pytest.raises(RuntimeError, match="nonnull"):
         N.call("rl_flash_bn_forward_with_fp16", *[_ptr(t) for t in (x, w, b, x, x, x, x, x, x)], None, batch,
                channels, eps, momentum, 1, 1, STREAM)
+    # rl_flash_bn_backward_controlled (flash_kernels.cuh:598-609): overwrite_dx 1 replaces dx, 0 adds to it
+    dy = torch.randn(batch, channels, device=gpu, generator=torch.Generator(device=gpu).manual_seed(3))
+    mean, var = torch.zeros(channels, device=gpu), torch.zeros(channels, device=gpu)
+    partial = torch.zeros(2 * chunks * channels, device=gpu)
+    y = torch.zeros(batch, channels, device=gpu)
+    N.call("rl_flash_bn_forward", *[_ptr(t) for t in (x, w, b, torch.zeros(channels, device=gpu),
+                                                      torch.ones(channels, device=gpu), mean, var, partial, y)],
+           batch, channels, eps, momentum, 1, 1, STREAM)
+    prefill = torch.randn(batch, channels, device=gpu)
+    for overwrite in (1, 0):
+        dx = prefill.clone()
+        dw, db = torch.zeros(channels, device=gpu), torch.zeros(channels, device=gpu)
+        half_dx = torch.zeros(batch, channels, dtype=torch.float16, device=gpu)
+        sums = torch.zeros(2 * channels, device=gpu)
+        N.call("rl_flash_bn_backward_controlled", *[_ptr(t) for t in (x, dy, y, w, mean, var, partial, sums, dx, dw,
+                                                                      db, half_dx)],
+               overwrite, batch, channels, eps, 1, 1, STREAM)
+        torch.cuda.synchronize()
+        expected = dx0 if overwrite else prefill + dx0
+        assert torch.equal(dx, expected), overwrite
+        assert torch.equal(half_dx, dx.to(torch.float16)), overwrite
+        assert torch.equal(dw, dw0) and torch.equal(db, db0)
+    with pytest.raises(RuntimeError, match="dx"):
+        N.call("rl_flash_bn_backward_controlled", *[_ptr(t) for t in (x, dy, y, w, mean, var, partial, sums)], None,
+               _ptr(dw), _ptr(db), None, 1, batch, channels, eps, 1, 1, STREAM)

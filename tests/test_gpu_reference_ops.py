@@ -8,12 +8,13 @@ a reference caller pointed at this library runs exactly these:
   D = op(A) op(B) + beta C + bias[m] (robolearn/cuda/kernels.cu:528-538,
   698-731; cuBLASLt semantics), all four transpose combinations, beta 0 and 1,
   with and without bias, padded leading dimensions, split-K shapes; fp32
-  operands (input_dtype 0), 16-bit operands written by rl_cast_f32_f16
+  operands (input_dtype 0), IEEE fp16 operands written by rl_cast_f32_f16
   (input_dtype 1, the CudaLinear path, robolearn/cuda/linear.py:82-138, 190),
-  and fp32 storage with 16-bit compute (input_dtype 2).  The 16-bit reference
-  is the float64 product of the bf16-rounded operands, which also shows that
-  the 16-bit producer (rl_cast_f32_f16) and consumer (the mixed plan) agree on
-  the format;
+  and this library's bf16 precisions: fp32 storage with bf16 compute
+  (input_dtype 2) and bf16 operands written by rl_cast_f32_bf16 (input_dtype 3).
+  The 16-bit reference is the float64 product of the operands rounded by
+  torch to float16 (bfloat16), which also shows that each 16-bit producer and
+  the mixed plan agree on the format;
 * rl_flash_categorical_forward / _backward / _target
   (categorical_kernels.cuh:31-110, 126-176): log-softmax and expectation;
   the gradient from both dlog_probs and dvalues accumulated into draw and the
@@ -45,11 +46,11 @@ def _column_major(matrix, ld, device, dtype=torch.float32):
     return storage.to(device).contiguous()
 
 
-def _bf16_round(x):
-    return x.to(torch.float32).to(torch.bfloat16).to(torch.float64)
+def _round16(x, dtype):
+    return x.to(torch.float32).to(dtype).to(torch.float64)
 
 
-@pytest.mark.parametrize("input_dtype", [0, 1, 2])
+@pytest.mark.parametrize("input_dtype", [0, 1, 2, 3])
 @pytest.mark.parametrize("transa,transb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("m,n,k", [(96, 80, 72), (300, 257, 1100)])
 def test_plan_run_matches_float64(gpu, input_dtype, transa, transb, m, n, k):
@@ -62,11 +63,13 @@ def test_plan_run_matches_float64(gpu, input_dtype, transa, transb, m, n, k):
     lda, ldb, ldd = a_stored.shape[0] + 3, b_stored.shape[0] + 5, m + 2
     a_dev = _column_major(a_stored, lda, gpu)
     b_dev = _column_major(b_stored, ldb, gpu)
-    if input_dtype == 1:  # 16-bit operands written by the reference's cast entry point
-        a16 = torch.empty(a_dev.numel(), dtype=torch.bfloat16, device=gpu)
-        b16 = torch.empty(b_dev.numel(), dtype=torch.bfloat16, device=gpu)
+    half = {1: torch.float16, 2: torch.bfloat16, 3: torch.bfloat16}.get(input_dtype)
+    if input_dtype in (1, 3):  # 16-bit operands written by the cast entry point of that format
+        cast = "rl_cast_f32_f16" if input_dtype == 1 else "rl_cast_f32_bf16"
+        a16 = torch.empty(a_dev.numel(), dtype=half, device=gpu)
+        b16 = torch.empty(b_dev.numel(), dtype=half, device=gpu)
         for src, dst in ((a_dev, a16), (b_dev, b16)):
-            _native.call("rl_cast_f32_f16", src.data_ptr(), dst.data_ptr(), src.numel(), _stream())
+            _native.call(cast, src.data_ptr(), dst.data_ptr(), src.numel(), _stream())
         a_arg, b_arg = a16, b16
     else:
         a_arg, b_arg = a_dev, b_dev
@@ -83,7 +86,7 @@ def test_plan_run_matches_float64(gpu, input_dtype, transa, transb, m, n, k):
 
     plans = {True: make(True), False: make(False)}
     try:
-        exact_a, exact_b = (opa, opb) if input_dtype == 0 else (_bf16_round(opa), _bf16_round(opb))
+        exact_a, exact_b = (opa, opb) if input_dtype == 0 else (_round16(opa, half), _round16(opb, half))
         product = exact_a @ exact_b  # m x n
         scale = (exact_a.abs() @ exact_b.abs()).max().item()
         tol = 2e-6 * scale * max(1.0, k / 256)
