@@ -83,16 +83,17 @@ def forward_split_count(m, n, k, batch, mode):
     """K splits for a forward or input-gradient product whose output tiles cannot fill the GPU (a
     narrow head, or a narrow layer over a long K at a small batch).
 
-    bf16 (the heads): 256x128 tiles, at least 256 workgroups, each split >= 256 of K.  A bf16 block
-    product is not split even where its tiles leave CUs idle (README shape): the split loses the
-    BatchNorm moments of the 256x256 kernel's epilogue and adds a reduction, which measured slower.
+    bf16 (heads, embedder input gradients, block input gradients): 256x128 tiles, at least 256
+    workgroups, each split >= 128 of K.  A bf16 block forward product is not split even where its
+    tiles leave CUs idle (README shape): the split loses the BatchNorm moments of the 256x256 kernel's
+    epilogue and adds a reduction, which measured slower.
     fp32: 64x64 tiles, whose K loop is latency-bound when few workgroups share a CU; at least 1024
     workgroups, each split >= 128 of K (four 32-deep steps)."""
     splits = 1
     if mode == BF16:
         tiles = ((m + 255) // 256) * ((n + 127) // 128) * batch
         ktiles = (k + 31) // 32
-        while tiles * splits < 256 and splits * 2 <= max(1, ktiles // 8) and splits < 16:
+        while tiles * splits < 256 and splits * 2 <= max(1, ktiles // 4) and splits < 16:
             splits *= 2
         return splits
     tiles = ((m + 63) // 64) * ((n + 63) // 64) * batch
@@ -161,16 +162,19 @@ def transpose16(src, dst, *, batch, rows, cols):
 def split_count(m, n, k, batch, mode):
     """K splits for a weight-gradient product (small output, K = rows).
 
-    bf16: at least two 256x128-tile workgroups per CU, each split >= 512 of K; >= 256 of K
+    bf16: at least two 256x128-tile workgroups per CU, each split >= 1024 of K; >= 256 of K
     when the output does not tile by 256 (a narrow head or embedder: those products run on
-    the 256x128 kernel, whose workgroups are short enough that more of them pays).
+    the 256x128 kernel, whose workgroups are short enough that more of them pays).  For the
+    256x256-tile kernel a longer split beats more workgroups: its partials cost a write and a
+    read of splits x M x N floats (README dW 2048 x 512 over 4096 rows: 44 us at 4 splits, 52 us
+    at 8).
     fp32: the MFMA-issue-bound fp32 kernel runs 64x64 tiles for such products;
     at least 1024 workgroups (four per CU), each split >= 64 of K."""
     splits = 1
     if mode == BF16:
         tiles = ((m + 255) // 256) * ((n + 127) // 128) * batch
         ktiles = (k + 31) // 32
-        min_ktiles = 16 if m % 256 == 0 and n % 256 == 0 else 8
+        min_ktiles = 32 if m % 256 == 0 and n % 256 == 0 else 8
         while tiles * splits < 512 and splits * 2 <= max(1, ktiles // min_ktiles) and splits < 64:
             splits *= 2
         return splits

@@ -379,7 +379,7 @@ class Trunk:
             d_u2 = self.op(self.d_u2, self.d_u2_h)
             K.linear_backward_input(d_u2, w[f"{pre}.w2{self.linear}"], self.d_r1, rows=rows, in_dim=4 * h,
                                     out_dim=h, ensemble=E, mode=mode, wt=wt.get(f"{pre}.w2{self.linear}"),
-                                    workspace=None if self.bf else workspace)
+                                    workspace=workspace)
             if g is not None:
                 K.linear_backward_weight(d_u2, self.op(self.r1[i], self.r1_h[i]), g[f"{pre}.w2{self.linear}"],
                                          rows=rows, in_dim=4 * h, out_dim=h, ensemble=E, mode=mode,
@@ -395,7 +395,7 @@ class Trunk:
             K.linear_backward_input(d_r1, w[f"{pre}.w1{self.linear}"], self.d_stream, rows=rows, in_dim=h,
                                     out_dim=4 * h, ensemble=E, mode=mode, c=self.d_stream, beta=1.0,
                                     d_bf16=self.d_stream_h if i == 0 else None,
-                                    wt=wt.get(f"{pre}.w1{self.linear}"), workspace=None if self.bf else workspace)
+                                    wt=wt.get(f"{pre}.w1{self.linear}"), workspace=workspace)
             if g is not None:
                 K.linear_backward_weight(d_r1, self.op(self.stream[i], self.stream_h[i]), g[f"{pre}.w1{self.linear}"],
                                          rows=rows, in_dim=h, out_dim=4 * h, ensemble=E, mode=mode,
@@ -407,7 +407,7 @@ class Trunk:
         if g is None and input_grad is None:
             return
         K.linear_backward_input(d_stream, w["embedder.w" + self.linear], self.dy0, rows=rows, in_dim=self.in_dim,
-                                out_dim=h, ensemble=E, mode=mode)
+                                out_dim=h, ensemble=E, mode=mode, workspace=workspace)
         name = "embedder.norm"
         mean, var = self._stats(name, running, training)
         K.bn_backward(x, self.dy0, None, p[name + ".weight"], mean, var, self.partial, self.sums, input_grad,
