@@ -88,7 +88,9 @@ def forward_split_count(m, n, k, batch, mode):
     tiles leave CUs idle (README shape): the split loses the BatchNorm moments of the 256x256 kernel's
     epilogue and adds a reduction, which measured slower.
     fp32: 64x64 tiles, whose K loop is latency-bound when few workgroups share a CU; at least 1024
-    workgroups, each split >= 128 of K (four 32-deep steps)."""
+    workgroups, each split >= 256 of K: a split costs a reduction launch, which a shorter K loop
+    repays only past that (Cartpole input gradient 1024 x 1024 over K = 256: 17.8 us unsplit, 25.2 us
+    in two splits)."""
     splits = 1
     if mode == BF16:
         tiles = ((m + 255) // 256) * ((n + 127) // 128) * batch
@@ -97,7 +99,7 @@ def forward_split_count(m, n, k, batch, mode):
             splits *= 2
         return splits
     tiles = ((m + 63) // 64) * ((n + 63) // 64) * batch
-    while tiles * splits < 1024 and k // (2 * splits) >= 128 and splits < 16:
+    while tiles * splits < 1024 and k // (2 * splits) >= 256 and splits < 16:
         splits *= 2
     return splits
 
@@ -168,8 +170,11 @@ def split_count(m, n, k, batch, mode):
     256x256-tile kernel a longer split beats more workgroups: its partials cost a write and a
     read of splits x M x N floats (README dW 2048 x 512 over 4096 rows: 44 us at 4 splits, 52 us
     at 8).
-    fp32: the MFMA-issue-bound fp32 kernel runs 64x64 tiles for such products;
-    at least 1024 workgroups (four per CU), each split >= 64 of K."""
+    fp32: the MFMA-issue-bound fp32 kernel runs 64x64 tiles for such products; at least 1024
+    workgroups (four per CU), each split >= 256 of K, whose reduction then costs less than the
+    shorter K loops save (Cartpole 256 x 1024 over 1024 rows: 23.6 us in 4 splits, 25.9 in 8); an
+    output of at most 65,536 values (a head) takes splits down to 64 of K, since its reduction is
+    nearly free."""
     splits = 1
     if mode == BF16:
         tiles = ((m + 255) // 256) * ((n + 127) // 128) * batch
@@ -180,7 +185,8 @@ def split_count(m, n, k, batch, mode):
         return splits
     tiles = ((m + 63) // 64) * ((n + 63) // 64) * batch
     steps = (k + 15) // 16
-    while tiles * splits < 1024 and splits * 2 <= max(1, steps // 4) and splits < 256:
+    min_steps = 4 if m * n * batch <= 65536 else 16
+    while tiles * splits < 1024 and splits * 2 <= max(1, steps // min_steps) and splits < 256:
         splits *= 2
     return splits
 
