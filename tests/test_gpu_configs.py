@@ -205,6 +205,69 @@ def test_g1_pair_graph_matches_oracle(gpu):
         assert cosine > 0.9, (label, drift, cosine)
 
 
+def test_g1_bf16_drift_over_100_updates(gpu):
+    """The north star's 100-update drift at the headline shape: the bf16 learner (bf16 operands, bf16
+    BatchNorm activations) and the fp32 learner start from the same weights and replay and run 50
+    captured UTD-2 pairs each; with the same seed their device samplers draw the same indices and
+    noise.  The fp32 learner is the reference of the drift, being itself held to the oracle (the
+    Cartpole and README tests above and in test_gpu_readme_shape.py).  Reported: the relative L2
+    distance of the parameters after 100 updates, the same over the fp32 learner's own movement, and
+    the largest relative difference of each loss over the run (printed, and written as JSON to
+    $RL_DRIFT_REPORT with the suffix _g1 when set)."""
+    import json
+
+    from robolearn_amd.flashsac import FlashSAC
+
+    print("case c2 G1: bf16 vs fp32 learner over 100 updates (50 captured pairs)", flush=True)
+    w = G1
+    cfg = _config(w)
+    store = O.synthetic_replay(cfg.buffer_max_length, w["obs"], w["act"], seed=0, gamma=cfg.gamma,
+                               reward_std=w["reward_std"], done_prob=w["done"])
+    low = FlashSAC(w["obs"], w["act"], num_envs=w["envs"], cfg=cfg)
+    ref = FlashSAC(w["obs"], w["act"], num_envs=w["envs"], cfg=_config(dict(w, amp=False)))
+    ref.load_state_dict(low.state_dict(include_replay=False))
+    for agent in (low, ref):
+        agent.load_replay(store)
+    del store
+    start = {k: torch.as_tensor(v).double() for k, v in ref.state_dict(include_replay=False).items()}
+    worst = {}
+    for pair in range(50):
+        m16 = low.update_pair(tensor_metrics=False)
+        m32 = ref.update_pair(tensor_metrics=False)
+        for key, value in m32.items():
+            worst[key] = max(worst.get(key, 0.0), abs(m16[key] - value) / max(abs(value), 1e-3))
+        if pair in (0, 4, 49):
+            print(f"updates {2 * pair + 2}: " + ", ".join(f"{k} {m32[k]:.5g}/{m16[k]:.5g}" for k in sorted(m32)),
+                  flush=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(low.indices.cpu().numpy(), ref.indices.cpu().numpy())  # same draws to the end
+    p16, p32 = low.state_dict(include_replay=False), ref.state_dict(include_replay=False)
+    groups = {}
+    for key, value in p32.items():
+        if "running" in key or not isinstance(value, np.ndarray) or value.dtype.kind != "f":
+            continue
+        a, b = torch.as_tensor(value).double(), torch.as_tensor(p16[key]).double()
+        g = groups.setdefault("actor" if key.startswith("actor") else "critic", [0.0, 0.0, 0.0])
+        g[0] += (b - a).pow(2).sum().item()
+        g[1] += a.pow(2).sum().item()
+        g[2] += (a - start[key]).pow(2).sum().item()
+    report = {
+        "updates": 100,
+        "shape": "G1 (obs 123, act 37, batch 8192, actor 256x2, critics 2x1024x2, 101 bins on [-20, 20])",
+        "activations": "bf16 BatchNorm inputs and ReLU-BN gradients",
+        "parameter_drift_rel_l2": {k: (v[0] / v[1]) ** 0.5 for k, v in groups.items()},
+        "drift_over_fp32_movement": {k: (v[0] / max(v[2], 1e-30)) ** 0.5 for k, v in groups.items()},
+        "max_rel_loss_difference": worst,
+    }
+    print(json.dumps(report, indent=1), flush=True)
+    path = os.environ.get("RL_DRIFT_REPORT")
+    if path:
+        with open(path.replace(".json", "_g1.json"), "w") as handle:
+            json.dump(report, handle, indent=1)
+    for group, value in report["parameter_drift_rel_l2"].items():
+        assert np.isfinite(value) and value < 0.05, (group, value)
+
+
 def test_cartpole_updates_match_float64_with_device_relu_decisions(gpu):
     """c0 at full size, an actor-phase update then a critic-only update run eagerly from injected batches
     and noise: every gradient and Adam moment within 1e-4 relative L2 (metrics 1e-4) of the float64 oracle
