@@ -21,6 +21,9 @@ Prints ONE JSON line: value = FlashSAC updates/sec on the GPU, with
   ppo             PPO update ms at configs[3] (one captured graph per update),
                   against the published fp32 matrix peak,
   kernel_sweep    configs[4]: the HBM-bound kernels at their sweep shapes,
+  bf16_drift_100_updates
+                  the bf16 learner against the fp32 learner over 100 G1 updates
+                  from the same weights, replay and device draws (not timed),
   cpu_baseline    the CPU oracle (PyTorch-CPU restatement of the reference update,
                   fp32) at G1 on this host's cores; cpu_baselines holds c0, c1,
                   c2 and c3 at all cores and at 8 threads with the CPU model.
@@ -719,6 +722,67 @@ def run_flashsac(name: str, steps: int, warmup: int, *, bf16_activations: bool =
     return result
 
 
+def bf16_drift(name: str = "g1", pairs: int = 50) -> dict:
+    """The 100-update drift of the bf16 learner against the fp32 learner at a workload shape: both start
+    from the same weights and seeded synthetic replay and run `pairs` captured UTD-2 steps; with one seed
+    their device samplers draw the same indices and noise.  Relative L2 parameter distance after the run
+    (to the parameters and to the fp32 learner's own movement) and the largest relative difference of
+    each loss over the run (absolute floor 1e-3).  Not timed."""
+    import numpy as np
+    import torch
+
+    from robolearn_amd.config import FlashSACConfig
+    from robolearn_amd.flashsac import FlashSAC
+
+    w = dict(WORKLOADS[name])
+    device = torch.device("cuda:0")
+    capacity = w["envs"] * w["horizon"]
+    agents = []
+    for amp in (True, False):
+        cfg = FlashSACConfig(**flashsac_config_kwargs(dict(w, amp=amp)))
+        agents.append(FlashSAC(w["obs"], w["act"], num_envs=w["envs"], cfg=cfg))
+    low, ref = agents
+    ref.load_state_dict(low.state_dict(include_replay=False))
+    g = torch.Generator(device=device).manual_seed(0)
+    data = {
+        "observation": torch.randn(capacity, w["obs"], generator=g, device=device),
+        "next_observation": torch.randn(capacity, w["obs"], generator=g, device=device),
+        "action": torch.rand(capacity, w["act"], generator=g, device=device) * 2 - 1,
+        "reward": torch.randn(capacity, generator=g, device=device) * w["reward_std"],
+        "terminated": (torch.rand(capacity, generator=g, device=device) < w["done"]).float(),
+        "truncated": torch.zeros(capacity, device=device),
+        "discount": torch.full((capacity,), low.cfg.gamma, device=device),
+    }
+    for agent in agents:
+        agent.load_replay(data)
+    del data
+    start = {k: np.asarray(v, dtype=np.float64) for k, v in ref.state_dict(include_replay=False).items()}
+    worst = {}
+    for _ in range(pairs):
+        m16, m32 = low.update_pair(tensor_metrics=False), ref.update_pair(tensor_metrics=False)
+        for key, value in m32.items():
+            worst[key] = max(worst.get(key, 0.0), abs(m16[key] - value) / max(abs(value), 1e-3))
+    p16, p32 = low.state_dict(include_replay=False), ref.state_dict(include_replay=False)
+    groups = {}
+    for key, value in p32.items():
+        value = np.asarray(value)
+        if "running" in key or value.dtype.kind != "f":
+            continue
+        a, b = value.astype(np.float64), np.asarray(p16[key], dtype=np.float64)
+        acc = groups.setdefault("actor" if key.startswith("actor") else "critic", [0.0, 0.0, 0.0])
+        acc[0] += float(((b - a) ** 2).sum())
+        acc[1] += float((a ** 2).sum())
+        acc[2] += float(((a - start[key]) ** 2).sum())
+    del agents, low, ref
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return {"workload": f"flashsac_{name}", "updates": 2 * pairs,
+            "bf16": "bf16 operands, bf16 BatchNorm activations", "reference": "the fp32 learner",
+            "parameter_drift_rel_l2": {k: round((v[0] / v[1]) ** 0.5, 6) for k, v in groups.items()},
+            "drift_over_fp32_movement": {k: round((v[0] / max(v[2], 1e-30)) ** 0.5, 6) for k, v in groups.items()},
+            "max_rel_loss_difference": {k: round(v, 6) for k, v in worst.items()}}
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
@@ -759,7 +823,7 @@ def main() -> int:
     print(f"[bench] {args.workload}: {head['ms_per_step']:.3f} ms per step, {head['updates_per_s']:.1f} updates/s",
           file=sys.stderr, flush=True)
 
-    others, ppo, sweep = None, None, None
+    others, ppo, sweep, drift = None, None, None, None
     if not args.no_extras:
         few = max(10, min(50, args.steps // 2))
         others = []
@@ -777,6 +841,8 @@ def main() -> int:
         ppo = bench_ppo(max(5, min(20, args.steps // 5)), 2)
         print("[bench] kernel sweep", file=sys.stderr, flush=True)
         sweep = kernel_sweep()
+        print("[bench] 100-update bf16 drift at G1", file=sys.stderr, flush=True)
+        drift = bf16_drift("g1")
 
     baselines, baseline = None, None
     if not args.no_cpu_baseline:
@@ -824,6 +890,7 @@ def main() -> int:
         "workloads": others,
         "ppo": ppo,
         "kernel_sweep": sweep,
+        "bf16_drift_100_updates": drift,
         "cpu_baselines": baselines,
     }
     print(json.dumps(result))
