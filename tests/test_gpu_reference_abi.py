@@ -285,6 +285,16 @@ def test_batchnorm_16bit_side_outputs(gpu):
     # flash_kernels.cuh:28: the 16-bit outputs are the exact IEEE fp16 rounding of the retained fp32 values
     assert torch.equal(half, y1.to(torch.float16))
     assert torch.equal(half_dx, dx1.to(torch.float16))
+    # this library's bf16 form writes the bf16 (RNE) rounding of the same y, from the apply pass itself
+    rm, rv = torch.zeros(channels, device=gpu), torch.ones(channels, device=gpu)
+    mean, var = torch.zeros(channels, device=gpu), torch.zeros(channels, device=gpu)
+    partial = torch.zeros(2 * chunks * channels, device=gpu)
+    y2 = torch.zeros(batch, channels, device=gpu)
+    y2_bf16 = torch.zeros(batch, channels, dtype=torch.bfloat16, device=gpu)
+    N.call("rl_flash_bn_forward_with_bf16", *[_ptr(t) for t in (x, w, b, rm, rv, mean, var, partial, y2, y2_bf16)],
+           batch, channels, eps, momentum, 1, 1, STREAM)
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y1) and torch.equal(y2_bf16, y1.to(torch.bfloat16))
     with pytest.raises(RuntimeError, match="nonnull"):
         N.call("rl_flash_bn_forward_with_fp16", *[_ptr(t) for t in (x, w, b, x, x, x, x, x, x)], None, batch,
                channels, eps, momentum, 1, 1, STREAM)
