@@ -607,57 +607,82 @@ static_assert(RPP == 8, "a pass stages acc[i][j][4q .. 4q + 3]: 8 rows");
 // one ds_read_b128 phase touches hit 16 distinct 4-bank groups.
 __device__ __forceinline__ int slot_of(int row) { return (row >> 1) & 7; }
 
-__device__ __forceinline__ void fetch(const unsigned short* A, const unsigned short* B, long long lda, long long ldb,
-                                      int m0, int n0, int k0, unsigned short* stage, int wave, int lane) {
-#pragma unroll
-    for (int j = 0; j < IPW; ++j) {
-        const int q = wave * IPW + j;
-        const int row = q * RPI + lane / CPR;
-        const int chunk = (lane % CPR) ^ slot_of(row);
-        __builtin_amdgcn_global_load_lds(
-            (__attribute__((address_space(1))) void*)(A + static_cast<long long>(m0 + row) * lda + k0 + chunk * 8),
-            (__attribute__((address_space(3))) void*)(stage + q * 512), 16, 0, 0);
-    }
-#pragma unroll
-    for (int j = 0; j < IPW; ++j) {
-        const int q = wave * IPW + j;
-        const int row = q * RPI + lane / CPR;
-        const int chunk = (lane % CPR) ^ slot_of(row);
-        __builtin_amdgcn_global_load_lds(
-            (__attribute__((address_space(1))) void*)(B + static_cast<long long>(n0 + row) * ldb + k0 + chunk * 8),
-            (__attribute__((address_space(3))) void*)(stage + BM * BK + q * 512), 16, 0, 0);
-    }
-}
-
+// DMA of one K tile through buffer resources.  Each operand's K tile is a
+// window of the operand (256 rows x 64 k, or 64 K rows x 256 m / n) whose base
+// address and byte extent are uniform per K tile, so the window's buffer
+// descriptor lives in scalar registers; a lane's offset into the window
+// depends only on the lane, the wave and the leading dimension and is computed
+// once per launch.  A DMA instruction then needs no vector address arithmetic,
+// and the LDS destination (M0) is uniform.  Loads past the window's extent
+// return zero: the descriptor bounds every access to the K tile's rows.
+//
+// K-contiguous operands (forward products, input gradients through transposed
+// weights): DMA instruction q fills rows q * RPI .. q * RPI + 7; lane l loads
+// the 16-byte k chunk (l % CPR) ^ slot_of(row) of row q * RPI + l / CPR, which
+// lands at LDS offset 16 l of the instruction's 1 KiB block.
+//
 // M/N-contiguous operands (a weight gradient dW = dY^T X reads both operands
 // along their rows): a stage holds 64 K rows x 256 M (N) of each operand, 512
 // bytes per K row, and the 16-byte M granule c of K row k sits in slot
 // c ^ tslot(k).  DMA instruction q of an operand fills K rows 2q and 2q + 1;
 // lane l loads the granule that belongs in slot l % 32 of row 2q + l / 32.
 __device__ __forceinline__ int tslot(int k) { return 4 * (k & 3); }
+static_assert(2 * IPW * NW == BK, "M/N-contiguous DMA: two K rows per instruction");
 
-__device__ __forceinline__ void fetch_mn(const unsigned short* A, const unsigned short* B, long long lda, long long ldb,
-                                         int m0, int n0, int k0, unsigned short* stage, int wave, int lane) {
+constexpr int kBufferWord3 = 0x00020000;  // raw dword access (gfx9 buffer descriptor word 3)
+
+struct DmaLanes {
+    unsigned a[IPW], b[IPW];  // byte offsets of this lane's 16-byte pieces in the A and B windows
+};
+
+template <bool MN>
+__device__ __forceinline__ DmaLanes dma_lanes(long long lda, long long ldb, int wave, int lane) {
+    DmaLanes l;
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
         const int q = wave * IPW + j;
-        const int k = 2 * q + lane / 32;
-        const int granule = (lane % 32) ^ tslot(k);
-        __builtin_amdgcn_global_load_lds(
-            (__attribute__((address_space(1))) void*)(A + static_cast<long long>(k0 + k) * lda + m0 + granule * 8),
-            (__attribute__((address_space(3))) void*)(stage + q * 512), 16, 0, 0);
+        if constexpr (MN) {
+            const int k = 2 * q + lane / 32;
+            const int granule = (lane % 32) ^ tslot(k);
+            l.a[j] = static_cast<unsigned>((k * lda + granule * 8) * 2);
+            l.b[j] = static_cast<unsigned>((k * ldb + granule * 8) * 2);
+        } else {
+            const int row = q * RPI + lane / CPR;
+            const int chunk = (lane % CPR) ^ slot_of(row);
+            l.a[j] = static_cast<unsigned>((row * lda + chunk * 8) * 2);
+            l.b[j] = static_cast<unsigned>((row * ldb + chunk * 8) * 2);
+        }
     }
-#pragma unroll
-    for (int j = 0; j < IPW; ++j) {
-        const int q = wave * IPW + j;
-        const int k = 2 * q + lane / 32;
-        const int granule = (lane % 32) ^ tslot(k);
-        __builtin_amdgcn_global_load_lds(
-            (__attribute__((address_space(1))) void*)(B + static_cast<long long>(k0 + k) * ldb + n0 + granule * 8),
-            (__attribute__((address_space(3))) void*)(stage + BM * BK + q * 512), 16, 0, 0);
-    }
+    return l;
 }
-static_assert(2 * IPW * NW == BK, "fetch_mn: two K rows per DMA instruction");
+
+// Byte extent of an operand's K-tile window (leading dimension ld).
+template <bool MN>
+__device__ __forceinline__ unsigned window_bytes(long long ld) {
+    return static_cast<unsigned>(MN ? ((BK - 1) * ld + BM) * 2 : ((BM - 1) * ld + BK) * 2);
+}
+static_assert(BM == BN, "A and B windows share the extent formula");
+
+// Largest leading dimension whose K-tile window and lane offsets fit the
+// descriptor's 31-bit extent.
+constexpr long long kMaxWindowLd = 1LL << 22;
+
+__device__ __forceinline__ void fetch(const unsigned short* a0, const unsigned short* b0, unsigned a_bytes,
+                                      unsigned b_bytes, const DmaLanes& l, unsigned short* stage, int wave) {
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(a0), (short)0, static_cast<int>(a_bytes), kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(b0), (short)0, static_cast<int>(b_bytes), kBufferWord3);
+#pragma unroll
+    for (int j = 0; j < IPW; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            ra, (__attribute__((address_space(3))) void*)(stage + (wave * IPW + j) * 512), 16, l.a[j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < IPW; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rb, (__attribute__((address_space(3))) void*)(stage + BM * BK + (wave * IPW + j) * 512), 16, l.b[j], 0,
+            0, 0);
+}
 
 // 8-byte transposing LDS read (ds_read_b64_tr_b16) of `p`, inline assembly for
 // the same reason as lds_read16 below.  In each 16-lane group, lane i receives
@@ -713,7 +738,7 @@ __device__ __forceinline__ void merge8(float& count, float (&mean)[8], float (&m
     count = total;
 }
 
-// MN: both operands M/N-contiguous (fetch_mn, transposing fragment reads); else
+// MN: both operands M/N-contiguous (M/N-contiguous windows, transposing fragment reads); else
 // both K-contiguous.  SPP: 16-byte stores every lane issues per 8-row epilogue
 // pass (2 for an fp32 D, 1 for the bf16 copy).  BIAS: the product adds a bias (a kernel without one
 // issues no epilogue loads, whose registers the next tile's fragment reads
@@ -744,18 +769,21 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
     const int G = static_cast<int>(gridDim.x);
     const int b = static_cast<int>(blockIdx.x);
     const int slot = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: LDS DMA targets in SGPRs
     const int lane = threadIdx.x % kWave;
     const int wm = wave / (BN / WTN);
     const int wn = wave % (BN / WTN);
     const int sw = slot_of(lane % 32);
     const bool direct = OUT == kBf16 || OUT == kBf16Moments || p.splits == 1;
 
+    const DmaLanes lanes = dma_lanes<MN>(p.lda, p.ldb, wave, lane);
+    const unsigned a_bytes = window_bytes<MN>(p.lda), b_bytes = window_bytes<MN>(p.ldb);
     const auto fetch_tile = [&](const Tile& t, int kt, unsigned short* stage) {
         const unsigned short* A = static_cast<const unsigned short*>(p.a) + t.batch * p.stride_a;
         const unsigned short* B = static_cast<const unsigned short*>(p.b) + t.batch * p.stride_b;
-        if constexpr (MN) fetch_mn(A, B, p.lda, p.ldb, t.m0, t.n0, t.split * p.k_per_split + kt * BK, stage, wave, lane);
-        else fetch(A, B, p.lda, p.ldb, t.m0, t.n0, t.split * p.k_per_split + kt * BK, stage, wave, lane);
+        const long long k0 = t.split * p.k_per_split + kt * BK;
+        if constexpr (MN) fetch(A + k0 * p.lda + t.m0, B + k0 * p.ldb + t.n0, a_bytes, b_bytes, lanes, stage, wave);
+        else fetch(A + t.m0 * p.lda + k0, B + t.n0 * p.ldb + k0, a_bytes, b_bytes, lanes, stage, wave);
     };
     // transposing reads (MN): lane l reads K rows 16 s + 8 (l / 32) + 4 r + (l % 16) / 4 of substep s,
     // r = 0, 1, at M offset 16 ((l / 16) % 2) + 4 (l % 4) of each 32-wide fragment; the K row's slot
@@ -1070,6 +1098,7 @@ void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream) {
     // the eight-wave kernel writes the bf16 copy as 16-byte pieces of 8 columns
     // (both operands K-contiguous, or both M/N-contiguous: the weight gradients)
     const bool wide = ak == bk && p.k % (2 * big::wide::BK) == 0 && p.k_per_split % (2 * big::wide::BK) == 0 &&
+                      p.lda <= big::wide::kMaxWindowLd && p.ldb <= big::wide::kMaxWindowLd &&
                       (!p.d_bf16 || (aligned(p.d_bf16, 16) && p.ldd % 8 == 0 && p.stride_d % 8 == 0));
     if (wide) {
         // unconditional 16-byte stores per lane per epilogue pass: the fp32 D (split-K partials or a

@@ -317,6 +317,36 @@ def test_big_tile_bf16_gemm_layouts(gpu, a_kcontig, b_kcontig, batch, m, n, k, s
     torch.testing.assert_close(d.cpu().double(), expected, rtol=1e-5, atol=1e-5 * math.sqrt(k))
 
 
+@pytest.mark.parametrize("kcontig", [True, False])
+@pytest.mark.parametrize("splits", [1, 2])
+def test_wide_gemm_padded_leading_dimensions(gpu, kcontig, splits):
+    """The eight-wave kernel's DMA windows at leading dimensions wider than the product: K-contiguous
+    operands that are K-slices of wider rows, M/N-contiguous ones that are row slices of wider rows.
+    A window offset or extent that assumed ld == K (or M) reads the wrong elements or zeros."""
+    batch, m, n, k = 2, 512, 768, 256
+    print(f"case padded-ld kcontig={kcontig} splits={splits}", flush=True)
+    g = torch.Generator().manual_seed(41 + splits)
+    a = torch.randn(batch, m, k, generator=g).to(torch.bfloat16)
+    b = torch.randn(batch, n, k, generator=g).to(torch.bfloat16)
+    if kcontig:
+        lda, ldb = k + 64, k + 192
+        a_mem = torch.randn(batch, m, lda, generator=g).to(torch.bfloat16)
+        b_mem = torch.randn(batch, n, ldb, generator=g).to(torch.bfloat16)
+        a_mem[:, :, :k], b_mem[:, :, :k] = a, b
+    else:
+        lda, ldb = m + 256, n + 512
+        a_mem = torch.randn(batch, k, lda, generator=g).to(torch.bfloat16)
+        b_mem = torch.randn(batch, k, ldb, generator=g).to(torch.bfloat16)
+        a_mem[:, :, :m], b_mem[:, :, :n] = a.transpose(1, 2), b.transpose(1, 2)
+    workspace = torch.empty(splits * batch * m * n * 4, dtype=torch.uint8, device=gpu) if splits > 1 else None
+    d = torch.empty(batch, m, n, device=gpu)
+    K.gemm(a_mem.to(gpu), b_mem.to(gpu), d, m=m, n=n, k=k, batch=batch, a_kcontig=kcontig, b_kcontig=kcontig,
+           lda=lda, ldb=ldb, ldd=n, stride_a=a_mem[0].numel(), stride_b=b_mem[0].numel(), stride_d=m * n,
+           mode=K.BF16, splits=splits, workspace=workspace)
+    ref = torch.einsum("bmk,bnk->bmn", a.double(), b.double())
+    torch.testing.assert_close(d.cpu().double(), ref, rtol=1e-5, atol=1e-5 * math.sqrt(k))
+
+
 def _chunk_moments(d):
     """Per-256-row-chunk column (mean, M2) in float64: [batch][chunk][2][n]."""
     batch, m, n = d.shape
