@@ -856,12 +856,19 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
         };
         // one K tile from `cur`; inside its last substep K tile kt + 1 (in `other`) has landed in every
         // wave and every wave holds its last fragments of kt, so `cur` takes K tile kt + 2 and the first
-        // fragments of kt + 1 are read under this substep's MFMAs
+        // fragments of kt + 1 are read under this substep's MFMAs.  The first row half (waves 0-3) issues
+        // its DMA of kt + 2 right after that barrier, the second half in the first substep of kt + 1:
+        // half the DMA instructions queue at the address unit after each barrier (measured 4 % faster
+        // than all eight waves issuing together).  Both land before the barrier that ends kt + 1.
         const auto k_tile = [&](int kt, unsigned short* cur, const unsigned short* other) {
             const auto substep = [&](auto s_const) {
                 constexpr int s = decltype(s_const)::value;
                 if constexpr (s + 1 < BK / 16) {
                     read(cur, std::integral_constant<int, s + 1>{}, af[(s + 1) & 1], bfr[(s + 1) & 1]);
+                    // the second row half's share of K tile kt + 1, one substep after the first half's
+                    // (`other` held K tile kt - 1, which every wave finished reading before the last barrier)
+                    if (s == 0 && wm == 1 && kt >= 1 && kt + 1 < nk)
+                        fetch_tile(tile, kt + 1, const_cast<unsigned short*>(other));
                     wait_lds_reads<kReads>();  // substep s's fragments have landed; s + 1's may stay in flight
                 } else {
                     if (kt + 1 < nk) {
@@ -872,7 +879,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                         } else {
                             big::dma_barrier<0>();
                         }
-                        if (kt + 2 < nk) fetch_tile(tile, kt + 2, cur);
+                        if (kt + 2 < nk && wm == 0) fetch_tile(tile, kt + 2, cur);
                         read(other, std::integral_constant<int, 0>{}, af[0], bfr[0]);
                     } else {
                         wait_lds_reads<0>();
@@ -940,13 +947,16 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
 #pragma unroll
             for (int pass = 0; pass < 32 / RPP; ++pass) {
                 // rows 8 pass .. 8 pass + 7 of the block: acc[i][j][4 pass + e] holds row 8 pass + 4 (lane / 32) + e
-                lds_fence();  // this wave's reads of the previous pass are done
+                // the staging rows are this wave's own and LDS executes a wave's operations in order,
+                // so overwriting the previous pass's rows and reading back this pass's need no wait:
+                // only the compiler must keep the accesses in program order
+                asm volatile("" ::: "memory");
 #pragma unroll
                 for (int j = 0; j < NJ; ++j)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         stagef[(4 * (lane / 32) + e) * EP + j * 32 + lane % 32] = acc[i][j][4 * pass + e];
-                lds_fence();
+                asm volatile("" ::: "memory");
                 const int r = pass * RPP + lane / LPR;
                 const f32x4 x0 = *reinterpret_cast<const f32x4*>(stagef + (lane / LPR) * EP + (lane % LPR) * 8);
                 const f32x4 x1 = *reinterpret_cast<const f32x4*>(stagef + (lane / LPR) * EP + (lane % LPR) * 8 + 4);
