@@ -6,8 +6,10 @@
 //   * gemm_wide_kernel (namespace wide), the one that carries the G1 update:
 //     8 waves (two per SIMD) of 128x64 outputs as 4x2
 //     v_mfma_f32_32x32x16_bf16 accumulators; operands move global -> LDS by
-//     global_load_lds_dwordx4 (no register staging) into two 64-deep K stages
-//     of 64 KB, 16-byte chunks XOR-swizzled so each ds_read_b128 phase hits 16
+//     buffer_load_dwordx4 ... lds (no register staging; the K tile's window in
+//     a scalar buffer descriptor, per-lane offsets fixed per launch) into two
+//     64-deep K stages of 64 KB, the two row halves issuing one substep apart,
+//     16-byte chunks XOR-swizzled so each ds_read_b128 phase hits 16
 //     distinct bank groups; fragments of the next 16-deep sub-step are read
 //     (inline-asm ds_read_b128, explicit lgkmcnt waits) under the current
 //     sub-step's MFMAs, and the barrier that publishes K tile k + 1 sits in
@@ -189,7 +191,7 @@ __device__ __forceinline__ float4 activate4(float4 v, int epilogue) {
 
 // Logical tile id -> output tile.  Within a (batch, split) slice tiles go in
 // groups of GroupM M-tiles, M fastest, so consecutive ids share operand panels.
-template <int GM = GroupM>
+template <int GM = GroupM, int TN = BN>
 __device__ __forceinline__ Tile tile_of(int id, int tiles_m, int tiles_n, int splits) {
     const int per_slice = tiles_m * tiles_n;
     const int slice = id / per_slice;
@@ -198,7 +200,7 @@ __device__ __forceinline__ Tile tile_of(int id, int tiles_m, int tiles_n, int sp
     const int first_m = group * GM;
     const int group_m = min(tiles_m - first_m, GM);
     const int local = t % (GM * tiles_n);
-    return Tile{(first_m + local % group_m) * BM, (local / group_m) * BN, slice / splits, slice % splits};
+    return Tile{(first_m + local % group_m) * BM, (local / group_m) * TN, slice / splits, slice % splits};
 }
 
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
@@ -631,12 +633,25 @@ static_assert(2 * IPW * NW == BK, "M/N-contiguous DMA: two K rows per instructio
 
 constexpr int kBufferWord3 = 0x00020000;  // raw dword access (gfx9 buffer descriptor word 3)
 
+// DMA instructions per wave per K tile for an operand of `rows` rows (256 for A,
+// the tile width for B): a K tile of a row is one 128-byte line, 8 rows per
+// instruction.
+template <int Rows>
+constexpr int dma_per_wave() {
+    static_assert(Rows % (RPI * NW) == 0, "whole DMA instructions per wave");
+    return Rows / (RPI * NW);
+}
+static_assert(dma_per_wave<BM>() == IPW, "256-row operands");
+
 struct DmaLanes {
     unsigned a[IPW], b[IPW];  // byte offsets of this lane's 16-byte pieces in the A and B windows
 };
 
-template <bool MN>
+// TN: rows of the B window (the output tile's columns); M/N-contiguous operands take 256 only.
+template <bool MN, int TN>
 __device__ __forceinline__ DmaLanes dma_lanes(long long lda, long long ldb, int wave, int lane) {
+    static_assert(!MN || TN == BN, "M/N-contiguous products use 256-wide tiles");
+    constexpr int IPW_B = dma_per_wave<TN>();
     DmaLanes l;
 #pragma unroll
     for (int j = 0; j < IPW; ++j) {
@@ -650,25 +665,33 @@ __device__ __forceinline__ DmaLanes dma_lanes(long long lda, long long ldb, int 
             const int row = q * RPI + lane / CPR;
             const int chunk = (lane % CPR) ^ slot_of(row);
             l.a[j] = static_cast<unsigned>((row * lda + chunk * 8) * 2);
-            l.b[j] = static_cast<unsigned>((row * ldb + chunk * 8) * 2);
+            if (j < IPW_B) {
+                const int row_b = (wave * IPW_B + j) * RPI + lane / CPR;
+                const int chunk_b = (lane % CPR) ^ slot_of(row_b);
+                l.b[j] = static_cast<unsigned>((row_b * ldb + chunk_b * 8) * 2);
+            } else {
+                l.b[j] = 0;
+            }
         }
     }
     return l;
 }
 
-// Byte extent of an operand's K-tile window (leading dimension ld).
-template <bool MN>
+// Byte extent of an operand's K-tile window (leading dimension ld, `Rows` rows
+// in the K-contiguous layout).
+template <bool MN, int Rows>
 __device__ __forceinline__ unsigned window_bytes(long long ld) {
-    return static_cast<unsigned>(MN ? ((BK - 1) * ld + BM) * 2 : ((BM - 1) * ld + BK) * 2);
+    return static_cast<unsigned>(MN ? ((BK - 1) * ld + Rows) * 2 : ((Rows - 1) * ld + BK) * 2);
 }
-static_assert(BM == BN, "A and B windows share the extent formula");
 
 // Largest leading dimension whose K-tile window and lane offsets fit the
 // descriptor's 31-bit extent.
 constexpr long long kMaxWindowLd = 1LL << 22;
 
+template <int TN>
 __device__ __forceinline__ void fetch(const unsigned short* a0, const unsigned short* b0, unsigned a_bytes,
                                       unsigned b_bytes, const DmaLanes& l, unsigned short* stage, int wave) {
+    constexpr int IPW_B = dma_per_wave<TN>();
     const __amdgpu_buffer_rsrc_t ra =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(a0), (short)0, static_cast<int>(a_bytes), kBufferWord3);
     const __amdgpu_buffer_rsrc_t rb =
@@ -678,9 +701,9 @@ __device__ __forceinline__ void fetch(const unsigned short* a0, const unsigned s
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             ra, (__attribute__((address_space(3))) void*)(stage + (wave * IPW + j) * 512), 16, l.a[j], 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < IPW; ++j)
+    for (int j = 0; j < IPW_B; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rb, (__attribute__((address_space(3))) void*)(stage + BM * BK + (wave * IPW + j) * 512), 16, l.b[j], 0,
+            rb, (__attribute__((address_space(3))) void*)(stage + BM * BK + (wave * IPW_B + j) * 512), 16, l.b[j], 0,
             0, 0);
 }
 
@@ -754,36 +777,49 @@ __device__ __forceinline__ void merge8(float& count, float (&mean)[8], float (&m
 // split-K partials or a direct output without a bf16 copy or moments).
 enum Out { kGeneral = 0, kBf16 = 1, kBf16Moments = 2, kFp32 = 3 };
 
-template <int SPP, bool BIAS, bool MN, int OUT>
+template <int SPP, bool BIAS, bool MN, int OUT, int TN>
 __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int tiles_m, int tiles_n, int total) {
     static_assert(OUT == kGeneral || !BIAS, "the plain epilogues add no bias");
     static_assert(OUT == kGeneral || SPP == (OUT == kFp32 ? 2 : 1), "stores per pass of the plain epilogues");
-    constexpr int S = MI * (32 / RPP) * SPP;
-    static_assert(SPP >= 1 && 2 * IPW + S < 64, "vmcnt is a 6-bit count");
+    // Tile of 256 rows x TN columns: the 8 waves keep 64-column wave tiles and stack WGM deep in rows
+    // (TN 256: 2 x 4 waves of 128 x 64; 128: 4 x 2 of 64 x 64; 64: 8 x 1 of 32 x 64).  The narrow
+    // tiles fill the GPU where 256-wide ones leave CUs idle; each still covers whole 256-row chunks.
+    static_assert(TN == 256 || TN == 128 || TN == 64, "tile widths");
+    static_assert(!MN || TN == BN, "M/N-contiguous products use 256-wide tiles");
+    constexpr int WGN = TN / WTN;                  // wave columns
+    constexpr int WGM = NW / WGN;                  // wave rows
+    constexpr int TWM = BM / WGM;                  // rows per wave tile
+    constexpr int TMI = TWM / 32;                  // 32-row fragments per wave tile
+    constexpr int DPW = IPW + dma_per_wave<TN>();  // DMA instructions per wave per K tile
+    constexpr int TSTAGE = (BM + TN) * BK;         // bf16 elements per stage
+    constexpr int S = TMI * (32 / RPP) * SPP;
+    static_assert(SPP >= 1 && DPW + S < 64, "vmcnt is a 6-bit count");
     // the two stages are separate objects: the compiler can then tell a fragment read of one
     // stage from a DMA into the other and does not make the read wait for that DMA
-    __shared__ __attribute__((aligned(16))) unsigned short stage0[STAGE];
-    __shared__ __attribute__((aligned(16))) unsigned short stage1[STAGE];
+    __shared__ __attribute__((aligned(16))) unsigned short stage0[TSTAGE];
+    __shared__ __attribute__((aligned(16))) unsigned short stage1[TSTAGE];
     __shared__ __attribute__((aligned(16))) float staging[NW * RPP * EP];
-    __shared__ __attribute__((aligned(16))) float exchange[2 * BN];  // (mean, M2) of the second row half
+    __shared__ __attribute__((aligned(16))) float exchange[(WGM - 1) * 2 * TN];  // (mean, M2) of row groups 1..
     const int G = static_cast<int>(gridDim.x);
     const int b = static_cast<int>(blockIdx.x);
     const int slot = G % 8 == 0 ? (b % 8) * (G / 8) + b / 8 : b;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // uniform: LDS DMA targets in SGPRs
     const int lane = threadIdx.x % kWave;
-    const int wm = wave / (BN / WTN);
-    const int wn = wave % (BN / WTN);
+    const int wm = wave / WGN;
+    const int wn = wave % WGN;
     const int sw = slot_of(lane % 32);
     const bool direct = OUT == kBf16 || OUT == kBf16Moments || p.splits == 1;
 
-    const DmaLanes lanes = dma_lanes<MN>(p.lda, p.ldb, wave, lane);
-    const unsigned a_bytes = window_bytes<MN>(p.lda), b_bytes = window_bytes<MN>(p.ldb);
+    const DmaLanes lanes = dma_lanes<MN, TN>(p.lda, p.ldb, wave, lane);
+    const unsigned a_bytes = window_bytes<MN, BM>(p.lda), b_bytes = window_bytes<MN, TN>(p.ldb);
     const auto fetch_tile = [&](const Tile& t, int kt, unsigned short* stage) {
         const unsigned short* A = static_cast<const unsigned short*>(p.a) + t.batch * p.stride_a;
         const unsigned short* B = static_cast<const unsigned short*>(p.b) + t.batch * p.stride_b;
         const long long k0 = t.split * p.k_per_split + kt * BK;
-        if constexpr (MN) fetch(A + k0 * p.lda + t.m0, B + k0 * p.ldb + t.n0, a_bytes, b_bytes, lanes, stage, wave);
-        else fetch(A + t.m0 * p.lda + k0, B + t.n0 * p.ldb + k0, a_bytes, b_bytes, lanes, stage, wave);
+        if constexpr (MN)
+            fetch<TN>(A + k0 * p.lda + t.m0, B + k0 * p.ldb + t.n0, a_bytes, b_bytes, lanes, stage, wave);
+        else
+            fetch<TN>(A + t.m0 * p.lda + k0, B + t.n0 * p.ldb + k0, a_bytes, b_bytes, lanes, stage, wave);
     };
     // transposing reads (MN): lane l reads K rows 16 s + 8 (l / 32) + 4 r + (l % 16) / 4 of substep s,
     // r = 0, 1, at M offset 16 ((l / 16) % 2) + 4 (l % 4) of each 32-wide fragment; the K row's slot
@@ -792,44 +828,44 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
     // fragment 0's granule group, fragment j of B at ((wn WTN / 8 + 4 j) ^ 4 tq) granules)
     const int tq = (lane % 16) / 4;
     const int t_low = 2 * ((lane / 16) % 2) + (lane % 4) / 2;
-    const int t_base_a = (8 * (lane / 32) + tq) * BM + ((wm * WTM) / 8 + t_low) * 8 + 4 * (lane % 2);
+    const int t_base_a = (8 * (lane / 32) + tq) * BM + ((wm * TWM) / 8 + t_low) * 8 + 4 * (lane % 2);
     const int t_base_b = BM * BK + (8 * (lane / 32) + tq) * BN + t_low * 8 + 4 * (lane % 2);
     const auto k_tiles = [&](const Tile& t) {
         const int k_begin = t.split * p.k_per_split;
         return (min(p.k, k_begin + p.k_per_split) - k_begin) / BK;  // even, >= 2: K splits are multiples of 128
     };
     if (slot >= total) return;
-    Tile tile = big::tile_of<kGroupM>(slot, tiles_m, tiles_n, p.splits);
+    Tile tile = big::tile_of<kGroupM, TN>(slot, tiles_m, tiles_n, p.splits);
     fetch_tile(tile, 0, stage0);
     fetch_tile(tile, 1, stage1);
     bool first = true;
     float* stagef = staging + wave * RPP * EP;
 
     for (int id = slot; id < total; id += G) {
-        const Tile next = id + G < total ? big::tile_of<kGroupM>(id + G, tiles_m, tiles_n, p.splits) : tile;
+        const Tile next = id + G < total ? big::tile_of<kGroupM, TN>(id + G, tiles_m, tiles_n, p.splits) : tile;
         const int nk = k_tiles(tile);
 
-        f32x16_t acc[MI][NJ];
+        f32x16_t acc[TMI][NJ];
 #pragma unroll
-        for (int i = 0; i < MI; ++i)
+        for (int i = 0; i < TMI; ++i)
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-        bf16x8_t af[2][MI], bfr[2][NJ];
-        // K-contiguous: MI + NJ = 6 reads per substep, fragments i / j 32 * BK elements (4 KiB) apart;
-        // MN: 2 (MI + NJ) = 12 transposing reads
-        static_assert(MI == 4 && NJ == 2, "the read sequence below");
-        constexpr int kReads = MN ? 2 * (MI + NJ) : MI + NJ;
-        const auto read = [&](const unsigned short* stage, auto s_const, bf16x8_t (&fa)[MI], bf16x8_t (&fb)[NJ]) {
+        bf16x8_t af[2][TMI], bfr[2][NJ];
+        // K-contiguous: TMI + NJ reads per substep (6 for 256-wide tiles), fragments i / j 32 * BK
+        // elements (4 KiB) apart; MN: 2 (TMI + NJ) = 12 transposing reads
+        static_assert(NJ == 2 && (!MN || TMI == 4), "the read sequence below");
+        constexpr int kReads = MN ? 2 * (TMI + NJ) : TMI + NJ;
+        const auto read = [&](const unsigned short* stage, auto s_const, bf16x8_t (&fa)[TMI], bf16x8_t (&fb)[NJ]) {
             constexpr int s = decltype(s_const)::value;
             if constexpr (MN) {
                 // substep rows and the second 4-row half go in the instruction's offset field (bytes)
                 constexpr int kLo = 2 * 16 * s * BM, kHi = kLo + 2 * 4 * BM;
                 static_assert(BM == BN, "A and B rows share the offsets");
 #pragma unroll
-                for (int i = 0; i < MI; ++i) {
+                for (int i = 0; i < TMI; ++i) {
                     const unsigned short* q = stage + t_base_a + 32 * (i ^ tq);
                     const u32x2_t lo = lds_read8_tr<kLo>(q);
                     const u32x2_t hi = lds_read8_tr<kHi>(q);
@@ -845,12 +881,14 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                 return;
             }
             const int off = 8 * ((2 * s + lane / 32) ^ sw);
-            const unsigned short* la = stage + (wm * WTM + lane % 32) * BK + off;
+            const unsigned short* la = stage + (wm * TWM + lane % 32) * BK + off;
             const unsigned short* lb = stage + BM * BK + (wn * WTN + lane % 32) * BK + off;
             fa[0] = lds_read16<0>(la);
-            fa[1] = lds_read16<64 * BK>(la);
-            fa[2] = lds_read16<128 * BK>(la);
-            fa[3] = lds_read16<192 * BK>(la);
+            if constexpr (TMI > 1) fa[1] = lds_read16<64 * BK>(la);
+            if constexpr (TMI > 2) {
+                fa[2] = lds_read16<128 * BK>(la);
+                fa[3] = lds_read16<192 * BK>(la);
+            }
             fb[0] = lds_read16<0>(lb);
             fb[1] = lds_read16<64 * BK>(lb);
         };
@@ -867,7 +905,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                     read(cur, std::integral_constant<int, s + 1>{}, af[(s + 1) & 1], bfr[(s + 1) & 1]);
                     // the second row half's share of K tile kt + 1, one substep after the first half's
                     // (`other` held K tile kt - 1, which every wave finished reading before the last barrier)
-                    if (s == 0 && wm == 1 && kt >= 1 && kt + 1 < nk)
+                    if (s == 0 && wave >= NW / 2 && kt >= 1 && kt + 1 < nk)
                         fetch_tile(tile, kt + 1, const_cast<unsigned short*>(other));
                     wait_lds_reads<kReads>();  // substep s's fragments have landed; s + 1's may stay in flight
                 } else {
@@ -879,7 +917,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                         } else {
                             big::dma_barrier<0>();
                         }
-                        if (kt + 2 < nk && wm == 0) fetch_tile(tile, kt + 2, cur);
+                        if (kt + 2 < nk && wave < NW / 2) fetch_tile(tile, kt + 2, cur);
                         read(other, std::integral_constant<int, 0>{}, af[0], bfr[0]);
                     } else {
                         wait_lds_reads<0>();
@@ -887,7 +925,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                 }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int i = 0; i < MI; ++i)
+                for (int i = 0; i < TMI; ++i)
 #pragma unroll
                     for (int j = 0; j < NJ; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s & 1][i], bfr[s & 1][j], acc[i][j], 0,
@@ -901,8 +939,8 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
             substep(std::integral_constant<int, 3>{});
         };
         // K tile 0 has landed in every wave (the previous epilogue's stores may still be in flight)
-        if (first) big::dma_barrier<2 * IPW>();
-        else big::dma_barrier<2 * IPW + S>();
+        if (first) big::dma_barrier<DPW>();
+        else big::dma_barrier<DPW + S>();
         read(stage0, std::integral_constant<int, 0>{}, af[0], bfr[0]);
         for (int kt = 0; kt < nk; kt += 2) {  // nk is even: K splits are multiples of 128
             k_tile(kt, stage0, stage1);
@@ -943,7 +981,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
 #pragma unroll
         for (int e = 0; e < 8; ++e) shift[e] = s1[e] = s2[e] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
+        for (int i = 0; i < TMI; ++i) {
 #pragma unroll
             for (int pass = 0; pass < 32 / RPP; ++pass) {
                 // rows 8 pass .. 8 pass + 7 of the block: acc[i][j][4 pass + e] holds row 8 pass + 4 (lane / 32) + e
@@ -961,7 +999,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                 const f32x4 x0 = *reinterpret_cast<const f32x4*>(stagef + (lane / LPR) * EP + (lane % LPR) * 8);
                 const f32x4 x1 = *reinterpret_cast<const f32x4*>(stagef + (lane / LPR) * EP + (lane % LPR) * 8 + 4);
                 float val[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-                const long long offset = static_cast<long long>(tile.m0 + wm * WTM + i * 32 + r) * ldd + col;
+                const long long offset = static_cast<long long>(tile.m0 + wm * TWM + i * 32 + r) * ldd + col;
                 if (general && direct) {
                     float4 lo = activate4(make_float4(val[0] + bias8[0], val[1] + bias8[1], val[2] + bias8[2],
                                                       val[3] + bias8[3]), p.epilogue);
@@ -1009,7 +1047,7 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
         if (moments) {
             // this lane's 16 rows -> (mean, M2), then butterflies over the 8 lane groups of the
             // same columns (partners lane ^ 8, ^ 16, ^ 32; the lower lane's moments go first)
-            constexpr float rows = 32 / RPP * MI;
+            constexpr float rows = 32 / RPP * TMI;
             float count = rows, mean[8], m2[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -1036,22 +1074,29 @@ __global__ __launch_bounds__(NW * kWave, 1) void gemm_wide_kernel(Params p, int 
                     merge8(count, mean, m2, count, om, oq);
                 }
             }
-            if (wm == 1 && lane < LPR) {
+            // row groups 1 .. WGM - 1 hand their (mean, M2) to row group 0, which merges them in order
+            if (wm > 0 && lane < LPR) {
+                float* slot_m = exchange + (wm - 1) * 2 * TN + wn * WTN + (lane % LPR) * 8;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    exchange[wn * WTN + (lane % LPR) * 8 + e] = mean[e];
-                    exchange[BN + wn * WTN + (lane % LPR) * 8 + e] = m2[e];
+                    slot_m[e] = mean[e];
+                    slot_m[TN + e] = m2[e];
                 }
             }
             big::lds_barrier();
             if (wm == 0 && lane < LPR) {
-                float bm[8], bq[8];
+                const float part = count;  // rows of one wave tile
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    bm[e] = exchange[wn * WTN + (lane % LPR) * 8 + e];
-                    bq[e] = exchange[BN + wn * WTN + (lane % LPR) * 8 + e];
+                for (int g = 0; g < WGM - 1; ++g) {
+                    const float* slot_m = exchange + g * 2 * TN + wn * WTN + (lane % LPR) * 8;
+                    float bm[8], bq[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        bm[e] = slot_m[e];
+                        bq[e] = slot_m[TN + e];
+                    }
+                    merge8(count, mean, m2, part, bm, bq);
                 }
-                merge8(count, mean, m2, count, bm, bq);
                 float* out = p.moments + (static_cast<long long>(tile.batch) * (p.m / BM) + tile.m0 / BM) * 2 * p.n + col;
                 *reinterpret_cast<float4*>(out) = make_float4(mean[0], mean[1], mean[2], mean[3]);
                 *reinterpret_cast<float4*>(out + 4) = make_float4(mean[4], mean[5], mean[6], mean[7]);
@@ -1098,6 +1143,35 @@ static int compute_units() {
     return cached[device];
 }
 
+// The eight-wave kernel at tile width `tn` (K-contiguous operands; the plain epilogue kinds take 256,
+// 128 or 64) or 256 (M/N-contiguous operands, the general epilogue).
+template <int SPP, bool BIAS, int OUT>
+static void launch_wide(const Params& p, bool mn, int tn, hipStream_t stream) {
+    const int tiles_m = p.m / big::BM;
+    const int tiles_n = p.n / tn;
+    const int total = tiles_m * tiles_n * p.batch * p.splits;
+    const dim3 grid(static_cast<unsigned>(std::min(total, compute_units())));
+    const dim3 block(big::wide::NW * kWave);
+    using big::wide::gemm_wide_kernel;
+    if (mn) {
+        hipLaunchKernelGGL((gemm_wide_kernel<SPP, BIAS, true, OUT, 256>), grid, block, 0, stream, p, tiles_m, tiles_n,
+                           total);
+    } else if constexpr (OUT != big::wide::kGeneral) {
+        if (tn == 64)
+            hipLaunchKernelGGL((gemm_wide_kernel<SPP, BIAS, false, OUT, 64>), grid, block, 0, stream, p, tiles_m,
+                               tiles_n, total);
+        else if (tn == 128)
+            hipLaunchKernelGGL((gemm_wide_kernel<SPP, BIAS, false, OUT, 128>), grid, block, 0, stream, p, tiles_m,
+                               tiles_n, total);
+        else
+            hipLaunchKernelGGL((gemm_wide_kernel<SPP, BIAS, false, OUT, 256>), grid, block, 0, stream, p, tiles_m,
+                               tiles_n, total);
+    } else {
+        hipLaunchKernelGGL((gemm_wide_kernel<SPP, BIAS, false, OUT, 256>), grid, block, 0, stream, p, tiles_m, tiles_n,
+                           total);
+    }
+}
+
 void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream) {
     const int tiles_m = p.m / big::BM;
     const int tiles_n = p.n / big::BN;
@@ -1116,32 +1190,31 @@ void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream) {
         const bool direct = p.splits == 1;
         const int spp = ((!direct || p.d) ? 2 : 0) + ((direct && p.d_bf16) ? 1 : 0);
         require(spp > 0, "The GEMM has no output.");
-        const dim3 wblock(big::wide::NW * kWave);
         const bool bias = direct && p.bias;
         // the plain epilogues: identity activation, no bias, no beta term (split-K partials have none)
         const bool plain = !direct || (!p.bias && p.beta == 0.0f && p.epilogue == 0);
         int out = big::wide::kGeneral;
         if (plain && direct && !p.d && p.d_bf16) out = p.moments ? big::wide::kBf16Moments : big::wide::kBf16;
         else if (plain && (!direct || (p.d && !p.d_bf16 && !p.moments))) out = big::wide::kFp32;
-#define RL_WIDE(SPP, BIAS, OUT)                                                                                      \
-    do {                                                                                                            \
-        if (ak)                                                                                                     \
-            hipLaunchKernelGGL((big::wide::gemm_wide_kernel<SPP, BIAS, false, OUT>), grid, wblock, 0, stream, p,    \
-                               tiles_m, tiles_n, total);                                                            \
-        else                                                                                                        \
-            hipLaunchKernelGGL((big::wide::gemm_wide_kernel<SPP, BIAS, true, OUT>), grid, wblock, 0, stream, p,     \
-                               tiles_m, tiles_n, total);                                                            \
-    } while (0)
-        if (out == big::wide::kBf16) RL_WIDE(1, false, big::wide::kBf16);
-        else if (out == big::wide::kBf16Moments) RL_WIDE(1, false, big::wide::kBf16Moments);
-        else if (out == big::wide::kFp32) RL_WIDE(2, false, big::wide::kFp32);
-        else if (spp == 1 && bias) RL_WIDE(1, true, big::wide::kGeneral);
-        else if (spp == 1) RL_WIDE(1, false, big::wide::kGeneral);
-        else if (spp == 2 && bias) RL_WIDE(2, true, big::wide::kGeneral);
-        else if (spp == 2) RL_WIDE(2, false, big::wide::kGeneral);
-        else if (bias) RL_WIDE(3, true, big::wide::kGeneral);
-        else RL_WIDE(3, false, big::wide::kGeneral);
-#undef RL_WIDE
+        // narrower tiles where 256-wide ones leave CUs idle (each still spans whole 256-row chunks, so
+        // the BatchNorm chunk moments stay in the epilogue): the widest that gives every CU a tile, else 64
+        int tn = 256;
+        if (ak && out != big::wide::kGeneral) {
+            const long long column_tiles = static_cast<long long>(tiles_m) * p.batch * p.splits;
+            const int cus = compute_units();
+            if (column_tiles * (p.n / 256) < cus) tn = column_tiles * (p.n / 128) >= cus ? 128 : 64;
+        }
+        const bool mn = !ak;
+        using namespace big::wide;
+        if (out == kBf16) launch_wide<1, false, kBf16>(p, mn, tn, stream);
+        else if (out == kBf16Moments) launch_wide<1, false, kBf16Moments>(p, mn, tn, stream);
+        else if (out == kFp32) launch_wide<2, false, kFp32>(p, mn, tn, stream);
+        else if (spp == 1 && bias) launch_wide<1, true, kGeneral>(p, mn, tn, stream);
+        else if (spp == 1) launch_wide<1, false, kGeneral>(p, mn, tn, stream);
+        else if (spp == 2 && bias) launch_wide<2, true, kGeneral>(p, mn, tn, stream);
+        else if (spp == 2) launch_wide<2, false, kGeneral>(p, mn, tn, stream);
+        else if (bias) launch_wide<3, true, kGeneral>(p, mn, tn, stream);
+        else launch_wide<3, false, kGeneral>(p, mn, tn, stream);
     }
     else if (dma) hipLaunchKernelGGL(big::gemm_dma_kernel, grid, block, 0, stream, p, tiles_m, tiles_n, total);
     else if (ak && bk) hipLaunchKernelGGL((big::gemm_big_kernel<true, true>), grid, block, 0, stream, p, tiles_m, tiles_n, total);

@@ -282,8 +282,11 @@ def test_td_cross_entropy_matches_oracle_projection(gpu, bins):
 # renumbering), more tiles than CUs (the persistent loop), partial M-tile groups,
 # split-K, and every operand layout (both K-contiguous and both M/N-contiguous
 # take the eight-wave DMA kernel, the mixed layouts the register-staged one).
+# On a 256-CU part the K-contiguous products with fewer 256-wide tiles than CUs take 128-wide tiles
+# (8192 x 512 over 2 members) or 64-wide ones (the smaller shapes).
 BIG_SHAPES = [(2, 512, 256, 128, 1), (2, 2560, 512, 256, 1), (1, 3072, 256, 128, 1), (2, 1024, 512, 1024, 4),
-              (2, 4096, 4096, 128, 1), (1, 512, 256, 8192, 2)]  # the last: a weight gradient's long K, split
+              (2, 4096, 4096, 128, 1), (1, 512, 256, 8192, 2),  # a weight gradient's long K, split
+              (2, 8192, 512, 256, 1)]
 
 
 @pytest.mark.parametrize("a_kcontig", [True, False])
@@ -364,7 +367,8 @@ def _chunk_moments(d):
 # (batch, m, n, k, splits, a_kcontig, b_kcontig): the first three run the
 # epilogue path of the 256x256 kernel (DMA and register-staged), the rest the
 # separate pass (split-K, a ragged M, fp32-sized shapes the big kernel rejects).
-MOMENT_SHAPES = [(2, 512, 256, 256, 1, True, True), (1, 1024, 512, 192, 1, True, False),
+MOMENT_SHAPES = [(2, 512, 256, 256, 1, True, True), (2, 8192, 512, 256, 1, True, True),
+                 (1, 1024, 512, 192, 1, True, False),
                  (2, 768, 256, 128, 1, False, False), (2, 1024, 512, 1024, 4, True, True),
                  (2, 300, 256, 64, 1, True, True), (1, 512, 96, 64, 1, True, True)]
 
@@ -449,8 +453,11 @@ def test_bf16_only_gemm_output(gpu, batch, m, n, k, splits, a_kcontig, b_kcontig
     only = torch.full((batch, m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
     moments = torch.full((batch, chunks, 2, n), float("nan"), device=gpu)
     K.gemm(a_mem, b_mem, only, moments=moments, **args)
+    plain = torch.full((batch, m, n), float("nan"), dtype=torch.bfloat16, device=gpu)
+    K.gemm(a_mem, b_mem, plain, **args)  # the bf16-only epilogue without moments
     torch.cuda.synchronize()
     assert torch.equal(only.cpu().view(torch.int16), copy.cpu().view(torch.int16))
+    assert torch.equal(plain.cpu().view(torch.int16), copy.cpu().view(torch.int16))
     expected = _chunk_moments(only.cpu().float())
     got = moments.cpu().double()
     torch.testing.assert_close(got[:, :, 0], expected[:, :, 0], rtol=1e-5, atol=1e-4)
