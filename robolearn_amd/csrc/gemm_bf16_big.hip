@@ -1143,8 +1143,8 @@ static int compute_units() {
     return cached[device];
 }
 
-// The eight-wave kernel at tile width `tn` (K-contiguous operands; the plain epilogue kinds take 256,
-// 128 or 64) or 256 (M/N-contiguous operands, the general epilogue).
+// The eight-wave kernel at tile width `tn` (K-contiguous operands: 256, 128 or 64) or 256 (M/N-contiguous
+// operands).
 template <int SPP, bool BIAS, int OUT>
 static void launch_wide(const Params& p, bool mn, int tn, hipStream_t stream) {
     const int tiles_m = p.m / big::BM;
@@ -1156,7 +1156,7 @@ static void launch_wide(const Params& p, bool mn, int tn, hipStream_t stream) {
     if (mn) {
         hipLaunchKernelGGL((gemm_wide_kernel<SPP, BIAS, true, OUT, 256>), grid, block, 0, stream, p, tiles_m, tiles_n,
                            total);
-    } else if constexpr (OUT != big::wide::kGeneral) {
+    } else {
         if (tn == 64)
             hipLaunchKernelGGL((gemm_wide_kernel<SPP, BIAS, false, OUT, 64>), grid, block, 0, stream, p, tiles_m,
                                tiles_n, total);
@@ -1166,9 +1166,6 @@ static void launch_wide(const Params& p, bool mn, int tn, hipStream_t stream) {
         else
             hipLaunchKernelGGL((gemm_wide_kernel<SPP, BIAS, false, OUT, 256>), grid, block, 0, stream, p, tiles_m,
                                tiles_n, total);
-    } else {
-        hipLaunchKernelGGL((gemm_wide_kernel<SPP, BIAS, false, OUT, 256>), grid, block, 0, stream, p, tiles_m, tiles_n,
-                           total);
     }
 }
 
@@ -1199,7 +1196,7 @@ void launch_big(const Params& p, bool ak, bool bk, hipStream_t stream) {
         // narrower tiles where 256-wide ones leave CUs idle (each still spans whole 256-row chunks, so
         // the BatchNorm chunk moments stay in the epilogue): the widest that gives every CU a tile, else 64
         int tn = 256;
-        if (ak && out != big::wide::kGeneral) {
+        if (ak) {
             const long long column_tiles = static_cast<long long>(tiles_m) * p.batch * p.splits;
             const int cus = compute_units();
             if (column_tiles * (p.n / 256) < cus) tn = column_tiles * (p.n / 128) >= cus ? 128 : 64;

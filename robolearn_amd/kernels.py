@@ -79,20 +79,27 @@ def gemm(
     )
 
 
-def forward_split_count(m, n, k, batch, mode):
+def forward_split_count(m, n, k, batch, mode, kcontig=True):
     """K splits for a forward or input-gradient product whose output tiles cannot fill the GPU (a
     narrow head, or a narrow layer over a long K at a small batch).
 
-    bf16 (heads, embedder input gradients, block input gradients): 256x128 tiles, at least 256
-    workgroups, each split >= 128 of K.  A bf16 block forward product is not split even where its
-    tiles leave CUs idle (README shape): the split loses the BatchNorm moments of the 256x256 kernel's
-    epilogue and adds a reduction, which measured slower.
+    bf16 (heads, embedder input gradients, block input gradients): at least 256 workgroups.  Products
+    the eight-wave kernel takes (both operands K-contiguous, m and n multiples of 256, K of 128) count
+    its narrowest tiles, 256 x 64, which fill the GPU without partials or a reduction launch, and split
+    only in multiples of 128 of K; the others count 256x128 tiles, each split >= 128 of K.  A bf16 block
+    forward product is not split even where its tiles leave CUs idle (README shape): the split loses
+    the BatchNorm moments of the epilogue and adds a reduction, which measured slower.
     fp32: 64x64 tiles, whose K loop is latency-bound when few workgroups share a CU; at least 1024
     workgroups, each split >= 256 of K: a split costs a reduction launch, which a shorter K loop
     repays only past that (Cartpole input gradient 1024 x 1024 over K = 256: 17.8 us unsplit, 25.2 us
     in two splits)."""
     splits = 1
     if mode == BF16:
+        if kcontig and m % 256 == 0 and n % 256 == 0 and k % 128 == 0:
+            tiles = (m // 256) * (n // 64) * batch
+            while tiles * splits < 256 and (k // (2 * splits)) % 128 == 0 and splits < 16:
+                splits *= 2
+            return splits
         tiles = ((m + 255) // 256) * ((n + 127) // 128) * batch
         ktiles = (k + 31) // 32
         while tiles * splits < 256 and splits * 2 <= max(1, ktiles // 4) and splits < 16:
@@ -104,11 +111,11 @@ def forward_split_count(m, n, k, batch, mode):
     return splits
 
 
-def _split_for(m, n, k, batch, mode, workspace):
+def _split_for(m, n, k, batch, mode, workspace, kcontig=True):
     """forward_split_count, limited to what the workspace holds (1 without one)."""
     if workspace is None:
         return 1
-    splits = forward_split_count(m, n, k, batch, mode)
+    splits = forward_split_count(m, n, k, batch, mode, kcontig)
     if splits > 1:
         need = _native.load().rl_gemm_workspace(mode, m, n, k, batch, splits)
         if need > workspace.numel() * workspace.element_size():
@@ -141,7 +148,7 @@ def linear_backward_input(dy, w, dx, *, rows, in_dim, out_dim, ensemble=1, mode=
     elu'(c), c holding the ELU outputs of the layer below.  With a workspace, a product too small
     to fill the GPU is split over K (fixed-order reduction)."""
     _check(dx, ensemble * rows * in_dim, "input gradient", dx.dtype)
-    splits = _split_for(rows, in_dim, out_dim, ensemble, mode, workspace)
+    splits = _split_for(rows, in_dim, out_dim, ensemble, mode, workspace, kcontig=wt is not None)
     ws = workspace if splits > 1 else None
     if wt is not None:
         _check(wt, ensemble * out_dim * in_dim, "transposed weight", wt.dtype)
