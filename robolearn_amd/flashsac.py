@@ -667,7 +667,7 @@ class FlashSAC:
         net.forward(p, self.actor_w, self.actor_running, self.actor_in, rows=2 * B, x_stride=0, training=True)
         net.post_norm(p, rows=2 * B, row0=0, count=2 * B)
         K.linear_forward(net.z_op, self.head_w_op, self.actor_head, rows=2 * B, in_dim=net.h, out_dim=2 * A,
-                         bias=self.head_b, mode=self.mode)
+                         bias=self.head_b, mode=self.mode, workspace=self.workspace)
         K.tanh_gaussian_forward(self.actor_head, self.actor_noise, self.actions_all, self.log_probs_all,
                                 rows=2 * B, action_dim=A)
         # frozen critic in eval mode on (obs, first-half actions)
@@ -735,7 +735,7 @@ class FlashSAC:
         net.forward(p, self.actor_w, self.actor_running, self.actor_in[B:], rows=B, x_stride=0, training=False)
         net.post_norm(p, rows=B, row0=0, count=B)
         K.linear_forward(net.z_op, self.head_w_op, self.actor_head, rows=B, in_dim=net.h, out_dim=2 * A,
-                         bias=self.head_b, mode=self.mode)
+                         bias=self.head_b, mode=self.mode, workspace=self.workspace)
         K.tanh_gaussian_forward(self.actor_head, self.next_noise, self.critic_in[B:].view(-1)[Oc:],
                                 self.next_log_probs, rows=B, action_dim=A, ld_actions=I)
         _native.call("rl_exp_scalar", self.log_temperature.data_ptr(), self.alpha.data_ptr(), K.stream())

@@ -171,9 +171,11 @@ def transpose16(src, dst, *, batch, rows, cols):
 def split_count(m, n, k, batch, mode):
     """K splits for a weight-gradient product (small output, K = rows).
 
-    bf16: at least two 256x128-tile workgroups per CU, each split >= 1024 of K; >= 256 of K
+    bf16: at least two 256x128-tile workgroups per CU, each split >= 1024 of K; >= 128 of K
     when the output does not tile by 256 (a narrow head or embedder: those products run on
-    the 256x128 kernel, whose workgroups are short enough that more of them pays).  For the
+    the 256x128 kernel, whose workgroups are short enough that more of them pays: README head
+    dW 101 x 512 over 2048 rows 30.7 us in 8 splits, 22.6 in 16; embedder dW 256 x 31 over 4096
+    rows 24.0 us in 16, 17.5 in 32).  For the
     256x256-tile kernel a longer split beats more workgroups: its partials cost a write and a
     read of splits x M x N floats (README dW 2048 x 512 over 4096 rows: 44 us at 4 splits, 52 us
     at 8).
@@ -186,7 +188,7 @@ def split_count(m, n, k, batch, mode):
     if mode == BF16:
         tiles = ((m + 255) // 256) * ((n + 127) // 128) * batch
         ktiles = (k + 31) // 32
-        min_ktiles = 32 if m % 256 == 0 and n % 256 == 0 else 8
+        min_ktiles = 32 if m % 256 == 0 and n % 256 == 0 else 4
         while tiles * splits < 512 and splits * 2 <= max(1, ktiles // min_ktiles) and splits < 64:
             splits *= 2
         return splits
