@@ -117,14 +117,37 @@ def elementwise_bytes(w: dict, act_bytes: int = 4) -> float:
 DOMINANT_SOURCES = ("common.hpp", "gemm.hpp", "gemm_bf16_big.hip")
 
 
+def _code_of(text: str) -> str:
+    """C++ source without its comments and blank lines (string literals kept as written)."""
+    out, i, n = [], 0, len(text)
+    while i < n:
+        if text.startswith("//", i):
+            i = text.find("\n", i)
+            i = n if i < 0 else i
+        elif text.startswith("/*", i):
+            j = text.find("*/", i + 2)
+            i = n if j < 0 else j + 2
+        elif text[i] == '"':
+            j = i + 1
+            while j < n and text[j] != '"':
+                j += 2 if text[j] == "\\" else 1
+            out.append(text[i:j + 1])
+            i = j + 1
+        else:
+            out.append(text[i])
+            i += 1
+    return "\n".join(line.rstrip() for line in "".join(out).splitlines() if line.strip())
+
+
 def source_fingerprint() -> str:
-    """First 16 hex digits of the SHA-256 of the dominant kernel's sources (names and bytes, in order)."""
+    """First 16 hex digits of the SHA-256 of the dominant kernel's sources (names and code, in order;
+    comments and blank lines do not count, so a comment edit does not orphan a measurement)."""
     import hashlib
 
     digest = hashlib.sha256()
     for name in DOMINANT_SOURCES:
         digest.update(name.encode())
-        digest.update((ROOT / "robolearn_amd" / "csrc" / name).read_bytes())
+        digest.update(_code_of((ROOT / "robolearn_amd" / "csrc" / name).read_text()).encode())
     return digest.hexdigest()[:16]
 
 

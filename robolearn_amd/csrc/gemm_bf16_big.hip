@@ -1,11 +1,13 @@
-// bf16 MFMA GEMMs for the large dense-layer products: 256x256 output tiles,
-// one persistent workgroup per CU, bf16 operands whose shapes tile exactly
-// (m, n multiples of 256, 16-byte aligned rows).  Same row-major contract as
+// bf16 MFMA GEMMs for the large dense-layer products: 256x256 output tiles
+// (256 x 128 or 256 x 64 where 256-wide tiles would leave CUs idle), one
+// persistent workgroup per CU, bf16 operands whose shapes tile exactly (m, n
+// multiples of 256, 16-byte aligned rows).  Same row-major contract as
 // gemm_bf16.hip.  Three kernels:
 //
 //   * gemm_wide_kernel (namespace wide), the one that carries the G1 update:
 //     8 waves (two per SIMD) of 128x64 outputs as 4x2
-//     v_mfma_f32_32x32x16_bf16 accumulators; operands move global -> LDS by
+//     v_mfma_f32_32x32x16_bf16 accumulators (narrow tiles: the waves stacked
+//     4 or 8 deep, 64x64 or 32x64 each); operands move global -> LDS by
 //     buffer_load_dwordx4 ... lds (no register staging; the K tile's window in
 //     a scalar buffer descriptor, per-lane offsets fixed per launch) into two
 //     64-deep K stages of 64 KB, the two row halves issuing one substep apart,
@@ -585,7 +587,8 @@ __global__ __launch_bounds__(T, 1) void gemm_dma_kernel(Params p, int tiles_m, i
 // and writes 8 consecutive columns per lane (32-byte fp32 / 16-byte bf16 row
 // pieces); per-column BatchNorm chunk moments are accumulated from the stored
 // values, merged across the 8 lane groups of a wave with butterflies (the lower
-// lane always first) and across the two row halves of the tile through LDS.
+// lane always first) and across the row groups of the tile (two for 256-wide
+// tiles, four or eight for the narrow ones) through LDS, in row-group order.
 // ---------------------------------------------------------------------------
 namespace wide {
 
