@@ -58,14 +58,14 @@ __device__ __forceinline__ void split3_pair(float a, float b, unsigned& p0, unsi
     p2 = __builtin_amdgcn_perm(__float_as_uint(sb), __float_as_uint(sa), kHighHalves);
 }
 
-// Loads one Rows x 16 operand tile into registers and later stores it to LDS.
-// Element (r, k) of the operand is src[r * ld + k] when KContig, else
-// src[k * ld + r].
-template <bool KContig, int Rows>
+// Loads one Rows x kFp32K operand tile into registers (Threads threads) and
+// later stores it to LDS.  Element (r, k) of the operand is src[r * ld + k]
+// when KContig, else src[k * ld + r].
+template <bool KContig, int Rows, int Threads>
 struct TileLoader {
     static constexpr int VecPerRow = kFp32K / 4;
-    static constexpr int PerThread = KContig ? Rows * VecPerRow / kThreads : 1;
-    static constexpr int Groups = kThreads / Rows;      // M/N-contiguous: k groups per tile
+    static constexpr int PerThread = KContig ? Rows * VecPerRow / Threads : 1;
+    static constexpr int Groups = Threads / Rows;      // M/N-contiguous: k groups per tile
     static constexpr int KPer = kFp32K / Groups;        // k values per thread
     static constexpr int Count = KContig ? PerThread * 4 : KPer;
     static_assert(KContig ? PerThread >= 1 : (KPer >= 1 && kFp32K % Groups == 0), "tile/thread mismatch");
@@ -76,7 +76,7 @@ struct TileLoader {
         if constexpr (KContig) {
 #pragma unroll
             for (int i = 0; i < PerThread; ++i) {
-                const int v = i * kThreads + t;
+                const int v = i * Threads + t;
                 const int r = r0 + v / VecPerRow;
                 const int k = k0 + (v % VecPerRow) * 4;
                 const float* q = src + static_cast<long long>(r) * ld + k;
@@ -108,7 +108,7 @@ struct TileLoader {
         if constexpr (KContig) {
 #pragma unroll
             for (int i = 0; i < PerThread; ++i) {
-                const int v = i * kThreads + t;
+                const int v = i * Threads + t;
                 *reinterpret_cast<float4*>(lds + (v / VecPerRow) * kFp32Pitch + (v % VecPerRow) * 4) =
                     make_float4(regs[i * 4 + 0], regs[i * 4 + 1], regs[i * 4 + 2], regs[i * 4 + 3]);
             }
@@ -126,7 +126,7 @@ struct TileLoader {
         if constexpr (KContig) {
 #pragma unroll
             for (int i = 0; i < PerThread; ++i) {
-                const int v = i * kThreads + t;
+                const int v = i * Threads + t;
                 const int offset = (v / VecPerRow) * kSplitPitch + (v % VecPerRow) * 4;
                 unsigned w[3][2];
                 split3_pair(regs[i * 4 + 0], regs[i * 4 + 1], w[0][0], w[1][0], w[2][0]);
@@ -158,9 +158,19 @@ struct TileLoader {
     }
 };
 
-template <int T, bool AK, bool BK, bool Split>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
-    constexpr int WB = T / 64;  // 32x32 accumulator blocks per wave and dimension
+// NW waves own the T x T tile as WGM x WGN wave tiles of (T / WGM) x (T / WGN):
+// 4 waves as 2 x 2, 8 waves (mode 2, 128-wide tiles) as 2 x 4.
+// Eight-wave workgroups are held to 128 VGPRs, so that two of them (four waves per
+// SIMD) share a CU.
+template <int T, int NW, bool AK, bool BK, bool Split>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 4 : 1))) void gemm_kernel(
+    Params p) {
+    constexpr int Threads = NW * kWave;
+    constexpr int WGN = NW == 4 ? 2 : 4;
+    constexpr int WGM = NW / WGN;
+    constexpr int WTM = T / WGM, WTN = T / WGN;    // wave tile
+    constexpr int WBM = WTM / 32, WBN = WTN / 32;  // 32x32 accumulator blocks per wave
+    static_assert((NW == 4 || NW == 8) && WBM >= 1 && WBN >= 1, "wave layouts");
     constexpr int Plane = T * kSplitPitch;  // bf16 per split plane
     constexpr int StageBytes = Split ? 3 * Plane * 2 : T * kFp32Pitch * 4;
     __shared__ __attribute__((aligned(16))) unsigned char sa_raw[StageBytes];
@@ -192,25 +202,25 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
 
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
-    const int wm = wave / 2;
-    const int wn = wave % 2;
+    const int wm = wave / WGN;
+    const int wn = wave % WGN;
 
-    f32x16_t acc[WB][WB];
+    f32x16_t acc[WBM][WBN];
 #pragma unroll
-    for (int i = 0; i < WB; ++i)
+    for (int i = 0; i < WBM; ++i)
 #pragma unroll
-        for (int j = 0; j < WB; ++j)
+        for (int j = 0; j < WBN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    TileLoader<AK, T> la;
-    TileLoader<BK, T> lb;
+    TileLoader<AK, T, Threads> la;
+    TileLoader<BK, T, Threads> lb;
     const bool avec = p.a_vec != 0;
     const bool bvec = p.b_vec != 0;
     // Row sums of op(A) over this split's K (the bias gradient of a weight-
     // gradient product), by the workgroups of the first N tile: thread t adds
-    // kFp32K * T / 256 staged values of row t / (256 / T) per step.
-    constexpr int SumLanes = kThreads / T;
+    // kFp32K * T / Threads staged values of row t / (Threads / T) per step.
+    constexpr int SumLanes = Threads / T;
     constexpr int SumPer = kFp32K / SumLanes;
     const bool row_sums = p.a_sums != nullptr && bx == 0;
     // compensated (Kahan) accumulation: bias gradients are sums over thousands of
@@ -256,24 +266,24 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
         if constexpr (Split) {
 #pragma unroll
           for (int sub = 0; sub < kFp32K / 16; ++sub) {
-            bf16x8_t af[WB][3], bf[WB][3];
+            bf16x8_t af[WBM][3], bf[WBN][3];
             const int koff = 16 * sub + 8 * (lane / 32);
 #pragma unroll
-            for (int i = 0; i < WB; ++i) {
-                const int off = (wm * (T / 2) + i * 32 + lane % 32) * kSplitPitch + koff;
+            for (int i = 0; i < WBM; ++i) {
+                const int off = (wm * WTM + i * 32 + lane % 32) * kSplitPitch + koff;
 #pragma unroll
                 for (int q = 0; q < 3; ++q) af[i][q] = *reinterpret_cast<const bf16x8_t*>(ha + q * Plane + off);
             }
 #pragma unroll
-            for (int j = 0; j < WB; ++j) {
-                const int off = (wn * (T / 2) + j * 32 + lane % 32) * kSplitPitch + koff;
+            for (int j = 0; j < WBN; ++j) {
+                const int off = (wn * WTN + j * 32 + lane % 32) * kSplitPitch + koff;
 #pragma unroll
                 for (int q = 0; q < 3; ++q) bf[j][q] = *reinterpret_cast<const bf16x8_t*>(hb + q * Plane + off);
             }
 #pragma unroll
-            for (int i = 0; i < WB; ++i) {
+            for (int i = 0; i < WBM; ++i) {
 #pragma unroll
-                for (int j = 0; j < WB; ++j) {
+                for (int j = 0; j < WBN; ++j) {
                     f32x16_t c = acc[i][j];
                     c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][0], bf[j][0], c, 0, 0, 0);
                     c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i][0], bf[j][1], c, 0, 0, 0);
@@ -297,26 +307,26 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
         }
 #pragma unroll
         for (int sub = 0; sub < kFp32K / 16; ++sub) {
-            float4 af[WB][2], bfr[WB][2];
+            float4 af[WBM][2], bfr[WBN][2];
 #pragma unroll
-            for (int i = 0; i < WB; ++i) {
-                const float* q = sa + (wm * (T / 2) + i * 32 + lane % 32) * kFp32Pitch + 16 * sub + (lane / 32) * 8;
+            for (int i = 0; i < WBM; ++i) {
+                const float* q = sa + (wm * WTM + i * 32 + lane % 32) * kFp32Pitch + 16 * sub + (lane / 32) * 8;
                 af[i][0] = *reinterpret_cast<const float4*>(q);
                 af[i][1] = *reinterpret_cast<const float4*>(q + 4);
             }
 #pragma unroll
-            for (int j = 0; j < WB; ++j) {
-                const float* q = sb + (wn * (T / 2) + j * 32 + lane % 32) * kFp32Pitch + 16 * sub + (lane / 32) * 8;
+            for (int j = 0; j < WBN; ++j) {
+                const float* q = sb + (wn * WTN + j * 32 + lane % 32) * kFp32Pitch + 16 * sub + (lane / 32) * 8;
                 bfr[j][0] = *reinterpret_cast<const float4*>(q);
                 bfr[j][1] = *reinterpret_cast<const float4*>(q + 4);
             }
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
 #pragma unroll
-                for (int i = 0; i < WB; ++i) {
+                for (int i = 0; i < WBM; ++i) {
                     const float a = s < 4 ? af[i][0][s] : af[i][1][s - 4];
 #pragma unroll
-                    for (int j = 0; j < WB; ++j) {
+                    for (int j = 0; j < WBN; ++j) {
                         const float b = s < 4 ? bfr[j][0][s] : bfr[j][1][s - 4];
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[i][j], 0, 0, 0);
                     }
@@ -337,7 +347,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
         if (t < T) {
             float total = part[t];
 #pragma unroll
-            for (int g = 1; g < kThreads / T; ++g) total += part[g * T + t];
+            for (int g = 1; g < Threads / T; ++g) total += part[g * T + t];
             const int r = m0 + t;
             if (r < p.m)
                 p.a_sums[(p.splits == 1 ? batch * p.sums_stride
@@ -362,15 +372,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(Params p) {
     const float* bias = p.bias ? p.bias + batch * p.stride_bias : nullptr;
     const float* C = p.c ? p.c + batch * p.stride_d : nullptr;
 #pragma unroll
-    for (int i = 0; i < WB; ++i) {
+    for (int i = 0; i < WBM; ++i) {
 #pragma unroll
-        for (int j = 0; j < WB; ++j) {
-            const int col = n0 + wn * (T / 2) + j * 32 + lane % 32;
+        for (int j = 0; j < WBN; ++j) {
+            const int col = n0 + wn * WTN + j * 32 + lane % 32;
             if (col >= p.n) continue;
             const float bcol = (direct && bias) ? bias[col] : 0.0f;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * (T / 2) + i * 32 + 8 * (v / 4) + 4 * (lane / 32) + (v % 4);
+                const int row = m0 + wm * WTM + i * 32 + 8 * (v / 4) + 4 * (lane / 32) + (v % 4);
                 if (row >= p.m) continue;
                 const long long offset = static_cast<long long>(row) * ldd + col;
                 float* out = D + offset;
@@ -514,23 +524,31 @@ __global__ __launch_bounds__(256) void splitk_reduce_grouped(const float* work, 
     if (d_bf16) d_bf16[offset] = f32_to_bf16_bits(value);
 }
 
+// Workgroups of 128 x 128 tiles (all splits) from which a mode-2 product runs
+// them on eight waves: each split staged value then feeds twice the MFMAs of a
+// 64 x 64 tile, and the operand reads per product halve.  Outputs of at most 64
+// rows or columns (heads) keep the 64 x 64 tiles, which waste less of a tile.
+constexpr long long kSplitWideTiles = 256;
+
 // Output tile edge for an fp32 product: 64 unless 128-wide tiles would still
-// give every SIMD several waves of work.
-int fp32_tile(const Params& p) {
+// give every SIMD several waves of work (mode 0), or every CU a workgroup of
+// eight waves (mode 2).
+int fp32_tile(const Params& p, bool split) {
     const long long big = static_cast<long long>(ceil_div(p.m, 128)) * ceil_div(p.n, 128) * p.batch * p.splits;
+    if (split) return p.m > 64 && p.n > 64 && big >= kSplitWideTiles ? 128 : 64;
     return big >= 2048 ? 128 : 64;
 }
 
-template <int T, bool AK, bool BK, bool Split>
+template <int T, int NW, bool AK, bool BK, bool Split>
 void launch_fp32_tiled(const Params& p, hipStream_t stream) {
     const dim3 grid(ceil_div(p.n, T), ceil_div(p.m, T), static_cast<unsigned>(p.batch * p.splits));
-    hipLaunchKernelGGL((gemm_kernel<T, AK, BK, Split>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((gemm_kernel<T, NW, AK, BK, Split>), grid, dim3(NW * kWave), 0, stream, p);
 }
 
 template <bool AK, bool BK, bool Split>
 void launch_fp32_layout(const Params& p, hipStream_t stream) {
-    if (fp32_tile(p) == 128) launch_fp32_tiled<128, AK, BK, Split>(p, stream);
-    else launch_fp32_tiled<64, AK, BK, Split>(p, stream);
+    if (fp32_tile(p, Split) == 128) launch_fp32_tiled<128, Split ? 8 : 4, AK, BK, Split>(p, stream);
+    else launch_fp32_tiled<64, 4, AK, BK, Split>(p, stream);
 }
 
 template <bool Split>

@@ -183,7 +183,10 @@ def split_count(m, n, k, batch, mode):
     workgroups (four per CU), each split >= 256 of K, whose reduction then costs less than the
     shorter K loops save (Cartpole 256 x 1024 over 1024 rows: 23.6 us in 4 splits, 25.9 in 8); an
     output of at most 65,536 values (a head) takes splits down to 64 of K, since its reduction is
-    nearly free."""
+    nearly free.  Mode 2 outputs of more than 64 rows and columns whose splits reach 256 of the
+    eight-wave 128x128-tile workgroups run there: at least 512 of them (two per CU), each split
+    >= 384 of K (PPO c3 dW 256 x 512 over 24576 rows: 105.7 us in 16 splits, 98.0 in 32; 128 x 256:
+    36.6 us in 64, 39.2 in 128)."""
     splits = 1
     if mode == BF16:
         tiles = ((m + 255) // 256) * ((n + 127) // 128) * batch
@@ -192,6 +195,13 @@ def split_count(m, n, k, batch, mode):
         while tiles * splits < 512 and splits * 2 <= max(1, ktiles // min_ktiles) and splits < 64:
             splits *= 2
         return splits
+    if mode == FP32_SPLIT and m > 64 and n > 64:
+        wide = ((m + 127) // 128) * ((n + 127) // 128) * batch
+        while wide * splits < 512 and splits * 2 <= k // 384 and splits < 256:
+            splits *= 2
+        if wide * splits >= 256:
+            return splits
+        splits = 1
     tiles = ((m + 63) // 64) * ((n + 63) // 64) * batch
     steps = (k + 15) // 16
     min_steps = 4 if m * n * batch <= 65536 else 16

@@ -578,7 +578,10 @@ def test_fp32_weight_gradient_with_fused_bias_gradient(gpu, rows, in_dim, out_di
     torch.testing.assert_close(db.cpu().double(), dy.double().sum(0), rtol=1e-4, atol=1e-4 * math.sqrt(rows))
 
 
-SPLIT_SHAPES = [(1, 5, 7, 3), (2, 130, 129, 40), (2, 257, 96, 160), (1, 300, 37, 123), (2, 2048, 512, 256)]
+# the last two run the forward products and the split weight gradients on eight-wave 128 x 128 tiles
+# (ragged in every dimension in the last)
+SPLIT_SHAPES = [(1, 5, 7, 3), (2, 130, 129, 40), (2, 257, 96, 160), (1, 300, 37, 123), (2, 2048, 512, 256),
+                (2, 8192, 512, 123), (2, 6000, 300, 130)]
 
 
 @pytest.mark.parametrize("batch,rows,out_dim,in_dim", SPLIT_SHAPES)
@@ -627,9 +630,12 @@ def test_fp32_split_products_are_fp32_accurate(gpu, batch, rows, out_dim, in_dim
     native, split = run(K.FP32), run(K.FP32_SPLIT)
     refs = {"y": ref_y, "g": torch.einsum("bri,boi->bro", x64, w64) * elu_grad, "dx": ref_dx,
             "dw_direct": ref_dw, "db_direct": ref_db, "dw_split": ref_dw, "db_split": ref_db}
+    # reduction length of each product: fp32 accumulation error grows as its square root
+    length = {"y": in_dim, "g": in_dim, "dx": out_dim, "dw_direct": rows, "db_direct": rows, "dw_split": rows,
+              "db_split": rows}
     for key, ref in refs.items():
         scale = ref.abs().max().item() + 1e-30
         err_native = (native[key] - ref).abs().max().item()
         err_split = (split[key] - ref).abs().max().item()
         assert err_split <= 4.0 * err_native + 2e-7 * scale, (key, err_split, err_native, scale)
-        assert err_split <= 2e-6 * scale, (key, err_split, scale)
+        assert err_split <= 2e-6 * scale * max(1.0, math.sqrt(length[key] / 2048)), (key, err_split, scale)
