@@ -71,6 +71,28 @@ struct TileLoader {
     static_assert(KContig ? PerThread >= 1 : (KPer >= 1 && kFp32K % Groups == 0), "tile/thread mismatch");
     float regs[Count];
 
+    // A tile wholly inside the operand (rows r0 .. r0 + Rows - 1 < rows, k0 + kFp32K <= ks) and, K-contiguous,
+    // with 16-byte aligned rows: the loads need no per-element checks.
+    __device__ __forceinline__ void load_full(const float* src, long long ld, int r0, int k0) {
+        const int t = threadIdx.x;
+        if constexpr (KContig) {
+#pragma unroll
+            for (int i = 0; i < PerThread; ++i) {
+                const int v = i * Threads + t;
+                const float4 x = *reinterpret_cast<const float4*>(
+                    src + static_cast<long long>(r0 + v / VecPerRow) * ld + k0 + (v % VecPerRow) * 4);
+                regs[i * 4 + 0] = x.x;
+                regs[i * 4 + 1] = x.y;
+                regs[i * 4 + 2] = x.z;
+                regs[i * 4 + 3] = x.w;
+            }
+        } else {
+            const float* q = src + static_cast<long long>(k0 + (t / Rows) * KPer) * ld + r0 + t % Rows;
+#pragma unroll
+            for (int e = 0; e < KPer; ++e) regs[e] = q[e * ld];
+        }
+    }
+
     __device__ __forceinline__ void load(const float* src, long long ld, int r0, int k0, int rows, int ks, bool vec) {
         const int t = threadIdx.x;
         if constexpr (KContig) {
@@ -250,19 +272,24 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(NW =
             lb.store(sb);
         }
     };
+    // K steps whose operand tiles lie wholly inside A and B (uniform per workgroup) take the unchecked loads
+    const bool a_full = (!AK || avec) && m0 + T <= p.m;
+    const bool b_full = (!BK || bvec) && n0 + T <= p.n;
+    const auto load_step = [&](int k0) {
+        if (a_full && k0 + kFp32K <= k_end) la.load_full(A, p.lda, m0, k0);
+        else la.load(A, p.lda, m0, k0, p.m, k_end, avec);
+        if (b_full && k0 + kFp32K <= k_end) lb.load_full(B, p.ldb, n0, k0);
+        else lb.load(B, p.ldb, n0, k0, p.n, k_end, bvec);
+    };
     if (k_begin < k_end) {
-        la.load(A, p.lda, m0, k_begin, p.m, k_end, avec);
-        lb.load(B, p.ldb, n0, k_begin, p.n, k_end, bvec);
+        load_step(k_begin);
         stage();
     }
     __syncthreads();
 
     for (int k0 = k_begin; k0 < k_end; k0 += kFp32K) {
         const bool more = k0 + kFp32K < k_end;
-        if (more) {
-            la.load(A, p.lda, m0, k0 + kFp32K, p.m, k_end, avec);
-            lb.load(B, p.ldb, n0, k0 + kFp32K, p.n, k_end, bvec);
-        }
+        if (more) load_step(k0 + kFp32K);
         if constexpr (Split) {
 #pragma unroll
           for (int sub = 0; sub < kFp32K / 16; ++sub) {
