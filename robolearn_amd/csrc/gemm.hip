@@ -398,6 +398,24 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(NW =
     const long long ldd = direct ? p.ldd : p.n;
     const float* bias = p.bias ? p.bias + batch * p.stride_bias : nullptr;
     const float* C = p.c ? p.c + batch * p.stride_d : nullptr;
+    // Every C value this lane needs is loaded before its first store: the compiler cannot tell C from D
+    // apart, so a load left inside the store loop would wait for the stores before it and expose one
+    // memory round trip per element (the ELU-gradient products of the PPO backward read C everywhere).
+    const bool read_c = direct && C && (p.epilogue == kEluGrad || p.beta != 0.0f);
+    float cv[WBM][WBN][16];
+    if (read_c) {
+#pragma unroll
+        for (int i = 0; i < WBM; ++i)
+#pragma unroll
+            for (int j = 0; j < WBN; ++j) {
+                const int col = n0 + wn * WTN + j * 32 + lane % 32;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int row = m0 + wm * WTM + i * 32 + 8 * (v / 4) + 4 * (lane / 32) + (v % 4);
+                    cv[i][j][v] = (col < p.n && row < p.m) ? C[static_cast<long long>(row) * ldd + col] : 0.0f;
+                }
+            }
+    }
 #pragma unroll
     for (int i = 0; i < WBM; ++i) {
 #pragma unroll
@@ -414,10 +432,10 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(NW =
                 if (direct) {
                     float value;
                     if (p.epilogue == kEluGrad) {
-                        value = acc[i][j][v] * elu_grad_from_output(C[offset]);
+                        value = acc[i][j][v] * elu_grad_from_output(cv[i][j][v]);
                     } else {
                         value = apply_epilogue(acc[i][j][v] + bcol, p.epilogue);
-                        if (p.beta != 0.0f) value += p.beta * C[offset];
+                        if (p.beta != 0.0f) value += p.beta * cv[i][j][v];
                     }
                     *out = value;
                     if (p.d_bf16) p.d_bf16[batch * p.stride_d + offset] = f32_to_bf16_bits(value);

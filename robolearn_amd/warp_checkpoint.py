@@ -314,7 +314,10 @@ def save(agent, path, *, include_replay: bool = False) -> None:
         "num_envs": agent.num_envs,
         "config": asdict(agent.cfg),
         "optimized_linear_backward": True,
-        "dense_backend": agent.dense_backend,
+        # the reference's name for its native dense backend, which this library stands in for: its
+        # constructor accepts only "warp" or "cuda" (warp/flashsac.py:354-358), and fused updates
+        # and mixed precision need "cuda"
+        "dense_backend": "cuda",
         "fused_updates": agent.fused_updates,
         "cuda_autotune": False,
         "fresh_training_gradients": False,

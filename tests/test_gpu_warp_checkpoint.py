@@ -66,6 +66,8 @@ def test_warp_arrays_follow_the_reference_definition(gpu, tmp_path):
     meta = json.loads((tmp_path / "ckpt" / "config.json").read_text())
     assert meta["format"] == "robolearn-warp-flashsac-v1" and meta["replay_included"] is False
     assert meta["observation_dim"] == OBS and meta["action_dim"] == ACT and meta["num_envs"] == ENVS
+    # a backend the reference's WarpFlashSAC constructor accepts with fused updates (flashsac.py:354-358)
+    assert meta["dense_backend"] == "cuda" and meta["fused_updates"] is True
     with np.load(tmp_path / "ckpt" / "agent.npz", allow_pickle=False) as archive:
         saved = {k: archive[k] for k in archive.files}
     actor_keys = list(_fixture("actor.pt")["network_state_dict"])
