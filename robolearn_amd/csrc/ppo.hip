@@ -308,6 +308,28 @@ struct LossArgs {
 
 // Clipped surrogate, clipped value and entropy terms of one row and their
 // gradients with respect to the mean, the value and the std parameter.
+// Terms of action dimension j that depend only on the std parameter (shared by every row): the log
+// std, its inverse exponential, d log std / d parameter and the std itself.
+struct DimTerms {
+    float ls, inv_std, dls_dp, std;
+};
+
+__device__ __forceinline__ DimTerms dim_terms(const LossArgs& a, int j) {
+    const float p = a.std_param[j];
+    DimTerms d;
+    if (a.std_type == 1) {
+        const float c = fminf(fmaxf(p, a.std_min), a.std_max);
+        d.ls = logf(c);
+        d.dls_dp = (p >= a.std_min && p <= a.std_max) ? 1.0f / c : 0.0f;
+    } else {
+        d.ls = p;
+        d.dls_dp = 1.0f;
+    }
+    d.inv_std = expf(-d.ls);
+    d.std = std_of(p, a.std_type, a.std_min, a.std_max);
+    return d;
+}
+
 __global__ __launch_bounds__(kRowThreads) void loss_kernel(LossArgs a) {
     __shared__ float waves[5][kRowWaves];
     __shared__ float std_cols[kRowWaves][kWave];
@@ -319,21 +341,63 @@ __global__ __launch_bounds__(kRowThreads) void loss_kernel(LossArgs a) {
     const int wave = threadIdx.x / kWave;
     float sums[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     float std_col = 0.0f;  // fused form: this lane's std-gradient column (lane < A, A <= 64)
-    for (int r = wave; r < kRowsPerBlock; r += kRowWaves) {
-        const long long i = blockIdx.x * static_cast<long long>(kRowsPerBlock) + r;
-        if (i >= a.rows) break;
-        float log_prob = 0.0f, entropy = 0.0f;
-        for (int j = lane; j < a.action_dim; j += kWave) {
-            const float p = a.std_param[j];
-            const float ls = a.std_type == 1 ? logf(fminf(fmaxf(p, a.std_min), a.std_max)) : p;
-            const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * expf(-ls);
-            log_prob -= 0.5f * (residual * residual + 2.0f * ls + ln_two_pi);
-            entropy += ls + entropy_const;
+    // At most one action dimension per lane (A <= 64): its std terms and the row entropy, which does not
+    // depend on the row, are computed once per wave instead of once per row (the same expressions, so the
+    // same values); wider actions take the per-row loops.
+    const bool one_dim = a.action_dim <= kWave;
+    const bool mine = lane < a.action_dim;
+    DimTerms own{0.0f, 0.0f, 0.0f, 1.0f};
+    float row_entropy = 0.0f;
+    if (one_dim) {
+        if (mine) own = dim_terms(a, lane);
+        row_entropy = wave_sum(mine ? own.ls + entropy_const : 0.0f);
+    }
+    // A row's inputs.  With one dimension per lane every wave loads all of its rows' inputs before it
+    // processes the first, so the rows' memory round trips overlap instead of following one another;
+    // the rows are then processed in the same order as the per-row form (the same sums).
+    struct RowIn {
+        float act, mu, old_mu, old_sd, old_lp, adv, v, ret, old_v;
+    };
+    const auto load_row = [&](long long i) {
+        RowIn in{0.0f, 0.0f, 0.0f, 1.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if (i < a.rows) {
+            if (one_dim && mine) {
+                in.act = a.actions[i * a.action_dim + lane];
+                in.mu = a.mean[i * a.ld_mean + lane];
+                if (a.fused) {
+                    in.old_mu = a.old_mean[i * a.action_dim + lane];
+                    in.old_sd = a.old_std[i * a.action_dim + lane];
+                }
+            }
+            in.old_lp = a.old_log_probs[i];
+            in.adv = a.advantages[i];
+            in.v = a.value[i * a.ld_value];
+            in.ret = a.returns[i];
+            if (a.clip_value) in.old_v = a.old_values[i];
         }
-        log_prob = wave_sum(log_prob);
-        entropy = wave_sum(entropy);
-        const float ratio = expf(log_prob - a.old_log_probs[i]);
-        const float adv = a.advantages[i];
+        return in;
+    };
+    const auto process = [&](long long i, const RowIn& in) {
+        float log_prob = 0.0f, entropy = 0.0f;
+        if (one_dim) {
+            if (mine) {
+                const float residual = (in.act - in.mu) * own.inv_std;
+                log_prob -= 0.5f * (residual * residual + 2.0f * own.ls + ln_two_pi);
+            }
+            log_prob = wave_sum(log_prob);
+            entropy = row_entropy;
+        } else {
+            for (int j = lane; j < a.action_dim; j += kWave) {
+                const DimTerms d = dim_terms(a, j);
+                const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * d.inv_std;
+                log_prob -= 0.5f * (residual * residual + 2.0f * d.ls + ln_two_pi);
+                entropy += d.ls + entropy_const;
+            }
+            log_prob = wave_sum(log_prob);
+            entropy = wave_sum(entropy);
+        }
+        const float ratio = expf(log_prob - in.old_lp);
+        const float adv = in.adv;
         const float clipped_ratio = fminf(fmaxf(ratio, lo), hi);
         const float unclipped = ratio * adv;
         const float clipped = clipped_ratio * adv;
@@ -343,14 +407,14 @@ __global__ __launch_bounds__(kRowThreads) void loss_kernel(LossArgs a) {
         float dratio;
         if (unclipped <= clipped) dratio = -adv;
         else dratio = (ratio > lo && ratio < hi) ? -adv : 0.0f;
-        const float v = a.value[i * a.ld_value];
-        const float error = v - a.returns[i];
+        const float v = in.v;
+        const float error = v - in.ret;
         float value_loss = error * error;
         float dv = 2.0f * error;
         if (a.clip_value) {
-            const float d = v - a.old_values[i];
-            const float cv = a.old_values[i] + fminf(fmaxf(d, -a.clip_ratio), a.clip_ratio);
-            const float ce = cv - a.returns[i];
+            const float d = v - in.old_v;
+            const float cv = in.old_v + fminf(fmaxf(d, -a.clip_ratio), a.clip_ratio);
+            const float ce = cv - in.ret;
             if (ce * ce > value_loss) {
                 value_loss = ce * ce;
                 dv = (d >= -a.clip_ratio && d <= a.clip_ratio) ? 2.0f * ce : 0.0f;
@@ -360,36 +424,59 @@ __global__ __launch_bounds__(kRowThreads) void loss_kernel(LossArgs a) {
         dv *= a.value_loss_scale;
         if (lane == 0) a.dvalue[i * a.ld_dvalue] = scale * a.value_coefficient * dv;
         const float dlp = scale * dratio * ratio;
-        for (int j = lane; j < a.action_dim; j += kWave) {
-            const float p = a.std_param[j];
-            float ls, dls_dp;
-            if (a.std_type == 1) {
-                const float c = fminf(fmaxf(p, a.std_min), a.std_max);
-                ls = logf(c);
-                dls_dp = (p >= a.std_min && p <= a.std_max) ? 1.0f / c : 0.0f;
-            } else {
-                ls = p;
-                dls_dp = 1.0f;
+        // KL(N_old || N_new) = log(s / s0) + (s0^2 + (m0 - m)^2) / (2 s^2) - 1/2 (ppo.py:207-230)
+        if (one_dim) {
+            if (mine) {
+                const float residual = (in.act - in.mu) * own.inv_std;
+                a.dmean[i * a.action_dim + lane] = dlp * residual * own.inv_std;
+                const float dstd = (dlp * (residual * residual - 1.0f) - scale * a.entropy_coefficient) * own.dls_dp;
+                if (a.fused) {
+                    std_col += dstd;
+                    const float sd_ratio = in.old_sd / own.std;
+                    const float delta = (in.old_mu - in.mu) / own.std;
+                    sums[4] += 0.5f * (sd_ratio * sd_ratio + delta * delta - 1.0f) - logf(sd_ratio);
+                } else {
+                    a.dstd_rows[i * a.action_dim + lane] = dstd;
+                }
             }
-            const float inv_std = expf(-ls);
-            const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * inv_std;
-            a.dmean[i * a.action_dim + j] = dlp * residual * inv_std;
-            const float dstd = (dlp * (residual * residual - 1.0f) - scale * a.entropy_coefficient) * dls_dp;
-            if (a.fused) {
-                std_col += dstd;
-                // KL(N_old || N_new) = log(s / s0) + (s0^2 + (m0 - m)^2) / (2 s^2) - 1/2 (ppo.py:207-230)
-                const float std = std_of(p, a.std_type, a.std_min, a.std_max);
-                const float ratio = a.old_std[i * a.action_dim + j] / std;
-                const float delta = (a.old_mean[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) / std;
-                sums[4] += 0.5f * (ratio * ratio + delta * delta - 1.0f) - logf(ratio);
-            } else {
-                a.dstd_rows[i * a.action_dim + j] = dstd;
+        } else {
+            for (int j = lane; j < a.action_dim; j += kWave) {
+                const DimTerms d = dim_terms(a, j);
+                const float residual = (a.actions[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) * d.inv_std;
+                a.dmean[i * a.action_dim + j] = dlp * residual * d.inv_std;
+                const float dstd = (dlp * (residual * residual - 1.0f) - scale * a.entropy_coefficient) * d.dls_dp;
+                if (a.fused) {
+                    std_col += dstd;
+                    const float sd_ratio = a.old_std[i * a.action_dim + j] / d.std;
+                    const float delta = (a.old_mean[i * a.action_dim + j] - a.mean[i * a.ld_mean + j]) / d.std;
+                    sums[4] += 0.5f * (sd_ratio * sd_ratio + delta * delta - 1.0f) - logf(sd_ratio);
+                } else {
+                    a.dstd_rows[i * a.action_dim + j] = dstd;
+                }
             }
         }
         sums[0] += scale * (policy_loss + a.value_coefficient * value_loss - a.entropy_coefficient * entropy);
         sums[1] += scale * policy_loss;
         sums[2] += scale * value_loss;
         sums[3] += scale * entropy;
+    };
+    constexpr int kPerWave = kRowsPerBlock / kRowWaves;
+    static_assert(kPerWave * kRowWaves == kRowsPerBlock, "whole rows per wave");
+    const long long first = blockIdx.x * static_cast<long long>(kRowsPerBlock) + wave;
+    if (one_dim) {
+        RowIn in[kPerWave];
+#pragma unroll
+        for (int q = 0; q < kPerWave; ++q) in[q] = load_row(first + q * kRowWaves);
+#pragma unroll
+        for (int q = 0; q < kPerWave; ++q) {
+            if (first + q * kRowWaves >= a.rows) break;
+            process(first + q * kRowWaves, in[q]);
+        }
+    } else {
+        for (int q = 0; q < kPerWave; ++q) {
+            if (first + q * kRowWaves >= a.rows) break;
+            process(first + q * kRowWaves, load_row(first + q * kRowWaves));
+        }
     }
     if (a.fused) {
         sums[4] = wave_sum(sums[4]);  // lanes hold different action dimensions
