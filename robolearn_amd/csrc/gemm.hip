@@ -448,6 +448,41 @@ __global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(NW =
 }
 
 // Fixed-order split-K reduction: D = act(sum_s W[s] + bias) + beta * C.
+// p[s * step] summed over s = first, first + stride, ... < splits, in that order.  Eight loads are issued
+// before the first of their adds: a plain loop waits for each load before issuing the next, one memory
+// round trip per split.  The adds keep the loop's order, so the sum is the same.
+__device__ __forceinline__ float ordered_sum(const float* p, long long step, int first, int stride, int splits) {
+    float value = 0.0f;
+    int s = first;
+    for (; s + 7 * stride < splits; s += 8 * stride) {
+        float w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w[u] = p[static_cast<long long>(s + u * stride) * step];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) value += w[u];
+    }
+    for (; s < splits; s += stride) value += p[static_cast<long long>(s) * step];
+    return value;
+}
+
+// The same over float4 pieces (p 16-byte aligned, step a multiple of 4).
+__device__ __forceinline__ float4 ordered_sum4(const float* p, long long step, int splits) {
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int s = 0;
+    for (; s + 3 < splits; s += 4) {
+        float4 w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = *reinterpret_cast<const float4*>(p + static_cast<long long>(s + u) * step);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v = make_float4(v.x + w[u].x, v.y + w[u].y, v.z + w[u].z, v.w + w[u].w);
+    }
+    for (; s < splits; ++s) {
+        const float4 w = *reinterpret_cast<const float4*>(p + static_cast<long long>(s) * step);
+        v = make_float4(v.x + w.x, v.y + w.y, v.z + w.z, v.w + w.w);
+    }
+    return v;
+}
+
 __global__ void splitk_reduce(const float* work, float* d, unsigned short* d_bf16, const float* c, const float* bias,
                               long long ldd, long long stride_d, long long stride_bias, int m, int n, int batch,
                               int splits, float beta, int epilogue) {
@@ -457,8 +492,8 @@ __global__ void splitk_reduce(const float* work, float* d, unsigned short* d_bf1
         const int col = static_cast<int>(idx % n);
         const int row = static_cast<int>((idx / n) % m);
         const int b = static_cast<int>(idx / (static_cast<long long>(m) * n));
-        float value = 0.0f;
-        for (int s = 0; s < splits; ++s) value += work[(static_cast<long long>(s) * batch + b) * m * n + static_cast<long long>(row) * n + col];
+        float value = ordered_sum(work + b * static_cast<long long>(m) * n + static_cast<long long>(row) * n + col,
+                                  static_cast<long long>(batch) * m * n, 0, 1, splits);
         const long long offset = b * stride_d + static_cast<long long>(row) * ldd + col;
         if (epilogue == kEluGrad) {
             value *= elu_grad_from_output(c[offset]);
@@ -486,11 +521,7 @@ __global__ void splitk_reduce_vec(const float* work, float* d, unsigned short* d
         const int row = static_cast<int>((idx / n4) % m);
         const int b = static_cast<int>(idx / (static_cast<long long>(m) * n4));
         const long long within = static_cast<long long>(row) * n + col;
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        for (int s = 0; s < splits; ++s) {
-            const float4 w = *reinterpret_cast<const float4*>(work + (static_cast<long long>(s) * batch + b) * plane + within);
-            v = make_float4(v.x + w.x, v.y + w.y, v.z + w.z, v.w + w.w);
-        }
+        float4 v = ordered_sum4(work + b * plane + within, static_cast<long long>(batch) * plane, splits);
         const long long offset = b * stride_d + static_cast<long long>(row) * ldd + col;
         if (epilogue == kEluGrad) {
             const float4 y = *reinterpret_cast<const float4*>(c + offset);
@@ -540,10 +571,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_grouped(const float* work, 
     if (idx < total) {
         const int b = static_cast<int>(idx / plane);
         const long long within = idx - b * plane;
-        for (int s = g; s < splits; s += kReduceGroups) value += work[(static_cast<long long>(s) * batch + b) * plane + within];
+        value = ordered_sum(work + b * plane + within, static_cast<long long>(batch) * plane, g, kReduceGroups, splits);
     } else if (idx < total + extra) {
         const long long j = idx - total;  // b * m + r
-        for (int s = g; s < splits; s += kReduceGroups) value += sums_work[static_cast<long long>(s) * batch * m + j];
+        value = ordered_sum(sums_work + j, static_cast<long long>(batch) * m, g, kReduceGroups, splits);
     }
     part[g][e] = value;
     __syncthreads();

@@ -56,33 +56,52 @@ __device__ float block_sum(float v, float* s) {
     return total;
 }
 
+// f(x[i]) summed over i = first, first + stride, ... < n, in that order.  Eight loads are issued before
+// their adds: a plain loop waits for each load before issuing the next, one memory round trip per term.
+template <typename F>
+__device__ __forceinline__ float strided_sum(const float* x, long long first, long long n, long long stride, F f) {
+    float v = 0.0f;
+    long long i = first;
+    for (; i + 7 * stride < n; i += 8 * stride) {
+        float w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w[u] = x[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v += f(w[u]);
+    }
+    for (; i < n; i += stride) v += f(x[i]);
+    return v;
+}
+
 // Single workgroup: mean, then centered variance, then normalize in place.
 // stats[0] = sum, stats[1] = sum of squared deviations.
 __global__ __launch_bounds__(kThreads) void normalize_kernel(float* advantages, long long n, int sample_std,
                                                              float* stats) {
     __shared__ float s[kThreads];
-    float sum = 0.0f;
-    for (long long i = threadIdx.x; i < n; i += kThreads) sum += advantages[i];
+    float sum = strided_sum(advantages, threadIdx.x, n, kThreads, [](float x) { return x; });
     sum = block_sum(sum, s);
     const float nf = static_cast<float>(n);
     const float mean = sum / nf;
-    float sq = 0.0f;
-    for (long long i = threadIdx.x; i < n; i += kThreads) {
-        const float c = advantages[i] - mean;
-        sq += c * c;
-    }
+    float sq = strided_sum(advantages, threadIdx.x, n, kThreads, [mean](float x) {
+        const float c = x - mean;
+        return c * c;
+    });
     sq = block_sum(sq, s);
     if (threadIdx.x == 0 && stats) {
         stats[0] = sum;
         stats[1] = sq;
     }
-    if (sample_std) {
-        const float std = sqrtf(sq / fmaxf(nf - 1.0f, 1.0f));
-        for (long long i = threadIdx.x; i < n; i += kThreads) advantages[i] = (advantages[i] - mean) / (std + 1.0e-8f);
-    } else {
-        const float denom = sqrtf(sq / nf + 1.0e-8f);
-        for (long long i = threadIdx.x; i < n; i += kThreads) advantages[i] = (advantages[i] - mean) / denom;
+    const float denom = sample_std ? sqrtf(sq / fmaxf(nf - 1.0f, 1.0f)) + 1.0e-8f : sqrtf(sq / nf + 1.0e-8f);
+    // eight loads ahead of their stores (each element is read and written by the same thread only)
+    long long i = threadIdx.x;
+    for (; i + 7 * kThreads < n; i += 8 * kThreads) {
+        float w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w[u] = advantages[i + u * kThreads];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) advantages[i + u * kThreads] = (w[u] - mean) / denom;
     }
+    for (; i < n; i += kThreads) advantages[i] = (advantages[i] - mean) / denom;
 }
 
 __device__ __forceinline__ unsigned int mix32(unsigned int x) {
@@ -546,10 +565,9 @@ __global__ __launch_bounds__(kThreads) void sum_rows_kernel(const float* terms, 
 // Sum of squares over a flat vector: per-block partials (fixed order), then one block.
 __global__ void sumsq_partials(const float* x, long long n, float* partial) {
     __shared__ float s[256];
-    float v = 0.0f;
     const long long start = static_cast<long long>(blockIdx.x) * 4096;
     const long long end = min(n, start + 4096);
-    for (long long i = start + threadIdx.x; i < end; i += 256) v += x[i] * x[i];
+    const float v = strided_sum(x, start + threadIdx.x, end, 256, [](float y) { return y * y; });
     s[threadIdx.x] = v;
     __syncthreads();
     for (int stride = 128; stride > 0; stride >>= 1) {
