@@ -27,20 +27,42 @@ __global__ void gae_kernel(int horizon, int num_envs, float gamma, float lambda,
                            const int* truncated, float* advantages, float* returns) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= num_envs) return;
+    // the inputs of eight steps are loaded before the first of them is processed: the stores of a step
+    // would otherwise hold back the next step's loads, one memory round trip per step
+    constexpr int kSteps = 8;
     float advantage = 0.0f;
-    for (int step = horizon - 1; step >= 0; --step) {
-        const long long k = static_cast<long long>(step) * num_envs + i;
-        float bootstrap = terminated[k] != 0 ? 0.0f : 1.0f;
-        const float continuation = (terminated[k] != 0 || truncated[k] != 0) ? 0.0f : 1.0f;
-        float next_value = next_values[k];
-        if (current_timeout_bootstrap && truncated[k] != 0) {
-            next_value = values[k];
-            bootstrap = 1.0f;
+    for (int top = horizon - 1; top >= 0; top -= kSteps) {
+        float reward[kSteps], value[kSteps], next[kSteps];
+        int term[kSteps], trunc[kSteps];
+#pragma unroll
+        for (int u = 0; u < kSteps; ++u) {
+            const int step = top - u;
+            if (step >= 0) {
+                const long long k = static_cast<long long>(step) * num_envs + i;
+                reward[u] = rewards[k];
+                value[u] = values[k];
+                next[u] = next_values[k];
+                term[u] = terminated[k];
+                trunc[u] = truncated[k];
+            }
         }
-        const float delta = rewards[k] + gamma * bootstrap * next_value - values[k];
-        advantage = delta + gamma * lambda * continuation * advantage;
-        advantages[k] = advantage;
-        returns[k] = advantage + values[k];
+#pragma unroll
+        for (int u = 0; u < kSteps; ++u) {
+            const int step = top - u;
+            if (step < 0) break;
+            const long long k = static_cast<long long>(step) * num_envs + i;
+            float bootstrap = term[u] != 0 ? 0.0f : 1.0f;
+            const float continuation = (term[u] != 0 || trunc[u] != 0) ? 0.0f : 1.0f;
+            float next_value = next[u];
+            if (current_timeout_bootstrap && trunc[u] != 0) {
+                next_value = value[u];
+                bootstrap = 1.0f;
+            }
+            const float delta = reward[u] + gamma * bootstrap * next_value - value[u];
+            advantage = delta + gamma * lambda * continuation * advantage;
+            advantages[k] = advantage;
+            returns[k] = advantage + value[u];
+        }
     }
 }
 
