@@ -117,32 +117,57 @@ struct GatherArgs {
 // reward, terminated, truncated, discount], grid-stride over batch * width so the
 // batch size has no launch-shape limit.  An index outside [0, capacity) raises
 // *error and reads row 0 instead.
+// One wave per sampled row: the row's index is read once, then every lane loads its (up to eight) values
+// of the row before storing any, so a row costs two memory round trips (the index, then the values).
+__device__ __forceinline__ float gather_value(const GatherArgs& a, long long k, int j) {
+    if (j < a.obs_dim) return a.obs[k * a.obs_dim + j];
+    if (j < 2 * a.obs_dim) return a.next_obs[k * a.obs_dim + (j - a.obs_dim)];
+    if (j < 2 * a.obs_dim + a.action_dim) return a.action[k * a.action_dim + (j - 2 * a.obs_dim)];
+    const int f = j - 2 * a.obs_dim - a.action_dim;
+    if (f == 0) return a.reward[k];
+    if (f == 1) return a.terminated[k];
+    if (f == 2) return a.truncated ? a.truncated[k] : 0.0f;
+    return a.discount[k];
+}
+
+__device__ __forceinline__ void gather_store(const GatherArgs& a, long long i, int j, float v) {
+    if (j < a.obs_dim) a.out_obs[i * a.obs_dim + j] = v;
+    else if (j < 2 * a.obs_dim) a.out_next_obs[i * a.obs_dim + (j - a.obs_dim)] = v;
+    else if (j < 2 * a.obs_dim + a.action_dim) a.out_action[i * a.action_dim + (j - 2 * a.obs_dim)] = v;
+    else {
+        const int f = j - 2 * a.obs_dim - a.action_dim;
+        if (f == 0) a.out_reward[i] = v;
+        else if (f == 1) a.out_terminated[i] = v;
+        else if (f == 2) {
+            if (a.out_truncated) a.out_truncated[i] = v;
+        } else a.out_discount[i] = v;
+    }
+}
+
 __global__ void gather_kernel(GatherArgs a) {
+    constexpr int kPer = 8;  // values per lane loaded before the first store
     const int width = 2 * a.obs_dim + a.action_dim + 4;
-    const long long total = a.batch * width;
-    const long long step = static_cast<long long>(gridDim.x) * blockDim.x;
-    for (long long t = blockIdx.x * static_cast<long long>(blockDim.x) + threadIdx.x; t < total; t += step) {
-        const long long i = t / width;
-        const int j = static_cast<int>(t - i * width);
+    const int lane = threadIdx.x % kWave;
+    const long long waves = static_cast<long long>(gridDim.x) * (blockDim.x / kWave);
+    for (long long i = static_cast<long long>(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave; i < a.batch;
+         i += waves) {
         long long k = a.idx[i];
         if (k < 0 || k >= a.capacity) {
-            if (j == 0 && a.error) atomicExch(a.error, 1);
+            if (lane == 0 && a.error) atomicExch(a.error, 1);
             k = 0;
         }
-        if (j < a.obs_dim) a.out_obs[i * a.obs_dim + j] = a.obs[k * a.obs_dim + j];
-        else if (j < 2 * a.obs_dim) {
-            const int c = j - a.obs_dim;
-            a.out_next_obs[i * a.obs_dim + c] = a.next_obs[k * a.obs_dim + c];
-        } else if (j < 2 * a.obs_dim + a.action_dim) {
-            const int c = j - 2 * a.obs_dim;
-            a.out_action[i * a.action_dim + c] = a.action[k * a.action_dim + c];
-        } else {
-            const int f = j - 2 * a.obs_dim - a.action_dim;
-            if (f == 0) a.out_reward[i] = a.reward[k];
-            else if (f == 1) a.out_terminated[i] = a.terminated[k];
-            else if (f == 2) {
-                if (a.out_truncated) a.out_truncated[i] = a.truncated ? a.truncated[k] : 0.0f;
-            } else a.out_discount[i] = a.discount[k];
+        for (int j0 = 0; j0 < width; j0 += kPer * kWave) {
+            float v[kPer];
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const int j = j0 + u * kWave + lane;
+                v[u] = j < width ? gather_value(a, k, j) : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < kPer; ++u) {
+                const int j = j0 + u * kWave + lane;
+                if (j < width) gather_store(a, i, j, v[u]);
+            }
         }
     }
 }
@@ -278,7 +303,28 @@ __global__ __launch_bounds__(kObjThreads) void objective_rows(const float* q0, c
     // this workgroup's rows of the action matrix, walked as one flat range
     const long long rows_here = max(0LL, min(batch, row0 + kObjThreads) - row0);
     const long long elements = rows_here * action_dim;
-    for (long long e = threadIdx.x; e < elements; e += kObjThreads) {
+    // eight elements per thread loaded before their adds (a plain loop waits for each load in turn); the
+    // adds keep the element order
+    long long e = threadIdx.x;
+    for (; e + 7 * kObjThreads < elements; e += 8 * kObjThreads) {
+        float v[8], w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const long long r = row0 + (e + u * kObjThreads) / action_dim;
+            const int j = static_cast<int>((e + u * kObjThreads) % action_dim);
+            v[u] = actions[r * ld_actions + j];
+            w[u] = bc_alpha > 0.0f ? replay_actions[r * action_dim + j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            terms[2] += v[u];
+            if (bc_alpha > 0.0f) {
+                const float d = v[u] - w[u];
+                terms[3] += d * d;
+            }
+        }
+    }
+    for (; e < elements; e += kObjThreads) {
         const long long r = row0 + e / action_dim;
         const int j = static_cast<int>(e % action_dim);
         const float v = actions[r * ld_actions + j];
@@ -497,8 +543,7 @@ RL_API int rl_replay_gather(const long long* idx, long long batch, long long cap
         P::GatherArgs a{idx, batch, obs, next_obs, action, reward, terminated, truncated, discount, out_obs,
                         out_next_obs, out_action, out_reward, out_terminated, out_truncated, out_discount, obs_dim,
                         action_dim, capacity, error};
-        const long long total = batch * (2LL * obs_dim + action_dim + 4);
-        const long long blocks = std::min<long long>((total + 255) / 256, 1LL << 20);
+        const long long blocks = std::min<long long>((batch + 3) / 4, 1LL << 20);  // a wave per row
         hipLaunchKernelGGL(P::gather_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, rl::as_stream(stream),
                            a);
         rl::check_launch("Launch replay gather");
