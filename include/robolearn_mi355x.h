@@ -78,6 +78,12 @@ size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, int splits);
  * so the input-gradient product reads both operands K-contiguously).  No
  * reference counterpart: part of the MI355X operand layout. */
 int rl_transpose16(const void* src, void* dst, int batch, int rows, int cols, void* stream);
+/* count (1..8) such transposes in one launch: job j transposes batch[j] matrices
+ * of rows[j] x cols[j] (multiples of 4, 8-byte aligned buffers) from srcs[j] to
+ * dsts[j].  The arrays are host memory, read at the call.  No reference
+ * counterpart: refreshes all of a parameter store's transposed copies at once. */
+int rl_transpose16_many(int count, const void* const* srcs, void* const* dsts, const int* batch, const int* rows,
+                        const int* cols, void* stream);
 
 /* ---- optimizer ---------------------------------------------------------- */
 /* One pass fusing Adam (form 0: torch.optim.Adam as robolearn/flashsac/agent.py:64-65;

@@ -35,6 +35,7 @@ SIGNATURES = {
                         P, P, c_ll, c_ll, P, c_ll, c_float, c_int, c_int, P, c_size, P, P, P, P]),
     "rl_gemm_workspace": (c_size, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "rl_transpose16": (c_int, [P, P, c_int, c_int, c_int, P]),
+    "rl_transpose16_many": (c_int, [c_int, PP, PP, P, P, P, P]),
     "rl_plan_create": (c_void, [c_int] * 10 + [c_size]),
     "rl_plan_create_mixed": (c_void, [c_int] * 11 + [c_size]),
     "rl_plan_workspace": (c_size, [P]),

@@ -700,6 +700,60 @@ __global__ __launch_bounds__(256) void transpose16_vec(const unsigned short* src
     }
 }
 
+// Up to kMaxTransposeJobs transposes of 16-bit [batch, rows, cols] matrices in one launch: the jobs'
+// 64 x 64 tiles are numbered one after another (job j's tiles from tile_start[j]), each workgroup
+// finds its job by a scan of the table held in its kernel arguments and runs transpose16_vec's body
+// on that tile (rows and cols multiples of 4, 8-byte aligned buffers).
+constexpr int kMaxTransposeJobs = 8;
+struct TransposeJobs {
+    int count;
+    const unsigned short* src[kMaxTransposeJobs];
+    unsigned short* dst[kMaxTransposeJobs];
+    int rows[kMaxTransposeJobs], cols[kMaxTransposeJobs];
+    long long tile_start[kMaxTransposeJobs + 1];
+};
+
+__global__ __launch_bounds__(256) void transpose16_jobs(TransposeJobs jobs) {
+    __shared__ unsigned short tile[64][66];
+    const long long id = blockIdx.x;
+    int j = 0;
+    while (j + 1 < jobs.count && id >= jobs.tile_start[j + 1]) ++j;
+    const int rows = jobs.rows[j], cols = jobs.cols[j];
+    const long long local = id - jobs.tile_start[j];
+    const int col_tiles = (cols + 63) / 64, row_tiles = (rows + 63) / 64;
+    const long long b = local / (static_cast<long long>(col_tiles) * row_tiles);
+    const int within = static_cast<int>(local - b * col_tiles * row_tiles);
+    const long long base = b * rows * cols;
+    const int r0 = (within / col_tiles) * 64;
+    const int c0 = (within % col_tiles) * 64;
+    const unsigned short* src = jobs.src[j];
+    unsigned short* dst = jobs.dst[j];
+    const int t = static_cast<int>(threadIdx.x);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = i * 16 + t / 16;
+        const int c = 4 * (t % 16);
+        if (r0 + r < rows && c0 + c < cols) {
+            const uint2 v = *reinterpret_cast<const uint2*>(src + base + static_cast<long long>(r0 + r) * cols + c0 + c);
+            tile[r][c] = static_cast<unsigned short>(v.x & 0xffffu);
+            tile[r][c + 1] = static_cast<unsigned short>(v.x >> 16);
+            tile[r][c + 2] = static_cast<unsigned short>(v.y & 0xffffu);
+            tile[r][c + 3] = static_cast<unsigned short>(v.y >> 16);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = i * 16 + t / 16;
+        const int r = 4 * (t % 16);
+        if (r0 + r < rows && c0 + c < cols) {
+            const uint2 v = make_uint2(static_cast<unsigned>(tile[r][c]) | (static_cast<unsigned>(tile[r + 1][c]) << 16),
+                                       static_cast<unsigned>(tile[r + 2][c]) | (static_cast<unsigned>(tile[r + 3][c]) << 16));
+            *reinterpret_cast<uint2*>(dst + base + static_cast<long long>(c0 + c) * rows + r0 + r) = v;
+        }
+    }
+}
+
 }  // namespace gemm
 
 // Row-major batched GEMM with optional split-K.  See the header for the
@@ -854,6 +908,36 @@ RL_API std::size_t rl_gemm_workspace(int mode, int m, int n, int k, int batch, i
     if (splits <= 1) return 0;
     // D partials plus the row-sum partials of A
     return static_cast<std::size_t>(splits) * batch * (static_cast<std::size_t>(m) * n + m) * sizeof(float);
+}
+
+// Several batched 16-bit transposes in one launch (the transposed weight copies of one parameter
+// store, refreshed after each optimizer step); no reference counterpart.
+RL_API int rl_transpose16_many(int count, const void* const* srcs, void* const* dsts, const int* batch,
+                               const int* rows, const int* cols, void* stream) noexcept {
+    return rl::guarded("rl_transpose16_many", [&] {
+        rl::require(count >= 1 && count <= rl::gemm::kMaxTransposeJobs, "Transpose job count must be 1 to 8.");
+        rl::require(srcs && dsts && batch && rows && cols, "Transpose jobs need every array.");
+        rl::gemm::TransposeJobs jobs{};
+        jobs.count = count;
+        long long tiles = 0;
+        for (int j = 0; j < count; ++j) {
+            rl::require(srcs[j] && dsts[j] && srcs[j] != dsts[j], "Transpose needs distinct source and destination buffers.");
+            rl::require(batch[j] > 0 && rows[j] > 0 && cols[j] > 0 && rows[j] % 4 == 0 && cols[j] % 4 == 0 &&
+                            rl::aligned(srcs[j], 8) && rl::aligned(dsts[j], 8),
+                        "Batched transpose jobs need rows and cols in multiples of 4 and 8-byte aligned buffers.");
+            jobs.src[j] = static_cast<const unsigned short*>(srcs[j]);
+            jobs.dst[j] = static_cast<unsigned short*>(dsts[j]);
+            jobs.rows[j] = rows[j];
+            jobs.cols[j] = cols[j];
+            jobs.tile_start[j] = tiles;
+            tiles += static_cast<long long>(batch[j]) * rl::ceil_div(rows[j], 64) * rl::ceil_div(cols[j], 64);
+        }
+        jobs.tile_start[count] = tiles;
+        rl::require(tiles <= (1LL << 31) - 1, "Too many transpose tiles.");
+        hipLaunchKernelGGL(rl::gemm::transpose16_jobs, dim3(static_cast<unsigned>(tiles)), dim3(256), 0,
+                           rl::as_stream(stream), jobs);
+        rl::check_launch("Launch batched transpose");
+    });
 }
 
 // Batched transpose of 16-bit matrices (bf16 weight copies laid out K-contiguous

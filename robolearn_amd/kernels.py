@@ -168,6 +168,17 @@ def transpose16(src, dst, *, batch, rows, cols):
     _native.call("rl_transpose16", ptr(src), ptr(dst), batch, rows, cols, stream())
 
 
+def transpose16_many(jobs):
+    """Several transpose16 calls in one launch: jobs is a list of (src, dst, batch, rows, cols) with rows and
+    cols multiples of 4 (at most 8 jobs)."""
+    for src, dst, batch, rows, cols in jobs:
+        _check(src, batch * rows * cols, "transpose source", src.dtype)
+        _check(dst, batch * rows * cols, "transpose destination", dst.dtype)
+    _native.call("rl_transpose16_many", len(jobs), _native.pointer_array([j[0].data_ptr() for j in jobs]),
+                 _native.pointer_array([j[1].data_ptr() for j in jobs]), _native.int_array([j[2] for j in jobs]),
+                 _native.int_array([j[3] for j in jobs]), _native.int_array([j[4] for j in jobs]), stream())
+
+
 def split_count(m, n, k, batch, mode):
     """K splits for a weight-gradient product (small output, K = rows).
 

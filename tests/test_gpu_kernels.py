@@ -528,6 +528,20 @@ def test_transpose16_is_exact(gpu, batch, rows, cols):
     assert torch.equal(dst.cpu(), src.cpu().transpose(1, 2))
 
 
+def test_transpose16_many_is_exact(gpu):
+    """Several bf16 transposes in one launch (a parameter store's transposed copies), edge tiles and
+    batches included, against torch's transpose of each source."""
+    print("case transpose16_many", flush=True)
+    g = torch.Generator().manual_seed(5)
+    shapes = [(2, 1024, 256), (1, 100, 36), (3, 64, 68), (2, 4, 1028)]
+    srcs = [torch.randn(b, r, c, generator=g).to(torch.bfloat16).to(gpu) for b, r, c in shapes]
+    dsts = [torch.full((b, c, r), float("nan"), dtype=torch.bfloat16, device=gpu) for b, r, c in shapes]
+    K.transpose16_many([(s, d, b, r, c) for s, d, (b, r, c) in zip(srcs, dsts, shapes)])
+    torch.cuda.synchronize()
+    for s, d in zip(srcs, dsts):
+        assert torch.equal(d.cpu().view(torch.int16), s.cpu().transpose(1, 2).contiguous().view(torch.int16))
+
+
 def test_input_gradient_with_transposed_weight(gpu):
     print("case linear_backward_input wt", flush=True)
     g = torch.Generator().manual_seed(11)
