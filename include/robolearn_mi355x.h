@@ -101,6 +101,16 @@ void* rl_fused_optimizer_create(size_t count, const int* kinds, const long long*
                                 double eps, double tau, int form, int schedule_enabled, double lr_init,
                                 double lr_peak, double lr_end, long long warmup_steps, long long decay_steps);
 int rl_fused_optimizer_step(void* plan, int do_adam, int do_project, int do_ema, const void* skip, void* stream);
+/* rl_fused_optimizer_step (do_adam 1, plan without dynamic loss scaling) with
+ * gradient-norm clipping of grad[0 .. count) folded in: one launch forms the
+ * sum-of-squares partials (partial: ceil(count / 4096) floats, rl_clip_grad_norm's
+ * order) and the step's scalars; the step scales every gradient by
+ * min(1, max_norm / (||grad|| + 1e-6)), writes it back and applies Adam;
+ * sum_squares receives ||grad||^2.  The plan's gradients lie in grad[0 .. count).
+ * Replaces the clip-then-step sequence of the combined-clipping PPO update
+ * (robolearn/warp/ppo.py:430-436, Adam(max_norm); robolearn/cuda/adam.py:147-149). */
+int rl_fused_optimizer_step_clipped(void* plan, int do_project, int do_ema, float* grad, long long count,
+                                    float* partial, float* sum_squares, float max_norm, void* stream);
 int rl_fused_optimizer_destroy(void* plan);
 
 /* robolearn/cuda/kernels.cu:760-820, 878-916 */

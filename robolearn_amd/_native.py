@@ -48,6 +48,7 @@ SIGNATURES = {
                                            c_double, c_double, c_int, c_int, c_double, c_double, c_double, c_ll,
                                            c_ll]),
     "rl_fused_optimizer_step": (c_int, [P, c_int, c_int, c_int, P, P]),
+    "rl_fused_optimizer_step_clipped": (c_int, [P, c_int, c_int, P, c_ll, P, P, c_float, P]),
     "rl_fused_optimizer_destroy": (c_int, [P]),
     "rl_adam_create": (c_void, [c_size, PP, PP, PP, PP, P, P, P, c_double, c_double, c_double]),
     "rl_adam_step": (c_int, [P, P]),

@@ -23,6 +23,7 @@
 // shadow and the EMA target.  All scalar step state lives on the device, so a
 // step is graph-capturable.
 #include "common.hpp"
+#include "reduce.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -113,6 +114,20 @@ __global__ void prepare(float* timestep, float* lr, Schedule schedule, double be
     prepare_body(timestep, lr, schedule, beta1, beta2, form, out);
 }
 
+// The gradient sum-of-squares partials of clipping (one per 4096-element block, the order of
+// rl_clip_grad_norm's partials), with the step's scalars prepared by workgroup 0 in the same launch.
+__global__ __launch_bounds__(256) void sumsq_prepare(const float* g, long long n, float* partial, float* timestep,
+                                                     float* lr, Schedule schedule, double beta1, double beta2,
+                                                     int form, Scalars* out) {
+    __shared__ float scratch[256];
+    const long long start = static_cast<long long>(blockIdx.x) * 4096;
+    const float total = block_sum_squares(g, start, min(n, start + 4096), scratch);
+    if (threadIdx.x == 0) {
+        partial[blockIdx.x] = total;
+        if (blockIdx.x == 0) prepare_body(timestep, lr, schedule, beta1, beta2, form, out);
+    }
+}
+
 // Dynamic loss scaling around an Adam step (robolearn/cuda/kernels.cu:356-405):
 // a step whose unscaled gradients held a non-finite value is skipped and the
 // scale backs off (floored at 2^-126); otherwise the step runs and the scale
@@ -151,6 +166,12 @@ struct StepArgs {
     int form, do_adam, do_project, do_ema;
     int shadow_f16;      // shadows hold IEEE fp16 (the reference projection/EMA plans) instead of bf16
     const int* skip;
+    // gradient-norm clipping folded into the step (null: none): the sum-of-squares partials of the
+    // gradients (one per 4096-element block), the norm bound, and where the sum of squares goes
+    const float* clip_partial;
+    long long clip_blocks;
+    float clip_max_norm;
+    float* clip_sum_squares;
 };
 
 __device__ __forceinline__ float adam_element(const StepArgs& a, const Scalars& s, float p, float g, float& m1, float& m2) {
@@ -179,8 +200,10 @@ __device__ __forceinline__ void store_shadow4(const StepArgs& a, unsigned short*
 
 // Pass 1 over one contiguous span: optional Adam, returns the squared norm of
 // the resulting parameters.
+// coef scales the gradients (gradient-norm clipping); with clipping on, the scaled gradients are written
+// back, as an in-place clip would leave them.
 __device__ float update_span(const StepArgs& a, const Scalars& s, const Part& part, long long offset, long long length,
-                             bool vec4) {
+                             bool vec4, float coef) {
     const int lane = threadIdx.x % kWave;
     float sumsq = 0.0f;
     float* p = part.p + offset;
@@ -189,9 +212,13 @@ __device__ float update_span(const StepArgs& a, const Scalars& s, const Part& pa
         for (long long i = lane; i < n4; i += kWave) {
             float4 pv = reinterpret_cast<float4*>(p)[i];
             if (a.do_adam) {
-                const float4 gv = reinterpret_cast<const float4*>(part.g + offset)[i];
+                float4 gv = reinterpret_cast<const float4*>(part.g + offset)[i];
                 float4 m1v = reinterpret_cast<float4*>(part.m1 + offset)[i];
                 float4 m2v = reinterpret_cast<float4*>(part.m2 + offset)[i];
+                if (a.clip_partial) {  // the clipped entry's grad range holds these gradients, writable
+                    gv = make_float4(gv.x * coef, gv.y * coef, gv.z * coef, gv.w * coef);
+                    reinterpret_cast<float4*>(const_cast<float*>(part.g) + offset)[i] = gv;
+                }
                 pv.x = adam_element(a, s, pv.x, gv.x, m1v.x, m2v.x);
                 pv.y = adam_element(a, s, pv.y, gv.y, m1v.y, m2v.y);
                 pv.z = adam_element(a, s, pv.z, gv.z, m1v.z, m2v.z);
@@ -208,7 +235,12 @@ __device__ float update_span(const StepArgs& a, const Scalars& s, const Part& pa
             if (a.do_adam) {
                 float m1 = part.m1[offset + i];
                 float m2 = part.m2[offset + i];
-                pv = adam_element(a, s, pv, part.g[offset + i], m1, m2);
+                float g = part.g[offset + i];
+                if (a.clip_partial) {  // the clipped entry's grad range holds these gradients, writable
+                    g *= coef;
+                    const_cast<float*>(part.g)[offset + i] = g;
+                }
+                pv = adam_element(a, s, pv, g, m1, m2);
                 part.m1[offset + i] = m1;
                 part.m2[offset + i] = m2;
                 p[i] = pv;
@@ -279,7 +311,7 @@ __device__ void finish_span(const StepArgs& a, const Part& part, long long offse
 // (rows up to 1024), since the buffer's registers cost occupancy for short rows.
 template <int R>
 __device__ void unit_row_in_registers(const StepArgs& a, const Scalars& s, const Part& part, long long offset,
-                                      long long cols) {
+                                      long long cols, float coef) {
     constexpr int kRegRow = R;
     const int lane = threadIdx.x % kWave;
     const long long n4 = cols / 4;
@@ -292,9 +324,13 @@ __device__ void unit_row_in_registers(const StepArgs& a, const Scalars& s, const
         if (i < n4) {
             float4 pv = p[i];
             if (a.do_adam) {
-                const float4 gv = reinterpret_cast<const float4*>(part.g + offset)[i];
+                float4 gv = reinterpret_cast<const float4*>(part.g + offset)[i];
                 float4 m1v = reinterpret_cast<float4*>(part.m1 + offset)[i];
                 float4 m2v = reinterpret_cast<float4*>(part.m2 + offset)[i];
+                if (a.clip_partial) {  // the clipped entry's grad range holds these gradients, writable
+                    gv = make_float4(gv.x * coef, gv.y * coef, gv.z * coef, gv.w * coef);
+                    reinterpret_cast<float4*>(const_cast<float*>(part.g) + offset)[i] = gv;
+                }
                 pv.x = adam_element(a, s, pv.x, gv.x, m1v.x, m2v.x);
                 pv.y = adam_element(a, s, pv.y, gv.y, m1v.y, m2v.y);
                 pv.z = adam_element(a, s, pv.z, gv.z, m1v.z, m2v.z);
@@ -335,6 +371,24 @@ __device__ void unit_row_in_registers(const StepArgs& a, const Scalars& s, const
 template <int R>
 __global__ __launch_bounds__(kThreads) void step_kernel(StepArgs a) {
     if (a.skip && a.skip[0]) return;
+    // clipping: every workgroup sums the partials in one fixed order (strided per-thread sums, then a
+    // halving tree; for up to 256 partials the same sum rl_clip_grad_norm forms) and derives the same
+    // coefficient; workgroup 0 publishes the sum of squares
+    float coef = 1.0f;
+    if (a.clip_partial) {
+        __shared__ float scratch[kThreads];
+        float v = 0.0f;
+        for (long long i = threadIdx.x; i < a.clip_blocks; i += kThreads) v += a.clip_partial[i];
+        scratch[threadIdx.x] = v;
+        __syncthreads();
+        for (int stride = kThreads / 2; stride > 0; stride >>= 1) {
+            if (static_cast<int>(threadIdx.x) < stride) scratch[threadIdx.x] += scratch[threadIdx.x + stride];
+            __syncthreads();
+        }
+        const float total = scratch[0];
+        if (blockIdx.x == 0 && threadIdx.x == 0) a.clip_sum_squares[0] = total;
+        coef = fminf(1.0f, a.clip_max_norm / (sqrtf(total) + 1.0e-6f));
+    }
     const int item = static_cast<int>(blockIdx.x) * kWaves + static_cast<int>(threadIdx.x) / kWave;
     if (item >= a.work_count) return;
     const Work w = a.work[item];
@@ -344,17 +398,17 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepArgs a) {
     if (t.kind == kPlain) {
         const long long offset = static_cast<long long>(w.unit) * kChunk;
         const long long length = min(static_cast<long long>(kChunk), t.cols - offset);
-        update_span(a, s, t.part[0], offset, length, vec4);
+        update_span(a, s, t.part[0], offset, length, vec4, coef);
         finish_span(a, t.part[0], offset, length, vec4, 2, 1.0f);
         return;
     }
     const long long offset = static_cast<long long>(w.unit) * t.cols;
     if (t.kind == kUnitRow && vec4 && a.do_project && t.cols <= 4LL * kWave * R) {
-        unit_row_in_registers<R>(a, s, t.part[0], offset, t.cols);
+        unit_row_in_registers<R>(a, s, t.part[0], offset, t.cols, coef);
         return;
     }
-    float sumsq = update_span(a, s, t.part[0], offset, t.cols, vec4);
-    if (t.kind == kBatchNormPair) sumsq += update_span(a, s, t.part[1], offset, t.cols, vec4);
+    float sumsq = update_span(a, s, t.part[0], offset, t.cols, vec4, coef);
+    if (t.kind == kBatchNormPair) sumsq += update_span(a, s, t.part[1], offset, t.cols, vec4, coef);
     sumsq = wave_sum(sumsq);
     if (!a.do_project) {
         finish_span(a, t.part[0], offset, t.cols, vec4, 2, 1.0f);
@@ -519,10 +573,22 @@ std::unique_ptr<Plan> build(std::vector<Tensor> tensors) {
     return plan;
 }
 
-void step(Plan* plan, int do_adam, int do_project, int do_ema, const int* skip, hipStream_t stream) {
+// clip (optional): the gradient buffer of clipping and its partial sums, prepared by the caller's
+// sumsq_prepare launch, which also ran the prepare step
+struct Clip {
+    const float* partial;
+    long long blocks;
+    float max_norm;
+    float* sum_squares;
+};
+
+void step(Plan* plan, int do_adam, int do_project, int do_ema, const int* skip, hipStream_t stream,
+          const Clip* clip = nullptr) {
     require(plan != nullptr, "Optimizer plan is null.");
     require(!do_adam || plan->has_adam, "This plan has no Adam state.");
-    if (do_adam && plan->loss_scale) {
+    if (clip) {
+        // the scalars were prepared with the clipping partials
+    } else if (do_adam && plan->loss_scale) {
         require(skip == nullptr, "A plan with dynamic loss scaling takes its skip flag from the scaler.");
         hipLaunchKernelGGL(scaled_prepare, dim3(1), dim3(1), 0, stream, plan->timestep, plan->lr, plan->schedule,
                            plan->beta1, plan->beta2, plan->form, plan->loss_scale, plan->growth_tracker,
@@ -553,11 +619,34 @@ void step(Plan* plan, int do_adam, int do_project, int do_ema, const int* skip, 
     a.do_ema = do_ema;
     a.shadow_f16 = plan->shadow_f16;
     a.skip = skip;
+    if (clip) {
+        a.clip_partial = clip->partial;
+        a.clip_blocks = clip->blocks;
+        a.clip_max_norm = clip->max_norm;
+        a.clip_sum_squares = clip->sum_squares;
+    }
     if (plan->long_rows)
         hipLaunchKernelGGL(step_kernel<16>, dim3(ceil_div(plan->work_count, kWaves)), dim3(kThreads), 0, stream, a);
     else
         hipLaunchKernelGGL(step_kernel<4>, dim3(ceil_div(plan->work_count, kWaves)), dim3(kThreads), 0, stream, a);
     check_launch("Launch fused optimizer step");
+}
+
+// Gradient-norm clipping of grad[0 .. n) folded into an Adam step: one launch for the sum-of-squares
+// partials and the step's scalars, one for the step with the clipped gradients.
+void step_clipped(Plan* plan, int do_project, int do_ema, float* grad, long long n, float* partial,
+                  float* sum_squares, float max_norm, hipStream_t stream) {
+    require(plan != nullptr, "Optimizer plan is null.");
+    require(plan->has_adam && !plan->loss_scale, "Clipped steps need an Adam plan without dynamic loss scaling.");
+    require(grad && partial && sum_squares && n > 0 && max_norm > 0.0f,
+            "Gradient-norm clipping needs buffers and a positive norm.");
+    const long long blocks = (n + 4095) / 4096;
+    require(blocks <= (1LL << 31) - 1, "Clipped gradient range is too large.");
+    hipLaunchKernelGGL(sumsq_prepare, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, grad, n, partial,
+                       plan->timestep, plan->lr, plan->schedule, plan->beta1, plan->beta2, plan->form, plan->scalars);
+    check_launch("Launch clipping partials and optimizer prepare");
+    const Clip clip{partial, blocks, max_norm, sum_squares};
+    step(plan, 1, do_project, do_ema, nullptr, stream, &clip);
 }
 
 void unscale(Plan* plan, hipStream_t stream) {
@@ -667,6 +756,14 @@ RL_API int rl_fused_optimizer_step(void* plan, int do_adam, int do_project, int 
     return rl::guarded("rl_fused_optimizer_step", [&] {
         rl::opt::step(static_cast<Plan*>(plan), do_adam, do_project, do_ema, static_cast<const int*>(skip),
                       rl::as_stream(stream));
+    });
+}
+
+RL_API int rl_fused_optimizer_step_clipped(void* plan, int do_project, int do_ema, float* grad, long long count,
+                                           float* partial, float* sum_squares, float max_norm, void* stream) noexcept {
+    return rl::guarded("rl_fused_optimizer_step_clipped", [&] {
+        rl::opt::step_clipped(static_cast<Plan*>(plan), do_project, do_ema, grad, count, partial, sum_squares,
+                              max_norm, rl::as_stream(stream));
     });
 }
 

@@ -13,6 +13,7 @@
 // All reductions are fixed-order (no atomics), so captured replays are
 // bitwise repeatable.
 #include "common.hpp"
+#include "reduce.hpp"
 
 #include <cmath>
 
@@ -76,23 +77,6 @@ __device__ float block_sum(float v, float* s) {
     const float total = s[0];
     __syncthreads();
     return total;
-}
-
-// f(x[i]) summed over i = first, first + stride, ... < n, in that order.  Eight loads are issued before
-// their adds: a plain loop waits for each load before issuing the next, one memory round trip per term.
-template <typename F>
-__device__ __forceinline__ float strided_sum(const float* x, long long first, long long n, long long stride, F f) {
-    float v = 0.0f;
-    long long i = first;
-    for (; i + 7 * stride < n; i += 8 * stride) {
-        float w[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) w[u] = x[i + u * stride];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v += f(w[u]);
-    }
-    for (; i < n; i += stride) v += f(x[i]);
-    return v;
 }
 
 // Single workgroup: mean, then centered variance, then normalize in place.
@@ -588,15 +572,8 @@ __global__ __launch_bounds__(kThreads) void sum_rows_kernel(const float* terms, 
 __global__ void sumsq_partials(const float* x, long long n, float* partial) {
     __shared__ float s[256];
     const long long start = static_cast<long long>(blockIdx.x) * 4096;
-    const long long end = min(n, start + 4096);
-    const float v = strided_sum(x, start + threadIdx.x, end, 256, [](float y) { return y * y; });
-    s[threadIdx.x] = v;
-    __syncthreads();
-    for (int stride = 128; stride > 0; stride >>= 1) {
-        if (static_cast<int>(threadIdx.x) < stride) s[threadIdx.x] += s[threadIdx.x + stride];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) partial[blockIdx.x] = s[0];
+    const float total = block_sum_squares(x, start, min(n, start + 4096), s);
+    if (threadIdx.x == 0) partial[blockIdx.x] = total;
 }
 
 __global__ __launch_bounds__(kThreads) void sumsq_finish(const float* partial, long long blocks, float* out) {

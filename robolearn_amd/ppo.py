@@ -318,6 +318,14 @@ class WarpPPO:
                      self.loss_partial.data_ptr(), self.totals.data_ptr(), self.kl.data_ptr(), self.lr.data_ptr(),
                      K.stream())
         self._joint_backward(M)
+        if len(self.group_ranges) == 1:
+            # combined clipping (Adam(max_norm), ppo.py:434): folded into the optimizer step's two launches
+            (start, end), norm = self.group_ranges[0], self.group_norms[0]
+            grad = self.flat.grad[start:end]
+            _native.call("rl_fused_optimizer_step_clipped", self.optimizer_handle, 0, 0, grad.data_ptr(),
+                         grad.numel(), self.norm_partial.data_ptr(), norm.data_ptr(), float(cfg.max_grad_norm),
+                         K.stream())
+            return
         for (start, end), norm in zip(self.group_ranges, self.group_norms):
             grad = self.flat.grad[start:end]
             _native.call("rl_clip_grad_norm", grad.data_ptr(), grad.numel(), self.norm_partial.data_ptr(),

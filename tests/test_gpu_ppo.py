@@ -291,6 +291,58 @@ def test_fused_clip_equals_sum_squares_then_clip(gpu, n, scale):
     assert torch.equal(a, b)
 
 
+def _plain_adam_plan(sizes, param, grad, m1, m2, timestep, lr):
+    offsets = np.cumsum([0] + sizes[:-1]).tolist()
+    ptrs = lambda buf: _native.pointer_array([buf[o:o + s].data_ptr() for o, s in zip(offsets, sizes)])  # noqa
+    n = len(sizes)
+    return _native.create("rl_fused_optimizer_create", n, _native.int_array([3] * n), _native.ll_array([1] * n),
+                          _native.ll_array(sizes), ptrs(param), ptrs(grad), ptrs(m1), ptrs(m2), None, None, None,
+                          _native.int_array([-1] * n), timestep.data_ptr(), lr.data_ptr(), 0.9, 0.999, 1e-8, 0.0, 1,
+                          0, 0.0, 0.0, 0.0, 0, 1)
+
+
+@pytest.mark.parametrize("scale", [0.3, 25.0])
+def test_clipped_optimizer_step_equals_clip_then_step(gpu, scale):
+    """rl_fused_optimizer_step_clipped (clipping folded into the Adam step, the combined-clipping PPO
+    update) leaves the same parameters, moments, clipped gradients, sum of squares and timestep, bit for
+    bit, as rl_clip_grad_norm followed by rl_fused_optimizer_step, over three steps, below and above the
+    norm bound, over tensors of the c3 layer sizes (4-aligned and not)."""
+    print(f"case clipped optimizer step scale={scale}", flush=True)
+    sizes = [123 * 512, 512, 512 * 256, 256, 37, 256 * 128, 128, 37 * 128, 37, 1]
+    g = torch.Generator().manual_seed(17)
+    n = sum(sizes)
+    param0 = torch.randn(n, generator=g)
+    states = []
+    for _ in range(2):
+        buffers = [param0.clone().to(gpu), torch.zeros(n, device=gpu), torch.zeros(n, device=gpu),
+                   torch.zeros(n, device=gpu), torch.zeros(1, device=gpu), torch.full((1,), 1e-3, device=gpu)]
+        states.append((buffers, _plain_adam_plan(sizes, *buffers)))
+    blocks = (n + 4095) // 4096
+    try:
+        for step in range(3):
+            grad = torch.randn(n, generator=g)
+            grad = (grad * (scale / grad.double().norm().item())).float()
+            outputs = []
+            for variant, (buffers, plan) in enumerate(states):
+                buffers[1].copy_(grad)
+                partial, sum_squares = torch.empty(blocks, device=gpu), torch.empty(1, device=gpu)
+                if variant == 0:
+                    _native.call("rl_clip_grad_norm", buffers[1].data_ptr(), n, partial.data_ptr(),
+                                 sum_squares.data_ptr(), 1.0, K.stream())
+                    _native.call("rl_fused_optimizer_step", plan, 1, 0, 0, None, K.stream())
+                else:
+                    _native.call("rl_fused_optimizer_step_clipped", plan, 0, 0, buffers[1].data_ptr(), n,
+                                 partial.data_ptr(), sum_squares.data_ptr(), 1.0, K.stream())
+                torch.cuda.synchronize()
+                outputs.append([b.cpu() for b in buffers[:5]] + [sum_squares.cpu()])
+            for name, x, y in zip(("param", "grad", "m1", "m2", "timestep", "sum_squares"), *outputs):
+                assert torch.equal(x, y), (step, name)
+            assert outputs[0][5].item() == pytest.approx(scale * scale, rel=1e-5)
+    finally:
+        for _, plan in states:
+            _native.load().rl_fused_optimizer_destroy(plan)
+
+
 def _device_kl_adapt(lr, old_mean, desired_kl):
     """rl_ppo_kl_adapt on one row with one action, unit old and new std (std_type 1, clamped): the
     KL is 0.5 d^2 for d = old_mean, exact in fp32 for dyadic d.  Returns (kl, learning rate)."""
