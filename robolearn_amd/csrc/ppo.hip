@@ -178,10 +178,20 @@ __global__ __launch_bounds__(kGatherWaves* kWave) void gather_kernel(GatherArgs 
     const long long r0 = (static_cast<long long>(blockIdx.x) * kGatherWaves + threadIdx.x / kWave) * kGatherRows;
     if (r0 >= a.rows) return;  // wave-uniform
     const long long mine = r0 + lane;
-    const long long kl = lane < kGatherRows && mine < a.rows ? a.indices[a.offset + mine] : 0;
+    const bool scalar_lane = lane < kGatherRows && mine < a.rows;
+    const long long kl = scalar_lane ? a.indices[a.offset + mine] : 0;
     long long k[kGatherRows];
 #pragma unroll
     for (int i = 0; i < kGatherRows; ++i) k[i] = __shfl(kl, i);
+    // the per-row scalars are loaded with the rows, ahead of every store (a load after the stores would
+    // wait for them: the compiler cannot tell the buffers apart)
+    float lp = 0.0f, value = 0.0f, advantage = 0.0f, ret = 0.0f;
+    if (scalar_lane) {
+        lp = a.log_probs[kl];
+        value = a.values[kl];
+        advantage = a.advantages[kl];
+        ret = a.returns[kl];
+    }
     constexpr int kObsPer = 4;  // observation values per lane and row (obs_dim <= 256)
     float obs[kGatherRows][kObsPer], act[kGatherRows], mean[kGatherRows], std[kGatherRows];
 #pragma unroll
@@ -212,11 +222,11 @@ __global__ __launch_bounds__(kGatherWaves* kWave) void gather_kernel(GatherArgs 
             a.b_stds[r * a.action_dim + lane] = std[i];
         }
     }
-    if (lane < kGatherRows && mine < a.rows) {
-        a.b_log_probs[mine] = a.log_probs[kl];
-        a.b_values[mine] = a.values[kl];
-        a.b_advantages[mine] = a.advantages[kl];
-        a.b_returns[mine] = a.returns[kl];
+    if (scalar_lane) {
+        a.b_log_probs[mine] = lp;
+        a.b_values[mine] = value;
+        a.b_advantages[mine] = advantage;
+        a.b_returns[mine] = ret;
     }
 }
 
