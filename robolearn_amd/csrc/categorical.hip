@@ -731,7 +731,17 @@ __global__ __launch_bounds__(kThreads) void project_target(TargetArgs a, const f
 __global__ __launch_bounds__(1024) void reduce_vector(const float* x, long long n, float scale, int op, float* out) {
     __shared__ float part[1024];
     float v = op == 1 ? -INFINITY : 0.0f;
-    for (long long i = threadIdx.x; i < n; i += blockDim.x) v = op == 1 ? fmaxf(v, x[i]) : v + x[i];
+    // eight loads ahead of their combines (same order): a plain loop waits for each load in turn
+    long long i = threadIdx.x;
+    const long long step = blockDim.x;
+    for (; i + 7 * step < n; i += 8 * step) {
+        float w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w[u] = x[i + u * step];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v = op == 1 ? fmaxf(v, w[u]) : v + w[u];
+    }
+    for (; i < n; i += step) v = op == 1 ? fmaxf(v, x[i]) : v + x[i];
     part[threadIdx.x] = v;
     __syncthreads();
     for (int s = blockDim.x / 2; s > 0; s >>= 1) {
