@@ -309,6 +309,43 @@ __device__ void finish_span(const StepArgs& a, const Part& part, long long offse
 // once.  The arithmetic is that of update_span and finish_span (mode 0).  R is 16
 // (rows up to 4096: the 4h -> h block weights) when the plan has such rows, else 4
 // (rows up to 1024), since the buffer's registers cost occupancy for short rows.
+// The Adam pass of a register-resident unit row: the updated row into v, its sum of squares returned.
+// The four arrays are distinct (restrict), so the compiler may issue a later element's loads ahead of
+// an earlier element's moment stores instead of waiting for them.  g is written only by a clipped step
+// (the clipped entry's grad range, writable); m1 and m2 are null in a plan without Adam.
+template <int R>
+__device__ __forceinline__ float adam_row(const StepArgs& a, const Scalars& s, const float4* __restrict__ p,
+                                          float4* __restrict__ g, float4* __restrict__ m1, float4* __restrict__ m2,
+                                          long long n4, float coef, float4 (&v)[R]) {
+    const int lane = threadIdx.x % kWave;
+    float sumsq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        const long long i = lane + static_cast<long long>(j) * kWave;
+        if (i < n4) {
+            float4 pv = p[i];
+            if (a.do_adam) {
+                float4 gv = g[i];
+                float4 m1v = m1[i];
+                float4 m2v = m2[i];
+                if (a.clip_partial) {
+                    gv = make_float4(gv.x * coef, gv.y * coef, gv.z * coef, gv.w * coef);
+                    g[i] = gv;
+                }
+                pv.x = adam_element(a, s, pv.x, gv.x, m1v.x, m2v.x);
+                pv.y = adam_element(a, s, pv.y, gv.y, m1v.y, m2v.y);
+                pv.z = adam_element(a, s, pv.z, gv.z, m1v.z, m2v.z);
+                pv.w = adam_element(a, s, pv.w, gv.w, m1v.w, m2v.w);
+                m1[i] = m1v;
+                m2[i] = m2v;
+            }
+            v[j] = pv;
+            sumsq += pv.x * pv.x + pv.y * pv.y + pv.z * pv.z + pv.w * pv.w;
+        }
+    }
+    return sumsq;
+}
+
 template <int R>
 __device__ void unit_row_in_registers(const StepArgs& a, const Scalars& s, const Part& part, long long offset,
                                       long long cols, float coef) {
@@ -317,31 +354,9 @@ __device__ void unit_row_in_registers(const StepArgs& a, const Scalars& s, const
     const long long n4 = cols / 4;
     float4* p = reinterpret_cast<float4*>(part.p + offset);
     float4 v[kRegRow];
-    float sumsq = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kRegRow; ++j) {
-        const long long i = lane + static_cast<long long>(j) * kWave;
-        if (i < n4) {
-            float4 pv = p[i];
-            if (a.do_adam) {
-                float4 gv = reinterpret_cast<const float4*>(part.g + offset)[i];
-                float4 m1v = reinterpret_cast<float4*>(part.m1 + offset)[i];
-                float4 m2v = reinterpret_cast<float4*>(part.m2 + offset)[i];
-                if (a.clip_partial) {  // the clipped entry's grad range holds these gradients, writable
-                    gv = make_float4(gv.x * coef, gv.y * coef, gv.z * coef, gv.w * coef);
-                    reinterpret_cast<float4*>(const_cast<float*>(part.g) + offset)[i] = gv;
-                }
-                pv.x = adam_element(a, s, pv.x, gv.x, m1v.x, m2v.x);
-                pv.y = adam_element(a, s, pv.y, gv.y, m1v.y, m2v.y);
-                pv.z = adam_element(a, s, pv.z, gv.z, m1v.z, m2v.z);
-                pv.w = adam_element(a, s, pv.w, gv.w, m1v.w, m2v.w);
-                reinterpret_cast<float4*>(part.m1 + offset)[i] = m1v;
-                reinterpret_cast<float4*>(part.m2 + offset)[i] = m2v;
-            }
-            v[j] = pv;
-            sumsq += pv.x * pv.x + pv.y * pv.y + pv.z * pv.z + pv.w * pv.w;
-        }
-    }
+    float sumsq = adam_row<kRegRow>(a, s, p, reinterpret_cast<float4*>(const_cast<float*>(part.g) + offset),
+                                    reinterpret_cast<float4*>(part.m1 + offset),
+                                    reinterpret_cast<float4*>(part.m2 + offset), n4, coef, v);
     sumsq = wave_sum(sumsq);
     const float factor = fmaxf(sqrtf(sumsq), 1.0e-8f);
 #pragma unroll
