@@ -106,7 +106,8 @@ int rl_fused_optimizer_step(void* plan, int do_adam, int do_project, int do_ema,
  * sum-of-squares partials (partial: ceil(count / 4096) floats, rl_clip_grad_norm's
  * order) and the step's scalars; the step scales every gradient by
  * min(1, max_norm / (||grad|| + 1e-6)), writes it back and applies Adam;
- * sum_squares receives ||grad||^2.  The plan's gradients lie in grad[0 .. count).
+ * sum_squares receives ||grad||^2.  The plan's gradients must lie in grad[0 .. count)
+ * (checked against the gradient pointers the plan was created with; -1 otherwise).
  * Replaces the clip-then-step sequence of the combined-clipping PPO update
  * (robolearn/warp/ppo.py:430-436, Adam(max_norm); robolearn/cuda/adam.py:147-149). */
 int rl_fused_optimizer_step_clipped(void* plan, int do_project, int do_ema, float* grad, long long count,

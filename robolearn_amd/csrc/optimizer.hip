@@ -525,6 +525,10 @@ struct Plan {
     int has_ema = 0;
     int long_rows = 0;  // a vector unit row longer than 1024 elements: step_kernel<16>
     int shadow_f16 = 0; // shadows are IEEE fp16 (reference projection/EMA plans), else bf16
+    // the lowest and one past the highest gradient element of the plan's tensors (host-side bounds, for
+    // the check that a clipped step's gradient range covers them); null without gradients
+    const float* grad_begin = nullptr;
+    const float* grad_end = nullptr;
     // dynamic loss scaling (reference-compatible rl_adam_set_scaler); null when unused
     float* loss_scale = nullptr;
     int* growth_tracker = nullptr;
@@ -583,8 +587,16 @@ std::unique_ptr<Plan> build(std::vector<Tensor> tensors) {
               "Copy optimizer work table");
     check_hip(hipMemset(plan->scalars, 0, sizeof(Scalars)), "Clear optimizer scalars");
     plan->work_count = static_cast<int>(work.size());
-    for (const Tensor& t : tensors)
+    for (const Tensor& t : tensors) {
         if (t.kind == kUnitRow && t.vec4 && t.cols > 1024) plan->long_rows = 1;
+        for (int q = 0; q < (t.kind == kBatchNormPair ? 2 : 1); ++q) {
+            const float* g = t.part[q].g;
+            if (!g) continue;
+            const float* end = g + t.rows * t.cols;
+            if (!plan->grad_begin || g < plan->grad_begin) plan->grad_begin = g;
+            if (!plan->grad_end || end > plan->grad_end) plan->grad_end = end;
+        }
+    }
     return plan;
 }
 
@@ -655,6 +667,8 @@ void step_clipped(Plan* plan, int do_project, int do_ema, float* grad, long long
     require(plan->has_adam && !plan->loss_scale, "Clipped steps need an Adam plan without dynamic loss scaling.");
     require(grad && partial && sum_squares && n > 0 && max_norm > 0.0f,
             "Gradient-norm clipping needs buffers and a positive norm.");
+    require(plan->grad_begin && plan->grad_begin >= grad && plan->grad_end <= grad + n,
+            "The clipped gradient range must hold every gradient of the optimizer plan.");
     const long long blocks = (n + 4095) / 4096;
     require(blocks <= (1LL << 31) - 1, "Clipped gradient range is too large.");
     hipLaunchKernelGGL(sumsq_prepare, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, grad, n, partial,

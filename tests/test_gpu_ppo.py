@@ -338,6 +338,12 @@ def test_clipped_optimizer_step_equals_clip_then_step(gpu, scale):
             for name, x, y in zip(("param", "grad", "m1", "m2", "timestep", "sum_squares"), *outputs):
                 assert torch.equal(x, y), (step, name)
             assert outputs[0][5].item() == pytest.approx(scale * scale, rel=1e-5)
+        # a gradient range that misses some of the plan's gradients is refused before any launch
+        buffers, plan = states[1]
+        partial, sum_squares = torch.empty(blocks, device=gpu), torch.empty(1, device=gpu)
+        with pytest.raises(RuntimeError, match="every gradient of the optimizer plan"):
+            _native.call("rl_fused_optimizer_step_clipped", plan, 0, 0, buffers[1].data_ptr(), n - 1,
+                         partial.data_ptr(), sum_squares.data_ptr(), 1.0, K.stream())
     finally:
         for _, plan in states:
             _native.load().rl_fused_optimizer_destroy(plan)
