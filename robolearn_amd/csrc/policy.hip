@@ -113,12 +113,12 @@ struct GatherArgs {
     int* error;
 };
 
-// One thread per (row, column) of the concatenated row [obs | next_obs | action |
-// reward, terminated, truncated, discount], grid-stride over batch * width so the
-// batch size has no launch-shape limit.  An index outside [0, capacity) raises
-// *error and reads row 0 instead.
-// One wave per sampled row: the row's index is read once, then every lane loads its (up to eight) values
-// of the row before storing any, so a row costs two memory round trips (the index, then the values).
+// Replay gather of the concatenated row [obs | next_obs | action | reward, terminated, truncated,
+// discount]: one wave per sampled row, grid-stride over the rows so the batch size has no launch-shape
+// limit.  The row's index is read once, then every lane loads its (up to eight) values of the row before
+// storing any, so a row costs two memory round trips (the index, then the values).  An index outside
+// [0, capacity) raises *error and reads row 0 instead.
+// Column j of the concatenated row of replay row k.
 __device__ __forceinline__ float gather_value(const GatherArgs& a, long long k, int j) {
     if (j < a.obs_dim) return a.obs[k * a.obs_dim + j];
     if (j < 2 * a.obs_dim) return a.next_obs[k * a.obs_dim + (j - a.obs_dim)];
@@ -130,6 +130,7 @@ __device__ __forceinline__ float gather_value(const GatherArgs& a, long long k, 
     return a.discount[k];
 }
 
+// Column j of batch row i of the outputs.
 __device__ __forceinline__ void gather_store(const GatherArgs& a, long long i, int j, float v) {
     if (j < a.obs_dim) a.out_obs[i * a.obs_dim + j] = v;
     else if (j < 2 * a.obs_dim) a.out_next_obs[i * a.obs_dim + (j - a.obs_dim)] = v;
